@@ -1,0 +1,220 @@
+"""logicaffeine_amd -- Python view of liblgx, the MI355X back-end of the Q8
+LLM-decode hot path.
+
+Every compute call goes through the C ABI in ``include/lgx.h`` (liblgx.so ->
+hipModuleLaunchKernel on lgx_kernels.hsaco).  There is no CPU or PyTorch
+fallback: if the library or its code object is missing, :class:`Context`
+raises.  torch is used only for device memory and the current stream.
+
+The loader mirrors the reference's AOT tier (load a built module, resolve its
+``extern "C"`` symbols, keep it alive, count calls;
+crates/logicaffeine_compile/src/vm/aot_tier.rs:86-111), and errors surface as
+:class:`LgxError` carrying the ``lgx_status`` and ``lgx_last_error()`` text
+(crates/logicaffeine_compile/src/codegen/ffi.rs:196-258).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liblgx.so")
+HSACO_PATH = os.path.join(HERE, "lgx_kernels.hsaco")
+
+Q8_ROWMAJOR = 0
+Q8_T16 = 1
+Q8_RANGE_BLOCKS = 32
+
+STATUS_NAMES = {
+    0: "LGX_OK", 1: "LGX_ERROR", 2: "LGX_INVALID_ARGUMENT", 3: "LGX_NULL_POINTER",
+    4: "LGX_OUT_OF_BOUNDS", 5: "LGX_MODULE_LOAD_FAILED", 6: "LGX_INVALID_HANDLE",
+    8: "LGX_INTERNAL_PANIC", 9: "LGX_OUT_OF_MEMORY", 10: "LGX_HIP_ERROR",
+    11: "LGX_NO_DEVICE", 12: "LGX_UNSUPPORTED",
+}
+
+# Exported symbols and their C signatures (include/lgx.h).
+_P = C.c_void_p
+_I32 = C.c_int32
+SIGNATURES = {
+    "lgx_abi_version": (C.c_uint32, []),
+    "lgx_version": (C.c_char_p, []),
+    "lgx_last_error": (C.c_char_p, []),
+    "lgx_clear_error": (None, []),
+    "lgx_ctx_create": (C.c_int, [_I32, C.c_char_p, C.POINTER(_P)]),
+    "lgx_ctx_destroy": (C.c_int, [_P]),
+    "lgx_ctx_launch_count": (C.c_uint64, [_P]),
+    "lgx_ctx_arch": (C.c_char_p, [_P]),
+    "lgx_q8_repack_t16": (C.c_int, [_P, _P, _I32, _I32, _P, _P]),
+    "lgx_q8_unpack_t16": (C.c_int, [_P, _P, _I32, _I32, _P, _P]),
+    "lgx_quantize_q8_0": (C.c_int, [_P, _P, _I32, _I32, _P, _P, _P]),
+    "lgx_q8_gemv_f32": (C.c_int, [_P, _P, _P, _P, _P]),
+    "lgx_q8q8_gemv": (C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
+    "lgx_q8_gemm": (C.c_int, [_P, _P, _P, _P, _I32, _P, _P]),
+}
+
+
+class LgxError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.status_name = STATUS_NAMES.get(status, str(status))
+        super().__init__(f"{self.status_name}: {message}")
+
+
+class Q8MatrixC(C.Structure):
+    _fields_ = [("qs", _P), ("d", _P), ("n", _I32), ("k", _I32), ("layout", _I32)]
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Load liblgx.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -m logicaffeine_amd.build`")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        msg = lib().lgx_last_error()
+        raise LgxError(status, msg.decode() if msg else "(no message)")
+
+
+def _stream(torch, device):
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class Q8Matrix:
+    """A Q8_0 weight matrix resident on the device in T16 order.
+
+    ``qs`` is an int8 device tensor (T16 order, n*k bytes); ``d`` an int16
+    device tensor holding the binary16 scale bits, shape [n, k/32]."""
+
+    def __init__(self, qs, d, n: int, k: int):
+        self.qs, self.d, self.n, self.k = qs, d, n, k
+        self._c = Q8MatrixC(qs.data_ptr(), d.data_ptr(), n, k, Q8_T16)
+
+    @property
+    def cstruct(self):
+        return C.byref(self._c)
+
+    @property
+    def nbytes(self) -> int:
+        return self.qs.numel() + 2 * self.d.numel()
+
+
+class Context:
+    """One lgx_ctx: the loaded code object on one device."""
+
+    def __init__(self, device: int = 0, hsaco: str | None = None):
+        import torch
+
+        self.torch = torch
+        self.device = device
+        self.dev = torch.device("cuda", device)
+        h = C.c_void_p()
+        _check(lib().lgx_ctx_create(device, hsaco.encode() if hsaco else None, C.byref(h)))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            _check(lib().lgx_ctx_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def launch_count(self) -> int:
+        return int(lib().lgx_ctx_launch_count(self.handle))
+
+    @property
+    def arch(self) -> str:
+        return lib().lgx_ctx_arch(self.handle).decode()
+
+    def _s(self):
+        return _stream(self.torch, self.dev)
+
+    # ---- layout ----------------------------------------------------------
+    def repack_t16(self, qs_rowmajor):
+        n, k = qs_rowmajor.shape
+        out = self.torch.empty(n * k, dtype=self.torch.int8, device=self.dev)
+        _check(lib().lgx_q8_repack_t16(self.handle, qs_rowmajor.data_ptr(), n, k,
+                                       out.data_ptr(), self._s()))
+        return out
+
+    def unpack_t16(self, qs_t16, n: int, k: int):
+        out = self.torch.empty((n, k), dtype=self.torch.int8, device=self.dev)
+        _check(lib().lgx_q8_unpack_t16(self.handle, qs_t16.data_ptr(), n, k,
+                                       out.data_ptr(), self._s()))
+        return out
+
+    def to_device(self, a, dtype=None):
+        """numpy array or tensor -> contiguous device tensor (uint16 data is
+        carried as int16 bit patterns)."""
+        t = self.torch
+        if not isinstance(a, t.Tensor):
+            import numpy as np
+
+            a = np.ascontiguousarray(a)
+            if a.dtype == np.uint16:
+                a = a.view(np.int16)
+            a = t.from_numpy(a)
+        elif a.dtype == t.uint16:
+            a = a.view(t.int16)
+        if dtype is not None and a.dtype != dtype:
+            a = a.to(dtype)
+        return a.to(self.dev).contiguous()
+
+    def q8_matrix(self, qs_rowmajor, d) -> Q8Matrix:
+        """Upload (if host) and repack row-major quants + binary16 scale bits."""
+        t = self.torch
+        qs = self.to_device(qs_rowmajor, t.int8)
+        dd = self.to_device(d, t.int16)
+        n, k = qs.shape
+        return Q8Matrix(self.repack_t16(qs), dd, n, k)
+
+    # ---- Q8_0 ------------------------------------------------------------
+    def quantize_q8_0(self, x, qs=None, d=None):
+        t = self.torch
+        m, k = x.shape
+        qs = t.empty((m, k), dtype=t.int8, device=self.dev) if qs is None else qs
+        d = t.empty((m, k // 32), dtype=t.int16, device=self.dev) if d is None else d
+        _check(lib().lgx_quantize_q8_0(self.handle, x.data_ptr(), m, k, qs.data_ptr(),
+                                       d.data_ptr(), self._s()))
+        return qs, d
+
+    def q8_gemv_f32(self, W: Q8Matrix, x, y=None):
+        y = self.torch.empty(W.n, dtype=self.torch.float32, device=self.dev) if y is None else y
+        _check(lib().lgx_q8_gemv_f32(self.handle, W.cstruct, x.data_ptr(), y.data_ptr(),
+                                     self._s()))
+        return y
+
+    def q8q8_gemv(self, W: Q8Matrix, xq, xd, y=None, blockdots: bool = False):
+        t = self.torch
+        y = t.empty(W.n, dtype=t.float32, device=self.dev) if y is None else y
+        dbg = t.empty((W.n, W.k // 32), dtype=t.int32, device=self.dev) if blockdots else None
+        _check(lib().lgx_q8q8_gemv(self.handle, W.cstruct, xq.data_ptr(), xd.data_ptr(),
+                                   y.data_ptr(), dbg.data_ptr() if dbg is not None else None,
+                                   self._s()))
+        return (y, dbg) if blockdots else y
+
+    def q8_gemm(self, W: Q8Matrix, xq, xd, y=None):
+        t = self.torch
+        m = xq.shape[0]
+        y = t.empty((m, W.n), dtype=t.float32, device=self.dev) if y is None else y
+        _check(lib().lgx_q8_gemm(self.handle, W.cstruct, xq.data_ptr(), xd.data_ptr(), m,
+                                 y.data_ptr(), self._s()))
+        return y

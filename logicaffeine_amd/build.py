@@ -1,0 +1,64 @@
+"""Build recipe of liblgx (no cmake, no JIT cache: everything lands in-tree).
+
+    lgx_kernels.hsaco  hipcc --genco --offload-arch=gfx950 (device code only)
+    liblgx.so          g++ host launcher over the HIP module API
+
+Run as ``python -m logicaffeine_amd.build``; ``__graft_entry__.build()`` calls
+:func:`build`.  Both artefacts sit next to this file, which is where
+``lgx_ctx_create(dev, NULL, ...)`` looks for the code object.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+ARCH = "gfx950"
+
+HSACO = os.path.join(HERE, "lgx_kernels.hsaco")
+LIB = os.path.join(HERE, "liblgx.so")
+
+# -ffp-contract=off: no implicit fusion, the float schedule is what the source
+# says.  Correctly rounded binary32 division and square root.  Packed-FP32
+# instructions disabled (v_pk_*_f32 are never generated).
+HIP_FLAGS = [
+    "--genco", f"--offload-arch={ARCH}", "-O3", "-std=c++17",
+    "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd):
+    print("[lgx build]", " ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def build_kernels() -> str:
+    src = os.path.join(CSRC, "lgx_kernels.hip")
+    tmp = HSACO + ".tmp"
+    _run([os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, "-I", CSRC, "-o", tmp, src])
+    os.replace(tmp, HSACO)
+    return HSACO
+
+
+def build_host() -> str:
+    src = os.path.join(CSRC, "lgx_host.cpp")
+    tmp = LIB + ".tmp"
+    _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-Wextra",
+          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", "-I", CSRC,
+          "-o", tmp, src, f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl"])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build() -> None:
+    build_kernels()
+    build_host()
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

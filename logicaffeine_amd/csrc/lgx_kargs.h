@@ -1,0 +1,39 @@
+// lgx_kargs.h -- kernel argument blocks shared by the host launcher and the
+// device code.  Every kernel takes exactly one of these structs by value, so
+// hipModuleLaunchKernel is called with kernelParams = { &args }.  Plain C
+// layout (pointers, int32, float), identical on x86-64 and amdgcn.
+#pragma once
+#include <stdint.h>
+
+#define LGX_Q8_RANGE_BLOCKS 32   // blocks of 32 per canonical accumulation range
+#define LGX_MAX_RANGES 32        // => K <= 32768
+#define LGX_WAVE 64
+
+typedef struct {
+    const int8_t* src;
+    int8_t* dst;
+    int32_t n, k;
+    int32_t to_t16;  // 1: row-major -> T16, 0: T16 -> row-major
+} lgx_repack_args;
+
+typedef struct {
+    const float* x;   // [m][k]
+    int8_t* qs;       // [m][k]
+    uint16_t* d;      // [m][k/32]
+    int32_t m, k;
+} lgx_quant_args;
+
+// One wave per (row tile of 16, range of 32 blocks[, m-group of 64 rows]).
+typedef struct {
+    const int8_t* wt;     // T16 weights
+    const uint16_t* wd;   // [n][nb] f16 scales
+    const float* xf;      // gemv_f32: x [k]
+    const int8_t* xq;     // q8 paths: [m][k]
+    const uint16_t* xd;   // q8 paths: [m][nb]
+    float* y;             // [m][n] when nranges == 1
+    float* part;          // [nranges][m][n] when nranges > 1
+    int32_t* counter;     // [ntiles][nmgroups] arrival counters (zero between calls)
+    int32_t* dbg;         // nullable: [n][nb] int32 block dots (gemv only)
+    int32_t n, k, m;
+    int32_t ntiles, nranges, nmgroups;
+} lgx_gemv_args;

@@ -1,0 +1,323 @@
+/*
+ * lgx_oracle.c -- CPU restatement of the lgx hot path (TEST INFRASTRUCTURE).
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use
+ * this file, as the checker.  Built with -ffp-contract=off: every fused
+ * multiply-add below is an explicit fmaf() standing where the device kernel
+ * issues v_fma_f32, and every other float operation is a separately rounded
+ * IEEE-754 binary32 operation, so a device kernel that follows the same
+ * schedule produces the same bits.
+ *
+ * The reference contains no implementation of these functions (no GPU
+ * back-end, no tensor code); see lgx_oracle.h for the conventions taken from
+ * it and for what pins each function.
+ */
+#include "lgx_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ------------------------------------------------------------------ */
+/* IEEE binary16 <-> binary32                                          */
+/* ------------------------------------------------------------------ */
+
+/* Round-to-nearest-even binary32 -> binary16 (IEEE 754-2008 convertFormat).
+ * Overflow (|x| >= 65520) gives +-inf; NaN gives the quiet NaN 0x7e00. */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x = f2u(f);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+    if (ax < 0x38800000u) {                 /* below 2^-14: binary16 subnormal */
+        if (ax <= 0x33000000u) return sign; /* <= 2^-25 rounds (ties-to-even) to 0 */
+        uint32_t e = ax >> 23;
+        uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        uint32_t sh = 126u - e;             /* value / 2^-24 = m >> sh */
+        uint32_t h = (m + (1u << (sh - 1)) - 1u + ((m >> sh) & 1u)) >> sh;
+        return (uint16_t)(sign | h);
+    }
+    ax -= 0x38000000u;                      /* rebias exponent 127 -> 15 */
+    ax += 0x0fffu + ((ax >> 13) & 1u);
+    return (uint16_t)(sign | (ax >> 13));
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = ((uint32_t)h >> 10) & 0x1fu;
+    uint32_t m = (uint32_t)h & 0x3ffu;
+    if (e == 0x1fu) return u2f(sign | 0x7f800000u | (m << 13));
+    if (e == 0) {
+        if (m == 0) return u2f(sign);
+        /* subnormal: m * 2^-24, exact in binary32 */
+        float v = (float)m * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    }
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+void orc_f32_to_f16_array(const float* x, uint16_t* h, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) h[i] = orc_f32_to_f16(x[i]);
+}
+
+void orc_f16_to_f32_array(const uint16_t* h, float* x, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) x[i] = orc_f16_to_f32(h[i]);
+}
+
+/* ------------------------------------------------------------------ */
+/* Canonical exp (binary32)                                            */
+/* ------------------------------------------------------------------ */
+/* Cody-Waite reduction x = n*ln2 + r with n = rint(x*log2(e)) (rint by the
+ * 1.5*2^23 magic constant under round-to-nearest-even), ln2 split into
+ * ln2_hi = 0x3f317200 (exact product with n) and ln2_lo; then the degree-7
+ * Taylor polynomial of e^r on |r| <= ln2/2 in Horner form with fmaf, and
+ * scaling by 2^n through the exponent field.  x < -87.33 returns +0 (no
+ * subnormal results), x > 88.72 returns +inf.  exp(0) == 1 exactly. */
+float orc_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72f) return INFINITY;
+    if (x < -87.33f) return 0.0f;
+    float t = x * 1.44269504088896341f;
+    float nf = (t + 12582912.0f) - 12582912.0f;
+    float r = fmaf(-nf, 0.693145751953125f, x);
+    r = fmaf(-nf, 1.42860682030941723e-06f, r);
+    float p = 1.98412698412698413e-04f;
+    p = fmaf(p, r, 1.38888888888888889e-03f);
+    p = fmaf(p, r, 8.33333333333333333e-03f);
+    p = fmaf(p, r, 4.16666666666666667e-02f);
+    p = fmaf(p, r, 1.66666666666666667e-01f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    int n = (int)nf;
+    if (n > 127) { p = p * 2.0f; n -= 1; }
+    return p * u2f((uint32_t)(n + 127) << 23);
+}
+
+/* silu(g) = g / (1 + exp(-g)), each step a separately rounded operation. */
+float orc_silu(float g) {
+    float e = orc_expf(-g);
+    float den = 1.0f + e;
+    return g / den;
+}
+
+void orc_expf_array(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_expf(x[i]);
+}
+
+/* ------------------------------------------------------------------ */
+/* Seeded generators                                                   */
+/* ------------------------------------------------------------------ */
+/* SplitMix64 (crates/logicaffeine_runtime/src/seed.rs:30-38): state +=
+ * 0x9E3779B97F4A7C15 then the xor-shift-multiply finaliser.  Output i of a
+ * sequence started at state s is mix(s + (i+1)*gamma), so every element of a
+ * stream is addressable by its index. */
+#define SM_GAMMA 0x9E3779B97F4A7C15ull
+
+static inline uint64_t sm_mix(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+void orc_splitmix64_seq(uint64_t state, uint64_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        state += SM_GAMMA;
+        out[i] = sm_mix(state);
+    }
+}
+
+/* Starting state of stream `stream` under `seed`. */
+uint64_t orc_stream_base(uint64_t seed, uint64_t stream) {
+    return sm_mix(seed + SM_GAMMA) ^ sm_mix((stream + 1ull) * 0xD1B54A32D192ED03ull);
+}
+
+static inline uint64_t stream_at(uint64_t base, uint64_t i) {
+    return sm_mix(base + (i + 1ull) * SM_GAMMA);
+}
+
+void orc_gen_u64(uint64_t seed, uint64_t stream, uint64_t* out, int64_t n) {
+    uint64_t b = orc_stream_base(seed, stream);
+    for (int64_t i = 0; i < n; ++i) out[i] = stream_at(b, (uint64_t)i);
+}
+
+/* Uniform integer in [0, bound) by the multiply-high map of the top 32 bits
+ * (bias <= bound / 2^32). */
+static inline uint32_t below32(uint64_t u, uint32_t bound) {
+    return (uint32_t)(((u >> 32) * (uint64_t)bound) >> 32);
+}
+
+/* int8 uniform on [-127, 127]. */
+void orc_gen_i8(uint64_t seed, uint64_t stream, int8_t* out, int64_t n) {
+    uint64_t b = orc_stream_base(seed, stream);
+    for (int64_t i = 0; i < n; ++i) out[i] = (int8_t)((int32_t)below32(stream_at(b, (uint64_t)i), 255u) - 127);
+}
+
+void orc_gen_below_i32(uint64_t seed, uint64_t stream, uint32_t bound, int32_t* out, int64_t n) {
+    uint64_t b = orc_stream_base(seed, stream);
+    for (int64_t i = 0; i < n; ++i) out[i] = (int32_t)below32(stream_at(b, (uint64_t)i), bound);
+}
+
+/* Standard normal for element i: Box-Muller on draws 2i and 2i+1 in binary64,
+ * u1 in (0,1], u2 in [0,1). */
+static inline double normal_at(uint64_t base, uint64_t i) {
+    uint64_t a = stream_at(base, 2ull * i);
+    uint64_t c = stream_at(base, 2ull * i + 1ull);
+    double u1 = (double)((a >> 11) + 1ull) * 0x1.0p-53;
+    double u2 = (double)(c >> 11) * 0x1.0p-53;
+    return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+}
+
+void orc_gen_normal_f32(uint64_t seed, uint64_t stream, double sigma, float* out, int64_t n) {
+    uint64_t b = orc_stream_base(seed, stream);
+    for (int64_t i = 0; i < n; ++i) out[i] = (float)(sigma * normal_at(b, (uint64_t)i));
+}
+
+void orc_gen_normal_f16(uint64_t seed, uint64_t stream, double sigma, uint16_t* out, int64_t n) {
+    uint64_t b = orc_stream_base(seed, stream);
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_f32_to_f16((float)(sigma * normal_at(b, (uint64_t)i)));
+}
+
+/* Weight block scales: d = |N(0, 0.02)| / 127, rounded to binary32 then to
+ * binary16 (RNE). */
+void orc_gen_q8_scales(uint64_t seed, uint64_t stream, uint16_t* out, int64_t n) {
+    uint64_t b = orc_stream_base(seed, stream);
+    for (int64_t i = 0; i < n; ++i) {
+        double z = fabs(0.02 * normal_at(b, (uint64_t)i)) / 127.0;
+        out[i] = orc_f32_to_f16((float)z);
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* Q8_0                                                                */
+/* ------------------------------------------------------------------ */
+/* Activation quantisation, GGML Q8_0 style: per 32-block amax = max|x|,
+ * d = amax / 127 (binary32 division), id = d != 0 ? 1/d : 0, q = round half
+ * away from zero of x*id clamped to [-127, 127]; the stored scale is
+ * binary16(d) (RNE) while q uses the binary32 id. */
+void orc_quantize_q8_0(const float* x, int64_t m, int32_t k, int8_t* qs, uint16_t* d) {
+    int32_t nb = k / 32;
+    for (int64_t r = 0; r < m; ++r) {
+        for (int32_t b = 0; b < nb; ++b) {
+            const float* xb = x + r * k + (int64_t)b * 32;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; ++i) {
+                float a = fabsf(xb[i]);
+                if (a > amax) amax = a;
+            }
+            float dd = amax / 127.0f;
+            float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+            d[r * nb + b] = orc_f32_to_f16(dd);
+            for (int i = 0; i < 32; ++i) {
+                float v = roundf(xb[i] * id);
+                if (v > 127.0f) v = 127.0f;
+                if (v < -127.0f) v = -127.0f;
+                qs[r * k + (int64_t)b * 32 + i] = (int8_t)v;
+            }
+        }
+    }
+}
+
+/* Device tile layout "T16": 16 rows x 2 blocks (1 KiB) per unit, unit index
+ * (row_tile * (k/64) + block_pair); inside a unit lane l = (row%16) + 16*c
+ * owns 16 bytes: bytes [0,8) are k = 64p + 8c + j of block 2p and bytes
+ * [8,16) the same offsets of block 2p+1.  This is the B-operand order of the
+ * 16x16x32 int8 MFMA, so one 128-bit load per lane feeds two MFMAs. */
+static inline int64_t t16_index(int32_t row, int32_t kk, int32_t k) {
+    int32_t t = row >> 4, r = row & 15;
+    int32_t p = kk >> 6, w = kk & 63;
+    int32_t hi = w >> 5, c = (w & 31) >> 3, j = w & 7;
+    int32_t lane = r + 16 * c;
+    return ((int64_t)t * (k >> 6) + p) * 1024 + lane * 16 + hi * 8 + j;
+}
+
+void orc_q8_repack_t16(const int8_t* qs, int32_t n, int32_t k, int8_t* out) {
+    for (int32_t row = 0; row < n; ++row)
+        for (int32_t kk = 0; kk < k; ++kk)
+            out[t16_index(row, kk, k)] = qs[(int64_t)row * k + kk];
+}
+
+void orc_q8_unpack_t16(const int8_t* t16, int32_t n, int32_t k, int8_t* qs) {
+    for (int32_t row = 0; row < n; ++row)
+        for (int32_t kk = 0; kk < k; ++kk)
+            qs[(int64_t)row * k + kk] = t16[t16_index(row, kk, k)];
+}
+
+/* y = W x with binary32 x.  Tolerance-checked path (1e-3 rel / 1e-4 abs),
+ * so the oracle accumulates in binary64 for accuracy. */
+void orc_q8_gemv_f32(const int8_t* qs, const uint16_t* d, int32_t n, int32_t k,
+                     const float* x, float* y) {
+    int32_t nb = k / 32;
+#pragma omp parallel for schedule(static)
+    for (int32_t row = 0; row < n; ++row) {
+        double acc = 0.0;
+        for (int32_t b = 0; b < nb; ++b) {
+            const int8_t* q = qs + (int64_t)row * k + (int64_t)b * 32;
+            const float* xb = x + (int64_t)b * 32;
+            double s = 0.0;
+            for (int i = 0; i < 32; ++i) s += (double)q[i] * (double)xb[i];
+            acc += (double)orc_f16_to_f32(d[(int64_t)row * nb + b]) * s;
+        }
+        y[row] = (float)acc;
+    }
+}
+
+static inline int32_t block_dot(const int8_t* a, const int8_t* b) {
+    int32_t s = 0;
+    for (int i = 0; i < 32; ++i) s += (int32_t)a[i] * (int32_t)b[i];
+    return s;
+}
+
+/* Exact int32 block dot products s[row][b] of W with a Q8_0 activation. */
+void orc_q8_blockdots(const int8_t* qs, int32_t n, int32_t k, const int8_t* xq, int32_t* s) {
+    int32_t nb = k / 32;
+#pragma omp parallel for schedule(static)
+    for (int32_t row = 0; row < n; ++row)
+        for (int32_t b = 0; b < nb; ++b)
+            s[(int64_t)row * nb + b] = block_dot(qs + (int64_t)row * k + (int64_t)b * 32, xq + (int64_t)b * 32);
+}
+
+/* Pairwise tree with doubling stride: for s = 1, 2, 4, ...: p[i] += p[i+s]
+ * for i = 0, 2s, 4s, ... with i+s < g.  Returns p[0]; modifies p. */
+float orc_tree_sum(float* p, int32_t g) {
+    for (int32_t s = 1; s < g; s <<= 1)
+        for (int32_t i = 0; i + s < g; i += 2 * s) p[i] = p[i] + p[i + s];
+    return g > 0 ? p[0] : 0.0f;
+}
+
+/* Canonical Q8 x Q8 product, the schedule every device kernel follows:
+ *   s_b  = sum_i qw[32b+i] * qx[32b+i]            (int32, exact)
+ *   dd_b = f32(dw_b) * f32(dx_b)                  (exact: 11x11-bit product)
+ *   range r covers blocks [32r, min(32r+32, nb)):
+ *       P_r = fmaf((float)s_b, dd_b, P_r), P_r starting at +0, b ascending
+ *   y = orc_tree_sum(P, ceil(nb/32)).
+ * y[m][n] for activation rows m.  Rows are independent (batch invariant). */
+void orc_q8_gemm(const int8_t* qs, const uint16_t* d, int32_t n, int32_t k,
+                 const int8_t* xq, const uint16_t* xd, int32_t m, float* y) {
+    int32_t nb = k / 32;
+    int32_t g = (nb + ORC_Q8_RANGE_BLOCKS - 1) / ORC_Q8_RANGE_BLOCKS;
+#pragma omp parallel for schedule(static)
+    for (int64_t idx = 0; idx < (int64_t)m * n; ++idx) {
+        int32_t mi = (int32_t)(idx / n), row = (int32_t)(idx % n);
+        float part[1024];
+        const int8_t* w = qs + (int64_t)row * k;
+        const int8_t* a = xq + (int64_t)mi * k;
+        for (int32_t r = 0; r < g; ++r) {
+            float acc = 0.0f;
+            int32_t b1 = (r + 1) * ORC_Q8_RANGE_BLOCKS;
+            if (b1 > nb) b1 = nb;
+            for (int32_t b = r * ORC_Q8_RANGE_BLOCKS; b < b1; ++b) {
+                int32_t s = block_dot(w + (int64_t)b * 32, a + (int64_t)b * 32);
+                float dd = orc_f16_to_f32(d[(int64_t)row * nb + b]) *
+                           orc_f16_to_f32(xd[(int64_t)mi * nb + b]);
+                acc = fmaf((float)s, dd, acc);
+            }
+            part[r] = acc;
+        }
+        y[(int64_t)mi * n + row] = orc_tree_sum(part, g);
+    }
+}

@@ -1,0 +1,84 @@
+/*
+ * lgx_oracle.h -- CPU oracle for the lgx Q8 LLM-decode hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker, never the product:
+ * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load it.  The product (liblgx.so + lgx_kernels.hsaco) never links, loads or
+ * falls back to it.
+ *
+ * Reference status.  The reference (LOGOS workspace 0.10.1) contains no
+ * implementation of any function restated here: it has no CUDA back-end, no
+ * tensor types and no LLM code (searches over the whole tree for cuda, gemv,
+ * qwen, rmsnorm, softmax, fp16 ... find nothing).  The arithmetic therefore
+ * follows the public definitions (GGML Q8_0 block format, Qwen2 decoder
+ * architecture) and the canonical reduction schedules written out below.
+ * What the reference does contribute are conventions, cited where used:
+ *   - SplitMix64 as the portable seeded generator
+ *     (crates/logicaffeine_runtime/src/seed.rs:15-38);
+ *   - "no implicit FMA, no reassociation" in the oracle tier
+ *     (crates/logicaffeine_tests/tests/jit_float_codegen.rs:13-18,
+ *      crates/logicaffeine_forge/src/vectorize.rs:9-12): this file is built
+ *     with -ffp-contract=off and every fused multiply-add is an explicit
+ *     fmaf() at the place the device kernels use one.
+ *
+ * Pinning (what checks each function; see tests/test_oracle.py):
+ *   f32<->f16        exhaustive 2^16 decode vs numpy, RNE encode vs numpy on
+ *                    2^20 random + all boundary values
+ *   expf             |rel err| < 2 ulp vs numpy float64 exp over the domain;
+ *                    exp(0) == 1 exactly; monotone; limits
+ *   generators       SplitMix64 published vectors for seed 0 / 1234567; moments
+ *   quantize_q8_0    closed forms (ramp, absmax -> +-127, zero block),
+ *                    numpy-f64 fixture
+ *   q8 block dots    brute-force int64 numpy (exact)
+ *   q8 gemv f32      one-hot x (exact column), linearity, numpy-f64 fixture
+ *   q8 gemm          per-row equality with the M=1 path (batch invariance),
+ *                    numpy-f64 fixture within 1e-5 rel, one-hot closed form
+ *   repack t16       round trip + explicit index formula on a tiny case
+ */
+#ifndef LGX_ORACLE_H
+#define LGX_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Blocks (of 32) per canonical accumulation range of a Q8 dot product. */
+#define ORC_Q8_RANGE_BLOCKS 32
+
+/* ---- scalar formats ---- */
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
+void orc_f32_to_f16_array(const float* x, uint16_t* h, int64_t n);
+void orc_f16_to_f32_array(const uint16_t* h, float* x, int64_t n);
+float orc_expf(float x);
+float orc_silu(float x);
+void orc_expf_array(const float* x, float* y, int64_t n);
+
+/* ---- seeded generators (SplitMix64 streams) ---- */
+uint64_t orc_stream_base(uint64_t seed, uint64_t stream);
+void orc_gen_u64(uint64_t seed, uint64_t stream, uint64_t* out, int64_t n);
+void orc_splitmix64_seq(uint64_t state, uint64_t* out, int64_t n);
+void orc_gen_i8(uint64_t seed, uint64_t stream, int8_t* out, int64_t n);
+void orc_gen_normal_f32(uint64_t seed, uint64_t stream, double sigma, float* out, int64_t n);
+void orc_gen_normal_f16(uint64_t seed, uint64_t stream, double sigma, uint16_t* out, int64_t n);
+void orc_gen_q8_scales(uint64_t seed, uint64_t stream, uint16_t* out, int64_t n);
+void orc_gen_below_i32(uint64_t seed, uint64_t stream, uint32_t bound, int32_t* out, int64_t n);
+
+/* ---- Q8_0 ---- */
+void orc_quantize_q8_0(const float* x, int64_t m, int32_t k, int8_t* qs, uint16_t* d);
+void orc_q8_repack_t16(const int8_t* qs, int32_t n, int32_t k, int8_t* out);
+void orc_q8_unpack_t16(const int8_t* t16, int32_t n, int32_t k, int8_t* qs);
+void orc_q8_gemv_f32(const int8_t* qs, const uint16_t* d, int32_t n, int32_t k,
+                     const float* x, float* y);
+void orc_q8_blockdots(const int8_t* qs, int32_t n, int32_t k, const int8_t* xq,
+                      int32_t* s);
+void orc_q8_gemm(const int8_t* qs, const uint16_t* d, int32_t n, int32_t k,
+                 const int8_t* xq, const uint16_t* xd, int32_t m, float* y);
+float orc_tree_sum(float* p, int32_t g);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

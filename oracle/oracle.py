@@ -1,0 +1,227 @@
+"""ctypes view of the CPU oracle (liblgx_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
+``bench.py``'s cpu_baseline leg, always as the checker.  The product package
+``logicaffeine_amd`` never imports this module.
+
+The arithmetic lives in ``lgx_oracle.c``; this file only marshals numpy arrays.
+The reference (LOGOS 0.10.1) has no implementation of this path (no GPU
+back-end, no tensor types), so each function is pinned by the checks listed in
+``lgx_oracle.h`` rather than by reference vectors.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liblgx_oracle.so")
+_lib = None
+
+Q8_RANGE_BLOCKS = 32
+
+_P = C.c_void_p
+_I64 = C.c_int64
+_I32 = C.c_int32
+_U64 = C.c_uint64
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc only)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = C.CDLL(_LIB_PATH)
+        sigs = {
+            "orc_f32_to_f16": (C.c_uint16, [C.c_float]),
+            "orc_f16_to_f32": (C.c_float, [C.c_uint16]),
+            "orc_f32_to_f16_array": (None, [_P, _P, _I64]),
+            "orc_f16_to_f32_array": (None, [_P, _P, _I64]),
+            "orc_expf": (C.c_float, [C.c_float]),
+            "orc_silu": (C.c_float, [C.c_float]),
+            "orc_expf_array": (None, [_P, _P, _I64]),
+            "orc_stream_base": (_U64, [_U64, _U64]),
+            "orc_gen_u64": (None, [_U64, _U64, _P, _I64]),
+            "orc_splitmix64_seq": (None, [_U64, _P, _I64]),
+            "orc_gen_i8": (None, [_U64, _U64, _P, _I64]),
+            "orc_gen_normal_f32": (None, [_U64, _U64, C.c_double, _P, _I64]),
+            "orc_gen_normal_f16": (None, [_U64, _U64, C.c_double, _P, _I64]),
+            "orc_gen_q8_scales": (None, [_U64, _U64, _P, _I64]),
+            "orc_gen_below_i32": (None, [_U64, _U64, C.c_uint32, _P, _I64]),
+            "orc_quantize_q8_0": (None, [_P, _I64, _I32, _P, _P]),
+            "orc_q8_repack_t16": (None, [_P, _I32, _I32, _P]),
+            "orc_q8_unpack_t16": (None, [_P, _I32, _I32, _P]),
+            "orc_q8_gemv_f32": (None, [_P, _P, _I32, _I32, _P, _P]),
+            "orc_q8_blockdots": (None, [_P, _I32, _I32, _P, _P]),
+            "orc_q8_gemm": (None, [_P, _P, _I32, _I32, _P, _P, _I32, _P]),
+            "orc_tree_sum": (C.c_float, [_P, _I32]),
+        }
+        for name, (res, args) in sigs.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---- scalar formats -------------------------------------------------------
+
+def f32_to_f16(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_array(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def f16_to_f32(h) -> np.ndarray:
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_f16_to_f32_array(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+def expf(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.float32)
+    lib().orc_expf_array(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def silu(x) -> np.ndarray:
+    x = _c(x, np.float32).ravel()
+    return np.array([lib().orc_silu(float(v)) for v in x], np.float32)
+
+
+def tree_sum(p) -> np.float32:
+    p = _c(p, np.float32).copy()
+    return np.float32(lib().orc_tree_sum(_ptr(p), p.size))
+
+
+# ---- generators -----------------------------------------------------------
+
+def gen_u64(seed: int, stream: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.uint64)
+    lib().orc_gen_u64(seed, stream, _ptr(out), n)
+    return out
+
+
+def splitmix64_seq(state: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.uint64)
+    lib().orc_splitmix64_seq(state, _ptr(out), n)
+    return out
+
+
+def gen_i8(seed: int, stream: int, shape) -> np.ndarray:
+    out = np.empty(shape, np.int8)
+    lib().orc_gen_i8(seed, stream, _ptr(out), out.size)
+    return out
+
+
+def gen_normal_f32(seed: int, stream: int, shape, sigma: float = 1.0) -> np.ndarray:
+    out = np.empty(shape, np.float32)
+    lib().orc_gen_normal_f32(seed, stream, sigma, _ptr(out), out.size)
+    return out
+
+
+def gen_normal_f16(seed: int, stream: int, shape, sigma: float = 1.0) -> np.ndarray:
+    out = np.empty(shape, np.uint16)
+    lib().orc_gen_normal_f16(seed, stream, sigma, _ptr(out), out.size)
+    return out
+
+
+def gen_q8_scales(seed: int, stream: int, shape) -> np.ndarray:
+    out = np.empty(shape, np.uint16)
+    lib().orc_gen_q8_scales(seed, stream, _ptr(out), out.size)
+    return out
+
+
+def gen_below_i32(seed: int, stream: int, bound: int, shape) -> np.ndarray:
+    out = np.empty(shape, np.int32)
+    lib().orc_gen_below_i32(seed, stream, bound, _ptr(out), out.size)
+    return out
+
+
+def gen_q8_matrix(seed: int, stream: int, n: int, k: int):
+    """Config-0 style weights: int8 U[-127,127] and d = |N(0,0.02)|/127 (f16)."""
+    qs = gen_i8(seed, stream, (n, k))
+    d = gen_q8_scales(seed, stream + 1, (n, k // 32))
+    return qs, d
+
+
+# ---- Q8_0 -----------------------------------------------------------------
+
+def quantize_q8_0(x):
+    x = _c(x, np.float32)
+    m, k = x.shape
+    qs = np.empty((m, k), np.int8)
+    d = np.empty((m, k // 32), np.uint16)
+    lib().orc_quantize_q8_0(_ptr(x), m, k, _ptr(qs), _ptr(d))
+    return qs, d
+
+
+def q8_repack_t16(qs):
+    qs = _c(qs, np.int8)
+    n, k = qs.shape
+    out = np.empty(n * k, np.int8)
+    lib().orc_q8_repack_t16(_ptr(qs), n, k, _ptr(out))
+    return out
+
+
+def q8_unpack_t16(t16, n: int, k: int):
+    t16 = _c(t16, np.int8)
+    out = np.empty((n, k), np.int8)
+    lib().orc_q8_unpack_t16(_ptr(t16), n, k, _ptr(out))
+    return out
+
+
+def q8_gemv_f32(qs, d, x):
+    qs = _c(qs, np.int8)
+    d = _c(d, np.uint16)
+    x = _c(x, np.float32)
+    n, k = qs.shape
+    y = np.empty(n, np.float32)
+    lib().orc_q8_gemv_f32(_ptr(qs), _ptr(d), n, k, _ptr(x), _ptr(y))
+    return y
+
+
+def q8_blockdots(qs, xq):
+    qs = _c(qs, np.int8)
+    xq = _c(xq, np.int8)
+    n, k = qs.shape
+    s = np.empty((n, k // 32), np.int32)
+    lib().orc_q8_blockdots(_ptr(qs), n, k, _ptr(xq), _ptr(s))
+    return s
+
+
+def q8_gemm(qs, d, xq, xd):
+    """Y[m][n] with the canonical range/tree schedule."""
+    qs = _c(qs, np.int8)
+    d = _c(d, np.uint16)
+    xq = _c(xq, np.int8)
+    xd = _c(xd, np.uint16)
+    n, k = qs.shape
+    if xq.ndim == 1:
+        xq = xq.reshape(1, k)
+        xd = xd.reshape(1, k // 32)
+    m = xq.shape[0]
+    y = np.empty((m, n), np.float32)
+    lib().orc_q8_gemm(_ptr(qs), _ptr(d), n, k, _ptr(xq), _ptr(xd), m, _ptr(y))
+    return y

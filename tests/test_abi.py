@@ -1,0 +1,86 @@
+"""The C-ABI library loads and exports every symbol include/lgx.h declares;
+error paths that need no device (no compute calls are made here)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lgx.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(lgx_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    import logicaffeine_amd as lgx
+
+    L = lgx.lib()
+    names = declared_functions()
+    assert len(names) >= 14
+    for n in names:
+        assert hasattr(L, n), f"liblgx.so does not export {n}"
+    # the Python mirror binds exactly the declared surface
+    assert sorted(lgx.SIGNATURES) == names
+
+
+def test_abi_version_and_status_values():
+    import logicaffeine_amd as lgx
+
+    src = open(HEADER).read()
+    assert int(re.search(r"LGX_ABI_VERSION (\d+)u", src).group(1)) == lgx.lib().lgx_abi_version()
+    enum = dict((name, int(v)) for name, v in re.findall(r"(LGX_[A-Z_]+) = (\d+)", src))
+    assert {v: k for k, v in enum.items()} == lgx.STATUS_NAMES
+    # LogosStatus values carried over (codegen/ffi.rs:196-209)
+    assert enum["LGX_OK"] == 0 and enum["LGX_NULL_POINTER"] == 3
+    assert enum["LGX_OUT_OF_BOUNDS"] == 4 and enum["LGX_INVALID_HANDLE"] == 6
+    assert enum["LGX_OUT_OF_MEMORY"] == 9
+
+
+def test_invalid_handle_and_null_pointer_paths():
+    import logicaffeine_amd as lgx
+
+    L = lgx.lib()
+    L.lgx_clear_error()
+    assert L.lgx_last_error() is None
+    assert L.lgx_ctx_launch_count(None) == 0
+    assert L.lgx_ctx_arch(None) is None
+    assert L.lgx_ctx_create(0, None, None) == 3
+    assert b"NULL" in L.lgx_last_error()
+    bogus = C.c_void_p(0)
+    assert L.lgx_ctx_destroy(bogus) == 6
+    assert L.lgx_quantize_q8_0(bogus, None, 1, 32, None, None, None) == 6
+    assert L.lgx_q8_gemm(bogus, None, None, None, 1, None, None) == 6
+    assert L.lgx_q8q8_gemv(bogus, None, None, None, None, None, None) == 6
+    assert L.lgx_q8_gemv_f32(bogus, None, None, None, None) == 6
+    assert L.lgx_q8_repack_t16(bogus, None, 16, 64, None, None) == 6
+    assert b"invalid lgx_ctx" in L.lgx_last_error()
+    L.lgx_clear_error()
+    assert L.lgx_last_error() is None
+
+
+def test_ctx_create_without_device_fails_loudly():
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU is present; covered by the gpu tests")
+    import logicaffeine_amd as lgx
+
+    with pytest.raises(lgx.LgxError) as ei:
+        lgx.lib()  # loads
+        h = C.c_void_p()
+        lgx._check(lgx.lib().lgx_ctx_create(0, None, C.byref(h)))
+    assert ei.value.status_name == "LGX_NO_DEVICE"
+
+
+def test_missing_code_object_is_a_load_error(tmp_path):
+    """With a device present a bad path gives LGX_MODULE_LOAD_FAILED; without
+    one the device check comes first.  Either way: an error, no fallback."""
+    import logicaffeine_amd as lgx
+
+    h = C.c_void_p()
+    st = lgx.lib().lgx_ctx_create(0, str(tmp_path / "nope.hsaco").encode(), C.byref(h))
+    assert st in (5, 11)
+    assert h.value is None
