@@ -3,13 +3,19 @@
 Workload: the Qwen2.5-1.5B MLP matmuls, gate and up
 [8960 x 1536] and down [1536 x 8960], all Q8_0, with binary32 activations
 ~N(0,1).  One step = for each of the three matrices: quantise the activation
-rows to Q8_0 and run the Q8 x Q8 product (M = 1: the dot4 GEMV; M > 1: the
-int8-MFMA GEMM).  Weights rotate over enough distinct copies (>= 2 x the
+rows to Q8_0 and run the Q8 x Q8 product (M = 1: the dot4 GEMV with the
+quantisation fused into its prologue; M > 1: quantise kernel + int8-MFMA
+GEMM), plus the range-combine kernel where K spans more than one 32-block
+range.  Weights rotate over enough distinct copies (>= 2 x the
 256 MB Infinity Cache) that every step streams them from HBM.
 
 Headline `value`: algorithmic GB/s of the M = 1 step (weights + scales +
 activations + outputs, each counted once).  `roofline` is the dominant kernel
-(lgx_k_q8q8_gemv) timed per launch with HIP events on its stream.  The M sweep
+(lgx_k_q8_gemv_mfma_qx, the fused-quantise GEMV writing range partials),
+timed per launch by HIP events attached to its own dispatch
+(lgx_ctx_set_kernel_timing) on its stream, in a separate pass over the same
+steps.  Launches are queued behind a device-side sleep before the timed
+region opens, so the step time is the device's, not the Python loop's.  The M sweep
 (1, 8, 32, 64) is reported alongside.  `cpu_baseline` times the CPU oracle
 (a port: the reference has no CPU implementation of this path) on a bounded
 sample of the same step.
@@ -28,6 +34,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+DOMINANT = "lgx_k_q8_gemv_mfma_qx"
 MALL_BYTES = 256 << 20
 SHAPES = (("gate", 8960, 1536), ("up", 8960, 1536), ("down", 1536, 8960))
 
@@ -43,8 +50,10 @@ def step_bytes(m):
 
 
 def gemv_launch_bytes(n, k):
-    """Algorithmic bytes of one lgx_k_q8q8_gemv launch: W + Q8 x + fp32 y."""
-    return q8_weight_bytes(n, k) + k + 2 * (k // 32) + 4 * n
+    """Algorithmic bytes of one lgx_k_q8_gemv_mfma_qx launch: W + fp32 x +
+    one fp32 range partial per row and range (= y with a single range)."""
+    nr = -(-(k // 32) // 32)
+    return q8_weight_bytes(n, k) + 4 * k + 4 * n * nr
 
 
 def build_sets(ctx, torch, nsets, seed=1):
@@ -66,21 +75,16 @@ def build_sets(ctx, torch, nsets, seed=1):
     return sets
 
 
-def run_step(ctx, sets, i, acts, m, ev=None):
+def run_step(ctx, sets, i, acts, m):
     W = sets[i % len(sets)]
     for name, n, k in SHAPES:
-        x, xq, xd, y = acts[name]
-        ctx.quantize_q8_0(x, xq, xd)
+        x, xq, xd, y, part = acts[name]
         if m == 1:
-            if ev is not None:
-                ev[0].record()
-            ctx.q8q8_gemv(W[name], xq[0], xd[0], y=y[0])
-            if ev is not None:
-                ev[1].record()
-                ev[2].append((ev[0], ev[1]))
-                ev[0] = ctx.torch.cuda.Event(enable_timing=True)
-                ev[1] = ctx.torch.cuda.Event(enable_timing=True)
+            ctx.q8q8_gemv_quantize_partials(W[name], x[0], part=part)
+            if part.dim() == 2:
+                ctx.range_combine(part, y=y[0])
         else:
+            ctx.quantize_q8_0(x, xq, xd)
             ctx.q8_gemm(W[name], xq, xd, y=y)
 
 
@@ -93,8 +97,29 @@ def make_acts(ctx, torch, m):
         xq = torch.empty((m, k), dtype=torch.int8, device=ctx.dev)
         xd = torch.empty((m, k // 32), dtype=torch.int16, device=ctx.dev)
         y = torch.empty((m, n), dtype=torch.float32, device=ctx.dev)
-        acts[name] = (x, xq, xd, y)
+        nr = -(-(k // 32) // 32)
+        part = torch.empty((nr, n), dtype=torch.float32, device=ctx.dev)
+        acts[name] = (x, xq, xd, y, part if nr > 1 else y[0])
     return acts
+
+
+_SLEEP_CYCLES_PER_MS = None
+
+
+def queue_ahead(torch, ms):
+    """Occupy the stream with a device-side spin of about `ms` so that the
+    launches queued behind it run back to back."""
+    global _SLEEP_CYCLES_PER_MS
+    if _SLEEP_CYCLES_PER_MS is None:
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        torch.cuda._sleep(10_000_000)
+        e1.record()
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_MS = 10_000_000 / max(e0.elapsed_time(e1), 1e-3)
+    torch.cuda._sleep(int(ms * _SLEEP_CYCLES_PER_MS))
 
 
 def time_m(ctx, torch, sets, m, steps, warmup, per_launch=False):
@@ -102,22 +127,28 @@ def time_m(ctx, torch, sets, m, steps, warmup, per_launch=False):
     for i in range(warmup):
         run_step(ctx, sets, i, acts, m)
     torch.cuda.synchronize()
-    ev = None
-    if per_launch:
-        ev = [torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True), []]
+    # host time to enqueue one step, to size the device-side queue-ahead
+    t = time.perf_counter()
+    run_step(ctx, sets, 0, acts, m)
+    host_ms = (time.perf_counter() - t) * 1e3
+    torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    if per_launch:
+        ctx.kernel_timing(True)
+    queue_ahead(torch, 2.0 * host_ms * steps + 5.0)
     t0.record()
     for i in range(steps):
-        run_step(ctx, sets, warmup + i, acts, m, ev)
+        run_step(ctx, sets, warmup + i, acts, m)
     t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
     gemv_ms = None
-    if ev is not None:
-        d = [a.elapsed_time(b) for a, b in ev[2]]
-        gemv_ms = sum(d) / len(d)
+    if per_launch:
+        ctx.kernel_timing(False)
+        n, tot = ctx.kernel_stats(DOMINANT)
+        gemv_ms = tot / max(n, 1)
     return ms, gemv_ms
 
 
@@ -211,7 +242,7 @@ def main():
         "data": "synthetic (int8 U[-127,127], d=|N(0,0.02)|/127 f16, x~N(0,1) f32)",
         "config": {
             "workload": "config1 Qwen2.5-1.5B MLP Q8_0 gate/up [8960x1536] + down [1536x8960], "
-                        "M=1 (quantise + Q8xQ8 GEMV per matrix)",
+                        "M=1 (fused quantise + Q8xQ8 GEMV per matrix, + range combine)",
             "rotating_weight_sets": nsets,
             "working_set_MB": round(nsets * set_bytes / 1e6, 1),
             "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
@@ -219,7 +250,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "lgx_k_q8q8_gemv",
+            "kernel": DOMINANT,
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -25,16 +25,17 @@
  *
  * Memory.  Every tensor argument is a device pointer owned by the caller; the
  * library never frees caller memory.  A ctx owns only its module and a
- * scratch workspace for range partials (grown on demand).  Calls are
+ * scratch workspace for range partials (grown on demand; with more than one
+ * 32-block range a product is two launches, the second applying the tree).  Calls are
  * asynchronous on `stream` (a hipStream_t; NULL = the null stream); argument
  * errors are reported synchronously, kernel faults at the caller's next
  * synchronisation.  Calls that share one ctx must be ordered on one stream
  * (they share the workspace); use one ctx per concurrent stream.
  *
  * Q8_0 matrices.  W is [n][k] with k % 32 == 0: int8 quants and one binary16
- * scale per 32-block (d[n][k/32], raw IEEE half bits).  The device kernels read
- * the quants in the T16 tile order (see lgx_q8_repack_t16); n % 16 == 0 and
- * k % 64 == 0, k <= 32768.
+ * scale per 32-block (raw IEEE half bits).  The device kernels read the quants
+ * in the T16 tile order and the scales in the S16 tile order (see
+ * lgx_q8_repack_t16); n % 16 == 0 and k % 64 == 0, k <= 32768.
  *
  * Canonical arithmetic.  y[m][n] of the Q8 x Q8 products is
  *   s_b = sum_{i<32} qw[n][32b+i] * qx[m][32b+i]                (int32)
@@ -81,7 +82,7 @@ typedef struct lgx_ctx lgx_ctx;
 
 typedef struct lgx_q8_matrix {
     const int8_t* qs;     /* quants in `layout` order */
-    const uint16_t* d;    /* [n][k/32] binary16 scales, row-major */
+    const uint16_t* d;    /* binary16 scales: row-major [n][k/32], or S16 with LGX_Q8_T16 */
     int32_t n, k;
     int32_t layout;       /* the kernels require LGX_Q8_T16 */
 } lgx_q8_matrix;
@@ -101,15 +102,28 @@ lgx_status lgx_ctx_destroy(lgx_ctx* ctx);
 uint64_t lgx_ctx_launch_count(const lgx_ctx* ctx);
 /* Name of the loaded code object's target (e.g. "gfx950"). */
 const char* lgx_ctx_arch(const lgx_ctx* ctx);
+/* Per-kernel device timing.  While enabled, every launch through ctx carries
+ * start/stop events on its own dispatch (hipExtModuleLaunchKernel), so the
+ * times are kernel execution only.  Enabling starts a fresh window.
+ * lgx_ctx_kernel_stats waits for the window's launches of `kernel_name` and
+ * returns their number and summed milliseconds. */
+lgx_status lgx_ctx_set_kernel_timing(lgx_ctx* ctx, int32_t enable);
+lgx_status lgx_ctx_kernel_stats(lgx_ctx* ctx, const char* kernel_name, uint64_t* count,
+                                double* total_ms);
 
 /* ---- Q8_0 layout ---- */
-/* Row-major quants [n][k] -> T16.  Unit u = (row/16)*(k/64) + k/64-pair p holds
- * 1 KiB; lane l = (row%16) + 16*c owns bytes [l*16, l*16+16): k = 64p+8c+j
- * (j < 8) then k = 64p+32+8c+j. */
-lgx_status lgx_q8_repack_t16(lgx_ctx* ctx, const int8_t* qs_rowmajor, int32_t n, int32_t k,
-                             int8_t* qs_t16, void* stream);
-lgx_status lgx_q8_unpack_t16(lgx_ctx* ctx, const int8_t* qs_t16, int32_t n, int32_t k,
-                             int8_t* qs_rowmajor, void* stream);
+/* Row-major quants [n][k] and scales [n][k/32] -> the device layouts.
+ * Quants, T16: unit u = (row/16)*(k/64) + k/64-pair p holds 1 KiB; lane
+ * l = (row%16) + 16*c owns bytes [l*16, l*16+16): k = 64p+8c+j (j < 8) then
+ * k = 64p+32+8c+j.  Scales, S16: element
+ * ((row/16 * nhalf + b/16) * 16 + row%16) * 16 + b%16 holds the scale of
+ * block b (zero past k/32), nhalf = ceil(k/512); lgx_q8_scale_count()
+ * elements.  The unpack calls invert both. */
+size_t lgx_q8_scale_count(int32_t n, int32_t k);
+lgx_status lgx_q8_repack_t16(lgx_ctx* ctx, const int8_t* qs_rowmajor, const uint16_t* d_rowmajor,
+                             int32_t n, int32_t k, int8_t* qs_t16, uint16_t* d_s16, void* stream);
+lgx_status lgx_q8_unpack_t16(lgx_ctx* ctx, const int8_t* qs_t16, const uint16_t* d_s16, int32_t n,
+                             int32_t k, int8_t* qs_rowmajor, uint16_t* d_rowmajor, void* stream);
 
 /* ---- Q8_0 activation quantisation (GGML reference rule) ----
  * x[m][k] binary32 -> qs[m][k] int8, d[m][k/32] binary16:
@@ -126,10 +140,30 @@ lgx_status lgx_q8_gemv_f32(lgx_ctx* ctx, const lgx_q8_matrix* W, const float* x,
  * dbg_blockdots (nullable): receives the int32 block dots s[n][k/32]. */
 lgx_status lgx_q8q8_gemv(lgx_ctx* ctx, const lgx_q8_matrix* W, const int8_t* xq,
                          const uint16_t* xd, float* y, int32_t* dbg_blockdots, void* stream);
+/* y[n] = W Q8_0(x) for a binary32 x[k]: the Q8_0 quantisation of x (bit-
+ * identical to lgx_quantize_q8_0) is fused into the GEMV prologue, then the
+ * canonical Q8 x Q8 schedule.  xq_out / xd_out (nullable) receive Q8_0(x). */
+lgx_status lgx_q8q8_gemv_quantize(lgx_ctx* ctx, const lgx_q8_matrix* W, const float* x, float* y,
+                                  int8_t* xq_out, uint16_t* xd_out, void* stream);
 /* Y[m][n] = Xq W^T for m Q8_0 activation rows (Xq[m][k], Xd[m][k/32]), int8
  * MFMA; canonical schedule, so row i equals lgx_q8q8_gemv of row i. */
 lgx_status lgx_q8_gemm(lgx_ctx* ctx, const lgx_q8_matrix* W, const int8_t* xq,
                        const uint16_t* xd, int32_t m, float* y, void* stream);
+
+/* ---- range partials (for consumers that fuse the range tree) ---- */
+/* Number of canonical 32-block ranges of K = the partial count of a product. */
+int32_t lgx_q8_range_count(int32_t k);
+/* part[r][n] = the canonical chain of range r of W Q8_0(x), r < range count
+ * (with one range, part is y).  Same quantisation outputs as above. */
+lgx_status lgx_q8q8_gemv_quantize_partials(lgx_ctx* ctx, const lgx_q8_matrix* W, const float* x,
+                                           float* part, int8_t* xq_out, uint16_t* xd_out,
+                                           void* stream);
+/* part[r][m][n] for m activation rows (M = 1 uses the GEMV kernel). */
+lgx_status lgx_q8_gemm_partials(lgx_ctx* ctx, const lgx_q8_matrix* W, const int8_t* xq,
+                                const uint16_t* xd, int32_t m, float* part, void* stream);
+/* y[i] = pairwise tree over part[0..nranges)[i], i < count. */
+lgx_status lgx_q8_range_combine(lgx_ctx* ctx, const float* part, int32_t nranges, int64_t count,
+                                float* y, void* stream);
 
 #ifdef __cplusplus
 }

@@ -44,12 +44,21 @@ SIGNATURES = {
     "lgx_ctx_destroy": (C.c_int, [_P]),
     "lgx_ctx_launch_count": (C.c_uint64, [_P]),
     "lgx_ctx_arch": (C.c_char_p, [_P]),
-    "lgx_q8_repack_t16": (C.c_int, [_P, _P, _I32, _I32, _P, _P]),
-    "lgx_q8_unpack_t16": (C.c_int, [_P, _P, _I32, _I32, _P, _P]),
+    "lgx_ctx_set_kernel_timing": (C.c_int, [_P, _I32]),
+    "lgx_ctx_kernel_stats": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_uint64),
+                                       C.POINTER(C.c_double)]),
+    "lgx_q8_scale_count": (C.c_size_t, [_I32, _I32]),
+    "lgx_q8_repack_t16": (C.c_int, [_P, _P, _P, _I32, _I32, _P, _P, _P]),
+    "lgx_q8_unpack_t16": (C.c_int, [_P, _P, _P, _I32, _I32, _P, _P, _P]),
     "lgx_quantize_q8_0": (C.c_int, [_P, _P, _I32, _I32, _P, _P, _P]),
     "lgx_q8_gemv_f32": (C.c_int, [_P, _P, _P, _P, _P]),
     "lgx_q8q8_gemv": (C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     "lgx_q8_gemm": (C.c_int, [_P, _P, _P, _P, _I32, _P, _P]),
+    "lgx_q8q8_gemv_quantize": (C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
+    "lgx_q8_range_count": (_I32, [_I32]),
+    "lgx_q8q8_gemv_quantize_partials": (C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
+    "lgx_q8_gemm_partials": (C.c_int, [_P, _P, _P, _P, _I32, _P, _P]),
+    "lgx_q8_range_combine": (C.c_int, [_P, _P, _I32, C.c_int64, _P, _P]),
 }
 
 
@@ -94,10 +103,11 @@ def _stream(torch, device):
 
 
 class Q8Matrix:
-    """A Q8_0 weight matrix resident on the device in T16 order.
+    """A Q8_0 weight matrix resident on the device in the tile layouts.
 
     ``qs`` is an int8 device tensor (T16 order, n*k bytes); ``d`` an int16
-    device tensor holding the binary16 scale bits, shape [n, k/32]."""
+    device tensor holding the binary16 scale bits in S16 order
+    (lgx_q8_scale_count(n, k) elements)."""
 
     def __init__(self, qs, d, n: int, k: int):
         self.qs, self.d, self.n, self.k = qs, d, n, k
@@ -147,19 +157,35 @@ class Context:
     def _s(self):
         return _stream(self.torch, self.dev)
 
-    # ---- layout ----------------------------------------------------------
-    def repack_t16(self, qs_rowmajor):
-        n, k = qs_rowmajor.shape
-        out = self.torch.empty(n * k, dtype=self.torch.int8, device=self.dev)
-        _check(lib().lgx_q8_repack_t16(self.handle, qs_rowmajor.data_ptr(), n, k,
-                                       out.data_ptr(), self._s()))
-        return out
+    def kernel_timing(self, enable: bool) -> None:
+        """Time every launch by its own dispatch (fresh window when enabled)."""
+        _check(lib().lgx_ctx_set_kernel_timing(self.handle, 1 if enable else 0))
 
-    def unpack_t16(self, qs_t16, n: int, k: int):
-        out = self.torch.empty((n, k), dtype=self.torch.int8, device=self.dev)
-        _check(lib().lgx_q8_unpack_t16(self.handle, qs_t16.data_ptr(), n, k,
-                                       out.data_ptr(), self._s()))
-        return out
+    def kernel_stats(self, kernel_name: str):
+        """(launch count, total ms) of `kernel_name` in the timing window."""
+        n, ms = C.c_uint64(), C.c_double()
+        _check(lib().lgx_ctx_kernel_stats(self.handle, kernel_name.encode(), C.byref(n),
+                                          C.byref(ms)))
+        return int(n.value), float(ms.value)
+
+    # ---- layout ----------------------------------------------------------
+    def repack_t16(self, qs_rowmajor, d_rowmajor):
+        """Row-major quants [n][k] + scales [n][k/32] -> (T16 quants, S16 scales)."""
+        t = self.torch
+        n, k = qs_rowmajor.shape
+        out = t.empty(n * k, dtype=t.int8, device=self.dev)
+        dout = t.empty(max(1, lib().lgx_q8_scale_count(n, k)), dtype=t.int16, device=self.dev)
+        _check(lib().lgx_q8_repack_t16(self.handle, qs_rowmajor.data_ptr(), d_rowmajor.data_ptr(),
+                                       n, k, out.data_ptr(), dout.data_ptr(), self._s()))
+        return out, dout
+
+    def unpack_t16(self, qs_t16, d_s16, n: int, k: int):
+        t = self.torch
+        out = t.empty((n, k), dtype=t.int8, device=self.dev)
+        dout = t.empty((n, k // 32), dtype=t.int16, device=self.dev)
+        _check(lib().lgx_q8_unpack_t16(self.handle, qs_t16.data_ptr(), d_s16.data_ptr(), n, k,
+                                       out.data_ptr(), dout.data_ptr(), self._s()))
+        return out, dout
 
     def to_device(self, a, dtype=None):
         """numpy array or tensor -> contiguous device tensor (uint16 data is
@@ -184,7 +210,8 @@ class Context:
         qs = self.to_device(qs_rowmajor, t.int8)
         dd = self.to_device(d, t.int16)
         n, k = qs.shape
-        return Q8Matrix(self.repack_t16(qs), dd, n, k)
+        qt, ds = self.repack_t16(qs, dd)
+        return Q8Matrix(qt, ds, n, k)
 
     # ---- Q8_0 ------------------------------------------------------------
     def quantize_q8_0(self, x, qs=None, d=None):
@@ -210,6 +237,42 @@ class Context:
                                    y.data_ptr(), dbg.data_ptr() if dbg is not None else None,
                                    self._s()))
         return (y, dbg) if blockdots else y
+
+    def q8q8_gemv_quantize(self, W: Q8Matrix, x, y=None, xq_out=None, xd_out=None):
+        """y = W Q8_0(x) with the quantisation fused into the GEMV."""
+        t = self.torch
+        y = t.empty(W.n, dtype=t.float32, device=self.dev) if y is None else y
+        _check(lib().lgx_q8q8_gemv_quantize(
+            self.handle, W.cstruct, x.data_ptr(), y.data_ptr(),
+            xq_out.data_ptr() if xq_out is not None else None,
+            xd_out.data_ptr() if xd_out is not None else None, self._s()))
+        return y
+
+    def q8q8_gemv_quantize_partials(self, W: Q8Matrix, x, part=None):
+        t = self.torch
+        g = lib().lgx_q8_range_count(W.k)
+        part = t.empty((g, W.n), dtype=t.float32, device=self.dev) if part is None else part
+        _check(lib().lgx_q8q8_gemv_quantize_partials(self.handle, W.cstruct, x.data_ptr(),
+                                                     part.data_ptr(), None, None, self._s()))
+        return part
+
+    def q8_gemm_partials(self, W: Q8Matrix, xq, xd, part=None):
+        t = self.torch
+        m = xq.shape[0] if xq.dim() == 2 else 1
+        g = lib().lgx_q8_range_count(W.k)
+        part = t.empty((g, m, W.n), dtype=t.float32, device=self.dev) if part is None else part
+        _check(lib().lgx_q8_gemm_partials(self.handle, W.cstruct, xq.data_ptr(), xd.data_ptr(), m,
+                                          part.data_ptr(), self._s()))
+        return part
+
+    def range_combine(self, part, y=None):
+        t = self.torch
+        g = part.shape[0]
+        count = part[0].numel()
+        y = t.empty(part.shape[1:], dtype=t.float32, device=self.dev) if y is None else y
+        _check(lib().lgx_q8_range_combine(self.handle, part.data_ptr(), g, count, y.data_ptr(),
+                                          self._s()))
+        return y
 
     def q8_gemm(self, W: Q8Matrix, xq, xd, y=None):
         t = self.torch

@@ -25,7 +25,7 @@ LIB = os.path.join(HERE, "liblgx.so")
 # says.  Correctly rounded binary32 division and square root.  Packed-FP32
 # instructions disabled (v_pk_*_f32 are never generated).
 HIP_FLAGS = [
-    "--genco", f"--offload-arch={ARCH}", "-O3", "-std=c++17",
+    "--genco", "--no-gpu-bundle-output", f"--offload-arch={ARCH}", "-O3", "-std=c++17",
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]

@@ -17,6 +17,13 @@ typedef struct {
 } lgx_repack_args;
 
 typedef struct {
+    const uint16_t* src;
+    uint16_t* dst;
+    int32_t n, k;
+    int32_t to_s16;  // 1: row-major [n][k/32] -> S16, 0: S16 -> row-major
+} lgx_srepack_args;
+
+typedef struct {
     const float* x;   // [m][k]
     int8_t* qs;       // [m][k]
     uint16_t* d;      // [m][k/32]
@@ -26,14 +33,25 @@ typedef struct {
 // One wave per (row tile of 16, range of 32 blocks[, m-group of 64 rows]).
 typedef struct {
     const int8_t* wt;     // T16 weights
-    const uint16_t* wd;   // [n][nb] f16 scales
+    const uint16_t* wd;   // S16 f16 scales
     const float* xf;      // gemv_f32: x [k]
     const int8_t* xq;     // q8 paths: [m][k]
     const uint16_t* xd;   // q8 paths: [m][nb]
     float* y;             // [m][n] when nranges == 1
     float* part;          // [nranges][m][n] when nranges > 1
-    int32_t* counter;     // [ntiles][nmgroups] arrival counters (zero between calls)
     int32_t* dbg;         // nullable: [n][nb] int32 block dots (gemv only)
+    int8_t* xq_out;       // fused-quantise GEMV: nullable copy of Q8_0(x) quants
+    uint16_t* xd_out;     // fused-quantise GEMV: nullable copy of Q8_0(x) scales
     int32_t n, k, m;
     int32_t ntiles, nranges, nmgroups;
+    int32_t tpw;          // streaming kernels: row tiles per wave (per workgroup for
+                          // the whole-K GEMV)
 } lgx_gemv_args;
+
+// Canonical tree over range partials: y[i] = tree(part[0][i], ..., part[g-1][i]).
+typedef struct {
+    const float* part;    // [nranges][count]
+    float* y;             // [count]
+    int64_t count;
+    int32_t nranges;
+} lgx_combine_args;

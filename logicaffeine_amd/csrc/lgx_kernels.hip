@@ -131,24 +131,67 @@ __device__ __forceinline__ float tree_sum(float (&p)[LGX_MAX_RANGES], int g) {
     return p[0];
 }
 
-// Cross-workgroup arrival for the range partials of one output slot: release
-// this wave's partial stores, count the arrival; the wave that arrives last
-// (whichever it is) acquires and runs the tree, so the result does not
-// depend on arrival order.  The counter is reset by that wave.
-__device__ __forceinline__ bool last_arrival(int32_t* counter, int slot, int nranges, int lane) {
-    __threadfence();
-    int old = 0;
-    if (lane == 0) old = atomicAdd(counter + slot, 1);
-    old = __shfl(old, 0, 64);
-    if (old != nranges - 1) return false;
-    __threadfence();
-    return true;
+// Exact int32 sum of the four k-chunk partials of two blocks.  Lane l = r+16c
+// holds s0 (block 2p) and s1 (block 2p+1) for its chunk c.  Two VALU lane
+// swaps (v_permlane32_swap, v_permlane16_swap) reduce over c; a third brings
+// the block-(2p+1) total next to the block-2p total, so that on return lanes
+// 0..15 (c = 0) hold both totals of row r.  Each step adds the two results
+// of a swap, which makes it independent of which result is which.
+__device__ __forceinline__ void reduce_chunks(int& s0, int& s1) {
+    const auto a = __builtin_amdgcn_permlane32_swap(s0, s1, false, false);
+    const int t = (int)a[0] + (int)a[1];      // lanes 0-31: s0(c)+s0(c+2); 32-63: s1(c-2)+s1(c)
+    const auto b = __builtin_amdgcn_permlane16_swap(t, t, false, false);
+    const int u = (int)b[0] + (int)b[1];      // lanes 0-31: total s0; lanes 32-63: total s1
+    const auto e = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    s0 = u;                                   // valid in lanes 0-31
+    s1 = ((int)e[0] + (int)e[1]) - u;         // lanes 0-31: (s0 + s1) - s0
+}
+
+__device__ __forceinline__ float reduce_chunks_f(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float t = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(t), __float_as_uint(t), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // ---------------------------------------------------------------------------
-// Shared pieces of the GEMV/GEMM kernels.
-//   grid.x = groups of 4 row tiles (one wave each), grid.y = range g,
-//   grid.z = m-group (GEMM only).  A range is 32 blocks = 16 T16 units.
+// Scale tile layout S16: the scales of row tile t and half-range u (16
+// blocks) are 16 rows x 16 binary16, contiguous and row-major, so the 32
+// bytes a lane needs for one half-range are two 16-byte loads and the 64
+// lanes of a wave touch 512 contiguous bytes.  nhalf = ceil(k/512).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int s16_nhalf(int k) { return (k + 511) >> 9; }
+
+__device__ __forceinline__ void load_scales_half(const uint16_t* wd, int t, int u, int nh, int r,
+                                                 uint32_t (&dw)[8]) {
+    const uint4* p = (const uint4*)(wd + (((int64_t)t * nh + u) * 16 + r) * 16);
+    const uint4 lo = p[0], hi = p[1];
+    dw[0] = lo.x; dw[1] = lo.y; dw[2] = lo.z; dw[3] = lo.w;
+    dw[4] = hi.x; dw[5] = hi.y; dw[6] = hi.z; dw[7] = hi.w;
+}
+
+extern "C" __global__ __launch_bounds__(256) void lgx_k_repack_s16(const lgx_srepack_args a) {
+    const int nb = a.k >> 5, nh = s16_nhalf(a.k);
+    const int64_t total = (int64_t)(a.n >> 4) * nh * 256;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int j = (int)(i & 15), r = (int)((i >> 4) & 15);
+    const int64_t tu = i >> 8;
+    const int64_t t = tu / nh;
+    const int u = (int)(tu - t * nh);
+    const int b = u * 16 + j;
+    const int64_t row = t * 16 + r;
+    if (a.to_s16)
+        a.dst[i] = b < nb ? a.src[row * nb + b] : (uint16_t)0;
+    else if (b < nb)
+        a.dst[row * nb + b] = a.src[i];
+}
+
+// ---------------------------------------------------------------------------
+// Ranges: a range is 32 blocks = 16 T16 units = two half-ranges.  Loops run
+// over all 16 units with the address clamped to the last valid unit and the
+// contribution of units past the range end forced to zero, so the body is
+// branch-free and loads overlap the arithmetic.
 // ---------------------------------------------------------------------------
 struct RangeInfo {
     int g, p0, npairs, b0, nbr;
@@ -165,104 +208,137 @@ __device__ __forceinline__ RangeInfo range_info(int g, int k) {
     return ri;
 }
 
-// End of a GEMV wave (m = 1): one range partial per row in the c == 0 lanes.
-__device__ __forceinline__ void finish_gemv(const lgx_gemv_args& a, int g, int t, int row, int c,
-                                            int lane, float acc) {
-    if (a.nranges == 1) {
-        if (c == 0) a.y[row] = acc;
-        return;
-    }
-    if (c == 0) a.part[(int64_t)g * a.n + row] = acc;
-    if (!last_arrival(a.counter, t, a.nranges, lane)) return;
-    if (c == 0) {
-        float p[LGX_MAX_RANGES];
+// Q8_0 quantisation of activation blocks [blo, bhi) of row x into LDS in the
+// T16 activation order: slot (p*4 + c) holds the 8 bytes of chunk c of block
+// 2p, then of block 2p+1 (slots numbered from block blo).  Eight threads per
+// block, four values each; the arithmetic is lgx_k_quantize_q8_0's, so quants
+// and scales are the same.  Threads of one block iterate together.
+__device__ __forceinline__ void quantize_blocks_to_lds(const lgx_gemv_args& a, int blo, int bhi,
+                                                       int8_t* xs, float* dxs, bool emit) {
+    const int j = threadIdx.x & 7;
+    for (int bl = (int)(threadIdx.x >> 3); bl < bhi - blo; bl += (int)(blockDim.x >> 3)) {
+        const int b = blo + bl;
+        const float4 v = *(const float4*)(a.xf + (int64_t)b * 32 + 4 * j);
+        float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        am = fmaxf(am, shfl_xor_f(am, 1));
+        am = fmaxf(am, shfl_xor_f(am, 2));
+        am = fmaxf(am, shfl_xor_f(am, 4));
+        const float d = am / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const float f[4] = {v.x, v.y, v.z, v.w};
+        uint32_t qw = 0;
 #pragma unroll
-        for (int j = 0; j < LGX_MAX_RANGES; ++j)
-            p[j] = j < a.nranges ? a.part[(int64_t)j * a.n + row] : 0.0f;
-        a.y[row] = tree_sum(p, a.nranges);
+        for (int e = 0; e < 4; ++e) {
+            float q = roundf(f[e] * id);
+            q = fminf(fmaxf(q, -127.0f), 127.0f);
+            qw |= ((uint32_t)(int32_t)q & 0xffu) << (8 * e);
+        }
+        const int p = bl >> 1, hi = bl & 1, c = j >> 1;
+        *(uint32_t*)(xs + (p * 4 + c) * 16 + hi * 8 + 4 * (j & 1)) = qw;
+        const uint16_t dh = f2h(d);
+        if (j == 0) dxs[bl] = h2f(dh);
+        if (emit) {
+            if (a.xq_out) *(uint32_t*)(a.xq_out + (int64_t)b * 32 + 4 * j) = qw;
+            if (a.xd_out && j == 0) a.xd_out[b] = dh;
+        }
     }
-    if (lane == 0) a.counter[t] = 0;
+}
+
+// Stage pairs [plo, phi) of a pre-quantised activation row into LDS (T16
+// order) and the scales of their blocks as binary32.
+__device__ __forceinline__ void stage_pairs_q8(const lgx_gemv_args& a, int plo, int phi, int8_t* xs,
+                                               float* dxs) {
+    for (int s = threadIdx.x; s < 4 * (phi - plo); s += blockDim.x) {
+        const int8_t* src = a.xq + (plo + (s >> 2)) * 64 + 8 * (s & 3);
+        const uint2 lo = *(const uint2*)src;
+        const uint2 hi = *(const uint2*)(src + 32);
+        *(uint4*)(xs + s * 16) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+    for (int b = threadIdx.x; b < 2 * (phi - plo); b += blockDim.x) dxs[b] = h2f(a.xd[2 * plo + b]);
 }
 
 // ---------------------------------------------------------------------------
-// Q8 x Q8 GEMV (M = 1), v_dot4_i32_i8 + cross-lane reduction.
-// Each lane holds 8 int8 of block 2p and 8 of block 2p+1 (its k-chunk c) of
-// row r; the four k-chunks of a block are summed with two xor-shuffles (exact
-// int32), then the range accumulator runs the canonical fmaf chain.
+// Q8 x Q8 GEMV (M = 1) on v_dot4_i32_i8, one wave per (row tile, range):
+// 128-bit streaming loads of T16 units, dot4 on each lane's 8-byte chunks,
+// exact cross-lane chunk sums (reduce_chunks), then the canonical fmaf chain
+// of the range.  Also the only kernel that can emit the int32 block dots.
 // ---------------------------------------------------------------------------
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8q8_gemv(const lgx_gemv_args a) {
     __shared__ __align__(16) int8_t xs[LGX_Q8_RANGE_BLOCKS * 32];
-    __shared__ float dxs[LGX_Q8_RANGE_BLOCKS];
+    __shared__ __align__(16) float dxs[LGX_Q8_RANGE_BLOCKS];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const RangeInfo ri = range_info(blockIdx.y, a.k);
-    const int nb = a.k >> 5;
-    {
-        const int off = ri.b0 * 32 + 4 * threadIdx.x;
-        int v = 0;
-        if (4 * (int)threadIdx.x < ri.nbr * 32) v = *(const int*)(a.xq + off);
-        *(int*)(xs + 4 * threadIdx.x) = v;
-        if (threadIdx.x < LGX_Q8_RANGE_BLOCKS)
-            dxs[threadIdx.x] = threadIdx.x < (unsigned)ri.nbr ? h2f(a.xd[ri.b0 + threadIdx.x]) : 0.0f;
-    }
+    const int nb = a.k >> 5, nh = s16_nhalf(a.k);
+    stage_pairs_q8(a, ri.p0, ri.p0 + ri.npairs, xs, dxs);
     __syncthreads();
     const int t = blockIdx.x * 4 + wave;
     if (t >= a.ntiles) return;
     const int r = lane & 15, c = lane >> 4;
     const int row = t * 16 + r;
     const int np = a.k >> 6;
+    const int last = ri.npairs - 1;
     const uint4* wp = (const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64 + lane;
-    const uint32_t* dwp = (const uint32_t*)(a.wd + (int64_t)row * nb + ri.b0);
     uint4 w[16];
     uint32_t dw[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        if (i < ri.npairs) {
-            w[i] = ld_stream(wp + i * 64);
-            dw[i] = dwp[i];
+    for (int i = 0; i < 16; ++i) w[i] = ld_stream(wp + min(i, last) * 64);
+    {
+        uint32_t d0[8], d1[8];
+        load_scales_half(a.wd, t, 2 * ri.g, nh, r, d0);
+        load_scales_half(a.wd, t, min(2 * ri.g + 1, nh - 1), nh, r, d1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            dw[i] = d0[i];
+            dw[8 + i] = d1[i];
         }
     }
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        if (i < ri.npairs) {
-            const int2 xa = *(const int2*)(xs + (2 * i) * 32 + 8 * c);
-            const int2 xb = *(const int2*)(xs + (2 * i + 1) * 32 + 8 * c);
-            int s0 = __builtin_amdgcn_sdot4((int)w[i].x, xa.x, 0, false);
-            s0 = __builtin_amdgcn_sdot4((int)w[i].y, xa.y, s0, false);
-            int s1 = __builtin_amdgcn_sdot4((int)w[i].z, xb.x, 0, false);
-            s1 = __builtin_amdgcn_sdot4((int)w[i].w, xb.y, s1, false);
-            s0 += shfl_xor_i(s0, 16);
-            s1 += shfl_xor_i(s1, 16);
-            s0 += shfl_xor_i(s0, 32);
-            s1 += shfl_xor_i(s1, 32);
-            const float d0 = h2f(dw[i] & 0xffffu) * dxs[2 * i];
-            const float d1 = h2f(dw[i] >> 16) * dxs[2 * i + 1];
-            acc = fmaf((float)s0, d0, acc);
-            acc = fmaf((float)s1, d1, acc);
-            if (a.dbg != nullptr && c == 0) {
-                a.dbg[(int64_t)row * nb + ri.b0 + 2 * i] = s0;
-                a.dbg[(int64_t)row * nb + ri.b0 + 2 * i + 1] = s1;
-            }
+        const int ic = min(i, last);
+        const int4 xv = *(const int4*)(xs + (ic * 4 + c) * 16);
+        int s0 = __builtin_amdgcn_sdot4((int)w[i].x, xv.x, 0, false);
+        s0 = __builtin_amdgcn_sdot4((int)w[i].y, xv.y, s0, false);
+        int s1 = __builtin_amdgcn_sdot4((int)w[i].z, xv.z, 0, false);
+        s1 = __builtin_amdgcn_sdot4((int)w[i].w, xv.w, s1, false);
+        reduce_chunks(s0, s1);
+        const bool on = i <= last;
+        const float d0 = on ? h2f(dw[i] & 0xffffu) * dxs[2 * ic] : 0.0f;
+        const float d1 = on ? h2f(dw[i] >> 16) * dxs[2 * ic + 1] : 0.0f;
+        acc = fmaf((float)s0, d0, acc);
+        acc = fmaf((float)s1, d1, acc);
+        if (a.dbg != nullptr && on && c == 0) {
+            a.dbg[(int64_t)row * nb + ri.b0 + 2 * i] = s0;
+            a.dbg[(int64_t)row * nb + ri.b0 + 2 * i + 1] = s1;
         }
     }
-    finish_gemv(a, ri.g, t, row, c, lane, acc);
+    if (c == 0) {
+        if (a.nranges == 1)
+            a.y[row] = acc;
+        else
+            a.part[(int64_t)ri.g * a.n + row] = acc;
+    }
 }
 
 // ---------------------------------------------------------------------------
 // Q8 GEMV with a binary32 activation (tolerance-checked path).  Same T16
-// walk; per lane an 8-term float dot per block, xor-shuffle sum of the four
-// k-chunks, then acc += d_w * dot.
+// walk; x staged in LDS as floats in T16 activation order (slot (p*4+c) =
+// 8 floats of block 2p chunk c, then 8 of block 2p+1).  Per lane an 8-term
+// float dot per block scaled by d_w, lane-swap sum over the chunks at the end.
 // ---------------------------------------------------------------------------
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_f32(const lgx_gemv_args a) {
     __shared__ __align__(16) float xs[LGX_Q8_RANGE_BLOCKS * 32];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const RangeInfo ri = range_info(blockIdx.y, a.k);
-    const int nb = a.k >> 5;
+    const int nh = s16_nhalf(a.k);
     {
-        const int e = 4 * threadIdx.x;
+        // thread i: slot i >> 2 (pair p, chunk c), quarter q = i & 3 of its 16 floats
+        const int slot = threadIdx.x >> 2, q = threadIdx.x & 3;
+        const int p = slot >> 2, c = slot & 3;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (e < ri.nbr * 32) v = *(const float4*)(a.xf + ri.b0 * 32 + e);
-        *(float4*)(xs + e) = v;
+        if (p < ri.npairs)
+            v = *(const float4*)(a.xf + (int64_t)(ri.p0 + p) * 64 + (q >> 1) * 32 + 8 * c + 4 * (q & 1));
+        *(float4*)(xs + slot * 16 + 4 * q) = v;
     }
     __syncthreads();
     const int t = blockIdx.x * 4 + wave;
@@ -270,142 +346,217 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_f32(const lgx_ge
     const int r = lane & 15, c = lane >> 4;
     const int row = t * 16 + r;
     const int np = a.k >> 6;
+    const int last = ri.npairs - 1;
     const uint4* wp = (const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64 + lane;
-    const uint32_t* dwp = (const uint32_t*)(a.wd + (int64_t)row * nb + ri.b0);
     uint4 w[16];
     uint32_t dw[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        if (i < ri.npairs) {
-            w[i] = ld_stream(wp + i * 64);
-            dw[i] = dwp[i];
+    for (int i = 0; i < 16; ++i) w[i] = ld_stream(wp + min(i, last) * 64);
+    {
+        uint32_t d0[8], d1[8];
+        load_scales_half(a.wd, t, 2 * ri.g, nh, r, d0);
+        load_scales_half(a.wd, t, min(2 * ri.g + 1, nh - 1), nh, r, d1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            dw[i] = d0[i];
+            dw[8 + i] = d1[i];
         }
     }
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        if (i < ri.npairs) {
-            const float4* x0 = (const float4*)(xs + (2 * i) * 32 + 8 * c);
-            const float4* x1 = (const float4*)(xs + (2 * i + 1) * 32 + 8 * c);
-            const float4 xa = x0[0], xb = x0[1], xc = x1[0], xd = x1[1];
-            const uint32_t q[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
-            const float xv0[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-            const float xv1[8] = {xc.x, xc.y, xc.z, xc.w, xd.x, xd.y, xd.z, xd.w};
-            float s0 = 0.0f, s1 = 0.0f;
+        const float4* xp = (const float4*)(xs + (i * 4 + c) * 16);
+        const float4 xa = xp[0], xb = xp[1], xc = xp[2], xd = xp[3];
+        const uint32_t q[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+        const float xv0[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        const float xv1[8] = {xc.x, xc.y, xc.z, xc.w, xd.x, xd.y, xd.z, xd.w};
+        float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float q0 = (float)(int8_t)(q[j >> 2] >> (8 * (j & 3)));
-                const float q1 = (float)(int8_t)(q[2 + (j >> 2)] >> (8 * (j & 3)));
-                s0 = fmaf(q0, xv0[j], s0);
-                s1 = fmaf(q1, xv1[j], s1);
-            }
-            s0 += shfl_xor_f(s0, 16);
-            s1 += shfl_xor_f(s1, 16);
-            s0 += shfl_xor_f(s0, 32);
-            s1 += shfl_xor_f(s1, 32);
-            acc = fmaf(h2f(dw[i] & 0xffffu), s0, acc);
-            acc = fmaf(h2f(dw[i] >> 16), s1, acc);
+        for (int j = 0; j < 8; ++j) {
+            s0 = fmaf((float)(int8_t)(q[j >> 2] >> (8 * (j & 3))), xv0[j], s0);
+            s1 = fmaf((float)(int8_t)(q[2 + (j >> 2)] >> (8 * (j & 3))), xv1[j], s1);
         }
+        const bool on = i <= last;
+        const float t0 = on ? h2f(dw[i] & 0xffffu) : 0.0f;
+        const float t1 = on ? h2f(dw[i] >> 16) : 0.0f;
+        acc = fmaf(t0, s0, acc);
+        acc = fmaf(t1, s1, acc);
     }
-    finish_gemv(a, ri.g, t, row, c, lane, acc);
+    acc = reduce_chunks_f(acc);
+    if (c == 0) {
+        if (a.nranges == 1)
+            a.y[row] = acc;
+        else
+            a.part[(int64_t)ri.g * a.n + row] = acc;
+    }
 }
 
 // ---------------------------------------------------------------------------
-// Q8 x Q8 GEMM on int8 MFMA (v_mfma_i32_16x16x32_i8), M in m-groups of 64.
-// The activation range (up to 64 rows x 32 blocks) is staged in LDS in MFMA
-// A-operand order (the T16 order applied to rows of X), the per-block
-// activation scales transposed to [block][row] as binary32.  Each wave owns a
-// 16-row weight tile; per block one MFMA per 16-row m-tile yields exact int32
-// block dots D[m][n] (lane holds m = 4c+v, n = r), and the epilogue runs the
-// canonical chain acc = fmaf((float)D, dw*dx, acc).
+// Q8 x Q8 GEMV (M = 1) on int8 MFMA, one wave per (row tile, range).
+//
+// The wave requests its whole tile-range (16 T16 units, 16 KiB, plus the 32
+// S16 scales of each of its rows) before the workgroup stages the range's
+// activation (or quantises it, QX) and meets the barrier, so the weight
+// stream never waits for the activation.  Per block the MFMA, with the
+// activation broadcast to all 16 A rows, yields the exact int32 block dots
+// of the wave's 16 rows (the hardware sums the four k-chunks); the c = 0
+// lanes run the canonical chain.  One range partial per row goes to `y`
+// (single range) or `part` (lgx_k_q8_combine applies the tree).
 // ---------------------------------------------------------------------------
-extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma(const lgx_gemv_args a) {
-    __shared__ __align__(16) uint4 xa_s[4 * 16 * 64];             // [mt][pair][lane] 64 KiB
-    __shared__ __align__(16) float dx_s[LGX_Q8_RANGE_BLOCKS * 64];   // [block][m]     8 KiB
+template <bool QX>
+__device__ __forceinline__ void q8_gemv_mfma_body(const lgx_gemv_args& a) {
+    __shared__ __align__(16) int8_t xs[LGX_Q8_RANGE_BLOCKS * 32];
+    __shared__ __align__(16) float dxs[LGX_Q8_RANGE_BLOCKS];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const RangeInfo ri = range_info(blockIdx.y, a.k);
-    const int nb = a.k >> 5;
-    const int m0 = blockIdx.z * 64;
-    const int mrows = min(64, a.m - m0);
-    const int mtiles = (mrows + 15) >> 4;
-    // Stage X: slot (mt, pl, l) holds X[m0+16mt+r][64(p0+pl) + 8c, +8) ++ [.. +32, +8).
-    for (int s = threadIdx.x; s < mtiles * 16 * 64; s += 256) {
-        const int mt = s >> 10, pl = (s >> 6) & 15, l = s & 63;
-        const int r = l & 15, c = l >> 4;
-        const int m = m0 + mt * 16 + r;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (m < a.m && pl < ri.npairs) {
-            const int8_t* src = a.xq + (int64_t)m * a.k + (ri.p0 + pl) * 64 + 8 * c;
-            const uint2 lo = *(const uint2*)src;
-            const uint2 hi = *(const uint2*)(src + 32);
-            v = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        }
-        xa_s[s] = v;
-    }
-    for (int s = threadIdx.x; s < LGX_Q8_RANGE_BLOCKS * 64; s += 256) {
-        const int b = s >> 6, m = s & 63;
-        float v = 0.0f;
-        if (m < mrows && b < ri.nbr) v = h2f(a.xd[(int64_t)(m0 + m) * nb + ri.b0 + b]);
-        dx_s[s] = v;
-    }
-    __syncthreads();
+    const int nh = s16_nhalf(a.k);
     const int t = blockIdx.x * 4 + wave;
-    if (t >= a.ntiles) return;
+    const int tc = min(t, a.ntiles - 1);
     const int r = lane & 15, c = lane >> 4;
-    const int col = t * 16 + r;
     const int np = a.k >> 6;
-    const uint4* wp = (const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64 + lane;
-    const uint32_t* dwp = (const uint32_t*)(a.wd + (int64_t)col * nb + ri.b0);
+    const int last = ri.npairs - 1;
+    const uint4* wp = (const uint4*)a.wt + ((int64_t)tc * np + ri.p0) * 64 + lane;
     uint4 w[16];
     uint32_t dw[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        if (i < ri.npairs) {
-            w[i] = ld_stream(wp + i * 64);
-            dw[i] = dwp[i];
+    for (int i = 0; i < 16; ++i) w[i] = ld_stream(wp + min(i, last) * 64);
+    {
+        uint32_t d0[8], d1[8];
+        load_scales_half(a.wd, tc, 2 * ri.g, nh, r, d0);
+        load_scales_half(a.wd, tc, min(2 * ri.g + 1, nh - 1), nh, r, d1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            dw[i] = d0[i];
+            dw[8 + i] = d1[i];
         }
     }
-    float acc[4][4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[mt][v] = 0.0f;
+    if (QX)
+        quantize_blocks_to_lds(a, ri.b0, ri.b0 + ri.nbr, xs, dxs, blockIdx.x == 0);
+    else
+        stage_pairs_q8(a, ri.p0, ri.p0 + ri.npairs, xs, dxs);
+    __syncthreads();
+    if (t >= a.ntiles) return;
     const v4i zero = {0, 0, 0, 0};
+    float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        if (i < ri.npairs) {
-            const float dw0 = h2f(dw[i] & 0xffffu), dw1 = h2f(dw[i] >> 16);
+        const int ic = min(i, last);
+        const bool on = i <= last;
+        const uint4 xv = *(const uint4*)(xs + (ic * 4 + c) * 16);
+        const long a0 = (long)(((uint64_t)xv.y << 32) | xv.x);
+        const long a1 = (long)(((uint64_t)xv.w << 32) | xv.z);
+        long b0 = (long)(((uint64_t)w[i].y << 32) | w[i].x);
+        long b1 = (long)(((uint64_t)w[i].w << 32) | w[i].z);
+        // keep unit i's MFMAs after unit i-1's chain step (volatile empty asm
+        // statements stay in order; b0/b1 pass through one, acc the other),
+        // so only one unit's products are live at a time
+        asm volatile("" : "+v"(b0), "+v"(b1));
+        const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, zero, 0, 0, 0);
+        const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, zero, 0, 0, 0);
+        const float e0 = on ? h2f(dw[i] & 0xffffu) * dxs[2 * ic] : 0.0f;
+        const float e1 = on ? h2f(dw[i] >> 16) * dxs[2 * ic + 1] : 0.0f;
+        acc = fmaf((float)d0[0], e0, acc);
+        acc = fmaf((float)d1[0], e1, acc);
+        asm volatile("" : "+v"(acc));
+    }
+    if (c == 0) {
+        const int row = t * 16 + r;
+        if (a.nranges == 1)
+            a.y[row] = acc;
+        else
+            a.part[(int64_t)ri.g * a.n + row] = acc;
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_mfma(const lgx_gemv_args a) {
+    q8_gemv_mfma_body<false>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_mfma_qx(const lgx_gemv_args a) {
+    q8_gemv_mfma_body<true>(a);
+}
+
+// ---------------------------------------------------------------------------
+// Streaming Q8 x Q8 GEMM on int8 MFMA (v_mfma_i32_16x16x32_i8), M > 1.
+//
+// grid = (tile groups, ranges, m-groups of MT*16 rows); 4 waves per
+// workgroup.  The workgroup stages its activation range once (LDS, MFMA
+// A-operand order; scales transposed to [block][row] as binary32), then each
+// wave streams `tpw` row tiles (tile = blockIdx.x*4*tpw + 4*j + wave) of the
+// range as 8 KiB halves, the next half requested before the current one is
+// consumed.  Per block one MFMA per m-tile gives the exact int32 block dots
+// D[m][n] (lane l = r + 16c holds n = r, m = 4c + v); the epilogue runs the
+// canonical chain acc = fmaf((float)D, dw*dx, acc).  Range partials go to
+// `part` (several ranges) and lgx_k_q8_combine applies the tree.
+// ---------------------------------------------------------------------------
+template <int MT>
+__device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
+    constexpr int XSLOTS = MT * 16 * 64;   // 16-byte A-operand slots
+    constexpr int DXROWS = MT * 16;
+    __shared__ __align__(16) uint4 xa_s[XSLOTS];
+    __shared__ __align__(16) float dx_s[LGX_Q8_RANGE_BLOCKS * DXROWS];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const RangeInfo ri = range_info(blockIdx.y, a.k);
+    const int nb = a.k >> 5, nh = s16_nhalf(a.k);
+    const int m0 = blockIdx.z * DXROWS;
+    const int mrows = min(DXROWS, a.m - m0);
+    const int r = lane & 15, c = lane >> 4;
+    const int np = a.k >> 6;
+    const int last = ri.npairs - 1;
+    const int tbase = blockIdx.x * 4 * a.tpw + wave;
+    const v4i zero = {0, 0, 0, 0};
+
+    auto load_half = [&](int j, int h, uint4 (&w)[8], uint32_t (&dw)[8]) {
+        const int t = min(tbase + 4 * j, a.ntiles - 1);
+        const uint4* wp = (const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = ld_stream(wp + min(8 * h + i, last) * 64);
+        load_scales_half(a.wd, t, min(2 * ri.g + h, nh - 1), nh, r, dw);
+    };
+    float acc[MT][4];
+    auto compute_half = [&](int h, const uint4 (&w)[8], const uint32_t (&dw)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int pi = 8 * h + i;
+            const bool on = pi <= last;
+            const int pc = min(pi, last);
+            const float dw0 = on ? h2f(dw[i] & 0xffffu) : 0.0f;
+            const float dw1 = on ? h2f(dw[i] >> 16) : 0.0f;
             const long b0 = (long)(((uint64_t)w[i].y << 32) | w[i].x);
             const long b1 = (long)(((uint64_t)w[i].w << 32) | w[i].z);
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                if (mt < mtiles) {
-                    const uint4 xv = xa_s[(mt * 16 + i) * 64 + lane];
-                    const long a0 = (long)(((uint64_t)xv.y << 32) | xv.x);
-                    const long a1 = (long)(((uint64_t)xv.w << 32) | xv.z);
-                    const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, zero, 0, 0, 0);
-                    const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, zero, 0, 0, 0);
-                    const float4 x0 = *(const float4*)(dx_s + (2 * i) * 64 + mt * 16 + 4 * c);
-                    const float4 x1 = *(const float4*)(dx_s + (2 * i + 1) * 64 + mt * 16 + 4 * c);
-                    acc[mt][0] = fmaf((float)d0[0], dw0 * x0.x, acc[mt][0]);
-                    acc[mt][1] = fmaf((float)d0[1], dw0 * x0.y, acc[mt][1]);
-                    acc[mt][2] = fmaf((float)d0[2], dw0 * x0.z, acc[mt][2]);
-                    acc[mt][3] = fmaf((float)d0[3], dw0 * x0.w, acc[mt][3]);
-                    acc[mt][0] = fmaf((float)d1[0], dw1 * x1.x, acc[mt][0]);
-                    acc[mt][1] = fmaf((float)d1[1], dw1 * x1.y, acc[mt][1]);
-                    acc[mt][2] = fmaf((float)d1[2], dw1 * x1.z, acc[mt][2]);
-                    acc[mt][3] = fmaf((float)d1[3], dw1 * x1.w, acc[mt][3]);
-                }
+            for (int mt = 0; mt < MT; ++mt) {
+                const uint4 xv = xa_s[(mt * 16 + pc) * 64 + lane];
+                const long a0 = (long)(((uint64_t)xv.y << 32) | xv.x);
+                const long a1 = (long)(((uint64_t)xv.w << 32) | xv.z);
+                const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, zero, 0, 0, 0);
+                const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, zero, 0, 0, 0);
+                const float4 x0 = *(const float4*)(dx_s + (2 * pc) * DXROWS + mt * 16 + 4 * c);
+                const float4 x1 = *(const float4*)(dx_s + (2 * pc + 1) * DXROWS + mt * 16 + 4 * c);
+                acc[mt][0] = fmaf((float)d0[0], dw0 * x0.x, acc[mt][0]);
+                acc[mt][1] = fmaf((float)d0[1], dw0 * x0.y, acc[mt][1]);
+                acc[mt][2] = fmaf((float)d0[2], dw0 * x0.z, acc[mt][2]);
+                acc[mt][3] = fmaf((float)d0[3], dw0 * x0.w, acc[mt][3]);
+                acc[mt][0] = fmaf((float)d1[0], dw1 * x1.x, acc[mt][0]);
+                acc[mt][1] = fmaf((float)d1[1], dw1 * x1.y, acc[mt][1]);
+                acc[mt][2] = fmaf((float)d1[2], dw1 * x1.z, acc[mt][2]);
+                acc[mt][3] = fmaf((float)d1[3], dw1 * x1.w, acc[mt][3]);
             }
+            // keep each unit's MFMAs next to their epilogue: bounded live
+            // ranges (occupancy) instead of all 16 MFMA results in flight
+            __builtin_amdgcn_sched_barrier(0);
         }
-    }
+    };
+    auto store_tile = [&](int j) {
+        const int t = tbase + 4 * j;
+        if (t >= a.ntiles) return;
+        const int col = t * 16 + r;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        if (mt < mtiles) {
+        for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int m = m0 + mt * 16 + 4 * c + v;
-                if (m < a.m) {
+                const int mm = mt * 16 + 4 * c + v;
+                const int m = m0 + mm;
+                if (mm < mrows) {
                     if (a.nranges == 1)
                         a.y[(int64_t)m * a.n + col] = acc[mt][v];
                     else
@@ -413,20 +564,71 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma(const lgx_g
                 }
             }
         }
-    }
-    if (a.nranges == 1) return;
-    const int slot = t * a.nmgroups + blockIdx.z;
-    if (!last_arrival(a.counter, slot, a.nranges, lane)) return;
-#pragma unroll 1
-    for (int o = 0; o < 16; ++o) {
-        const int m = m0 + (o >> 2) * 16 + 4 * c + (o & 3);
-        if ((o >> 2) < mtiles && m < a.m) {
-            float p[LGX_MAX_RANGES];
-#pragma unroll
-            for (int j = 0; j < LGX_MAX_RANGES; ++j)
-                p[j] = j < a.nranges ? a.part[((int64_t)j * a.m + m) * a.n + col] : 0.0f;
-            a.y[(int64_t)m * a.n + col] = tree_sum(p, a.nranges);
+    };
+
+    uint4 wn[8];
+    uint32_t dn[8];
+    load_half(0, 0, wn, dn);
+    for (int s = threadIdx.x; s < XSLOTS; s += 256) {
+        const int mt = s >> 10, pl = (s >> 6) & 15, l = s & 63;
+        const int rr = l & 15, cc = l >> 4;
+        const int m = m0 + mt * 16 + rr;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (m < a.m && pl < ri.npairs) {
+            const int8_t* src = a.xq + (int64_t)m * a.k + (ri.p0 + pl) * 64 + 8 * cc;
+            const uint2 lo = *(const uint2*)src;
+            const uint2 hi = *(const uint2*)(src + 32);
+            v = make_uint4(lo.x, lo.y, hi.x, hi.y);
         }
+        xa_s[s] = v;
     }
-    if (lane == 0) a.counter[slot] = 0;
+    for (int s = threadIdx.x; s < LGX_Q8_RANGE_BLOCKS * DXROWS; s += 256) {
+        const int b = s / DXROWS, m = s - b * DXROWS;
+        float v = 0.0f;
+        if (m < mrows && b < ri.nbr) v = h2f(a.xd[(int64_t)(m0 + m) * nb + ri.b0 + b]);
+        dx_s[s] = v;
+    }
+    __syncthreads();
+    const int nhalves = 2 * a.tpw;
+#pragma unroll 1
+    for (int q = 0; q < nhalves; ++q) {
+        uint4 w[8];
+        uint32_t dw[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            w[i] = wn[i];
+            dw[i] = dn[i];
+        }
+        if (q + 1 < nhalves) load_half((q + 1) >> 1, (q + 1) & 1, wn, dn);
+        if ((q & 1) == 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[mt][v] = 0.0f;
+        }
+        compute_half(q & 1, w, dw);
+        if (q & 1) store_tile(q >> 1);
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16(const lgx_gemv_args a) {
+    q8_stream_body<1>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma32(const lgx_gemv_args a) {
+    q8_stream_body<2>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma64(const lgx_gemv_args a) {
+    q8_stream_body<4>(a);
+}
+
+// ---------------------------------------------------------------------------
+// Range combine: y[i] = canonical pairwise tree over the range partials.
+// ---------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_combine(const lgx_combine_args a) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.count) return;
+    float p[LGX_MAX_RANGES];
+#pragma unroll
+    for (int j = 0; j < LGX_MAX_RANGES; ++j) p[j] = j < a.nranges ? a.part[j * a.count + i] : 0.0f;
+    a.y[i] = tree_sum(p, a.nranges);
 }

@@ -241,6 +241,23 @@ void orc_q8_repack_t16(const int8_t* qs, int32_t n, int32_t k, int8_t* out) {
             out[t16_index(row, kk, k)] = qs[(int64_t)row * k + kk];
 }
 
+/* Device scale layout "S16": per row tile and half-range (16 blocks) the
+ * 16 rows x 16 scales are contiguous, row-major: element
+ * ((tile * nhalf + b/16) * 16 + row%16) * 16 + b%16, nhalf = ceil(k/512);
+ * entries past k/32 are zero. */
+int64_t orc_q8_s16_count(int32_t n, int32_t k) {
+    return (int64_t)(n / 16) * ((k + 511) / 512) * 256;
+}
+
+void orc_q8_repack_s16(const uint16_t* d, int32_t n, int32_t k, uint16_t* out) {
+    int32_t nb = k / 32, nh = (k + 511) / 512;
+    memset(out, 0, (size_t)orc_q8_s16_count(n, k) * 2);
+    for (int32_t row = 0; row < n; ++row)
+        for (int32_t b = 0; b < nb; ++b)
+            out[(((int64_t)(row >> 4) * nh + (b >> 4)) * 16 + (row & 15)) * 16 + (b & 15)] =
+                d[(int64_t)row * nb + b];
+}
+
 void orc_q8_unpack_t16(const int8_t* t16, int32_t n, int32_t k, int8_t* qs) {
     for (int32_t row = 0; row < n; ++row)
         for (int32_t kk = 0; kk < k; ++kk)

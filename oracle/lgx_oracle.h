@@ -33,7 +33,7 @@
  *   q8 gemv f32      one-hot x (exact column), linearity, numpy-f64 fixture
  *   q8 gemm          per-row equality with the M=1 path (batch invariance),
  *                    numpy-f64 fixture within 1e-5 rel, one-hot closed form
- *   repack t16       round trip + explicit index formula on a tiny case
+ *   repack t16/s16   round trip + explicit index formula on a tiny case
  */
 #ifndef LGX_ORACLE_H
 #define LGX_ORACLE_H
@@ -70,6 +70,8 @@ void orc_gen_below_i32(uint64_t seed, uint64_t stream, uint32_t bound, int32_t* 
 void orc_quantize_q8_0(const float* x, int64_t m, int32_t k, int8_t* qs, uint16_t* d);
 void orc_q8_repack_t16(const int8_t* qs, int32_t n, int32_t k, int8_t* out);
 void orc_q8_unpack_t16(const int8_t* t16, int32_t n, int32_t k, int8_t* qs);
+int64_t orc_q8_s16_count(int32_t n, int32_t k);
+void orc_q8_repack_s16(const uint16_t* d, int32_t n, int32_t k, uint16_t* out);
 void orc_q8_gemv_f32(const int8_t* qs, const uint16_t* d, int32_t n, int32_t k,
                      const float* x, float* y);
 void orc_q8_blockdots(const int8_t* qs, int32_t n, int32_t k, const int8_t* xq,

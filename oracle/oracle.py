@@ -60,6 +60,8 @@ def lib():
             "orc_quantize_q8_0": (None, [_P, _I64, _I32, _P, _P]),
             "orc_q8_repack_t16": (None, [_P, _I32, _I32, _P]),
             "orc_q8_unpack_t16": (None, [_P, _I32, _I32, _P]),
+            "orc_q8_s16_count": (_I64, [_I32, _I32]),
+            "orc_q8_repack_s16": (None, [_P, _I32, _I32, _P]),
             "orc_q8_gemv_f32": (None, [_P, _P, _I32, _I32, _P, _P]),
             "orc_q8_blockdots": (None, [_P, _I32, _I32, _P, _P]),
             "orc_q8_gemm": (None, [_P, _P, _I32, _I32, _P, _P, _I32, _P]),
@@ -189,6 +191,13 @@ def q8_unpack_t16(t16, n: int, k: int):
     t16 = _c(t16, np.int8)
     out = np.empty((n, k), np.int8)
     lib().orc_q8_unpack_t16(_ptr(t16), n, k, _ptr(out))
+    return out
+
+
+def q8_repack_s16(d, n: int, k: int):
+    d = _c(d, np.uint16)
+    out = np.empty(lib().orc_q8_s16_count(n, k), np.uint16)
+    lib().orc_q8_repack_s16(_ptr(d), n, k, _ptr(out))
     return out
 
 

@@ -57,10 +57,21 @@ def test_invalid_handle_and_null_pointer_paths():
     assert L.lgx_q8_gemm(bogus, None, None, None, 1, None, None) == 6
     assert L.lgx_q8q8_gemv(bogus, None, None, None, None, None, None) == 6
     assert L.lgx_q8_gemv_f32(bogus, None, None, None, None) == 6
-    assert L.lgx_q8_repack_t16(bogus, None, 16, 64, None, None) == 6
+    assert L.lgx_q8_repack_t16(bogus, None, None, 16, 64, None, None, None) == 6
+    assert L.lgx_q8_unpack_t16(bogus, None, None, 16, 64, None, None, None) == 6
     assert b"invalid lgx_ctx" in L.lgx_last_error()
     L.lgx_clear_error()
     assert L.lgx_last_error() is None
+
+
+def test_scale_count_matches_oracle_layout():
+    import logicaffeine_amd as lgx
+    from oracle import oracle as orc
+
+    L = lgx.lib()
+    for n, k in ((16, 64), (4864, 896), (8960, 1536), (3584, 18944), (32, 2112)):
+        assert L.lgx_q8_scale_count(n, k) == orc.lib().orc_q8_s16_count(n, k)
+    assert L.lgx_q8_scale_count(17, 64) == 0 and L.lgx_q8_scale_count(16, 32) == 0
 
 
 def test_ctx_create_without_device_fails_loudly():
@@ -84,3 +95,25 @@ def test_missing_code_object_is_a_load_error(tmp_path):
     st = lgx.lib().lgx_ctx_create(0, str(tmp_path / "nope.hsaco").encode(), C.byref(h))
     assert st in (5, 11)
     assert h.value is None
+
+
+def test_every_host_kernel_exists_in_code_object():
+    """The launcher resolves kernels by name (hipModuleGetFunction); every
+    name in its table must be a kernel symbol of the built lgx_kernels.hsaco."""
+    import subprocess
+
+    import logicaffeine_amd as lgx
+
+    src = open(os.path.join(ROOT, "logicaffeine_amd", "csrc", "lgx_host.cpp")).read()
+    table = src[src.index("kKernelNames[K_COUNT] = {"):]
+    table = table[:table.index("};")]
+    names = re.findall(r'"(lgx_k_[a-z0-9_]+)"', table)
+    enum = src[src.index("enum Kern {"):src.index("K_COUNT")]
+    assert len(names) == len(re.findall(r"\bK_[A-Z0-9_]+,", enum))
+    readelf = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib", "llvm", "bin",
+                           "llvm-readelf")
+    syms = subprocess.run([readelf, "-sW", lgx.HSACO_PATH], capture_output=True,
+                          text=True, check=True).stdout
+    defined = set(line.split()[-1] for line in syms.splitlines() if " FUNC " in line)
+    for n in names:
+        assert n in defined, f"{n} missing from {lgx.HSACO_PATH}"

@@ -36,8 +36,10 @@ def w0(ctx, orc):
 def test_repack_matches_oracle_and_round_trips(ctx, orc, w0):
     qs, d, _, W = w0
     assert np.array_equal(host(W.qs), orc.q8_repack_t16(qs))
-    back = ctx.unpack_t16(W.qs, 4864, 896)
-    assert np.array_equal(host(back), qs)
+    assert np.array_equal(u16(W.d), orc.q8_repack_s16(d, 4864, 896))
+    bq, bd = ctx.unpack_t16(W.qs, W.d, 4864, 896)
+    assert np.array_equal(host(bq), qs)
+    assert np.array_equal(u16(bd), d)
 
 
 @pytest.mark.parametrize("m,k", [(1, 896), (64, 8960), (7, 1536)])
@@ -132,12 +134,123 @@ def test_shape_errors_and_launch_count(ctx, orc):
     t = ctx.torch
     before = ctx.launch_count
     bad = t.zeros(17 * 64, dtype=t.int8, device=ctx.dev)
+    dbad = t.zeros(17 * 2, dtype=t.int16, device=ctx.dev)
     with pytest.raises(lgx.LgxError) as ei:
-        ctx.repack_t16(bad.view(17, 64))
+        ctx.repack_t16(bad.view(17, 64), dbad.view(17, 2))
     assert ei.value.status_name == "LGX_INVALID_ARGUMENT"
     assert ctx.launch_count == before
     qs, d = orc.gen_q8_matrix(0, 50, 16, 64)
     W = ctx.q8_matrix(qs, d)
-    assert ctx.launch_count == before + 1
+    assert ctx.launch_count == before + 2      # T16 quants + S16 scales
     ctx.torch.cuda.synchronize()
     assert W.n == 16 and ctx.arch == "gfx950"
+
+
+def test_workspace_reuse_across_shapes(ctx, orc):
+    """Regression: alternating multi-range shapes and batch sizes on one ctx
+    (scratch reused, arrival counters must stay zero between calls)."""
+    cases = []
+    for n, k in ((1536, 8960), (8960, 1536), (32, 2112), (1536, 8960)):
+        qs, d = orc.gen_q8_matrix(1, 60 + n + k, n, k)
+        cases.append((qs, d, ctx.q8_matrix(qs, d)))
+    for rep in range(2):
+        for i, (qs, d, W) in enumerate(cases):
+            m = (1, 3, 64, 70)[(i + rep) % 4]
+            x = orc.gen_normal_f32(1, 200 + 10 * i + rep, (m, W.k))
+            xq, xd = orc.quantize_q8_0(x)
+            gx, gd = ctx.to_device(xq), ctx.to_device(xd)
+            y = host(ctx.q8_gemm(W, gx, gd)) if m > 1 else host(ctx.q8q8_gemv(W, gx[0], gd[0]))[None]
+            assert np.array_equal(y, orc.q8_gemm(qs, d, xq, xd)), (rep, i, m)
+
+
+@pytest.mark.parametrize("n,k", [(4864, 896), (8960, 1536), (1536, 8960)])
+def test_q8q8_gemv_fused_quantize_bit_exact(ctx, orc, n, k):
+    """Fused Q8_0(x) prologue: the GEMV output and the emitted quants/scales
+    equal the separate quantise + GEMV and the oracle bit-for-bit."""
+    t = ctx.torch
+    qs, d = orc.gen_q8_matrix(1, 40 + n, n, k)
+    x = orc.gen_normal_f32(1, 50 + n, (1, k))
+    x[0, 64:96] = 0.0
+    xq, xd = orc.quantize_q8_0(x)
+    W = ctx.q8_matrix(qs, d)
+    gq = t.empty(k, dtype=t.int8, device=ctx.dev)
+    gd = t.empty(k // 32, dtype=t.int16, device=ctx.dev)
+    y = ctx.q8q8_gemv_quantize(W, ctx.to_device(x[0]), xq_out=gq, xd_out=gd)
+    assert np.array_equal(host(gq), xq[0])
+    assert np.array_equal(u16(gd), xd[0])
+    assert np.array_equal(host(y), orc.q8_gemm(qs, d, xq, xd)[0])
+
+
+def _ctx_with_env(**env):
+    import os
+
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
+    try:
+        return lgx.Context(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("n,k", [(4864, 896), (1536, 8960), (272, 2112)])
+def test_kernel_variants_agree(ctx, orc, n, k):
+    """The v_dot4 GEMV, the MFMA GEMV and the MFMA GEMM at every m-tile
+    width, with one or many row tiles per wave, all give the oracle's bits."""
+    qs, d = orc.gen_q8_matrix(2, n + k, n, k)
+    x = orc.gen_normal_f32(2, 7, (40, k))
+    xq, xd = orc.quantize_q8_0(x)
+    ref = orc.q8_gemm(qs, d, xq, xd)
+    for c in (ctx, _ctx_with_env(LGX_GEMV="dot4"), _ctx_with_env(LGX_WG_TARGET=3)):
+        W = c.q8_matrix(qs, d)
+        gx, gd = c.to_device(xq), c.to_device(xd)
+        assert np.array_equal(host(c.q8q8_gemv(W, gx[0], gd[0])), ref[0])
+        assert np.array_equal(host(c.q8q8_gemv_quantize(W, c.to_device(x[0]))), ref[0])
+        for m in (1, 5, 16, 17, 32, 40):
+            assert np.array_equal(host(c.q8_gemm(W, gx[:m].contiguous(), gd[:m].contiguous())),
+                                  ref[:m]), m
+        if c is not ctx:
+            c.close()
+
+
+@pytest.mark.parametrize("n,k", [(4864, 896), (1536, 8960)])
+def test_partials_then_combine_equal_full_product(ctx, orc, n, k):
+    """Range partials + lgx_q8_range_combine == the one-call product, and each
+    partial is the oracle's chain of that range alone."""
+    qs, d = orc.gen_q8_matrix(3, n + k, n, k)
+    x = orc.gen_normal_f32(3, 1, (24, k))
+    xq, xd = orc.quantize_q8_0(x)
+    W = ctx.q8_matrix(qs, d)
+    gx, gd = ctx.to_device(xq), ctx.to_device(xd)
+    g = lgx.lib().lgx_q8_range_count(k)
+    for m in (1, 24):
+        part = ctx.q8_gemm_partials(W, gx[:m].contiguous(), gd[:m].contiguous())
+        assert tuple(part.shape) == (g, m, n)
+        y = host(ctx.range_combine(part))
+        assert np.array_equal(y, orc.q8_gemm(qs, d, xq[:m], xd[:m]))
+        # partial r alone = the product restricted to range r's 32 blocks
+        r = g - 1
+        lo, hi = 1024 * r, min(1024 * (r + 1), k)
+        pr = orc.q8_gemm(np.ascontiguousarray(qs[:, lo:hi]), np.ascontiguousarray(d[:, lo // 32:hi // 32]),
+                         np.ascontiguousarray(xq[:m, lo:hi]), np.ascontiguousarray(xd[:m, lo // 32:hi // 32]))
+        assert np.array_equal(host(part[r]), pr)
+    p1 = host(ctx.q8q8_gemv_quantize_partials(W, ctx.to_device(x[0])))
+    assert np.array_equal(p1, host(ctx.q8_gemm_partials(W, gx[0:1], gd[0:1]))[:, 0, :])
+
+
+def test_kernel_timing_window(ctx, orc):
+    qs, d = orc.gen_q8_matrix(0, 90, 1536, 8960)
+    W = ctx.q8_matrix(qs, d)
+    x = ctx.to_device(orc.gen_normal_f32(0, 91, (8960,)))
+    ctx.kernel_timing(True)
+    for _ in range(3):
+        ctx.q8q8_gemv_quantize(W, x)
+    ctx.kernel_timing(False)
+    ctx.q8q8_gemv_quantize(W, x)          # outside the window: not recorded
+    n, ms = ctx.kernel_stats("lgx_k_q8_gemv_mfma_qx")
+    assert n == 3 and 0.0 < ms < 100.0
+    assert ctx.kernel_stats("lgx_k_q8_combine")[0] == 3
+    assert ctx.kernel_stats("lgx_k_quantize_q8_0") == (0, 0.0)

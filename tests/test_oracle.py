@@ -221,3 +221,16 @@ def test_t16_repack_round_trip_and_formula(orc):
     unit = 1 * 2 + 1
     lane = 1 + 16 * 2
     assert t[unit * 1024 + lane * 16 + 8 + 5] == qs[17, k]
+
+
+def test_s16_scale_layout_formula(orc):
+    n, k = 32, 896                     # nb = 28 -> two half-ranges, the second padded
+    d = np.arange(n * (k // 32), dtype=np.uint16).reshape(n, k // 32) + 1
+    s = orc.q8_repack_s16(d, n, k)
+    nh = 2
+    assert s.size == (n // 16) * nh * 256
+    # row 17 (tile 1, r 1), block 20 (half 1, j 4)
+    assert s[((1 * nh + 1) * 16 + 1) * 16 + 4] == d[17, 20]
+    # padding past nb is zero, and every scale appears exactly once
+    assert s[((0 * nh + 1) * 16 + 3) * 16 + 12] == 0
+    assert np.array_equal(np.sort(s[s != 0]), np.sort(d.ravel()))
