@@ -150,6 +150,23 @@ lgx_status lgx_q8q8_gemv_quantize(lgx_ctx* ctx, const lgx_q8_matrix* W, const fl
 lgx_status lgx_q8_gemm(lgx_ctx* ctx, const lgx_q8_matrix* W, const int8_t* xq,
                        const uint16_t* xd, int32_t m, float* y, void* stream);
 
+/* ---- paged GQA decode attention ---- */
+/* out[b][h][:] = softmax(q[b][h] . K_t / sqrt(d)) V_t over the first
+ * seq_len[b] cached tokens of sequence b, for KV head h / (hq/hkv).
+ * K/V pages are binary16 [num_pages][hkv][16][d]; token t of sequence b is
+ * slot t%16 of page page_table[b][t/16] (page_table is [B][maxp] int32).
+ * d is 64 or 128, hq/hkv in 1..8.  Canonical schedule: 256-token
+ * chunks, per chunk the score chain over d, max, exp, halving-tree sum and
+ * the PV chain over tokens; chunks merged by log-sum-exp in chunk order.
+ * Device-side seq_len values are clamped to max_seq_len (<= maxp*16, host
+ * argument sizing the grid) and page ids to [0, num_pages); seq_len 0 gives
+ * zeros.  Replaces no reference interface: the reference has no attention. */
+lgx_status lgx_gqa_decode_attn(lgx_ctx* ctx, const float* q, const uint16_t* kpages,
+                               const uint16_t* vpages, const int32_t* page_table,
+                               const int32_t* seq_len, int32_t B, int32_t hq, int32_t hkv,
+                               int32_t d, int32_t maxp, int32_t num_pages, int32_t max_seq_len,
+                               float* out, void* stream);
+
 /* ---- range partials (for consumers that fuse the range tree) ---- */
 /* Number of canonical 32-block ranges of K = the partial count of a product. */
 int32_t lgx_q8_range_count(int32_t k);

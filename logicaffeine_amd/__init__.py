@@ -59,6 +59,8 @@ SIGNATURES = {
     "lgx_q8q8_gemv_quantize_partials": (C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     "lgx_q8_gemm_partials": (C.c_int, [_P, _P, _P, _P, _I32, _P, _P]),
     "lgx_q8_range_combine": (C.c_int, [_P, _P, _I32, C.c_int64, _P, _P]),
+    "lgx_gqa_decode_attn": (C.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32,
+                                      _I32, _I32, _P, _P]),
 }
 
 
@@ -273,6 +275,20 @@ class Context:
         _check(lib().lgx_q8_range_combine(self.handle, part.data_ptr(), g, count, y.data_ptr(),
                                           self._s()))
         return y
+
+    def gqa_decode_attn(self, q, kpages, vpages, page_table, seq_len, max_seq_len: int,
+                        out=None):
+        """q [B][hq][d] f32; pages [P][hkv][16][d] (int16 bit patterns of binary16)."""
+        t = self.torch
+        B, hq, d = q.shape
+        num_pages, hkv = kpages.shape[0], kpages.shape[1]
+        maxp = page_table.shape[1]
+        out = t.empty((B, hq, d), dtype=t.float32, device=self.dev) if out is None else out
+        _check(lib().lgx_gqa_decode_attn(self.handle, q.data_ptr(), kpages.data_ptr(),
+                                         vpages.data_ptr(), page_table.data_ptr(),
+                                         seq_len.data_ptr(), B, hq, hkv, d, maxp, num_pages,
+                                         max_seq_len, out.data_ptr(), self._s()))
+        return out
 
     def q8_gemm(self, W: Q8Matrix, xq, xd, y=None):
         t = self.torch

@@ -16,6 +16,7 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -87,14 +88,34 @@ enum Kern {
     K_GEMM_MFMA32,
     K_GEMM_MFMA64,
     K_REPACK_S16,
+    K_ATTN_D64_G1,   // + (gq - 1): gq = 1..8
+    K_ATTN_D128_G1 = K_ATTN_D64_G1 + 8,
+    K_ATTN_COMBINE_D64 = K_ATTN_D128_G1 + 8,
+    K_ATTN_COMBINE_D128,
     K_COUNT
 };
-const char* const kKernelNames[K_COUNT] = {
+const char* const kKernelNames[] = {
     "lgx_k_repack_t16", "lgx_k_quantize_q8_0", "lgx_k_q8q8_gemv",
     "lgx_k_q8_gemv_f32", "lgx_k_q8_combine",
     "lgx_k_q8_gemv_mfma", "lgx_k_q8_gemv_mfma_qx", "lgx_k_q8_gemm_mfma16",
     "lgx_k_q8_gemm_mfma32", "lgx_k_q8_gemm_mfma64", "lgx_k_repack_s16",
+    "lgx_k_attn_chunk_d64_g1", "lgx_k_attn_chunk_d64_g2", "lgx_k_attn_chunk_d64_g3",
+    "lgx_k_attn_chunk_d64_g4", "lgx_k_attn_chunk_d64_g5", "lgx_k_attn_chunk_d64_g6",
+    "lgx_k_attn_chunk_d64_g7", "lgx_k_attn_chunk_d64_g8",
+    "lgx_k_attn_chunk_d128_g1", "lgx_k_attn_chunk_d128_g2", "lgx_k_attn_chunk_d128_g3",
+    "lgx_k_attn_chunk_d128_g4", "lgx_k_attn_chunk_d128_g5", "lgx_k_attn_chunk_d128_g6",
+    "lgx_k_attn_chunk_d128_g7", "lgx_k_attn_chunk_d128_g8",
+    "lgx_k_attn_combine_d64", "lgx_k_attn_combine_d128",
 };
+
+static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
+              "one code-object name per kernel slot");
+
+// Attention chunk kernel for head_dim d and query heads per KV head gq.
+int attn_kernel(int d, int gq) {
+    if (gq < 1 || gq > 8) return -1;
+    return (d == 64 ? K_ATTN_D64_G1 : K_ATTN_D128_G1) + gq - 1;
+}
 
 // Debug/tuning knobs read once per ctx (documented in DESIGN.md):
 //   LGX_GEMV=dot4   route lgx_q8q8_gemv to the v_dot4 GEMV instead of MFMA
@@ -517,6 +538,49 @@ lgx_status lgx_q8_range_combine(lgx_ctx* c, const float* part, int32_t nranges, 
             return fail(LGX_INVALID_ARGUMENT, "nranges %d / count %lld", nranges, (long long)count);
         lgx_combine_args ca{part, y, count, nranges};
         return launch(c, K_COMBINE, dim3(cdiv(count, 256)), dim3(256), ca, stream);
+    });
+}
+
+lgx_status lgx_gqa_decode_attn(lgx_ctx* c, const float* q, const uint16_t* kpages,
+                               const uint16_t* vpages, const int32_t* page_table,
+                               const int32_t* seq_len, int32_t B, int32_t hq, int32_t hkv,
+                               int32_t d, int32_t maxp, int32_t num_pages, int32_t max_seq_len,
+                               float* out, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!q || !kpages || !vpages || !page_table || !seq_len || !out)
+            return fail(LGX_NULL_POINTER, "NULL tensor pointer");
+        if (B <= 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0 || maxp <= 0 || num_pages <= 0)
+            return fail(LGX_INVALID_ARGUMENT, "B=%d hq=%d hkv=%d maxp=%d num_pages=%d", B, hq, hkv,
+                        maxp, num_pages);
+        const int k = attn_kernel(d, hq / hkv);
+        if ((d != 64 && d != 128) || k < 0)
+            return fail(LGX_UNSUPPORTED, "head_dim %d / %d query heads per KV head", d, hq / hkv);
+        if (max_seq_len <= 0 || max_seq_len > maxp * LGX_PAGE)
+            return fail(LGX_OUT_OF_BOUNDS, "max_seq_len %d outside (0, %d]", max_seq_len,
+                        maxp * LGX_PAGE);
+        lgx_attn_args a{};
+        a.q = q;
+        a.kpages = kpages;
+        a.vpages = vpages;
+        a.page_table = page_table;
+        a.seq_len = seq_len;
+        a.out = out;
+        a.B = B;
+        a.hq = hq;
+        a.hkv = hkv;
+        a.maxp = maxp;
+        a.num_pages = num_pages;
+        a.maxlen = max_seq_len;
+        a.nchunk = (max_seq_len + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
+        a.scale = (float)(1.0 / std::sqrt((double)d));
+        st = ensure_ws(c, (size_t)B * hq * a.nchunk * (d + 2) * sizeof(float), &a.part);
+        if (st != LGX_OK) return st;
+        st = launch(c, (Kern)k, dim3(a.nchunk, B * hkv), dim3(256), a, stream);
+        if (st != LGX_OK) return st;
+        return launch(c, d == 64 ? K_ATTN_COMBINE_D64 : K_ATTN_COMBINE_D128, dim3(B * hq), dim3(d),
+                      a, stream);
     });
 }
 

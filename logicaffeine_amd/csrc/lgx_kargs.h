@@ -55,3 +55,20 @@ typedef struct {
     int64_t count;
     int32_t nranges;
 } lgx_combine_args;
+
+// Paged GQA decode attention.  K/V pages: binary16 [num_pages][hkv][16][d].
+typedef struct {
+    const float* q;            // [B][hq][d]
+    const uint16_t* kpages;
+    const uint16_t* vpages;
+    const int32_t* page_table; // [B][maxp]
+    const int32_t* seq_len;    // [B]
+    float* part;               // [B][hq][nchunk][d + 2]: o_c[0..d), m_c, l_c
+    float* out;                // [B][hq][d]
+    int32_t B, hq, hkv, maxp, nchunk, num_pages;
+    int32_t maxlen;            // tokens beyond min(max_seq_len, maxp*16) are ignored
+    float scale;
+} lgx_attn_args;
+
+#define LGX_PAGE 16
+#define LGX_ATTN_CHUNK 256

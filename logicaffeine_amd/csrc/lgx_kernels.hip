@@ -632,3 +632,206 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_combine(const lgx_com
     for (int j = 0; j < LGX_MAX_RANGES; ++j) p[j] = j < a.nranges ? a.part[j * a.count + i] : 0.0f;
     a.y[i] = tree_sum(p, a.nranges);
 }
+
+// ---------------------------------------------------------------------------
+// Canonical binary32 exp, the same operation sequence as the CPU oracle:
+// Cody-Waite reduction x = n ln2 + r (n by the 1.5*2^23 rounding constant,
+// ln2 = 0x3f317200 + 1.42860682e-6), degree-7 Taylor polynomial of e^r in
+// Horner form with fmaf, scaling through the exponent field.  x < -87.33
+// gives +0, x > 88.72 gives +inf, exp(0) == 1.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float lgx_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72f) return __builtin_inff();
+    if (x < -87.33f) return 0.0f;
+    const float t = x * 1.44269504088896341f;
+    const float nf = (t + 12582912.0f) - 12582912.0f;
+    float r = fmaf(-nf, 0.693145751953125f, x);
+    r = fmaf(-nf, 1.42860682030941723e-06f, r);
+    float p = 1.98412698412698413e-04f;
+    p = fmaf(p, r, 1.38888888888888889e-03f);
+    p = fmaf(p, r, 8.33333333333333333e-03f);
+    p = fmaf(p, r, 4.16666666666666667e-02f);
+    p = fmaf(p, r, 1.66666666666666667e-01f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    int n = (int)nf;
+    if (n > 127) {
+        p = p * 2.0f;
+        n -= 1;
+    }
+    return p * __uint_as_float((uint32_t)(n + 127) << 23);
+}
+
+// ---------------------------------------------------------------------------
+// Paged GQA decode attention, split over 256-token chunks.
+//
+// grid = (chunks, B * hkv), 256 threads: one workgroup per (sequence, KV
+// head, chunk) serves all GQ query heads of the group, so every K/V row is
+// read once per group.  Phase 1: thread t owns token t of the chunk and runs
+// the canonical score chain over d for the GQ heads (query rows read as
+// workgroup-uniform values).  Phase 2: per head the chunk max (exact in any
+// order), p_t = lgx_expf(s_t - m), and the halving-tree sum of the 256 slots.
+// Phase 3: thread (i, head group) runs the canonical chain over the chunk's
+// tokens, o[i] = fmaf(p_t, V_t[i], o[i]).  Partials (o_c, m_c, l_c) go to
+// `part`; lgx_k_attn_combine merges the chunks.
+// ---------------------------------------------------------------------------
+template <int D, int GQ>
+__device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
+    constexpr int C = LGX_ATTN_CHUNK;
+    constexpr int NG = 256 / D;                   // head groups in phase 3
+    constexpr int KH = (GQ + NG - 1) / NG;        // heads per thread in phase 3
+    __shared__ float p_s[GQ][C];
+    __shared__ float t_s[GQ][C];
+    __shared__ float mx_s[GQ][4];
+    __shared__ int pg_s[C / LGX_PAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = blockIdx.x, bg = blockIdx.y;
+    const int b = bg / a.hkv, g = bg - b * a.hkv;
+    const int L = min(a.seq_len[b], a.maxlen);
+    const int t0 = c * C;
+    if (t0 >= L) return;                          // whole workgroup: chunk past the end
+    const int n = min(C, L - t0);
+    const int h0 = g * GQ;
+    if (tid < C / LGX_PAGE) {
+        int pg = 0;
+        if (t0 + tid * LGX_PAGE < L) pg = a.page_table[(int64_t)b * a.maxp + t0 / LGX_PAGE + tid];
+        pg_s[tid] = min(max(pg, 0), a.num_pages - 1);
+    }
+    __syncthreads();
+
+    // phase 1: scores
+    float s[GQ];
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) s[h] = 0.0f;
+    const bool valid = tid < n;
+    if (valid) {
+        const uint4* kr = (const uint4*)(a.kpages +
+                                         (((int64_t)pg_s[tid >> 4] * a.hkv + g) * LGX_PAGE + (tid & 15)) * D);
+        const float* qb = a.q + ((int64_t)b * a.hq + h0) * D;
+#pragma unroll 2
+        for (int j = 0; j < D / 8; ++j) {
+            const uint4 kv = kr[j];
+            const float kf[8] = {h2f(kv.x & 0xffffu), h2f(kv.x >> 16), h2f(kv.y & 0xffffu),
+                                 h2f(kv.y >> 16),     h2f(kv.z & 0xffffu), h2f(kv.z >> 16),
+                                 h2f(kv.w & 0xffffu), h2f(kv.w >> 16)};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+#pragma unroll
+                for (int h = 0; h < GQ; ++h) s[h] = fmaf(qb[h * D + 8 * j + e], kf[e], s[h]);
+            }
+        }
+    }
+    // phase 2: max, exp, halving-tree sum
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) {
+        s[h] = valid ? s[h] * a.scale : -__builtin_inff();
+        float m = s[h];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, shfl_xor_f(m, o));
+        if (lane == 0) mx_s[h][wave] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) {
+        const float m = fmaxf(fmaxf(mx_s[h][0], mx_s[h][1]), fmaxf(mx_s[h][2], mx_s[h][3]));
+        const float p = valid ? lgx_expf(s[h] - m) : 0.0f;
+        p_s[h][tid] = p;
+        t_s[h][tid] = p;
+    }
+    __syncthreads();
+    if (tid < 128) {
+#pragma unroll
+        for (int h = 0; h < GQ; ++h) t_s[h][tid] = t_s[h][tid] + t_s[h][tid + 128];
+    }
+    __syncthreads();
+    if (tid < 64) {
+        float l[GQ];
+#pragma unroll
+        for (int h = 0; h < GQ; ++h) l[h] = t_s[h][tid] + t_s[h][tid + 64];
+#pragma unroll
+        for (int s2 = 32; s2 >= 1; s2 >>= 1) {
+#pragma unroll
+            for (int h = 0; h < GQ; ++h) l[h] = l[h] + __shfl_down(l[h], s2, 64);
+        }
+        if (tid == 0) {
+#pragma unroll
+            for (int h = 0; h < GQ; ++h) {
+                const float m = fmaxf(fmaxf(mx_s[h][0], mx_s[h][1]), fmaxf(mx_s[h][2], mx_s[h][3]));
+                float* pp = a.part + (((int64_t)b * a.hq + h0 + h) * a.nchunk + c) * (D + 2);
+                pp[D] = m;
+                pp[D + 1] = l[h];
+            }
+        }
+    }
+    // phase 3: o_c[i] = chain_t fmaf(p_t, V_t[i], o)
+    const int i = tid % D, hg = tid / D;
+    float o[KH];
+#pragma unroll
+    for (int k = 0; k < KH; ++k) o[k] = 0.0f;
+    const uint16_t* vb = a.vpages + (int64_t)g * LGX_PAGE * D + i;
+    for (int t = 0; t < n; ++t) {
+        const float v = h2f(vb[((int64_t)pg_s[t >> 4] * a.hkv * LGX_PAGE + (t & 15)) * D]);
+#pragma unroll
+        for (int k = 0; k < KH; ++k) {
+            const int h = hg + NG * k;
+            if (h < GQ) o[k] = fmaf(p_s[h][t], v, o[k]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < KH; ++k) {
+        const int h = hg + NG * k;
+        if (h < GQ) a.part[(((int64_t)b * a.hq + h0 + h) * a.nchunk + c) * (D + 2) + i] = o[k];
+    }
+}
+
+// Merge of the chunk partials of one (sequence, query head): M = max m_c,
+// w_c = lgx_expf(m_c - M), L = chain fmaf(w_c, l_c), O[i] = chain
+// fmaf(w_c, o_c[i]), out = O / L (0 for an empty sequence).
+template <int D>
+__device__ __forceinline__ void attn_combine_body(const lgx_attn_args& a) {
+    const int bh = blockIdx.x, i = threadIdx.x;
+    const int b = bh / a.hq;
+    const int L = min(a.seq_len[b], a.maxlen);
+    const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
+    const float* pp = a.part + (int64_t)bh * a.nchunk * (D + 2);
+    float M = -__builtin_inff();
+    for (int c = 0; c < nc; ++c) M = fmaxf(M, pp[c * (D + 2) + D]);
+    float Ls = 0.0f, O = 0.0f;
+    for (int c = 0; c < nc; ++c) {
+        const float w = lgx_expf(pp[c * (D + 2) + D] - M);
+        Ls = fmaf(w, pp[c * (D + 2) + D + 1], Ls);
+        O = fmaf(w, pp[c * (D + 2) + i], O);
+    }
+    a.out[(int64_t)bh * D + i] = nc > 0 ? O / Ls : 0.0f;
+}
+
+#define LGX_ATTN_KERNELS(D, G)                                                                    \
+    extern "C" __global__ __launch_bounds__(256) void lgx_k_attn_chunk_d##D##_g##G(              \
+        const lgx_attn_args a) {                                                                 \
+        attn_chunk_body<D, G>(a);                                                                \
+    }
+LGX_ATTN_KERNELS(64, 1)
+LGX_ATTN_KERNELS(64, 2)
+LGX_ATTN_KERNELS(64, 3)
+LGX_ATTN_KERNELS(64, 4)
+LGX_ATTN_KERNELS(64, 5)
+LGX_ATTN_KERNELS(64, 6)
+LGX_ATTN_KERNELS(64, 7)
+LGX_ATTN_KERNELS(64, 8)
+LGX_ATTN_KERNELS(128, 1)
+LGX_ATTN_KERNELS(128, 2)
+LGX_ATTN_KERNELS(128, 3)
+LGX_ATTN_KERNELS(128, 4)
+LGX_ATTN_KERNELS(128, 5)
+LGX_ATTN_KERNELS(128, 6)
+LGX_ATTN_KERNELS(128, 7)
+LGX_ATTN_KERNELS(128, 8)
+
+extern "C" __global__ __launch_bounds__(128) void lgx_k_attn_combine_d128(const lgx_attn_args a) {
+    attn_combine_body<128>(a);
+}
+extern "C" __global__ __launch_bounds__(64) void lgx_k_attn_combine_d64(const lgx_attn_args a) {
+    attn_combine_body<64>(a);
+}

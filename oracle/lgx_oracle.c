@@ -338,3 +338,97 @@ void orc_q8_gemm(const int8_t* qs, const uint16_t* d, int32_t n, int32_t k,
         y[(int64_t)mi * n + row] = orc_tree_sum(part, g);
     }
 }
+
+/* ------------------------------------------------------------------ */
+/* Paged KV cache + GQA decode attention                               */
+/* ------------------------------------------------------------------ */
+/* Cache layout: K and V pages are binary16 [num_pages][hkv][16][d]; token t
+ * of sequence b lives in page page_table[b*maxp + t/16], slot t%16. */
+#define ORC_PAGE 16
+#define ORC_ATTN_CHUNK 256
+
+static inline const uint16_t* kv_row(const uint16_t* pages, const int32_t* page_table,
+                                     int32_t b, int32_t maxp, int32_t t, int32_t g,
+                                     int32_t hkv, int32_t d) {
+    int32_t page = page_table[(int64_t)b * maxp + t / ORC_PAGE];
+    return pages + (((int64_t)page * hkv + g) * ORC_PAGE + (t % ORC_PAGE)) * d;
+}
+
+/* Halving tree over a power-of-two count: for s = n/2, n/4, ..., 1:
+ * p[j] = p[j] + p[j+s] for j < s.  Returns p[0]; modifies p. */
+float orc_halving_sum(float* p, int32_t n) {
+    for (int32_t s = n / 2; s >= 1; s /= 2)
+        for (int32_t j = 0; j < s; ++j) p[j] = p[j] + p[j + s];
+    return p[0];
+}
+
+/* Canonical decode attention for one (b, h) over seq_len[b] cached tokens:
+ *   s_t  = chain_i fmaf(q[i], f32(K_t[i]), acc) from +0, then * scale
+ *   chunks of 256 tokens: m_c = max s_t, p_t = orc_expf(s_t - m_c),
+ *   l_c  = halving sum over the chunk's 256 slots (0 past the end),
+ *   o_c[i] = chain_t fmaf(p_t, f32(V_t[i]), acc) from +0, t ascending
+ *   M = max m_c, w_c = orc_expf(m_c - M),
+ *   L = chain_c fmaf(w_c, l_c, L), O[i] = chain_c fmaf(w_c, o_c[i], O[i]),
+ *   out[i] = O[i] / L (0 for an empty sequence). */
+void orc_gqa_decode_attn(const float* q, const uint16_t* kpages, const uint16_t* vpages,
+                         const int32_t* page_table, const int32_t* seq_len, int32_t B,
+                         int32_t hq, int32_t hkv, int32_t d, int32_t maxp, float scale,
+                         float* out) {
+    int32_t gq = hq / hkv;
+#pragma omp parallel for schedule(dynamic)
+    for (int64_t bh = 0; bh < (int64_t)B * hq; ++bh) {
+        int32_t b = (int32_t)(bh / hq), h = (int32_t)(bh % hq), g = h / gq;
+        int32_t L = seq_len[b];
+        const float* qv = q + bh * d;
+        int32_t nc = (L + ORC_ATTN_CHUNK - 1) / ORC_ATTN_CHUNK;
+        float* s = (float*)malloc(sizeof(float) * ORC_ATTN_CHUNK);
+        float* pbuf = (float*)malloc(sizeof(float) * ORC_ATTN_CHUNK);
+        float* oc = (float*)calloc((size_t)nc * d, sizeof(float));
+        float* mc = (float*)malloc(sizeof(float) * (nc > 0 ? nc : 1));
+        float* lc = (float*)malloc(sizeof(float) * (nc > 0 ? nc : 1));
+        for (int32_t c = 0; c < nc; ++c) {
+            int32_t t0 = c * ORC_ATTN_CHUNK, n = L - t0 < ORC_ATTN_CHUNK ? L - t0 : ORC_ATTN_CHUNK;
+            float m = -INFINITY;
+            for (int32_t j = 0; j < n; ++j) {
+                const uint16_t* kr = kv_row(kpages, page_table, b, maxp, t0 + j, g, hkv, d);
+                float acc = 0.0f;
+                for (int32_t i = 0; i < d; ++i) acc = fmaf(qv[i], orc_f16_to_f32(kr[i]), acc);
+                s[j] = acc * scale;
+                if (s[j] > m) m = s[j];
+            }
+            for (int32_t j = 0; j < ORC_ATTN_CHUNK; ++j) pbuf[j] = j < n ? orc_expf(s[j] - m) : 0.0f;
+            for (int32_t i = 0; i < d; ++i) {
+                float acc = 0.0f;
+                for (int32_t j = 0; j < n; ++j) {
+                    const uint16_t* vr = kv_row(vpages, page_table, b, maxp, t0 + j, g, hkv, d);
+                    acc = fmaf(pbuf[j], orc_f16_to_f32(vr[i]), acc);
+                }
+                oc[(int64_t)c * d + i] = acc;
+            }
+            mc[c] = m;
+            lc[c] = orc_halving_sum(pbuf, ORC_ATTN_CHUNK);
+        }
+        float M = -INFINITY;
+        for (int32_t c = 0; c < nc; ++c) if (mc[c] > M) M = mc[c];
+        float Ls = 0.0f;
+        for (int32_t c = 0; c < nc; ++c) Ls = fmaf(orc_expf(mc[c] - M), lc[c], Ls);
+        for (int32_t i = 0; i < d; ++i) {
+            float O = 0.0f;
+            for (int32_t c = 0; c < nc; ++c) O = fmaf(orc_expf(mc[c] - M), oc[(int64_t)c * d + i], O);
+            out[bh * d + i] = nc > 0 ? O / Ls : 0.0f;
+        }
+        free(s); free(pbuf); free(oc); free(mc); free(lc);
+    }
+}
+
+/* Random page table: the B * maxp page ids are a seeded permutation of
+ * 0..B*maxp-1 (Fisher-Yates with the multiply-high bounded draw). */
+void orc_gen_page_table(uint64_t seed, uint64_t stream, int32_t B, int32_t maxp, int32_t* pt) {
+    int64_t n = (int64_t)B * maxp;
+    uint64_t base = orc_stream_base(seed, stream);
+    for (int64_t i = 0; i < n; ++i) pt[i] = (int32_t)i;
+    for (int64_t i = n - 1; i > 0; --i) {
+        int64_t j = (int64_t)below32(stream_at(base, (uint64_t)(n - 1 - i)), (uint32_t)(i + 1));
+        int32_t tmp = pt[i]; pt[i] = pt[j]; pt[j] = tmp;
+    }
+}

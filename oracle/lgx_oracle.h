@@ -80,6 +80,14 @@ void orc_q8_gemm(const int8_t* qs, const uint16_t* d, int32_t n, int32_t k,
                  const int8_t* xq, const uint16_t* xd, int32_t m, float* y);
 float orc_tree_sum(float* p, int32_t g);
 
+/* ---- paged KV cache + GQA decode attention ---- */
+float orc_halving_sum(float* p, int32_t n);
+void orc_gqa_decode_attn(const float* q, const uint16_t* kpages, const uint16_t* vpages,
+                         const int32_t* page_table, const int32_t* seq_len, int32_t B,
+                         int32_t hq, int32_t hkv, int32_t d, int32_t maxp, float scale,
+                         float* out);
+void orc_gen_page_table(uint64_t seed, uint64_t stream, int32_t B, int32_t maxp, int32_t* pt);
+
 #ifdef __cplusplus
 }
 #endif

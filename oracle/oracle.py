@@ -66,6 +66,10 @@ def lib():
             "orc_q8_blockdots": (None, [_P, _I32, _I32, _P, _P]),
             "orc_q8_gemm": (None, [_P, _P, _I32, _I32, _P, _P, _I32, _P]),
             "orc_tree_sum": (C.c_float, [_P, _I32]),
+            "orc_halving_sum": (C.c_float, [_P, _I32]),
+            "orc_gqa_decode_attn": (None, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32,
+                                           C.c_float, _P]),
+            "orc_gen_page_table": (None, [_U64, _U64, _I32, _I32, _P]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -234,3 +238,47 @@ def q8_gemm(qs, d, xq, xd):
     y = np.empty((m, n), np.float32)
     lib().orc_q8_gemm(_ptr(qs), _ptr(d), n, k, _ptr(xq), _ptr(xd), m, _ptr(y))
     return y
+
+
+# ---- paged KV cache + attention --------------------------------------------
+
+PAGE = 16
+ATTN_CHUNK = 256
+
+
+def attn_scale(d: int) -> np.float32:
+    return np.float32(1.0 / np.sqrt(np.float64(d)))
+
+
+def halving_sum(p) -> np.float32:
+    p = _c(p, np.float32).copy()
+    return np.float32(lib().orc_halving_sum(_ptr(p), p.size))
+
+
+def gen_page_table(seed: int, stream: int, B: int, maxp: int) -> np.ndarray:
+    out = np.empty((B, maxp), np.int32)
+    lib().orc_gen_page_table(seed, stream, B, maxp, _ptr(out))
+    return out
+
+
+def gqa_decode_attn(q, kpages, vpages, page_table, seq_len, scale=None):
+    """q [B][hq][d] f32; k/v pages [P][hkv][16][d] f16 bits; page_table [B][maxp]."""
+    q = _c(q, np.float32)
+    kpages = _c(kpages, np.uint16)
+    vpages = _c(vpages, np.uint16)
+    page_table = _c(page_table, np.int32)
+    seq_len = _c(seq_len, np.int32)
+    B, hq, d = q.shape
+    hkv = kpages.shape[1]
+    maxp = page_table.shape[1]
+    scale = attn_scale(d) if scale is None else np.float32(scale)
+    out = np.empty((B, hq, d), np.float32)
+    lib().orc_gqa_decode_attn(_ptr(q), _ptr(kpages), _ptr(vpages), _ptr(page_table),
+                              _ptr(seq_len), B, hq, hkv, d, maxp, float(scale), _ptr(out))
+    return out
+
+
+def paged_to_dense(pages, page_table, b, L):
+    """[L][hkv][d] view of sequence b's cached rows (test helper)."""
+    rows = [pages[page_table[b, t // PAGE], :, t % PAGE, :] for t in range(L)]
+    return np.stack(rows) if rows else np.zeros((0,) + pages.shape[1:2] + pages.shape[3:], pages.dtype)

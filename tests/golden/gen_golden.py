@@ -60,6 +60,28 @@ def case(rng, n, k, m):
                 y_q8q8=y_q8q8, y_q8q8_abs=y_q8q8_abs, y_f32=y_f32, y_f32_abs=y_f32_abs)
 
 
+def attn_case(rng, B, hq, hkv, d, lens, maxp):
+    """Paged fp16 KV cache with a random page table, float64 softmax attention."""
+    npages = B * maxp
+    k = rng.standard_normal((npages, hkv, 16, d)).astype(np.float16)
+    v = rng.standard_normal((npages, hkv, 16, d)).astype(np.float16)
+    pt = rng.permutation(npages).astype(np.int32).reshape(B, maxp)
+    q = rng.standard_normal((B, hq, d)).astype(np.float32)
+    out = np.zeros((B, hq, d))
+    gq = hq // hkv
+    for b in range(B):
+        L = lens[b]
+        kk = np.stack([k[pt[b, t // 16], :, t % 16, :] for t in range(L)]).astype(np.float64)
+        vv = np.stack([v[pt[b, t // 16], :, t % 16, :] for t in range(L)]).astype(np.float64)
+        for h in range(hq):
+            g = h // gq
+            sc = kk[:, g, :] @ q[b, h].astype(np.float64) / np.sqrt(d)
+            w = np.exp(sc - sc.max())
+            out[b, h] = (w[:, None] * vv[:, g, :]).sum(0) / w.sum()
+    return dict(q=q, k=k.view(np.uint16), v=v.view(np.uint16), pt=pt,
+                lens=np.asarray(lens, np.int32), out=out)
+
+
 def main():
     rng = np.random.default_rng(20261201)
     out = {}
@@ -75,6 +97,8 @@ def main():
     e[3] = np.float32(3e-7) * np.arange(-16, 16, dtype=np.float32)
     eq, ed = quantize_q8_0_np(e)
     out.update(edge_x=e, edge_q=eq, edge_d=ed)
+    for key, val in attn_case(rng, 3, 6, 2, 64, [1, 300, 700], 48).items():
+        out[f"attn_{key}"] = val
     path = os.path.join(HERE, "q8_golden.npz")
     np.savez_compressed(path, **out)
     print(path, os.path.getsize(path), "bytes")

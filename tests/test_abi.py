@@ -105,11 +105,11 @@ def test_every_host_kernel_exists_in_code_object():
     import logicaffeine_amd as lgx
 
     src = open(os.path.join(ROOT, "logicaffeine_amd", "csrc", "lgx_host.cpp")).read()
-    table = src[src.index("kKernelNames[K_COUNT] = {"):]
+    table = src[src.index("kKernelNames[] = {"):]
     table = table[:table.index("};")]
     names = re.findall(r'"(lgx_k_[a-z0-9_]+)"', table)
-    enum = src[src.index("enum Kern {"):src.index("K_COUNT")]
-    assert len(names) == len(re.findall(r"\bK_[A-Z0-9_]+,", enum))
+    # the count against the kernel enum is a static_assert in lgx_host.cpp
+    assert len(names) == len(set(names)) > 20
     readelf = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib", "llvm", "bin",
                            "llvm-readelf")
     syms = subprocess.run([readelf, "-sW", lgx.HSACO_PATH], capture_output=True,

@@ -1,0 +1,108 @@
+"""Parity of the paged GQA decode attention kernels with the CPU oracle.
+
+The canonical schedule (256-token chunks, sequential score and PV chains,
+halving-tree sums, log-sum-exp merge in chunk order) is followed by both, so
+outputs are compared bit-for-bit; the float64 golden fixture checks the
+north star's 2e-3 tolerance."""
+import numpy as np
+import pytest
+
+import logicaffeine_amd as lgx
+
+pytestmark = pytest.mark.gpu
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def make_cache(B, hkv, d, lens, seed):
+    rng = np.random.default_rng(seed)
+    maxp = max(1, -(-max(lens) // 16))
+    npages = B * maxp
+    k = rng.standard_normal((npages, hkv, 16, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((npages, hkv, 16, d)).astype(np.float16).view(np.uint16)
+    pt = rng.permutation(npages).astype(np.int32).reshape(B, maxp)
+    return k, v, pt, maxp
+
+
+def run(ctx, q, k, v, pt, lens, max_seq_len=None):
+    lens = np.asarray(lens, np.int32)
+    msl = int(max_seq_len or max(1, lens.max()))
+    return host(ctx.gqa_decode_attn(ctx.to_device(q), ctx.to_device(k), ctx.to_device(v),
+                                    ctx.to_device(pt), ctx.to_device(lens), msl))
+
+
+def test_golden_fixture(ctx, orc, golden):
+    out = run(ctx, golden["attn_q"], golden["attn_k"], golden["attn_v"], golden["attn_pt"],
+              golden["attn_lens"])
+    ref = orc.gqa_decode_attn(golden["attn_q"], golden["attn_k"], golden["attn_v"],
+                              golden["attn_pt"], golden["attn_lens"])
+    assert np.array_equal(out, ref)
+    f64 = golden["attn_out"]
+    assert np.all(np.abs(out - f64) <= 2e-3 * (np.abs(f64) + 1e-2))
+
+
+@pytest.mark.parametrize("L", [512, 4096])
+def test_config2_uniform_bit_exact(ctx, orc, L):
+    B, hq, hkv, d = 16, 12, 2, 128
+    lens = [L] * B
+    k, v, pt, _ = make_cache(B, hkv, d, lens, seed=L)
+    q = orc.gen_normal_f32(2, 10 + L, (B, hq, d))
+    out = run(ctx, q, k, v, pt, lens)
+    assert np.array_equal(out, orc.gqa_decode_attn(q, k, v, pt, np.asarray(lens, np.int32)))
+
+
+def test_config2_ragged_long_bit_exact(ctx, orc):
+    B, hq, hkv, d = 4, 12, 2, 128
+    lens = list(orc.gen_below_i32(2, 30, 32768 - 256 + 1, (B,)) + 256)
+    lens[0] = 32768
+    k, v, pt, _ = make_cache(B, hkv, d, lens, seed=3)
+    q = orc.gen_normal_f32(2, 31, (B, hq, d))
+    out = run(ctx, q, k, v, pt, lens)
+    assert np.array_equal(out, orc.gqa_decode_attn(q, k, v, pt, np.asarray(lens, np.int32)))
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (28, 4, 128), (8, 8, 64), (8, 1, 128)])
+def test_head_layouts_bit_exact(ctx, orc, hq, hkv, d):
+    B = 5
+    lens = [1, 16, 255, 257, 1500]
+    k, v, pt, _ = make_cache(B, hkv, d, lens, seed=hq * d)
+    q = orc.gen_normal_f32(3, hq + d, (B, hq, d))
+    out = run(ctx, q, k, v, pt, lens)
+    assert np.array_equal(out, orc.gqa_decode_attn(q, k, v, pt, np.asarray(lens, np.int32)))
+    # single cached token: the output is that token's V row exactly
+    for h in range(hq):
+        assert np.array_equal(out[0, h], orc.f16_to_f32(v[pt[0, 0], h // (hq // hkv), 0]))
+
+
+def test_lengths_clamped_to_max_seq_len(ctx, orc):
+    B, hq, hkv, d = 3, 6, 2, 64
+    lens = np.array([700, 100, 0], np.int32)
+    k, v, pt, maxp = make_cache(B, hkv, d, [700, 700, 700], seed=9)
+    q = orc.gen_normal_f32(3, 77, (B, hq, d))
+    out = run(ctx, q, k, v, pt, lens, max_seq_len=300)
+    ref = orc.gqa_decode_attn(q, k, v, pt, np.minimum(lens, 300))
+    assert np.array_equal(out, ref)
+    assert np.all(out[2] == 0.0)                      # empty sequence
+
+
+def test_attention_argument_errors(ctx, orc):
+    t = ctx.torch
+    q = t.zeros((1, 6, 96), dtype=t.float32, device=ctx.dev)
+    pages = t.zeros((4, 2, 16, 96), dtype=t.int16, device=ctx.dev)
+    pt = t.zeros((1, 4), dtype=t.int32, device=ctx.dev)
+    sl = t.ones(1, dtype=t.int32, device=ctx.dev)
+    with pytest.raises(lgx.LgxError) as ei:
+        ctx.gqa_decode_attn(q, pages, pages, pt, sl, 16)
+    assert ei.value.status_name == "LGX_UNSUPPORTED"
+    q = t.zeros((1, 6, 64), dtype=t.float32, device=ctx.dev)
+    pages = t.zeros((4, 2, 16, 64), dtype=t.int16, device=ctx.dev)
+    with pytest.raises(lgx.LgxError) as ei:
+        ctx.gqa_decode_attn(q, pages, pages, pt, sl, 65)
+    assert ei.value.status_name == "LGX_OUT_OF_BOUNDS"
+    q3 = t.zeros((1, 6, 64), dtype=t.float32, device=ctx.dev)
+    pages3 = t.zeros((4, 4, 16, 64), dtype=t.int16, device=ctx.dev)
+    with pytest.raises(lgx.LgxError) as ei:                 # 6 / 4 heads
+        ctx.gqa_decode_attn(q3, pages3, pages3, pt, sl, 16)
+    assert ei.value.status_name == "LGX_INVALID_ARGUMENT"
