@@ -432,3 +432,327 @@ void orc_gen_page_table(uint64_t seed, uint64_t stream, int32_t B, int32_t maxp,
         int32_t tmp = pt[i]; pt[i] = pt[j]; pt[j] = tmp;
     }
 }
+
+/* ------------------------------------------------------------------ */
+/* Decode-step glue                                                    */
+/* ------------------------------------------------------------------ */
+static int32_t pow2_at_least(int32_t n) {
+    int32_t p = 1;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+/* RMSNorm: S = halving sum of x_i*x_i over the next power of two >= h (zeros
+ * past h), ms = S / h, r = 1 / sqrtf(ms + eps), y_i = (x_i * r) * w_i. */
+void orc_rmsnorm(const float* x, const float* w, int32_t m, int32_t h, float eps, float* y) {
+    int32_t n2 = pow2_at_least(h);
+    float* t = (float*)malloc(sizeof(float) * n2);
+    for (int32_t r = 0; r < m; ++r) {
+        const float* xr = x + (int64_t)r * h;
+        for (int32_t i = 0; i < n2; ++i) t[i] = i < h ? xr[i] * xr[i] : 0.0f;
+        float ms = orc_halving_sum(t, n2) / (float)h;
+        float rr = 1.0f / sqrtf(ms + eps);
+        for (int32_t i = 0; i < h; ++i) y[(int64_t)r * h + i] = (xr[i] * rr) * w[i];
+    }
+    free(t);
+}
+
+/* RoPE tables: angle = pos * theta^(-2i/d) in binary64, rounded to binary32
+ * after cos / sin.  cos_t, sin_t are [max_seq][d/2]. */
+void orc_rope_tables(int32_t max_seq, int32_t d, double theta, float* cos_t, float* sin_t) {
+    for (int32_t p = 0; p < max_seq; ++p)
+        for (int32_t i = 0; i < d / 2; ++i) {
+            double inv = pow(theta, -(2.0 * i) / (double)d);
+            double ang = (double)p * inv;
+            cos_t[(int64_t)p * (d / 2) + i] = (float)cos(ang);
+            sin_t[(int64_t)p * (d / 2) + i] = (float)sin(ang);
+        }
+}
+
+/* Rotate-half RoPE of nheads vectors of length d in place:
+ * x[i] <- x[i]*c - x[i+d/2]*s, x[i+d/2] <- x[i+d/2]*c + x[i]*s. */
+void orc_rope(float* x, int32_t nheads, int32_t d, const float* cos_row, const float* sin_row) {
+    for (int32_t hh = 0; hh < nheads; ++hh) {
+        float* v = x + (int64_t)hh * d;
+        for (int32_t i = 0; i < d / 2; ++i) {
+            float a = v[i], b = v[i + d / 2], c = cos_row[i], s = sin_row[i];
+            float t0 = a * c, t1 = b * s, t2 = b * c, t3 = a * s;
+            v[i] = t0 - t1;
+            v[i + d / 2] = t2 + t3;
+        }
+    }
+}
+
+/* a_i = silu(g_i) * u_i for gu = [gate(0..I) | up(0..I)]. */
+void orc_swiglu(const float* gu, int32_t m, int32_t inter, float* a) {
+    for (int32_t r = 0; r < m; ++r)
+        for (int32_t i = 0; i < inter; ++i)
+            a[(int64_t)r * inter + i] = orc_silu(gu[(int64_t)r * 2 * inter + i]) *
+                                        gu[(int64_t)r * 2 * inter + inter + i];
+}
+
+/* First index of the maximum: NaN entries are skipped, ties go to the lowest
+ * index, -0 == +0; an all-NaN row gives 0. */
+int32_t orc_argmax(const float* x, int32_t n) {
+    int32_t best = -1;
+    for (int32_t i = 0; i < n; ++i)
+        if (x[i] == x[i] && (best < 0 || x[i] > x[best])) best = i;
+    return best < 0 ? 0 : best;
+}
+
+/* logits[r][v] = canonical dot of binary32 x[r] with binary16 row E[v]:
+ * ranges of 1024 elements, each a sequential fmaf chain from +0, then the
+ * pairwise tree over ranges. */
+void orc_lm_head_f16(const float* x, int32_t m, const uint16_t* E, int32_t V, int32_t h,
+                     float* logits) {
+    int32_t g = (h + 1023) / 1024;
+#pragma omp parallel for schedule(static)
+    for (int32_t v = 0; v < V; ++v) {
+        float part[64];
+        const uint16_t* er = E + (int64_t)v * h;
+        for (int32_t r = 0; r < m; ++r) {
+            const float* xr = x + (int64_t)r * h;
+            for (int32_t q = 0; q < g; ++q) {
+                float acc = 0.0f;
+                int32_t k1 = (q + 1) * 1024 < h ? (q + 1) * 1024 : h;
+                for (int32_t k = q * 1024; k < k1; ++k) acc = fmaf(xr[k], orc_f16_to_f32(er[k]), acc);
+                part[q] = acc;
+            }
+            logits[(int64_t)r * V + v] = orc_tree_sum(part, g);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* Random-init Qwen2-shaped Q8_0 model                                 */
+/* ------------------------------------------------------------------ */
+/* Seed streams (one per tensor; a Q8_0 matrix uses stream s for its quants
+ * and s+1 for its scales):
+ *   1        embedding, binary16 N(0, emb_sigma)       [vocab][hidden]
+ *   2, 3     lm_head Q8_0 (untied models only)          [vocab][hidden]
+ *   L+0,1    Wqkv Q8_0, rows q heads | k heads | v heads [(hq+2hkv)d][hidden]
+ *   L+2,3    Wo Q8_0                                    [hidden][hq d]
+ *   L+4,5    Wgu Q8_0, rows gate | up                   [2 inter][hidden]
+ *   L+6,7    Wdown Q8_0                                 [hidden][inter]
+ *   L+8      qkv bias, binary32 N(0, 0.02)              [(hq+2hkv)d]
+ * with L = 1000 + 16 * layer.  RMSNorm weights are 1.0. */
+struct orc_model {
+    orc_qwen_config c;
+    uint64_t seed;
+    int32_t qkv_n, maxp;
+    uint16_t* emb;
+    int8_t* lm_qs;
+    uint16_t* lm_d;
+    int8_t **qkv_qs, **o_qs, **gu_qs, **dn_qs;
+    uint16_t **qkv_d, **o_d, **gu_d, **dn_d;
+    float** bias;
+    float* ones;
+    float *cos_t, *sin_t;
+    uint16_t **kc, **vc;   /* per layer paged [max_batch*maxp][hkv][16][d] */
+    int32_t* page_table;   /* identity: slot b page p -> b*maxp + p */
+    int32_t* seq_len;
+};
+
+static void* xmalloc(size_t n) {
+    void* p = malloc(n ? n : 1);
+    if (!p) abort();
+    return p;
+}
+
+static void gen_q8(uint64_t seed, uint64_t stream, int64_t n, int64_t k, int8_t** qs,
+                   uint16_t** d) {
+    *qs = (int8_t*)xmalloc((size_t)(n * k));
+    *d = (uint16_t*)xmalloc((size_t)(n * (k / 32)) * 2);
+    /* element-indexed streams, so chunks can be generated in parallel */
+    uint64_t bq = orc_stream_base(seed, stream), bd = orc_stream_base(seed, stream + 1);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n * k; ++i)
+        (*qs)[i] = (int8_t)((int32_t)below32(stream_at(bq, (uint64_t)i), 255u) - 127);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n * (k / 32); ++i)
+        (*d)[i] = orc_f32_to_f16((float)(fabs(0.02 * normal_at(bd, (uint64_t)i)) / 127.0));
+}
+
+orc_model* orc_model_create(const orc_qwen_config* cfg, uint64_t seed) {
+    orc_model* m = (orc_model*)calloc(1, sizeof(orc_model));
+    m->c = *cfg;
+    m->seed = seed;
+    const orc_qwen_config* c = cfg;
+    int32_t H = c->hidden, I = c->inter, d = c->head_dim, hq = c->n_heads, hkv = c->n_kv;
+    m->qkv_n = (hq + 2 * hkv) * d;
+    m->maxp = (c->max_seq + ORC_PAGE - 1) / ORC_PAGE;
+    m->emb = (uint16_t*)xmalloc((size_t)c->vocab * H * 2);
+    {
+        uint64_t be = orc_stream_base(seed, 1);
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < (int64_t)c->vocab * H; ++i)
+            m->emb[i] = orc_f32_to_f16((float)(c->emb_sigma * normal_at(be, (uint64_t)i)));
+    }
+    if (!c->tied) gen_q8(seed, 2, c->vocab, H, &m->lm_qs, &m->lm_d);
+    int32_t nl = c->n_layers;
+    m->qkv_qs = (int8_t**)calloc(nl, sizeof(void*));
+    m->o_qs = (int8_t**)calloc(nl, sizeof(void*));
+    m->gu_qs = (int8_t**)calloc(nl, sizeof(void*));
+    m->dn_qs = (int8_t**)calloc(nl, sizeof(void*));
+    m->qkv_d = (uint16_t**)calloc(nl, sizeof(void*));
+    m->o_d = (uint16_t**)calloc(nl, sizeof(void*));
+    m->gu_d = (uint16_t**)calloc(nl, sizeof(void*));
+    m->dn_d = (uint16_t**)calloc(nl, sizeof(void*));
+    m->bias = (float**)calloc(nl, sizeof(void*));
+    m->kc = (uint16_t**)calloc(nl, sizeof(void*));
+    m->vc = (uint16_t**)calloc(nl, sizeof(void*));
+    size_t kv_elems = (size_t)c->max_batch * m->maxp * hkv * ORC_PAGE * d;
+    for (int32_t l = 0; l < nl; ++l) {
+        uint64_t L = 1000 + 16 * (uint64_t)l;
+        gen_q8(seed, L + 0, m->qkv_n, H, &m->qkv_qs[l], &m->qkv_d[l]);
+        gen_q8(seed, L + 2, H, hq * d, &m->o_qs[l], &m->o_d[l]);
+        gen_q8(seed, L + 4, 2 * I, H, &m->gu_qs[l], &m->gu_d[l]);
+        gen_q8(seed, L + 6, H, I, &m->dn_qs[l], &m->dn_d[l]);
+        m->bias[l] = (float*)xmalloc(sizeof(float) * m->qkv_n);
+        orc_gen_normal_f32(seed, L + 8, 0.02, m->bias[l], m->qkv_n);
+        m->kc[l] = (uint16_t*)calloc(kv_elems, 2);
+        m->vc[l] = (uint16_t*)calloc(kv_elems, 2);
+    }
+    int32_t mx = H > I ? H : I;
+    m->ones = (float*)xmalloc(sizeof(float) * mx);
+    for (int32_t i = 0; i < mx; ++i) m->ones[i] = 1.0f;
+    m->cos_t = (float*)xmalloc(sizeof(float) * (size_t)c->max_seq * (d / 2));
+    m->sin_t = (float*)xmalloc(sizeof(float) * (size_t)c->max_seq * (d / 2));
+    orc_rope_tables(c->max_seq, d, c->theta, m->cos_t, m->sin_t);
+    m->page_table = (int32_t*)xmalloc(sizeof(int32_t) * (size_t)c->max_batch * m->maxp);
+    for (int64_t i = 0; i < (int64_t)c->max_batch * m->maxp; ++i) m->page_table[i] = (int32_t)i;
+    m->seq_len = (int32_t*)calloc(c->max_batch, sizeof(int32_t));
+    return m;
+}
+
+void orc_model_destroy(orc_model* m) {
+    if (!m) return;
+    for (int32_t l = 0; l < m->c.n_layers; ++l) {
+        free(m->qkv_qs[l]); free(m->o_qs[l]); free(m->gu_qs[l]); free(m->dn_qs[l]);
+        free(m->qkv_d[l]); free(m->o_d[l]); free(m->gu_d[l]); free(m->dn_d[l]);
+        free(m->bias[l]); free(m->kc[l]); free(m->vc[l]);
+    }
+    free(m->qkv_qs); free(m->o_qs); free(m->gu_qs); free(m->dn_qs);
+    free(m->qkv_d); free(m->o_d); free(m->gu_d); free(m->dn_d);
+    free(m->bias); free(m->kc); free(m->vc);
+    free(m->emb); free(m->lm_qs); free(m->lm_d); free(m->ones);
+    free(m->cos_t); free(m->sin_t); free(m->page_table); free(m->seq_len);
+    free(m);
+}
+
+int32_t orc_model_seq_len(const orc_model* m, int32_t slot) { return m->seq_len[slot]; }
+
+/* Host copies of the generated tensors, for comparing the device model's own
+ * generator: which = 0 emb, 1 lm q, 2 lm d, 3 qkv q, 4 qkv d, 5 o q, 6 o d,
+ * 7 gu q, 8 gu d, 9 down q, 10 down d, 11 bias.  Returns the pointer. */
+const void* orc_model_tensor(const orc_model* m, int32_t layer, int32_t which) {
+    switch (which) {
+        case 0: return m->emb;
+        case 1: return m->lm_qs;
+        case 2: return m->lm_d;
+        case 3: return m->qkv_qs[layer];
+        case 4: return m->qkv_d[layer];
+        case 5: return m->o_qs[layer];
+        case 6: return m->o_d[layer];
+        case 7: return m->gu_qs[layer];
+        case 8: return m->gu_d[layer];
+        case 9: return m->dn_qs[layer];
+        case 10: return m->dn_d[layer];
+        case 11: return m->bias[layer];
+        default: return NULL;
+    }
+}
+
+/* Copy of the cached K (kv = 0) or V (kv = 1) rows of slot b at layer l,
+ * tokens [0, n): out[n][hkv][d] binary16. */
+void orc_model_kv(const orc_model* m, int32_t layer, int32_t kv, int32_t b, int32_t n,
+                  uint16_t* out) {
+    int32_t hkv = m->c.n_kv, d = m->c.head_dim;
+    const uint16_t* pages = kv ? m->vc[layer] : m->kc[layer];
+    for (int32_t t = 0; t < n; ++t)
+        for (int32_t g = 0; g < hkv; ++g)
+            memcpy(out + ((int64_t)t * hkv + g) * d,
+                   kv_row(pages, m->page_table, b, m->maxp, t, g, hkv, d), (size_t)d * 2);
+}
+
+/* One decode step for nseq sequences: sequence slots[i] consumes tokens[i]
+ * at position seq_len[slot]; returns the greedy next tokens, the final hidden
+ * rows (nullable [nseq][hidden]) and logits (nullable [nseq][vocab]).  Rows
+ * are independent, so any subset of slots can be stepped. */
+void orc_model_step(orc_model* m, int32_t nseq, const int32_t* slots, const int32_t* tokens,
+                    int32_t* next, float* hidden_out, float* logits_out) {
+    const orc_qwen_config* c = &m->c;
+    int32_t H = c->hidden, I = c->inter, d = c->head_dim, hq = c->n_heads, hkv = c->n_kv;
+    int32_t B = nseq, qn = m->qkv_n;
+    float* h = (float*)xmalloc(sizeof(float) * B * H);
+    float* xn = (float*)xmalloc(sizeof(float) * B * (H > I ? H : I));
+    int32_t kmax = H > I ? H : I;
+    if (hq * d > kmax) kmax = hq * d;
+    int8_t* xq = (int8_t*)xmalloc((size_t)B * kmax);
+    uint16_t* xd = (uint16_t*)xmalloc((size_t)B * (kmax / 32) * 2);
+    float* qkv = (float*)xmalloc(sizeof(float) * B * qn);
+    float* q = (float*)xmalloc(sizeof(float) * B * hq * d);
+    float* att = (float*)xmalloc(sizeof(float) * B * hq * d);
+    float* y = (float*)xmalloc(sizeof(float) * B * (2 * I > H ? 2 * I : H));
+    float* a = (float*)xmalloc(sizeof(float) * B * I);
+    int32_t* pt = (int32_t*)xmalloc(sizeof(int32_t) * B * m->maxp);
+    int32_t* lens = (int32_t*)xmalloc(sizeof(int32_t) * B);
+    float scale = (float)(1.0 / sqrt((double)d));
+    for (int32_t i = 0; i < B; ++i) {
+        for (int32_t k = 0; k < H; ++k)
+            h[(int64_t)i * H + k] = orc_f16_to_f32(m->emb[(int64_t)tokens[i] * H + k]);
+        memcpy(pt + (int64_t)i * m->maxp, m->page_table + (int64_t)slots[i] * m->maxp,
+               sizeof(int32_t) * m->maxp);
+        lens[i] = m->seq_len[slots[i]] + 1;
+    }
+    for (int32_t l = 0; l < c->n_layers; ++l) {
+        orc_rmsnorm(h, m->ones, B, H, c->eps, xn);
+        orc_quantize_q8_0(xn, B, H, xq, xd);
+        orc_q8_gemm(m->qkv_qs[l], m->qkv_d[l], qn, H, xq, xd, B, qkv);
+        for (int32_t i = 0; i < B; ++i) {
+            float* r = qkv + (int64_t)i * qn;
+            for (int32_t j = 0; j < qn; ++j) r[j] = r[j] + m->bias[l][j];
+            int32_t pos = lens[i] - 1;
+            const float* cr = m->cos_t + (int64_t)pos * (d / 2);
+            const float* sr = m->sin_t + (int64_t)pos * (d / 2);
+            orc_rope(r, hq + hkv, d, cr, sr);         /* q heads then k heads */
+            memcpy(q + (int64_t)i * hq * d, r, sizeof(float) * hq * d);
+            int32_t b = slots[i];
+            for (int32_t g = 0; g < hkv; ++g) {
+                int32_t page = m->page_table[(int64_t)b * m->maxp + pos / ORC_PAGE];
+                int64_t off = (((int64_t)page * hkv + g) * ORC_PAGE + pos % ORC_PAGE) * d;
+                for (int32_t e = 0; e < d; ++e) {
+                    m->kc[l][off + e] = orc_f32_to_f16(r[(hq + g) * d + e]);
+                    m->vc[l][off + e] = orc_f32_to_f16(r[(hq + hkv + g) * d + e]);
+                }
+            }
+        }
+        orc_gqa_decode_attn(q, m->kc[l], m->vc[l], pt, lens, B, hq, hkv, d, m->maxp, scale, att);
+        orc_quantize_q8_0(att, B, hq * d, xq, xd);
+        orc_q8_gemm(m->o_qs[l], m->o_d[l], H, hq * d, xq, xd, B, y);
+        for (int64_t j = 0; j < (int64_t)B * H; ++j) h[j] = h[j] + y[j];
+        orc_rmsnorm(h, m->ones, B, H, c->eps, xn);
+        orc_quantize_q8_0(xn, B, H, xq, xd);
+        orc_q8_gemm(m->gu_qs[l], m->gu_d[l], 2 * I, H, xq, xd, B, y);
+        orc_swiglu(y, B, I, a);
+        orc_quantize_q8_0(a, B, I, xq, xd);
+        orc_q8_gemm(m->dn_qs[l], m->dn_d[l], H, I, xq, xd, B, y);
+        for (int64_t j = 0; j < (int64_t)B * H; ++j) h[j] = h[j] + y[j];
+    }
+    orc_rmsnorm(h, m->ones, B, H, c->eps, xn);
+    if (hidden_out) memcpy(hidden_out, xn, sizeof(float) * B * H);
+    float* logits = (float*)xmalloc(sizeof(float) * (size_t)B * c->vocab);
+    if (c->tied) {
+        orc_lm_head_f16(xn, B, m->emb, c->vocab, H, logits);
+    } else {
+        orc_quantize_q8_0(xn, B, H, xq, xd);
+        orc_q8_gemm(m->lm_qs, m->lm_d, c->vocab, H, xq, xd, B, logits);
+    }
+    for (int32_t i = 0; i < B; ++i) {
+        next[i] = orc_argmax(logits + (int64_t)i * c->vocab, c->vocab);
+        m->seq_len[slots[i]] = lens[i];
+    }
+    if (logits_out) memcpy(logits_out, logits, sizeof(float) * (size_t)B * c->vocab);
+    free(logits); free(h); free(xn); free(xq); free(xd); free(qkv); free(q); free(att);
+    free(y); free(a); free(pt); free(lens);
+}

@@ -88,6 +88,34 @@ void orc_gqa_decode_attn(const float* q, const uint16_t* kpages, const uint16_t*
                          float* out);
 void orc_gen_page_table(uint64_t seed, uint64_t stream, int32_t B, int32_t maxp, int32_t* pt);
 
+/* ---- decode-step glue ---- */
+void orc_rmsnorm(const float* x, const float* w, int32_t m, int32_t h, float eps, float* y);
+void orc_rope_tables(int32_t max_seq, int32_t d, double theta, float* cos_t, float* sin_t);
+void orc_rope(float* x, int32_t nheads, int32_t d, const float* cos_row, const float* sin_row);
+void orc_swiglu(const float* gu, int32_t m, int32_t inter, float* a);
+int32_t orc_argmax(const float* x, int32_t n);
+void orc_lm_head_f16(const float* x, int32_t m, const uint16_t* E, int32_t V, int32_t h,
+                     float* logits);
+
+/* ---- random-init Qwen2-shaped Q8_0 model ---- */
+typedef struct orc_qwen_config {
+    int32_t n_layers, hidden, inter, n_heads, n_kv, head_dim, vocab;
+    int32_t tied;              /* 1: logits from the binary16 embedding */
+    int32_t max_batch, max_seq;
+    float eps;
+    double theta;
+    double emb_sigma;          /* embedding N(0, emb_sigma) */
+} orc_qwen_config;
+typedef struct orc_model orc_model;
+orc_model* orc_model_create(const orc_qwen_config* cfg, uint64_t seed);
+void orc_model_destroy(orc_model* m);
+int32_t orc_model_seq_len(const orc_model* m, int32_t slot);
+const void* orc_model_tensor(const orc_model* m, int32_t layer, int32_t which);
+void orc_model_kv(const orc_model* m, int32_t layer, int32_t kv, int32_t b, int32_t n,
+                  uint16_t* out);
+void orc_model_step(orc_model* m, int32_t nseq, const int32_t* slots, const int32_t* tokens,
+                    int32_t* next, float* hidden_out, float* logits_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,18 @@ def lib():
             "orc_gqa_decode_attn": (None, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32,
                                            C.c_float, _P]),
             "orc_gen_page_table": (None, [_U64, _U64, _I32, _I32, _P]),
+            "orc_rmsnorm": (None, [_P, _P, _I32, _I32, C.c_float, _P]),
+            "orc_rope_tables": (None, [_I32, _I32, C.c_double, _P, _P]),
+            "orc_rope": (None, [_P, _I32, _I32, _P, _P]),
+            "orc_swiglu": (None, [_P, _I32, _I32, _P]),
+            "orc_argmax": (_I32, [_P, _I32]),
+            "orc_lm_head_f16": (None, [_P, _I32, _P, _I32, _I32, _P]),
+            "orc_model_create": (_P, [_P, _U64]),
+            "orc_model_destroy": (None, [_P]),
+            "orc_model_seq_len": (_I32, [_P, _I32]),
+            "orc_model_tensor": (_P, [_P, _I32, _I32]),
+            "orc_model_kv": (None, [_P, _I32, _I32, _I32, _I32, _P]),
+            "orc_model_step": (None, [_P, _I32, _P, _P, _P, _P, _P]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -282,3 +294,145 @@ def paged_to_dense(pages, page_table, b, L):
     """[L][hkv][d] view of sequence b's cached rows (test helper)."""
     rows = [pages[page_table[b, t // PAGE], :, t % PAGE, :] for t in range(L)]
     return np.stack(rows) if rows else np.zeros((0,) + pages.shape[1:2] + pages.shape[3:], pages.dtype)
+
+
+# ---- decode-step glue -------------------------------------------------------
+
+def rmsnorm(x, w=None, eps=1e-6):
+    x = _c(x, np.float32)
+    m, h = x.shape
+    w = np.ones(h, np.float32) if w is None else _c(w, np.float32)
+    y = np.empty_like(x)
+    lib().orc_rmsnorm(_ptr(x), _ptr(w), m, h, eps, _ptr(y))
+    return y
+
+
+def rope_tables(max_seq: int, d: int, theta: float = 1e6):
+    c = np.empty((max_seq, d // 2), np.float32)
+    s = np.empty((max_seq, d // 2), np.float32)
+    lib().orc_rope_tables(max_seq, d, theta, _ptr(c), _ptr(s))
+    return c, s
+
+
+def rope(x, cos_row, sin_row):
+    """x [nheads][d] rotated in a copy."""
+    x = _c(x, np.float32).copy()
+    nh, d = x.shape
+    cr, sr = _c(cos_row, np.float32), _c(sin_row, np.float32)
+    lib().orc_rope(_ptr(x), nh, d, _ptr(cr), _ptr(sr))
+    return x
+
+
+def swiglu(gu):
+    gu = _c(gu, np.float32)
+    m, n2 = gu.shape
+    a = np.empty((m, n2 // 2), np.float32)
+    lib().orc_swiglu(_ptr(gu), m, n2 // 2, _ptr(a))
+    return a
+
+
+def argmax(x) -> int:
+    x = _c(x, np.float32)
+    return int(lib().orc_argmax(_ptr(x), x.size))
+
+
+def lm_head_f16(x, E):
+    x = _c(x, np.float32)
+    E = _c(E, np.uint16)
+    m, h = x.shape
+    V = E.shape[0]
+    out = np.empty((m, V), np.float32)
+    lib().orc_lm_head_f16(_ptr(x), m, _ptr(E), V, h, _ptr(out))
+    return out
+
+
+# ---- random-init Qwen2-shaped model ------------------------------------------
+
+class QwenConfigC(C.Structure):
+    _fields_ = [("n_layers", _I32), ("hidden", _I32), ("inter", _I32), ("n_heads", _I32),
+                ("n_kv", _I32), ("head_dim", _I32), ("vocab", _I32), ("tied", _I32),
+                ("max_batch", _I32), ("max_seq", _I32), ("eps", C.c_float),
+                ("theta", C.c_double), ("emb_sigma", C.c_double)]
+
+
+TENSORS = {"emb": 0, "lm_q": 1, "lm_d": 2, "qkv_q": 3, "qkv_d": 4, "o_q": 5, "o_d": 6,
+           "gu_q": 7, "gu_d": 8, "dn_q": 9, "dn_d": 10, "bias": 11}
+
+
+class Model:
+    """The oracle's random-init Qwen2-shaped Q8_0 model (C implementation)."""
+
+    def __init__(self, cfg: dict, seed: int):
+        self.cfg = dict(cfg)
+        self.c = QwenConfigC(**{k: cfg[k] for k, _ in QwenConfigC._fields_})
+        self.h = lib().orc_model_create(C.byref(self.c), seed)
+
+    def close(self):
+        if self.h:
+            lib().orc_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def seq_len(self, slot: int) -> int:
+        return int(lib().orc_model_seq_len(self.h, slot))
+
+    def tensor(self, name: str, layer: int = 0) -> np.ndarray:
+        c = self.cfg
+        H, I, d = c["hidden"], c["inter"], c["head_dim"]
+        qn = (c["n_heads"] + 2 * c["n_kv"]) * d
+        shapes = {"emb": ((c["vocab"], H), np.uint16), "lm_q": ((c["vocab"], H), np.int8),
+                  "lm_d": ((c["vocab"], H // 32), np.uint16), "qkv_q": ((qn, H), np.int8),
+                  "qkv_d": ((qn, H // 32), np.uint16), "o_q": ((H, c["n_heads"] * d), np.int8),
+                  "o_d": ((H, c["n_heads"] * d // 32), np.uint16), "gu_q": ((2 * I, H), np.int8),
+                  "gu_d": ((2 * I, H // 32), np.uint16), "dn_q": ((H, I), np.int8),
+                  "dn_d": ((H, I // 32), np.uint16), "bias": ((qn,), np.float32)}
+        shape, dt = shapes[name]
+        ptr = lib().orc_model_tensor(self.h, layer, TENSORS[name])
+        n = int(np.prod(shape)) * np.dtype(dt).itemsize
+        return np.frombuffer(C.string_at(ptr, n), dtype=dt).reshape(shape).copy()
+
+    def kv(self, layer: int, which: int, slot: int, n: int) -> np.ndarray:
+        c = self.cfg
+        out = np.empty((n, c["n_kv"], c["head_dim"]), np.uint16)
+        lib().orc_model_kv(self.h, layer, which, slot, n, _ptr(out))
+        return out
+
+    def step(self, slots, tokens, want_logits=False, want_hidden=False):
+        slots = _c(slots, np.int32)
+        tokens = _c(tokens, np.int32)
+        B = slots.size
+        nxt = np.empty(B, np.int32)
+        hid = np.empty((B, self.cfg["hidden"]), np.float32) if want_hidden else None
+        lg = np.empty((B, self.cfg["vocab"]), np.float32) if want_logits else None
+        lib().orc_model_step(self.h, B, _ptr(slots), _ptr(tokens), _ptr(nxt),
+                             _ptr(hid) if hid is not None else None,
+                             _ptr(lg) if lg is not None else None)
+        out = [nxt]
+        if want_logits:
+            out.append(lg)
+        if want_hidden:
+            out.append(hid)
+        return out[0] if len(out) == 1 else tuple(out)
+
+
+EMB_SIGMA = 0.002
+
+
+def qwen_config(name: str) -> dict:
+    """Shapes of BASELINE configs 3 and 4 and a tiny test model."""
+    base = dict(eps=1e-6, theta=1e6, emb_sigma=EMB_SIGMA)
+    if name == "0.5b":
+        return dict(base, n_layers=24, hidden=896, inter=4864, n_heads=14, n_kv=2, head_dim=64,
+                    vocab=151936, tied=1, max_batch=32, max_seq=2048 + 64)
+    if name == "7b":
+        return dict(base, n_layers=28, hidden=3584, inter=18944, n_heads=28, n_kv=4,
+                    head_dim=128, vocab=152064, tied=0, max_batch=64, max_seq=4096 + 64)
+    if name == "tiny":
+        return dict(base, n_layers=2, hidden=256, inter=512, n_heads=4, n_kv=2, head_dim=64,
+                    vocab=1000, tied=1, max_batch=4, max_seq=320)
+    if name == "tiny_untied":
+        return dict(base, n_layers=2, hidden=256, inter=512, n_heads=4, n_kv=1, head_dim=128,
+                    vocab=1024, tied=0, max_batch=4, max_seq=320)
+    raise KeyError(name)
