@@ -182,6 +182,103 @@ lgx_status lgx_q8_gemm_partials(lgx_ctx* ctx, const lgx_q8_matrix* W, const int8
 lgx_status lgx_q8_range_combine(lgx_ctx* ctx, const float* part, int32_t nranges, int64_t count,
                                 float* y, void* stream);
 
+/* ---- decode-step glue (each also fused into lgx_qwen_decode_step) ----
+ * The reference has none of these; the bit-level rules are fixed here and
+ * match the CPU oracle exactly. */
+/* out[m][h] = binary32 of the binary16 rows emb[tokens[i]] (ids clamped to
+ * [0, vocab)). */
+lgx_status lgx_embed_f16(lgx_ctx* ctx, const uint16_t* emb, const int32_t* tokens, int32_t m,
+                         int32_t h, int32_t vocab, float* out, void* stream);
+/* y = x * (1/sqrtf(S/n + eps)) * w per row, S = halving tree of squares
+ * over the next power of two >= n (zero padded); y (binary32) and/or its
+ * Q8_0 (xq, xd: the lgx_quantize_q8_0 rule) are written.  n <= 8192. */
+lgx_status lgx_rmsnorm_quant(lgx_ctx* ctx, const float* x, const float* w, int32_t m, int32_t n,
+                             float eps, float* y, int8_t* xq, uint16_t* xd, void* stream);
+/* For each sequence b: r = qkv[b] (+ bias) with rows q heads | k heads |
+ * v heads; rotate-half RoPE at position p = seq_len[b] on the q and k heads
+ * (pairs (i, i + d/2), cos/sin from the tables [max_seq][d/2]); q -> q_out
+ * [B][hq][d]; k, v -> binary16 (RNE) slot p % 16 of page
+ * page_table[b][p / 16] (pages [num_pages][hkv][16][d]).  seq_len is not
+ * advanced.  Positions clamp to max_seq - 1 and page ids to [0, num_pages). */
+lgx_status lgx_rope_kv_append(lgx_ctx* ctx, const float* qkv, const float* bias,
+                              const float* cos_t, const float* sin_t, const int32_t* seq_len,
+                              const int32_t* page_table, uint16_t* kpages, uint16_t* vpages,
+                              float* q_out, int32_t B, int32_t hq, int32_t hkv, int32_t d,
+                              int32_t maxp, int32_t num_pages, int32_t max_seq, void* stream);
+/* a[m][i] = silu(g) * u with g = gu[m][i], u = gu[m][inter + i],
+ * silu(g) = g / (1 + exp(-g)); a (binary32) and/or Q8_0(a) written. */
+lgx_status lgx_swiglu_quant(lgx_ctx* ctx, const float* gu, int32_t m, int32_t inter, float* y,
+                            int8_t* xq, uint16_t* xd, void* stream);
+/* logits[m][v] = sequential fmaf chain over k of x[m][k] * emb[v][k]
+ * (binary16 tied embedding); h % 64 == 0, h <= 1024. */
+lgx_status lgx_lm_head_f16(lgx_ctx* ctx, const float* x, const uint16_t* emb, int32_t m,
+                           int32_t h, int32_t vocab, float* logits, void* stream);
+/* out[i] = first index of the maximum of logits[i][:], NaN skipped (all NaN
+ * gives 0); -0 and +0 compare equal. */
+lgx_status lgx_argmax(lgx_ctx* ctx, const float* logits, int32_t m, int32_t vocab, int32_t* out,
+                      void* stream);
+
+/* ---- random-init Qwen2-shaped Q8_0 model (batched greedy decode) ---- */
+/* Opaque model handle, created from a seed and freed explicitly, as the
+ * reference's handle classes are (codegen/ffi.rs:62-75).  The reference has
+ * no model runtime; these are the entry points its emitted host code would
+ * bind for the decode step. */
+typedef struct lgx_model lgx_model;
+
+typedef struct {
+    int32_t n_layers, hidden, intermediate, n_heads, n_kv_heads, head_dim, vocab;
+    int32_t tied_embedding; /* 1: logits from the binary16 embedding (exact chain) */
+    int32_t max_batch, max_seq;
+    float rms_eps;          /* 1e-6 */
+    double rope_theta;      /* 1e6 */
+    double emb_sigma;       /* embedding N(0, emb_sigma) */
+} lgx_qwen_config;
+
+/* Tensor ids of lgx_model_tensor (device pointers owned by the model). */
+enum {
+    LGX_T_EMB = 0,        /* binary16 [vocab][hidden] */
+    LGX_T_LM_Q = 1,       /* untied lm_head quants, T16 layout */
+    LGX_T_LM_D = 2,       /* untied lm_head scales, S16 layout */
+    LGX_T_QKV_Q = 3, LGX_T_QKV_D = 4,
+    LGX_T_O_Q = 5, LGX_T_O_D = 6,
+    LGX_T_GU_Q = 7, LGX_T_GU_D = 8,
+    LGX_T_DOWN_Q = 9, LGX_T_DOWN_D = 10,
+    LGX_T_QKV_BIAS = 11,  /* binary32 [(hq + 2 hkv) d] */
+    LGX_T_K_PAGES = 12,   /* binary16 [num_pages][hkv][16][d] */
+    LGX_T_V_PAGES = 13,
+    LGX_T_PAGE_TABLE = 14,/* int32 [max_batch][maxp], a seeded permutation */
+    LGX_T_SEQ_LEN = 15,   /* int32 [max_batch] */
+    LGX_T_HIDDEN = 16     /* binary32 [max_batch][hidden]: last final-norm output */
+};
+
+/* Generates every tensor from SplitMix64 streams of `seed` (quants uniform on
+ * [-127, 127], scales |N(0, 0.02)|/127, qkv bias N(0, 0.02), embedding
+ * N(0, emb_sigma), norm weights 1) and allocates the paged KV cache for
+ * max_batch sequences of max_seq tokens.  Synchronous. */
+lgx_status lgx_model_create(lgx_ctx* ctx, const lgx_qwen_config* cfg, uint64_t seed,
+                            lgx_model** out);
+lgx_status lgx_model_destroy(lgx_model* m);
+/* seq_len[:] = 0 (the KV cache is overwritten as sequences grow again). */
+lgx_status lgx_model_reset(lgx_model* m, void* stream);
+/* One greedy decode step for sequences 0..B-1: tokens[b] (device int32) is
+ * the current token of sequence b, appended at position seq_len[b]; on return
+ * (stream order) tokens[b] holds the argmax next token and seq_len[b] += 1. */
+lgx_status lgx_qwen_decode_step(lgx_model* m, int32_t B, int32_t* tokens, void* stream);
+/* Feeds prompt[b][0..P) (device int32 [B][P]) for sequences 0..B-1 at
+ * positions seq_len[b]..+P, filling the KV cache; next[b] receives the
+ * greedy token after the prompt and seq_len[b] += P.  Each position goes
+ * through the decode schedule, so prefill and decode produce the same
+ * cache bits. */
+lgx_status lgx_qwen_prefill(lgx_model* m, int32_t B, int32_t P, const int32_t* prompt,
+                            int32_t* next, void* stream);
+/* Device pointer and size in bytes of a model tensor (layer ignored for the
+ * global ones). */
+lgx_status lgx_model_tensor(lgx_model* m, int32_t layer, int32_t which, const void** dev,
+                            size_t* bytes);
+/* out[B][vocab] = logits of the last decode/prefill step (binary32); B must
+ * be that step's batch. */
+lgx_status lgx_qwen_logits(lgx_model* m, int32_t B, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

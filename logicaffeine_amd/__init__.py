@@ -61,7 +61,26 @@ SIGNATURES = {
     "lgx_q8_range_combine": (C.c_int, [_P, _P, _I32, C.c_int64, _P, _P]),
     "lgx_gqa_decode_attn": (C.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32,
                                       _I32, _I32, _P, _P]),
+    "lgx_embed_f16": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _P, _P]),
+    "lgx_rmsnorm_quant": (C.c_int, [_P, _P, _P, _I32, _I32, C.c_float, _P, _P, _P, _P]),
+    "lgx_rope_kv_append": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                                     _I32, _I32, _I32, _I32, _P]),
+    "lgx_swiglu_quant": (C.c_int, [_P, _P, _I32, _I32, _P, _P, _P, _P]),
+    "lgx_lm_head_f16": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _P, _P]),
+    "lgx_argmax": (C.c_int, [_P, _P, _I32, _I32, _P, _P]),
+    "lgx_model_create": (C.c_int, [_P, _P, C.c_uint64, C.POINTER(_P)]),
+    "lgx_model_destroy": (C.c_int, [_P]),
+    "lgx_model_reset": (C.c_int, [_P, _P]),
+    "lgx_qwen_decode_step": (C.c_int, [_P, _I32, _P, _P]),
+    "lgx_qwen_prefill": (C.c_int, [_P, _I32, _I32, _P, _P, _P]),
+    "lgx_model_tensor": (C.c_int, [_P, _I32, _I32, C.POINTER(_P), C.POINTER(C.c_size_t)]),
+    "lgx_qwen_logits": (C.c_int, [_P, _I32, _P, _P]),
 }
+
+# Tensor ids of lgx_model_tensor.
+MODEL_TENSORS = {"emb": 0, "lm_q": 1, "lm_d": 2, "qkv_q": 3, "qkv_d": 4, "o_q": 5, "o_d": 6,
+                 "gu_q": 7, "gu_d": 8, "dn_q": 9, "dn_d": 10, "bias": 11, "k_pages": 12,
+                 "v_pages": 13, "page_table": 14, "seq_len": 15, "hidden": 16}
 
 
 class LgxError(RuntimeError):
@@ -73,6 +92,14 @@ class LgxError(RuntimeError):
 
 class Q8MatrixC(C.Structure):
     _fields_ = [("qs", _P), ("d", _P), ("n", _I32), ("k", _I32), ("layout", _I32)]
+
+
+class QwenConfigC(C.Structure):
+    """lgx_qwen_config."""
+    _fields_ = [("n_layers", _I32), ("hidden", _I32), ("intermediate", _I32),
+                ("n_heads", _I32), ("n_kv_heads", _I32), ("head_dim", _I32), ("vocab", _I32),
+                ("tied_embedding", _I32), ("max_batch", _I32), ("max_seq", _I32),
+                ("rms_eps", C.c_float), ("rope_theta", C.c_double), ("emb_sigma", C.c_double)]
 
 
 _lib = None
@@ -297,3 +324,146 @@ class Context:
         _check(lib().lgx_q8_gemm(self.handle, W.cstruct, xq.data_ptr(), xd.data_ptr(), m,
                                  y.data_ptr(), self._s()))
         return y
+
+    # ---- decode-step glue ------------------------------------------------
+    def embed_f16(self, emb, tokens, out=None):
+        t = self.torch
+        vocab, h = emb.shape
+        m = tokens.numel()
+        out = t.empty((m, h), dtype=t.float32, device=self.dev) if out is None else out
+        _check(lib().lgx_embed_f16(self.handle, emb.data_ptr(), tokens.data_ptr(), m, h, vocab,
+                                   out.data_ptr(), self._s()))
+        return out
+
+    def rmsnorm_quant(self, x, w, eps: float, y: bool = True, q8: bool = True):
+        """(y, xq, xd) of RMSNorm(x) * w; unrequested outputs are None."""
+        t = self.torch
+        m, n = x.shape
+        yo = t.empty((m, n), dtype=t.float32, device=self.dev) if y else None
+        xq = t.empty((m, n), dtype=t.int8, device=self.dev) if q8 else None
+        xd = t.empty((m, n // 32), dtype=t.int16, device=self.dev) if q8 else None
+        _check(lib().lgx_rmsnorm_quant(self.handle, x.data_ptr(), w.data_ptr(), m, n, eps,
+                                       _ptr_or_none(yo), _ptr_or_none(xq), _ptr_or_none(xd),
+                                       self._s()))
+        return yo, xq, xd
+
+    def rope_kv_append(self, qkv, bias, cos_t, sin_t, seq_len, page_table, kpages, vpages,
+                       hq: int, max_seq: int, q_out=None):
+        t = self.torch
+        B = qkv.shape[0]
+        num_pages, hkv, _, d = kpages.shape
+        maxp = page_table.shape[1]
+        q_out = t.empty((B, hq, d), dtype=t.float32, device=self.dev) if q_out is None else q_out
+        _check(lib().lgx_rope_kv_append(
+            self.handle, qkv.data_ptr(), _ptr_or_none(bias), cos_t.data_ptr(), sin_t.data_ptr(),
+            seq_len.data_ptr(), page_table.data_ptr(), kpages.data_ptr(), vpages.data_ptr(),
+            q_out.data_ptr(), B, hq, hkv, d, maxp, num_pages, max_seq, self._s()))
+        return q_out
+
+    def swiglu_quant(self, gu, y: bool = True, q8: bool = True):
+        t = self.torch
+        m, i2 = gu.shape
+        inter = i2 // 2
+        yo = t.empty((m, inter), dtype=t.float32, device=self.dev) if y else None
+        xq = t.empty((m, inter), dtype=t.int8, device=self.dev) if q8 else None
+        xd = t.empty((m, inter // 32), dtype=t.int16, device=self.dev) if q8 else None
+        _check(lib().lgx_swiglu_quant(self.handle, gu.data_ptr(), m, inter, _ptr_or_none(yo),
+                                      _ptr_or_none(xq), _ptr_or_none(xd), self._s()))
+        return yo, xq, xd
+
+    def lm_head_f16(self, x, emb, out=None):
+        t = self.torch
+        m, h = x.shape
+        vocab = emb.shape[0]
+        out = t.empty((m, vocab), dtype=t.float32, device=self.dev) if out is None else out
+        _check(lib().lgx_lm_head_f16(self.handle, x.data_ptr(), emb.data_ptr(), m, h, vocab,
+                                     out.data_ptr(), self._s()))
+        return out
+
+    def argmax(self, logits, out=None):
+        t = self.torch
+        m, vocab = logits.shape
+        out = t.empty(m, dtype=t.int32, device=self.dev) if out is None else out
+        _check(lib().lgx_argmax(self.handle, logits.data_ptr(), m, vocab, out.data_ptr(),
+                                self._s()))
+        return out
+
+
+def _ptr_or_none(tensor):
+    return tensor.data_ptr() if tensor is not None else None
+
+
+class Model:
+    """lgx_model: the seeded random-init Qwen2-shaped Q8_0 model on one device.
+
+    ``cfg`` uses the oracle's keys (n_layers, hidden, inter, n_heads, n_kv,
+    head_dim, vocab, tied, max_batch, max_seq, eps, theta, emb_sigma)."""
+
+    def __init__(self, ctx: Context, cfg: dict, seed: int):
+        self.ctx = ctx
+        self.cfg = dict(cfg)
+        self.c = QwenConfigC(cfg["n_layers"], cfg["hidden"], cfg["inter"], cfg["n_heads"],
+                             cfg["n_kv"], cfg["head_dim"], cfg["vocab"], cfg["tied"],
+                             cfg["max_batch"], cfg["max_seq"], cfg["eps"], cfg["theta"],
+                             cfg["emb_sigma"])
+        h = C.c_void_p()
+        _check(lib().lgx_model_create(ctx.handle, C.byref(self.c), seed, C.byref(h)))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            _check(lib().lgx_model_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self) -> None:
+        _check(lib().lgx_model_reset(self.handle, self.ctx._s()))
+
+    def decode_step(self, tokens) -> None:
+        """tokens: device int32 [B], replaced in place by the next tokens."""
+        _check(lib().lgx_qwen_decode_step(self.handle, tokens.numel(), tokens.data_ptr(),
+                                          self.ctx._s()))
+
+    def prefill(self, prompt, next_tokens=None):
+        """prompt: device int32 [B][P]; returns the device int32 [B] next tokens."""
+        t = self.ctx.torch
+        B, P = prompt.shape
+        nxt = t.empty(B, dtype=t.int32, device=self.ctx.dev) if next_tokens is None else next_tokens
+        _check(lib().lgx_qwen_prefill(self.handle, B, P, prompt.data_ptr(), nxt.data_ptr(),
+                                      self.ctx._s()))
+        return nxt
+
+    def logits(self, B: int):
+        t = self.ctx.torch
+        out = t.empty((B, self.cfg["vocab"]), dtype=t.float32, device=self.ctx.dev)
+        _check(lib().lgx_qwen_logits(self.handle, B, out.data_ptr(), self.ctx._s()))
+        return out
+
+    def tensor_ptr(self, name: str, layer: int = 0):
+        """(device pointer, bytes) of a model tensor."""
+        p, n = C.c_void_p(), C.c_size_t()
+        _check(lib().lgx_model_tensor(self.handle, layer, MODEL_TENSORS[name], C.byref(p),
+                                      C.byref(n)))
+        return int(p.value or 0), int(n.value)
+
+    def tensor_bytes(self, name: str, layer: int = 0):
+        """Host copy (numpy uint8) of a model tensor's bytes."""
+        import numpy as np
+
+        t = self.ctx.torch
+        p, n = self.tensor_ptr(name, layer)
+        t.cuda.current_stream(self.ctx.dev).synchronize()
+        out = np.empty(n, np.uint8)
+        _check_hip(C.CDLL("libamdhip64.so").hipMemcpy(
+            out.ctypes.data_as(C.c_void_p), C.c_void_p(p), C.c_size_t(n), 2))
+        return out
+
+
+def _check_hip(err: int) -> None:
+    if err != 0:
+        raise LgxError(10, f"hipMemcpy failed with hipError {err}")

@@ -44,12 +44,15 @@ def build_kernels() -> str:
     return HSACO
 
 
+HOST_SOURCES = ["lgx_host.cpp", "lgx_glue.cpp", "lgx_model.cpp", "lgx_gen.cpp"]
+
+
 def build_host() -> str:
-    src = os.path.join(CSRC, "lgx_host.cpp")
+    srcs = [os.path.join(CSRC, s) for s in HOST_SOURCES]
     tmp = LIB + ".tmp"
-    _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-Wextra",
+    _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-ffp-contract=off", "-Wall", "-Wextra", "-pthread",
           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", "-I", CSRC,
-          "-o", tmp, src, f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl"])
+          "-o", tmp, *srcs, f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl"])
     os.replace(tmp, LIB)
     return LIB
 

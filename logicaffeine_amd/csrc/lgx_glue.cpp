@@ -1,0 +1,147 @@
+// lgx_glue.cpp -- standalone entry points of the decode-step glue kernels
+// (embedding gather, RMSNorm + Q8_0, RoPE + paged KV append, SwiGLU + Q8_0,
+// binary16 lm_head, argmax).  The decode step in lgx_model.cpp launches the
+// same kernels with range partials as inputs; here every input is a plain
+// binary32 tensor (one range), which is how a caller outside the model uses
+// them and how the tests compare each one with the CPU oracle.
+#include <algorithm>
+#include <cmath>
+
+#include "lgx_internal.h"
+
+using namespace lgxi;
+
+namespace {
+constexpr int kNormMax = 8192, kQkvMax = 8192, kLmMaxH = 1024, kLmMaxM = 64;
+}
+
+extern "C" {
+
+lgx_status lgx_embed_f16(lgx_ctx* c, const uint16_t* emb, const int32_t* tokens, int32_t m,
+                         int32_t h, int32_t vocab, float* out, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!emb || !tokens || !out) return fail(LGX_NULL_POINTER, "NULL tensor");
+        if (m <= 0 || h <= 0 || vocab <= 0)
+            return fail(LGX_INVALID_ARGUMENT, "m %d, h %d, vocab %d", m, h, vocab);
+        lgx_embed_args a{emb, tokens, out, m, h, vocab, 1};
+        return launch(c, K_EMBED, dim3(m), dim3(256), a, stream);
+    });
+}
+
+lgx_status lgx_rmsnorm_quant(lgx_ctx* c, const float* x, const float* w, int32_t m, int32_t n,
+                             float eps, float* y, int8_t* xq, uint16_t* xd, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!x || !w) return fail(LGX_NULL_POINTER, "NULL x or w");
+        if (!y && !xq) return fail(LGX_NULL_POINTER, "no output (y and xq are NULL)");
+        if ((xq == nullptr) != (xd == nullptr)) return fail(LGX_NULL_POINTER, "xq and xd go together");
+        if (m <= 0 || n <= 0 || n > kNormMax)
+            return fail(LGX_INVALID_ARGUMENT, "m %d, n %d (n <= %d)", m, n, kNormMax);
+        if (xq && n % 32) return fail(LGX_INVALID_ARGUMENT, "Q8_0 output needs n %% 32 == 0");
+        lgx_norm_args a{};
+        a.part = nullptr;
+        a.nr = 1;
+        a.h = const_cast<float*>(x);   // read only when part is NULL
+        a.w = w;
+        a.xn = y;
+        a.xq = xq;
+        a.xd = xd;
+        a.m = m;
+        a.n = n;
+        a.eps = eps;
+        return launch(c, K_ADD_RMSNORM_QUANT, dim3(m), dim3(256), a, stream);
+    });
+}
+
+lgx_status lgx_rope_kv_append(lgx_ctx* c, const float* qkv, const float* bias, const float* cos_t,
+                              const float* sin_t, const int32_t* seq_len,
+                              const int32_t* page_table, uint16_t* kpages, uint16_t* vpages,
+                              float* q_out, int32_t B, int32_t hq, int32_t hkv, int32_t d,
+                              int32_t maxp, int32_t num_pages, int32_t max_seq, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!qkv || !cos_t || !sin_t || !seq_len || !page_table || !kpages || !vpages || !q_out)
+            return fail(LGX_NULL_POINTER, "NULL tensor");
+        if (B <= 0 || hq <= 0 || hkv <= 0 || d <= 0 || d % 2 || maxp <= 0 || num_pages <= 0 ||
+            max_seq <= 0)
+            return fail(LGX_INVALID_ARGUMENT, "B %d hq %d hkv %d d %d maxp %d pages %d max_seq %d",
+                        B, hq, hkv, d, maxp, num_pages, max_seq);
+        if ((int64_t)(hq + 2 * hkv) * d > kQkvMax)
+            return fail(LGX_UNSUPPORTED, "(hq + 2 hkv) d = %d > %d", (hq + 2 * hkv) * d, kQkvMax);
+        if ((int64_t)maxp * LGX_PAGE < max_seq)
+            return fail(LGX_OUT_OF_BOUNDS, "max_seq %d exceeds maxp * 16 = %d", max_seq,
+                        maxp * LGX_PAGE);
+        lgx_qkv_args a{};
+        a.part = qkv;
+        a.nr = 1;
+        a.bias = bias;
+        a.cos_t = cos_t;
+        a.sin_t = sin_t;
+        a.seq_len = seq_len;
+        a.page_table = page_table;
+        a.kpages = kpages;
+        a.vpages = vpages;
+        a.q_out = q_out;
+        a.m = B;
+        a.hq = hq;
+        a.hkv = hkv;
+        a.d = d;
+        a.maxp = maxp;
+        a.num_pages = num_pages;
+        a.max_seq = max_seq;
+        return launch(c, K_QKV_ROPE_APPEND, dim3(B), dim3(256), a, stream);
+    });
+}
+
+lgx_status lgx_swiglu_quant(lgx_ctx* c, const float* gu, int32_t m, int32_t inter, float* y,
+                            int8_t* xq, uint16_t* xd, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!gu) return fail(LGX_NULL_POINTER, "NULL gate|up");
+        if (!y && !xq) return fail(LGX_NULL_POINTER, "no output (y and xq are NULL)");
+        if ((xq == nullptr) != (xd == nullptr)) return fail(LGX_NULL_POINTER, "xq and xd go together");
+        if (m <= 0 || inter <= 0 || inter % 32)
+            return fail(LGX_INVALID_ARGUMENT, "m %d, inter %d (multiple of 32)", m, inter);
+        lgx_swiglu_args a{gu, 1, xq, xd, y, m, inter};
+        return launch(c, K_SWIGLU_QUANT, dim3(m, cdiv(inter / 32, 32)), dim3(256), a, stream);
+    });
+}
+
+lgx_status lgx_lm_head_f16(lgx_ctx* c, const float* x, const uint16_t* emb, int32_t m, int32_t h,
+                           int32_t vocab, float* logits, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!x || !emb || !logits) return fail(LGX_NULL_POINTER, "NULL tensor");
+        if (m <= 0 || vocab <= 0 || h <= 0 || h % 64 || h > kLmMaxH)
+            return fail(LGX_UNSUPPORTED, "m %d, vocab %d, h %d (h %% 64 == 0, h <= %d)", m, vocab,
+                        h, kLmMaxH);
+        for (int r0 = 0; r0 < m; r0 += kLmMaxM) {
+            lgx_lmhead_args a{x + (int64_t)r0 * h, emb, logits + (int64_t)r0 * vocab,
+                              std::min(kLmMaxM, m - r0), h, vocab};
+            if ((st = launch(c, K_LM_HEAD_F16, dim3(cdiv(vocab, 256)), dim3(256), a, stream)) !=
+                LGX_OK)
+                return st;
+        }
+        return LGX_OK;
+    });
+}
+
+lgx_status lgx_argmax(lgx_ctx* c, const float* logits, int32_t m, int32_t vocab, int32_t* out,
+                      void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!logits || !out) return fail(LGX_NULL_POINTER, "NULL tensor");
+        if (m <= 0 || vocab <= 0) return fail(LGX_INVALID_ARGUMENT, "m %d, vocab %d", m, vocab);
+        lgx_argmax_args a{logits, 1, out, nullptr, m, vocab, 0};
+        return launch(c, K_ARGMAX_ADVANCE, dim3(m), dim3(256), a, stream);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,301 @@
+// lgx_internal.h -- definitions shared by the liblgx translation units:
+// error state, the kernel table resolved from lgx_kernels.hsaco, the context
+// object, and the launch helpers.  Not part of the ABI.
+#pragma once
+#include <hip/hip_runtime_api.h>
+
+#include <dlfcn.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/lgx.h"
+#include "lgx_kargs.h"
+
+// From hip/hip_ext.h (whose templates need the HIP compiler; this file is
+// plain C++): module launch with start/stop events on the dispatch itself.
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX,
+                                               uint32_t globalWorkSizeY, uint32_t globalWorkSizeZ,
+                                               uint32_t localWorkSizeX, uint32_t localWorkSizeY,
+                                               uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void** kernelParams,
+                                               void** extra, hipEvent_t startEvent,
+                                               hipEvent_t stopEvent, uint32_t flags);
+
+namespace lgxi {
+
+inline thread_local std::string g_last_error;
+inline thread_local bool g_has_error = false;
+
+inline lgx_status fail(lgx_status st, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    g_has_error = true;
+    return st;
+}
+
+template <class F>
+lgx_status guarded(const char* name, F&& f) {
+    try {
+        return f();
+    } catch (const std::bad_alloc&) {
+        return fail(LGX_OUT_OF_MEMORY, "%s: host allocation failed", name);
+    } catch (const std::exception& e) {
+        return fail(LGX_INTERNAL_PANIC, "%s: internal error: %s", name, e.what());
+    } catch (...) {
+        return fail(LGX_INTERNAL_PANIC, "%s: unknown internal error", name);
+    }
+}
+
+#define LGX_HIP(call)                                                                   \
+    do {                                                                                \
+        hipError_t e_ = (call);                                                         \
+        if (e_ != hipSuccess)                                                           \
+            return fail(LGX_HIP_ERROR, "%s: %s failed: %s", __func__, #call,            \
+                        hipGetErrorString(e_));                                         \
+    } while (0)
+
+// Kernel table: name in the code object -> slot.
+enum Kern {
+    K_REPACK,
+    K_QUANT,
+    K_Q8Q8_GEMV,
+    K_Q8_GEMV_F32,
+    K_COMBINE,
+    K_GEMV_MFMA,
+    K_GEMV_MFMA_QX,
+    K_GEMM_MFMA16,
+    K_GEMM_MFMA32,
+    K_GEMM_MFMA64,
+    K_REPACK_S16,
+    K_ATTN_D64_G1,   // + (gq - 1): gq = 1..8
+    K_ATTN_D128_G1 = K_ATTN_D64_G1 + 8,
+    K_ATTN_COMBINE_D64 = K_ATTN_D128_G1 + 8,
+    K_ATTN_COMBINE_D128,
+    K_EMBED,
+    K_ADD_RMSNORM_QUANT,
+    K_QKV_ROPE_APPEND,
+    K_ATTN_COMBINE_QUANT_D64,
+    K_ATTN_COMBINE_QUANT_D128,
+    K_SWIGLU_QUANT,
+    K_LM_HEAD_F16,
+    K_ARGMAX_ADVANCE,
+    K_ADVANCE,
+    K_COUNT
+};
+inline const char* const kKernelNames[] = {
+    "lgx_k_repack_t16", "lgx_k_quantize_q8_0", "lgx_k_q8q8_gemv",
+    "lgx_k_q8_gemv_f32", "lgx_k_q8_combine",
+    "lgx_k_q8_gemv_mfma", "lgx_k_q8_gemv_mfma_qx", "lgx_k_q8_gemm_mfma16",
+    "lgx_k_q8_gemm_mfma32", "lgx_k_q8_gemm_mfma64", "lgx_k_repack_s16",
+    "lgx_k_attn_chunk_d64_g1", "lgx_k_attn_chunk_d64_g2", "lgx_k_attn_chunk_d64_g3",
+    "lgx_k_attn_chunk_d64_g4", "lgx_k_attn_chunk_d64_g5", "lgx_k_attn_chunk_d64_g6",
+    "lgx_k_attn_chunk_d64_g7", "lgx_k_attn_chunk_d64_g8",
+    "lgx_k_attn_chunk_d128_g1", "lgx_k_attn_chunk_d128_g2", "lgx_k_attn_chunk_d128_g3",
+    "lgx_k_attn_chunk_d128_g4", "lgx_k_attn_chunk_d128_g5", "lgx_k_attn_chunk_d128_g6",
+    "lgx_k_attn_chunk_d128_g7", "lgx_k_attn_chunk_d128_g8",
+    "lgx_k_attn_combine_d64", "lgx_k_attn_combine_d128",
+    "lgx_k_embed", "lgx_k_add_rmsnorm_quant", "lgx_k_qkv_rope_append",
+    "lgx_k_attn_combine_quant_d64", "lgx_k_attn_combine_quant_d128", "lgx_k_swiglu_quant",
+    "lgx_k_lm_head_f16", "lgx_k_argmax_advance", "lgx_k_advance",
+};
+
+static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
+              "one code-object name per kernel slot");
+
+// Attention chunk kernel for head_dim d and query heads per KV head gq.
+inline int attn_kernel(int d, int gq) {
+    if (gq < 1 || gq > 8) return -1;
+    return (d == 64 ? K_ATTN_D64_G1 : K_ATTN_D128_G1) + gq - 1;
+}
+
+// Debug/tuning knobs read once per ctx (documented in DESIGN.md):
+//   LGX_GEMV=dot4   route lgx_q8q8_gemv to the v_dot4 GEMV instead of MFMA
+//   LGX_WG_TARGET=n workgroups the streaming kernels aim for (default 512)
+inline int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+}  // namespace lgxi
+
+struct lgx_ctx {
+    uint32_t magic = 0x4c47584bu;  // "LGXK"
+    int device = 0;
+    hipModule_t module = nullptr;
+    hipFunction_t fn[lgxi::K_COUNT] = {};
+    std::string arch;
+    bool gemv_dot4 = false;
+    int wg_target = 512;
+    std::atomic<uint64_t> launches{0};
+    void* ws = nullptr;       // range partials
+    size_t ws_bytes = 0;
+    std::mutex ws_mu;
+    // per-kernel device timing (lgx_ctx_set_kernel_timing): launches go
+    // through hipExtModuleLaunchKernel with start/stop events attached to the
+    // dispatch itself
+    bool timing = false;
+    struct Timed {
+        int kern;
+        hipEvent_t start, stop;
+    };
+    std::vector<Timed> timed;
+    std::vector<hipEvent_t> event_pool;
+};
+
+namespace lgxi {
+
+inline bool valid_ctx(const lgx_ctx* c) { return c != nullptr && c->magic == 0x4c47584bu; }
+
+inline std::string default_hsaco_path() {
+    Dl_info info{};
+    if (dladdr((void*)&lgx_abi_version, &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        size_t slash = p.rfind('/');
+        std::string dir = slash == std::string::npos ? std::string(".") : p.substr(0, slash);
+        return dir + "/lgx_kernels.hsaco";
+    }
+    return "lgx_kernels.hsaco";
+}
+
+inline hipError_t pooled_event(lgx_ctx* c, hipEvent_t* ev) {
+    if (!c->event_pool.empty()) {
+        *ev = c->event_pool.back();
+        c->event_pool.pop_back();
+        return hipSuccess;
+    }
+    return hipEventCreate(ev);
+}
+
+template <class Args>
+lgx_status launch(lgx_ctx* c, Kern k, dim3 grid, dim3 block, const Args& args, void* stream,
+                  unsigned shmem = 0) {
+    void* params[] = {(void*)&args};
+    hipError_t e;
+    if (c->timing) {
+        lgx_ctx::Timed t{k, nullptr, nullptr};
+        if ((e = pooled_event(c, &t.start)) != hipSuccess || (e = pooled_event(c, &t.stop)) != hipSuccess)
+            return fail(LGX_HIP_ERROR, "hipEventCreate: %s", hipGetErrorString(e));
+        e = hipExtModuleLaunchKernel(c->fn[k], grid.x * block.x, grid.y * block.y,
+                                     grid.z * block.z, block.x, block.y, block.z, shmem,
+                                     (hipStream_t)stream, params, nullptr, t.start, t.stop, 0);
+        if (e == hipSuccess) c->timed.push_back(t);
+    } else {
+        e = hipModuleLaunchKernel(c->fn[k], grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                                  shmem, (hipStream_t)stream, params, nullptr);
+    }
+    if (e != hipSuccess)
+        return fail(LGX_HIP_ERROR, "hipModuleLaunchKernel(%s): %s", kKernelNames[k],
+                    hipGetErrorString(e));
+    c->launches.fetch_add(1, std::memory_order_relaxed);
+    return LGX_OK;
+}
+
+inline lgx_status enter(lgx_ctx* c) {
+    if (!valid_ctx(c)) return fail(LGX_INVALID_HANDLE, "invalid lgx_ctx handle");
+    LGX_HIP(hipSetDevice(c->device));
+    g_has_error = false;
+    return LGX_OK;
+}
+
+// Scratch for range partials, grown on demand.  hipFree of the old buffer
+// waits for the device, so work still using it has finished.
+inline lgx_status ensure_ws(lgx_ctx* c, size_t bytes, float** out) {
+    std::lock_guard<std::mutex> lk(c->ws_mu);
+    if (bytes > c->ws_bytes) {
+        size_t nb = bytes < (size_t)1 << 20 ? (size_t)1 << 20 : bytes + bytes / 2;
+        if (c->ws) LGX_HIP(hipFree(c->ws));
+        c->ws = nullptr;
+        c->ws_bytes = 0;
+        hipError_t e = hipMalloc(&c->ws, nb);
+        if (e != hipSuccess)
+            return fail(LGX_OUT_OF_MEMORY, "workspace of %zu bytes: %s", nb, hipGetErrorString(e));
+        c->ws_bytes = nb;
+    }
+    *out = (float*)c->ws;
+    return LGX_OK;
+}
+
+inline lgx_status check_q8(const lgx_q8_matrix* W) {
+    if (!W) return fail(LGX_NULL_POINTER, "W is NULL");
+    if (!W->qs || !W->d) return fail(LGX_NULL_POINTER, "W->qs / W->d is NULL");
+    if (W->layout != LGX_Q8_T16)
+        return fail(LGX_INVALID_ARGUMENT, "W->layout must be LGX_Q8_T16 (got %d)", W->layout);
+    if (W->n <= 0 || W->k <= 0 || W->n % 16 != 0 || W->k % 64 != 0)
+        return fail(LGX_INVALID_ARGUMENT, "W shape [%d x %d]: need n %% 16 == 0, k %% 64 == 0",
+                    W->n, W->k);
+    if (W->k > 32 * LGX_Q8_RANGE_BLOCKS * LGX_MAX_RANGES)
+        return fail(LGX_OUT_OF_BOUNDS, "W->k = %d exceeds %d", W->k,
+                    32 * LGX_Q8_RANGE_BLOCKS * LGX_MAX_RANGES);
+    return LGX_OK;
+}
+
+inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
+inline int nranges_of(int k) { return (k / 32 + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS; }
+
+// Shared driver of the GEMV/GEMM kernels: one launch over (row tiles, ranges,
+// m-groups); with more than one range the partials go to the workspace and
+// the combine kernel applies the canonical tree.
+inline lgx_status run_q8(lgx_ctx* c, Kern kern, const lgx_q8_matrix* W, const float* xf,
+                  const int8_t* xq, const uint16_t* xd, int m, float* y, int32_t* dbg,
+                  void* stream, int8_t* xq_out = nullptr, uint16_t* xd_out = nullptr,
+                  float* part_out = nullptr) {
+    lgx_gemv_args a{};
+    a.wt = W->qs;
+    a.wd = W->d;
+    a.xf = xf;
+    a.xq = xq;
+    a.xd = xd;
+    a.y = y;
+    a.dbg = dbg;
+    a.xq_out = xq_out;
+    a.xd_out = xd_out;
+    a.n = W->n;
+    a.k = W->k;
+    a.m = m;
+    a.ntiles = W->n / 16;
+    a.nranges = nranges_of(W->k);
+    a.nmgroups = (m + 63) / 64;
+    if (part_out) {
+        // caller-owned partials [nranges][m][n]; no tree here
+        a.part = part_out;
+        a.y = part_out;
+    } else if (a.nranges > 1) {
+        lgx_status st = ensure_ws(c, (size_t)a.nranges * m * W->n * sizeof(float), &a.part);
+        if (st != LGX_OK) return st;
+    }
+    const bool streaming =
+        kern == K_GEMM_MFMA16 || kern == K_GEMM_MFMA32 || kern == K_GEMM_MFMA64;
+    const int mrows = kern == K_GEMM_MFMA16 ? 16 : kern == K_GEMM_MFMA32 ? 32 : 64;
+    a.nmgroups = streaming ? (m + mrows - 1) / mrows : 1;
+    a.tpw = 1;
+    if (streaming) {
+        // tiles per wave: enough work per wave that the grid is about
+        // wg_target workgroups of 4 waves
+        int64_t tasks = (int64_t)a.ntiles * a.nranges * a.nmgroups;
+        int64_t tpw = (tasks + 4LL * c->wg_target - 1) / (4LL * c->wg_target);
+        a.tpw = (int)(tpw < 1 ? 1 : tpw > 64 ? 64 : tpw);
+    }
+    dim3 grid(cdiv(a.ntiles, 4LL * a.tpw), a.nranges,
+              streaming ? a.nmgroups : 1);
+    lgx_status st = launch(c, kern, grid, dim3(256), a, stream);
+    if (st != LGX_OK || a.nranges == 1 || part_out) return st;
+    lgx_combine_args ca{a.part, y, (int64_t)m * W->n, a.nranges};
+    return launch(c, K_COMBINE, dim3(cdiv(ca.count, 256)), dim3(256), ca, stream);
+}
+
+}  // namespace lgxi
+

@@ -67,8 +67,85 @@ typedef struct {
     float* out;                // [B][hq][d]
     int32_t B, hq, hkv, maxp, nchunk, num_pages;
     int32_t maxlen;            // tokens beyond min(max_seq_len, maxp*16) are ignored
+    int32_t len_add;           // attended length = seq_len[b] + len_add (decode step: 1)
     float scale;
+    int8_t* xq;                // combine+quantise variant: Q8_0 of out rows [B][hq*d]
+    uint16_t* xd;
 } lgx_attn_args;
 
 #define LGX_PAGE 16
 #define LGX_ATTN_CHUNK 256
+
+// ---- decode-step glue ----
+typedef struct {
+    const uint16_t* emb;   // [vocab][n] binary16
+    const int32_t* tokens; // token of row b at tokens[b * tokens_stride]
+    float* h;              // [m][n]
+    int32_t m, n, vocab, tokens_stride;
+} lgx_embed_args;
+
+// seq_len[b] = (keep ? seq_len[b] : 0) + add for b < m
+typedef struct {
+    int32_t* seq_len;
+    int32_t m, add, keep;
+} lgx_advance_args;
+
+// h += tree(part) (when part != NULL), then y = RMSNorm(h) * w, written as
+// binary32 (xn, nullable) and/or Q8_0 (xq/xd, nullable).
+typedef struct {
+    const float* part;     // [nr][m][n] range partials of the residual update
+    int32_t nr;
+    float* h;              // [m][n]
+    const float* w;        // [n] norm weight
+    float* xn;
+    int8_t* xq;
+    uint16_t* xd;
+    int32_t m, n;
+    float eps;
+} lgx_norm_args;
+
+// qkv = tree(part) (+ bias, nullable); RoPE on the q and k heads at position seq_len[b];
+// q -> q_out (binary32), k and v -> binary16 cache slot (page, pos % 16).
+typedef struct {
+    const float* part;     // [nr][m][(hq+2hkv)d]
+    int32_t nr;
+    const float* bias;
+    const float* cos_t;    // [max_seq][d/2]
+    const float* sin_t;
+    const int32_t* seq_len;
+    const int32_t* page_table;
+    uint16_t* kpages;
+    uint16_t* vpages;
+    float* q_out;          // [m][hq][d]
+    int32_t m, hq, hkv, d, maxp, num_pages, max_seq;
+} lgx_qkv_args;
+
+// a = silu(gate) * up from tree(part) ([nr][m][2*inter]), then Q8_0(a)
+// (xq/xd) and/or binary32 a (y); each output nullable.
+typedef struct {
+    const float* part;
+    int32_t nr;
+    int8_t* xq;
+    uint16_t* xd;
+    float* y;
+    int32_t m, inter;
+} lgx_swiglu_args;
+
+// logits[m][v] = canonical dot of binary32 x[m] with binary16 row E[v]
+// (1024-element ranges, pairwise tree).
+typedef struct {
+    const float* x;        // [m][h]
+    const uint16_t* emb;   // [vocab][h]
+    float* logits;         // [m][vocab]
+    int32_t m, h, vocab;
+} lgx_lmhead_args;
+
+// next[b] = first index of the max of tree(part[.][b][:]) (NaN skipped);
+// then tokens[b] = next[b] and seq_len[b] += advance.
+typedef struct {
+    const float* part;     // [nr][m][vocab]
+    int32_t nr;
+    int32_t* tokens;
+    int32_t* seq_len;
+    int32_t m, vocab, advance;
+} lgx_argmax_args;

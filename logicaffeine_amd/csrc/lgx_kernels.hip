@@ -689,7 +689,7 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = blockIdx.x, bg = blockIdx.y;
     const int b = bg / a.hkv, g = bg - b * a.hkv;
-    const int L = min(a.seq_len[b], a.maxlen);
+    const int L = min(a.seq_len[b] + a.len_add, a.maxlen);
     const int t0 = c * C;
     if (t0 >= L) return;                          // whole workgroup: chunk past the end
     const int n = min(C, L - t0);
@@ -793,7 +793,7 @@ template <int D>
 __device__ __forceinline__ void attn_combine_body(const lgx_attn_args& a) {
     const int bh = blockIdx.x, i = threadIdx.x;
     const int b = bh / a.hq;
-    const int L = min(a.seq_len[b], a.maxlen);
+    const int L = min(a.seq_len[b] + a.len_add, a.maxlen);
     const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
     const float* pp = a.part + (int64_t)bh * a.nchunk * (D + 2);
     float M = -__builtin_inff();
@@ -834,4 +834,321 @@ extern "C" __global__ __launch_bounds__(128) void lgx_k_attn_combine_d128(const 
 }
 extern "C" __global__ __launch_bounds__(64) void lgx_k_attn_combine_d64(const lgx_attn_args a) {
     attn_combine_body<64>(a);
+}
+
+// ---------------------------------------------------------------------------
+// Decode-step glue.  Each kernel applies the canonical range tree to the
+// partials of the product before it (so no separate combine launch), then
+// the element-wise step, then (where the next product needs it) the Q8_0
+// quantisation of its output row.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float lgx_silu(float g) {
+    const float e = lgx_expf(-g);
+    const float den = 1.0f + e;
+    return g / den;
+}
+
+// tree over nr partials of element i (stride = elements per partial)
+__device__ __forceinline__ float tree_partials(const float* part, int nr, int64_t stride,
+                                               int64_t i) {
+    float p[LGX_MAX_RANGES];
+#pragma unroll
+    for (int j = 0; j < LGX_MAX_RANGES; ++j) p[j] = j < nr ? part[j * stride + i] : 0.0f;
+    return tree_sum(p, nr);
+}
+
+// Q8_0 of one 32-block held by 8 consecutive lanes (4 values each): the
+// lgx_k_quantize_q8_0 rule.  Returns the packed quants of this lane's four
+// values and the binary16 scale.
+__device__ __forceinline__ uint32_t quantize4(const float (&f)[4], uint16_t& dh) {
+    float am = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
+    am = fmaxf(am, shfl_xor_f(am, 1));
+    am = fmaxf(am, shfl_xor_f(am, 2));
+    am = fmaxf(am, shfl_xor_f(am, 4));
+    const float d = am / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t qw = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float q = roundf(f[e] * id);
+        q = fminf(fmaxf(q, -127.0f), 127.0f);
+        qw |= ((uint32_t)(int32_t)q & 0xffu) << (8 * e);
+    }
+    dh = f2h(d);
+    return qw;
+}
+
+// Quantise a row held in LDS (n floats, n % 32 == 0) to xq/xd (256 threads;
+// 8 threads per block, the 8 lanes of a block always active together).
+__device__ __forceinline__ void quantize_row_from_lds(const float* row, int n, int8_t* xq,
+                                                      uint16_t* xd) {
+    const int j = threadIdx.x & 7;
+    for (int bl = threadIdx.x >> 3; bl < n / 32; bl += 32) {
+        const float f[4] = {row[bl * 32 + 4 * j], row[bl * 32 + 4 * j + 1], row[bl * 32 + 4 * j + 2],
+                            row[bl * 32 + 4 * j + 3]};
+        uint16_t dh;
+        const uint32_t qw = quantize4(f, dh);
+        *(uint32_t*)(xq + bl * 32 + 4 * j) = qw;
+        if (j == 0) xd[bl] = dh;
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void lgx_k_embed(const lgx_embed_args a) {
+    const int b = blockIdx.x;
+    const int tok = min(max(a.tokens[(int64_t)b * a.tokens_stride], 0), a.vocab - 1);
+    const uint16_t* er = a.emb + (int64_t)tok * a.n;
+    for (int i = threadIdx.x; i < a.n; i += 256) a.h[(int64_t)b * a.n + i] = h2f(er[i]);
+}
+
+// Residual combine + RMSNorm (+ Q8_0).  One workgroup per row; n <= 8192.
+// Sum of squares: halving tree over the next power of two >= n, levels of
+// stride >= 256 inside each thread (thread t owns slots t + 256k), the rest
+// across threads (LDS, then wave shuffles) -- the oracle's order.
+#define LGX_NORM_MAX 8192
+extern "C" __global__ __launch_bounds__(256) void lgx_k_add_rmsnorm_quant(const lgx_norm_args a) {
+    __shared__ float row[LGX_NORM_MAX];
+    __shared__ float red[256];
+    const int b = blockIdx.x, t = threadIdx.x;
+    float* hr = a.h + (int64_t)b * a.n;
+    for (int i = t; i < a.n; i += 256) {
+        float v = hr[i];
+        if (a.part) {
+            v = v + tree_partials(a.part, a.nr, (int64_t)a.m * a.n, (int64_t)b * a.n + i);
+            hr[i] = v;
+        }
+        row[i] = v;
+    }
+    int n2 = 256;
+    while (n2 < a.n) n2 <<= 1;
+    float v[LGX_NORM_MAX / 256];
+#pragma unroll
+    for (int k = 0; k < LGX_NORM_MAX / 256; ++k) {
+        const int i = t + 256 * k;
+        v[k] = (i < a.n) ? row[i] * row[i] : 0.0f;
+    }
+    // levels s = n2/2 ... 256: slot j += slot j + s, both owned by this thread
+    for (int s = n2 >> 1; s >= 256; s >>= 1) {
+        const int ks = s / 256;
+#pragma unroll
+        for (int k = 0; k < LGX_NORM_MAX / 256; ++k)
+            if (k < ks) v[k] = v[k] + v[k + ks];
+    }
+    red[t] = v[0];
+    __syncthreads();
+    if (t < 128) red[t] = red[t] + red[t + 128];
+    __syncthreads();
+    float S = 0.0f;
+    if (t < 64) {
+        S = red[t] + red[t + 64];
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) S = S + __shfl_down(S, s, 64);
+    }
+    __syncthreads();
+    if (t == 0) red[0] = S;
+    __syncthreads();
+    const float ms = red[0] / (float)a.n;
+    const float r = 1.0f / sqrtf(ms + a.eps);
+    for (int i = t; i < a.n; i += 256) {
+        const float y = (row[i] * r) * a.w[i];
+        row[i] = y;
+        if (a.xn) a.xn[(int64_t)b * a.n + i] = y;
+    }
+    if (a.xq) {
+        __syncthreads();
+        quantize_row_from_lds(row, a.n, a.xq + (int64_t)b * a.n, a.xd + (int64_t)b * (a.n / 32));
+    }
+}
+
+// QKV combine + bias + RoPE + paged KV append.  One workgroup per sequence.
+#define LGX_QKV_MAX 8192
+extern "C" __global__ __launch_bounds__(256) void lgx_k_qkv_rope_append(const lgx_qkv_args a) {
+    __shared__ float row[LGX_QKV_MAX];
+    const int b = blockIdx.x, t = threadIdx.x;
+    const int d = a.d, half = d / 2;
+    const int nq = (a.hq + 2 * a.hkv) * d;
+    for (int i = t; i < nq; i += 256) {
+        const float v = tree_partials(a.part, a.nr, (int64_t)a.m * nq, (int64_t)b * nq + i);
+        row[i] = a.bias ? v + a.bias[i] : v;
+    }
+    __syncthreads();
+    const int pos = min(max(a.seq_len[b], 0), a.max_seq - 1);
+    const float* cr = a.cos_t + (int64_t)pos * half;
+    const float* sr = a.sin_t + (int64_t)pos * half;
+    const int page = min(max(a.page_table[(int64_t)b * a.maxp + pos / LGX_PAGE], 0), a.num_pages - 1);
+    const int slot = pos % LGX_PAGE;
+    // rotate q heads and k heads: pair (i, i + d/2) of head hh
+    for (int e = t; e < (a.hq + a.hkv) * half; e += 256) {
+        const int hh = e / half, i = e - hh * half;
+        const float x0 = row[hh * d + i], x1 = row[hh * d + i + half];
+        const float c = cr[i], s = sr[i];
+        const float t0 = x0 * c, t1 = x1 * s, t2 = x1 * c, t3 = x0 * s;
+        const float y0 = t0 - t1, y1 = t2 + t3;
+        if (hh < a.hq) {
+            float* qo = a.q_out + ((int64_t)b * a.hq + hh) * d;
+            qo[i] = y0;
+            qo[i + half] = y1;
+        } else {
+            const int g = hh - a.hq;
+            uint16_t* kd = a.kpages + (((int64_t)page * a.hkv + g) * LGX_PAGE + slot) * d;
+            kd[i] = f2h(y0);
+            kd[i + half] = f2h(y1);
+        }
+    }
+    for (int e = t; e < a.hkv * d; e += 256) {
+        const int g = e / d, i = e - g * d;
+        uint16_t* vd = a.vpages + (((int64_t)page * a.hkv + g) * LGX_PAGE + slot) * d;
+        vd[i] = f2h(row[(a.hq + a.hkv) * d + e]);
+    }
+}
+
+// Attention chunk merge for one sequence (all heads) + Q8_0 of the row.
+template <int D>
+__device__ __forceinline__ void attn_combine_quant_body(const lgx_attn_args& a) {
+    __shared__ float row[64 * 128];
+    const int b = blockIdx.x, t = threadIdx.x;
+    const int L = min(a.seq_len[b] + a.len_add, a.maxlen);
+    const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
+    for (int e = t; e < a.hq * D; e += 256) {
+        const int h = e / D, i = e - h * D;
+        const float* pp = a.part + ((int64_t)b * a.hq + h) * a.nchunk * (D + 2);
+        float M = -__builtin_inff();
+        for (int c = 0; c < nc; ++c) M = fmaxf(M, pp[c * (D + 2) + D]);
+        float Ls = 0.0f, O = 0.0f;
+        for (int c = 0; c < nc; ++c) {
+            const float w = lgx_expf(pp[c * (D + 2) + D] - M);
+            Ls = fmaf(w, pp[c * (D + 2) + D + 1], Ls);
+            O = fmaf(w, pp[c * (D + 2) + i], O);
+        }
+        const float o = nc > 0 ? O / Ls : 0.0f;
+        row[e] = o;
+        if (a.out) a.out[(int64_t)b * a.hq * D + e] = o;
+    }
+    __syncthreads();
+    quantize_row_from_lds(row, a.hq * D, a.xq + (int64_t)b * a.hq * D,
+                          a.xd + (int64_t)b * (a.hq * D / 32));
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_attn_combine_quant_d64(const lgx_attn_args a) {
+    attn_combine_quant_body<64>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_attn_combine_quant_d128(const lgx_attn_args a) {
+    attn_combine_quant_body<128>(a);
+}
+
+// SwiGLU from gate|up partials + Q8_0.  grid = (rows, ceil(blocks / 32)),
+// 256 threads = 32 blocks of 32 values.
+extern "C" __global__ __launch_bounds__(256) void lgx_k_swiglu_quant(const lgx_swiglu_args a) {
+    const int b = blockIdx.x;
+    const int bl = blockIdx.y * 32 + (threadIdx.x >> 3), j = threadIdx.x & 7;
+    const int nbl = a.inter / 32;
+    const bool on = bl < nbl;
+    const int64_t stride = (int64_t)a.m * 2 * a.inter;
+    float f[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        f[e] = 0.0f;
+        if (on) {
+            const int i = bl * 32 + 4 * j + e;
+            const int64_t base = (int64_t)b * 2 * a.inter;
+            const float g = tree_partials(a.part, a.nr, stride, base + i);
+            const float u = tree_partials(a.part, a.nr, stride, base + a.inter + i);
+            f[e] = lgx_silu(g) * u;
+        }
+    }
+    if (on && a.y) {
+        float* yo = a.y + (int64_t)b * a.inter + bl * 32 + 4 * j;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) yo[e] = f[e];
+    }
+    uint16_t dh;
+    const uint32_t qw = quantize4(f, dh);
+    if (on && a.xq) {
+        *(uint32_t*)(a.xq + (int64_t)b * a.inter + bl * 32 + 4 * j) = qw;
+        if (j == 0) a.xd[(int64_t)b * nbl + bl] = dh;
+    }
+}
+
+// Tied binary16 lm_head (h <= 1024: a single canonical range, so the logit
+// is the sequential fmaf chain over the columns).  A workgroup owns 256
+// vocabulary rows (one per thread); 64-column slabs of its rows are staged in
+// LDS with coalesced loads and every thread runs the chain of its row for
+// all m activation rows (activation values are workgroup-uniform).  m <= 64.
+#define LGX_LM_MAXM 64
+extern "C" __global__ __launch_bounds__(256) void lgx_k_lm_head_f16(const lgx_lmhead_args a) {
+    __shared__ uint32_t slab[256][33];             // 64 binary16 per row, padded
+    const int t = threadIdx.x;
+    const int v0 = blockIdx.x * 256;
+    const int v = v0 + t;
+    float acc[LGX_LM_MAXM];
+#pragma unroll
+    for (int r = 0; r < LGX_LM_MAXM; ++r) acc[r] = 0.0f;
+    for (int k0 = 0; k0 < a.h; k0 += 64) {
+        __syncthreads();
+        for (int s = t; s < 256 * 32; s += 256) {
+            const int rr = s >> 5, cc = s & 31;
+            const int vv = min(v0 + rr, a.vocab - 1);
+            slab[rr][cc] = *(const uint32_t*)(a.emb + (int64_t)vv * a.h + k0 + 2 * cc);
+        }
+        __syncthreads();
+        for (int cc = 0; cc < 32; ++cc) {
+            const uint32_t w2 = slab[t][cc];
+            const float e0 = h2f(w2 & 0xffffu), e1 = h2f(w2 >> 16);
+            const int k = k0 + 2 * cc;
+#pragma unroll
+            for (int r = 0; r < LGX_LM_MAXM; ++r) {
+                if (r < a.m) {
+                    acc[r] = fmaf(a.x[(int64_t)r * a.h + k], e0, acc[r]);
+                    acc[r] = fmaf(a.x[(int64_t)r * a.h + k + 1], e1, acc[r]);
+                }
+            }
+        }
+    }
+    if (v >= a.vocab) return;
+#pragma unroll
+    for (int r = 0; r < LGX_LM_MAXM; ++r)
+        if (r < a.m) a.logits[(int64_t)r * a.vocab + v] = acc[r];
+}
+
+// Greedy token + state advance.  One workgroup per row: per-thread first
+// maximum over a strided scan (NaN skipped), then a (value, index) reduction
+// preferring the larger value and, on ties, the lower index.
+extern "C" __global__ __launch_bounds__(256) void lgx_k_argmax_advance(const lgx_argmax_args a) {
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    const int b = blockIdx.x, t = threadIdx.x;
+    const int64_t stride = (int64_t)a.m * a.vocab;
+    float best = -__builtin_inff();
+    int idx = 0x7fffffff;
+    for (int v = t; v < a.vocab; v += 256) {
+        const float x = a.nr == 1 ? a.part[(int64_t)b * a.vocab + v]
+                                  : tree_partials(a.part, a.nr, stride, (int64_t)b * a.vocab + v);
+        if (x == x && (idx == 0x7fffffff || x > best)) {
+            best = x;
+            idx = v;
+        }
+    }
+    bv[t] = best;
+    bi[t] = idx;
+    __syncthreads();
+    for (int s = 128; s >= 1; s >>= 1) {
+        if (t < s) {
+            const float ov = bv[t + s];
+            const int oi = bi[t + s];
+            if (oi != 0x7fffffff &&
+                (bi[t] == 0x7fffffff || ov > bv[t] || (ov == bv[t] && oi < bi[t]))) {
+                bv[t] = ov;
+                bi[t] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        const int nxt = bi[0] == 0x7fffffff ? 0 : bi[0];
+        a.tokens[b] = nxt;
+        if (a.seq_len) a.seq_len[b] += a.advance;
+    }
+}
+
+extern "C" __global__ __launch_bounds__(64) void lgx_k_advance(const lgx_advance_args a) {
+    const int b = blockIdx.x * 64 + threadIdx.x;
+    if (b < a.m) a.seq_len[b] = (a.keep ? a.seq_len[b] : 0) + a.add;
 }

@@ -1,0 +1,525 @@
+// lgx_model.cpp -- the random-init Qwen2-shaped Q8_0 model on one device:
+// creation from a seed, the batched greedy decode step and the teacher-forced
+// prefill.  One decode step is a chain of stream-ordered launches that never
+// returns to the host:
+//
+//   embed(tokens) -> h
+//   per layer:  norm+Q8(h [+= down partials of the previous layer])
+//               -> QKV product (range partials) -> tree+bias+RoPE+KV append
+//               -> attention chunks -> chunk merge+Q8
+//               -> O product -> h += tree, norm+Q8
+//               -> gate|up product -> tree+SwiGLU+Q8 -> down product
+//   final norm (+Q8) -> lm_head (fp16 tied: exact chain; Q8 untied: product)
+//   -> argmax over the vocabulary, tokens <- next, seq_len += 1
+//
+// Every product writes its canonical range partials and the consumer applies
+// the tree, so the step has no combine launches and every value is the one
+// the CPU oracle computes.  The reference has no model runtime; the seam it
+// would bind is the extern "C" surface in include/lgx.h.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "lgx_gen.h"
+#include "lgx_internal.h"
+
+using namespace lgxi;
+
+namespace {
+constexpr uint32_t kModelMagic = 0x4c47584du;  // "LGXM"
+
+struct DevQ8 {
+    int8_t* qs = nullptr;
+    uint16_t* d = nullptr;
+    lgx_q8_matrix m{};
+};
+}  // namespace
+
+struct lgx_model {
+    uint32_t magic = kModelMagic;
+    lgx_ctx* ctx = nullptr;
+    lgx_qwen_config c{};
+    uint64_t seed = 0;
+    int32_t qkv_n = 0, maxp = 0, num_pages = 0, nchunk = 0;
+    std::vector<DevQ8> qkv, o, gu, dn;
+    DevQ8 lm;
+    std::vector<float*> bias;
+    std::vector<uint16_t*> kc, vc;
+    uint16_t* emb = nullptr;
+    float* ones = nullptr;
+    float *cos_t = nullptr, *sin_t = nullptr;
+    int32_t* page_table = nullptr;
+    int32_t* seq_len = nullptr;
+    // activations for max_batch rows
+    float* h = nullptr;
+    float* xn = nullptr;
+    int8_t* xq = nullptr;
+    uint16_t* xd = nullptr;
+    float* q = nullptr;
+    float* part = nullptr;
+    float* attn_part = nullptr;
+    float* logits = nullptr;
+    int32_t* scratch_tok = nullptr;
+    int32_t last_nr = 1;       // partial count of the last lm_head
+    int32_t last_B = 0;        // batch of the last lm_head
+    std::vector<void*> allocs;
+
+    ~lgx_model() {
+        for (void* p : allocs) (void)hipFree(p);
+    }
+};
+
+namespace {
+
+bool valid_model(const lgx_model* m) { return m && m->magic == kModelMagic && valid_ctx(m->ctx); }
+
+template <class T>
+lgx_status dev_alloc(lgx_model* m, T** p, size_t count) {
+    void* v = nullptr;
+    hipError_t e = hipMalloc(&v, std::max<size_t>(count * sizeof(T), 256));
+    if (e != hipSuccess)
+        return fail(LGX_OUT_OF_MEMORY, "model allocation of %zu bytes: %s", count * sizeof(T),
+                    hipGetErrorString(e));
+    m->allocs.push_back(v);
+    *p = (T*)v;
+    return LGX_OK;
+}
+
+// Generate a Q8_0 matrix on the host (streams s, s+1), upload it row-major
+// into the staging buffers and repack into the device tile layouts.
+lgx_status make_q8(lgx_model* m, uint64_t stream, int32_t n, int32_t k, DevQ8* out,
+                   int8_t* stage_q, uint16_t* stage_d, std::vector<int8_t>& hq,
+                   std::vector<uint16_t>& hd) {
+    const int64_t nq = (int64_t)n * k, nd = (int64_t)n * (k / 32);
+    hq.resize(nq);
+    hd.resize(nd);
+    lgxg::gen_i8(m->seed, stream, hq.data(), nq);
+    lgxg::gen_q8_scales(m->seed, stream + 1, hd.data(), nd);
+    lgx_status st;
+    if ((st = dev_alloc(m, &out->qs, (size_t)nq)) != LGX_OK) return st;
+    if ((st = dev_alloc(m, &out->d, lgx_q8_scale_count(n, k))) != LGX_OK) return st;
+    LGX_HIP(hipMemcpy(stage_q, hq.data(), nq, hipMemcpyHostToDevice));
+    LGX_HIP(hipMemcpy(stage_d, hd.data(), nd * 2, hipMemcpyHostToDevice));
+    lgx_repack_args ra{stage_q, out->qs, n, k, 1};
+    if ((st = launch(m->ctx, K_REPACK, dim3(cdiv((int64_t)(n / 16) * (k / 64) * 64, 256)), dim3(256),
+                     ra, nullptr)) != LGX_OK)
+        return st;
+    lgx_srepack_args sa{stage_d, out->d, n, k, 1};
+    if ((st = launch(m->ctx, K_REPACK_S16, dim3(cdiv((int64_t)lgx_q8_scale_count(n, k), 256)),
+                     dim3(256), sa, nullptr)) != LGX_OK)
+        return st;
+    LGX_HIP(hipDeviceSynchronize());     // staging reused by the next matrix
+    out->m = lgx_q8_matrix{out->qs, out->d, n, k, LGX_Q8_T16};
+    return LGX_OK;
+}
+
+lgx_status check_config(const lgx_qwen_config* c) {
+    const int hq = c->n_heads, hkv = c->n_kv_heads, d = c->head_dim, H = c->hidden,
+              I = c->intermediate;
+    if (c->n_layers <= 0 || H <= 0 || I <= 0 || hq <= 0 || hkv <= 0 || c->vocab <= 0 ||
+        c->max_batch <= 0 || c->max_seq <= 0)
+        return fail(LGX_INVALID_ARGUMENT, "non-positive model dimension");
+    if ((d != 64 && d != 128) || hq % hkv != 0 || hq / hkv > 8)
+        return fail(LGX_UNSUPPORTED, "head_dim %d, %d/%d heads", d, hq, hkv);
+    if (H % 64 || I % 64 || (hq * d) % 64 || ((hq + 2 * hkv) * d) % 16)
+        return fail(LGX_UNSUPPORTED, "hidden/intermediate/head sizes must be multiples of 64");
+    if (H > 8192 || (hq + 2 * hkv) * d > 8192 || hq * d > 8192 || I > 32768)
+        return fail(LGX_UNSUPPORTED, "hidden %d / qkv %d / intermediate %d too large", H,
+                    (hq + 2 * hkv) * d, I);
+    if (c->tied_embedding && H > 1024)
+        return fail(LGX_UNSUPPORTED, "tied binary16 lm_head needs hidden <= 1024 (got %d)", H);
+    if (!c->tied_embedding && c->vocab % 16)
+        return fail(LGX_UNSUPPORTED, "untied Q8_0 lm_head needs vocab %% 16 == 0");
+    return LGX_OK;
+}
+
+inline Kern prod_kernel(int m) {
+    return m == 1 ? K_GEMV_MFMA : m <= 16 ? K_GEMM_MFMA16 : m <= 32 ? K_GEMM_MFMA32 : K_GEMM_MFMA64;
+}
+
+lgx_status product(lgx_model* md, const DevQ8& W, int m, void* stream) {
+    return run_q8(md->ctx, prod_kernel(m), &W.m, nullptr, md->xq, md->xd, m, md->part, nullptr,
+                  stream, nullptr, nullptr, md->part);
+}
+
+lgx_status norm(lgx_model* md, int m, int n, int nr_part, bool with_part, float* xn, bool q8,
+                void* stream) {
+    lgx_norm_args a{};
+    a.part = with_part ? md->part : nullptr;
+    a.nr = nr_part;
+    a.h = md->h;
+    a.w = md->ones;
+    a.xn = xn;
+    a.xq = q8 ? md->xq : nullptr;
+    a.xd = q8 ? md->xd : nullptr;
+    a.m = m;
+    a.n = n;
+    a.eps = md->c.rms_eps;
+    return launch(md->ctx, K_ADD_RMSNORM_QUANT, dim3(m), dim3(256), a, stream);
+}
+
+// One token per sequence 0..B-1 through every layer; leaves the down
+// partials of the last layer in md->part (for the final norm).
+lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride, void* stream) {
+    lgx_ctx* c = md->ctx;
+    const lgx_qwen_config& cf = md->c;
+    const int H = cf.hidden, I = cf.intermediate, d = cf.head_dim, hq = cf.n_heads,
+              hkv = cf.n_kv_heads;
+    lgx_status st;
+    lgx_embed_args ea{md->emb, tokens, md->h, B, H, cf.vocab, tokens_stride};
+    if ((st = launch(c, K_EMBED, dim3(B), dim3(256), ea, stream)) != LGX_OK) return st;
+    for (int l = 0; l < cf.n_layers; ++l) {
+        // norm (+ residual of the previous layer's down product) -> Q8
+        if ((st = norm(md, B, H, nranges_of(I), l > 0, nullptr, true, stream)) != LGX_OK) return st;
+        if ((st = product(md, md->qkv[l], B, stream)) != LGX_OK) return st;
+        lgx_qkv_args qa{};
+        qa.part = md->part;
+        qa.nr = nranges_of(H);
+        qa.bias = md->bias[l];
+        qa.cos_t = md->cos_t;
+        qa.sin_t = md->sin_t;
+        qa.seq_len = md->seq_len;
+        qa.page_table = md->page_table;
+        qa.kpages = md->kc[l];
+        qa.vpages = md->vc[l];
+        qa.q_out = md->q;
+        qa.m = B;
+        qa.hq = hq;
+        qa.hkv = hkv;
+        qa.d = d;
+        qa.maxp = md->maxp;
+        qa.num_pages = md->num_pages;
+        qa.max_seq = cf.max_seq;
+        if ((st = launch(c, K_QKV_ROPE_APPEND, dim3(B), dim3(256), qa, stream)) != LGX_OK) return st;
+        lgx_attn_args aa{};
+        aa.q = md->q;
+        aa.kpages = md->kc[l];
+        aa.vpages = md->vc[l];
+        aa.page_table = md->page_table;
+        aa.seq_len = md->seq_len;
+        aa.part = md->attn_part;
+        aa.out = nullptr;
+        aa.B = B;
+        aa.hq = hq;
+        aa.hkv = hkv;
+        aa.maxp = md->maxp;
+        aa.nchunk = md->nchunk;
+        aa.num_pages = md->num_pages;
+        aa.maxlen = cf.max_seq;
+        aa.len_add = 1;
+        aa.scale = (float)(1.0 / std::sqrt((double)d));
+        aa.xq = md->xq;
+        aa.xd = md->xd;
+        if ((st = launch(c, (Kern)attn_kernel(d, hq / hkv), dim3(md->nchunk, B * hkv), dim3(256), aa,
+                         stream)) != LGX_OK)
+            return st;
+        if ((st = launch(c, d == 64 ? K_ATTN_COMBINE_QUANT_D64 : K_ATTN_COMBINE_QUANT_D128, dim3(B),
+                         dim3(256), aa, stream)) != LGX_OK)
+            return st;
+        if ((st = product(md, md->o[l], B, stream)) != LGX_OK) return st;
+        if ((st = norm(md, B, H, nranges_of(hq * d), true, nullptr, true, stream)) != LGX_OK)
+            return st;
+        if ((st = product(md, md->gu[l], B, stream)) != LGX_OK) return st;
+        lgx_swiglu_args sw{md->part, nranges_of(H), md->xq, md->xd, nullptr, B, I};
+        if ((st = launch(c, K_SWIGLU_QUANT, dim3(B, cdiv(I / 32, 32)), dim3(256), sw, stream)) !=
+            LGX_OK)
+            return st;
+        if ((st = product(md, md->dn[l], B, stream)) != LGX_OK) return st;
+    }
+    return LGX_OK;
+}
+
+// Final norm, lm_head and greedy token into `next`; seq_len += 1.
+lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
+    lgx_ctx* c = md->ctx;
+    const lgx_qwen_config& cf = md->c;
+    const int H = cf.hidden;
+    lgx_status st;
+    const bool tied = cf.tied_embedding != 0;
+    if ((st = norm(md, B, H, nranges_of(cf.intermediate), true, md->xn, !tied, stream)) != LGX_OK)
+        return st;
+    lgx_argmax_args am{};
+    if (tied) {
+        for (int r0 = 0; r0 < B; r0 += 64) {
+            lgx_lmhead_args la{md->xn + (int64_t)r0 * H, md->emb, md->logits + (int64_t)r0 * cf.vocab,
+                               std::min(64, B - r0), H, cf.vocab};
+            if ((st = launch(c, K_LM_HEAD_F16, dim3(cdiv(cf.vocab, 256)), dim3(256), la, stream)) !=
+                LGX_OK)
+                return st;
+        }
+        am.part = md->logits;
+        am.nr = 1;
+    } else {
+        if ((st = product(md, md->lm, B, stream)) != LGX_OK) return st;
+        am.part = md->part;
+        am.nr = nranges_of(H);
+    }
+    md->last_nr = am.nr;
+    md->last_B = B;
+    am.tokens = next;
+    am.seq_len = md->seq_len;
+    am.m = B;
+    am.vocab = cf.vocab;
+    am.advance = 1;
+    return launch(c, K_ARGMAX_ADVANCE, dim3(B), dim3(256), am, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+lgx_status lgx_model_create(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed,
+                            lgx_model** out) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!cfg || !out) return fail(LGX_NULL_POINTER, "NULL config or out");
+        *out = nullptr;
+        if ((st = check_config(cfg)) != LGX_OK) return st;
+        auto* m = new lgx_model();
+        m->ctx = c;
+        m->c = *cfg;
+        m->seed = seed;
+        const lgx_qwen_config& cf = *cfg;
+        const int H = cf.hidden, I = cf.intermediate, d = cf.head_dim, hq = cf.n_heads,
+                  hkv = cf.n_kv_heads, L = cf.n_layers, B = cf.max_batch;
+        m->qkv_n = (hq + 2 * hkv) * d;
+        m->maxp = (cf.max_seq + LGX_PAGE - 1) / LGX_PAGE;
+        m->num_pages = B * m->maxp;
+        m->nchunk = (cf.max_seq + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
+        auto done = [&](lgx_status s) {
+            if (s != LGX_OK) delete m;
+            else *out = m;
+            return s;
+        };
+        // staging for the row-major upload of the largest Q8 matrix
+        int64_t big = std::max<int64_t>({(int64_t)m->qkv_n * H, (int64_t)H * hq * d,
+                                         (int64_t)2 * I * H, (int64_t)H * I,
+                                         cf.tied_embedding ? 0 : (int64_t)cf.vocab * H});
+        int8_t* stage_q = nullptr;
+        uint16_t* stage_d = nullptr;
+        if ((st = dev_alloc(m, &stage_q, (size_t)big)) != LGX_OK) return done(st);
+        if ((st = dev_alloc(m, &stage_d, (size_t)(big / 32))) != LGX_OK) return done(st);
+        std::vector<int8_t> hq8;
+        std::vector<uint16_t> hd16;
+        m->qkv.resize(L);
+        m->o.resize(L);
+        m->gu.resize(L);
+        m->dn.resize(L);
+        m->bias.resize(L);
+        m->kc.resize(L);
+        m->vc.resize(L);
+        const size_t kv_elems = (size_t)m->num_pages * hkv * LGX_PAGE * d;
+        std::vector<float> hb(m->qkv_n);
+        for (int l = 0; l < L; ++l) {
+            const uint64_t base = 1000 + 16 * (uint64_t)l;
+            if ((st = make_q8(m, base + 0, m->qkv_n, H, &m->qkv[l], stage_q, stage_d, hq8, hd16)) ||
+                (st = make_q8(m, base + 2, H, hq * d, &m->o[l], stage_q, stage_d, hq8, hd16)) ||
+                (st = make_q8(m, base + 4, 2 * I, H, &m->gu[l], stage_q, stage_d, hq8, hd16)) ||
+                (st = make_q8(m, base + 6, H, I, &m->dn[l], stage_q, stage_d, hq8, hd16)))
+                return done(st);
+            lgxg::gen_normal_f32(seed, base + 8, 0.02, hb.data(), m->qkv_n);
+            if ((st = dev_alloc(m, &m->bias[l], m->qkv_n)) != LGX_OK) return done(st);
+            LGX_HIP(hipMemcpy(m->bias[l], hb.data(), m->qkv_n * 4, hipMemcpyHostToDevice));
+            if ((st = dev_alloc(m, &m->kc[l], kv_elems)) != LGX_OK ||
+                (st = dev_alloc(m, &m->vc[l], kv_elems)) != LGX_OK)
+                return done(st);
+            LGX_HIP(hipMemset(m->kc[l], 0, kv_elems * 2));
+            LGX_HIP(hipMemset(m->vc[l], 0, kv_elems * 2));
+        }
+        if (!cf.tied_embedding &&
+            (st = make_q8(m, 2, cf.vocab, H, &m->lm, stage_q, stage_d, hq8, hd16)) != LGX_OK)
+            return done(st);
+        hq8.clear();
+        hq8.shrink_to_fit();
+        {
+            std::vector<uint16_t> he((size_t)cf.vocab * H);
+            lgxg::gen_normal_f16(seed, 1, cf.emb_sigma, he.data(), (int64_t)he.size());
+            if ((st = dev_alloc(m, &m->emb, he.size())) != LGX_OK) return done(st);
+            LGX_HIP(hipMemcpy(m->emb, he.data(), he.size() * 2, hipMemcpyHostToDevice));
+        }
+        {
+            const int mx = std::max(H, I);
+            std::vector<float> one(mx, 1.0f);
+            if ((st = dev_alloc(m, &m->ones, mx)) != LGX_OK) return done(st);
+            LGX_HIP(hipMemcpy(m->ones, one.data(), mx * 4, hipMemcpyHostToDevice));
+            std::vector<float> ct((size_t)cf.max_seq * (d / 2)), stb(ct.size());
+            for (int p = 0; p < cf.max_seq; ++p)
+                for (int i = 0; i < d / 2; ++i) {
+                    const double inv = std::pow(cf.rope_theta, -(2.0 * i) / (double)d);
+                    const double ang = (double)p * inv;
+                    ct[(size_t)p * (d / 2) + i] = (float)std::cos(ang);
+                    stb[(size_t)p * (d / 2) + i] = (float)std::sin(ang);
+                }
+            if ((st = dev_alloc(m, &m->cos_t, ct.size())) != LGX_OK ||
+                (st = dev_alloc(m, &m->sin_t, ct.size())) != LGX_OK)
+                return done(st);
+            LGX_HIP(hipMemcpy(m->cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice));
+            LGX_HIP(hipMemcpy(m->sin_t, stb.data(), stb.size() * 4, hipMemcpyHostToDevice));
+            std::vector<int32_t> pt(m->num_pages);
+            lgxg::gen_permutation(seed, 4, pt.data(), m->num_pages);
+            if ((st = dev_alloc(m, &m->page_table, pt.size())) != LGX_OK) return done(st);
+            LGX_HIP(hipMemcpy(m->page_table, pt.data(), pt.size() * 4, hipMemcpyHostToDevice));
+        }
+        if ((st = dev_alloc(m, &m->seq_len, B)) != LGX_OK) return done(st);
+        LGX_HIP(hipMemset(m->seq_len, 0, B * 4));
+        const int kmax = std::max({H, I, hq * d});
+        int64_t part = 0;
+        auto upd = [&](int n, int k) {
+            part = std::max<int64_t>(part, (int64_t)nranges_of(k) * B * n);
+        };
+        upd(m->qkv_n, H);
+        upd(H, hq * d);
+        upd(2 * I, H);
+        upd(H, I);
+        if (!cf.tied_embedding) upd(cf.vocab, H);
+        if ((st = dev_alloc(m, &m->h, (size_t)B * H)) || (st = dev_alloc(m, &m->xn, (size_t)B * H)) ||
+            (st = dev_alloc(m, &m->xq, (size_t)B * kmax)) ||
+            (st = dev_alloc(m, &m->xd, (size_t)B * kmax / 32)) ||
+            (st = dev_alloc(m, &m->q, (size_t)B * hq * d)) || (st = dev_alloc(m, &m->part, (size_t)part)) ||
+            (st = dev_alloc(m, &m->attn_part, (size_t)B * hq * m->nchunk * (d + 2))) ||
+            (st = dev_alloc(m, &m->logits, cf.tied_embedding ? (size_t)B * cf.vocab : 1)) ||
+            (st = dev_alloc(m, &m->scratch_tok, (size_t)B)))
+            return done(st);
+        // staging no longer needed
+        LGX_HIP(hipDeviceSynchronize());
+        for (void* p : {(void*)stage_q, (void*)stage_d}) {
+            (void)hipFree(p);
+            m->allocs.erase(std::find(m->allocs.begin(), m->allocs.end(), p));
+        }
+        return done(LGX_OK);
+    });
+}
+
+lgx_status lgx_model_destroy(lgx_model* m) {
+    return guarded(__func__, [&]() -> lgx_status {
+        if (!valid_model(m)) return fail(LGX_INVALID_HANDLE, "invalid lgx_model handle");
+        (void)hipSetDevice(m->ctx->device);
+        (void)hipDeviceSynchronize();
+        m->magic = 0;
+        delete m;
+        return LGX_OK;
+    });
+}
+
+lgx_status lgx_model_reset(lgx_model* m, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        if (!valid_model(m)) return fail(LGX_INVALID_HANDLE, "invalid lgx_model handle");
+        lgx_status st = enter(m->ctx);
+        if (st != LGX_OK) return st;
+        lgx_advance_args a{m->seq_len, m->c.max_batch, 0, 0};
+        return launch(m->ctx, K_ADVANCE, dim3(cdiv(m->c.max_batch, 64)), dim3(64), a, stream);
+    });
+}
+
+lgx_status lgx_qwen_decode_step(lgx_model* m, int32_t B, int32_t* tokens, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        if (!valid_model(m)) return fail(LGX_INVALID_HANDLE, "invalid lgx_model handle");
+        lgx_status st = enter(m->ctx);
+        if (st != LGX_OK) return st;
+        if (!tokens) return fail(LGX_NULL_POINTER, "NULL tokens");
+        if (B <= 0 || B > m->c.max_batch)
+            return fail(LGX_OUT_OF_BOUNDS, "B = %d outside [1, %d]", B, m->c.max_batch);
+        if ((st = layers(m, B, tokens, 1, stream)) != LGX_OK) return st;
+        return head(m, B, tokens, stream);
+    });
+}
+
+lgx_status lgx_qwen_prefill(lgx_model* m, int32_t B, int32_t P, const int32_t* prompt,
+                            int32_t* next, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        if (!valid_model(m)) return fail(LGX_INVALID_HANDLE, "invalid lgx_model handle");
+        lgx_status st = enter(m->ctx);
+        if (st != LGX_OK) return st;
+        if (!prompt || !next) return fail(LGX_NULL_POINTER, "NULL prompt or next");
+        if (B <= 0 || B > m->c.max_batch || P <= 0)
+            return fail(LGX_OUT_OF_BOUNDS, "B = %d, P = %d", B, P);
+        for (int p = 0; p < P; ++p) {
+            if ((st = layers(m, B, prompt + p, P, stream)) != LGX_OK) return st;
+            if (p + 1 < P) {
+                lgx_advance_args a{m->seq_len, B, 1, 1};
+                if ((st = launch(m->ctx, K_ADVANCE, dim3(cdiv(B, 64)), dim3(64), a, stream)) != LGX_OK)
+                    return st;
+            } else if ((st = head(m, B, next, stream)) != LGX_OK) {
+                return st;
+            }
+        }
+        return LGX_OK;
+    });
+}
+
+lgx_status lgx_model_tensor(lgx_model* m, int32_t layer, int32_t which, const void** dev,
+                            size_t* bytes) {
+    return guarded(__func__, [&]() -> lgx_status {
+        if (!valid_model(m)) return fail(LGX_INVALID_HANDLE, "invalid lgx_model handle");
+        if (!dev || !bytes) return fail(LGX_NULL_POINTER, "NULL out pointer");
+        if (layer < 0 || layer >= m->c.n_layers) return fail(LGX_OUT_OF_BOUNDS, "layer %d", layer);
+        const lgx_qwen_config& cf = m->c;
+        auto q8 = [&](const DevQ8& w, bool scales) -> lgx_status {
+            if (!w.qs) return fail(LGX_INVALID_ARGUMENT, "tensor %d not present", which);
+            *dev = scales ? (const void*)w.d : (const void*)w.qs;
+            *bytes = scales ? lgx_q8_scale_count(w.m.n, w.m.k) * 2 : (size_t)w.m.n * w.m.k;
+            return LGX_OK;
+        };
+        switch (which) {
+            case LGX_T_EMB:
+                *dev = m->emb;
+                *bytes = (size_t)cf.vocab * cf.hidden * 2;
+                return LGX_OK;
+            case LGX_T_LM_Q: return q8(m->lm, false);
+            case LGX_T_LM_D: return q8(m->lm, true);
+            case LGX_T_QKV_Q: return q8(m->qkv[layer], false);
+            case LGX_T_QKV_D: return q8(m->qkv[layer], true);
+            case LGX_T_O_Q: return q8(m->o[layer], false);
+            case LGX_T_O_D: return q8(m->o[layer], true);
+            case LGX_T_GU_Q: return q8(m->gu[layer], false);
+            case LGX_T_GU_D: return q8(m->gu[layer], true);
+            case LGX_T_DOWN_Q: return q8(m->dn[layer], false);
+            case LGX_T_DOWN_D: return q8(m->dn[layer], true);
+            case LGX_T_QKV_BIAS:
+                *dev = m->bias[layer];
+                *bytes = (size_t)m->qkv_n * 4;
+                return LGX_OK;
+            case LGX_T_K_PAGES:
+                *dev = m->kc[layer];
+                *bytes = (size_t)m->num_pages * cf.n_kv_heads * LGX_PAGE * cf.head_dim * 2;
+                return LGX_OK;
+            case LGX_T_V_PAGES:
+                *dev = m->vc[layer];
+                *bytes = (size_t)m->num_pages * cf.n_kv_heads * LGX_PAGE * cf.head_dim * 2;
+                return LGX_OK;
+            case LGX_T_PAGE_TABLE:
+                *dev = m->page_table;
+                *bytes = (size_t)m->num_pages * 4;
+                return LGX_OK;
+            case LGX_T_SEQ_LEN:
+                *dev = m->seq_len;
+                *bytes = (size_t)cf.max_batch * 4;
+                return LGX_OK;
+            case LGX_T_HIDDEN:
+                *dev = m->xn;
+                *bytes = (size_t)cf.max_batch * cf.hidden * 4;
+                return LGX_OK;
+            default:
+                return fail(LGX_INVALID_ARGUMENT, "unknown tensor id %d", which);
+        }
+    });
+}
+
+lgx_status lgx_qwen_logits(lgx_model* m, int32_t B, float* out, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        if (!valid_model(m)) return fail(LGX_INVALID_HANDLE, "invalid lgx_model handle");
+        lgx_status st = enter(m->ctx);
+        if (st != LGX_OK) return st;
+        if (!out) return fail(LGX_NULL_POINTER, "NULL out");
+        if (B != m->last_B)
+            return fail(LGX_INVALID_ARGUMENT, "B = %d, but the last step ran %d sequences", B,
+                        m->last_B);
+        const int64_t count = (int64_t)B * m->c.vocab;
+        lgx_combine_args ca{m->c.tied_embedding ? m->logits : m->part, out, count, m->last_nr};
+        return launch(m->ctx, K_COMBINE, dim3(cdiv(count, 256)), dim3(256), ca, stream);
+    });
+}
+
+}  // extern "C"

@@ -33,8 +33,15 @@ def test_abi_version_and_status_values():
 
     src = open(HEADER).read()
     assert int(re.search(r"LGX_ABI_VERSION (\d+)u", src).group(1)) == lgx.lib().lgx_abi_version()
-    enum = dict((name, int(v)) for name, v in re.findall(r"(LGX_[A-Z_]+) = (\d+)", src))
+    block = re.search(r"typedef enum lgx_status \{(.*?)\} lgx_status;", src, re.S).group(1)
+    enum = dict((name, int(v)) for name, v in re.findall(r"(LGX_[A-Z_]+) = (\d+)", block))
     assert {v: k for k, v in enum.items()} == lgx.STATUS_NAMES
+    # model tensor ids
+    tids = dict((name[6:].lower(), int(v))
+                for name, v in re.findall(r"(LGX_T_[A-Z_]+) = (\d+)", src))
+    tids["dn_q"], tids["dn_d"] = tids.pop("down_q"), tids.pop("down_d")
+    tids["bias"] = tids.pop("qkv_bias")
+    assert tids == lgx.MODEL_TENSORS
     # LogosStatus values carried over (codegen/ffi.rs:196-209)
     assert enum["LGX_OK"] == 0 and enum["LGX_NULL_POINTER"] == 3
     assert enum["LGX_OUT_OF_BOUNDS"] == 4 and enum["LGX_INVALID_HANDLE"] == 6
@@ -104,11 +111,11 @@ def test_every_host_kernel_exists_in_code_object():
 
     import logicaffeine_amd as lgx
 
-    src = open(os.path.join(ROOT, "logicaffeine_amd", "csrc", "lgx_host.cpp")).read()
+    src = open(os.path.join(ROOT, "logicaffeine_amd", "csrc", "lgx_internal.h")).read()
     table = src[src.index("kKernelNames[] = {"):]
     table = table[:table.index("};")]
     names = re.findall(r'"(lgx_k_[a-z0-9_]+)"', table)
-    # the count against the kernel enum is a static_assert in lgx_host.cpp
+    # the count against the kernel enum is a static_assert in lgx_internal.h
     assert len(names) == len(set(names)) > 20
     readelf = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib", "llvm", "bin",
                            "llvm-readelf")
