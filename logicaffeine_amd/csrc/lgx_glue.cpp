@@ -52,7 +52,7 @@ lgx_status lgx_rmsnorm_quant(lgx_ctx* c, const float* x, const float* w, int32_t
         a.m = m;
         a.n = n;
         a.eps = eps;
-        return launch(c, K_ADD_RMSNORM_QUANT, dim3(m), dim3(256), a, stream);
+        return launch(c, K_ADD_RMSNORM_QUANT, dim3(m), dim3(LGX_GLUE_NT), a, stream);
     });
 }
 
@@ -93,7 +93,7 @@ lgx_status lgx_rope_kv_append(lgx_ctx* c, const float* qkv, const float* bias, c
         a.maxp = maxp;
         a.num_pages = num_pages;
         a.max_seq = max_seq;
-        return launch(c, K_QKV_ROPE_APPEND, dim3(B), dim3(256), a, stream);
+        return launch(c, K_QKV_ROPE_APPEND, dim3(B), dim3(LGX_GLUE_NT), a, stream);
     });
 }
 
@@ -139,8 +139,9 @@ lgx_status lgx_argmax(lgx_ctx* c, const float* logits, int32_t m, int32_t vocab,
         if (st != LGX_OK) return st;
         if (!logits || !out) return fail(LGX_NULL_POINTER, "NULL tensor");
         if (m <= 0 || vocab <= 0) return fail(LGX_INVALID_ARGUMENT, "m %d, vocab %d", m, vocab);
-        lgx_argmax_args a{logits, 1, out, nullptr, m, vocab, 0};
-        return launch(c, K_ARGMAX_ADVANCE, dim3(m), dim3(256), a, stream);
+        float* cand = nullptr;
+        if ((st = ensure_ws(c, (size_t)m * argmax_slices(vocab) * 8, &cand)) != LGX_OK) return st;
+        return launch_argmax(c, logits, 1, m, vocab, out, nullptr, 0, cand, stream);
     });
 }
 

@@ -92,7 +92,8 @@ enum Kern {
     K_ATTN_COMBINE_QUANT_D128,
     K_SWIGLU_QUANT,
     K_LM_HEAD_F16,
-    K_ARGMAX_ADVANCE,
+    K_ARGMAX_PARTIAL,
+    K_ARGMAX_FINAL,
     K_ADVANCE,
     K_COUNT
 };
@@ -110,7 +111,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_attn_combine_d64", "lgx_k_attn_combine_d128",
     "lgx_k_embed", "lgx_k_add_rmsnorm_quant", "lgx_k_qkv_rope_append",
     "lgx_k_attn_combine_quant_d64", "lgx_k_attn_combine_quant_d128", "lgx_k_swiglu_quant",
-    "lgx_k_lm_head_f16", "lgx_k_argmax_advance", "lgx_k_advance",
+    "lgx_k_lm_head_f16", "lgx_k_argmax_partial", "lgx_k_argmax_final", "lgx_k_advance",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -229,6 +230,16 @@ inline lgx_status ensure_ws(lgx_ctx* c, size_t bytes, float** out) {
     return LGX_OK;
 }
 
+inline unsigned cdiv(int64_t a, int64_t b);
+inline int argmax_slices(int vocab) { return (vocab + LGX_ARGMAX_SLICE - 1) / LGX_ARGMAX_SLICE; }
+
+// Greedy token of m rows of (range-partial) logits: candidates per slice,
+// then the per-row pick (+ seq_len advance).  cand holds m * slices floats
+// followed by m * slices ints.
+inline lgx_status launch_argmax(lgx_ctx* c, const float* part, int nr, int m, int vocab,
+                                int32_t* tokens, int32_t* seq_len, int advance, void* cand,
+                                void* stream);
+
 inline lgx_status check_q8(const lgx_q8_matrix* W) {
     if (!W) return fail(LGX_NULL_POINTER, "W is NULL");
     if (!W->qs || !W->d) return fail(LGX_NULL_POINTER, "W->qs / W->d is NULL");
@@ -299,3 +310,25 @@ inline lgx_status run_q8(lgx_ctx* c, Kern kern, const lgx_q8_matrix* W, const fl
 
 }  // namespace lgxi
 
+
+namespace lgxi {
+inline lgx_status launch_argmax(lgx_ctx* c, const float* part, int nr, int m, int vocab,
+                                int32_t* tokens, int32_t* seq_len, int advance, void* cand,
+                                void* stream) {
+    const int ns = argmax_slices(vocab);
+    lgx_argmax_args a{};
+    a.part = part;
+    a.nr = nr;
+    a.tokens = tokens;
+    a.seq_len = seq_len;
+    a.cand_v = (float*)cand;
+    a.cand_i = (int32_t*)((float*)cand + (int64_t)m * ns);
+    a.m = m;
+    a.vocab = vocab;
+    a.advance = advance;
+    a.nslices = ns;
+    lgx_status st = launch(c, K_ARGMAX_PARTIAL, dim3(ns, m), dim3(256), a, stream);
+    if (st != LGX_OK) return st;
+    return launch(c, K_ARGMAX_FINAL, dim3(m), dim3(64), a, stream);
+}
+}  // namespace lgxi

@@ -8,6 +8,7 @@
 #define LGX_Q8_RANGE_BLOCKS 32   // blocks of 32 per canonical accumulation range
 #define LGX_MAX_RANGES 32        // => K <= 32768
 #define LGX_WAVE 64
+#define LGX_GLUE_NT 1024         // threads of the row-wise glue kernels (norm, qkv)
 
 typedef struct {
     const int8_t* src;
@@ -141,11 +142,15 @@ typedef struct {
 } lgx_lmhead_args;
 
 // next[b] = first index of the max of tree(part[.][b][:]) (NaN skipped);
-// then tokens[b] = next[b] and seq_len[b] += advance.
+// then tokens[b] = next[b] and seq_len[b] += advance.  Two launches through
+// per-slice candidates cand_v/cand_i [m][nslices].
+#define LGX_ARGMAX_SLICE 4096
 typedef struct {
     const float* part;     // [nr][m][vocab]
     int32_t nr;
     int32_t* tokens;
     int32_t* seq_len;
-    int32_t m, vocab, advance;
+    float* cand_v;
+    int32_t* cand_i;
+    int32_t m, vocab, advance, nslices;
 } lgx_argmax_args;

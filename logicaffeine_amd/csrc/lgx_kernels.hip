@@ -701,7 +701,8 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
     }
     __syncthreads();
 
-    // phase 1: scores
+    // phase 1: scores.  Thread t owns token t; its whole K row is requested
+    // before the first use so all of its loads are in flight together.
     float s[GQ];
 #pragma unroll
     for (int h = 0; h < GQ; ++h) s[h] = 0.0f;
@@ -710,12 +711,15 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
         const uint4* kr = (const uint4*)(a.kpages +
                                          (((int64_t)pg_s[tid >> 4] * a.hkv + g) * LGX_PAGE + (tid & 15)) * D);
         const float* qb = a.q + ((int64_t)b * a.hq + h0) * D;
-#pragma unroll 2
+        uint4 kv[D / 8];
+#pragma unroll
+        for (int j = 0; j < D / 8; ++j) kv[j] = kr[j];
+        __builtin_amdgcn_sched_barrier(0);       // keep every load ahead of the FMAs
+#pragma unroll
         for (int j = 0; j < D / 8; ++j) {
-            const uint4 kv = kr[j];
-            const float kf[8] = {h2f(kv.x & 0xffffu), h2f(kv.x >> 16), h2f(kv.y & 0xffffu),
-                                 h2f(kv.y >> 16),     h2f(kv.z & 0xffffu), h2f(kv.z >> 16),
-                                 h2f(kv.w & 0xffffu), h2f(kv.w >> 16)};
+            const float kf[8] = {h2f(kv[j].x & 0xffffu), h2f(kv[j].x >> 16), h2f(kv[j].y & 0xffffu),
+                                 h2f(kv[j].y >> 16),     h2f(kv[j].z & 0xffffu), h2f(kv[j].z >> 16),
+                                 h2f(kv[j].w & 0xffffu), h2f(kv[j].w >> 16)};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
 #pragma unroll
@@ -765,46 +769,97 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
             }
         }
     }
-    // phase 3: o_c[i] = chain_t fmaf(p_t, V_t[i], o)
-    const int i = tid % D, hg = tid / D;
-    float o[KH];
+    // phase 3: o_c[i] = chain_t fmaf(p_t, V_t[i], o).  Thread = (dimension
+    // pair, head group): a wave reads whole 2-byte-pair V rows (coalesced),
+    // 16 tokens (one page) of loads in flight before their FMAs.  t is
+    // workgroup-uniform, so the bounds tests do not diverge.
+    constexpr int NP = D / 2;                     // dimension pairs
+    constexpr int NHG = 256 / NP;                 // head groups
+    constexpr int HPG = (GQ + NHG - 1) / NHG;     // heads per group
+    const int ip = tid % NP, hg = tid / NP;
+    float o[HPG][2];
 #pragma unroll
-    for (int k = 0; k < KH; ++k) o[k] = 0.0f;
-    const uint16_t* vb = a.vpages + (int64_t)g * LGX_PAGE * D + i;
-    for (int t = 0; t < n; ++t) {
-        const float v = h2f(vb[((int64_t)pg_s[t >> 4] * a.hkv * LGX_PAGE + (t & 15)) * D]);
+    for (int k = 0; k < HPG; ++k) o[k][0] = o[k][1] = 0.0f;
+    const uint32_t* vb = (const uint32_t*)(a.vpages + (int64_t)g * LGX_PAGE * D) + ip;
+    for (int tp = 0; tp < n; tp += LGX_PAGE) {
+        const uint32_t* vp = vb + (int64_t)pg_s[tp >> 4] * a.hkv * LGX_PAGE * (D / 2);
+        uint32_t vv[LGX_PAGE];
 #pragma unroll
-        for (int k = 0; k < KH; ++k) {
-            const int h = hg + NG * k;
-            if (h < GQ) o[k] = fmaf(p_s[h][t], v, o[k]);
+        for (int u = 0; u < LGX_PAGE; ++u) vv[u] = tp + u < n ? vp[u * (D / 2)] : 0u;
+#pragma unroll
+        for (int u = 0; u < LGX_PAGE; ++u) {
+            if (tp + u < n) {
+                const float v0 = h2f(vv[u] & 0xffffu), v1 = h2f(vv[u] >> 16);
+#pragma unroll
+                for (int k = 0; k < HPG; ++k) {
+                    const int h = hg + NHG * k;
+                    if (h < GQ) {
+                        const float pt = p_s[h][tp + u];
+                        o[k][0] = fmaf(pt, v0, o[k][0]);
+                        o[k][1] = fmaf(pt, v1, o[k][1]);
+                    }
+                }
+            }
         }
     }
 #pragma unroll
-    for (int k = 0; k < KH; ++k) {
-        const int h = hg + NG * k;
-        if (h < GQ) a.part[(((int64_t)b * a.hq + h0 + h) * a.nchunk + c) * (D + 2) + i] = o[k];
+    for (int k = 0; k < HPG; ++k) {
+        const int h = hg + NHG * k;
+        if (h < GQ) {
+            float* pp = a.part + (((int64_t)b * a.hq + h0 + h) * a.nchunk + c) * (D + 2) + 2 * ip;
+            pp[0] = o[k][0];
+            pp[1] = o[k][1];
+        }
     }
 }
 
 // Merge of the chunk partials of one (sequence, query head): M = max m_c,
 // w_c = lgx_expf(m_c - M), L = chain fmaf(w_c, l_c), O[i] = chain
-// fmaf(w_c, o_c[i]), out = O / L (0 for an empty sequence).
+// fmaf(w_c, o_c[i]), out = O / L (0 for an empty sequence).  One workgroup of
+// D threads per (sequence, head); chunk values are loaded 8 at a time so
+// their loads overlap.
 template <int D>
-__device__ __forceinline__ void attn_combine_body(const lgx_attn_args& a) {
-    const int bh = blockIdx.x, i = threadIdx.x;
+__device__ __forceinline__ float attn_merge(const lgx_attn_args& a, int bh) {
+    const int i = threadIdx.x;
     const int b = bh / a.hq;
     const int L = min(a.seq_len[b] + a.len_add, a.maxlen);
     const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
     const float* pp = a.part + (int64_t)bh * a.nchunk * (D + 2);
     float M = -__builtin_inff();
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, pp[c * (D + 2) + D]);
-    float Ls = 0.0f, O = 0.0f;
-    for (int c = 0; c < nc; ++c) {
-        const float w = lgx_expf(pp[c * (D + 2) + D] - M);
-        Ls = fmaf(w, pp[c * (D + 2) + D + 1], Ls);
-        O = fmaf(w, pp[c * (D + 2) + i], O);
+    for (int c0 = 0; c0 < nc; c0 += 8) {
+        float mv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) mv[u] = c0 + u < nc ? pp[(c0 + u) * (D + 2) + D] : -__builtin_inff();
+#pragma unroll
+        for (int u = 0; u < 8; ++u) M = fmaxf(M, mv[u]);
     }
-    a.out[(int64_t)bh * D + i] = nc > 0 ? O / Ls : 0.0f;
+    float Ls = 0.0f, O = 0.0f;
+    for (int c0 = 0; c0 < nc; c0 += 8) {
+        float mv[8], lv[8], ov[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const bool on = c0 + u < nc;
+            const float* q = pp + (c0 + u) * (D + 2);
+            mv[u] = on ? q[D] : 0.0f;
+            lv[u] = on ? q[D + 1] : 0.0f;
+            ov[u] = on ? q[i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (c0 + u < nc) {
+                const float w = lgx_expf(mv[u] - M);
+                Ls = fmaf(w, lv[u], Ls);
+                O = fmaf(w, ov[u], O);
+            }
+        }
+    }
+    return nc > 0 ? O / Ls : 0.0f;
+}
+
+template <int D>
+__device__ __forceinline__ void attn_combine_body(const lgx_attn_args& a) {
+    const int bh = blockIdx.x;
+    a.out[(int64_t)bh * D + threadIdx.x] = attn_merge<D>(a, bh);
 }
 
 #define LGX_ATTN_KERNELS(D, G)                                                                    \
@@ -878,12 +933,13 @@ __device__ __forceinline__ uint32_t quantize4(const float (&f)[4], uint16_t& dh)
     return qw;
 }
 
-// Quantise a row held in LDS (n floats, n % 32 == 0) to xq/xd (256 threads;
-// 8 threads per block, the 8 lanes of a block always active together).
+// Quantise a row held in LDS (n floats, n % 32 == 0) to xq/xd with NT
+// threads: 8 threads per block, the 8 lanes of a block always active together.
+template <int NT>
 __device__ __forceinline__ void quantize_row_from_lds(const float* row, int n, int8_t* xq,
                                                       uint16_t* xd) {
     const int j = threadIdx.x & 7;
-    for (int bl = threadIdx.x >> 3; bl < n / 32; bl += 32) {
+    for (int bl = threadIdx.x >> 3; bl < n / 32; bl += NT / 8) {
         const float f[4] = {row[bl * 32 + 4 * j], row[bl * 32 + 4 * j + 1], row[bl * 32 + 4 * j + 2],
                             row[bl * 32 + 4 * j + 3]};
         uint16_t dh;
@@ -893,6 +949,32 @@ __device__ __forceinline__ void quantize_row_from_lds(const float* row, int n, i
     }
 }
 
+// Canonical tree over the nr (<= R) range partials of NE elements i0,
+// i0 + di, ... of one thread, with every load issued before the first add.
+template <int R>
+__device__ __forceinline__ float tree_sum_r(float (&p)[R], int g) {
+#pragma unroll
+    for (int s = 1; s < R; s <<= 1) {
+#pragma unroll
+        for (int i = 0; i + s < R; i += 2 * s)
+            if (i + s < g) p[i] = p[i] + p[i + s];
+    }
+    return p[0];
+}
+template <int NE, int R>
+__device__ __forceinline__ void tree_partials_n(const float* part, int nr, int64_t stride,
+                                                int64_t i0, int64_t di, const bool (&on)[NE],
+                                                float (&out)[NE]) {
+    float p[NE][R];
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+        for (int e = 0; e < NE; ++e)
+            p[e][j] = (j < nr && on[e]) ? part[j * stride + i0 + e * di] : 0.0f;
+#pragma unroll
+    for (int e = 0; e < NE; ++e) out[e] = tree_sum_r<R>(p[e], nr);
+}
+
 extern "C" __global__ __launch_bounds__(256) void lgx_k_embed(const lgx_embed_args a) {
     const int b = blockIdx.x;
     const int tok = min(max(a.tokens[(int64_t)b * a.tokens_stride], 0), a.vocab - 1);
@@ -900,75 +982,126 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_embed(const lgx_embed_ar
     for (int i = threadIdx.x; i < a.n; i += 256) a.h[(int64_t)b * a.n + i] = h2f(er[i]);
 }
 
-// Residual combine + RMSNorm (+ Q8_0).  One workgroup per row; n <= 8192.
-// Sum of squares: halving tree over the next power of two >= n, levels of
-// stride >= 256 inside each thread (thread t owns slots t + 256k), the rest
-// across threads (LDS, then wave shuffles) -- the oracle's order.
+// Residual combine + RMSNorm (+ Q8_0).  One workgroup of 1024 threads per
+// row; n <= 8192.  Sum of squares: halving tree over the next power of two
+// >= n (zero padded), levels of stride >= 1024 inside each thread (thread t
+// owns slots t + 1024k), then across threads (LDS, then wave shuffles) --
+// the oracle's order, whatever the thread count.
 #define LGX_NORM_MAX 8192
-extern "C" __global__ __launch_bounds__(256) void lgx_k_add_rmsnorm_quant(const lgx_norm_args a) {
+extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_add_rmsnorm_quant(const lgx_norm_args a) {
+    constexpr int NT = LGX_GLUE_NT, KV = LGX_NORM_MAX / NT;
     __shared__ float row[LGX_NORM_MAX];
-    __shared__ float red[256];
+    __shared__ float red[NT];
     const int b = blockIdx.x, t = threadIdx.x;
     float* hr = a.h + (int64_t)b * a.n;
-    for (int i = t; i < a.n; i += 256) {
-        float v = hr[i];
-        if (a.part) {
-            v = v + tree_partials(a.part, a.nr, (int64_t)a.m * a.n, (int64_t)b * a.n + i);
-            hr[i] = v;
+    bool on[KV];
+    float upd[KV];
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+        on[k] = t + NT * k < a.n;
+        upd[k] = 0.0f;
+    }
+    if (a.part) {
+        // two elements per round: 2 x nr loads in flight, bounded registers
+#pragma unroll
+        for (int k = 0; k < KV; k += 2) {
+            if (on[k]) {
+                const bool o2[2] = {on[k], on[k + 1]};
+                float u2[2];
+                tree_partials_n<2, LGX_MAX_RANGES>(a.part, a.nr, (int64_t)a.m * a.n,
+                                                   (int64_t)b * a.n + t + NT * k, NT, o2, u2);
+                upd[k] = u2[0];
+                upd[k + 1] = u2[1];
+            }
         }
-        row[i] = v;
     }
-    int n2 = 256;
+    float v[KV];
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+        float x = on[k] ? hr[t + NT * k] : 0.0f;
+        if (a.part && on[k]) {
+            x = x + upd[k];
+            hr[t + NT * k] = x;
+        }
+        if (on[k]) row[t + NT * k] = x;
+        v[k] = x * x;                              // zero past n
+    }
+    int n2 = NT;
     while (n2 < a.n) n2 <<= 1;
-    float v[LGX_NORM_MAX / 256];
+    // in-thread levels s = n2/2 ... NT: slot j += slot j + s
+    for (int sl = n2 >> 1; sl >= NT; sl >>= 1) {
+        const int ks = sl / NT;
 #pragma unroll
-    for (int k = 0; k < LGX_NORM_MAX / 256; ++k) {
-        const int i = t + 256 * k;
-        v[k] = (i < a.n) ? row[i] * row[i] : 0.0f;
-    }
-    // levels s = n2/2 ... 256: slot j += slot j + s, both owned by this thread
-    for (int s = n2 >> 1; s >= 256; s >>= 1) {
-        const int ks = s / 256;
-#pragma unroll
-        for (int k = 0; k < LGX_NORM_MAX / 256; ++k)
+        for (int k = 0; k < KV; ++k)
             if (k < ks) v[k] = v[k] + v[k + ks];
     }
     red[t] = v[0];
     __syncthreads();
-    if (t < 128) red[t] = red[t] + red[t + 128];
-    __syncthreads();
+#pragma unroll
+    for (int sl = NT / 2; sl >= 64; sl >>= 1) {
+        if (t < sl) red[t] = red[t] + red[t + sl];
+        __syncthreads();
+    }
     float S = 0.0f;
     if (t < 64) {
-        S = red[t] + red[t + 64];
+        S = red[t];
 #pragma unroll
-        for (int s = 32; s >= 1; s >>= 1) S = S + __shfl_down(S, s, 64);
+        for (int sl = 32; sl >= 1; sl >>= 1) S = S + __shfl_down(S, sl, 64);
     }
     __syncthreads();
     if (t == 0) red[0] = S;
     __syncthreads();
     const float ms = red[0] / (float)a.n;
     const float r = 1.0f / sqrtf(ms + a.eps);
-    for (int i = t; i < a.n; i += 256) {
-        const float y = (row[i] * r) * a.w[i];
-        row[i] = y;
-        if (a.xn) a.xn[(int64_t)b * a.n + i] = y;
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+        if (on[k]) {
+            const int i = t + NT * k;
+            const float y = (row[i] * r) * a.w[i];
+            row[i] = y;
+            if (a.xn) a.xn[(int64_t)b * a.n + i] = y;
+        }
     }
     if (a.xq) {
         __syncthreads();
-        quantize_row_from_lds(row, a.n, a.xq + (int64_t)b * a.n, a.xd + (int64_t)b * (a.n / 32));
+        quantize_row_from_lds<NT>(row, a.n, a.xq + (int64_t)b * a.n, a.xd + (int64_t)b * (a.n / 32));
     }
 }
 
-// QKV combine + bias + RoPE + paged KV append.  One workgroup per sequence.
+// QKV combine + bias + RoPE + paged KV append.  One workgroup of 1024
+// threads per sequence.
 #define LGX_QKV_MAX 8192
-extern "C" __global__ __launch_bounds__(256) void lgx_k_qkv_rope_append(const lgx_qkv_args a) {
+extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_qkv_rope_append(const lgx_qkv_args a) {
+    constexpr int NT = LGX_GLUE_NT, KV = LGX_QKV_MAX / NT;
     __shared__ float row[LGX_QKV_MAX];
     const int b = blockIdx.x, t = threadIdx.x;
     const int d = a.d, half = d / 2;
     const int nq = (a.hq + 2 * a.hkv) * d;
-    for (int i = t; i < nq; i += 256) {
-        const float v = tree_partials(a.part, a.nr, (int64_t)a.m * nq, (int64_t)b * nq + i);
-        row[i] = a.bias ? v + a.bias[i] : v;
+    bool on[KV];
+    float v[KV];
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+        on[k] = t + NT * k < nq;
+        v[k] = 0.0f;
+    }
+    // qkv partials: K = hidden <= 8192, so at most 8 ranges
+#pragma unroll
+    for (int k = 0; k < KV; k += 4) {
+        if (on[k]) {
+            const bool o4[4] = {on[k], on[k + 1], on[k + 2], on[k + 3]};
+            float u4[4];
+            tree_partials_n<4, 8>(a.part, a.nr, (int64_t)a.m * nq, (int64_t)b * nq + t + NT * k, NT,
+                                  o4, u4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[k + e] = u4[e];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+        if (on[k]) {
+            const int i = t + NT * k;
+            row[i] = a.bias ? v[k] + a.bias[i] : v[k];
+        }
     }
     __syncthreads();
     const int pos = min(max(a.seq_len[b], 0), a.max_seq - 1);
@@ -977,11 +1110,11 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_qkv_rope_append(const lg
     const int page = min(max(a.page_table[(int64_t)b * a.maxp + pos / LGX_PAGE], 0), a.num_pages - 1);
     const int slot = pos % LGX_PAGE;
     // rotate q heads and k heads: pair (i, i + d/2) of head hh
-    for (int e = t; e < (a.hq + a.hkv) * half; e += 256) {
+    for (int e = t; e < (a.hq + a.hkv) * half; e += NT) {
         const int hh = e / half, i = e - hh * half;
         const float x0 = row[hh * d + i], x1 = row[hh * d + i + half];
-        const float c = cr[i], s = sr[i];
-        const float t0 = x0 * c, t1 = x1 * s, t2 = x1 * c, t3 = x0 * s;
+        const float c = cr[i], sn = sr[i];
+        const float t0 = x0 * c, t1 = x1 * sn, t2 = x1 * c, t3 = x0 * sn;
         const float y0 = t0 - t1, y1 = t2 + t3;
         if (hh < a.hq) {
             float* qo = a.q_out + ((int64_t)b * a.hq + hh) * d;
@@ -994,66 +1127,60 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_qkv_rope_append(const lg
             kd[i + half] = f2h(y1);
         }
     }
-    for (int e = t; e < a.hkv * d; e += 256) {
+    for (int e = t; e < a.hkv * d; e += NT) {
         const int g = e / d, i = e - g * d;
         uint16_t* vd = a.vpages + (((int64_t)page * a.hkv + g) * LGX_PAGE + slot) * d;
         vd[i] = f2h(row[(a.hq + a.hkv) * d + e]);
     }
 }
 
-// Attention chunk merge for one sequence (all heads) + Q8_0 of the row.
+// Attention chunk merge for one (sequence, head) + Q8_0 of its D values (D/32
+// whole blocks of the attention row, so heads quantise independently).
 template <int D>
 __device__ __forceinline__ void attn_combine_quant_body(const lgx_attn_args& a) {
-    __shared__ float row[64 * 128];
-    const int b = blockIdx.x, t = threadIdx.x;
-    const int L = min(a.seq_len[b] + a.len_add, a.maxlen);
-    const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
-    for (int e = t; e < a.hq * D; e += 256) {
-        const int h = e / D, i = e - h * D;
-        const float* pp = a.part + ((int64_t)b * a.hq + h) * a.nchunk * (D + 2);
-        float M = -__builtin_inff();
-        for (int c = 0; c < nc; ++c) M = fmaxf(M, pp[c * (D + 2) + D]);
-        float Ls = 0.0f, O = 0.0f;
-        for (int c = 0; c < nc; ++c) {
-            const float w = lgx_expf(pp[c * (D + 2) + D] - M);
-            Ls = fmaf(w, pp[c * (D + 2) + D + 1], Ls);
-            O = fmaf(w, pp[c * (D + 2) + i], O);
-        }
-        const float o = nc > 0 ? O / Ls : 0.0f;
-        row[e] = o;
-        if (a.out) a.out[(int64_t)b * a.hq * D + e] = o;
-    }
+    __shared__ float row[D];
+    const int bh = blockIdx.x, t = threadIdx.x;
+    const float o = attn_merge<D>(a, bh);
+    row[t] = o;
+    if (a.out) a.out[(int64_t)bh * D + t] = o;
     __syncthreads();
-    quantize_row_from_lds(row, a.hq * D, a.xq + (int64_t)b * a.hq * D,
-                          a.xd + (int64_t)b * (a.hq * D / 32));
+    if (t < D / 4) {                              // 8 lanes per 32-block, all active
+        const float f[4] = {row[4 * t], row[4 * t + 1], row[4 * t + 2], row[4 * t + 3]};
+        uint16_t dh;
+        const uint32_t qw = quantize4(f, dh);
+        *(uint32_t*)(a.xq + (int64_t)bh * D + 4 * t) = qw;
+        if ((t & 7) == 0) a.xd[(int64_t)bh * (D / 32) + (t >> 3)] = dh;
+    }
 }
-extern "C" __global__ __launch_bounds__(256) void lgx_k_attn_combine_quant_d64(const lgx_attn_args a) {
+extern "C" __global__ __launch_bounds__(64) void lgx_k_attn_combine_quant_d64(const lgx_attn_args a) {
     attn_combine_quant_body<64>(a);
 }
-extern "C" __global__ __launch_bounds__(256) void lgx_k_attn_combine_quant_d128(const lgx_attn_args a) {
+extern "C" __global__ __launch_bounds__(128) void lgx_k_attn_combine_quant_d128(const lgx_attn_args a) {
     attn_combine_quant_body<128>(a);
 }
 
 // SwiGLU from gate|up partials + Q8_0.  grid = (rows, ceil(blocks / 32)),
-// 256 threads = 32 blocks of 32 values.
+// 256 threads = 32 blocks of 32 values; all partial loads of a thread are
+// issued together.
 extern "C" __global__ __launch_bounds__(256) void lgx_k_swiglu_quant(const lgx_swiglu_args a) {
     const int b = blockIdx.x;
     const int bl = blockIdx.y * 32 + (threadIdx.x >> 3), j = threadIdx.x & 7;
     const int nbl = a.inter / 32;
     const bool on = bl < nbl;
     const int64_t stride = (int64_t)a.m * 2 * a.inter;
+    const int64_t base = (int64_t)b * 2 * a.inter + bl * 32 + 4 * j;
+    float gu[8];   // gate 0..3 at base + e, up 4..7 at base + inter + e
+    float p[8][8]; // gate|up partials: K = hidden <= 8192, so at most 8 ranges
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            p[e][r] = (r < a.nr && on) ? a.part[r * stride + base + (e & 3) + (e >> 2) * a.inter] : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gu[e] = tree_sum_r<8>(p[e], a.nr);
     float f[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        f[e] = 0.0f;
-        if (on) {
-            const int i = bl * 32 + 4 * j + e;
-            const int64_t base = (int64_t)b * 2 * a.inter;
-            const float g = tree_partials(a.part, a.nr, stride, base + i);
-            const float u = tree_partials(a.part, a.nr, stride, base + a.inter + i);
-            f[e] = lgx_silu(g) * u;
-        }
-    }
+    for (int e = 0; e < 4; ++e) f[e] = on ? lgx_silu(gu[e]) * gu[4 + e] : 0.0f;
     if (on && a.y) {
         float* yo = a.y + (int64_t)b * a.inter + bl * 32 + 4 * j;
 #pragma unroll
@@ -1069,12 +1196,14 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_swiglu_quant(const lgx_s
 
 // Tied binary16 lm_head (h <= 1024: a single canonical range, so the logit
 // is the sequential fmaf chain over the columns).  A workgroup owns 256
-// vocabulary rows (one per thread); 64-column slabs of its rows are staged in
-// LDS with coalesced loads and every thread runs the chain of its row for
-// all m activation rows (activation values are workgroup-uniform).  m <= 64.
+// vocabulary rows (one per thread); per 64-column slab, the binary16 rows and
+// the activation rows (m <= 64) are staged in LDS with coalesced loads, and
+// every thread runs the chain of its vocabulary row for all m rows
+// (activation reads are LDS broadcasts).
 #define LGX_LM_MAXM 64
 extern "C" __global__ __launch_bounds__(256) void lgx_k_lm_head_f16(const lgx_lmhead_args a) {
     __shared__ uint32_t slab[256][33];             // 64 binary16 per row, padded
+    __shared__ float4 xs[LGX_LM_MAXM][16];         // 64 columns of each activation row
     const int t = threadIdx.x;
     const int v0 = blockIdx.x * 256;
     const int v = v0 + t;
@@ -1083,21 +1212,29 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_lm_head_f16(const lgx_lm
     for (int r = 0; r < LGX_LM_MAXM; ++r) acc[r] = 0.0f;
     for (int k0 = 0; k0 < a.h; k0 += 64) {
         __syncthreads();
-        for (int s = t; s < 256 * 32; s += 256) {
-            const int rr = s >> 5, cc = s & 31;
+        for (int s2 = t; s2 < 256 * 32; s2 += 256) {
+            const int rr = s2 >> 5, cc = s2 & 31;
             const int vv = min(v0 + rr, a.vocab - 1);
             slab[rr][cc] = *(const uint32_t*)(a.emb + (int64_t)vv * a.h + k0 + 2 * cc);
         }
+        for (int s2 = t; s2 < a.m * 16; s2 += 256) {
+            const int rr = s2 >> 4, q = s2 & 15;
+            xs[rr][q] = *(const float4*)(a.x + (int64_t)rr * a.h + k0 + 4 * q);
+        }
         __syncthreads();
-        for (int cc = 0; cc < 32; ++cc) {
-            const uint32_t w2 = slab[t][cc];
-            const float e0 = h2f(w2 & 0xffffu), e1 = h2f(w2 >> 16);
-            const int k = k0 + 2 * cc;
+#pragma unroll 2
+        for (int q = 0; q < 16; ++q) {
+            const uint32_t w01 = slab[t][2 * q], w23 = slab[t][2 * q + 1];
+            const float e0 = h2f(w01 & 0xffffu), e1 = h2f(w01 >> 16);
+            const float e2 = h2f(w23 & 0xffffu), e3 = h2f(w23 >> 16);
 #pragma unroll
             for (int r = 0; r < LGX_LM_MAXM; ++r) {
                 if (r < a.m) {
-                    acc[r] = fmaf(a.x[(int64_t)r * a.h + k], e0, acc[r]);
-                    acc[r] = fmaf(a.x[(int64_t)r * a.h + k + 1], e1, acc[r]);
+                    const float4 xv = xs[r][q];
+                    acc[r] = fmaf(xv.x, e0, acc[r]);
+                    acc[r] = fmaf(xv.y, e1, acc[r]);
+                    acc[r] = fmaf(xv.z, e2, acc[r]);
+                    acc[r] = fmaf(xv.w, e3, acc[r]);
                 }
             }
         }
@@ -1108,42 +1245,74 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_lm_head_f16(const lgx_lm
         if (r < a.m) a.logits[(int64_t)r * a.vocab + v] = acc[r];
 }
 
-// Greedy token + state advance.  One workgroup per row: per-thread first
-// maximum over a strided scan (NaN skipped), then a (value, index) reduction
-// preferring the larger value and, on ties, the lower index.
-extern "C" __global__ __launch_bounds__(256) void lgx_k_argmax_advance(const lgx_argmax_args a) {
-    __shared__ float bv[256];
-    __shared__ int bi[256];
-    const int b = blockIdx.x, t = threadIdx.x;
+// Greedy token, in two launches.  Partial: workgroup (slice, row) takes the
+// first maximum of its LGX_ARGMAX_SLICE logits (tree of the range partials,
+// NaN skipped) -> candidate (value, index).  Final: per row, the candidate
+// with the larger value, on ties the lower index (the first maximum of the
+// row; -0 == +0; no candidate -> 0); then tokens[b] = it, seq_len[b] += advance.
+__device__ __forceinline__ void better(float& bv, int& bi, float ov, int oi) {
+    if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
+        bv = ov;
+        bi = oi;
+    }
+}
+
+__device__ __forceinline__ void wave_best(float& bv, int& bi) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = shfl_xor_f(bv, o);
+        const int oi = __shfl_xor(bi, o, 64);
+        better(bv, bi, ov, oi);
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void lgx_k_argmax_partial(const lgx_argmax_args a) {
+    __shared__ float wv[4];
+    __shared__ int wi[4];
+    const int sl = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
     const int64_t stride = (int64_t)a.m * a.vocab;
+    const int v0 = sl * LGX_ARGMAX_SLICE + t;
     float best = -__builtin_inff();
     int idx = 0x7fffffff;
-    for (int v = t; v < a.vocab; v += 256) {
-        const float x = a.nr == 1 ? a.part[(int64_t)b * a.vocab + v]
-                                  : tree_partials(a.part, a.nr, stride, (int64_t)b * a.vocab + v);
-        if (x == x && (idx == 0x7fffffff || x > best)) {
-            best = x;
-            idx = v;
-        }
-    }
-    bv[t] = best;
-    bi[t] = idx;
-    __syncthreads();
-    for (int s = 128; s >= 1; s >>= 1) {
-        if (t < s) {
-            const float ov = bv[t + s];
-            const int oi = bi[t + s];
-            if (oi != 0x7fffffff &&
-                (bi[t] == 0x7fffffff || ov > bv[t] || (ov == bv[t] && oi < bi[t]))) {
-                bv[t] = ov;
-                bi[t] = oi;
+    for (int k0 = 0; k0 < LGX_ARGMAX_SLICE / 256; k0 += 4) {
+        bool on[4];
+        float x[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) on[e] = v0 + 256 * (k0 + e) < a.vocab;
+        // lm_head partials: K = hidden <= 8192, so at most 8 ranges
+        tree_partials_n<4, 8>(a.part, a.nr, stride, (int64_t)b * a.vocab + v0 + 256 * k0, 256, on, x);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (on[e] && x[e] == x[e] && (idx == 0x7fffffff || x[e] > best)) {
+                best = x[e];
+                idx = v0 + 256 * (k0 + e);
             }
         }
-        __syncthreads();
     }
+    wave_best(best, idx);
+    if ((t & 63) == 0) {
+        wv[t >> 6] = best;
+        wi[t >> 6] = idx;
+    }
+    __syncthreads();
     if (t == 0) {
-        const int nxt = bi[0] == 0x7fffffff ? 0 : bi[0];
-        a.tokens[b] = nxt;
+        float bv = wv[0];
+        int bi = wi[0];
+        for (int w = 1; w < 4; ++w) better(bv, bi, wv[w], wi[w]);
+        a.cand_v[(int64_t)b * a.nslices + sl] = bv;
+        a.cand_i[(int64_t)b * a.nslices + sl] = bi;
+    }
+}
+
+extern "C" __global__ __launch_bounds__(64) void lgx_k_argmax_final(const lgx_argmax_args a) {
+    const int b = blockIdx.x, l = threadIdx.x;
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+    for (int s2 = l; s2 < a.nslices; s2 += 64)
+        better(bv, bi, a.cand_v[(int64_t)b * a.nslices + s2], a.cand_i[(int64_t)b * a.nslices + s2]);
+    wave_best(bv, bi);
+    if (l == 0) {
+        a.tokens[b] = bi == 0x7fffffff ? 0 : bi;
         if (a.seq_len) a.seq_len[b] += a.advance;
     }
 }

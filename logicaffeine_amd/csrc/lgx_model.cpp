@@ -60,7 +60,7 @@ struct lgx_model {
     float* part = nullptr;
     float* attn_part = nullptr;
     float* logits = nullptr;
-    int32_t* scratch_tok = nullptr;
+    float* cand = nullptr;     // argmax candidates [max_batch][slices] (value, index)
     int32_t last_nr = 1;       // partial count of the last lm_head
     int32_t last_B = 0;        // batch of the last lm_head
     std::vector<void*> allocs;
@@ -156,7 +156,7 @@ lgx_status norm(lgx_model* md, int m, int n, int nr_part, bool with_part, float*
     a.m = m;
     a.n = n;
     a.eps = md->c.rms_eps;
-    return launch(md->ctx, K_ADD_RMSNORM_QUANT, dim3(m), dim3(256), a, stream);
+    return launch(md->ctx, K_ADD_RMSNORM_QUANT, dim3(m), dim3(LGX_GLUE_NT), a, stream);
 }
 
 // One token per sequence 0..B-1 through every layer; leaves the down
@@ -191,7 +191,7 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
         qa.maxp = md->maxp;
         qa.num_pages = md->num_pages;
         qa.max_seq = cf.max_seq;
-        if ((st = launch(c, K_QKV_ROPE_APPEND, dim3(B), dim3(256), qa, stream)) != LGX_OK) return st;
+        if ((st = launch(c, K_QKV_ROPE_APPEND, dim3(B), dim3(LGX_GLUE_NT), qa, stream)) != LGX_OK) return st;
         lgx_attn_args aa{};
         aa.q = md->q;
         aa.kpages = md->kc[l];
@@ -214,8 +214,8 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
         if ((st = launch(c, (Kern)attn_kernel(d, hq / hkv), dim3(md->nchunk, B * hkv), dim3(256), aa,
                          stream)) != LGX_OK)
             return st;
-        if ((st = launch(c, d == 64 ? K_ATTN_COMBINE_QUANT_D64 : K_ATTN_COMBINE_QUANT_D128, dim3(B),
-                         dim3(256), aa, stream)) != LGX_OK)
+        if ((st = launch(c, d == 64 ? K_ATTN_COMBINE_QUANT_D64 : K_ATTN_COMBINE_QUANT_D128,
+                         dim3(B * hq), dim3(d), aa, stream)) != LGX_OK)
             return st;
         if ((st = product(md, md->o[l], B, stream)) != LGX_OK) return st;
         if ((st = norm(md, B, H, nranges_of(hq * d), true, nullptr, true, stream)) != LGX_OK)
@@ -239,7 +239,8 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
     const bool tied = cf.tied_embedding != 0;
     if ((st = norm(md, B, H, nranges_of(cf.intermediate), true, md->xn, !tied, stream)) != LGX_OK)
         return st;
-    lgx_argmax_args am{};
+    const float* lg;
+    int nr;
     if (tied) {
         for (int r0 = 0; r0 < B; r0 += 64) {
             lgx_lmhead_args la{md->xn + (int64_t)r0 * H, md->emb, md->logits + (int64_t)r0 * cf.vocab,
@@ -248,21 +249,16 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
                 LGX_OK)
                 return st;
         }
-        am.part = md->logits;
-        am.nr = 1;
+        lg = md->logits;
+        nr = 1;
     } else {
         if ((st = product(md, md->lm, B, stream)) != LGX_OK) return st;
-        am.part = md->part;
-        am.nr = nranges_of(H);
+        lg = md->part;
+        nr = nranges_of(H);
     }
-    md->last_nr = am.nr;
+    md->last_nr = nr;
     md->last_B = B;
-    am.tokens = next;
-    am.seq_len = md->seq_len;
-    am.m = B;
-    am.vocab = cf.vocab;
-    am.advance = 1;
-    return launch(c, K_ARGMAX_ADVANCE, dim3(B), dim3(256), am, stream);
+    return launch_argmax(c, lg, nr, B, cf.vocab, next, md->seq_len, 1, md->cand, stream);
 }
 
 }  // namespace
@@ -380,7 +376,7 @@ lgx_status lgx_model_create(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t see
             (st = dev_alloc(m, &m->q, (size_t)B * hq * d)) || (st = dev_alloc(m, &m->part, (size_t)part)) ||
             (st = dev_alloc(m, &m->attn_part, (size_t)B * hq * m->nchunk * (d + 2))) ||
             (st = dev_alloc(m, &m->logits, cf.tied_embedding ? (size_t)B * cf.vocab : 1)) ||
-            (st = dev_alloc(m, &m->scratch_tok, (size_t)B)))
+            (st = dev_alloc(m, &m->cand, (size_t)B * argmax_slices(cf.vocab) * 2)))
             return done(st);
         // staging no longer needed
         LGX_HIP(hipDeviceSynchronize());
