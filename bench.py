@@ -3,24 +3,30 @@
 Workload: the Qwen2.5-1.5B MLP matmuls, gate and up
 [8960 x 1536] and down [1536 x 8960], all Q8_0, with binary32 activations
 ~N(0,1).  One step = for each of the three matrices: quantise the activation
-rows to Q8_0 and run the Q8 x Q8 product (M = 1: the dot4 GEMV with the
-quantisation fused into its prologue; M > 1: quantise kernel + int8-MFMA
-GEMM), plus the range-combine kernel where K spans more than one 32-block
-range.  Weights rotate over enough distinct copies (>= 2 x the
-256 MB Infinity Cache) that every step streams them from HBM.
+rows to Q8_0 and run the Q8 x Q8 product.  At M = 1 the three products are
+one launch of the grouped GEMV (lgx_q8q8_gemv_quantize_group: the Q8_0
+quantisation fused into each workgroup's prologue, the canonical range tree
+applied in-workgroup); at M > 1 a quantise kernel + the int8-MFMA GEMM per
+matrix.  Weights rotate over enough distinct copies (>= 2 x the 256 MB
+Infinity Cache) that every step streams them from HBM.
 
 Headline `value`: algorithmic GB/s of the M = 1 step (weights + scales +
 activations + outputs, each counted once).  `roofline` is the dominant kernel
-(lgx_k_q8_gemv_mfma_qx, the fused-quantise GEMV writing range partials),
-timed per launch by HIP events attached to its own dispatch
-(lgx_ctx_set_kernel_timing) on its stream, in a separate pass over the same
-steps.  Launches are queued behind a device-side sleep before the timed
-region opens, so the step time is the device's, not the Python loop's.  The M sweep
-(1, 8, 32, 64) is reported alongside.  `cpu_baseline` times the CPU oracle
-(a port: the reference has no CPU implementation of this path) on a bounded
-sample of the same step.
+(lgx_k_q8_gemv_grp16 for this group: the grouped launch itself), timed per launch by HIP
+events attached to its own dispatch (lgx_ctx_set_kernel_timing) on its
+stream, in a separate pass over the same steps.  Launches are queued behind a
+device-side sleep before the timed region opens, so the step time is the
+device's, not the Python loop's.  The M sweep (1, 8, 32, 64) is reported
+alongside.  `cpu_baseline` times the CPU oracle (a port: the reference has no
+CPU implementation of this path) on a bounded sample of the same step.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 5]
+The decode part (BASELINE.json configs 3 and 4) builds the seeded
+random-init Qwen2.5-0.5B- and 7B-shaped Q8_0 models on the device, prefills a
+random prompt for every sequence, and times the 64 greedy decode steps
+(`qwen_decode`: tokens/s, and the step's algorithmic bytes -- weights,
+lm_head, K/V cache read and append -- against the HBM peak).
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--decode config3,config4]
 """
 from __future__ import annotations
 
@@ -34,7 +40,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-DOMINANT = "lgx_k_q8_gemv_mfma_qx"
+DOMINANT = ("lgx_k_q8_gemv_grp4", "lgx_k_q8_gemv_grp8", "lgx_k_q8_gemv_grp16")
+DOMINANT_USED = DOMINANT[2]
 MALL_BYTES = 256 << 20
 SHAPES = (("gate", 8960, 1536), ("up", 8960, 1536), ("down", 1536, 8960))
 
@@ -49,11 +56,10 @@ def step_bytes(m):
     return sum(q8_weight_bytes(n, k) + 4 * m * (k + n) for _, n, k in SHAPES)
 
 
-def gemv_launch_bytes(n, k):
-    """Algorithmic bytes of one lgx_k_q8_gemv_mfma_qx launch: W + fp32 x +
-    one fp32 range partial per row and range (= y with a single range)."""
-    nr = -(-(k // 32) // 32)
-    return q8_weight_bytes(n, k) + 4 * k + 4 * n * nr
+def gemv_launch_bytes():
+    """Algorithmic bytes of the grouped lgx_k_q8_gemv_grp16 launch of one M = 1
+    step: the three Q8_0 matrices, their binary32 activations and outputs."""
+    return step_bytes(1)
 
 
 def build_sets(ctx, torch, nsets, seed=1):
@@ -77,15 +83,16 @@ def build_sets(ctx, torch, nsets, seed=1):
 
 def run_step(ctx, sets, i, acts, m):
     W = sets[i % len(sets)]
+    if m == 1:
+        # the three products in one launch of the grouped GEMV
+        ctx.q8q8_gemv_quantize_group([W[name] for name, _, _ in SHAPES],
+                                     [acts[name][0][0] for name, _, _ in SHAPES],
+                                     [acts[name][3][0] for name, _, _ in SHAPES])
+        return
     for name, n, k in SHAPES:
         x, xq, xd, y, part = acts[name]
-        if m == 1:
-            ctx.q8q8_gemv_quantize_partials(W[name], x[0], part=part)
-            if part.dim() == 2:
-                ctx.range_combine(part, y=y[0])
-        else:
-            ctx.quantize_q8_0(x, xq, xd)
-            ctx.q8_gemm(W[name], xq, xd, y=y)
+        ctx.quantize_q8_0(x, xq, xd)
+        ctx.q8_gemm(W[name], xq, xd, y=y)
 
 
 def make_acts(ctx, torch, m):
@@ -147,8 +154,11 @@ def time_m(ctx, torch, sets, m, steps, warmup, per_launch=False):
     gemv_ms = None
     if per_launch:
         ctx.kernel_timing(False)
-        n, tot = ctx.kernel_stats(DOMINANT)
+        stats = [ctx.kernel_stats(name) for name in DOMINANT]
+        n, tot = sum(st[0] for st in stats), sum(st[1] for st in stats)
         gemv_ms = tot / max(n, 1)
+        global DOMINANT_USED
+        DOMINANT_USED = DOMINANT[max(range(len(stats)), key=lambda i: stats[i][0])]
     return ms, gemv_ms
 
 
@@ -187,6 +197,130 @@ def cpu_baseline(seconds=12.0):
     }
 
 
+SUSTAINED_SHAPE = (152064, 3584)   # Qwen2.5-7B lm_head as a Q8_0 matrix (579 MB)
+
+
+def sustained_gemv(ctx, torch, iters=60):
+    """Fused-quantise M = 1 GEMV streaming one large Q8_0 matrix (two copies
+    alternate, > 2 x the Infinity Cache), per-launch dispatch-event time."""
+    import numpy as np
+
+    import logicaffeine_amd as lgx
+
+    n, k = SUSTAINED_SHAPE
+    rng = np.random.default_rng(11)
+    qs = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    d = (np.abs(rng.normal(0.0, 0.02, size=(n, k // 32))) / 127.0).astype(np.float16)
+    W0 = ctx.q8_matrix(qs, d.view(np.uint16))
+    Ws = [W0, lgx.Q8Matrix(W0.qs.clone(), W0.d.clone(), n, k)]
+    x = torch.randn(k, device=ctx.dev)
+    y = torch.empty(n, device=ctx.dev)
+    for i in range(4):
+        ctx.q8q8_gemv_quantize(Ws[i % 2], x, y=y)
+    torch.cuda.synchronize()
+    ctx.kernel_timing(True)
+    for i in range(iters):
+        ctx.q8q8_gemv_quantize(Ws[i % 2], x, y=y)
+    torch.cuda.synchronize()
+    ctx.kernel_timing(False)
+    stats = [(name, ctx.kernel_stats(name)) for name in DOMINANT]
+    name, (cnt, tot) = max(stats, key=lambda s: s[1][0])
+    us = tot / max(cnt, 1) * 1e3
+    nbytes = q8_weight_bytes(n, k) + 4 * (k + n)
+    del Ws, W0
+    torch.cuda.empty_cache()
+    return {"shape": [n, k], "kernel": name, "us_per_launch": round(us, 2),
+            "GB_s": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+DECODE_CONFIGS = {
+    # BASELINE.json config 3 and 4: (shape, batch, prompt tokens, greedy steps)
+    "config3": ("0.5b", 32, 2048, 64),
+    "config4": ("7b", 64, 4096, 64),
+}
+
+
+def decode_bench(ctx, torch, key, seed=3):
+    """Prefill a random prompt per sequence, then time the greedy decode
+    steps (each: the whole model for B sequences + argmax + KV append)."""
+    import logicaffeine_amd as lgx
+
+    shape, B, P, steps = DECODE_CONFIGS[key]
+    cfg = lgx.qwen_shape(shape, B, P + steps)
+    t = time.perf_counter()
+    gm = lgx.Model(ctx, cfg, seed)
+    torch.cuda.synchronize()
+    create_s = time.perf_counter() - t
+    g = torch.Generator(device=ctx.dev)
+    g.manual_seed(seed)
+    prompt = torch.randint(0, cfg["vocab"], (B, P), generator=g, device=ctx.dev,
+                           dtype=torch.int32)
+    t = time.perf_counter()
+    tok = gm.prefill(prompt)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t
+    print(f"[bench] {key}: model {create_s:.1f} s, prefill {B}x{P} in {prefill_s:.1f} s",
+          file=sys.stderr, flush=True)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        gm.decode_step(tok)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    ctxlen = P + (steps + 1) / 2.0            # mean attended tokens over the steps
+    step_bytes_ = lgx.decode_step_bytes(cfg, B, ctxlen)
+    gbs = step_bytes_ / (ms * 1e-3) / 1e9
+    gm.close()
+    torch.cuda.empty_cache()
+    out = {
+        "model": f"random-init Qwen2.5-{shape.upper()}-shaped Q8_0 "
+                 f"({'tied binary16' if cfg['tied'] else 'Q8_0'} lm_head)",
+        "batch": B, "prompt": P, "steps": steps,
+        "tokens_per_s": round(B / (ms * 1e-3), 1),
+        "ms_per_step": round(ms, 4),
+        "prefill_s": round(prefill_s, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "bytes_per_step": int(step_bytes_),
+                     "roofline_tokens_per_s": round(B * HBM_PEAK_GBS * 1e9 / step_bytes_, 1)},
+    }
+    print(f"[bench] {key}: {out['tokens_per_s']} tok/s, {ms:.3f} ms/step, {gbs:.0f} GB/s",
+          file=sys.stderr, flush=True)
+    return out
+
+
+def cpu_decode_baseline(key, seconds=8.0):
+    """The CPU oracle model (a port; exact canonical arithmetic) on a bounded
+    sample: the same shape, one sequence, 8-token prompt, greedy steps until
+    `seconds` have passed."""
+    import numpy as np
+
+    import logicaffeine_amd as lgx
+    from oracle import oracle as orc
+
+    shape = DECODE_CONFIGS[key][0]
+    cfg = lgx.qwen_shape(shape, 1, 64)
+    om = orc.Model(cfg, 3)
+    tok = np.arange(8, dtype=np.int32) * 7 + 1
+    for p in range(8):
+        nxt = om.step(np.zeros(1, np.int32), tok[p:p + 1])
+    t0 = time.perf_counter()
+    n = 0
+    while n < 48:
+        nxt = om.step(np.zeros(1, np.int32), nxt)
+        n += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    el = time.perf_counter() - t0
+    om.close()
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(n / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{shape} shape, batch 1, 8-token prompt, {n} greedy steps in {el:.1f} s"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -194,6 +328,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--decode", default="config3,config4",
+                    help="decode configs to run (comma list; empty for none)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -225,7 +361,7 @@ def main():
               file=sys.stderr, flush=True)
 
     value = step_bytes(1) / (ms1_plain * 1e-3) / 1e9
-    per_launch = sum(gemv_launch_bytes(n, k) for _, n, k in SHAPES) / 3
+    per_launch = gemv_launch_bytes()
     achieved = per_launch / (gemv_ms * 1e-3) / 1e9
     out = {
         "metric": "Q8 GEMV HBM GB/s (% peak); batched Qwen decode tokens/sec on 1 MI355X",
@@ -242,7 +378,8 @@ def main():
         "data": "synthetic (int8 U[-127,127], d=|N(0,0.02)|/127 f16, x~N(0,1) f32)",
         "config": {
             "workload": "config1 Qwen2.5-1.5B MLP Q8_0 gate/up [8960x1536] + down [1536x8960], "
-                        "M=1 (fused quantise + Q8xQ8 GEMV per matrix, + range combine)",
+                        "M=1 (one grouped launch: fused quantise + whole-K Q8xQ8 GEMV of the "
+                        "three matrices)",
             "rotating_weight_sets": nsets,
             "working_set_MB": round(nsets * set_bytes / 1e6, 1),
             "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
@@ -250,7 +387,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": DOMINANT,
+            "kernel": DOMINANT_USED,
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -260,6 +397,19 @@ def main():
             "bytes_per_launch": int(per_launch),
         },
     }
+    del sets
+    torch.cuda.empty_cache()
+    sustained = sustained_gemv(ctx, torch)
+    print(f"[bench] sustained GEMV {SUSTAINED_SHAPE}: {sustained['us_per_launch']} us, "
+          f"{sustained['GB_s']} GB/s", file=sys.stderr, flush=True)
+    out["config"]["sustained_gemv_m1"] = sustained
+    decode = {}
+    for key in [k for k in args.decode.split(",") if k]:
+        decode[key] = decode_bench(ctx, torch, key)
+        if not args.no_cpu:
+            decode[key]["cpu_baseline"] = cpu_decode_baseline(key)
+    if decode:
+        out["qwen_decode"] = decode
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     ctx.close()

@@ -145,6 +145,10 @@ lgx_status lgx_q8q8_gemv(lgx_ctx* ctx, const lgx_q8_matrix* W, const int8_t* xq,
  * canonical Q8 x Q8 schedule.  xq_out / xd_out (nullable) receive Q8_0(x). */
 lgx_status lgx_q8q8_gemv_quantize(lgx_ctx* ctx, const lgx_q8_matrix* W, const float* x, float* y,
                                   int8_t* xq_out, uint16_t* xd_out, void* stream);
+/* Grouped y[i] = W[i] Q8_0(x[i]) for `count` (1..8) independent matrices in
+ * one launch (the lgx_q8q8_gemv_quantize schedule for each). */
+lgx_status lgx_q8q8_gemv_quantize_group(lgx_ctx* ctx, int32_t count, const lgx_q8_matrix* W,
+                                        const float* const* x, float* const* y, void* stream);
 /* Y[m][n] = Xq W^T for m Q8_0 activation rows (Xq[m][k], Xd[m][k/32]), int8
  * MFMA; canonical schedule, so row i equals lgx_q8q8_gemv of row i. */
 lgx_status lgx_q8_gemm(lgx_ctx* ctx, const lgx_q8_matrix* W, const int8_t* xq,

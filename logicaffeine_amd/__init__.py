@@ -55,6 +55,7 @@ SIGNATURES = {
     "lgx_q8q8_gemv": (C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     "lgx_q8_gemm": (C.c_int, [_P, _P, _P, _P, _I32, _P, _P]),
     "lgx_q8q8_gemv_quantize": (C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
+    "lgx_q8q8_gemv_quantize_group": (C.c_int, [_P, _I32, _P, _P, _P, _P]),
     "lgx_q8_range_count": (_I32, [_I32]),
     "lgx_q8q8_gemv_quantize_partials": (C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     "lgx_q8_gemm_partials": (C.c_int, [_P, _P, _P, _P, _I32, _P, _P]),
@@ -76,6 +77,35 @@ SIGNATURES = {
     "lgx_model_tensor": (C.c_int, [_P, _I32, _I32, C.POINTER(_P), C.POINTER(C.c_size_t)]),
     "lgx_qwen_logits": (C.c_int, [_P, _I32, _P, _P]),
 }
+
+# Model shapes of the decode benchmarks (random-init Qwen2.5-0.5B / -7B shaped
+# Q8_0 models): keys as lgx.Model's cfg.
+QWEN_SHAPES = {
+    "0.5b": dict(n_layers=24, hidden=896, inter=4864, n_heads=14, n_kv=2, head_dim=64,
+                 vocab=151936, tied=1),
+    "7b": dict(n_layers=28, hidden=3584, inter=18944, n_heads=28, n_kv=4, head_dim=128,
+               vocab=152064, tied=0),
+}
+
+
+def qwen_shape(name: str, max_batch: int, max_seq: int, emb_sigma: float = 0.002) -> dict:
+    """cfg dict for lgx.Model: shape `name` with RMSNorm eps 1e-6, RoPE theta 1e6."""
+    return dict(QWEN_SHAPES[name], max_batch=max_batch, max_seq=max_seq, eps=1e-6, theta=1e6,
+                emb_sigma=emb_sigma)
+
+
+def decode_step_bytes(cfg: dict, B: int, context: float) -> float:
+    """Algorithmic HBM bytes of one greedy decode step of B sequences whose
+    attention spans `context` cached tokens on average (the new token
+    included): Q8_0 weights (1.0625 B/weight), the lm_head (binary16 tied
+    embedding or Q8_0), the K/V cache read and the new K/V rows written."""
+    H, I, d = cfg["hidden"], cfg["inter"], cfg["head_dim"]
+    hq, hkv, L, V = cfg["n_heads"], cfg["n_kv"], cfg["n_layers"], cfg["vocab"]
+    per_layer = ((hq + 2 * hkv) * d * H + H * hq * d + 2 * I * H + H * I) * 1.0625
+    lm = V * H * (2.0 if cfg["tied"] else 1.0625)
+    kv_row = L * hkv * d * 2 * 2                    # K and V, binary16, all layers
+    return L * per_layer + lm + B * context * kv_row + B * kv_row
+
 
 # Tensor ids of lgx_model_tensor.
 MODEL_TENSORS = {"emb": 0, "lm_q": 1, "lm_d": 2, "qkv_q": 3, "qkv_d": 4, "o_q": 5, "o_d": 6,
@@ -276,6 +306,17 @@ class Context:
             xq_out.data_ptr() if xq_out is not None else None,
             xd_out.data_ptr() if xd_out is not None else None, self._s()))
         return y
+
+    def q8q8_gemv_quantize_group(self, Ws, xs, ys=None):
+        """ys[i] = Ws[i] Q8_0(xs[i]) for up to 8 matrices in one launch."""
+        t = self.torch
+        n = len(Ws)
+        ys = [t.empty(W.n, dtype=t.float32, device=self.dev) for W in Ws] if ys is None else ys
+        arr = (Q8MatrixC * n)(*[W._c for W in Ws])
+        xp = (C.c_void_p * n)(*[x.data_ptr() for x in xs])
+        yp = (C.c_void_p * n)(*[y.data_ptr() for y in ys])
+        _check(lib().lgx_q8q8_gemv_quantize_group(self.handle, n, arr, xp, yp, self._s()))
+        return ys
 
     def q8q8_gemv_quantize_partials(self, W: Q8Matrix, x, part=None):
         t = self.torch

@@ -9,6 +9,8 @@
 // every entry point returns a status, stores a thread-local message, and
 // catches every C++ exception at the boundary (ffi.rs:329-340 wraps every
 // export in catch_unwind the same way).
+#include <algorithm>
+
 #include "lgx_internal.h"
 
 using namespace lgxi;
@@ -57,6 +59,14 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
         c->arch = arch;
         const char* gv = getenv("LGX_GEMV");
         c->gemv_dot4 = gv && std::string(gv) == "dot4";
+        c->gemv_split = gv && std::string(gv) == "split";
+        c->gemv_whole = gv && std::string(gv) == "whole";
+        c->gemv_wgs = env_int("LGX_GEMV_WGS", 0);
+        int ncu = 0;
+        if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) ==
+                hipSuccess &&
+            ncu > 0)
+            c->ncu = ncu;
         c->wg_target = env_int("LGX_WG_TARGET", 512);
         if (c->wg_target < 1) c->wg_target = 1;
         for (int k = 0; k < K_COUNT; ++k) {
@@ -192,6 +202,10 @@ lgx_status lgx_q8_gemv_f32(lgx_ctx* c, const lgx_q8_matrix* W, const float* x, f
     });
 }
 
+static bool use_wg(const lgx_ctx* c, const lgx_q8_matrix* W) {
+    return !c->gemv_dot4 && !c->gemv_split && gemv_group_ok(c, W->k);
+}
+
 lgx_status lgx_q8q8_gemv(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq,
                          const uint16_t* xd, float* y, int32_t* dbg, void* stream) {
     return guarded(__func__, [&]() -> lgx_status {
@@ -199,7 +213,11 @@ lgx_status lgx_q8q8_gemv(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq,
         if (st != LGX_OK) return st;
         if ((st = check_q8(W)) != LGX_OK) return st;
         if (!xq || !xd || !y) return fail(LGX_NULL_POINTER, "NULL xq, xd or y");
-        // the block-dot debug output exists only in the v_dot4 kernel
+        if (use_wg(c, W)) {
+            lgx_gemv_mat m = gemv_mat(W, nullptr, xq, xd, y, 0);
+            m.dbg = dbg;
+            return run_gemv_group(c, &m, 1, stream);
+        }
         if (dbg || c->gemv_dot4)
             return run_q8(c, K_Q8Q8_GEMV, W, nullptr, xq, xd, 1, y, dbg, stream);
         return run_q8(c, K_GEMV_MFMA, W, nullptr, xq, xd, 1, y, nullptr, stream);
@@ -213,8 +231,39 @@ lgx_status lgx_q8q8_gemv_quantize(lgx_ctx* c, const lgx_q8_matrix* W, const floa
         if (st != LGX_OK) return st;
         if ((st = check_q8(W)) != LGX_OK) return st;
         if (!x || !y) return fail(LGX_NULL_POINTER, "NULL x or y");
+        if ((xq_out == nullptr) != (xd_out == nullptr))
+            return fail(LGX_NULL_POINTER, "xq_out and xd_out go together");
+        if (use_wg(c, W)) {
+            lgx_gemv_mat m = gemv_mat(W, x, nullptr, nullptr, y, 0);
+            m.xq_out = xq_out;
+            m.xd_out = xd_out;
+            return run_gemv_group(c, &m, 1, stream);
+        }
         return run_q8(c, K_GEMV_MFMA_QX, W, x, nullptr, nullptr, 1, y, nullptr, stream, xq_out,
                       xd_out);
+    });
+}
+
+lgx_status lgx_q8q8_gemv_quantize_group(lgx_ctx* c, int32_t count, const lgx_q8_matrix* W,
+                                        const float* const* x, float* const* y, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!W || !x || !y) return fail(LGX_NULL_POINTER, "NULL W, x or y array");
+        if (count < 1 || count > LGX_GROUP_MAX)
+            return fail(LGX_OUT_OF_BOUNDS, "count = %d (1..%d)", count, LGX_GROUP_MAX);
+        lgx_gemv_mat mats[LGX_GROUP_MAX];
+        for (int i = 0; i < count; ++i) {
+            if ((st = check_q8(&W[i])) != LGX_OK) return st;
+            if (!x[i] || !y[i]) return fail(LGX_NULL_POINTER, "NULL x[%d] or y[%d]", i, i);
+            if (!gemv_group_ok(c, W[i].k))
+                return fail(LGX_UNSUPPORTED, "W[%d].k = %d too long for a grouped GEMV", i, W[i].k);
+            mats[i] = gemv_mat(&W[i], x[i], nullptr, nullptr, y[i], 0);
+        }
+        // longest reductions first: their workgroups start earliest
+        std::stable_sort(mats, mats + count,
+                         [](const lgx_gemv_mat& a, const lgx_gemv_mat& b) { return a.k > b.k; });
+        return run_gemv_group(c, mats, count, stream);
     });
 }
 
@@ -228,6 +277,14 @@ lgx_status lgx_q8q8_gemv_quantize_partials(lgx_ctx* c, const lgx_q8_matrix* W, c
         if (st != LGX_OK) return st;
         if ((st = check_q8(W)) != LGX_OK) return st;
         if (!x || !part) return fail(LGX_NULL_POINTER, "NULL x or part");
+        if ((xq_out == nullptr) != (xd_out == nullptr))
+            return fail(LGX_NULL_POINTER, "xq_out and xd_out go together");
+        if (use_wg(c, W)) {
+            lgx_gemv_mat m = gemv_mat(W, x, nullptr, nullptr, part, 1);
+            m.xq_out = xq_out;
+            m.xd_out = xd_out;
+            return run_gemv_group(c, &m, 1, stream);
+        }
         return run_q8(c, K_GEMV_MFMA_QX, W, x, nullptr, nullptr, 1, part, nullptr, stream, xq_out,
                       xd_out, part);
     });
@@ -241,6 +298,10 @@ lgx_status lgx_q8_gemm_partials(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t
         if ((st = check_q8(W)) != LGX_OK) return st;
         if (!xq || !xd || !part) return fail(LGX_NULL_POINTER, "NULL xq, xd or part");
         if (m <= 0 || m > 65535 * 64) return fail(LGX_OUT_OF_BOUNDS, "m = %d out of range", m);
+        if (m == 1 && use_wg(c, W)) {
+            lgx_gemv_mat g = gemv_mat(W, nullptr, xq, xd, part, 1);
+            return run_gemv_group(c, &g, 1, stream);
+        }
         Kern k = m == 1 ? K_GEMV_MFMA : m <= 16 ? K_GEMM_MFMA16 : m <= 32 ? K_GEMM_MFMA32
                                                                           : K_GEMM_MFMA64;
         return run_q8(c, k, W, nullptr, xq, xd, m, part, nullptr, stream, nullptr, nullptr, part);
@@ -311,6 +372,10 @@ lgx_status lgx_q8_gemm(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq, con
         if ((st = check_q8(W)) != LGX_OK) return st;
         if (!xq || !xd || !y) return fail(LGX_NULL_POINTER, "NULL xq, xd or y");
         if (m <= 0 || m > 65535 * 64) return fail(LGX_OUT_OF_BOUNDS, "m = %d out of range", m);
+        if (m == 1 && use_wg(c, W)) {
+            lgx_gemv_mat g = gemv_mat(W, nullptr, xq, xd, y, 0);
+            return run_gemv_group(c, &g, 1, stream);
+        }
         Kern k = m <= 16 ? K_GEMM_MFMA16 : m <= 32 ? K_GEMM_MFMA32 : K_GEMM_MFMA64;
         return run_q8(c, k, W, nullptr, xq, xd, m, y, nullptr, stream);
     });

@@ -6,6 +6,7 @@
 
 #include <dlfcn.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -95,6 +96,12 @@ enum Kern {
     K_ARGMAX_PARTIAL,
     K_ARGMAX_FINAL,
     K_ADVANCE,
+    K_GEMV_WG4,
+    K_GEMV_WG8,
+    K_GEMV_WG16,
+    K_GEMV_GRP4,
+    K_GEMV_GRP8,
+    K_GEMV_GRP16,
     K_COUNT
 };
 inline const char* const kKernelNames[] = {
@@ -112,6 +119,8 @@ inline const char* const kKernelNames[] = {
     "lgx_k_embed", "lgx_k_add_rmsnorm_quant", "lgx_k_qkv_rope_append",
     "lgx_k_attn_combine_quant_d64", "lgx_k_attn_combine_quant_d128", "lgx_k_swiglu_quant",
     "lgx_k_lm_head_f16", "lgx_k_argmax_partial", "lgx_k_argmax_final", "lgx_k_advance",
+    "lgx_k_q8_gemv_wg4", "lgx_k_q8_gemv_wg8", "lgx_k_q8_gemv_wg16",
+    "lgx_k_q8_gemv_grp4", "lgx_k_q8_gemv_grp8", "lgx_k_q8_gemv_grp16",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -139,7 +148,11 @@ struct lgx_ctx {
     hipModule_t module = nullptr;
     hipFunction_t fn[lgxi::K_COUNT] = {};
     std::string arch;
-    bool gemv_dot4 = false;
+    bool gemv_dot4 = false;       // LGX_GEMV=dot4: per-(tile, range) dot4 GEMV
+    bool gemv_split = false;      // LGX_GEMV=split: per-(tile, range) MFMA GEMV
+    int gemv_wgs = 0;             // LGX_GEMV_WGS: M = 1 GEMV waves per workgroup (0: auto)
+    bool gemv_whole = false;      // LGX_GEMV=whole: block dots through LDS, chains after
+    int ncu = 256;                // compute units of the device
     int wg_target = 512;
     std::atomic<uint64_t> launches{0};
     void* ws = nullptr;       // range partials
@@ -330,5 +343,92 @@ inline lgx_status launch_argmax(lgx_ctx* c, const float* part, int nr, int m, in
     lgx_status st = launch(c, K_ARGMAX_PARTIAL, dim3(ns, m), dim3(256), a, stream);
     if (st != LGX_OK) return st;
     return launch(c, K_ARGMAX_FINAL, dim3(m), dim3(64), a, stream);
+}
+}  // namespace lgxi
+
+namespace lgxi {
+// Whole-K GEMV shape for reduction length k in a workgroup of W waves:
+// log2 of the waves per tile (about 8 of the 64-column pairs per wave) and
+// the LDS bytes (0 if they exceed 64 KiB).
+inline int gemv_wg_lwt(int k, int W) {
+    const int np = k / 64;
+    int lwt = 0;
+    while ((1 << lwt) < W && (1 << lwt) * 8 < np) ++lwt;
+    return lwt;
+}
+inline size_t gemv_wg_lds(int k, int W = 4) {
+    const size_t nb = k / 32, nr = (nb + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS;
+    const size_t tpw = (size_t)W >> gemv_wg_lwt(k, W);
+    const size_t bytes = (size_t)k + 4 * nb + tpw * (64 * nb + 64 * nr);
+    return bytes <= 65536 ? bytes : 0;
+}
+
+// Launch the M = 1 GEMV over `count` independent matrices: by default the
+// grouped kernel with a tile's ranges inside one workgroup; LGX_GEMV=whole
+// selects the whole-K kernel (block dots through LDS).
+inline lgx_status run_gemv_group(lgx_ctx* c, const lgx_gemv_mat* mats, int count, void* stream) {
+    if (count < 1 || count > LGX_GROUP_MAX)
+        return fail(LGX_INVALID_ARGUMENT, "group of %d matrices (1..%d)", count, LGX_GROUP_MAX);
+    lgx_gemv_group_args ga{};
+    ga.count = count;
+    int wgs = 0;
+    size_t lds = 0;
+    if (c->gemv_whole) {
+        int npmax = 0;
+        for (int i = 0; i < count; ++i) npmax = std::max(npmax, mats[i].k / 64);
+        int W = npmax > 64 ? 16 : 4;
+        if (c->gemv_wgs == 4 || c->gemv_wgs == 8 || c->gemv_wgs == 16) W = c->gemv_wgs;
+        for (int i = 0; i < count; ++i) {
+            ga.mat[i] = mats[i];
+            const int lwt = gemv_wg_lwt(mats[i].k, W);
+            ga.mat[i].pad = lwt;
+            ga.tile0[i] = wgs;
+            const int tpw = W >> lwt;
+            wgs += (mats[i].n / 16 + tpw - 1) / tpw;
+            const size_t l = gemv_wg_lds(mats[i].k, W);
+            if (l == 0)
+                return fail(LGX_UNSUPPORTED, "k = %d too long for the whole-K GEMV", mats[i].k);
+            lds = std::max(lds, l);
+        }
+        ga.tile0[count] = wgs;
+        const Kern k = W == 16 ? K_GEMV_WG16 : W == 8 ? K_GEMV_WG8 : K_GEMV_WG4;
+        return launch(c, k, dim3(wgs), dim3(64 * W), ga, stream, (unsigned)lds);
+    }
+    int nrmax = 1;
+    for (int i = 0; i < count; ++i)
+        nrmax = std::max(nrmax, (mats[i].k / 32 + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS);
+    int W = nrmax <= 4 ? 4 : nrmax <= 8 ? 8 : 16;
+    if (c->gemv_wgs == 4 || c->gemv_wgs == 8 || c->gemv_wgs == 16) W = c->gemv_wgs;
+    for (int i = 0; i < count; ++i) {
+        ga.mat[i] = mats[i];
+        const int nb = mats[i].k / 32, nr = (nb + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS;
+        const int tpw = W / std::min(nr, W);
+        ga.tile0[i] = wgs;
+        wgs += (mats[i].n / 16 + tpw - 1) / tpw;
+        lds = std::max(lds, (size_t)mats[i].k + 4 * (size_t)nb + 64 * (size_t)tpw * nr);
+    }
+    ga.tile0[count] = wgs;
+    const Kern k = W == 16 ? K_GEMV_GRP16 : W == 8 ? K_GEMV_GRP8 : K_GEMV_GRP4;
+    return launch(c, k, dim3(wgs), dim3(64 * W), ga, stream, (unsigned)lds);
+}
+
+// Whether the M = 1 products of reduction length k go through run_gemv_group.
+inline bool gemv_group_ok(const lgx_ctx* c, int k) {
+    return !c->gemv_whole || gemv_wg_lds(k) != 0;
+}
+
+inline lgx_gemv_mat gemv_mat(const lgx_q8_matrix* W, const float* xf, const int8_t* xq,
+                             const uint16_t* xd, float* y, int part_out) {
+    lgx_gemv_mat m{};
+    m.wt = W->qs;
+    m.wd = W->d;
+    m.xf = xf;
+    m.xq = xq;
+    m.xd = xd;
+    m.y = y;
+    m.n = W->n;
+    m.k = W->k;
+    m.part_out = part_out;
+    return m;
 }
 }  // namespace lgxi

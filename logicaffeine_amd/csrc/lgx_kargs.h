@@ -49,6 +49,29 @@ typedef struct {
                           // the whole-K GEMV)
 } lgx_gemv_args;
 
+// Whole-K GEMV (M = 1): one workgroup per 16-row tile of one matrix of a
+// group of independent products in a single launch.
+#define LGX_GROUP_MAX 8
+typedef struct {
+    const int8_t* wt;      // T16 quants
+    const uint16_t* wd;    // S16 scales
+    const float* xf;       // binary32 activation, quantised in the prologue (or NULL)
+    const int8_t* xq;      // Q8_0 activation when xf is NULL
+    const uint16_t* xd;
+    float* y;              // [n]; the range partials [nranges][n] when part_out
+    int8_t* xq_out;        // nullable: Q8_0(xf), written by the matrix's first workgroup
+    uint16_t* xd_out;
+    int32_t* dbg;          // nullable: int32 block dots [n][k/32]
+    int32_t n, k, part_out;
+    int32_t pad;           // set by the launcher: log2 of the waves per tile
+} lgx_gemv_mat;
+
+typedef struct {
+    lgx_gemv_mat mat[LGX_GROUP_MAX];
+    int32_t tile0[LGX_GROUP_MAX + 1];  // first workgroup of each matrix; tile0[count] = grid
+    int32_t count, pad;
+} lgx_gemv_group_args;
+
 // Canonical tree over range partials: y[i] = tree(part[0][i], ..., part[g-1][i]).
 typedef struct {
     const float* part;    // [nranges][count]

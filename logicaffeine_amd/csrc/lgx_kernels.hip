@@ -42,6 +42,27 @@ __device__ __forceinline__ uint16_t f2h(float f) {
 __device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, 64); }
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
+// Q8_0 of one 32-block held by 8 consecutive lanes (4 values each): the
+// lgx_k_quantize_q8_0 rule.  Returns the packed quants of this lane's four
+// values and the binary16 scale.
+__device__ __forceinline__ uint32_t quantize4(const float (&f)[4], uint16_t& dh) {
+    float am = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
+    am = fmaxf(am, shfl_xor_f(am, 1));
+    am = fmaxf(am, shfl_xor_f(am, 2));
+    am = fmaxf(am, shfl_xor_f(am, 4));
+    const float d = am / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t qw = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float q = roundf(f[e] * id);
+        q = fminf(fmaxf(q, -127.0f), 127.0f);
+        qw |= ((uint32_t)(int32_t)q & 0xffu) << (8 * e);
+    }
+    dh = f2h(d);
+    return qw;
+}
+
 // ---------------------------------------------------------------------------
 // T16 repack / unpack.  One thread per 16-byte lane slot of a 1 KiB unit:
 // unit u = tile * (k/64) + pair, lane l = r + 16c; the slot holds bytes
@@ -321,6 +342,180 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8q8_gemv(const lgx_gemv
 }
 
 // ---------------------------------------------------------------------------
+// Whole-K Q8 x Q8 GEMV (M = 1).  A workgroup of W waves serves W / Wt
+// 16-row tiles of one matrix of a group of independent products, Wt waves
+// per tile (Wt per matrix, a power of two <= W, so that a wave owns at most
+// about 8-16 of the tile's 64-column pairs); tile0 maps workgroups:
+//  * every 128-bit load of the first round (a contiguous stretch of the T16
+//    array per tile) and the scales of the range chains are requested first;
+//  * prologue: the activation, quantised to Q8_0 from binary32 (the
+//    lgx_k_quantize_q8_0 rule) or copied, into LDS in (pair, chunk) order;
+//  * exact int32 block dots (v_dot4 on each lane's two 8-byte chunks,
+//    reduce_chunks across the chunk lanes) go to LDS;
+//  * thread (tile, row, range) runs the canonical fmaf chain of its range
+//    and thread (tile, row) the pairwise tree over ranges -> y (no partials,
+//    no combine launch), or the chains are stored as range partials.
+// LDS (dynamic): k bytes of activation, k/32 scales, then per tile 16 x k/32
+// block dots and 16 x ranges partials.
+// ---------------------------------------------------------------------------
+template <int W, int PS>
+__device__ __forceinline__ void q8_gemv_wg_body(const lgx_gemv_group_args& ga) {
+    extern __shared__ __align__(16) uint8_t lds_dyn[];
+    constexpr int NT = 64 * W;                     // PS: pairs per wave per round
+    const int bx = blockIdx.x;
+    int g = 0;
+#pragma unroll 1
+    while (g + 1 < ga.count && bx >= ga.tile0[g + 1]) ++g;
+    const lgx_gemv_mat& a = ga.mat[g];
+    const int lwt = a.pad;                         // log2 of waves per tile
+    const int Wt = 1 << lwt, tpw = W >> lwt;
+    const int k = a.k, nb = k >> 5, np = k >> 6, nh = s16_nhalf(k);
+    const int nr = (nb + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS;
+    const int ntiles = a.n >> 4;
+    const int tile_base = (bx - ga.tile0[g]) * tpw;
+    int8_t* xs = (int8_t*)lds_dyn;                 // k bytes, (pair, chunk) order
+    float* dxs = (float*)(lds_dyn + k);            // nb
+    int* ss = (int*)(dxs + nb);                    // [tpw][nb][16]
+    float* ps = (float*)(ss + tpw * nb * 16);      // [tpw][nr][16]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int r = lane & 15, c = lane >> 4;
+    const int ts = wave >> lwt, wt = wave & (Wt - 1);
+    const int t = tile_base + ts;
+    const bool tile_on = t < ntiles;
+
+    const uint4* wp = (const uint4*)a.wt + (int64_t)t * np * 64 + lane;
+    uint4 wv[PS];
+    if (tile_on) {
+#pragma unroll
+        for (int i = 0; i < PS; ++i) {
+            const int p = wt + Wt * i;
+            if (p < np) wv[i] = ld_stream(wp + (int64_t)p * 64);
+        }
+    }
+    // chain thread q = tid: (tile q / (16 nr), row q % 16, range (q / 16) % nr)
+    uint32_t dwa[8], dwb[8];
+    {
+        const int qt = tid / (16 * nr), qg = (tid >> 4) % nr, qr = tid & 15;
+        if (qt < tpw && tile_base + qt < ntiles) {
+            load_scales_half(a.wd, tile_base + qt, min(2 * qg, nh - 1), nh, qr, dwa);
+            load_scales_half(a.wd, tile_base + qt, min(2 * qg + 1, nh - 1), nh, qr, dwb);
+        }
+    }
+
+    if (a.xf) {
+        const bool first = bx == ga.tile0[g];
+        for (int s2 = tid; s2 < nb * 8; s2 += NT) {   // 8 lanes per block, whole groups
+            const int bl = s2 >> 3, j = s2 & 7;
+            const float4 v = *(const float4*)(a.xf + bl * 32 + 4 * j);
+            const float f[4] = {v.x, v.y, v.z, v.w};
+            uint16_t dh;
+            const uint32_t qw = quantize4(f, dh);
+            *(uint32_t*)(xs + ((bl >> 1) * 4 + (j >> 1)) * 16 + (bl & 1) * 8 + 4 * (j & 1)) = qw;
+            if (j == 0) dxs[bl] = h2f(dh);
+            if (first && a.xq_out) {
+                *(uint32_t*)(a.xq_out + bl * 32 + 4 * j) = qw;
+                if (j == 0) a.xd_out[bl] = dh;
+            }
+        }
+    } else {
+        for (int s2 = tid; s2 < 4 * np; s2 += NT) {
+            const int8_t* src = a.xq + (s2 >> 2) * 64 + 8 * (s2 & 3);
+            const uint2 lo = *(const uint2*)src;
+            const uint2 hi = *(const uint2*)(src + 32);
+            *(uint4*)(xs + s2 * 16) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        }
+        for (int b = tid; b < nb; b += NT) dxs[b] = h2f(a.xd[b]);
+    }
+    __syncthreads();
+
+    if (tile_on) {
+        int* sst = ss + ts * nb * 16;
+        const int row = t * 16 + r;
+#pragma unroll 1
+        for (int p0 = 0; p0 < np; p0 += PS * Wt) {
+            if (p0 > 0) {
+#pragma unroll
+                for (int i = 0; i < PS; ++i) {
+                    const int p = p0 + wt + Wt * i;
+                    if (p < np) wv[i] = ld_stream(wp + (int64_t)p * 64);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < PS; ++i) {
+                const int p = p0 + wt + Wt * i;
+                if (p < np) {                      // wave-uniform
+                    const int4 xv = *(const int4*)(xs + (p * 4 + c) * 16);
+                    int s0 = __builtin_amdgcn_sdot4((int)wv[i].x, xv.x, 0, false);
+                    s0 = __builtin_amdgcn_sdot4((int)wv[i].y, xv.y, s0, false);
+                    int s1 = __builtin_amdgcn_sdot4((int)wv[i].z, xv.z, 0, false);
+                    s1 = __builtin_amdgcn_sdot4((int)wv[i].w, xv.w, s1, false);
+                    reduce_chunks(s0, s1);
+                    if (c == 0) {
+                        sst[(2 * p) * 16 + r] = s0;
+                        sst[(2 * p + 1) * 16 + r] = s1;
+                        if (a.dbg) {
+                            a.dbg[(int64_t)row * nb + 2 * p] = s0;
+                            a.dbg[(int64_t)row * nb + 2 * p + 1] = s1;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // canonical chains
+#pragma unroll 1
+    for (int q = tid; q < tpw * 16 * nr; q += NT) {
+        const int qt = q / (16 * nr), qg = (q >> 4) % nr, qr = q & 15;
+        const int tq = tile_base + qt;
+        if (tq >= ntiles) continue;
+        if (q != tid) {
+            load_scales_half(a.wd, tq, min(2 * qg, nh - 1), nh, qr, dwa);
+            load_scales_half(a.wd, tq, min(2 * qg + 1, nh - 1), nh, qr, dwb);
+        }
+        const int* sst = ss + qt * nb * 16;
+        const int b0 = qg * LGX_Q8_RANGE_BLOCKS;
+        const int nbr = min(LGX_Q8_RANGE_BLOCKS, nb - b0);
+        float P = 0.0f;
+#pragma unroll
+        for (int j = 0; j < LGX_Q8_RANGE_BLOCKS; ++j) {
+            if (j < nbr) {
+                const uint32_t w2 = j < 16 ? dwa[(j & 15) >> 1] : dwb[(j & 15) >> 1];
+                const float dwf = h2f((j & 1) ? (w2 >> 16) : (w2 & 0xffffu));
+                P = fmaf((float)sst[(b0 + j) * 16 + qr], dwf * dxs[b0 + j], P);
+            }
+        }
+        if (a.part_out)
+            a.y[(int64_t)qg * a.n + tq * 16 + qr] = P;
+        else
+            ps[(qt * nr + qg) * 16 + qr] = P;
+    }
+    if (a.part_out) return;
+    __syncthreads();
+    if (tid < tpw * 16) {
+        const int qt = tid >> 4, qr = tid & 15;
+        const int tq = tile_base + qt;
+        if (tq < ntiles) {
+            float p[LGX_MAX_RANGES];
+#pragma unroll
+            for (int j = 0; j < LGX_MAX_RANGES; ++j) p[j] = j < nr ? ps[(qt * nr + j) * 16 + qr] : 0.0f;
+            a.y[tq * 16 + qr] = tree_sum(p, nr);
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_wg4(const lgx_gemv_group_args a) {
+    q8_gemv_wg_body<4, 16>(a);
+}
+extern "C" __global__ __launch_bounds__(512) void lgx_k_q8_gemv_wg8(const lgx_gemv_group_args a) {
+    q8_gemv_wg_body<8, 16>(a);
+}
+extern "C" __global__ __launch_bounds__(1024) void lgx_k_q8_gemv_wg16(const lgx_gemv_group_args a) {
+    q8_gemv_wg_body<16, 10>(a);
+}
+
+// ---------------------------------------------------------------------------
 // Q8 GEMV with a binary32 activation (tolerance-checked path).  Same T16
 // walk; x staged in LDS as floats in T16 activation order (slot (p*4+c) =
 // 8 floats of block 2p chunk c, then 8 of block 2p+1).  Per lane an 8-term
@@ -473,6 +668,183 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_mfma(const lgx_g
 }
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_mfma_qx(const lgx_gemv_args a) {
     q8_gemv_mfma_body<true>(a);
+}
+
+// ---------------------------------------------------------------------------
+// Grouped Q8 x Q8 GEMV (M = 1), ranges of a tile inside one workgroup.
+// A launch covers independent matrices (tile0 maps workgroups to matrices).
+// A workgroup of W waves (4, 8 or 16: the group's largest range count,
+// rounded up) serves tpw = W / min(ranges, W) row tiles of one matrix; wave (tile slot, range) requests all 16 of its range's 128-bit
+// T16 loads and scale words at once, multiplies on int8 MFMA with the
+// activation broadcast (D row = block dot of weight row r), and runs the
+// canonical fmaf chain of its range (lanes 0-15 hold row r); the pairwise
+// tree over the tile's ranges is applied in LDS -> y, or the chains are
+// stored as range partials.  Rows of more than W ranges take several
+// ranges per wave.  The activation (quantised to Q8_0 from binary32 by the
+// lgx_k_quantize_q8_0 rule, or copied) is staged in LDS in (pair, chunk)
+// order.  LDS (dynamic): k bytes, k/32 scales, tpw x ranges x 16 chains.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void grp_stage(const lgx_gemv_mat& a, int8_t* xs, float* dxs,
+                                          bool emit) {
+    const int nb = a.k >> 5, np = a.k >> 6, tid = threadIdx.x, nt = blockDim.x;
+    if (a.xf) {
+        // 8 lanes per block, whole groups; two blocks' loads in flight per lane
+#pragma unroll 1
+        for (int s0 = tid; s0 < nb * 8; s0 += 2 * nt) {
+            float4 v[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int s2 = s0 + u * nt;
+                if (s2 < nb * 8) v[u] = *(const float4*)(a.xf + (s2 >> 3) * 32 + 4 * (s2 & 7));
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int s2 = s0 + u * nt;
+                if (s2 < nb * 8) {                 // all 8 lanes of a block or none
+                    const int bl = s2 >> 3, j = s2 & 7;
+                    const float f[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+                    uint16_t dh;
+                    const uint32_t qw = quantize4(f, dh);
+                    *(uint32_t*)(xs + ((bl >> 1) * 4 + (j >> 1)) * 16 + (bl & 1) * 8 + 4 * (j & 1)) = qw;
+                    if (j == 0) dxs[bl] = h2f(dh);
+                    if (emit && a.xq_out) {
+                        *(uint32_t*)(a.xq_out + bl * 32 + 4 * j) = qw;
+                        if (j == 0) a.xd_out[bl] = dh;
+                    }
+                }
+            }
+        }
+    } else {
+        for (int s2 = tid; s2 < 4 * np; s2 += nt) {
+            const int8_t* src = a.xq + (s2 >> 2) * 64 + 8 * (s2 & 3);
+            const uint2 lo = *(const uint2*)src;
+            const uint2 hi = *(const uint2*)(src + 32);
+            *(uint4*)(xs + s2 * 16) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        }
+        for (int b = tid; b < nb; b += nt) dxs[b] = h2f(a.xd[b]);
+    }
+}
+
+// One wave's range: loads (issued by grp_issue) -> MFMA -> canonical chain.
+__device__ __forceinline__ void grp_issue(const lgx_gemv_mat& a, int t, const RangeInfo& ri,
+                                          int lane, uint4 (&w)[16], uint32_t (&dw)[16]) {
+    const int np = a.k >> 6, nh = s16_nhalf(a.k), r = lane & 15;
+    const uint4* wp = (const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if (i < ri.npairs) w[i] = ld_stream(wp + i * 64);
+    uint32_t d0[8], d1[8];
+    load_scales_half(a.wd, t, 2 * ri.g, nh, r, d0);
+    load_scales_half(a.wd, t, min(2 * ri.g + 1, nh - 1), nh, r, d1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        dw[i] = d0[i];
+        dw[8 + i] = d1[i];
+    }
+}
+
+__device__ __forceinline__ float grp_range(const lgx_gemv_mat& a, int t, const RangeInfo& ri,
+                                           int lane, const int8_t* xs, const float* dxs,
+                                           const uint4 (&w)[16], const uint32_t (&dw)[16]) {
+    const int r = lane & 15, c = lane >> 4, nb = a.k >> 5;
+    const v4i zero = {0, 0, 0, 0};
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        if (i < ri.npairs) {                       // wave-uniform
+            const int p = ri.p0 + i;
+            const uint4 xv = *(const uint4*)(xs + (p * 4 + c) * 16);
+            const long a0 = (long)(((uint64_t)xv.y << 32) | xv.x);
+            const long a1 = (long)(((uint64_t)xv.w << 32) | xv.z);
+            long b0 = (long)(((uint64_t)w[i].y << 32) | w[i].x);
+            long b1 = (long)(((uint64_t)w[i].w << 32) | w[i].z);
+            // unit i's MFMAs after unit i-1's chain step: one unit live at a time
+            asm volatile("" : "+v"(b0), "+v"(b1));
+            const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, zero, 0, 0, 0);
+            const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, zero, 0, 0, 0);
+            const float e0 = h2f(dw[i] & 0xffffu) * dxs[2 * p];
+            const float e1 = h2f(dw[i] >> 16) * dxs[2 * p + 1];
+            acc = fmaf((float)d0[0], e0, acc);
+            acc = fmaf((float)d1[0], e1, acc);
+            asm volatile("" : "+v"(acc));
+            if (a.dbg && c == 0) {
+                a.dbg[(int64_t)(t * 16 + r) * nb + 2 * p] = d0[0];
+                a.dbg[(int64_t)(t * 16 + r) * nb + 2 * p + 1] = d1[0];
+            }
+        }
+    }
+    return acc;
+}
+
+template <int W>
+__device__ __forceinline__ void q8_gemv_grp_body(const lgx_gemv_group_args& ga) {
+    extern __shared__ __align__(16) uint8_t lds_dyn[];
+    const int bx = blockIdx.x;
+    int g = 0;
+#pragma unroll 1
+    while (g + 1 < ga.count && bx >= ga.tile0[g + 1]) ++g;
+    const lgx_gemv_mat& a = ga.mat[g];
+    const int k = a.k, nb = k >> 5;
+    const int nr = (nb + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS;
+    const int nrs = min(nr, W), tpw = W / nrs;
+    const int ntiles = a.n >> 4;
+    const int tile_base = (bx - ga.tile0[g]) * tpw;
+    int8_t* xs = (int8_t*)lds_dyn;                 // k bytes, (pair, chunk) order
+    float* dxs = (float*)(lds_dyn + k);            // nb
+    float* ps = dxs + nb;                          // [tpw][nr][16]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int ts = wave / nrs, rg = wave - ts * nrs;
+    const int t = tile_base + ts;
+    const bool on = ts < tpw && t < ntiles;
+
+    uint4 w[16];
+    uint32_t dw[16];
+    const RangeInfo ri = range_info(rg, k);
+    if (on) grp_issue(a, t, ri, lane, w, dw);
+    grp_stage(a, xs, dxs, bx == ga.tile0[g]);
+    __syncthreads();
+    if (on) {
+        float acc = grp_range(a, t, ri, lane, xs, dxs, w, dw);
+        if (lane < 16) {
+            if (a.part_out)
+                a.y[(int64_t)rg * a.n + t * 16 + lane] = acc;
+            else
+                ps[(ts * nr + rg) * 16 + lane] = acc;
+        }
+#pragma unroll 1
+        for (int rg2 = rg + W; rg2 < nr; rg2 += W) {   // rows of more than W ranges
+            const RangeInfo r2 = range_info(rg2, k);
+            grp_issue(a, t, r2, lane, w, dw);
+            acc = grp_range(a, t, r2, lane, xs, dxs, w, dw);
+            if (lane < 16) {
+                if (a.part_out)
+                    a.y[(int64_t)rg2 * a.n + t * 16 + lane] = acc;
+                else
+                    ps[(ts * nr + rg2) * 16 + lane] = acc;
+            }
+        }
+    }
+    if (a.part_out) return;
+    __syncthreads();
+    if (tid < tpw * 16) {
+        const int qt = tid >> 4, qr = tid & 15;
+        if (tile_base + qt < ntiles) {
+            float p[LGX_MAX_RANGES];
+#pragma unroll
+            for (int j = 0; j < LGX_MAX_RANGES; ++j) p[j] = j < nr ? ps[(qt * nr + j) * 16 + qr] : 0.0f;
+            a.y[(tile_base + qt) * 16 + qr] = tree_sum(p, nr);
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_grp4(const lgx_gemv_group_args a) {
+    q8_gemv_grp_body<4>(a);
+}
+extern "C" __global__ __launch_bounds__(512) void lgx_k_q8_gemv_grp8(const lgx_gemv_group_args a) {
+    q8_gemv_grp_body<8>(a);
+}
+extern "C" __global__ __launch_bounds__(1024) void lgx_k_q8_gemv_grp16(const lgx_gemv_group_args a) {
+    q8_gemv_grp_body<16>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -910,27 +1282,6 @@ __device__ __forceinline__ float tree_partials(const float* part, int nr, int64_
 #pragma unroll
     for (int j = 0; j < LGX_MAX_RANGES; ++j) p[j] = j < nr ? part[j * stride + i] : 0.0f;
     return tree_sum(p, nr);
-}
-
-// Q8_0 of one 32-block held by 8 consecutive lanes (4 values each): the
-// lgx_k_quantize_q8_0 rule.  Returns the packed quants of this lane's four
-// values and the binary16 scale.
-__device__ __forceinline__ uint32_t quantize4(const float (&f)[4], uint16_t& dh) {
-    float am = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
-    am = fmaxf(am, shfl_xor_f(am, 1));
-    am = fmaxf(am, shfl_xor_f(am, 2));
-    am = fmaxf(am, shfl_xor_f(am, 4));
-    const float d = am / 127.0f;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t qw = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        float q = roundf(f[e] * id);
-        q = fminf(fmaxf(q, -127.0f), 127.0f);
-        qw |= ((uint32_t)(int32_t)q & 0xffu) << (8 * e);
-    }
-    dh = f2h(d);
-    return qw;
 }
 
 // Quantise a row held in LDS (n floats, n % 32 == 0) to xq/xd with NT

@@ -139,6 +139,10 @@ inline Kern prod_kernel(int m) {
 }
 
 lgx_status product(lgx_model* md, const DevQ8& W, int m, void* stream) {
+    if (m == 1 && gemv_group_ok(md->ctx, W.m.k)) {
+        const lgx_gemv_mat g = gemv_mat(&W.m, nullptr, md->xq, md->xd, md->part, 1);
+        return run_gemv_group(md->ctx, &g, 1, stream);
+    }
     return run_q8(md->ctx, prod_kernel(m), &W.m, nullptr, md->xq, md->xd, m, md->part, nullptr,
                   stream, nullptr, nullptr, md->part);
 }

@@ -198,13 +198,16 @@ def _ctx_with_env(**env):
 
 @pytest.mark.parametrize("n,k", [(4864, 896), (1536, 8960), (272, 2112)])
 def test_kernel_variants_agree(ctx, orc, n, k):
-    """The v_dot4 GEMV, the MFMA GEMV and the MFMA GEMM at every m-tile
-    width, with one or many row tiles per wave, all give the oracle's bits."""
+    """The whole-K workgroup GEMV, the per-(tile, range) v_dot4 and MFMA
+    GEMVs and the MFMA GEMM at every m-tile width, with one or many row tiles
+    per wave, all give the oracle's bits."""
     qs, d = orc.gen_q8_matrix(2, n + k, n, k)
     x = orc.gen_normal_f32(2, 7, (40, k))
     xq, xd = orc.quantize_q8_0(x)
     ref = orc.q8_gemm(qs, d, xq, xd)
-    for c in (ctx, _ctx_with_env(LGX_GEMV="dot4"), _ctx_with_env(LGX_WG_TARGET=3)):
+    for c in (ctx, _ctx_with_env(LGX_GEMV="dot4"), _ctx_with_env(LGX_GEMV="split"),
+              _ctx_with_env(LGX_GEMV="whole"), _ctx_with_env(LGX_GEMV_WGS=4),
+              _ctx_with_env(LGX_GEMV_WGS=16), _ctx_with_env(LGX_WG_TARGET=3)):
         W = c.q8_matrix(qs, d)
         gx, gd = c.to_device(xq), c.to_device(xd)
         assert np.array_equal(host(c.q8q8_gemv(W, gx[0], gd[0])), ref[0])
@@ -250,7 +253,53 @@ def test_kernel_timing_window(ctx, orc):
         ctx.q8q8_gemv_quantize(W, x)
     ctx.kernel_timing(False)
     ctx.q8q8_gemv_quantize(W, x)          # outside the window: not recorded
-    n, ms = ctx.kernel_stats("lgx_k_q8_gemv_mfma_qx")
+    stats = [ctx.kernel_stats(f"lgx_k_q8_gemv_grp{w}") for w in (4, 8, 16)]
+    n, ms = sum(s[0] for s in stats), sum(s[1] for s in stats)
     assert n == 3 and 0.0 < ms < 100.0
-    assert ctx.kernel_stats("lgx_k_q8_combine")[0] == 3
+    # the whole-K GEMV applies the range tree itself: no combine launches
+    assert ctx.kernel_stats("lgx_k_q8_combine")[0] == 0
     assert ctx.kernel_stats("lgx_k_quantize_q8_0") == (0, 0.0)
+
+
+def test_grouped_gemv_bit_exact(ctx, orc):
+    """One launch over independent matrices of different shapes (config 1's
+    gate/up/down, config 0, a 19-range K): each output equals its own
+    fused-quantise GEMV and the oracle."""
+    shapes = [(8960, 1536), (8960, 1536), (1536, 8960), (4864, 896), (512, 18944)]
+    Ws, xs, refs = [], [], []
+    for i, (n, k) in enumerate(shapes):
+        qs, d = orc.gen_q8_matrix(4, 100 + i, n, k)
+        x = orc.gen_normal_f32(4, 200 + i, (1, k))
+        xq, xd = orc.quantize_q8_0(x)
+        Ws.append(ctx.q8_matrix(qs, d))
+        xs.append(ctx.to_device(x[0]))
+        refs.append(orc.q8_gemm(qs, d, xq, xd)[0])
+    before = ctx.launch_count
+    ys = ctx.q8q8_gemv_quantize_group(Ws, xs)
+    assert ctx.launch_count == before + 1
+    for y, ref, W, x in zip(ys, refs, Ws, xs):
+        assert np.array_equal(host(y), ref)
+        assert np.array_equal(host(ctx.q8q8_gemv_quantize(W, x)), ref)
+
+
+def test_grouped_gemv_long_k_and_errors(ctx, orc):
+    """The longest K (32 ranges, two per wave) in a group; the whole-K variant
+    rejects it for LDS, and single products then take the per-range path."""
+    qs, d = orc.gen_q8_matrix(5, 1, 32, 32768)
+    x = orc.gen_normal_f32(5, 2, (1, 32768))
+    xq, xd = orc.quantize_q8_0(x)
+    ref = orc.q8_gemm(qs, d, xq, xd)[0]
+    W = ctx.q8_matrix(qs, d)
+    gx = ctx.to_device(x[0])
+    assert np.array_equal(host(ctx.q8q8_gemv_quantize_group([W], [gx])[0]), ref)
+    with pytest.raises(lgx.LgxError):
+        ctx.q8q8_gemv_quantize_group([W] * 9, [gx] * 9)
+    cw = _ctx_with_env(LGX_GEMV="whole")
+    Ww = cw.q8_matrix(qs, d)
+    gw = cw.to_device(x[0])
+    with pytest.raises(lgx.LgxError) as e:
+        cw.q8q8_gemv_quantize_group([Ww], [gw])
+    assert e.value.status_name == "LGX_UNSUPPORTED"
+    assert np.array_equal(host(cw.q8q8_gemv_quantize(Ww, gw)), ref)
+    assert np.array_equal(host(cw.q8q8_gemv(Ww, cw.to_device(xq[0]), cw.to_device(xd[0]))), ref)
+    cw.close()
