@@ -42,6 +42,11 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 DOMINANT = ("lgx_k_q8_gemv_grp4", "lgx_k_q8_gemv_grp8", "lgx_k_q8_gemv_grp16")
 DOMINANT_USED = DOMINANT[2]
+# HBM bytes per dispatch of the grouped config-1 launch, from rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE passes of this script (--copy-calibration): the
+# counters scaled by what they read for a plain 256 MiB device copy (FETCH_SIZE
+# x 2.0, WRITE_SIZE x 1.0); profiles/q8_gemv_grouped_config1.md.
+TRAFFIC_BYTES = (21697.0 * 2.0 + 76.0) * 1024
 MALL_BYTES = 256 << 20
 SHAPES = (("gate", 8960, 1536), ("up", 8960, 1536), ("down", 1536, 8960))
 
@@ -330,6 +335,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--decode", default="config3,config4",
                     help="decode configs to run (comma list; empty for none)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 4 plain 256 MiB device copies (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -392,13 +399,23 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC_BYTES if DOMINANT_USED == "lgx_k_q8_gemv_grp16" else None,
             "avg_launch_us": round(gemv_ms * 1e3, 3),
             "bytes_per_launch": int(per_launch),
         },
     }
     del sets
     torch.cuda.empty_cache()
+    if args.copy_calibration:
+        # reference kernel for the FETCH_SIZE / WRITE_SIZE counters: reads and
+        # writes exactly 256 MiB each
+        src = torch.empty(64 << 20, dtype=torch.float32, device=ctx.dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
     sustained = sustained_gemv(ctx, torch)
     print(f"[bench] sustained GEMV {SUSTAINED_SHAPE}: {sustained['us_per_launch']} us, "
           f"{sustained['GB_s']} GB/s", file=sys.stderr, flush=True)

@@ -34,6 +34,26 @@
  *   q8 gemm          per-row equality with the M=1 path (batch invariance),
  *                    numpy-f64 fixture within 1e-5 rel, one-hot closed form
  *   repack t16/s16   round trip + explicit index formula on a tiny case
+ *   gqa decode attn  numpy float64 softmax attention on the golden fixture
+ *                    (tests/test_oracle_attn.py) within 2e-3, a head-swap
+ *                    mutant rejected; single token -> v0 exactly; equal
+ *                    scores -> mean; constant V -> V; page-order invariance
+ *   rmsnorm          numpy float64 within 3e-6 rel; scale invariance;
+ *                    constant row -> sign (the halving-sum order itself is
+ *                    checked by tests/test_oracle_attn.py)
+ *   rope             norm preservation, position 0 identity, the rotate-half
+ *                    pair formula, relative-position property
+ *                    <R_p q, R_s k> = f(p - s)
+ *   swiglu / silu    silu(0) = 0, large-|g| asymptotes, numpy float64
+ *   argmax           first maximum, NaN skipped, all-NaN -> 0, -0 == +0
+ *   lm_head_f16      one-hot rows select embedding columns exactly; numpy
+ *                    float64 within the chain's error bound
+ *   model step       a numpy float64 forward of the same Qwen2 decoder
+ *                    (tests/test_oracle_model.py) agrees within 1e-3 of the
+ *                    logit scale, an interleaved-RoPE mutant does not; batch
+ *                    and slot invariance
+ * None of these is "parity unpinned": each has the checks above, chosen so
+ * that a dropped term, wrong sign or transposed operand fails one of them.
  */
 #ifndef LGX_ORACLE_H
 #define LGX_ORACLE_H
