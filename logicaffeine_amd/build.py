@@ -23,11 +23,15 @@ LIB = os.path.join(HERE, "liblgx.so")
 
 # -ffp-contract=off: no implicit fusion, the float schedule is what the source
 # says.  Correctly rounded binary32 division and square root.  Packed-FP32
-# instructions disabled (v_pk_*_f32 are never generated).
+# instructions disabled (v_pk_*_f32 are never generated).  MFMA destinations
+# in VGPRs.
 HIP_FLAGS = [
     "--genco", "--no-gpu-bundle-output", f"--offload-arch={ARCH}", "-O3", "-std=c++17",
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs (gfx950 allows it): the epilogues read
+    # them directly instead of copying each value out of an AGPR first
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -62,6 +62,7 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
         c->gemv_split = gv && std::string(gv) == "split";
         c->gemv_whole = gv && std::string(gv) == "whole";
         c->gemv_wgs = env_int("LGX_GEMV_WGS", 0);
+        c->gemm_mt = env_int("LGX_GEMM_MT", 0);
         int ncu = 0;
         if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) ==
                 hipSuccess &&
@@ -302,8 +303,7 @@ lgx_status lgx_q8_gemm_partials(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t
             lgx_gemv_mat g = gemv_mat(W, nullptr, xq, xd, part, 1);
             return run_gemv_group(c, &g, 1, stream);
         }
-        Kern k = m == 1 ? K_GEMV_MFMA : m <= 16 ? K_GEMM_MFMA16 : m <= 32 ? K_GEMM_MFMA32
-                                                                          : K_GEMM_MFMA64;
+        Kern k = m == 1 ? K_GEMV_MFMA : gemm_kernel(c, m);
         return run_q8(c, k, W, nullptr, xq, xd, m, part, nullptr, stream, nullptr, nullptr, part);
     });
 }
@@ -376,8 +376,7 @@ lgx_status lgx_q8_gemm(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq, con
             lgx_gemv_mat g = gemv_mat(W, nullptr, xq, xd, y, 0);
             return run_gemv_group(c, &g, 1, stream);
         }
-        Kern k = m <= 16 ? K_GEMM_MFMA16 : m <= 32 ? K_GEMM_MFMA32 : K_GEMM_MFMA64;
-        return run_q8(c, k, W, nullptr, xq, xd, m, y, nullptr, stream);
+        return run_q8(c, gemm_kernel(c, m), W, nullptr, xq, xd, m, y, nullptr, stream);
     });
 }
 

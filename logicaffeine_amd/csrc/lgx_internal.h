@@ -152,6 +152,7 @@ struct lgx_ctx {
     bool gemv_split = false;      // LGX_GEMV=split: per-(tile, range) MFMA GEMV
     int gemv_wgs = 0;             // LGX_GEMV_WGS: M = 1 GEMV waves per workgroup (0: auto)
     bool gemv_whole = false;      // LGX_GEMV=whole: block dots through LDS, chains after
+    int gemm_mt = 0;              // LGX_GEMM_MT: force the M > 1 m-tile width (0: by m)
     int ncu = 256;                // compute units of the device
     int wg_target = 512;
     std::atomic<uint64_t> launches{0};
@@ -270,6 +271,15 @@ inline lgx_status check_q8(const lgx_q8_matrix* W) {
 inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 inline int nranges_of(int k) { return (k / 32 + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS; }
 
+// M > 1 product kernel: m-tile width 16 / 32 / 64 rows (LGX_GEMM_MT forces one).
+inline Kern gemm_kernel(const lgx_ctx* c, int m) {
+    const int mt = c->gemm_mt;
+    if (mt == 16) return K_GEMM_MFMA16;
+    if (mt == 32) return K_GEMM_MFMA32;
+    if (mt == 64) return K_GEMM_MFMA64;
+    return m <= 16 ? K_GEMM_MFMA16 : m <= 32 ? K_GEMM_MFMA32 : K_GEMM_MFMA64;
+}
+
 // Shared driver of the GEMV/GEMM kernels: one launch over (row tiles, ranges,
 // m-groups); with more than one range the partials go to the workspace and
 // the combine kernel applies the canonical tree.
@@ -304,18 +314,19 @@ inline lgx_status run_q8(lgx_ctx* c, Kern kern, const lgx_q8_matrix* W, const fl
     const bool streaming =
         kern == K_GEMM_MFMA16 || kern == K_GEMM_MFMA32 || kern == K_GEMM_MFMA64;
     const int mrows = kern == K_GEMM_MFMA16 ? 16 : kern == K_GEMM_MFMA32 ? 32 : 64;
+    const int nw = kern == K_GEMM_MFMA64 ? 8 : 4;  // waves per workgroup
     a.nmgroups = streaming ? (m + mrows - 1) / mrows : 1;
     a.tpw = 1;
     if (streaming) {
         // tiles per wave: enough work per wave that the grid is about
-        // wg_target workgroups of 4 waves
+        // wg_target workgroups of nw waves
         int64_t tasks = (int64_t)a.ntiles * a.nranges * a.nmgroups;
-        int64_t tpw = (tasks + 4LL * c->wg_target - 1) / (4LL * c->wg_target);
+        int64_t tpw = (tasks + (int64_t)nw * c->wg_target - 1) / ((int64_t)nw * c->wg_target);
         a.tpw = (int)(tpw < 1 ? 1 : tpw > 64 ? 64 : tpw);
     }
-    dim3 grid(cdiv(a.ntiles, 4LL * a.tpw), a.nranges,
-              streaming ? a.nmgroups : 1);
-    lgx_status st = launch(c, kern, grid, dim3(256), a, stream);
+    dim3 grid(cdiv(a.ntiles, (int64_t)(streaming ? nw : 4) * a.tpw) * (streaming ? a.nmgroups : 1),
+              a.nranges, 1);
+    lgx_status st = launch(c, kern, grid, dim3(streaming ? 64 * nw : 256), a, stream);
     if (st != LGX_OK || a.nranges == 1 || part_out) return st;
     lgx_combine_args ca{a.part, y, (int64_t)m * W->n, a.nranges};
     return launch(c, K_COMBINE, dim3(cdiv(ca.count, 256)), dim3(256), ca, stream);

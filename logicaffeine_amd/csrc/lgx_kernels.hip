@@ -860,35 +860,52 @@ extern "C" __global__ __launch_bounds__(1024) void lgx_k_q8_gemv_grp16(const lgx
 // canonical chain acc = fmaf((float)D, dw*dx, acc).  Range partials go to
 // `part` (several ranges) and lgx_k_q8_combine applies the tree.
 // ---------------------------------------------------------------------------
-template <int MT>
+template <int MT, int W, int PB>
 __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
     constexpr int XSLOTS = MT * 16 * 64;   // 16-byte A-operand slots
     constexpr int DXROWS = MT * 16;
+    constexpr int NT = 64 * W;
+    constexpr int NB = 16 / PB;            // batches per tile-range (16 pairs)
     __shared__ __align__(16) uint4 xa_s[XSLOTS];
     __shared__ __align__(16) float dx_s[LGX_Q8_RANGE_BLOCKS * DXROWS];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const RangeInfo ri = range_info(blockIdx.y, a.k);
     const int nb = a.k >> 5, nh = s16_nhalf(a.k);
-    const int m0 = blockIdx.z * DXROWS;
+    // m-group fastest along x: the groups of one set of row tiles run
+    // together and share the weight stream through L2 / MALL
+    const int mg = blockIdx.x % a.nmgroups, tg = blockIdx.x / a.nmgroups;
+    const int m0 = mg * DXROWS;
     const int mrows = min(DXROWS, a.m - m0);
     const int r = lane & 15, c = lane >> 4;
     const int np = a.k >> 6;
     const int last = ri.npairs - 1;
-    const int tbase = blockIdx.x * 4 * a.tpw + wave;
+    const int tbase = tg * W * a.tpw + wave;
     const v4i zero = {0, 0, 0, 0};
 
-    auto load_half = [&](int j, int h, uint4 (&w)[8], uint32_t (&dw)[8]) {
-        const int t = min(tbase + 4 * j, a.ntiles - 1);
+    // batch q of tile j: pairs [PB*(q % NB), +PB) of the range; scales of the
+    // batch are 2*PB consecutive blocks of the S16 half-range (q*PB)/8
+    auto load_batch = [&](int j, int qb, uint4 (&w)[PB], uint32_t (&dw)[PB]) {
+        const int t = min(tbase + W * j, a.ntiles - 1);
         const uint4* wp = (const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64 + lane;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = ld_stream(wp + min(8 * h + i, last) * 64);
-        load_scales_half(a.wd, t, min(2 * ri.g + h, nh - 1), nh, r, dw);
+        for (int i = 0; i < PB; ++i) w[i] = ld_stream(wp + min(PB * qb + i, last) * 64);
+        const int pair0 = PB * qb;                 // first pair of the batch
+        const int hh = min(2 * ri.g + pair0 / 8, nh - 1);
+        const uint4* sp = (const uint4*)(a.wd + (((int64_t)t * nh + hh) * 16 + r) * 16);
+        // 8 pairs (16 scales) per 32-byte row: a PB-pair batch is PB words
+        // starting at word pair0 % 8
+        uint32_t row[8];
+        const uint4 lo = sp[0], hi = sp[1];
+        row[0] = lo.x; row[1] = lo.y; row[2] = lo.z; row[3] = lo.w;
+        row[4] = hi.x; row[5] = hi.y; row[6] = hi.z; row[7] = hi.w;
+#pragma unroll
+        for (int i = 0; i < PB; ++i) dw[i] = row[(pair0 % 8) + i];
     };
     float acc[MT][4];
-    auto compute_half = [&](int h, const uint4 (&w)[8], const uint32_t (&dw)[8]) {
+    auto compute_batch = [&](int qb, const uint4 (&w)[PB], const uint32_t (&dw)[PB]) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int pi = 8 * h + i;
+        for (int i = 0; i < PB; ++i) {
+            const int pi = PB * qb + i;
             const bool on = pi <= last;
             const int pc = min(pi, last);
             const float dw0 = on ? h2f(dw[i] & 0xffffu) : 0.0f;
@@ -914,12 +931,12 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
                 acc[mt][3] = fmaf((float)d1[3], dw1 * x1.w, acc[mt][3]);
             }
             // keep each unit's MFMAs next to their epilogue: bounded live
-            // ranges (occupancy) instead of all 16 MFMA results in flight
+            // ranges (occupancy) instead of all the batch's MFMA results
             __builtin_amdgcn_sched_barrier(0);
         }
     };
     auto store_tile = [&](int j) {
-        const int t = tbase + 4 * j;
+        const int t = tbase + W * j;
         if (t >= a.ntiles) return;
         const int col = t * 16 + r;
 #pragma unroll
@@ -938,59 +955,75 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
         }
     };
 
-    uint4 wn[8];
-    uint32_t dn[8];
-    load_half(0, 0, wn, dn);
-    for (int s = threadIdx.x; s < XSLOTS; s += 256) {
-        const int mt = s >> 10, pl = (s >> 6) & 15, l = s & 63;
-        const int rr = l & 15, cc = l >> 4;
-        const int m = m0 + mt * 16 + rr;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (m < a.m && pl < ri.npairs) {
-            const int8_t* src = a.xq + (int64_t)m * a.k + (ri.p0 + pl) * 64 + 8 * cc;
-            const uint2 lo = *(const uint2*)src;
-            const uint2 hi = *(const uint2*)(src + 32);
-            v = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    uint4 wn[PB];
+    uint32_t dn[PB];
+    load_batch(0, 0, wn, dn);
+    // stage the activation range: every load of a thread is requested before
+    // the first LDS store (one L2 round trip, not one per slot)
+    {
+        constexpr int XS = XSLOTS / NT;            // slots per thread
+        uint2 lo[XS], hi[XS];
+#pragma unroll
+        for (int k = 0; k < XS; ++k) {
+            const int s = threadIdx.x + k * NT;
+            const int mt = s >> 10, pl = (s >> 6) & 15, l = s & 63;
+            const int rr = l & 15, cc = l >> 4;
+            const int m = m0 + mt * 16 + rr;
+            lo[k] = hi[k] = make_uint2(0, 0);
+            if (m < a.m && pl < ri.npairs) {
+                const int8_t* src = a.xq + (int64_t)m * a.k + (ri.p0 + pl) * 64 + 8 * cc;
+                lo[k] = *(const uint2*)src;
+                hi[k] = *(const uint2*)(src + 32);
+            }
         }
-        xa_s[s] = v;
-    }
-    for (int s = threadIdx.x; s < LGX_Q8_RANGE_BLOCKS * DXROWS; s += 256) {
-        const int b = s / DXROWS, m = s - b * DXROWS;
-        float v = 0.0f;
-        if (m < mrows && b < ri.nbr) v = h2f(a.xd[(int64_t)(m0 + m) * nb + ri.b0 + b]);
-        dx_s[s] = v;
+        constexpr int DS = LGX_Q8_RANGE_BLOCKS * DXROWS / NT;   // scales per thread
+        uint16_t dh[DS];
+#pragma unroll
+        for (int k = 0; k < DS; ++k) {
+            const int s = threadIdx.x + k * NT;
+            const int b = s / DXROWS, m = s - b * DXROWS;
+            dh[k] = (m < mrows && b < ri.nbr) ? a.xd[(int64_t)(m0 + m) * nb + ri.b0 + b] : (uint16_t)0;
+        }
+#pragma unroll
+        for (int k = 0; k < XS; ++k)
+            xa_s[threadIdx.x + k * NT] = make_uint4(lo[k].x, lo[k].y, hi[k].x, hi[k].y);
+#pragma unroll
+        for (int k = 0; k < DS; ++k) dx_s[threadIdx.x + k * NT] = h2f(dh[k]);
     }
     __syncthreads();
-    const int nhalves = 2 * a.tpw;
+    // batches of the range that hold pairs (the last range may be short)
+    const int nbq = min(NB, (ri.npairs + PB - 1) / PB);
+    const int nbat = nbq * a.tpw;
 #pragma unroll 1
-    for (int q = 0; q < nhalves; ++q) {
-        uint4 w[8];
-        uint32_t dw[8];
+    for (int q = 0; q < nbat; ++q) {
+        uint4 w[PB];
+        uint32_t dw[PB];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < PB; ++i) {
             w[i] = wn[i];
             dw[i] = dn[i];
         }
-        if (q + 1 < nhalves) load_half((q + 1) >> 1, (q + 1) & 1, wn, dn);
-        if ((q & 1) == 0) {
+        if (q + 1 < nbat) load_batch((q + 1) / nbq, (q + 1) % nbq, wn, dn);
+        const int qb = q % nbq;
+        if (qb == 0) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[mt][v] = 0.0f;
         }
-        compute_half(q & 1, w, dw);
-        if (q & 1) store_tile(q >> 1);
+        compute_batch(qb, w, dw);
+        if (qb == nbq - 1) store_tile(q / nbq);
     }
 }
 
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16(const lgx_gemv_args a) {
-    q8_stream_body<1>(a);
+    q8_stream_body<1, 4, 8>(a);
 }
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma32(const lgx_gemv_args a) {
-    q8_stream_body<2>(a);
+    q8_stream_body<2, 4, 8>(a);
 }
-extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma64(const lgx_gemv_args a) {
-    q8_stream_body<4>(a);
+extern "C" __global__ __launch_bounds__(512) void lgx_k_q8_gemm_mfma64(const lgx_gemv_args a) {
+    q8_stream_body<4, 8, 4>(a);
 }
 
 // ---------------------------------------------------------------------------

@@ -134,16 +134,13 @@ lgx_status check_config(const lgx_qwen_config* c) {
     return LGX_OK;
 }
 
-inline Kern prod_kernel(int m) {
-    return m == 1 ? K_GEMV_MFMA : m <= 16 ? K_GEMM_MFMA16 : m <= 32 ? K_GEMM_MFMA32 : K_GEMM_MFMA64;
-}
 
 lgx_status product(lgx_model* md, const DevQ8& W, int m, void* stream) {
     if (m == 1 && gemv_group_ok(md->ctx, W.m.k)) {
         const lgx_gemv_mat g = gemv_mat(&W.m, nullptr, md->xq, md->xd, md->part, 1);
         return run_gemv_group(md->ctx, &g, 1, stream);
     }
-    return run_q8(md->ctx, prod_kernel(m), &W.m, nullptr, md->xq, md->xd, m, md->part, nullptr,
+    return run_q8(md->ctx, m == 1 ? K_GEMV_MFMA : gemm_kernel(md->ctx, m), &W.m, nullptr, md->xq, md->xd, m, md->part, nullptr,
                   stream, nullptr, nullptr, md->part);
 }
 
