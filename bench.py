@@ -251,7 +251,8 @@ def decode_bench(ctx, torch, key, seed=3):
     import logicaffeine_amd as lgx
 
     shape, B, P, steps = DECODE_CONFIGS[key]
-    cfg = lgx.qwen_shape(shape, B, P + steps)
+    eager_steps = min(8, steps)
+    cfg = lgx.qwen_shape(shape, B, P + 1 + steps + eager_steps)
     t = time.perf_counter()
     gm = lgx.Model(ctx, cfg, seed)
     torch.cuda.synchronize()
@@ -268,14 +269,21 @@ def decode_bench(ctx, torch, key, seed=3):
           file=sys.stderr, flush=True)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
+    gm.generate(tok, 1)                       # records the step's HIP graph (untimed)
     torch.cuda.synchronize()
     e0.record()
-    for _ in range(steps):
-        gm.decode_step(tok)
+    gm.generate(tok, steps)                   # `steps` graph replays
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
-    ctxlen = P + (steps + 1) / 2.0            # mean attended tokens over the steps
+    # the same step launched kernel by kernel, for the launch-overhead figure
+    e0.record()
+    for _ in range(eager_steps):
+        gm.decode_step(tok)
+    e1.record()
+    torch.cuda.synchronize()
+    eager_ms = e0.elapsed_time(e1) / eager_steps
+    ctxlen = P + 1 + (steps + 1) / 2.0        # mean attended tokens over the timed steps
     step_bytes_ = lgx.decode_step_bytes(cfg, B, ctxlen)
     gbs = step_bytes_ / (ms * 1e-3) / 1e9
     gm.close()
@@ -286,13 +294,15 @@ def decode_bench(ctx, torch, key, seed=3):
         "batch": B, "prompt": P, "steps": steps,
         "tokens_per_s": round(B / (ms * 1e-3), 1),
         "ms_per_step": round(ms, 4),
+        "eager_ms_per_step": round(eager_ms, 4),
         "prefill_s": round(prefill_s, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "bytes_per_step": int(step_bytes_),
                      "roofline_tokens_per_s": round(B * HBM_PEAK_GBS * 1e9 / step_bytes_, 1)},
     }
-    print(f"[bench] {key}: {out['tokens_per_s']} tok/s, {ms:.3f} ms/step, {gbs:.0f} GB/s",
+    print(f"[bench] {key}: {out['tokens_per_s']} tok/s, {ms:.3f} ms/step (graph), "
+          f"{eager_ms:.3f} ms/step (eager), {gbs:.0f} GB/s",
           file=sys.stderr, flush=True)
     return out
 

@@ -275,6 +275,14 @@ lgx_status lgx_qwen_decode_step(lgx_model* m, int32_t B, int32_t* tokens, void* 
  * cache bits. */
 lgx_status lgx_qwen_prefill(lgx_model* m, int32_t B, int32_t P, const int32_t* prompt,
                             int32_t* next, void* stream);
+/* nsteps greedy decode steps, each identical in effect to
+ * lgx_qwen_decode_step(m, B, tokens).  The first call for a (B, tokens)
+ * pair records one step into a HIP graph (no memset nodes, no allocation)
+ * and every step replays it, so a step costs one graph launch on the host.
+ * history (NULL or device int32 [nsteps][B]) receives tokens after each
+ * step.  With per-kernel timing on, the steps are launched eagerly. */
+lgx_status lgx_qwen_generate(lgx_model* m, int32_t B, int32_t* tokens, int32_t nsteps,
+                             int32_t* history, void* stream);
 /* Device pointer and size in bytes of a model tensor (layer ignored for the
  * global ones). */
 lgx_status lgx_model_tensor(lgx_model* m, int32_t layer, int32_t which, const void** dev,

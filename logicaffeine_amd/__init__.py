@@ -74,6 +74,7 @@ SIGNATURES = {
     "lgx_model_reset": (C.c_int, [_P, _P]),
     "lgx_qwen_decode_step": (C.c_int, [_P, _I32, _P, _P]),
     "lgx_qwen_prefill": (C.c_int, [_P, _I32, _I32, _P, _P, _P]),
+    "lgx_qwen_generate": (C.c_int, [_P, _I32, _P, _I32, _P, _P]),
     "lgx_model_tensor": (C.c_int, [_P, _I32, _I32, C.POINTER(_P), C.POINTER(C.c_size_t)]),
     "lgx_qwen_logits": (C.c_int, [_P, _I32, _P, _P]),
 }
@@ -469,6 +470,14 @@ class Model:
         """tokens: device int32 [B], replaced in place by the next tokens."""
         _check(lib().lgx_qwen_decode_step(self.handle, tokens.numel(), tokens.data_ptr(),
                                           self.ctx._s()))
+
+    def generate(self, tokens, nsteps: int, history=None) -> None:
+        """nsteps decode steps replayed from a recorded HIP graph; tokens
+        (device int32 [B]) ends as the last step's next tokens and history
+        (device int32 [nsteps][B], optional) receives every step's."""
+        _check(lib().lgx_qwen_generate(self.handle, tokens.numel(), tokens.data_ptr(), nsteps,
+                                       0 if history is None else history.data_ptr(),
+                                       self.ctx._s()))
 
     def prefill(self, prompt, next_tokens=None):
         """prompt: device int32 [B][P]; returns the device int32 [B] next tokens."""

@@ -64,8 +64,19 @@ struct lgx_model {
     int32_t last_nr = 1;       // partial count of the last lm_head
     int32_t last_B = 0;        // batch of the last lm_head
     std::vector<void*> allocs;
+    // recorded decode steps (lgx_qwen_generate), one per (B, tokens) pair
+    struct StepGraph {
+        int32_t B;
+        int32_t* tokens;
+        int32_t last_nr;
+        hipGraphExec_t exec;
+    };
+    std::vector<StepGraph> graphs;
+    hipStream_t capture = nullptr;   // recording only: capture needs a non-null stream
 
     ~lgx_model() {
+        for (StepGraph& g : graphs) (void)hipGraphExecDestroy(g.exec);
+        if (capture) (void)hipStreamDestroy(capture);
         for (void* p : allocs) (void)hipFree(p);
     }
 };
@@ -262,6 +273,45 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
     return launch_argmax(c, lg, nr, B, cf.vocab, next, md->seq_len, 1, md->cand, stream);
 }
 
+constexpr size_t kGraphMax = 8;
+
+// The recorded decode step for (B, tokens): captured on the model's private
+// stream (nothing runs while recording) and instantiated once.  Every kernel
+// argument is a model buffer, B or tokens, so a replay is the eager step.
+lgx_status step_graph(lgx_model* md, int B, int32_t* tokens, hipGraphExec_t* out) {
+    for (const lgx_model::StepGraph& g : md->graphs)
+        if (g.B == B && g.tokens == tokens) {
+            md->last_nr = g.last_nr;
+            md->last_B = B;
+            *out = g.exec;
+            return LGX_OK;
+        }
+    if (!md->capture) LGX_HIP(hipStreamCreateWithFlags(&md->capture, hipStreamNonBlocking));
+    if (md->graphs.size() >= kGraphMax) {
+        LGX_HIP(hipDeviceSynchronize());   // the oldest recording may still be running
+        (void)hipGraphExecDestroy(md->graphs.front().exec);
+        md->graphs.erase(md->graphs.begin());
+    }
+    LGX_HIP(hipStreamBeginCapture(md->capture, hipStreamCaptureModeThreadLocal));
+    lgx_status st = layers(md, B, tokens, 1, md->capture);
+    if (st == LGX_OK) st = head(md, B, tokens, md->capture);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(md->capture, &graph);
+    if (st != LGX_OK || e != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        if (st != LGX_OK) return st;
+        return fail(LGX_HIP_ERROR, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ei != hipSuccess)
+        return fail(LGX_HIP_ERROR, "hipGraphInstantiate: %s", hipGetErrorString(ei));
+    md->graphs.push_back({B, tokens, md->last_nr, exec});
+    *out = exec;
+    return LGX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -420,6 +470,36 @@ lgx_status lgx_qwen_decode_step(lgx_model* m, int32_t B, int32_t* tokens, void* 
             return fail(LGX_OUT_OF_BOUNDS, "B = %d outside [1, %d]", B, m->c.max_batch);
         if ((st = layers(m, B, tokens, 1, stream)) != LGX_OK) return st;
         return head(m, B, tokens, stream);
+    });
+}
+
+lgx_status lgx_qwen_generate(lgx_model* m, int32_t B, int32_t* tokens, int32_t nsteps,
+                             int32_t* history, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        if (!valid_model(m)) return fail(LGX_INVALID_HANDLE, "invalid lgx_model handle");
+        lgx_status st = enter(m->ctx);
+        if (st != LGX_OK) return st;
+        if (!tokens) return fail(LGX_NULL_POINTER, "NULL tokens");
+        if (B <= 0 || B > m->c.max_batch)
+            return fail(LGX_OUT_OF_BOUNDS, "B = %d outside [1, %d]", B, m->c.max_batch);
+        if (nsteps < 0) return fail(LGX_INVALID_ARGUMENT, "nsteps = %d", nsteps);
+        if (nsteps == 0) return LGX_OK;
+        hipGraphExec_t exec = nullptr;
+        // per-kernel timing attaches events to each dispatch, which a graph
+        // cannot hold: launch those steps eagerly
+        if (!m->ctx->timing && (st = step_graph(m, B, tokens, &exec)) != LGX_OK) return st;
+        for (int s = 0; s < nsteps; ++s) {
+            if (exec) {
+                LGX_HIP(hipGraphLaunch(exec, (hipStream_t)stream));
+            } else if ((st = layers(m, B, tokens, 1, stream)) != LGX_OK ||
+                       (st = head(m, B, tokens, stream)) != LGX_OK) {
+                return st;
+            }
+            if (history)
+                LGX_HIP(hipMemcpyAsync(history + (int64_t)s * B, tokens, (size_t)B * 4,
+                                       hipMemcpyDeviceToDevice, (hipStream_t)stream));
+        }
+        return LGX_OK;
     });
 }
 

@@ -175,3 +175,70 @@ def test_qwen_0_5b_shape_token_identity_64_steps(ctx):
     assert len(np.unique(np.stack(ref_seq))) > 8
     gm.close()
     om.close()
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny_untied"])
+def test_generate_graph_replays_match_eager_and_oracle(name, ctx):
+    """lgx_qwen_generate replays one recorded decode step.  Every replay is
+    checked against the eager step of a second model and the oracle, with
+    eager steps, reads and synchronisations of the same model between the
+    replays; then a multi-step call with history, a second recording for a
+    smaller batch on a side stream, and the argument errors."""
+    from oracle import oracle as orc
+
+    t = ctx.torch
+    cfg = orc.qwen_config(name)
+    seed = 4242
+    B, V = cfg["max_batch"], cfg["vocab"]
+    gg, ge, om = lgx.Model(ctx, cfg, seed), lgx.Model(ctx, cfg, seed), orc.Model(cfg, seed)
+    rng = np.random.default_rng(13)
+    prompt = rng.integers(0, V, size=(B, 3)).astype(np.int32)
+    tg = gg.prefill(ctx.to_device(prompt))
+    te = ge.prefill(ctx.to_device(prompt))
+    for p in range(prompt.shape[1]):
+        ref = om.step(np.arange(B), prompt[:, p])
+    assert np.array_equal(host(tg), ref)
+    for s in range(8):
+        if s % 3 == 2:
+            gg.decode_step(tg)                  # eager work between the replays
+        else:
+            gg.generate(tg, 1)
+        ge.decode_step(te)
+        ref, lg = om.step(np.arange(B), ref, want_logits=True)
+        t.cuda.synchronize()
+        assert np.array_equal(host(tg), ref), f"step {s}"
+        assert np.array_equal(host(te), ref), f"step {s}"
+        assert np.array_equal(bits(host(gg.logits(B))), bits(lg)), f"step {s}"
+    # several replays in one call, with every step's tokens kept
+    hist = t.full((5, B), -1, dtype=t.int32, device=ctx.dev)
+    gg.generate(tg, 5, hist)
+    refs = []
+    for _ in range(5):
+        ref, lg = om.step(np.arange(B), ref, want_logits=True)
+        refs.append(ref)
+    assert np.array_equal(host(hist), np.stack(refs))
+    assert np.array_equal(host(tg), ref)
+    assert np.array_equal(bits(host(gg.logits(B))), bits(lg))
+    # a second recording (smaller batch, other tokens tensor) on a side stream
+    side = t.cuda.Stream(ctx.dev)
+    t1 = tg[:1].clone()
+    side.wait_stream(t.cuda.current_stream(ctx.dev))
+    with t.cuda.stream(side):
+        gg.generate(t1, 2)
+    side.synchronize()
+    r1 = ref[:1]
+    for _ in range(2):
+        r1 = om.step(np.arange(1), r1)
+    assert np.array_equal(host(t1), r1)
+    lens = dev_array(gg, "seq_len", np.int32, (B,))
+    assert [int(x) for x in lens] == [om.seq_len(b) for b in range(B)]
+    assert int(lens[0]) == int(lens[1]) + 2
+    gg.generate(tg, 0)                              # no-op
+    with pytest.raises(lgx.LgxError) as e:
+        gg.generate(tg, -1)
+    assert e.value.status_name == "LGX_INVALID_ARGUMENT"
+    with pytest.raises(lgx.LgxError) as e:
+        gg.generate(ctx.to_device(np.zeros(B + 1, np.int32)), 1)
+    assert e.value.status_name == "LGX_OUT_OF_BOUNDS"
+    for m in (gg, ge, om):
+        m.close()
