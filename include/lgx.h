@@ -217,6 +217,17 @@ lgx_status lgx_swiglu_quant(lgx_ctx* ctx, const float* gu, int32_t m, int32_t in
  * (binary16 tied embedding); h % 64 == 0, h <= 1024. */
 lgx_status lgx_lm_head_f16(lgx_ctx* ctx, const float* x, const uint16_t* emb, int32_t m,
                            int32_t h, int32_t vocab, float* logits, void* stream);
+/* Binary16 rows [rows][h] -> T64 order: 1 KiB units (g, j), lane l of a
+ * unit holding columns [8j, 8j+8) of row 64g + l (zero rows pad the last
+ * group); dst holds lgx_f16_t64_count(rows, h) binary16 values.  h % 8 == 0. */
+int64_t lgx_f16_t64_count(int32_t rows, int32_t h);
+lgx_status lgx_f16_repack_t64(lgx_ctx* ctx, const uint16_t* src, int32_t rows, int32_t h,
+                              uint16_t* dst, void* stream);
+/* lgx_lm_head_f16 over a T64 embedding (same logits, bit for bit): one
+ * whole-1 KiB wave load per 64 rows x 8 columns, activations through the
+ * scalar cache.  h % 64 == 0, h <= 1024, m <= 64. */
+lgx_status lgx_lm_head_f16_t64(lgx_ctx* ctx, const float* x, const uint16_t* emb_t64, int32_t m,
+                               int32_t h, int32_t vocab, float* logits, void* stream);
 /* out[i] = first index of the maximum of logits[i][:], NaN skipped (all NaN
  * gives 0); -0 and +0 compare equal. */
 lgx_status lgx_argmax(lgx_ctx* ctx, const float* logits, int32_t m, int32_t vocab, int32_t* out,

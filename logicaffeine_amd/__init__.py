@@ -68,6 +68,9 @@ SIGNATURES = {
                                      _I32, _I32, _I32, _I32, _P]),
     "lgx_swiglu_quant": (C.c_int, [_P, _P, _I32, _I32, _P, _P, _P, _P]),
     "lgx_lm_head_f16": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _P, _P]),
+    "lgx_f16_t64_count": (C.c_int64, [_I32, _I32]),
+    "lgx_f16_repack_t64": (C.c_int, [_P, _P, _I32, _I32, _P, _P]),
+    "lgx_lm_head_f16_t64": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _P, _P]),
     "lgx_argmax": (C.c_int, [_P, _P, _I32, _I32, _P, _P]),
     "lgx_model_create": (C.c_int, [_P, _P, C.c_uint64, C.POINTER(_P)]),
     "lgx_model_destroy": (C.c_int, [_P]),
@@ -420,6 +423,23 @@ class Context:
         out = t.empty((m, vocab), dtype=t.float32, device=self.dev) if out is None else out
         _check(lib().lgx_lm_head_f16(self.handle, x.data_ptr(), emb.data_ptr(), m, h, vocab,
                                      out.data_ptr(), self._s()))
+        return out
+
+    def f16_repack_t64(self, emb):
+        """binary16 rows (int16/uint16 bits, [rows][h]) -> T64 order (flat)."""
+        t = self.torch
+        rows, h = emb.shape
+        out = t.empty(int(lib().lgx_f16_t64_count(rows, h)), dtype=t.int16, device=self.dev)
+        _check(lib().lgx_f16_repack_t64(self.handle, emb.data_ptr(), rows, h, out.data_ptr(),
+                                        self._s()))
+        return out
+
+    def lm_head_f16_t64(self, x, emb_t64, vocab, out=None):
+        t = self.torch
+        m, h = x.shape
+        out = t.empty((m, vocab), dtype=t.float32, device=self.dev) if out is None else out
+        _check(lib().lgx_lm_head_f16_t64(self.handle, x.data_ptr(), emb_t64.data_ptr(), m, h,
+                                         vocab, out.data_ptr(), self._s()))
         return out
 
     def argmax(self, logits, out=None):

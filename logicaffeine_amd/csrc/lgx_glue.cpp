@@ -132,6 +132,47 @@ lgx_status lgx_lm_head_f16(lgx_ctx* c, const float* x, const uint16_t* emb, int3
     });
 }
 
+int64_t lgx_f16_t64_count(int32_t rows, int32_t h) {
+    if (rows <= 0 || h <= 0) return 0;
+    return (int64_t)((rows + 63) / 64) * 64 * h;
+}
+
+lgx_status lgx_f16_repack_t64(lgx_ctx* c, const uint16_t* src, int32_t rows, int32_t h,
+                              uint16_t* dst, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!src || !dst) return fail(LGX_NULL_POINTER, "NULL src or dst");
+        if (rows <= 0 || h <= 0 || h % 8)
+            return fail(LGX_INVALID_ARGUMENT, "rows %d, h %d (h %% 8 == 0)", rows, h);
+        lgx_t64_args a{src, dst, rows, h};
+        return launch(c, K_REPACK_F16_T64, dim3(cdiv(lgx_f16_t64_count(rows, h) / 8, 256)),
+                      dim3(256), a, stream);
+    });
+}
+
+lgx_status lgx_lm_head_f16_t64(lgx_ctx* c, const float* x, const uint16_t* emb_t64, int32_t m,
+                               int32_t h, int32_t vocab, float* logits, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!x || !emb_t64 || !logits) return fail(LGX_NULL_POINTER, "NULL tensor");
+        if (m <= 0 || m > kLmMaxM || vocab <= 0 || h <= 0 || h % 64 || h > kLmMaxH)
+            return fail(LGX_UNSUPPORTED, "m %d (<= %d), vocab %d, h %d (h %% 64 == 0, h <= %d)",
+                        m, kLmMaxM, vocab, h, kLmMaxH);
+        // the activation in T16 column order, in the workspace
+        const int mc = (m + 15) / 16;
+        float* xt = nullptr;
+        if ((st = ensure_ws(c, (size_t)mc * 16 * h * sizeof(float), &xt)) != LGX_OK) return st;
+        lgx_t64_args ta{x, xt, m, h};
+        if ((st = launch(c, K_ROWS_TO_T16, dim3(cdiv((int64_t)m * h, 256)), dim3(256), ta,
+                         stream)) != LGX_OK)
+            return st;
+        lgx_lmhead_args a{xt, emb_t64, logits, m, h, vocab};
+        return launch(c, K_LM_HEAD_T64, dim3(cdiv(vocab, 64), mc), dim3(64), a, stream);
+    });
+}
+
 lgx_status lgx_argmax(lgx_ctx* c, const float* logits, int32_t m, int32_t vocab, int32_t* out,
                       void* stream) {
     return guarded(__func__, [&]() -> lgx_status {

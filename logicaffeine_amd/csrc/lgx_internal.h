@@ -102,6 +102,9 @@ enum Kern {
     K_GEMV_GRP4,
     K_GEMV_GRP8,
     K_GEMV_GRP16,
+    K_REPACK_F16_T64,
+    K_LM_HEAD_T64,
+    K_ROWS_TO_T16,
     K_COUNT
 };
 inline const char* const kKernelNames[] = {
@@ -121,6 +124,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_lm_head_f16", "lgx_k_argmax_partial", "lgx_k_argmax_final", "lgx_k_advance",
     "lgx_k_q8_gemv_wg4", "lgx_k_q8_gemv_wg8", "lgx_k_q8_gemv_wg16",
     "lgx_k_q8_gemv_grp4", "lgx_k_q8_gemv_grp8", "lgx_k_q8_gemv_grp16",
+    "lgx_k_repack_f16_t64", "lgx_k_lm_head_t64", "lgx_k_rows_to_t16",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,

@@ -115,7 +115,9 @@ typedef struct {
 } lgx_advance_args;
 
 // h += tree(part) (when part != NULL), then y = RMSNorm(h) * w, written as
-// binary32 (xn, nullable) and/or Q8_0 (xq/xd, nullable).
+// binary32 (xn, nullable), binary32 in T16 column order (xt, nullable:
+// xt[((row/16) n + i) 16 + row%16], the lm_head's activation layout) and/or
+// Q8_0 (xq/xd, nullable).
 typedef struct {
     const float* part;     // [nr][m][n] range partials of the residual update
     int32_t nr;
@@ -126,6 +128,7 @@ typedef struct {
     uint16_t* xd;
     int32_t m, n;
     float eps;
+    float* xt;
 } lgx_norm_args;
 
 // qkv = tree(part) (+ bias, nullable); RoPE on the q and k heads at position seq_len[b];
@@ -163,6 +166,14 @@ typedef struct {
     float* logits;         // [m][vocab]
     int32_t m, h, vocab;
 } lgx_lmhead_args;
+
+// Binary16 [rows][h] -> T64 units (lgx_k_repack_f16_t64); binary32
+// [rows][h] -> T16 column order (lgx_k_rows_to_t16, src/dst as floats).
+typedef struct {
+    const void* src;
+    void* dst;
+    int32_t rows, h;
+} lgx_t64_args;
 
 // next[b] = first index of the max of tree(part[.][b][:]) (NaN skipped);
 // then tokens[b] = next[b] and seq_len[b] += advance.  Two launches through

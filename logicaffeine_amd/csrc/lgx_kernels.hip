@@ -1074,20 +1074,52 @@ __device__ __forceinline__ float lgx_expf(float x) {
 //
 // grid = (chunks, B * hkv), 256 threads: one workgroup per (sequence, KV
 // head, chunk) serves all GQ query heads of the group, so every K/V row is
-// read once per group.  Phase 1: thread t owns token t of the chunk and runs
-// the canonical score chain over d for the GQ heads (query rows read as
-// workgroup-uniform values).  Phase 2: per head the chunk max (exact in any
-// order), p_t = lgx_expf(s_t - m), and the halving-tree sum of the 256 slots.
+// read once per group.  Loads: thread t requests its token's whole K row
+// into registers, then the workgroup's direct global->LDS loads
+// (global_load_lds_dwordx4, 1 KiB per wave instruction) bring the chunk's V
+// pages into LDS in token order; both are in flight together and V lands
+// while the scores are computed.  Phase 1: thread t runs the canonical score
+// chain over d for the GQ heads (query rows read as workgroup-uniform
+// values).  Phase 2: per head the chunk max (exact in any order),
+// p_t = lgx_expf(s_t - m), and the halving-tree sum of the 256 slots.
 // Phase 3: thread (i, head group) runs the canonical chain over the chunk's
-// tokens, o[i] = fmaf(p_t, V_t[i], o[i]).  Partials (o_c, m_c, l_c) go to
-// `part`; lgx_k_attn_combine merges the chunks.
+// tokens, o[i] = fmaf(p_t, V_t[i], o[i]), reading V from LDS.  Partials
+// (o_c, m_c, l_c) go to `part`; lgx_k_attn_combine merges the chunks.
+// LDS: 512*D bytes of V + 2 KiB per head.
 // ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+
+// The chunk's V rows (n tokens of KV head g, pages pg_s) into v_s in token
+// order: wave instruction j moves bytes [1024 j, +1024) of the chunk, which
+// lie in page j / (D/32).  Every instruction is issued, so the compiler can
+// count them and wait for the K loads alone before the scores; one for a
+// page past the last token re-reads the chunk's first page (a cache hit)
+// into slots that are never used.
+template <int D>
+__device__ __forceinline__ void attn_stage_v(const lgx_attn_args& a, int g, int n,
+                                             const int* pg_s, uint16_t* v_s, int wave, int lane) {
+    constexpr int PER_PAGE = LGX_PAGE * D * 2 / 1024;   // wave instructions per page
+    constexpr int NJ = LGX_ATTN_CHUNK * D * 2 / 1024;   // per chunk
+#pragma unroll
+    for (int i = 0; i < NJ / 4; ++i) {
+        const int j = wave + 4 * i;
+        const int u = j / PER_PAGE;
+        const int pg = u * LGX_PAGE < n ? pg_s[u] : pg_s[0];
+        const uint16_t* src = a.vpages + ((int64_t)pg * a.hkv + g) * LGX_PAGE * D +
+                              (j - u * PER_PAGE) * 512 + lane * 8;
+        __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(v_s + j * 512), 16, 0, 0);
+    }
+}
+
 template <int D, int GQ>
 __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
     constexpr int C = LGX_ATTN_CHUNK;
-    constexpr int NG = 256 / D;                   // head groups in phase 3
-    constexpr int KH = (GQ + NG - 1) / NG;        // heads per thread in phase 3
-    __shared__ float p_s[GQ][C];
+    // V through LDS at D = 64 (47 KiB with 7 heads: 3 workgroups per CU).
+    // At D = 128 the 64 KiB buffer would leave 2 workgroups per CU, fewer
+    // than the loads need in flight; there V is read from the pages directly.
+    constexpr bool VLDS = D == 64;
+    __shared__ __align__(16) uint16_t v_s[VLDS ? C * D : 8];
+    __shared__ __align__(16) float p_s[GQ][C];
     __shared__ float t_s[GQ][C];
     __shared__ float mx_s[GQ][4];
     __shared__ int pg_s[C / LGX_PAGE];
@@ -1107,19 +1139,36 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
     __syncthreads();
 
     // phase 1: scores.  Thread t owns token t; its whole K row is requested
-    // before the first use so all of its loads are in flight together.
+    // before the first use so all of its loads are in flight together (the
+    // row address is a real page slot for every thread: pg_s is clamped).
     float s[GQ];
 #pragma unroll
     for (int h = 0; h < GQ; ++h) s[h] = 0.0f;
     const bool valid = tid < n;
-    if (valid) {
+    uint4 kv[D / 8];
+    {
         const uint4* kr = (const uint4*)(a.kpages +
                                          (((int64_t)pg_s[tid >> 4] * a.hkv + g) * LGX_PAGE + (tid & 15)) * D);
-        const float* qb = a.q + ((int64_t)b * a.hq + h0) * D;
-        uint4 kv[D / 8];
 #pragma unroll
         for (int j = 0; j < D / 8; ++j) kv[j] = kr[j];
-        __builtin_amdgcn_sched_barrier(0);       // keep every load ahead of the FMAs
+    }
+    if constexpr (VLDS) {
+        // the K row has arrived before V is requested: the compiler waits
+        // for every outstanding load before the first use of any of them
+        // once the LDS loads are in flight, so V's transfer overlaps the
+        // score chain only when it is requested after K is in registers
+#pragma unroll
+        for (int j = 0; j < D / 8; ++j)
+            asm volatile("" : "+v"(kv[j].x), "+v"(kv[j].y), "+v"(kv[j].z), "+v"(kv[j].w));
+        attn_stage_v<D>(a, g, n, pg_s, v_s, wave, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);           // keep every load ahead of the FMAs
+    if (valid) {
+        // workgroup-uniform query rows through the scalar cache (the LDS
+        // loads above would otherwise keep the compiler from proving them
+        // read-only and scalar)
+        const __attribute__((address_space(4))) float* qb =
+            (const __attribute__((address_space(4))) float*)(a.q + ((int64_t)b * a.hq + h0) * D);
 #pragma unroll
         for (int j = 0; j < D / 8; ++j) {
             const float kf[8] = {h2f(kv[j].x & 0xffffu), h2f(kv[j].x >> 16), h2f(kv[j].y & 0xffffu),
@@ -1149,7 +1198,8 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
         p_s[h][tid] = p;
         t_s[h][tid] = p;
     }
-    __syncthreads();
+    if constexpr (VLDS) __builtin_amdgcn_s_waitcnt(0);   // this wave's V loads are in LDS
+    __syncthreads();                             // ... and every other wave's
     if (tid < 128) {
 #pragma unroll
         for (int h = 0; h < GQ; ++h) t_s[h][tid] = t_s[h][tid] + t_s[h][tid + 128];
@@ -1175,9 +1225,9 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
         }
     }
     // phase 3: o_c[i] = chain_t fmaf(p_t, V_t[i], o).  Thread = (dimension
-    // pair, head group): a wave reads whole 2-byte-pair V rows (coalesced),
-    // 16 tokens (one page) of loads in flight before their FMAs.  t is
-    // workgroup-uniform, so the bounds tests do not diverge.
+    // pair, head group) reads its pair of each V row (a wave reads whole
+    // rows: coalesced from the pages, conflict-free from LDS).  n is
+    // workgroup-uniform, so the loop bounds do not diverge.
     constexpr int NP = D / 2;                     // dimension pairs
     constexpr int NHG = 256 / NP;                 // head groups
     constexpr int HPG = (GQ + NHG - 1) / NHG;     // heads per group
@@ -1185,23 +1235,60 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
     float o[HPG][2];
 #pragma unroll
     for (int k = 0; k < HPG; ++k) o[k][0] = o[k][1] = 0.0f;
-    const uint32_t* vb = (const uint32_t*)(a.vpages + (int64_t)g * LGX_PAGE * D) + ip;
-    for (int tp = 0; tp < n; tp += LGX_PAGE) {
-        const uint32_t* vp = vb + (int64_t)pg_s[tp >> 4] * a.hkv * LGX_PAGE * (D / 2);
-        uint32_t vv[LGX_PAGE];
+    if constexpr (VLDS) {
+        // four tokens per step, p as one float4
+        const uint32_t* vs = (const uint32_t*)v_s + ip;
+        int t = 0;
+        for (; t + 4 <= n; t += 4) {
+            uint32_t vv[4];
 #pragma unroll
-        for (int u = 0; u < LGX_PAGE; ++u) vv[u] = tp + u < n ? vp[u * (D / 2)] : 0u;
+            for (int u = 0; u < 4; ++u) vv[u] = vs[(t + u) * NP];
 #pragma unroll
-        for (int u = 0; u < LGX_PAGE; ++u) {
-            if (tp + u < n) {
-                const float v0 = h2f(vv[u] & 0xffffu), v1 = h2f(vv[u] >> 16);
+            for (int k = 0; k < HPG; ++k) {
+                const int h = hg + NHG * k;
+                if (h < GQ) {
+                    const float4 p4 = *(const float4*)&p_s[h][t];
+                    const float pt[4] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
-                for (int k = 0; k < HPG; ++k) {
-                    const int h = hg + NHG * k;
-                    if (h < GQ) {
-                        const float pt = p_s[h][tp + u];
-                        o[k][0] = fmaf(pt, v0, o[k][0]);
-                        o[k][1] = fmaf(pt, v1, o[k][1]);
+                    for (int u = 0; u < 4; ++u) {
+                        o[k][0] = fmaf(pt[u], h2f(vv[u] & 0xffffu), o[k][0]);
+                        o[k][1] = fmaf(pt[u], h2f(vv[u] >> 16), o[k][1]);
+                    }
+                }
+            }
+        }
+        for (; t < n; ++t) {
+            const uint32_t v = vs[t * NP];
+#pragma unroll
+            for (int k = 0; k < HPG; ++k) {
+                const int h = hg + NHG * k;
+                if (h < GQ) {
+                    const float pt = p_s[h][t];
+                    o[k][0] = fmaf(pt, h2f(v & 0xffffu), o[k][0]);
+                    o[k][1] = fmaf(pt, h2f(v >> 16), o[k][1]);
+                }
+            }
+        }
+    } else {
+        // a page (16 tokens) of loads in flight before their FMAs
+        const uint32_t* vb = (const uint32_t*)(a.vpages + (int64_t)g * LGX_PAGE * D) + ip;
+        for (int tp = 0; tp < n; tp += LGX_PAGE) {
+            const uint32_t* vp = vb + (int64_t)pg_s[tp >> 4] * a.hkv * LGX_PAGE * (D / 2);
+            uint32_t vv[LGX_PAGE];
+#pragma unroll
+            for (int u = 0; u < LGX_PAGE; ++u) vv[u] = tp + u < n ? vp[u * (D / 2)] : 0u;
+#pragma unroll
+            for (int u = 0; u < LGX_PAGE; ++u) {
+                if (tp + u < n) {
+                    const float v0 = h2f(vv[u] & 0xffffu), v1 = h2f(vv[u] >> 16);
+#pragma unroll
+                    for (int k = 0; k < HPG; ++k) {
+                        const int h = hg + NHG * k;
+                        if (h < GQ) {
+                            const float pt = p_s[h][tp + u];
+                            o[k][0] = fmaf(pt, v0, o[k][0]);
+                            o[k][1] = fmaf(pt, v1, o[k][1]);
+                        }
                     }
                 }
             }
@@ -1444,6 +1531,7 @@ extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_add_rmsnorm_quan
             const float y = (row[i] * r) * a.w[i];
             row[i] = y;
             if (a.xn) a.xn[(int64_t)b * a.n + i] = y;
+            if (a.xt) a.xt[((int64_t)(b >> 4) * a.n + i) * 16 + (b & 15)] = y;
         }
     }
     if (a.xq) {
@@ -1627,6 +1715,81 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_lm_head_f16(const lgx_lm
 #pragma unroll
     for (int r = 0; r < LGX_LM_MAXM; ++r)
         if (r < a.m) a.logits[(int64_t)r * a.vocab + v] = acc[r];
+}
+
+// Binary16 rows in T64 order: unit (g, j) = 1 KiB, lane l holds columns
+// [8j, 8j+8) of row 64g + l (zero past the last row), so one wave load of a
+// unit is one contiguous 1 KiB request.  out has ceil(rows/64) * (h/8)
+// units; one thread per 16-byte piece.
+extern "C" __global__ __launch_bounds__(256) void lgx_k_repack_f16_t64(const lgx_t64_args a) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int ncg = a.h >> 3;
+    const int64_t total = (int64_t)((a.rows + 63) >> 6) * ncg * 64;
+    if (i >= total) return;
+    const int l = (int)(i & 63);
+    const int64_t u = i >> 6;
+    const int g = (int)(u / ncg), j = (int)(u - (int64_t)g * ncg);
+    const int row = 64 * g + l;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < a.rows) v = *(const uint4*)((const uint16_t*)a.src + (int64_t)row * a.h + 8 * j);
+    ((uint4*)a.dst)[i] = v;
+}
+
+// Binary32 rows [rows][h] -> T16 column order [rows/16][h][16] (the
+// activation layout of lgx_k_lm_head_t64); one thread per element.
+extern "C" __global__ __launch_bounds__(256) void lgx_k_rows_to_t16(const lgx_t64_args a) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)a.rows * a.h) return;
+    const int row = (int)(i / a.h), col = (int)(i - (int64_t)row * a.h);
+    ((float*)a.dst)[((int64_t)(row >> 4) * a.h + col) * 16 + (row & 15)] = ((const float*)a.src)[i];
+}
+
+// Tied binary16 lm_head over T64 rows (h <= 1024: one canonical range, the
+// logit is the sequential fmaf chain over the columns).  One wave per (64
+// vocabulary rows, 16 activation rows): lane l owns vocabulary row 64g + l
+// and keeps 16 chains.  The activation comes in T16 column order, so the 16
+// values of one column are one 64-byte scalar load into SGPRs (wave-uniform,
+// no LDS traffic) feeding 16 independent chains; the binary16 units stream
+// in as whole 1 KiB wave loads, LGX_LMT_PF units ahead.
+#define LGX_LMT_PF 4
+extern "C" __global__ __launch_bounds__(64) void lgx_k_lm_head_t64(const lgx_lmhead_args a) {
+    typedef const __attribute__((address_space(4))) float* cfloat_p;
+    const int g = blockIdx.x, lane = threadIdx.x;
+    const int m0 = blockIdx.y * 16, nm = min(16, a.m - m0);
+    const int ncg = a.h >> 3;
+    const uint4* ep = (const uint4*)a.emb + (int64_t)g * ncg * 64 + lane;
+    const cfloat_p xt = (cfloat_p)(a.x + (int64_t)blockIdx.y * a.h * 16);
+    float acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    // h % 32 == 0 (host check): whole groups of LGX_LMT_PF units, and every
+    // prefetch is issued (the last unit is re-requested at the tail) so the
+    // compiler's wait counts stay exact
+    uint4 e[LGX_LMT_PF];
+#pragma unroll
+    for (int u = 0; u < LGX_LMT_PF; ++u) e[u] = ep[u * 64];
+    for (int j0 = 0; j0 < ncg; j0 += LGX_LMT_PF) {
+#pragma unroll
+        for (int u = 0; u < LGX_LMT_PF; ++u) {
+            const int j = j0 + u;
+            const uint4 cur = e[u];
+            e[u] = ep[min(j + LGX_LMT_PF, ncg - 1) * 64];
+            const float ev[8] = {h2f(cur.x & 0xffffu), h2f(cur.x >> 16), h2f(cur.y & 0xffffu),
+                                 h2f(cur.y >> 16),     h2f(cur.z & 0xffffu), h2f(cur.z >> 16),
+                                 h2f(cur.w & 0xffffu), h2f(cur.w >> 16)};
+            const cfloat_p xc = xt + (int64_t)j * 128;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[r] = fmaf(xc[c * 16 + r], ev[c], acc[r]);
+            }
+        }
+    }
+    const int v = 64 * g + lane;
+    if (v >= a.vocab) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+        if (r < nm) a.logits[(int64_t)(m0 + r) * a.vocab + v] = acc[r];
 }
 
 // Greedy token, in two launches.  Partial: workgroup (slice, row) takes the

@@ -47,6 +47,8 @@ struct lgx_model {
     std::vector<float*> bias;
     std::vector<uint16_t*> kc, vc;
     uint16_t* emb = nullptr;
+    uint16_t* emb_t64 = nullptr;   // tied lm_head: the embedding in T64 order
+    float* xt = nullptr;           // tied lm_head: final-norm rows in T16 column order
     float* ones = nullptr;
     float *cos_t = nullptr, *sin_t = nullptr;
     int32_t* page_table = nullptr;
@@ -156,8 +158,9 @@ lgx_status product(lgx_model* md, const DevQ8& W, int m, void* stream) {
 }
 
 lgx_status norm(lgx_model* md, int m, int n, int nr_part, bool with_part, float* xn, bool q8,
-                void* stream) {
+                void* stream, float* xt = nullptr) {
     lgx_norm_args a{};
+    a.xt = xt;
     a.part = with_part ? md->part : nullptr;
     a.nr = nr_part;
     a.h = md->h;
@@ -249,18 +252,16 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
     const int H = cf.hidden;
     lgx_status st;
     const bool tied = cf.tied_embedding != 0;
-    if ((st = norm(md, B, H, nranges_of(cf.intermediate), true, md->xn, !tied, stream)) != LGX_OK)
+    if ((st = norm(md, B, H, nranges_of(cf.intermediate), true, md->xn, !tied, stream,
+                   tied ? md->xt : nullptr)) != LGX_OK)
         return st;
     const float* lg;
     int nr;
     if (tied) {
-        for (int r0 = 0; r0 < B; r0 += 64) {
-            lgx_lmhead_args la{md->xn + (int64_t)r0 * H, md->emb, md->logits + (int64_t)r0 * cf.vocab,
-                               std::min(64, B - r0), H, cf.vocab};
-            if ((st = launch(c, K_LM_HEAD_F16, dim3(cdiv(cf.vocab, 256)), dim3(256), la, stream)) !=
-                LGX_OK)
-                return st;
-        }
+        lgx_lmhead_args la{md->xt, md->emb_t64, md->logits, B, H, cf.vocab};
+        if ((st = launch(c, K_LM_HEAD_T64, dim3(cdiv(cf.vocab, 64), cdiv(B, 16)), dim3(64), la,
+                         stream)) != LGX_OK)
+            return st;
         lg = md->logits;
         nr = 1;
     } else {
@@ -385,6 +386,16 @@ lgx_status lgx_model_create(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t see
             lgxg::gen_normal_f16(seed, 1, cf.emb_sigma, he.data(), (int64_t)he.size());
             if ((st = dev_alloc(m, &m->emb, he.size())) != LGX_OK) return done(st);
             LGX_HIP(hipMemcpy(m->emb, he.data(), he.size() * 2, hipMemcpyHostToDevice));
+        }
+        if (cf.tied_embedding) {
+            const int64_t nt = lgx_f16_t64_count(cf.vocab, H);
+            if ((st = dev_alloc(m, &m->emb_t64, (size_t)nt)) != LGX_OK ||
+                (st = dev_alloc(m, &m->xt, (size_t)cdiv(B, 16) * 16 * H)) != LGX_OK)
+                return done(st);
+            lgx_t64_args ta{m->emb, m->emb_t64, cf.vocab, H};
+            if ((st = launch(c, K_REPACK_F16_T64, dim3(cdiv(nt / 8, 256)), dim3(256), ta, nullptr)) !=
+                LGX_OK)
+                return done(st);
         }
         {
             const int mx = std::max(H, I);

@@ -115,6 +115,30 @@ def test_lm_head_f16_bit_exact(ctx, orc, m, h, vocab):
     assert np.array_equal(bits(out), bits(orc.lm_head_f16(x, E)))
 
 
+@pytest.mark.parametrize("m,h,vocab", [(1, 64, 300), (5, 256, 1000), (17, 896, 2048),
+                                       (64, 1024, 4160), (32, 896, 151936)])
+def test_lm_head_f16_t64_bit_exact(ctx, orc, m, h, vocab):
+    """The T64 path (repacked embedding, activations in SGPRs) gives the
+    oracle's logits bit for bit, including a ragged last row group and a
+    partial last group of 16 activation rows."""
+    rng = np.random.default_rng(m + h + vocab)
+    x = rng.standard_normal((m, h)).astype(np.float32)
+    E = orc.f32_to_f16((rng.standard_normal((vocab, h)) * 0.02).astype(np.float32))
+    Et = ctx.f16_repack_t64(ctx.to_device(E))
+    # the documented layout: unit (g, j), lane l = columns [8j, 8j+8) of row 64g + l
+    g = -(-vocab // 64)
+    Ep = np.zeros((g * 64, h), np.uint16)
+    Ep[:vocab] = E
+    want = Ep.reshape(g, 64, h // 8, 8).transpose(0, 2, 1, 3).reshape(-1)
+    assert np.array_equal(host(Et).view(np.uint16), want)
+    out = host(ctx.lm_head_f16_t64(ctx.to_device(x), Et, vocab))
+    if vocab > 4096:                             # the oracle chain on a row sample
+        rows = np.unique(np.r_[rng.integers(0, vocab, 3000), 0, vocab - 1])
+        assert np.array_equal(bits(out[:, rows]), bits(orc.lm_head_f16(x, E[rows])))
+    else:
+        assert np.array_equal(bits(out), bits(orc.lm_head_f16(x, E)))
+
+
 def test_lm_head_one_hot_selects_embedding_column(ctx, orc):
     rng = np.random.default_rng(3)
     h, vocab = 128, 512
@@ -153,6 +177,10 @@ def test_glue_argument_errors(ctx):
     with pytest.raises(lgx.LgxError) as e:
         ctx.lm_head_f16(t.zeros((1, 1088), dtype=t.float32, device=ctx.dev),
                         t.zeros((4, 1088), dtype=t.int16, device=ctx.dev))
+    assert e.value.status_name == "LGX_UNSUPPORTED"
+    with pytest.raises(lgx.LgxError) as e:          # m > 64 on the T64 path
+        ctx.lm_head_f16_t64(t.zeros((65, 64), dtype=t.float32, device=ctx.dev),
+                            t.zeros(64 * 64, dtype=t.int16, device=ctx.dev), 64)
     assert e.value.status_name == "LGX_UNSUPPORTED"
     with pytest.raises(lgx.LgxError):
         ctx.rmsnorm_quant(t.zeros((1, 8224), dtype=t.float32, device=ctx.dev), x[0], 1e-6)
