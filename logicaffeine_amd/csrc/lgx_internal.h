@@ -105,6 +105,9 @@ enum Kern {
     K_REPACK_F16_T64,
     K_LM_HEAD_T64,
     K_ROWS_TO_T16,
+    K_GEMV_GRPQ4,
+    K_GEMV_GRPQ8,
+    K_GEMV_GRPQ16,
     K_COUNT
 };
 inline const char* const kKernelNames[] = {
@@ -125,6 +128,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_q8_gemv_wg4", "lgx_k_q8_gemv_wg8", "lgx_k_q8_gemv_wg16",
     "lgx_k_q8_gemv_grp4", "lgx_k_q8_gemv_grp8", "lgx_k_q8_gemv_grp16",
     "lgx_k_repack_f16_t64", "lgx_k_lm_head_t64", "lgx_k_rows_to_t16",
+    "lgx_k_q8_gemv_grpq4", "lgx_k_q8_gemv_grpq8", "lgx_k_q8_gemv_grpq16",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -410,8 +414,12 @@ inline lgx_status run_gemv_group(lgx_ctx* c, const lgx_gemv_mat* mats, int count
         return launch(c, k, dim3(wgs), dim3(64 * W), ga, stream, (unsigned)lds);
     }
     int nrmax = 1;
-    for (int i = 0; i < count; ++i)
+    const bool xf = mats[0].xf != nullptr;
+    for (int i = 0; i < count; ++i) {
         nrmax = std::max(nrmax, (mats[i].k / 32 + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS);
+        if ((mats[i].xf != nullptr) != xf)
+            return fail(LGX_INVALID_ARGUMENT, "a group mixes binary32 and Q8_0 activations");
+    }
     int W = nrmax <= 4 ? 4 : nrmax <= 8 ? 8 : 16;
     if (c->gemv_wgs == 4 || c->gemv_wgs == 8 || c->gemv_wgs == 16) W = c->gemv_wgs;
     for (int i = 0; i < count; ++i) {
@@ -423,7 +431,8 @@ inline lgx_status run_gemv_group(lgx_ctx* c, const lgx_gemv_mat* mats, int count
         lds = std::max(lds, (size_t)mats[i].k + 4 * (size_t)nb + 64 * (size_t)tpw * nr);
     }
     ga.tile0[count] = wgs;
-    const Kern k = W == 16 ? K_GEMV_GRP16 : W == 8 ? K_GEMV_GRP8 : K_GEMV_GRP4;
+    const Kern k = xf ? (W == 16 ? K_GEMV_GRP16 : W == 8 ? K_GEMV_GRP8 : K_GEMV_GRP4)
+                      : (W == 16 ? K_GEMV_GRPQ16 : W == 8 ? K_GEMV_GRPQ8 : K_GEMV_GRPQ4);
     return launch(c, k, dim3(wgs), dim3(64 * W), ga, stream, (unsigned)lds);
 }
 

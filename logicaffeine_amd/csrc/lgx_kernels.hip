@@ -684,55 +684,84 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_mfma_qx(const lg
 // lgx_k_quantize_q8_0 rule, or copied) is staged in LDS in (pair, chunk)
 // order.  LDS (dynamic): k bytes, k/32 scales, tpw x ranges x 16 chains.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void grp_stage(const lgx_gemv_mat& a, int8_t* xs, float* dxs,
-                                          bool emit) {
+// The activation loads are issued before the weight loads: the hardware
+// counts loads in issue order, so waiting for the activation then does not
+// also wait for the weights, and the range math can start as soon as each
+// weight unit arrives.  Every load is issued (addresses clamped), which keeps
+// the compiler's wait counts exact.  GRP_XB 16-byte slots per thread cover
+// k <= 8 * GRP_XB * threads (binary32) or k <= 16 * threads (Q8_0); the rest
+// (rows longer than the workgroup's range count) goes through a loop.
+#define GRP_XB 3
+template <bool XF>
+__device__ __forceinline__ void grp_x_issue(const lgx_gemv_mat& a, uint4 (&xr)[GRP_XB]) {
     const int nb = a.k >> 5, np = a.k >> 6, tid = threadIdx.x, nt = blockDim.x;
-    if (a.xf) {
-        // 8 lanes per block, whole groups; two blocks' loads in flight per lane
-#pragma unroll 1
-        for (int s0 = tid; s0 < nb * 8; s0 += 2 * nt) {
-            float4 v[2];
+    if constexpr (XF) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int s2 = s0 + u * nt;
-                if (s2 < nb * 8) v[u] = *(const float4*)(a.xf + (s2 >> 3) * 32 + 4 * (s2 & 7));
-            }
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int s2 = s0 + u * nt;
-                if (s2 < nb * 8) {                 // all 8 lanes of a block or none
-                    const int bl = s2 >> 3, j = s2 & 7;
-                    const float f[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-                    uint16_t dh;
-                    const uint32_t qw = quantize4(f, dh);
-                    *(uint32_t*)(xs + ((bl >> 1) * 4 + (j >> 1)) * 16 + (bl & 1) * 8 + 4 * (j & 1)) = qw;
-                    if (j == 0) dxs[bl] = h2f(dh);
-                    if (emit && a.xq_out) {
-                        *(uint32_t*)(a.xq_out + bl * 32 + 4 * j) = qw;
-                        if (j == 0) a.xd_out[bl] = dh;
-                    }
-                }
-            }
+        for (int u = 0; u < GRP_XB; ++u) {
+            const int sl = min(tid + u * nt, nb * 8 - 1);
+            xr[u] = *(const uint4*)(a.xf + (sl >> 3) * 32 + 4 * (sl & 7));
         }
     } else {
-        for (int s2 = tid; s2 < 4 * np; s2 += nt) {
+        const int s2 = min(tid, 4 * np - 1);
+        const int8_t* src = a.xq + (s2 >> 2) * 64 + 8 * (s2 & 3);
+        const uint2 lo = *(const uint2*)src;
+        const uint2 hi = *(const uint2*)(src + 32);
+        xr[0] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        xr[1].x = a.xd[min(tid, nb - 1)];
+    }
+}
+
+// Q8_0 of the 32-block slot sl (8 lanes per block, whole groups) into the
+// LDS staging in (pair, chunk) order (+ the optional Q8_0 outputs).
+__device__ __forceinline__ void grp_quant_slot(const lgx_gemv_mat& a, int sl, const uint4& v,
+                                               int8_t* xs, float* dxs, bool emit) {
+    const int bl = sl >> 3, j = sl & 7;
+    const float f[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
+                        __uint_as_float(v.w)};
+    uint16_t dh;
+    const uint32_t qw = quantize4(f, dh);
+    *(uint32_t*)(xs + ((bl >> 1) * 4 + (j >> 1)) * 16 + (bl & 1) * 8 + 4 * (j & 1)) = qw;
+    if (j == 0) dxs[bl] = h2f(dh);
+    if (emit && a.xq_out) {
+        *(uint32_t*)(a.xq_out + bl * 32 + 4 * j) = qw;
+        if (j == 0) a.xd_out[bl] = dh;
+    }
+}
+
+template <bool XF>
+__device__ __forceinline__ void grp_x_finish(const lgx_gemv_mat& a, int8_t* xs, float* dxs,
+                                             bool emit, const uint4 (&xr)[GRP_XB]) {
+    const int nb = a.k >> 5, np = a.k >> 6, tid = threadIdx.x, nt = blockDim.x;
+    if constexpr (XF) {
+#pragma unroll
+        for (int u = 0; u < GRP_XB; ++u) {
+            const int sl = tid + u * nt;
+            if (sl < nb * 8) grp_quant_slot(a, sl, xr[u], xs, dxs, emit);   // whole groups
+        }
+#pragma unroll 1
+        for (int sl = tid + GRP_XB * nt; sl < nb * 8; sl += nt)
+            grp_quant_slot(a, sl, *(const uint4*)(a.xf + (sl >> 3) * 32 + 4 * (sl & 7)), xs, dxs,
+                           emit);
+    } else {
+        if (tid < 4 * np) *(uint4*)(xs + tid * 16) = xr[0];
+        if (tid < nb) dxs[tid] = h2f(xr[1].x);
+        for (int s2 = tid + nt; s2 < 4 * np; s2 += nt) {
             const int8_t* src = a.xq + (s2 >> 2) * 64 + 8 * (s2 & 3);
             const uint2 lo = *(const uint2*)src;
             const uint2 hi = *(const uint2*)(src + 32);
             *(uint4*)(xs + s2 * 16) = make_uint4(lo.x, lo.y, hi.x, hi.y);
         }
-        for (int b = tid; b < nb; b += nt) dxs[b] = h2f(a.xd[b]);
+        for (int b = tid + nt; b < nb; b += nt) dxs[b] = h2f(a.xd[b]);
     }
 }
 
 // One wave's range: loads (issued by grp_issue) -> MFMA -> canonical chain.
+// Scales first, then the 16 weight units (clamped to the range's last pair),
+// so unit i's math waits only for the loads issued up to it.
 __device__ __forceinline__ void grp_issue(const lgx_gemv_mat& a, int t, const RangeInfo& ri,
-                                          int lane, uint4 (&w)[16], uint32_t (&dw)[16]) {
+                                          int lane, uint4 (&w)[16], uint32_t (&dw)[16],
+                                          bool idle = false) {
     const int np = a.k >> 6, nh = s16_nhalf(a.k), r = lane & 15;
-    const uint4* wp = (const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64 + lane;
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-        if (i < ri.npairs) w[i] = ld_stream(wp + i * 64);
     uint32_t d0[8], d1[8];
     load_scales_half(a.wd, t, 2 * ri.g, nh, r, d0);
     load_scales_half(a.wd, t, min(2 * ri.g + 1, nh - 1), nh, r, d1);
@@ -741,6 +770,12 @@ __device__ __forceinline__ void grp_issue(const lgx_gemv_mat& a, int t, const Ra
         dw[i] = d0[i];
         dw[8 + i] = d1[i];
     }
+    __builtin_amdgcn_sched_barrier(0);            // issue order: scales, then weights
+    const uint4* wp = (const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64 + lane;
+    const int last = idle ? 0 : ri.npairs - 1;    // an idle wave re-reads one unit
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = ld_stream(wp + min(i, last) * 64);
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 __device__ __forceinline__ float grp_range(const lgx_gemv_mat& a, int t, const RangeInfo& ri,
@@ -756,27 +791,27 @@ __device__ __forceinline__ float grp_range(const lgx_gemv_mat& a, int t, const R
             const uint4 xv = *(const uint4*)(xs + (p * 4 + c) * 16);
             const long a0 = (long)(((uint64_t)xv.y << 32) | xv.x);
             const long a1 = (long)(((uint64_t)xv.w << 32) | xv.z);
-            long b0 = (long)(((uint64_t)w[i].y << 32) | w[i].x);
-            long b1 = (long)(((uint64_t)w[i].w << 32) | w[i].z);
-            // unit i's MFMAs after unit i-1's chain step: one unit live at a time
-            asm volatile("" : "+v"(b0), "+v"(b1));
+            const long b0 = (long)(((uint64_t)w[i].y << 32) | w[i].x);
+            const long b1 = (long)(((uint64_t)w[i].w << 32) | w[i].z);
             const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, zero, 0, 0, 0);
             const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, zero, 0, 0, 0);
             const float e0 = h2f(dw[i] & 0xffffu) * dxs[2 * p];
             const float e1 = h2f(dw[i] >> 16) * dxs[2 * p + 1];
             acc = fmaf((float)d0[0], e0, acc);
             acc = fmaf((float)d1[0], e1, acc);
-            asm volatile("" : "+v"(acc));
             if (a.dbg && c == 0) {
                 a.dbg[(int64_t)(t * 16 + r) * nb + 2 * p] = d0[0];
                 a.dbg[(int64_t)(t * 16 + r) * nb + 2 * p + 1] = d1[0];
             }
         }
+        // unit i's MFMAs stay after unit i-1's chain step: one unit live at a
+        // time, each waiting only for its own weights
+        __builtin_amdgcn_sched_barrier(0);
     }
     return acc;
 }
 
-template <int W>
+template <int W, bool XF>
 __device__ __forceinline__ void q8_gemv_grp_body(const lgx_gemv_group_args& ga) {
     extern __shared__ __align__(16) uint8_t lds_dyn[];
     const int bx = blockIdx.x;
@@ -792,17 +827,23 @@ __device__ __forceinline__ void q8_gemv_grp_body(const lgx_gemv_group_args& ga) 
     int8_t* xs = (int8_t*)lds_dyn;                 // k bytes, (pair, chunk) order
     float* dxs = (float*)(lds_dyn + k);            // nb
     float* ps = dxs + nb;                          // [tpw][nr][16]
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int ts = wave / nrs, rg = wave - ts * nrs;
     const int t = tile_base + ts;
     const bool on = ts < tpw && t < ntiles;
 
     uint4 w[16];
     uint32_t dw[16];
+    uint4 xr[GRP_XB];
     const RangeInfo ri = range_info(rg, k);
-    if (on) grp_issue(a, t, ri, lane, w, dw);
-    grp_stage(a, xs, dxs, bx == ga.tile0[g]);
+    grp_x_issue<XF>(a, xr);
+    __builtin_amdgcn_sched_barrier(0);            // activation loads first
+    // every wave issues its loads (an idle wave re-reads one unit of the
+    // first tile, a cache hit), so no branch hides them from the wait counts
+    grp_issue(a, on ? t : min(tile_base, ntiles - 1), ri, lane, w, dw, !on);
+    grp_x_finish<XF>(a, xs, dxs, bx == ga.tile0[g], xr);
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
     if (on) {
         float acc = grp_range(a, t, ri, lane, xs, dxs, w, dw);
         if (lane < 16) {
@@ -837,14 +878,25 @@ __device__ __forceinline__ void q8_gemv_grp_body(const lgx_gemv_group_args& ga) 
     }
 }
 
+// binary32 activations (quantised in the prologue) ...
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_grp4(const lgx_gemv_group_args a) {
-    q8_gemv_grp_body<4>(a);
+    q8_gemv_grp_body<4, true>(a);
 }
 extern "C" __global__ __launch_bounds__(512) void lgx_k_q8_gemv_grp8(const lgx_gemv_group_args a) {
-    q8_gemv_grp_body<8>(a);
+    q8_gemv_grp_body<8, true>(a);
 }
 extern "C" __global__ __launch_bounds__(1024) void lgx_k_q8_gemv_grp16(const lgx_gemv_group_args a) {
-    q8_gemv_grp_body<16>(a);
+    q8_gemv_grp_body<16, true>(a);
+}
+// ... and Q8_0 activations (copied)
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_grpq4(const lgx_gemv_group_args a) {
+    q8_gemv_grp_body<4, false>(a);
+}
+extern "C" __global__ __launch_bounds__(512) void lgx_k_q8_gemv_grpq8(const lgx_gemv_group_args a) {
+    q8_gemv_grp_body<8, false>(a);
+}
+extern "C" __global__ __launch_bounds__(1024) void lgx_k_q8_gemv_grpq16(const lgx_gemv_group_args a) {
+    q8_gemv_grp_body<16, false>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -1078,16 +1130,17 @@ __device__ __forceinline__ float lgx_expf(float x) {
 // into registers, then the workgroup's direct global->LDS loads
 // (global_load_lds_dwordx4, 1 KiB per wave instruction) bring the chunk's V
 // pages into LDS in token order; both are in flight together and V lands
-// while the scores are computed.  Phase 1: thread t runs the canonical score
-// chain over d for the GQ heads (query rows read as workgroup-uniform
-// values).  Phase 2: per head the chunk max (exact in any order),
-// p_t = lgx_expf(s_t - m), and the halving-tree sum of the 256 slots.
-// Phase 3: thread (i, head group) runs the canonical chain over the chunk's
-// tokens, o[i] = fmaf(p_t, V_t[i], o[i]), reading V from LDS.  Partials
-// (o_c, m_c, l_c) go to `part`; lgx_k_attn_combine merges the chunks.
-// LDS: 512*D bytes of V + 2 KiB per head.
+// while the scores are computed (D = 64; at D = 128 V is streamed in phase
+// 3).  Phase 1: thread t runs the canonical score chain over d for the GQ
+// heads (query rows read as workgroup-uniform values).  Phase 2: per head
+// the chunk max (exact in any order), p_t = lgx_expf(s_t - m), and the
+// halving-tree sum of the 256 slots.  Phase 3: the canonical chain over the
+// chunk's tokens, o[i] = fmaf(p_t, V_t[i], o[i]), for every (head, i).
+// Partials (o_c, m_c, l_c) go to `part`; lgx_k_attn_combine merges the
+// chunks.  LDS: 2 KiB per head (+ 32 KiB of V at D = 64).
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
+#define LGX_PV_VB 8
 
 // The chunk's V rows (n tokens of KV head g, pages pg_s) into v_s in token
 // order: wave instruction j moves bytes [1024 j, +1024) of the chunk, which
@@ -1224,10 +1277,11 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
             }
         }
     }
-    // phase 3: o_c[i] = chain_t fmaf(p_t, V_t[i], o).  Thread = (dimension
-    // pair, head group) reads its pair of each V row (a wave reads whole
-    // rows: coalesced from the pages, conflict-free from LDS).  n is
-    // workgroup-uniform, so the loop bounds do not diverge.
+    // phase 3: o_c[i] = chain_t fmaf(p_t, V_t[i], o).  D = 64: thread =
+    // (dimension pair, head group) reads its pair of each V row from LDS (a
+    // wave reads whole rows, conflict-free).  D = 128: one wave streams the
+    // V rows from the pages (below).  n is workgroup-uniform, so the loop
+    // bounds do not diverge.
     constexpr int NP = D / 2;                     // dimension pairs
     constexpr int NHG = 256 / NP;                 // head groups
     constexpr int HPG = (GQ + NHG - 1) / NHG;     // heads per group
@@ -1270,29 +1324,62 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
             }
         }
     } else {
-        // a page (16 tokens) of loads in flight before their FMAs
-        const uint32_t* vb = (const uint32_t*)(a.vpages + (int64_t)g * LGX_PAGE * D) + ip;
-        for (int tp = 0; tp < n; tp += LGX_PAGE) {
-            const uint32_t* vp = vb + (int64_t)pg_s[tp >> 4] * a.hkv * LGX_PAGE * (D / 2);
-            uint32_t vv[LGX_PAGE];
+        // One wave: lane = (dimension octet j, head slot hs), chains of heads
+        // hs and hs + 4 for 8 dimensions; each token's V row is one 16-byte
+        // load per lane (the four head slots share it), two batches of
+        // LGX_PV_VB tokens in flight.  The other waves are done.
+        constexpr int VB = LGX_PV_VB;
+        static_assert(D == 128 && GQ <= 8, "single-wave PV covers 128 dimensions, 8 heads");
+        if (wave != 0) return;
+        const int j = lane & 15, hs = lane >> 4;
+        const int hh[2] = {hs, hs + 4};
+        float acc[2][8];
 #pragma unroll
-            for (int u = 0; u < LGX_PAGE; ++u) vv[u] = tp + u < n ? vp[u * (D / 2)] : 0u;
+        for (int k = 0; k < 2; ++k)
 #pragma unroll
-            for (int u = 0; u < LGX_PAGE; ++u) {
+            for (int e = 0; e < 8; ++e) acc[k][e] = 0.0f;
+        const uint16_t* vbase = a.vpages + (int64_t)g * LGX_PAGE * D + 8 * j;
+        // token t's row (clamped to the last token: always a real page slot)
+        auto ld = [&](int tp, uint4 (&vv)[VB]) {
+#pragma unroll
+            for (int u = 0; u < VB; ++u) {
+                const int t = min(tp + u, n - 1);
+                vv[u] = *(const uint4*)(vbase + ((int64_t)pg_s[t >> 4] * a.hkv * LGX_PAGE + (t & 15)) * D);
+            }
+        };
+        auto use = [&](int tp, const uint4 (&vv)[VB]) {
+#pragma unroll
+            for (int u = 0; u < VB; ++u) {
                 if (tp + u < n) {
-                    const float v0 = h2f(vv[u] & 0xffffu), v1 = h2f(vv[u] >> 16);
+                    const float ve[8] = {h2f(vv[u].x & 0xffffu), h2f(vv[u].x >> 16), h2f(vv[u].y & 0xffffu),
+                                         h2f(vv[u].y >> 16),     h2f(vv[u].z & 0xffffu), h2f(vv[u].z >> 16),
+                                         h2f(vv[u].w & 0xffffu), h2f(vv[u].w >> 16)};
 #pragma unroll
-                    for (int k = 0; k < HPG; ++k) {
-                        const int h = hg + NHG * k;
-                        if (h < GQ) {
-                            const float pt = p_s[h][tp + u];
-                            o[k][0] = fmaf(pt, v0, o[k][0]);
-                            o[k][1] = fmaf(pt, v1, o[k][1]);
-                        }
+                    for (int k = 0; k < 2; ++k) {
+                        const float pt = p_s[min(hh[k], GQ - 1)][tp + u];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc[k][e] = fmaf(pt, ve[e], acc[k][e]);
                     }
                 }
             }
+        };
+        uint4 va[VB], vb2[VB];
+        ld(0, va);
+        for (int tp = 0; tp < n; tp += 2 * VB) {
+            ld(tp + VB, vb2);
+            use(tp, va);
+            ld(tp + 2 * VB, va);
+            use(tp + VB, vb2);
         }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            if (hh[k] < GQ) {
+                float* pp = a.part + (((int64_t)b * a.hq + h0 + hh[k]) * a.nchunk + c) * (D + 2) + 8 * j;
+                *(float4*)pp = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+                *(float4*)(pp + 4) = make_float4(acc[k][4], acc[k][5], acc[k][6], acc[k][7]);
+            }
+        }
+        return;
     }
 #pragma unroll
     for (int k = 0; k < HPG; ++k) {
