@@ -198,6 +198,12 @@ lgx_status lgx_embed_f16(lgx_ctx* ctx, const uint16_t* emb, const int32_t* token
  * Q8_0 (xq, xd: the lgx_quantize_q8_0 rule) are written.  n <= 8192. */
 lgx_status lgx_rmsnorm_quant(lgx_ctx* ctx, const float* x, const float* w, int32_t m, int32_t n,
                              float eps, float* y, int8_t* xq, uint16_t* xd, void* stream);
+/* The decode step's residual form: h[m][n] += pairwise tree over the nr
+ * range partials part[nr][m][n] (the output of lgx_q8_gemm_partials), h is
+ * written back, then lgx_rmsnorm_quant of the new h.  nr <= 32. */
+lgx_status lgx_add_rmsnorm_quant(lgx_ctx* ctx, const float* part, int32_t nr, float* h,
+                                 const float* w, int32_t m, int32_t n, float eps, float* y,
+                                 int8_t* xq, uint16_t* xd, void* stream);
 /* For each sequence b: r = qkv[b] (+ bias) with rows q heads | k heads |
  * v heads; rotate-half RoPE at position p = seq_len[b] on the q and k heads
  * (pairs (i, i + d/2), cos/sin from the tables [max_seq][d/2]); q -> q_out

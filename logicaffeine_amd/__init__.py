@@ -64,6 +64,8 @@ SIGNATURES = {
                                       _I32, _I32, _P, _P]),
     "lgx_embed_f16": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _P, _P]),
     "lgx_rmsnorm_quant": (C.c_int, [_P, _P, _P, _I32, _I32, C.c_float, _P, _P, _P, _P]),
+    "lgx_add_rmsnorm_quant": (C.c_int, [_P, _P, _I32, _P, _P, _I32, _I32, C.c_float, _P, _P, _P,
+                                        _P]),
     "lgx_rope_kv_append": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                      _I32, _I32, _I32, _I32, _P]),
     "lgx_swiglu_quant": (C.c_int, [_P, _P, _I32, _I32, _P, _P, _P, _P]),
@@ -390,6 +392,18 @@ class Context:
         _check(lib().lgx_rmsnorm_quant(self.handle, x.data_ptr(), w.data_ptr(), m, n, eps,
                                        _ptr_or_none(yo), _ptr_or_none(xq), _ptr_or_none(xd),
                                        self._s()))
+        return yo, xq, xd
+
+    def add_rmsnorm_quant(self, part, h, w, eps: float, y: bool = True, q8: bool = True):
+        """h += tree(part) in place; then (y, xq, xd) of RMSNorm(h) * w."""
+        t = self.torch
+        nr, m, n = part.shape
+        yo = t.empty((m, n), dtype=t.float32, device=self.dev) if y else None
+        xq = t.empty((m, n), dtype=t.int8, device=self.dev) if q8 else None
+        xd = t.empty((m, n // 32), dtype=t.int16, device=self.dev) if q8 else None
+        _check(lib().lgx_add_rmsnorm_quant(self.handle, part.data_ptr(), nr, h.data_ptr(),
+                                           w.data_ptr(), m, n, eps, _ptr_or_none(yo),
+                                           _ptr_or_none(xq), _ptr_or_none(xd), self._s()))
         return yo, xq, xd
 
     def rope_kv_append(self, qkv, bias, cos_t, sin_t, seq_len, page_table, kpages, vpages,

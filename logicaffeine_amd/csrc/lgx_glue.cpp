@@ -52,7 +52,36 @@ lgx_status lgx_rmsnorm_quant(lgx_ctx* c, const float* x, const float* w, int32_t
         a.m = m;
         a.n = n;
         a.eps = eps;
-        return launch(c, K_ADD_RMSNORM_QUANT, dim3(m), dim3(LGX_GLUE_NT), a, stream);
+        return launch_norm(c, a, stream);
+    });
+}
+
+lgx_status lgx_add_rmsnorm_quant(lgx_ctx* c, const float* part, int32_t nr, float* h,
+                                 const float* w, int32_t m, int32_t n, float eps, float* y,
+                                 int8_t* xq, uint16_t* xd, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!part || !h || !w) return fail(LGX_NULL_POINTER, "NULL part, h or w");
+        if (!y && !xq) return fail(LGX_NULL_POINTER, "no output (y and xq are NULL)");
+        if ((xq == nullptr) != (xd == nullptr)) return fail(LGX_NULL_POINTER, "xq and xd go together");
+        if (m <= 0 || n <= 0 || n > kNormMax)
+            return fail(LGX_INVALID_ARGUMENT, "m %d, n %d (n <= %d)", m, n, kNormMax);
+        if (nr <= 0 || nr > LGX_MAX_RANGES)
+            return fail(LGX_INVALID_ARGUMENT, "nr %d outside [1, %d]", nr, LGX_MAX_RANGES);
+        if (xq && n % 32) return fail(LGX_INVALID_ARGUMENT, "Q8_0 output needs n %% 32 == 0");
+        lgx_norm_args a{};
+        a.part = part;
+        a.nr = nr;
+        a.h = h;
+        a.w = w;
+        a.xn = y;
+        a.xq = xq;
+        a.xd = xd;
+        a.m = m;
+        a.n = n;
+        a.eps = eps;
+        return launch_norm(c, a, stream);
     });
 }
 

@@ -108,6 +108,8 @@ enum Kern {
     K_GEMV_GRPQ4,
     K_GEMV_GRPQ8,
     K_GEMV_GRPQ16,
+    K_NORM4_R8,
+    K_NORM4_R20,
     K_COUNT
 };
 inline const char* const kKernelNames[] = {
@@ -129,6 +131,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_q8_gemv_grp4", "lgx_k_q8_gemv_grp8", "lgx_k_q8_gemv_grp16",
     "lgx_k_repack_f16_t64", "lgx_k_lm_head_t64", "lgx_k_rows_to_t16",
     "lgx_k_q8_gemv_grpq4", "lgx_k_q8_gemv_grpq8", "lgx_k_q8_gemv_grpq16",
+    "lgx_k_add_rmsnorm_quant4_r8", "lgx_k_add_rmsnorm_quant4_r20",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -253,6 +256,15 @@ inline lgx_status ensure_ws(lgx_ctx* c, size_t bytes, float** out) {
 }
 
 inline unsigned cdiv(int64_t a, int64_t b);
+
+// Residual + RMSNorm (+ Q8_0) of a.m rows: the float4-slot kernels where the
+// row fits them (n % 4 == 0, n <= 4096, nr <= 20), else the general one.
+inline lgx_status launch_norm(lgx_ctx* c, const lgx_norm_args& a, void* stream) {
+    const int nr = a.part ? a.nr : 1;
+    if (a.n % 4 == 0 && a.n <= 4096 && nr <= 20)
+        return launch(c, nr <= 8 ? K_NORM4_R8 : K_NORM4_R20, dim3(a.m), dim3(512), a, stream, 0u);
+    return launch(c, K_ADD_RMSNORM_QUANT, dim3(a.m), dim3(LGX_GLUE_NT), a, stream, 0u);
+}
 inline int argmax_slices(int vocab) { return (vocab + LGX_ARGMAX_SLICE - 1) / LGX_ARGMAX_SLICE; }
 
 // Greedy token of m rows of (range-partial) logits: candidates per slice,

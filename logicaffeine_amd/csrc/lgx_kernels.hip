@@ -1540,49 +1540,126 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_embed(const lgx_embed_ar
     for (int i = threadIdx.x; i < a.n; i += 256) a.h[(int64_t)b * a.n + i] = h2f(er[i]);
 }
 
-// Residual combine + RMSNorm (+ Q8_0).  One workgroup of 1024 threads per
-// row; n <= 8192.  Sum of squares: halving tree over the next power of two
-// >= n (zero padded), levels of stride >= 1024 inside each thread (thread t
-// owns slots t + 1024k), then across threads (LDS, then wave shuffles) --
-// the oracle's order, whatever the thread count.
+// The canonical pairwise tree over nr (<= R) values, evaluated as they
+// arrive in index order: after value j the pending subtrees are the set bits
+// of j + 1 (L[k] holds one of 2^k values), merged earlier + later as in the
+// level-by-level tree; at the end the pending subtrees fold from the
+// smallest (latest) up: T = L[hi] + (... + L[lo]).  j is a compile-time
+// constant in the unrolled loop, so every L index is static.
+__device__ __forceinline__ float4 add4(const float4& x, const float4& y) {
+    return make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+}
+template <int R>
+__device__ __forceinline__ float4 tree_stream4(const float4 (&p)[R], int nr) {
+    float4 L[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) L[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        if (j < nr) {
+            float4 v = p[j];
+            int k = 0;
+#pragma unroll
+            for (; k < 5; ++k) {
+                if (!((j >> k) & 1)) break;
+                v = add4(L[k], v);
+            }
+            L[k] = v;
+        }
+    }
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    bool have = false;
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        if ((nr >> k) & 1) {
+            acc = have ? add4(L[k], acc) : L[k];
+            have = true;
+        }
+    }
+    return acc;
+}
+
+// Residual combine + RMSNorm (+ Q8_0).  One workgroup of NT threads per row;
+// n <= 8192.  Residual: h += tree of the nr range partials (when part is
+// set).  S > 0: thread t owns the float4 slots t + NT k (k < S; n % 4 == 0,
+// n <= 4 NT S, nr <= R) and requests h and every partial of them at once,
+// one round of memory latency; S == 0: thread t owns elements t + NT k,
+// partials two elements at a time.  Sum of squares: halving tree over the
+// next power of two >= n (zero padded), levels of stride >= NT inside each
+// thread (thread t owns slots t + NT k), then across threads (LDS, then wave
+// shuffles) -- the oracle's order, whatever the thread count.
 #define LGX_NORM_MAX 8192
-extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_add_rmsnorm_quant(const lgx_norm_args a) {
-    constexpr int NT = LGX_GLUE_NT, KV = LGX_NORM_MAX / NT;
-    __shared__ float row[LGX_NORM_MAX];
+template <int NT, int S, int R>
+__device__ __forceinline__ void norm_body(const lgx_norm_args& a) {
+    constexpr int KV = LGX_NORM_MAX / NT;
+    __shared__ __align__(16) float row[LGX_NORM_MAX];
     __shared__ float red[NT];
     const int b = blockIdx.x, t = threadIdx.x;
     float* hr = a.h + (int64_t)b * a.n;
     bool on[KV];
-    float upd[KV];
 #pragma unroll
-    for (int k = 0; k < KV; ++k) {
-        on[k] = t + NT * k < a.n;
-        upd[k] = 0.0f;
-    }
-    if (a.part) {
-        // two elements per round: 2 x nr loads in flight, bounded registers
+    for (int k = 0; k < KV; ++k) on[k] = t + NT * k < a.n;
+    float v[KV];
+    if constexpr (S > 0) {
+        const int n4 = a.n >> 2;
+        float4 x4[S];
 #pragma unroll
-        for (int k = 0; k < KV; k += 2) {
-            if (on[k]) {
-                const bool o2[2] = {on[k], on[k + 1]};
-                float u2[2];
-                tree_partials_n<2, LGX_MAX_RANGES>(a.part, a.nr, (int64_t)a.m * a.n,
-                                                   (int64_t)b * a.n + t + NT * k, NT, o2, u2);
-                upd[k] = u2[0];
-                upd[k + 1] = u2[1];
+        for (int k = 0; k < S; ++k)
+            x4[k] = *(const float4*)(hr + 4 * min(t + NT * k, n4 - 1));
+        if (a.part) {
+            // every load issued (range index clamped), consumed in order
+            float4 pv[S][R];
+            const int64_t stride = (int64_t)a.m * a.n;
+            const float* pb = a.part + (int64_t)b * a.n;
+#pragma unroll
+            for (int j = 0; j < R; ++j)
+#pragma unroll
+                for (int k = 0; k < S; ++k)
+                    pv[k][j] = *(const float4*)(pb + min(j, a.nr - 1) * stride +
+                                                4 * min(t + NT * k, n4 - 1));
+#pragma unroll
+            for (int k = 0; k < S; ++k) {
+                x4[k] = add4(x4[k], tree_stream4<R>(pv[k], a.nr));
+                if (t + NT * k < n4) *(float4*)(hr + 4 * (t + NT * k)) = x4[k];
             }
         }
-    }
-    float v[KV];
 #pragma unroll
-    for (int k = 0; k < KV; ++k) {
-        float x = on[k] ? hr[t + NT * k] : 0.0f;
-        if (a.part && on[k]) {
-            x = x + upd[k];
-            hr[t + NT * k] = x;
+        for (int k = 0; k < S; ++k)
+            if (t + NT * k < n4) *(float4*)(row + 4 * (t + NT * k)) = x4[k];
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < KV; ++k) {
+            const float x = on[k] ? row[t + NT * k] : 0.0f;
+            v[k] = x * x;                          // zero past n
         }
-        if (on[k]) row[t + NT * k] = x;
-        v[k] = x * x;                              // zero past n
+    } else {
+        float upd[KV];
+#pragma unroll
+        for (int k = 0; k < KV; ++k) upd[k] = 0.0f;
+        if (a.part) {
+            // two elements per round: 2 x nr loads in flight, bounded registers
+#pragma unroll
+            for (int k = 0; k < KV; k += 2) {
+                if (on[k]) {
+                    const bool o2[2] = {on[k], on[k + 1]};
+                    float u2[2];
+                    tree_partials_n<2, LGX_MAX_RANGES>(a.part, a.nr, (int64_t)a.m * a.n,
+                                                       (int64_t)b * a.n + t + NT * k, NT, o2, u2);
+                    upd[k] = u2[0];
+                    upd[k + 1] = u2[1];
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < KV; ++k) {
+            float x = on[k] ? hr[t + NT * k] : 0.0f;
+            if (a.part && on[k]) {
+                x = x + upd[k];
+                hr[t + NT * k] = x;
+            }
+            if (on[k]) row[t + NT * k] = x;
+            v[k] = x * x;                          // zero past n
+        }
     }
     int n2 = NT;
     while (n2 < a.n) n2 <<= 1;
@@ -1600,14 +1677,14 @@ extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_add_rmsnorm_quan
         if (t < sl) red[t] = red[t] + red[t + sl];
         __syncthreads();
     }
-    float S = 0.0f;
+    float Ssq = 0.0f;
     if (t < 64) {
-        S = red[t];
+        Ssq = red[t];
 #pragma unroll
-        for (int sl = 32; sl >= 1; sl >>= 1) S = S + __shfl_down(S, sl, 64);
+        for (int sl = 32; sl >= 1; sl >>= 1) Ssq = Ssq + __shfl_down(Ssq, sl, 64);
     }
     __syncthreads();
-    if (t == 0) red[0] = S;
+    if (t == 0) red[0] = Ssq;
     __syncthreads();
     const float ms = red[0] / (float)a.n;
     const float r = 1.0f / sqrtf(ms + a.eps);
@@ -1625,6 +1702,17 @@ extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_add_rmsnorm_quan
         __syncthreads();
         quantize_row_from_lds<NT>(row, a.n, a.xq + (int64_t)b * a.n, a.xd + (int64_t)b * (a.n / 32));
     }
+}
+
+extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_add_rmsnorm_quant(const lgx_norm_args a) {
+    norm_body<LGX_GLUE_NT, 0, 1>(a);
+}
+// n % 4 == 0, n <= 4096: 512 threads, two float4 slots each, nr <= 8 / 20
+extern "C" __global__ __launch_bounds__(512) void lgx_k_add_rmsnorm_quant4_r8(const lgx_norm_args a) {
+    norm_body<512, 2, 8>(a);
+}
+extern "C" __global__ __launch_bounds__(512) void lgx_k_add_rmsnorm_quant4_r20(const lgx_norm_args a) {
+    norm_body<512, 2, 20>(a);
 }
 
 // QKV combine + bias + RoPE + paged KV append.  One workgroup of 1024

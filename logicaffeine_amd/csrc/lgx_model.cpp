@@ -171,7 +171,7 @@ lgx_status norm(lgx_model* md, int m, int n, int nr_part, bool with_part, float*
     a.m = m;
     a.n = n;
     a.eps = md->c.rms_eps;
-    return launch(md->ctx, K_ADD_RMSNORM_QUANT, dim3(m), dim3(LGX_GLUE_NT), a, stream);
+    return launch_norm(md->ctx, a, stream);
 }
 
 // One token per sequence 0..B-1 through every layer; leaves the down

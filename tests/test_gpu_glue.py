@@ -49,6 +49,40 @@ def test_rmsnorm_quant_bit_exact(ctx, orc, m, n):
         assert np.array_equal(host(xd2).view(np.uint16), rd)
 
 
+def _tree_rows(part):
+    """Canonical pairwise tree over axis 0 of part[nr][m][n] (oracle)."""
+    from oracle import oracle as orc
+
+    nr, m, n = part.shape
+    flat = part.reshape(nr, -1)
+    return np.array([orc.tree_sum(flat[:, i].copy()) for i in range(flat.shape[1])],
+                    np.float32).reshape(m, n)
+
+
+@pytest.mark.parametrize("m,n,nr", [(3, 896, 1), (4, 896, 5), (2, 3584, 4), (5, 3584, 19),
+                                    (2, 4096, 8), (2, 4096, 20), (2, 3584, 21), (1, 8192, 32),
+                                    (2, 1000, 9), (1, 4096, 13)])
+def test_add_rmsnorm_quant_bit_exact(ctx, orc, m, n, nr):
+    """Residual form: h += tree of the range partials (the float4-slot
+    kernels for n % 4 == 0, n <= 4096, nr <= 20; the general kernel past
+    those), written back, then the RMSNorm + Q8_0 of the new h."""
+    rng = np.random.default_rng(m * 7 + n + nr)
+    part = rng.standard_normal((nr, m, n)).astype(np.float32)
+    h = (rng.standard_normal((m, n)) * 3).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, size=n).astype(np.float32)
+    hd = ctx.to_device(h)
+    q8 = n % 32 == 0
+    y, xq, xd = ctx.add_rmsnorm_quant(ctx.to_device(part), hd, ctx.to_device(w), 1e-6, q8=q8)
+    h_ref = (h + _tree_rows(part)).astype(np.float32)
+    assert np.array_equal(bits(host(hd)), bits(h_ref))
+    ref = orc.rmsnorm(h_ref, w, 1e-6)
+    assert np.array_equal(bits(host(y)), bits(ref))
+    if q8:
+        rq, rd = orc.quantize_q8_0(ref)
+        assert np.array_equal(host(xq), rq)
+        assert np.array_equal(host(xd).view(np.uint16), rd)
+
+
 @pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (28, 4, 128), (12, 2, 128), (4, 4, 64)])
 def test_rope_kv_append_bit_exact(ctx, orc, hq, hkv, d):
     rng = np.random.default_rng(hq * 1000 + d)
