@@ -944,14 +944,18 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
         const int pair0 = PB * qb;                 // first pair of the batch
         const int hh = min(2 * ri.g + pair0 / 8, nh - 1);
         const uint4* sp = (const uint4*)(a.wd + (((int64_t)t * nh + hh) * 16 + r) * 16);
-        // 8 pairs (16 scales) per 32-byte row: a PB-pair batch is PB words
-        // starting at word pair0 % 8
-        uint32_t row[8];
-        const uint4 lo = sp[0], hi = sp[1];
-        row[0] = lo.x; row[1] = lo.y; row[2] = lo.z; row[3] = lo.w;
-        row[4] = hi.x; row[5] = hi.y; row[6] = hi.z; row[7] = hi.w;
+        // 8 pairs (16 scales) per 32-byte row: a PB-pair batch (PB = 4 or 8,
+        // pair0 a multiple of PB) is the PB words from word pair0 % 8, i.e.
+        // PB / 4 whole 16-byte pieces
+        static_assert(PB == 4 || PB == 8, "scale words come in 16-byte pieces");
 #pragma unroll
-        for (int i = 0; i < PB; ++i) dw[i] = row[(pair0 % 8) + i];
+        for (int v = 0; v < PB / 4; ++v) {
+            const uint4 q = sp[(pair0 % 8) / 4 + v];
+            dw[4 * v] = q.x;
+            dw[4 * v + 1] = q.y;
+            dw[4 * v + 2] = q.z;
+            dw[4 * v + 3] = q.w;
+        }
     };
     float acc[MT][4];
     auto compute_batch = [&](int qb, const uint4 (&w)[PB], const uint32_t (&dw)[PB]) {
@@ -1007,8 +1011,8 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
         }
     };
 
-    uint4 wn[PB];
-    uint32_t dn[PB];
+    uint4 wn[PB], wn2[PB];
+    uint32_t dn[PB], dn2[PB];
     load_batch(0, 0, wn, dn);
     // stage the activation range: every load of a thread is requested before
     // the first LDS store (one L2 round trip, not one per slot)
@@ -1046,16 +1050,9 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
     // batches of the range that hold pairs (the last range may be short)
     const int nbq = min(NB, (ri.npairs + PB - 1) / PB);
     const int nbat = nbq * a.tpw;
-#pragma unroll 1
-    for (int q = 0; q < nbat; ++q) {
-        uint4 w[PB];
-        uint32_t dw[PB];
-#pragma unroll
-        for (int i = 0; i < PB; ++i) {
-            w[i] = wn[i];
-            dw[i] = dn[i];
-        }
-        if (q + 1 < nbat) load_batch((q + 1) / nbq, (q + 1) % nbq, wn, dn);
+    // batch q of the wave's stream: zero the chains at a tile's first batch,
+    // store them after its last
+    auto run_batch = [&](int q, const uint4 (&w)[PB], const uint32_t (&dw)[PB]) {
         const int qb = q % nbq;
         if (qb == 0) {
 #pragma unroll
@@ -1065,6 +1062,16 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
         }
         compute_batch(qb, w, dw);
         if (qb == nbq - 1) store_tile(q / nbq);
+    };
+    // two buffers in turn (no register copies): batch q + 1 is requested
+    // before batch q is consumed
+#pragma unroll 1
+    for (int q = 0; q < nbat; q += 2) {
+        if (q + 1 < nbat) load_batch((q + 1) / nbq, (q + 1) % nbq, wn2, dn2);
+        run_batch(q, wn, dn);
+        if (q + 1 >= nbat) break;
+        if (q + 2 < nbat) load_batch((q + 2) / nbq, (q + 2) % nbq, wn, dn);
+        run_batch(q + 1, wn2, dn2);
     }
 }
 
