@@ -17,7 +17,9 @@ events attached to its own dispatch (lgx_ctx_set_kernel_timing) on its
 stream, in a separate pass over the same steps.  Launches are queued behind a
 device-side sleep before the timed region opens, so the step time is the
 device's, not the Python loop's.  The M sweep (1, 8, 32, 64) is reported
-alongside.  `cpu_baseline` times the CPU oracle (a port: the reference has no
+alongside, with its int8 MFMA utilisation (the M x N x K block-dot work
+against the dense int8 peak): at these M the products are HBM- and
+epilogue-bound, far from the MFMA roofline.  `cpu_baseline` times the CPU oracle (a port: the reference has no
 CPU implementation of this path) on a bounded sample of the same step.
 
 The decode part (BASELINE.json configs 3 and 4) builds the seeded
@@ -40,6 +42,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+INT8_MFMA_PEAK_TOPS = 5000.0   # dense int8 MFMA, MI355X datasheet
 DOMINANT = ("lgx_k_q8_gemv_grp4", "lgx_k_q8_gemv_grp8", "lgx_k_q8_gemv_grp16")
 DOMINANT_USED = DOMINANT[2]
 # HBM bytes per dispatch of the grouped config-1 launch, from rocprofv3 --pmc
@@ -371,9 +374,13 @@ def main():
     sweep = {}
     for m in (1, 8, 32, 64):
         ms = ms1_plain if m == 1 else time_m(ctx, torch, sets, m, args.steps, args.warmup)[0]
+        # int8 MFMA work of the step: the M x N x K block dots (2 ops per MAC)
+        tops = 2.0 * m * sum(n * k for _, n, k in SHAPES) / (ms * 1e-3) / 1e12
         sweep[str(m)] = {"ms_per_step": round(ms, 5),
                          "GB_s": round(step_bytes(m) / (ms * 1e-3) / 1e9, 1),
-                         "tokens_s": round(m / (ms * 1e-3), 1)}
+                         "tokens_s": round(m / (ms * 1e-3), 1),
+                         "int8_TOPS": round(tops, 2),
+                         "mfma_util": round(tops / INT8_MFMA_PEAK_TOPS, 5)}
         print(f"[bench] M={m}: {ms * 1e3:.1f} us/step {sweep[str(m)]['GB_s']} GB/s",
               file=sys.stderr, flush=True)
 
