@@ -171,6 +171,19 @@ lgx_status lgx_gqa_decode_attn(lgx_ctx* ctx, const float* q, const uint16_t* kpa
                                int32_t d, int32_t maxp, int32_t num_pages, int32_t max_seq_len,
                                float* out, void* stream);
 
+/* Causal attention of a prefill chunk: B sequences with P new query rows
+ * each.  Row b*P + j of q ([B*P][hq][d]) is the query at position
+ * seq_len[b] + j, whose K/V rows are already cached; it attends to the first
+ * seq_len[b] + j + 1 tokens of sequence b (clamped to max_seq_len).  Each row
+ * runs the decode schedule above, so its output equals lgx_gqa_decode_attn
+ * of that row at length seq_len[b] + j + 1.  out: [B*P][hq][d].  Replaces no
+ * reference interface: the reference has no attention. */
+lgx_status lgx_gqa_prefill_attn(lgx_ctx* ctx, const float* q, const uint16_t* kpages,
+                                const uint16_t* vpages, const int32_t* page_table,
+                                const int32_t* seq_len, int32_t B, int32_t P, int32_t hq,
+                                int32_t hkv, int32_t d, int32_t maxp, int32_t num_pages,
+                                int32_t max_seq_len, float* out, void* stream);
+
 /* ---- range partials (for consumers that fuse the range tree) ---- */
 /* Number of canonical 32-block ranges of K = the partial count of a product. */
 int32_t lgx_q8_range_count(int32_t k);

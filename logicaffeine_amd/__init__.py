@@ -62,6 +62,8 @@ SIGNATURES = {
     "lgx_q8_range_combine": (C.c_int, [_P, _P, _I32, C.c_int64, _P, _P]),
     "lgx_gqa_decode_attn": (C.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32,
                                       _I32, _I32, _P, _P]),
+    "lgx_gqa_prefill_attn": (C.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32,
+                                       _I32, _I32, _I32, _P, _P]),
     "lgx_embed_f16": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _P, _P]),
     "lgx_rmsnorm_quant": (C.c_int, [_P, _P, _P, _I32, _I32, C.c_float, _P, _P, _P, _P]),
     "lgx_add_rmsnorm_quant": (C.c_int, [_P, _P, _I32, _P, _P, _I32, _I32, C.c_float, _P, _P, _P,
@@ -362,6 +364,24 @@ class Context:
                                          vpages.data_ptr(), page_table.data_ptr(),
                                          seq_len.data_ptr(), B, hq, hkv, d, maxp, num_pages,
                                          max_seq_len, out.data_ptr(), self._s()))
+        return out
+
+    def gqa_prefill_attn(self, q, kpages, vpages, page_table, seq_len, P: int, max_seq_len: int,
+                         out=None):
+        """q [B*P][hq][d] f32: row b*P + j is the query at position seq_len[b] + j
+        (causal over the first seq_len[b] + j + 1 cached tokens)."""
+        t = self.torch
+        rows, hq, d = q.shape
+        B = seq_len.numel()
+        if rows != B * P:
+            raise ValueError(f"q has {rows} rows, expected B*P = {B * P}")
+        num_pages, hkv = kpages.shape[0], kpages.shape[1]
+        maxp = page_table.shape[1]
+        out = t.empty((rows, hq, d), dtype=t.float32, device=self.dev) if out is None else out
+        _check(lib().lgx_gqa_prefill_attn(self.handle, q.data_ptr(), kpages.data_ptr(),
+                                          vpages.data_ptr(), page_table.data_ptr(),
+                                          seq_len.data_ptr(), B, P, hq, hkv, d, maxp, num_pages,
+                                          max_seq_len, out.data_ptr(), self._s()))
         return out
 
     def q8_gemm(self, W: Q8Matrix, xq, xd, y=None):

@@ -25,7 +25,7 @@ lgx_status lgx_embed_f16(lgx_ctx* c, const uint16_t* emb, const int32_t* tokens,
         if (!emb || !tokens || !out) return fail(LGX_NULL_POINTER, "NULL tensor");
         if (m <= 0 || h <= 0 || vocab <= 0)
             return fail(LGX_INVALID_ARGUMENT, "m %d, h %d, vocab %d", m, h, vocab);
-        lgx_embed_args a{emb, tokens, out, m, h, vocab, 1};
+        lgx_embed_args a{emb, tokens, out, m, h, vocab, 1, 1};
         return launch(c, K_EMBED, dim3(m), dim3(256), a, stream);
     });
 }

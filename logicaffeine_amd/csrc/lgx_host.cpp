@@ -63,6 +63,10 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
         c->gemv_whole = gv && std::string(gv) == "whole";
         c->gemv_wgs = env_int("LGX_GEMV_WGS", 0);
         c->gemm_mt = env_int("LGX_GEMM_MT", 0);
+        c->tiled_min = env_int("LGX_GEMM_TILED_MIN", 128);
+        const char* pfv = getenv("LGX_PREFILL");
+        c->prefill_serial = pfv && std::string(pfv) == "serial";
+        c->prefill_chunk = env_int("LGX_PREFILL_CHUNK", 0);
         int ncu = 0;
         if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) ==
                 hipSuccess &&
@@ -364,6 +368,51 @@ lgx_status lgx_gqa_decode_attn(lgx_ctx* c, const float* q, const uint16_t* kpage
     });
 }
 
+lgx_status lgx_gqa_prefill_attn(lgx_ctx* c, const float* q, const uint16_t* kpages,
+                                const uint16_t* vpages, const int32_t* page_table,
+                                const int32_t* seq_len, int32_t B, int32_t P, int32_t hq,
+                                int32_t hkv, int32_t d, int32_t maxp, int32_t num_pages,
+                                int32_t max_seq_len, float* out, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!q || !kpages || !vpages || !page_table || !seq_len || !out)
+            return fail(LGX_NULL_POINTER, "NULL tensor pointer");
+        if (B <= 0 || P <= 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0 || maxp <= 0 || num_pages <= 0)
+            return fail(LGX_INVALID_ARGUMENT, "B=%d P=%d hq=%d hkv=%d maxp=%d num_pages=%d", B, P, hq,
+                        hkv, maxp, num_pages);
+        if ((d != 64 && d != 128) || prefill_attn_kernel(d, hq / hkv) < 0)
+            return fail(LGX_UNSUPPORTED, "head_dim %d / %d query heads per KV head", d, hq / hkv);
+        if (max_seq_len <= 0 || max_seq_len > maxp * LGX_PAGE)
+            return fail(LGX_OUT_OF_BOUNDS, "max_seq_len %d outside (0, %d]", max_seq_len,
+                        maxp * LGX_PAGE);
+        if ((int64_t)B * P * hq > INT32_MAX) return fail(LGX_OUT_OF_BOUNDS, "B*P*hq too large");
+        lgx_attn_args a{};
+        a.q = q;
+        a.kpages = kpages;
+        a.vpages = vpages;
+        a.page_table = page_table;
+        a.seq_len = seq_len;
+        a.out = out;
+        a.B = B;
+        a.hq = hq;
+        a.hkv = hkv;
+        a.maxp = maxp;
+        a.num_pages = num_pages;
+        a.maxlen = max_seq_len;
+        a.nchunk = (max_seq_len + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
+        a.ncg = a.nchunk;
+        a.len_add = 1;
+        a.qpr = P;
+        a.scale = (float)(1.0 / std::sqrt((double)d));
+        st = ensure_ws(c, (size_t)B * P * hq * a.nchunk * (d + 2) * sizeof(float), &a.part);
+        if (st != LGX_OK) return st;
+        if ((st = launch_prefill_attn(c, a, d, stream)) != LGX_OK) return st;
+        return launch(c, d == 64 ? K_ATTN_COMBINE_D64 : K_ATTN_COMBINE_D128, dim3(B * P * hq), dim3(d),
+                      a, stream);
+    });
+}
+
 lgx_status lgx_q8_gemm(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq, const uint16_t* xd,
                        int32_t m, float* y, void* stream) {
     return guarded(__func__, [&]() -> lgx_status {
@@ -375,6 +424,22 @@ lgx_status lgx_q8_gemm(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq, con
         if (m == 1 && use_wg(c, W)) {
             lgx_gemv_mat g = gemv_mat(W, nullptr, xq, xd, y, 0);
             return run_gemv_group(c, &g, 1, stream);
+        }
+        if (m >= c->tiled_min) {
+            // T16 copy of the activations, then the group partials (straight
+            // into y when K is one group) and the tree over the groups
+            const int ng = tiled_groups(W->k);
+            const size_t xbytes = ((size_t)cdiv(m, 16) * 16 * W->k + 255) / 256 * 256;
+            float* ws = nullptr;
+            if ((st = ensure_ws(c, xbytes + (ng > 1 ? (size_t)ng * m * W->n * 4 : 0), &ws)) != LGX_OK)
+                return st;
+            int8_t* xt = (int8_t*)ws;
+            float* part = ng > 1 ? (float*)((char*)ws + xbytes) : y;
+            if ((st = act_to_t16(c, xq, m, W->k, xt, stream)) != LGX_OK ||
+                (st = run_q8_tiled(c, W, xt, xd, m, part, stream)) != LGX_OK || ng == 1)
+                return st;
+            lgx_combine_args ca{part, y, (int64_t)m * W->n, ng};
+            return launch(c, K_COMBINE, dim3(cdiv(ca.count, 256)), dim3(256), ca, stream);
         }
         return run_q8(c, gemm_kernel(c, m), W, nullptr, xq, xd, m, y, nullptr, stream);
     });

@@ -110,7 +110,11 @@ enum Kern {
     K_GEMV_GRPQ16,
     K_NORM4_R8,
     K_NORM4_R20,
-    K_COUNT
+    K_ACT_T16,
+    K_GEMM_TILED,
+    K_PFA_D64_G1,    // + (gq - 1)
+    K_PFA_D128_G1 = K_PFA_D64_G1 + 8,
+    K_COUNT = K_PFA_D128_G1 + 8
 };
 inline const char* const kKernelNames[] = {
     "lgx_k_repack_t16", "lgx_k_quantize_q8_0", "lgx_k_q8q8_gemv",
@@ -132,6 +136,13 @@ inline const char* const kKernelNames[] = {
     "lgx_k_repack_f16_t64", "lgx_k_lm_head_t64", "lgx_k_rows_to_t16",
     "lgx_k_q8_gemv_grpq4", "lgx_k_q8_gemv_grpq8", "lgx_k_q8_gemv_grpq16",
     "lgx_k_add_rmsnorm_quant4_r8", "lgx_k_add_rmsnorm_quant4_r20",
+    "lgx_k_act_to_t16", "lgx_k_q8_gemm_tiled",
+    "lgx_k_attn_prefill_d64_g1", "lgx_k_attn_prefill_d64_g2", "lgx_k_attn_prefill_d64_g3",
+    "lgx_k_attn_prefill_d64_g4", "lgx_k_attn_prefill_d64_g5", "lgx_k_attn_prefill_d64_g6",
+    "lgx_k_attn_prefill_d64_g7", "lgx_k_attn_prefill_d64_g8",
+    "lgx_k_attn_prefill_d128_g1", "lgx_k_attn_prefill_d128_g2", "lgx_k_attn_prefill_d128_g3",
+    "lgx_k_attn_prefill_d128_g4", "lgx_k_attn_prefill_d128_g5", "lgx_k_attn_prefill_d128_g6",
+    "lgx_k_attn_prefill_d128_g7", "lgx_k_attn_prefill_d128_g8",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -143,6 +154,11 @@ inline int attn_kernel(int d, int gq) {
     return (d == 64 ? K_ATTN_D64_G1 : K_ATTN_D128_G1) + gq - 1;
 }
 
+// Prefill (multi-query causal) attention kernel for head_dim d, gq heads per KV head.
+inline int prefill_attn_kernel(int d, int gq) {
+    if (gq < 1 || gq > 8) return -1;
+    return (d == 64 ? K_PFA_D64_G1 : K_PFA_D128_G1) + gq - 1;
+}
 // Debug/tuning knobs read once per ctx (documented in DESIGN.md):
 //   LGX_GEMV=dot4   route lgx_q8q8_gemv to the v_dot4 GEMV instead of MFMA
 //   LGX_WG_TARGET=n workgroups the streaming kernels aim for (default 512)
@@ -164,6 +180,9 @@ struct lgx_ctx {
     int gemv_wgs = 0;             // LGX_GEMV_WGS: M = 1 GEMV waves per workgroup (0: auto)
     bool gemv_whole = false;      // LGX_GEMV=whole: block dots through LDS, chains after
     int gemm_mt = 0;              // LGX_GEMM_MT: force the M > 1 m-tile width (0: by m)
+    int tiled_min = 128;          // LGX_GEMM_TILED_MIN: smallest m through the tiled product
+    bool prefill_serial = false;  // LGX_PREFILL=serial: prefill as P decode passes
+    int prefill_chunk = 0;        // LGX_PREFILL_CHUNK: positions per prefill chunk (0: by batch)
     int ncu = 256;                // compute units of the device
     int wg_target = 512;
     std::atomic<uint64_t> launches{0};
@@ -350,6 +369,45 @@ inline lgx_status run_q8(lgx_ctx* c, Kern kern, const lgx_q8_matrix* W, const fl
     if (st != LGX_OK || a.nranges == 1 || part_out) return st;
     lgx_combine_args ca{a.part, y, (int64_t)m * W->n, a.nranges};
     return launch(c, K_COMBINE, dim3(cdiv(ca.count, 256)), dim3(256), ca, stream);
+}
+
+// Large-M product: activations in T16 tiles (ceil(m/16) of them), group
+// partials part[tiled_groups(k)][m][n] (canonical subtrees of 4 ranges).
+inline int tiled_groups(int k) { return (nranges_of(k) + LGX_TG_RANGES - 1) / LGX_TG_RANGES; }
+inline lgx_status run_q8_tiled(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xt,
+                               const uint16_t* xd, int m, float* part, void* stream) {
+    lgx_gemm_tiled_args a{};
+    a.wt = W->qs;
+    a.wd = W->d;
+    a.xt = xt;
+    a.xd = xd;
+    a.part = part;
+    a.n = W->n;
+    a.k = W->k;
+    a.m = m;
+    a.ngroups = tiled_groups(W->k);
+    a.ntn = (int)cdiv(W->n, LGX_TG_N);
+    a.ntm = (int)cdiv(m, LGX_TG_M);
+    const int64_t wgs = (int64_t)a.ntn * a.ntm * a.ngroups;
+    if (wgs > INT32_MAX) return fail(LGX_OUT_OF_BOUNDS, "tiled product of %lld workgroups", (long long)wgs);
+    return launch(c, K_GEMM_TILED, dim3((unsigned)wgs), dim3(256), a, stream);
+}
+
+// Launch of the prefill attention over B sequences x a.qpr query rows:
+// one workgroup per (sequence, KV head, chunk of the grid, block of 4 rows).
+inline lgx_status launch_prefill_attn(lgx_ctx* c, const lgx_attn_args& a, int d, void* stream) {
+    const int k = prefill_attn_kernel(d, a.hq / a.hkv);
+    const int64_t wgs = (int64_t)a.B * a.hkv * a.ncg * ((std::max(a.qpr, 1) + 3) / 4);
+    if (k < 0 || wgs > INT32_MAX) return fail(LGX_UNSUPPORTED, "prefill attention shape");
+    if (wgs == 0) return LGX_OK;
+    return launch(c, (Kern)k, dim3((unsigned)wgs), dim3(512), a, stream);
+}
+
+// Row-major int8 activations [m][k] -> T16 tiles at dst (ceil(m/16)*16*k bytes).
+inline lgx_status act_to_t16(lgx_ctx* c, const int8_t* xq, int m, int k, int8_t* dst, void* stream) {
+    lgx_act_t16_args a{xq, dst, m, k};
+    const int64_t slots = (int64_t)cdiv(m, 16) * (k / 64) * 64;
+    return launch(c, K_ACT_T16, dim3(cdiv(slots, 256)), dim3(256), a, stream);
 }
 
 }  // namespace lgxi

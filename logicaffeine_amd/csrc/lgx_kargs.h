@@ -95,6 +95,12 @@ typedef struct {
     float scale;
     int8_t* xq;                // combine+quantise variant: Q8_0 of out rows [B][hq*d]
     uint16_t* xd;
+    // prefill (several queries per sequence): row r = b * qpr + j is the query
+    // at position seq_len[b] + j, attending to seq_len[b] + j + len_add
+    // tokens; B counts sequences, the q / part / out rows are B * qpr.  0 or
+    // 1: one query per sequence (decode).
+    int32_t qpr;
+    int32_t ncg;               // prefill: chunks covered by the grid
 } lgx_attn_args;
 
 #define LGX_PAGE 16
@@ -103,9 +109,10 @@ typedef struct {
 // ---- decode-step glue ----
 typedef struct {
     const uint16_t* emb;   // [vocab][n] binary16
-    const int32_t* tokens; // token of row b at tokens[b * tokens_stride]
+    const int32_t* tokens; // token of row r = b * qpr + j at tokens[b * tokens_stride + j]
     float* h;              // [m][n]
     int32_t m, n, vocab, tokens_stride;
+    int32_t qpr;           // rows per sequence (0 or 1: one)
 } lgx_embed_args;
 
 // seq_len[b] = (keep ? seq_len[b] : 0) + add for b < m
@@ -145,6 +152,8 @@ typedef struct {
     uint16_t* vpages;
     float* q_out;          // [m][hq][d]
     int32_t m, hq, hkv, d, maxp, num_pages, max_seq;
+    int32_t qpr;           // rows per sequence: row b * qpr + j is position seq_len[b] + j
+                           // of sequence b (0 or 1: one row per sequence)
 } lgx_qkv_args;
 
 // a = silu(gate) * up from tree(part) ([nr][m][2*inter]), then Q8_0(a)
@@ -188,3 +197,29 @@ typedef struct {
     int32_t* cand_i;
     int32_t m, vocab, advance, nslices;
 } lgx_argmax_args;
+
+// Large-M Q8_0 product (prefill): one workgroup per (64 weight rows, 128
+// activation rows, group of LGX_TG_RANGES ranges).  Activations in the T16
+// tile layout of the weights (row tiles of 16, 1 KiB per 64-column pair).
+// part[g][m][n] = canonical tree over the ranges of group g, so the tree
+// over the groups is the tree over all ranges.
+#define LGX_TG_RANGES 4
+#define LGX_TG_N 64
+#define LGX_TG_M 128
+typedef struct {
+    const int8_t* wt;      // T16 weights [n/16][k/64][64][16]
+    const uint16_t* wd;    // S16 scales
+    const int8_t* xt;      // T16 activations [ceil(m/16)][k/64][64][16]
+    const uint16_t* xd;    // activation scales [m][k/32]
+    float* part;           // [ngroups][m][n]
+    int32_t n, k, m, ngroups;
+    int32_t ntn, ntm;      // workgroup tiles along n and m
+} lgx_gemm_tiled_args;
+
+// Row-major int8 [rows][k] -> T16 tiles of ceil(rows/16) * 16 rows, the rows
+// past `rows` zero.
+typedef struct {
+    const int8_t* src;
+    int8_t* dst;
+    int32_t rows, k;
+} lgx_act_t16_args;

@@ -1407,8 +1407,9 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
 template <int D>
 __device__ __forceinline__ float attn_merge(const lgx_attn_args& a, int bh) {
     const int i = threadIdx.x;
-    const int b = bh / a.hq;
-    const int L = min(a.seq_len[b] + a.len_add, a.maxlen);
+    const int qpr = max(a.qpr, 1);
+    const int row = bh / a.hq, b = row / qpr;
+    const int L = min(a.seq_len[b] + (row - b * qpr) + a.len_add, a.maxlen);
     const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
     const float* pp = a.part + (int64_t)bh * a.nchunk * (D + 2);
     float M = -__builtin_inff();
@@ -1541,10 +1542,10 @@ __device__ __forceinline__ void tree_partials_n(const float* part, int nr, int64
 }
 
 extern "C" __global__ __launch_bounds__(256) void lgx_k_embed(const lgx_embed_args a) {
-    const int b = blockIdx.x;
-    const int tok = min(max(a.tokens[(int64_t)b * a.tokens_stride], 0), a.vocab - 1);
+    const int row = blockIdx.x, qpr = max(a.qpr, 1), b = row / qpr;
+    const int tok = min(max(a.tokens[(int64_t)b * a.tokens_stride + (row - b * qpr)], 0), a.vocab - 1);
     const uint16_t* er = a.emb + (int64_t)tok * a.n;
-    for (int i = threadIdx.x; i < a.n; i += 256) a.h[(int64_t)b * a.n + i] = h2f(er[i]);
+    for (int i = threadIdx.x; i < a.n; i += 256) a.h[(int64_t)row * a.n + i] = h2f(er[i]);
 }
 
 // The canonical pairwise tree over nr (<= R) values, evaluated as they
@@ -1728,7 +1729,9 @@ extern "C" __global__ __launch_bounds__(512) void lgx_k_add_rmsnorm_quant4_r20(c
 extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_qkv_rope_append(const lgx_qkv_args a) {
     constexpr int NT = LGX_GLUE_NT, KV = LGX_QKV_MAX / NT;
     __shared__ float row[LGX_QKV_MAX];
+    // workgroup = row b of the product (sequence bs, its query j)
     const int b = blockIdx.x, t = threadIdx.x;
+    const int qpr = max(a.qpr, 1), bs = b / qpr;
     const int d = a.d, half = d / 2;
     const int nq = (a.hq + 2 * a.hkv) * d;
     bool on[KV];
@@ -1758,10 +1761,10 @@ extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_qkv_rope_append(
         }
     }
     __syncthreads();
-    const int pos = min(max(a.seq_len[b], 0), a.max_seq - 1);
+    const int pos = min(max(a.seq_len[bs] + (b - bs * qpr), 0), a.max_seq - 1);
     const float* cr = a.cos_t + (int64_t)pos * half;
     const float* sr = a.sin_t + (int64_t)pos * half;
-    const int page = min(max(a.page_table[(int64_t)b * a.maxp + pos / LGX_PAGE], 0), a.num_pages - 1);
+    const int page = min(max(a.page_table[(int64_t)bs * a.maxp + pos / LGX_PAGE], 0), a.num_pages - 1);
     const int slot = pos % LGX_PAGE;
     // rotate q heads and k heads: pair (i, i + d/2) of head hh
     for (int e = t; e < (a.hq + a.hkv) * half; e += NT) {
@@ -2050,3 +2053,511 @@ extern "C" __global__ __launch_bounds__(64) void lgx_k_advance(const lgx_advance
     const int b = blockIdx.x * 64 + threadIdx.x;
     if (b < a.m) a.seq_len[b] = (a.keep ? a.seq_len[b] : 0) + a.add;
 }
+
+// ---------------------------------------------------------------------------
+// Activation rows to T16 tiles: thread per 16-byte lane slot of a 1 KiB unit
+// (unit = row tile x 64-column pair); rows past `rows` are zero.
+// ---------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(256) void lgx_k_act_to_t16(const lgx_act_t16_args a) {
+    const int64_t np = a.k >> 6;
+    const int64_t total = (int64_t)((a.rows + 15) >> 4) * np * 64;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int64_t u = i >> 6;
+    const int lane = (int)(i & 63);
+    const int64_t t = u / np, p = u - t * np;
+    const int64_t row = t * 16 + (lane & 15);
+    uint2 lo = make_uint2(0, 0), hi = make_uint2(0, 0);
+    if (row < a.rows) {
+        const int8_t* s = a.src + row * a.k + p * 64 + 8 * (lane >> 4);
+        lo = *(const uint2*)s;
+        hi = *(const uint2*)(s + 32);
+    }
+    *(uint4*)(a.dst + i * 16) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
+// ---------------------------------------------------------------------------
+// Large-M Q8_0 product (prefill).  Workgroup tile: 64 weight rows (4 row
+// tiles) x 128 activation rows (8 row tiles) over one group of up to
+// LGX_TG_RANGES ranges.  Four waves; wave (wn, wm) owns weight tiles 2wn,
+// 2wn+1 and activation tiles 4wm..4wm+3.  Per 64-column pair a wave issues
+// one MFMA i32_16x16x32_i8 per (block, weight tile, activation tile) with the
+// weight tile as A, so lane (r, c) of a result holds weight rows 4c..4c+3 of
+// the tile against activation row r; the epilogue runs the canonical chain
+// acc = fmaf((float)s, f32(dw) * f32(dx), acc) of each element.  When a
+// range ends its values fold into the group's subtree (a binary counter over
+// at most four ranges: earlier + later, as in the level-by-level tree) and
+// the group's values go to part[g].
+// Staging: two LDS stages of LGX_TG_S pairs filled by direct global->LDS
+// loads, 16-byte lanes for the T16 tiles and 4-byte lanes for the scale
+// pairs of a 64-column pair, which land pre-arranged: dw as [pair][64 rows]
+// (the four rows of a lane are one 16-byte read), dx as [pair][r][8 tiles]
+// (the four tiles of a wave are one 16-byte read).
+// Workgroup order: physical ids go round-robin over the 8 XCDs; each XCD
+// takes a contiguous run of logical tiles, which walk bands of 8 activation
+// tiles, n-tile by n-tile (activation tile fastest), so the tiles in flight
+// on one XCD share their operands through its L2.
+// ---------------------------------------------------------------------------
+#define LGX_TG_S 2
+struct TgSmem {
+    uint4 w[4][LGX_TG_S][64];
+    uint4 x[8][LGX_TG_S][64];
+    uint32_t dw[LGX_TG_S][64];
+    uint32_t dx[LGX_TG_S][128];
+};
+
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_gemm_tiled_args a) {
+    // two stage buffers as two variables: a direct load into one is known
+    // not to alias reads of the other, so reads of the current stage do not
+    // wait for the next stage's loads
+    __shared__ TgSmem sm0, sm1;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int wn = wave & 1, wm = wave >> 1;
+    const int r = lane & 15, c = lane >> 4;
+    // XCD-aware logical id, then (group, band of 8 activation tiles, n tile)
+    const int T = a.ntn * a.ntm * a.ngroups;
+    const int P = blockIdx.x, xcd = P & 7, slot = P >> 3;
+    const int q8 = T >> 3, r8 = T & 7;
+    const int id = xcd * q8 + min(xcd, r8) + slot;
+    const int per_g = a.ntn * a.ntm;
+    const int g = id / per_g;
+    const int rem = id - g * per_g;
+    const int band = rem / (8 * a.ntn);
+    const int bsz = min(8, a.ntm - 8 * band);
+    const int loc = rem - band * 8 * a.ntn;
+    const int tn = loc / bsz, tm = 8 * band + (loc - (loc / bsz) * bsz);
+    const int tn0 = tn * 4, tm0 = tm * 8;
+
+    const int np = a.k >> 6, nb = a.k >> 5, nh = (a.k + 511) >> 9;
+    const int ntw = a.n >> 4, ntx = (a.m + 15) >> 4;
+    const int pg0 = g * (LGX_TG_RANGES * LGX_Q8_RANGE_BLOCKS / 2);
+    const int pend = min(pg0 + LGX_TG_RANGES * LGX_Q8_RANGE_BLOCKS / 2, np);
+    const int nst = (pend - pg0 + LGX_TG_S - 1) / LGX_TG_S;
+    const v4i zero = {0, 0, 0, 0};
+
+    // Direct loads of a stage (pairs pair0 .. pair0 + S - 1, clamped to the
+    // group): uniform base + per-lane byte offset fixed over the stages.
+    //   weights: 4 tiles x S pairs, units j = wave + 4i (tile j / S, pair j % S)
+    //   activations: 8 tiles x S pairs, likewise
+    //   weight scale pairs: [s][64 rows], one 4-byte lane per row (waves < S)
+    //   activation scale pairs: [s][r][tile], wave instruction j = wave
+    const uint32_t off_t16 = lane * 16;
+    const uint32_t off_dw = ((uint32_t)min(tn0 + (lane >> 4), ntw - 1) * nh * 256 + (lane & 15) * 16) * 2;
+    static_assert(LGX_TG_S == 2, "one activation scale instruction per wave");
+    const int dx_ml = (((wave & 1) * 64 + lane) & 7) * 16 + ((((wave & 1) * 64 + lane) & 127) >> 3);
+    const uint32_t off_dx = (uint32_t)min(tm0 * 16 + dx_ml, a.m - 1) * nb * 2;
+    auto stage = [&](TgSmem& sm, int pair0) {
+#pragma unroll
+        for (int i = 0; i < LGX_TG_S; ++i) {
+            const int j = wave + 4 * i;
+            const int tile = j / LGX_TG_S, s = j - tile * LGX_TG_S;
+            const int t = min(tn0 + tile, ntw - 1), p = min(pair0 + s, pend - 1);
+            const char* base = (const char*)a.wt + ((int64_t)t * np + p) * 1024;
+            __builtin_amdgcn_global_load_lds((const void*)(base + off_t16), (lds_void*)&sm.w[tile][s][0], 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 2 * LGX_TG_S; ++i) {
+            const int j = wave + 4 * i;
+            const int tile = j / LGX_TG_S, s = j - tile * LGX_TG_S;
+            const int t = min(tm0 + tile, ntx - 1), p = min(pair0 + s, pend - 1);
+            const char* base = (const char*)a.xt + ((int64_t)t * np + p) * 1024;
+            __builtin_amdgcn_global_load_lds((const void*)(base + off_t16), (lds_void*)&sm.x[tile][s][0], 16, 0, 0);
+        }
+        if (wave < LGX_TG_S) {
+            const int b = 2 * min(pair0 + wave, pend - 1);
+            const char* base = (const char*)(a.wd + (b >> 4) * 256 + (b & 15));
+            __builtin_amdgcn_global_load_lds((const void*)(base + off_dw), (lds_void*)&sm.dw[wave][0], 4, 0, 0);
+        }
+        {
+            const int s = wave >> 1;
+            const char* base = (const char*)(a.xd + 2 * min(pair0 + s, pend - 1));
+            __builtin_amdgcn_global_load_lds((const void*)(base + off_dx),
+                                             (lds_void*)(&sm.dx[0][0] + wave * 64), 4, 0, 0);
+        }
+    };
+
+    float acc[2][4][4], l0[2][4][4], l1[2][4][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[i][j][v] = l0[i][j][v] = l1[i][j][v] = 0.0f;
+    int cnt = 0;
+
+    // One stage: its products from `cur` while the next stage loads into `nxt`.
+    auto run = [&](int q, TgSmem& cur, TgSmem& nxt) {
+        __syncthreads();                          // stage q landed; stage q-1 fully read
+        // every operand of the stage into registers (per pair: two weight
+        // tiles, four activation tiles, the scale pairs of the lane's four
+        // weight rows per tile and of its activation row per tile), then the
+        // next stage's direct loads: issued after the stage's last LDS read,
+        // they overlap the products without the compiler waiting for them
+        uint4 A[LGX_TG_S][2], B[LGX_TG_S][4], DW[LGX_TG_S][2], DX[LGX_TG_S];
+#pragma unroll
+        for (int s = 0; s < LGX_TG_S; ++s) {
+            A[s][0] = cur.w[2 * wn][s][lane];
+            A[s][1] = cur.w[2 * wn + 1][s][lane];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) B[s][j] = cur.x[4 * wm + j][s][lane];
+            DW[s][0] = *(const uint4*)&cur.dw[s][(2 * wn) * 16 + 4 * c];
+            DW[s][1] = *(const uint4*)&cur.dw[s][(2 * wn + 1) * 16 + 4 * c];
+            DX[s] = *(const uint4*)&cur.dx[s][r * 8 + 4 * wm];
+        }
+        if (q + 1 < nst) stage(nxt, pg0 + LGX_TG_S * (q + 1));
+#pragma unroll
+        for (int s = 0; s < LGX_TG_S; ++s) {
+            if (pg0 + LGX_TG_S * q + s >= pend) continue;      // workgroup-uniform
+            const uint32_t dxw[4] = {DX[s].x, DX[s].y, DX[s].z, DX[s].w};
+            // product u = (block, weight tile, activation tile); product u + 1
+            // is issued before the epilogue of u, so the MFMA latency is
+            // covered by that epilogue
+            auto mf = [&](int u) -> v4i {
+                const int blk = u >> 3, i = (u >> 2) & 1, j = u & 3;
+                const long av = blk ? (long)(((uint64_t)A[s][i].w << 32) | A[s][i].z)
+                                    : (long)(((uint64_t)A[s][i].y << 32) | A[s][i].x);
+                const long bv = blk ? (long)(((uint64_t)B[s][j].w << 32) | B[s][j].z)
+                                    : (long)(((uint64_t)B[s][j].y << 32) | B[s][j].x);
+                return __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, zero, 0, 0, 0);
+            };
+            auto ep = [&](int u, const v4i& d) {
+                const int blk = u >> 3, i = (u >> 2) & 1, j = u & 3;
+                const uint32_t dww[4] = {DW[s][i].x, DW[s][i].y, DW[s][i].z, DW[s][i].w};
+                const float dx = h2f(blk ? dxw[j] >> 16 : dxw[j] & 0xffffu);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float dw = h2f(blk ? dww[v] >> 16 : dww[v] & 0xffffu);
+                    // f16 x f16 is exact in binary32: fmaf(dw, dx, +0) is the
+                    // product (>= +0), one v_fma_mix from the binary16 halves
+                    acc[i][j][v] = fmaf((float)d[v], fmaf(dw, dx, 0.0f), acc[i][j][v]);
+                }
+            };
+            v4i dcur = mf(0);
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                v4i dnext = dcur;
+                if (u + 1 < 16) dnext = mf(u + 1);
+                __builtin_amdgcn_sched_barrier(0);
+                ep(u, dcur);
+                __builtin_amdgcn_sched_barrier(0);
+                dcur = dnext;
+            }
+        }
+        const int done = LGX_TG_S * (q + 1);
+        if (done % (LGX_Q8_RANGE_BLOCKS / 2) == 0 || q == nst - 1) {
+            // range end: fold into the group's subtree (cnt is uniform: one
+            // branch per fold)
+            float* A0 = &acc[0][0][0];
+            float* L0 = &l0[0][0][0];
+            float* L1 = &l1[0][0][0];
+            if (cnt == 0 || cnt == 2) {
+#pragma unroll
+                for (int e = 0; e < 32; ++e) L0[e] = A0[e];
+            } else if (cnt == 1) {
+#pragma unroll
+                for (int e = 0; e < 32; ++e) L1[e] = L0[e] + A0[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 32; ++e) L1[e] = L1[e] + (L0[e] + A0[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 32; ++e) A0[e] = 0.0f;
+            ++cnt;
+        }
+    };
+
+    stage(sm0, pg0);
+#pragma unroll 1
+    for (int q = 0; q < nst; q += 2) {
+        run(q, sm0, sm1);
+        if (q + 1 < nst) run(q + 1, sm1, sm0);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int t = tn0 + 2 * wn + i;
+        if (t >= ntw) continue;
+        const int n0 = t * 16 + 4 * c;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int m = (tm0 + 4 * wm + j) * 16 + r;
+            if (m >= a.m) continue;
+            float f[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                f[v] = cnt == 1 ? l0[i][j][v] : cnt == 3 ? l1[i][j][v] + l0[i][j][v] : l1[i][j][v];
+            *(float4*)(a.part + ((int64_t)g * a.m + m) * a.n + n0) = make_float4(f[0], f[1], f[2], f[3]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Causal multi-query attention of a prefill chunk.  Row r = b * qpr + j of q
+// is the query at position seq_len[b] + j and attends to its first
+// L = seq_len[b] + j + len_add cached tokens.  Every row runs exactly the
+// decode schedule (per 256-token chunk: the score chain over d, the chunk
+// max, lgx_expf, the halving-tree sum over 256 slots, the PV chain over the
+// chunk's tokens; chunks merged by attn_merge), so a prefilled position has
+// the bits of a decoded one.
+// Workgroup: 512 threads = 8 waves for (sequence b, KV head g, block of
+// PFA_QB query rows, chunk c).  The chunk's K rows, then its V rows, pass
+// through one 32 KiB LDS tile in stages of PFA_TOK tokens (direct
+// global->LDS loads; each row's 16-byte pieces are stored XOR-swizzled by
+// the row, so row-wise and column-wise reads are conflict-free) and serve
+// the PFA_QB rows x GQ heads.
+//   scores:  wave (row qp = w/2, half w%2); lane l owns chunk tokens
+//            64 (w%2) + l and + 128 for the GQ heads, the query row read
+//            through the scalar cache (uniform in the wave).
+//   softmax: per (row, head) the max over both waves, p to LDS, the halving
+//            tree's 128-level in-lane, its 64-level across the two waves,
+//            the rest across lanes (as the decode kernel).
+//   PV:      wave (row qp = w/2, head group w%2); 16-lane row rho is head
+//            4 (w%2) + rho, lane k owns dims [D/16 k, +D/16); the row's p_t
+//            comes from lane t%16 of a 16-token register (DPP row_newbcast).
+// ---------------------------------------------------------------------------
+#define PFA_QB 4
+// p of lane J of the lane's 16-lane row (DPP row_newbcast: J is an immediate)
+template <int J>
+__device__ __forceinline__ float row_bcast(int v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0x150 + J, 0xf, 0xf, false));
+}
+template <int J>
+struct IdxC {
+    static constexpr int value = J;
+};
+template <int J, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (J < N) {
+        f(IdxC<J>{});
+        static_for<J + 1, N>(f);
+    }
+}
+template <int D>
+__device__ __forceinline__ int pfa_swz(int t) {
+    return D == 128 ? (t & 15) : ((t >> 1) & 7);
+}
+
+template <int D, int GQ>
+__device__ __forceinline__ void attn_prefill_body(const lgx_attn_args& a) {
+    constexpr int C = LGX_ATTN_CHUNK;
+    constexpr int TOK = 32768 / (2 * D);          // tokens per K/V stage
+    constexpr int NST = C / TOK;
+    constexpr int CPR = D / 8;                    // 16-byte pieces per row
+    constexpr int NU = TOK / 128;                 // tokens per lane per stage
+    __shared__ __align__(16) uint16_t kv_s[TOK * D];
+    __shared__ __align__(16) float p_s[PFA_QB][GQ][C];
+    __shared__ float xm_s[PFA_QB][GQ][2];
+    __shared__ float xl_s[PFA_QB][GQ][64];
+    __shared__ int pg_s[C / LGX_PAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int qpr = max(a.qpr, 1);
+    const int nqb = (qpr + PFA_QB - 1) / PFA_QB;
+    // XCD-aware logical id, then (sequence x KV head, chunk, query block):
+    // the blocks that share a chunk's K/V run on one XCD together
+    const int T = a.B * a.hkv * a.ncg * nqb;
+    const int P = blockIdx.x, xcd = P & 7, slot = P >> 3;
+    const int id = xcd * (T >> 3) + min(xcd, T & 7) + slot;
+    const int bg = id / (a.ncg * nqb), rem = id - bg * (a.ncg * nqb);
+    const int c = rem / nqb, qb = rem - c * nqb;
+    const int b = bg / a.hkv, g = bg - b * a.hkv;
+    const int j0 = qb * PFA_QB, t0 = c * C;
+    const int sl = a.seq_len[b];
+    const int jl = min(j0 + PFA_QB, qpr) - 1;              // last row of the block
+    const int Lmax = min(max(sl + jl + a.len_add, 0), a.maxlen);
+    if (t0 >= Lmax) return;                       // whole workgroup, before any barrier
+    if (tid < C / LGX_PAGE) {
+        int pg = 0;
+        if (t0 + tid * LGX_PAGE < Lmax) pg = a.page_table[(int64_t)b * a.maxp + t0 / LGX_PAGE + tid];
+        pg_s[tid] = min(max(pg, 0), a.num_pages - 1);
+    }
+    __syncthreads();
+
+    // direct loads of stage kap (tokens [kap TOK, +TOK) of the chunk) of K
+    // or V: 32 wave instructions of 1 KiB, wave w issues w, w + 8, ...
+    auto stage = [&](const uint16_t* pages, int kap) {
+#pragma unroll
+        for (int i = 0; i < TOK * CPR / 64 / 8; ++i) {
+            const int ins = wave + 8 * i;
+            const int pos = ins * 64 + lane;
+            const int t = pos / CPR, sp = pos - t * CPR;
+            const int tok = kap * TOK + t;
+            const uint16_t* src = pages +
+                (((int64_t)pg_s[tok >> 4] * a.hkv + g) * LGX_PAGE + (tok & 15)) * D + (sp ^ pfa_swz<D>(t)) * 8;
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(kv_s + ins * 512), 16, 0, 0);
+        }
+    };
+
+    // ---- scores ----
+    const int qp = wave >> 1, wh = wave & 1;
+    const int jq = j0 + qp;
+    const int row = b * qpr + min(jq, qpr - 1);
+    const int nq = jq < qpr ? min(C, min(max(sl + jq + a.len_add, 0), a.maxlen) - t0) : 0;
+    const __attribute__((address_space(4))) float* qs =
+        (const __attribute__((address_space(4))) float*)(a.q + ((int64_t)row * a.hq + g * GQ) * D);
+    float sc[GQ][2];
+#pragma unroll
+    for (int kap = 0; kap < NST; ++kap) {
+        if (kap > 0) __syncthreads();             // the previous stage is fully read
+        stage(a.kpages, kap);
+        __syncthreads();                          // every wave's loads have landed
+        float acc[GQ][NU];
+#pragma unroll
+        for (int h = 0; h < GQ; ++h)
+#pragma unroll
+            for (int u = 0; u < NU; ++u) acc[h][u] = 0.0f;
+        // 4 dimensions per step: the step's GQ x 4 query values (scalar
+        // registers) are requested one step ahead
+        float4 qn[GQ];
+#pragma unroll
+        for (int h = 0; h < GQ; ++h) qn[h] = *(const __attribute__((address_space(4))) float4*)(qs + h * D);
+#pragma unroll 2
+        for (int s4 = 0; s4 < D / 4; ++s4) {
+            float4 qc[GQ];
+#pragma unroll
+            for (int h = 0; h < GQ; ++h) qc[h] = qn[h];
+            if (s4 + 1 < D / 4) {
+#pragma unroll
+                for (int h = 0; h < GQ; ++h)
+                    qn[h] = *(const __attribute__((address_space(4))) float4*)(qs + h * D + 4 * (s4 + 1));
+            }
+            float kf[NU][4];
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                const int t = 64 * wh + lane + 128 * u;
+                const uint2 kv = *(const uint2*)(kv_s + t * D + ((s4 >> 1) ^ pfa_swz<D>(t)) * 8 + (s4 & 1) * 4);
+                kf[u][0] = h2f(kv.x & 0xffffu);
+                kf[u][1] = h2f(kv.x >> 16);
+                kf[u][2] = h2f(kv.y & 0xffffu);
+                kf[u][3] = h2f(kv.y >> 16);
+            }
+#pragma unroll
+            for (int h = 0; h < GQ; ++h) {
+                const float qv[4] = {qc[h].x, qc[h].y, qc[h].z, qc[h].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int u = 0; u < NU; ++u) acc[h][u] = fmaf(qv[e], kf[u][e], acc[h][u]);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < GQ; ++h)
+#pragma unroll
+            for (int u = 0; u < NU; ++u) sc[h][kap * NU + u] = acc[h][u] * a.scale;
+    }
+    __syncthreads();                              // K fully read: the tile takes V
+    stage(a.vpages, 0);
+
+    // ---- softmax ----
+    const int tt0 = 64 * wh + lane, tt1 = tt0 + 128;
+    float m[GQ];
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) {
+        sc[h][0] = tt0 < nq ? sc[h][0] : -__builtin_inff();
+        sc[h][1] = tt1 < nq ? sc[h][1] : -__builtin_inff();
+        float mm = fmaxf(sc[h][0], sc[h][1]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) mm = fmaxf(mm, shfl_xor_f(mm, o));
+        if (lane == 0) xm_s[qp][h][wh] = mm;
+    }
+    __syncthreads();
+    float l1[GQ];
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) {
+        m[h] = fmaxf(xm_s[qp][h][0], xm_s[qp][h][1]);
+        const float p0 = tt0 < nq ? lgx_expf(sc[h][0] - m[h]) : 0.0f;
+        const float p1 = tt1 < nq ? lgx_expf(sc[h][1] - m[h]) : 0.0f;
+        p_s[qp][h][tt0] = p0;
+        p_s[qp][h][tt1] = p1;
+        l1[h] = p0 + p1;                          // halving tree, level 128
+        if (wh == 1) xl_s[qp][h][lane] = l1[h];
+    }
+    __syncthreads();
+    if (wh == 0 && nq > 0) {
+#pragma unroll
+        for (int h = 0; h < GQ; ++h) {
+            float l = l1[h] + xl_s[qp][h][lane];  // level 64
+#pragma unroll
+            for (int s2 = 32; s2 >= 1; s2 >>= 1) l = l + __shfl_down(l, s2, 64);
+            if (lane == 0) {
+                float* pp = a.part + (((int64_t)row * a.hq + g * GQ + h) * a.nchunk + c) * (D + 2);
+                pp[D] = m[h];
+                pp[D + 1] = l;
+            }
+        }
+    }
+
+    // ---- PV ----
+    constexpr int DL = D / 16;
+    const int rho = lane >> 4, k = lane & 15;
+    const int h = 4 * (wave & 1) + rho, hc = min(h, GQ - 1);
+    float o[DL];
+#pragma unroll
+    for (int e = 0; e < DL; ++e) o[e] = 0.0f;
+    auto pv_token = [&](int t, float pb) {      // t: row of the stage tile
+        const int sw = pfa_swz<D>(t);
+        float vf[DL];
+        if constexpr (D == 128) {
+            const uint4 vv = *(const uint4*)(kv_s + t * D + (k ^ sw) * 8);
+            const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vf[2 * e] = h2f(w4[e] & 0xffffu);
+                vf[2 * e + 1] = h2f(w4[e] >> 16);
+            }
+        } else {
+            const uint2 vv = *(const uint2*)(kv_s + t * D + ((k >> 1) ^ sw) * 8 + (k & 1) * 4);
+            vf[0] = h2f(vv.x & 0xffffu);
+            vf[1] = h2f(vv.x >> 16);
+            vf[2] = h2f(vv.y & 0xffffu);
+            vf[3] = h2f(vv.y >> 16);
+        }
+#pragma unroll
+        for (int e = 0; e < DL; ++e) o[e] = fmaf(pb, vf[e], o[e]);
+    };
+#pragma unroll
+    for (int kap = 0; kap < NST; ++kap) {
+        if (kap > 0) {
+            __syncthreads();
+            stage(a.vpages, kap);
+        }
+        __syncthreads();                          // V stage kap has landed
+        const int tb = kap * TOK, te = min(nq, tb + TOK);   // uniform in the wave
+        for (int ts = tb; ts < te; ts += 16) {
+            const int pr = __builtin_bit_cast(int, p_s[qp][hc][ts + k]);
+            if (ts + 16 <= te) {
+                static_for<0, 16>([&](auto J) { pv_token(ts + J.value - tb, row_bcast<J.value>(pr)); });
+            } else {
+                static_for<0, 16>([&](auto J) {
+                    if (ts + J.value < te) pv_token(ts + J.value - tb, row_bcast<J.value>(pr));
+                });
+            }
+        }
+    }
+    if (h < GQ && nq > 0) {
+        float* pp = a.part + (((int64_t)row * a.hq + g * GQ + h) * a.nchunk + c) * (D + 2) + DL * k;
+#pragma unroll
+        for (int e = 0; e < DL; e += 4) *(float4*)(pp + e) = make_float4(o[e], o[e + 1], o[e + 2], o[e + 3]);
+    }
+}
+
+#define LGX_PFA_KERNELS(D, G)                                                                     \
+    extern "C" __global__ __launch_bounds__(512) void lgx_k_attn_prefill_d##D##_g##G(            \
+        const lgx_attn_args a) {                                                                 \
+        attn_prefill_body<D, G>(a);                                                              \
+    }
+LGX_PFA_KERNELS(64, 1)
+LGX_PFA_KERNELS(64, 2)
+LGX_PFA_KERNELS(64, 3)
+LGX_PFA_KERNELS(64, 4)
+LGX_PFA_KERNELS(64, 5)
+LGX_PFA_KERNELS(64, 6)
+LGX_PFA_KERNELS(64, 7)
+LGX_PFA_KERNELS(64, 8)
+LGX_PFA_KERNELS(128, 1)
+LGX_PFA_KERNELS(128, 2)
+LGX_PFA_KERNELS(128, 3)
+LGX_PFA_KERNELS(128, 4)
+LGX_PFA_KERNELS(128, 5)
+LGX_PFA_KERNELS(128, 6)
+LGX_PFA_KERNELS(128, 7)
+LGX_PFA_KERNELS(128, 8)

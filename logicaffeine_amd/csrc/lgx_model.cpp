@@ -75,6 +75,17 @@ struct lgx_model {
     };
     std::vector<StepGraph> graphs;
     hipStream_t capture = nullptr;   // recording only: capture needs a non-null stream
+    // batched prefill: buffers for max_batch * chunk rows, allocated on first use
+    struct Prefill {
+        int32_t chunk = 0;           // positions per sequence per chunk
+        float* h = nullptr;          // [rows][H] residual stream
+        int8_t* xq = nullptr;        // [rows][kmax] Q8_0 activations, row-major
+        int8_t* xt = nullptr;        // the same in T16 tiles (the tiled product's operand)
+        uint16_t* xd = nullptr;      // [rows][kmax / 32]
+        float* q = nullptr;          // [rows][hq][d]
+        float* part = nullptr;       // group partials of the products
+        float* attn_part = nullptr;  // [rows][hq][nchunk][d + 2]
+    } pf;
 
     ~lgx_model() {
         for (StepGraph& g : graphs) (void)hipGraphExecDestroy(g.exec);
@@ -182,7 +193,7 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
     const int H = cf.hidden, I = cf.intermediate, d = cf.head_dim, hq = cf.n_heads,
               hkv = cf.n_kv_heads;
     lgx_status st;
-    lgx_embed_args ea{md->emb, tokens, md->h, B, H, cf.vocab, tokens_stride};
+    lgx_embed_args ea{md->emb, tokens, md->h, B, H, cf.vocab, tokens_stride, 1};
     if ((st = launch(c, K_EMBED, dim3(B), dim3(256), ea, stream)) != LGX_OK) return st;
     for (int l = 0; l < cf.n_layers; ++l) {
         // norm (+ residual of the previous layer's down product) -> Q8
@@ -272,6 +283,138 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
     md->last_nr = nr;
     md->last_B = B;
     return launch_argmax(c, lg, nr, B, cf.vocab, next, md->seq_len, 1, md->cand, stream);
+}
+
+// ---- batched prefill ----------------------------------------------------
+// Rows b * n + j of a chunk are positions seq_len[b] + j of the B sequences;
+// every kernel runs the decode step's schedule per row, so the cache holds
+// the values a token-by-token prefill writes.
+
+lgx_status prefill_alloc(lgx_model* md) {
+    if (md->pf.chunk) return LGX_OK;
+    const lgx_qwen_config& cf = md->c;
+    const int H = cf.hidden, I = cf.intermediate, d = cf.head_dim, hq = cf.n_heads;
+    // about 8192 rows per chunk: enough rows for the tiled products
+    int chunk = std::max(16, (8192 / cf.max_batch + 15) / 16 * 16);
+    if (md->ctx->prefill_chunk > 0) chunk = md->ctx->prefill_chunk;
+    chunk = std::min(chunk, (cf.max_seq + 15) / 16 * 16);
+    const int64_t rows = (int64_t)cf.max_batch * chunk, rows16 = (rows + 15) / 16 * 16;
+    const int kmax = std::max({H, I, hq * d});
+    int64_t part = 0;
+    auto upd = [&](int n, int k) { part = std::max<int64_t>(part, (int64_t)tiled_groups(k) * rows * n); };
+    upd(md->qkv_n, H);
+    upd(H, hq * d);
+    upd(2 * I, H);
+    upd(H, I);
+    lgx_model::Prefill& pf = md->pf;
+    lgx_status st;
+    if ((st = dev_alloc(md, &pf.h, (size_t)rows * H)) || (st = dev_alloc(md, &pf.xq, (size_t)rows * kmax)) ||
+        (st = dev_alloc(md, &pf.xt, (size_t)rows16 * kmax)) ||
+        (st = dev_alloc(md, &pf.xd, (size_t)rows * kmax / 32)) ||
+        (st = dev_alloc(md, &pf.q, (size_t)rows * hq * d)) || (st = dev_alloc(md, &pf.part, (size_t)part)) ||
+        (st = dev_alloc(md, &pf.attn_part, (size_t)rows * hq * md->nchunk * (d + 2))))
+        return st;
+    pf.chunk = chunk;
+    return LGX_OK;
+}
+
+// Product of W over the chunk's M rows (Q8_0 in pf.xq/pf.xd): T16 copy of
+// the activations, then the tiled product's group partials into pf.part.
+lgx_status pf_product(lgx_model* md, const DevQ8& W, int M, void* stream) {
+    lgx_status st = act_to_t16(md->ctx, md->pf.xq, M, W.m.k, md->pf.xt, stream);
+    if (st != LGX_OK) return st;
+    return run_q8_tiled(md->ctx, &W.m, md->pf.xt, md->pf.xd, M, md->pf.part, stream);
+}
+
+lgx_status pf_norm(lgx_model* md, int M, int n, int nr, bool with_part, void* stream) {
+    lgx_norm_args a{};
+    a.part = with_part ? md->pf.part : nullptr;
+    a.nr = nr;
+    a.h = md->pf.h;
+    a.w = md->ones;
+    a.xq = md->pf.xq;
+    a.xd = md->pf.xd;
+    a.m = M;
+    a.n = n;
+    a.eps = md->c.rms_eps;
+    return launch_norm(md->ctx, a, stream);
+}
+
+// One chunk: positions seq_len[b] + j (j < n) of the B sequences, tokens
+// tokens[b * stride + j]; ncg chunks of 256 cached tokens bound the
+// attention grid.  Leaves seq_len[b] += n.  The last layer stops after its
+// KV append: its attention and MLP only feed the hidden state of these
+// positions, which no later step reads.
+lgx_status prefill_chunk(lgx_model* md, int B, int n, const int32_t* tokens, int stride, int ncg,
+                         void* stream) {
+    lgx_ctx* c = md->ctx;
+    const lgx_qwen_config& cf = md->c;
+    const int H = cf.hidden, I = cf.intermediate, d = cf.head_dim, hq = cf.n_heads,
+              hkv = cf.n_kv_heads;
+    const int M = B * n;
+    lgx_model::Prefill& pf = md->pf;
+    lgx_status st;
+    lgx_embed_args ea{md->emb, tokens, pf.h, M, H, cf.vocab, stride, n};
+    if ((st = launch(c, K_EMBED, dim3(M), dim3(256), ea, stream)) != LGX_OK) return st;
+    for (int l = 0; l < cf.n_layers; ++l) {
+        if ((st = pf_norm(md, M, H, tiled_groups(I), l > 0, stream)) != LGX_OK) return st;
+        if ((st = pf_product(md, md->qkv[l], M, stream)) != LGX_OK) return st;
+        lgx_qkv_args qa{};
+        qa.part = pf.part;
+        qa.nr = tiled_groups(H);
+        qa.bias = md->bias[l];
+        qa.cos_t = md->cos_t;
+        qa.sin_t = md->sin_t;
+        qa.seq_len = md->seq_len;
+        qa.page_table = md->page_table;
+        qa.kpages = md->kc[l];
+        qa.vpages = md->vc[l];
+        qa.q_out = pf.q;
+        qa.m = M;
+        qa.hq = hq;
+        qa.hkv = hkv;
+        qa.d = d;
+        qa.maxp = md->maxp;
+        qa.num_pages = md->num_pages;
+        qa.max_seq = cf.max_seq;
+        qa.qpr = n;
+        if ((st = launch(c, K_QKV_ROPE_APPEND, dim3(M), dim3(LGX_GLUE_NT), qa, stream)) != LGX_OK)
+            return st;
+        if (l == cf.n_layers - 1) break;
+        lgx_attn_args aa{};
+        aa.q = pf.q;
+        aa.kpages = md->kc[l];
+        aa.vpages = md->vc[l];
+        aa.page_table = md->page_table;
+        aa.seq_len = md->seq_len;
+        aa.part = pf.attn_part;
+        aa.B = B;
+        aa.hq = hq;
+        aa.hkv = hkv;
+        aa.maxp = md->maxp;
+        aa.nchunk = md->nchunk;
+        aa.num_pages = md->num_pages;
+        aa.maxlen = cf.max_seq;
+        aa.len_add = 1;
+        aa.scale = (float)(1.0 / std::sqrt((double)d));
+        aa.xq = pf.xq;
+        aa.xd = pf.xd;
+        aa.qpr = n;
+        aa.ncg = ncg;
+        if ((st = launch_prefill_attn(c, aa, d, stream)) != LGX_OK) return st;
+        if ((st = launch(c, d == 64 ? K_ATTN_COMBINE_QUANT_D64 : K_ATTN_COMBINE_QUANT_D128,
+                         dim3(M * hq), dim3(d), aa, stream)) != LGX_OK)
+            return st;
+        if ((st = pf_product(md, md->o[l], M, stream)) != LGX_OK) return st;
+        if ((st = pf_norm(md, M, H, tiled_groups(hq * d), true, stream)) != LGX_OK) return st;
+        if ((st = pf_product(md, md->gu[l], M, stream)) != LGX_OK) return st;
+        lgx_swiglu_args sw{pf.part, tiled_groups(H), pf.xq, pf.xd, nullptr, M, I};
+        if ((st = launch(c, K_SWIGLU_QUANT, dim3(M, cdiv(I / 32, 32)), dim3(256), sw, stream)) != LGX_OK)
+            return st;
+        if ((st = pf_product(md, md->dn[l], M, stream)) != LGX_OK) return st;
+    }
+    lgx_advance_args av{md->seq_len, B, n, 1};
+    return launch(c, K_ADVANCE, dim3(cdiv(B, 64)), dim3(64), av, stream);
 }
 
 constexpr size_t kGraphMax = 8;
@@ -523,6 +666,32 @@ lgx_status lgx_qwen_prefill(lgx_model* m, int32_t B, int32_t P, const int32_t* p
         if (!prompt || !next) return fail(LGX_NULL_POINTER, "NULL prompt or next");
         if (B <= 0 || B > m->c.max_batch || P <= 0)
             return fail(LGX_OUT_OF_BOUNDS, "B = %d, P = %d", B, P);
+        if (!m->ctx->prefill_serial && P > 1) {
+            // current lengths (one synchronising read): the prompt must fit,
+            // and they bound each chunk's attention grid
+            std::vector<int32_t> sl(B);
+            LGX_HIP(hipMemcpyAsync(sl.data(), m->seq_len, (size_t)B * 4, hipMemcpyDeviceToHost,
+                                   (hipStream_t)stream));
+            LGX_HIP(hipStreamSynchronize((hipStream_t)stream));
+            int smax = 0;
+            for (int32_t v : sl) {
+                if (v < 0) return fail(LGX_INVALID_ARGUMENT, "negative sequence length %d", v);
+                smax = std::max(smax, (int)v);
+            }
+            if ((int64_t)smax + P > m->c.max_seq)
+                return fail(LGX_OUT_OF_BOUNDS, "prompt of %d tokens after %d exceeds max_seq %d", P,
+                            smax, m->c.max_seq);
+            if ((st = prefill_alloc(m)) != LGX_OK) return st;
+            const int chunk = m->pf.chunk;
+            for (int p0 = 0; p0 < P - 1; p0 += chunk) {
+                const int n = std::min(chunk, P - 1 - p0);
+                const int ncg = (int)cdiv(std::min(smax + p0 + n, m->c.max_seq), LGX_ATTN_CHUNK);
+                if ((st = prefill_chunk(m, B, n, prompt + p0, P, ncg, stream)) != LGX_OK) return st;
+            }
+            // the last position through the decode step: its logits give `next`
+            if ((st = layers(m, B, prompt + (P - 1), P, stream)) != LGX_OK) return st;
+            return head(m, B, next, stream);
+        }
         for (int p = 0; p < P; ++p) {
             if ((st = layers(m, B, prompt + p, P, stream)) != LGX_OK) return st;
             if (p + 1 < P) {

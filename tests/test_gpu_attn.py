@@ -106,3 +106,50 @@ def test_attention_argument_errors(ctx, orc):
     with pytest.raises(lgx.LgxError) as ei:                 # 6 / 4 heads
         ctx.gqa_decode_attn(q3, pages3, pages3, pt, sl, 16)
     assert ei.value.status_name == "LGX_INVALID_ARGUMENT"
+
+
+# ---- prefill: several causal query rows per sequence ----
+
+def prefill_ref(orc, q, k, v, pt, ctx_len, P):
+    """Oracle: row b*P + j is a decode query of sequence b at length
+    ctx_len[b] + j + 1 (the page table row repeated per query row)."""
+    B = len(ctx_len)
+    lens = np.array([ctx_len[b] + j + 1 for b in range(B) for j in range(P)], np.int32)
+    ptr = np.repeat(pt, P, axis=0)
+    return orc.gqa_decode_attn(q, k, v, ptr, lens)
+
+
+@pytest.mark.parametrize("hq,hkv,d,ctx_len,P", [
+    (14, 2, 64, [0, 37], 40),            # fresh sequence + short context, ragged row block
+    (28, 4, 128, [0, 200], 72),          # rows cross the first chunk boundary
+    (12, 2, 128, [500, 0, 255], 9),      # GQ 6; P not a multiple of the row block
+    (8, 8, 64, [3], 257),                # GQ 1, rows spanning two chunks
+    (8, 1, 128, [1000], 20),             # GQ 8
+])
+def test_prefill_attn_bit_exact(ctx, orc, hq, hkv, d, ctx_len, P):
+    """Every prefill row equals the decode schedule at its own length."""
+    B = len(ctx_len)
+    lens_end = [c + P for c in ctx_len]
+    k, v, pt, maxp = make_cache(B, hkv, d, lens_end, seed=hq * d + P)
+    q = orc.gen_normal_f32(4, hq + d + P, (B * P, hq, d))
+    msl = maxp * 16
+    out = host(ctx.gqa_prefill_attn(ctx.to_device(q), ctx.to_device(k), ctx.to_device(v),
+                                    ctx.to_device(pt), ctx.to_device(np.asarray(ctx_len, np.int32)),
+                                    P, msl))
+    assert np.array_equal(out, prefill_ref(orc, q, k, v, pt, ctx_len, P))
+
+
+def test_prefill_attn_config4_shape_sampled(ctx, orc):
+    """Config-4 head layout at a 4096-token context: 64 new rows after 4032
+    cached tokens (17 chunks), checked on a sample of rows."""
+    B, hq, hkv, d, P = 2, 28, 4, 128, 64
+    ctx_len = [4032, 1111]
+    k, v, pt, maxp = make_cache(B, hkv, d, [c + P for c in ctx_len], seed=77)
+    q = orc.gen_normal_f32(4, 99, (B * P, hq, d))
+    out = host(ctx.gqa_prefill_attn(ctx.to_device(q), ctx.to_device(k), ctx.to_device(v),
+                                    ctx.to_device(pt), ctx.to_device(np.asarray(ctx_len, np.int32)),
+                                    P, maxp * 16))
+    rows = [0, 1, 31, 63, 64, 100, 127]
+    lens = np.array([ctx_len[r // P] + r % P + 1 for r in rows], np.int32)
+    ref = orc.gqa_decode_attn(q[rows], k, v, pt[[r // P for r in rows]], lens)
+    assert np.array_equal(out[rows], ref)

@@ -120,6 +120,55 @@ def test_prefill_then_decode_bit_exact(pair, ctx):
                 assert np.array_equal(got, om.kv(layer, which, b, int(lens[b]))), (layer, b, which)
 
 
+@pytest.mark.parametrize("chunk", [48, 16])
+def test_chunked_prefill_equals_oracle(chunk):
+    """The batched prefill in several chunks (positions per chunk forced
+    small: chunk boundaries inside and across 256-token attention chunks,
+    ragged starting lengths) leaves the oracle's tokens, logits and KV bits."""
+    import os
+
+    from oracle import oracle as orc
+
+    old = os.environ.get("LGX_PREFILL_CHUNK")
+    os.environ["LGX_PREFILL_CHUNK"] = str(chunk)
+    try:
+        c = lgx.Context(0)
+    finally:
+        if old is None:
+            os.environ.pop("LGX_PREFILL_CHUNK")
+        else:
+            os.environ["LGX_PREFILL_CHUNK"] = old
+    cfg = orc.qwen_config("tiny_untied")
+    gm = lgx.Model(c, cfg, 31)
+    om = orc.Model(cfg, 31)
+    rng = np.random.default_rng(chunk)
+    B = cfg["max_batch"]
+    p1 = rng.integers(0, cfg["vocab"], size=(1, 70)).astype(np.int32)
+    nxt = host(gm.prefill(c.to_device(p1)))
+    for p in range(p1.shape[1]):
+        on = om.step(np.arange(1), p1[:, p])
+    assert np.array_equal(nxt, on)
+    p2 = rng.integers(0, cfg["vocab"], size=(B, 221)).astype(np.int32)
+    nxt = host(gm.prefill(c.to_device(p2)))
+    for p in range(p2.shape[1]):
+        on, lg = om.step(np.arange(B), p2[:, p], want_logits=True)
+    assert np.array_equal(nxt, on)
+    assert np.array_equal(bits(host(gm.logits(B))), bits(lg))
+    lens = dev_array(gm, "seq_len", np.int32, (B,))
+    assert [int(x) for x in lens] == [291, 221, 221, 221]
+    for layer in range(cfg["n_layers"]):
+        for b in range(B):
+            for which in (0, 1):
+                got = kv_dense(gm, cfg, layer, which, b, int(lens[b]))
+                assert np.array_equal(got, om.kv(layer, which, b, int(lens[b]))), (layer, b, which)
+    # a prompt past max_seq is an error, not a silent clamp
+    with pytest.raises(lgx.LgxError):
+        gm.prefill(c.to_device(rng.integers(0, 10, size=(B, 100)).astype(np.int32)))
+    gm.close()
+    om.close()
+    c.close()
+
+
 def test_decode_uses_only_first_B_sequences(pair, ctx):
     """A step over B < max_batch leaves the other sequences' state alone."""
     cfg, gm, om = pair

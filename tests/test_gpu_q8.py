@@ -219,6 +219,45 @@ def test_kernel_variants_agree(ctx, orc, n, k):
             c.close()
 
 
+@pytest.mark.parametrize("n,k,m", [
+    (8960, 1536, 128),     # config-1 gate, one range group, whole tiles
+    (1536, 8960, 200),     # config-1 down: 9 ranges = 3 groups, ragged m tile
+    (272, 2112, 131),      # 17 row tiles (last workgroup tile mostly empty), 1-pair last range
+    (4864, 896, 384),      # 3 m tiles
+    (512, 18944, 130),     # 19 ranges = 5 groups (4, 4, 4, 4, 3)
+    (64, 192, 129),        # 3 pairs: a half-filled last stage
+])
+def test_tiled_gemm_bit_exact(ctx, orc, n, k, m):
+    """The large-M tiled product (T16 activations, group partials, tree over
+    the groups) gives the oracle's bits."""
+    qs, d = orc.gen_q8_matrix(3, n + k, n, k)
+    x = orc.gen_normal_f32(3, m, (m, k))
+    xq, xd = orc.quantize_q8_0(x)
+    W = ctx.q8_matrix(qs, d)
+    y = host(ctx.q8_gemm(W, ctx.to_device(xq), ctx.to_device(xd)))
+    assert np.array_equal(y, orc.q8_gemm(qs, d, xq, xd))
+
+
+def test_tiled_gemm_small_m_forced(ctx, orc):
+    """LGX_GEMM_TILED_MIN=1 routes every m > 1 through the tiled product: a
+    single row, ragged row tiles and rows spanning workgroup tiles agree with
+    the oracle and with the streaming kernels."""
+    n, k = 1536, 8960
+    qs, d = orc.gen_q8_matrix(3, 5, n, k)
+    x = orc.gen_normal_f32(3, 6, (140, k))
+    xq, xd = orc.quantize_q8_0(x)
+    ref = orc.q8_gemm(qs, d, xq, xd)
+    c = _ctx_with_env(LGX_GEMM_TILED_MIN=2)
+    try:
+        W = c.q8_matrix(qs, d)
+        gx, gd = c.to_device(xq), c.to_device(xd)
+        for m in (2, 15, 16, 17, 64, 140):
+            assert np.array_equal(host(c.q8_gemm(W, gx[:m].contiguous(), gd[:m].contiguous())),
+                                  ref[:m]), m
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("n,k", [(4864, 896), (1536, 8960)])
 def test_partials_then_combine_equal_full_product(ctx, orc, n, k):
     """Range partials + lgx_q8_range_combine == the one-call product, and each
