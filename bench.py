@@ -268,7 +268,9 @@ def decode_bench(ctx, torch, key, seed=3):
     tok = gm.prefill(prompt)
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t
-    print(f"[bench] {key}: model {create_s:.1f} s, prefill {B}x{P} in {prefill_s:.1f} s",
+    pf_ops = lgx.prefill_valu_ops(cfg, B, P)
+    print(f"[bench] {key}: model {create_s:.1f} s, prefill {B}x{P} in {prefill_s:.1f} s "
+          f"({B * P / prefill_s:.0f} tok/s, {pf_ops / prefill_s / lgx.VALU_LANE_OPS_PEAK:.2f} of the VALU bound)",
           file=sys.stderr, flush=True)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -299,6 +301,11 @@ def decode_bench(ctx, torch, key, seed=3):
         "ms_per_step": round(ms, 4),
         "eager_ms_per_step": round(eager_ms, 4),
         "prefill_s": round(prefill_s, 2),
+        "prefill": {"tokens_per_s": round(B * P / prefill_s, 1),
+                    "roofline": {"bound": "valu", "achieved": round(pf_ops / prefill_s / 1e12, 2),
+                                 "peak": round(lgx.VALU_LANE_OPS_PEAK / 1e12, 2),
+                                 "unit": "T lane-op/s", "frac": round(pf_ops / prefill_s / lgx.VALU_LANE_OPS_PEAK, 4),
+                                 "ops": pf_ops}},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "bytes_per_step": int(step_bytes_),

@@ -302,7 +302,10 @@ lgx_status lgx_qwen_decode_step(lgx_model* m, int32_t B, int32_t* tokens, void* 
  * positions seq_len[b]..+P, filling the KV cache; next[b] receives the
  * greedy token after the prompt and seq_len[b] += P.  Each position goes
  * through the decode schedule, so prefill and decode produce the same
- * cache bits. */
+ * cache bits.  The first P-1 positions run as batched chunks (large-M
+ * products, causal multi-query attention); the call reads the current
+ * lengths once (synchronising the stream) and fails with
+ * LGX_OUT_OF_BOUNDS when seq_len[b] + P exceeds max_seq. */
 lgx_status lgx_qwen_prefill(lgx_model* m, int32_t B, int32_t P, const int32_t* prompt,
                             int32_t* next, void* stream);
 /* nsteps greedy decode steps, each identical in effect to

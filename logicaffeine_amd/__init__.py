@@ -115,6 +115,33 @@ def decode_step_bytes(cfg: dict, B: int, context: float) -> float:
     return L * per_layer + lm + B * context * kv_row + B * kv_row
 
 
+# Non-packed binary32 VALU lane operations per second of MI355X: 256 CUs x 4
+# SIMDs x 16 lanes x 2.4 GHz (the published 157.3 TFLOP/s counts an FMA as
+# two flops and packed FP32, which this build does not use).
+VALU_LANE_OPS_PEAK = 256 * 4 * 16 * 2.4e9
+
+
+def prefill_valu_ops(cfg: dict, B: int, P: int) -> float:
+    """Essential VALU lane operations of the canonical prefill of B prompts of
+    P tokens (rows B x (P - 1) through the batched chunks, the last position
+    through the decode step): 3 per (row, output, 32-block) of every Q8_0
+    product (cvt of the int32 block dot, scale product, chain FMA) and 1 per
+    attention FMA (score chain over d and PV chain over the attended tokens,
+    per query head).  The last layer of a batched chunk stops after its KV
+    append (QKV product only)."""
+    H, I, d = cfg["hidden"], cfg["inter"], cfg["head_dim"]
+    hq, hkv, L, V = cfg["n_heads"], cfg["n_kv"], cfg["n_layers"], cfg["vocab"]
+    qkv = (hq + 2 * hkv) * d * H / 32
+    full = qkv + (H * hq * d + 2 * I * H + H * I) / 32
+    rows = B * (P - 1)
+    gemm = 3.0 * (rows * ((L - 1) * full + qkv) + B * L * full)
+    gemm += B * V * H * (1.0 if cfg["tied"] else 3.0 / 32)
+    # attention: row at position p attends p + 1 tokens (2d FMAs per head each)
+    att_rows = B * (P - 1) * P / 2.0            # sum over p < P - 1 of (p + 1)
+    attn = 2.0 * d * hq * (att_rows * (L - 1) + B * P * L)
+    return gemm + attn
+
+
 # Tensor ids of lgx_model_tensor.
 MODEL_TENSORS = {"emb": 0, "lm_q": 1, "lm_d": 2, "qkv_q": 3, "qkv_d": 4, "o_q": 5, "o_d": 6,
                  "gu_q": 7, "gu_d": 8, "dn_q": 9, "dn_d": 10, "bias": 11, "k_pages": 12,

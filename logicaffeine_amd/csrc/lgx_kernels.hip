@@ -2304,12 +2304,12 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_
 // global->LDS loads; each row's 16-byte pieces are stored XOR-swizzled by
 // the row, so row-wise and column-wise reads are conflict-free) and serve
 // the PFA_QB rows x GQ heads.
-//   scores:  wave (row qp = w/2, half w%2); lane l owns chunk tokens
-//            64 (w%2) + l and + 128 for the GQ heads, the query row read
-//            through the scalar cache (uniform in the wave).
-//   softmax: per (row, head) the max over both waves, p to LDS, the halving
-//            tree's 128-level in-lane, its 64-level across the two waves,
-//            the rest across lanes (as the decode kernel).
+//   scores:  wave (row qp = w/2, head group hg = w%2) owns heads
+//            4 hg .. 4 hg + 3 over the whole chunk, lane l the tokens
+//            l + 64 u; the query values come through the scalar cache
+//            (uniform in the wave), 4 heads x 8 dimensions per step.
+//   softmax: within the wave: per head the max, p to LDS, the halving tree
+//            (levels 128 and 64 in-lane, the rest across lanes).
 //   PV:      wave (row qp = w/2, head group w%2); 16-lane row rho is head
 //            4 (w%2) + rho, lane k owns dims [D/16 k, +D/16); the row's p_t
 //            comes from lane t%16 of a 16-token register (DPP row_newbcast).
@@ -2344,9 +2344,9 @@ __device__ __forceinline__ void attn_prefill_body(const lgx_attn_args& a) {
     constexpr int CPR = D / 8;                    // 16-byte pieces per row
     constexpr int NU = TOK / 128;                 // tokens per lane per stage
     __shared__ __align__(16) uint16_t kv_s[TOK * D];
-    __shared__ __align__(16) float p_s[PFA_QB][GQ][C];
-    __shared__ float xm_s[PFA_QB][GQ][2];
-    __shared__ float xl_s[PFA_QB][GQ][64];
+    // p rows padded by 16 floats: the four heads of a wave read the same
+    // token column in four distinct bank groups
+    __shared__ __align__(16) float p_s[PFA_QB][GQ][C + 16];
     __shared__ int pg_s[C / LGX_PAGE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2387,109 +2387,112 @@ __device__ __forceinline__ void attn_prefill_body(const lgx_attn_args& a) {
         }
     };
 
-    // ---- scores ----
-    const int qp = wave >> 1, wh = wave & 1;
+    // ---- scores: wave (row qp, head group hg) owns heads 4 hg + hh (hh < 4)
+    // over all C tokens of the chunk, lane l the tokens l + 64 u (u < 4) ----
+    constexpr int HW = 4;                         // heads per wave
+    constexpr int UPS = TOK / 64;                 // tokens per lane per stage
+    const int qp = wave >> 1, hg = wave & 1;
     const int jq = j0 + qp;
     const int row = b * qpr + min(jq, qpr - 1);
     const int nq = jq < qpr ? min(C, min(max(sl + jq + a.len_add, 0), a.maxlen) - t0) : 0;
-    const __attribute__((address_space(4))) float* qs =
-        (const __attribute__((address_space(4))) float*)(a.q + ((int64_t)row * a.hq + g * GQ) * D);
-    float sc[GQ][2];
+    typedef const __attribute__((address_space(4))) float* qptr_t;
+    const qptr_t q0 = (qptr_t)(a.q + ((int64_t)row * a.hq + g * GQ) * D);
+    int qoff[HW];                                 // heads past GQ re-read the last one
+#pragma unroll
+    for (int hh = 0; hh < HW; ++hh) qoff[hh] = min(4 * hg + hh, GQ - 1) * D;
+    auto qh_at = [&](int hh, int i) { return q0[qoff[hh] + i]; };
+    float sc[HW][4];
 #pragma unroll
     for (int kap = 0; kap < NST; ++kap) {
         if (kap > 0) __syncthreads();             // the previous stage is fully read
         stage(a.kpages, kap);
         __syncthreads();                          // every wave's loads have landed
-        float acc[GQ][NU];
+        float acc[HW][UPS];
 #pragma unroll
-        for (int h = 0; h < GQ; ++h)
+        for (int hh = 0; hh < HW; ++hh)
 #pragma unroll
-            for (int u = 0; u < NU; ++u) acc[h][u] = 0.0f;
-        // 4 dimensions per step: the step's GQ x 4 query values (scalar
-        // registers) are requested one step ahead
-        float4 qn[GQ];
+            for (int v = 0; v < UPS; ++v) acc[hh][v] = 0.0f;
+        // 8 dimensions per step (one 16-byte K read per token), the query
+        // values in two halves of 4 x 4 scalar registers: each half is
+        // requested one half-step before its products
+        float qa[HW][4], qb[HW][4];
+        auto qload = [&](float (&qv)[HW][4], int s4) {
 #pragma unroll
-        for (int h = 0; h < GQ; ++h) qn[h] = *(const __attribute__((address_space(4))) float4*)(qs + h * D);
-#pragma unroll 2
-        for (int s4 = 0; s4 < D / 4; ++s4) {
-            float4 qc[GQ];
+            for (int hh = 0; hh < HW; ++hh)
 #pragma unroll
-            for (int h = 0; h < GQ; ++h) qc[h] = qn[h];
-            if (s4 + 1 < D / 4) {
+                for (int e = 0; e < 4; ++e) qv[hh][e] = qh_at(hh, 4 * s4 + e);
+        };
+        auto qk_half = [&](const float (&qv)[HW][4], const float (&kf)[UPS][8], int e0) {
 #pragma unroll
-                for (int h = 0; h < GQ; ++h)
-                    qn[h] = *(const __attribute__((address_space(4))) float4*)(qs + h * D + 4 * (s4 + 1));
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int hh = 0; hh < HW; ++hh)
+#pragma unroll
+                    for (int v = 0; v < UPS; ++v)
+                        acc[hh][v] = fmaf(qv[hh][e], kf[v][e0 + e], acc[hh][v]);
+        };
+        qload(qa, 0);
+#pragma unroll 1
+        for (int s8 = 0; s8 < CPR; ++s8) {
+            float kf[UPS][8];
+#pragma unroll
+            for (int v = 0; v < UPS; ++v) {
+                const int t = lane + 64 * v;
+                const uint4 kv = *(const uint4*)(kv_s + t * D + (s8 ^ pfa_swz<D>(t)) * 8);
+                const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    kf[v][2 * e] = h2f(w4[e] & 0xffffu);
+                    kf[v][2 * e + 1] = h2f(w4[e] >> 16);
+                }
             }
-            float kf[NU][4];
-#pragma unroll
-            for (int u = 0; u < NU; ++u) {
-                const int t = 64 * wh + lane + 128 * u;
-                const uint2 kv = *(const uint2*)(kv_s + t * D + ((s4 >> 1) ^ pfa_swz<D>(t)) * 8 + (s4 & 1) * 4);
-                kf[u][0] = h2f(kv.x & 0xffffu);
-                kf[u][1] = h2f(kv.x >> 16);
-                kf[u][2] = h2f(kv.y & 0xffffu);
-                kf[u][3] = h2f(kv.y >> 16);
-            }
-#pragma unroll
-            for (int h = 0; h < GQ; ++h) {
-                const float qv[4] = {qc[h].x, qc[h].y, qc[h].z, qc[h].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-#pragma unroll
-                    for (int u = 0; u < NU; ++u) acc[h][u] = fmaf(qv[e], kf[u][e], acc[h][u]);
-            }
+            qload(qb, 2 * s8 + 1);
+            qk_half(qa, kf, 0);
+            if (s8 + 1 < CPR) qload(qa, 2 * s8 + 2);
+            qk_half(qb, kf, 4);
         }
 #pragma unroll
-        for (int h = 0; h < GQ; ++h)
+        for (int hh = 0; hh < HW; ++hh)
 #pragma unroll
-            for (int u = 0; u < NU; ++u) sc[h][kap * NU + u] = acc[h][u] * a.scale;
+            for (int v = 0; v < UPS; ++v) sc[hh][kap * UPS + v] = acc[hh][v] * a.scale;
     }
     __syncthreads();                              // K fully read: the tile takes V
     stage(a.vpages, 0);
 
-    // ---- softmax ----
-    const int tt0 = 64 * wh + lane, tt1 = tt0 + 128;
-    float m[GQ];
+    // ---- softmax, within the wave: max, p to LDS, halving tree (levels
+    // 128 and 64 in-lane, the rest across lanes) ----
 #pragma unroll
-    for (int h = 0; h < GQ; ++h) {
-        sc[h][0] = tt0 < nq ? sc[h][0] : -__builtin_inff();
-        sc[h][1] = tt1 < nq ? sc[h][1] : -__builtin_inff();
-        float mm = fmaxf(sc[h][0], sc[h][1]);
+    for (int hh = 0; hh < HW; ++hh) {
+        const int h = 4 * hg + hh;
+        float mm = -__builtin_inff();
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            sc[hh][u] = lane + 64 * u < nq ? sc[hh][u] : -__builtin_inff();
+            mm = fmaxf(mm, sc[hh][u]);
+        }
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) mm = fmaxf(mm, shfl_xor_f(mm, o));
-        if (lane == 0) xm_s[qp][h][wh] = mm;
-    }
-    __syncthreads();
-    float l1[GQ];
+        float p[4];
 #pragma unroll
-    for (int h = 0; h < GQ; ++h) {
-        m[h] = fmaxf(xm_s[qp][h][0], xm_s[qp][h][1]);
-        const float p0 = tt0 < nq ? lgx_expf(sc[h][0] - m[h]) : 0.0f;
-        const float p1 = tt1 < nq ? lgx_expf(sc[h][1] - m[h]) : 0.0f;
-        p_s[qp][h][tt0] = p0;
-        p_s[qp][h][tt1] = p1;
-        l1[h] = p0 + p1;                          // halving tree, level 128
-        if (wh == 1) xl_s[qp][h][lane] = l1[h];
-    }
-    __syncthreads();
-    if (wh == 0 && nq > 0) {
+        for (int u = 0; u < 4; ++u) p[u] = lane + 64 * u < nq ? lgx_expf(sc[hh][u] - mm) : 0.0f;
+        if (h < GQ) {
 #pragma unroll
-        for (int h = 0; h < GQ; ++h) {
-            float l = l1[h] + xl_s[qp][h][lane];  // level 64
+            for (int u = 0; u < 4; ++u) p_s[qp][h][lane + 64 * u] = p[u];
+        }
+        float l = (p[0] + p[2]) + (p[1] + p[3]);  // levels 128 and 64
 #pragma unroll
-            for (int s2 = 32; s2 >= 1; s2 >>= 1) l = l + __shfl_down(l, s2, 64);
-            if (lane == 0) {
-                float* pp = a.part + (((int64_t)row * a.hq + g * GQ + h) * a.nchunk + c) * (D + 2);
-                pp[D] = m[h];
-                pp[D + 1] = l;
-            }
+        for (int s2 = 32; s2 >= 1; s2 >>= 1) l = l + __shfl_down(l, s2, 64);
+        if (lane == 0 && h < GQ && nq > 0) {
+            float* pp = a.part + (((int64_t)row * a.hq + g * GQ + h) * a.nchunk + c) * (D + 2);
+            pp[D] = mm;
+            pp[D + 1] = l;
         }
     }
 
     // ---- PV ----
     constexpr int DL = D / 16;
     const int rho = lane >> 4, k = lane & 15;
-    const int h = 4 * (wave & 1) + rho, hc = min(h, GQ - 1);
+    const int h = 4 * hg + rho, hc = min(h, GQ - 1);
     float o[DL];
 #pragma unroll
     for (int e = 0; e < DL; ++e) o[e] = 0.0f;
