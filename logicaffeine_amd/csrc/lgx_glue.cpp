@@ -136,7 +136,7 @@ lgx_status lgx_swiglu_quant(lgx_ctx* c, const float* gu, int32_t m, int32_t inte
         if ((xq == nullptr) != (xd == nullptr)) return fail(LGX_NULL_POINTER, "xq and xd go together");
         if (m <= 0 || inter <= 0 || inter % 32)
             return fail(LGX_INVALID_ARGUMENT, "m %d, inter %d (multiple of 32)", m, inter);
-        lgx_swiglu_args a{gu, 1, xq, xd, y, m, inter};
+        lgx_swiglu_args a{gu, 1, xq, xd, y, m, inter, 0};
         return launch(c, K_SWIGLU_QUANT, dim3(m, cdiv(inter / 32, 32)), dim3(256), a, stream);
     });
 }

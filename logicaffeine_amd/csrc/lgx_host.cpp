@@ -64,6 +64,11 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
         c->gemv_wgs = env_int("LGX_GEMV_WGS", 0);
         c->gemm_mt = env_int("LGX_GEMM_MT", 0);
         c->tiled_min = env_int("LGX_GEMM_TILED_MIN", 128);
+        c->tiled_rows = env_int("LGX_GEMM_TILED_ROWS", 0);
+        c->tiled_grp = env_int("LGX_GEMM_TILED_GRP", 0);
+        if (c->tiled_grp != 1 && c->tiled_grp != 2 && c->tiled_grp != 4) c->tiled_grp = 0;
+        const char* dg = getenv("LGX_DECODE_GEMM");
+        c->decode_streaming = dg && std::string(dg) == "streaming";
         const char* pfv = getenv("LGX_PREFILL");
         c->prefill_serial = pfv && std::string(pfv) == "serial";
         c->prefill_chunk = env_int("LGX_PREFILL_CHUNK", 0);
@@ -428,7 +433,9 @@ lgx_status lgx_q8_gemm(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq, con
         if (m >= c->tiled_min) {
             // T16 copy of the activations, then the group partials (straight
             // into y when K is one group) and the tree over the groups
-            const int ng = tiled_groups(W->k);
+            const Kern kern = tiled_kernel(c, m);
+            const int grp = tiled_grp(c, kern, W->n, W->k, m);
+            const int ng = tiled_groups(W->k, grp);
             const size_t xbytes = ((size_t)cdiv(m, 16) * 16 * W->k + 255) / 256 * 256;
             float* ws = nullptr;
             if ((st = ensure_ws(c, xbytes + (ng > 1 ? (size_t)ng * m * W->n * 4 : 0), &ws)) != LGX_OK)
@@ -436,7 +443,7 @@ lgx_status lgx_q8_gemm(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq, con
             int8_t* xt = (int8_t*)ws;
             float* part = ng > 1 ? (float*)((char*)ws + xbytes) : y;
             if ((st = act_to_t16(c, xq, m, W->k, xt, stream)) != LGX_OK ||
-                (st = run_q8_tiled(c, W, xt, xd, m, part, stream)) != LGX_OK || ng == 1)
+                (st = run_q8_tiled(c, W, xt, xd, m, part, stream, kern, grp)) != LGX_OK || ng == 1)
                 return st;
             lgx_combine_args ca{part, y, (int64_t)m * W->n, ng};
             return launch(c, K_COMBINE, dim3(cdiv(ca.count, 256)), dim3(256), ca, stream);

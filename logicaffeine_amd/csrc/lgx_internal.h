@@ -112,6 +112,8 @@ enum Kern {
     K_NORM4_R20,
     K_ACT_T16,
     K_GEMM_TILED,
+    K_GEMM_TILED64,
+    K_GEMM_TILED32,
     K_PFA_D64_G1,    // + (gq - 1)
     K_PFA_D128_G1 = K_PFA_D64_G1 + 8,
     K_COUNT = K_PFA_D128_G1 + 8
@@ -136,7 +138,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_repack_f16_t64", "lgx_k_lm_head_t64", "lgx_k_rows_to_t16",
     "lgx_k_q8_gemv_grpq4", "lgx_k_q8_gemv_grpq8", "lgx_k_q8_gemv_grpq16",
     "lgx_k_add_rmsnorm_quant4_r8", "lgx_k_add_rmsnorm_quant4_r20",
-    "lgx_k_act_to_t16", "lgx_k_q8_gemm_tiled",
+    "lgx_k_act_to_t16", "lgx_k_q8_gemm_tiled", "lgx_k_q8_gemm_tiled64", "lgx_k_q8_gemm_tiled32",
     "lgx_k_attn_prefill_d64_g1", "lgx_k_attn_prefill_d64_g2", "lgx_k_attn_prefill_d64_g3",
     "lgx_k_attn_prefill_d64_g4", "lgx_k_attn_prefill_d64_g5", "lgx_k_attn_prefill_d64_g6",
     "lgx_k_attn_prefill_d64_g7", "lgx_k_attn_prefill_d64_g8",
@@ -181,6 +183,10 @@ struct lgx_ctx {
     bool gemv_whole = false;      // LGX_GEMV=whole: block dots through LDS, chains after
     int gemm_mt = 0;              // LGX_GEMM_MT: force the M > 1 m-tile width (0: by m)
     int tiled_min = 128;          // LGX_GEMM_TILED_MIN: smallest m through the tiled product
+    int tiled_rows = 0;           // LGX_GEMM_TILED_ROWS: force 128/64/32 activation rows per workgroup
+    int tiled_grp = 0;            // LGX_GEMM_TILED_GRP: force 1/2/4 ranges per group
+    bool decode_streaming = false; // LGX_DECODE_GEMM=streaming: decode products of m >= 17
+                                   // rows through the streaming kernels
     bool prefill_serial = false;  // LGX_PREFILL=serial: prefill as P decode passes
     int prefill_chunk = 0;        // LGX_PREFILL_CHUNK: positions per prefill chunk (0: by batch)
     int ncu = 256;                // compute units of the device
@@ -371,11 +377,15 @@ inline lgx_status run_q8(lgx_ctx* c, Kern kern, const lgx_q8_matrix* W, const fl
     return launch(c, K_COMBINE, dim3(cdiv(ca.count, 256)), dim3(256), ca, stream);
 }
 
-// Large-M product: activations in T16 tiles (ceil(m/16) of them), group
-// partials part[tiled_groups(k)][m][n] (canonical subtrees of 4 ranges).
-inline int tiled_groups(int k) { return (nranges_of(k) + LGX_TG_RANGES - 1) / LGX_TG_RANGES; }
+// Tiled product: activations in T16 tiles (ceil(m/16) of them), group
+// partials part[ceil(nr / grp)][m][n] (canonical subtrees of grp aligned
+// ranges, grp in {1, 2, 4}).  Activation rows per workgroup: 128
+// (K_GEMM_TILED), 64 or 32.
+inline int tiled_groups(int k, int grp = LGX_TG_RANGES) { return (nranges_of(k) + grp - 1) / grp; }
 inline lgx_status run_q8_tiled(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xt,
-                               const uint16_t* xd, int m, float* part, void* stream) {
+                               const uint16_t* xd, int m, float* part, void* stream,
+                               Kern kern = K_GEMM_TILED, int grp = LGX_TG_RANGES) {
+    const int mrows = kern == K_GEMM_TILED ? 128 : kern == K_GEMM_TILED64 ? 64 : 32;
     lgx_gemm_tiled_args a{};
     a.wt = W->qs;
     a.wd = W->d;
@@ -385,12 +395,37 @@ inline lgx_status run_q8_tiled(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t*
     a.n = W->n;
     a.k = W->k;
     a.m = m;
-    a.ngroups = tiled_groups(W->k);
+    a.grp = grp;
+    a.ngroups = tiled_groups(W->k, grp);
     a.ntn = (int)cdiv(W->n, LGX_TG_N);
-    a.ntm = (int)cdiv(m, LGX_TG_M);
+    a.ntm = (int)cdiv(m, mrows);
     const int64_t wgs = (int64_t)a.ntn * a.ntm * a.ngroups;
     if (wgs > INT32_MAX) return fail(LGX_OUT_OF_BOUNDS, "tiled product of %lld workgroups", (long long)wgs);
-    return launch(c, K_GEMM_TILED, dim3((unsigned)wgs), dim3(256), a, stream);
+    return launch(c, kern, dim3((unsigned)wgs), dim3(256), a, stream);
+}
+// Tiled kernel for m rows: 128 activation rows per workgroup from m >= 128,
+// else 32, which also beats 64 at m = 64 (LGX_GEMM_TILED_ROWS forces one).
+inline Kern tiled_kernel(const lgx_ctx* c, int m) {
+    const int rows = c->tiled_rows ? c->tiled_rows : m >= 128 ? 128 : 32;
+    return rows == 128 ? K_GEMM_TILED : rows == 64 ? K_GEMM_TILED64 : K_GEMM_TILED32;
+}
+// Ranges per group for a product of n outputs, reduction k, over m rows
+// through `kern`: the largest of 4, 2, 1 that still gives four workgroups
+// per compute unit (fewer partials when the grid is full anyway).
+inline int tiled_grp(const lgx_ctx* c, Kern kern, int n, int k, int m) {
+    if (c->tiled_grp) return c->tiled_grp;
+    const int mrows = kern == K_GEMM_TILED ? 128 : kern == K_GEMM_TILED64 ? 64 : 32;
+    const int64_t tiles = (int64_t)cdiv(n, LGX_TG_N) * cdiv(m, mrows);
+    for (int grp = 4; grp > 1; grp >>= 1)
+        if (tiles * tiled_groups(k, grp) >= 4LL * c->ncu) return grp;
+    return 1;
+}
+
+// Row-major int8 activations [m][k] -> T16 tiles at dst (ceil(m/16)*16*k bytes).
+inline lgx_status act_to_t16(lgx_ctx* c, const int8_t* xq, int m, int k, int8_t* dst, void* stream) {
+    lgx_act_t16_args a{xq, dst, m, k};
+    const int64_t slots = (int64_t)cdiv(m, 16) * (k / 64) * 64;
+    return launch(c, K_ACT_T16, dim3(cdiv(slots, 256)), dim3(256), a, stream);
 }
 
 // Launch of the prefill attention over B sequences x a.qpr query rows:
@@ -401,13 +436,6 @@ inline lgx_status launch_prefill_attn(lgx_ctx* c, const lgx_attn_args& a, int d,
     if (k < 0 || wgs > INT32_MAX) return fail(LGX_UNSUPPORTED, "prefill attention shape");
     if (wgs == 0) return LGX_OK;
     return launch(c, (Kern)k, dim3((unsigned)wgs), dim3(512), a, stream);
-}
-
-// Row-major int8 activations [m][k] -> T16 tiles at dst (ceil(m/16)*16*k bytes).
-inline lgx_status act_to_t16(lgx_ctx* c, const int8_t* xq, int m, int k, int8_t* dst, void* stream) {
-    lgx_act_t16_args a{xq, dst, m, k};
-    const int64_t slots = (int64_t)cdiv(m, 16) * (k / 64) * 64;
-    return launch(c, K_ACT_T16, dim3(cdiv(slots, 256)), dim3(256), a, stream);
 }
 
 }  // namespace lgxi

@@ -101,6 +101,7 @@ typedef struct {
     // 1: one query per sequence (decode).
     int32_t qpr;
     int32_t ncg;               // prefill: chunks covered by the grid
+    int32_t xq_t16;            // combine+quantise: xq in T16 tiles instead of row-major
 } lgx_attn_args;
 
 #define LGX_PAGE 16
@@ -136,6 +137,7 @@ typedef struct {
     int32_t m, n;
     float eps;
     float* xt;
+    int32_t xq_t16;        // xq in T16 tiles (the tiled product's operand) instead of row-major
 } lgx_norm_args;
 
 // qkv = tree(part) (+ bias, nullable); RoPE on the q and k heads at position seq_len[b];
@@ -165,6 +167,7 @@ typedef struct {
     uint16_t* xd;
     float* y;
     int32_t m, inter;
+    int32_t xq_t16;        // xq in T16 tiles instead of row-major
 } lgx_swiglu_args;
 
 // logits[m][v] = canonical dot of binary32 x[m] with binary16 row E[v]
@@ -214,6 +217,7 @@ typedef struct {
     float* part;           // [ngroups][m][n]
     int32_t n, k, m, ngroups;
     int32_t ntn, ntm;      // workgroup tiles along n and m
+    int32_t grp;           // ranges per group: 1, 2 or 4 (ngroups = ceil(nranges / grp))
 } lgx_gemm_tiled_args;
 
 // Row-major int8 [rows][k] -> T16 tiles of ceil(rows/16) * 16 rows, the rows

@@ -1499,19 +1499,32 @@ __device__ __forceinline__ float tree_partials(const float* part, int nr, int64_
     return tree_sum(p, nr);
 }
 
-// Quantise a row held in LDS (n floats, n % 32 == 0) to xq/xd with NT
-// threads: 8 threads per block, the 8 lanes of a block always active together.
+// Byte offset of element (row m, column i) of an m x k int8 activation held
+// in T16 tiles (the tiled product's operand: 1 KiB per 16 rows x 64
+// columns, lane (r + 16 c) holding bytes [8c, +8) of both blocks of row r);
+// four bytes from a column i % 4 == 0 stay contiguous.
+__device__ __forceinline__ int64_t t16_off(int64_t m, int i, int k) {
+    return ((m >> 4) * (k >> 6) + (i >> 6)) * 1024 + ((m & 15) + 16 * ((i & 31) >> 3)) * 16 +
+           ((i & 63) >> 5) * 8 + (i & 7);
+}
+__device__ __forceinline__ int64_t xq_off(int64_t m, int i, int k, bool t16) {
+    return t16 ? t16_off(m, i, k) : m * k + i;
+}
+
+// Quantise row m held in LDS (n floats, n % 32 == 0) into the n-column
+// matrix xq (row-major or T16) and its scales xd[m][n/32] with NT threads:
+// 8 threads per block, the 8 lanes of a block always active together.
 template <int NT>
 __device__ __forceinline__ void quantize_row_from_lds(const float* row, int n, int8_t* xq,
-                                                      uint16_t* xd) {
+                                                      uint16_t* xd, int64_t m, bool t16) {
     const int j = threadIdx.x & 7;
     for (int bl = threadIdx.x >> 3; bl < n / 32; bl += NT / 8) {
         const float f[4] = {row[bl * 32 + 4 * j], row[bl * 32 + 4 * j + 1], row[bl * 32 + 4 * j + 2],
                             row[bl * 32 + 4 * j + 3]};
         uint16_t dh;
         const uint32_t qw = quantize4(f, dh);
-        *(uint32_t*)(xq + bl * 32 + 4 * j) = qw;
-        if (j == 0) xd[bl] = dh;
+        *(uint32_t*)(xq + xq_off(m, bl * 32 + 4 * j, n, t16)) = qw;
+        if (j == 0) xd[m * (n / 32) + bl] = dh;
     }
 }
 
@@ -1708,7 +1721,7 @@ __device__ __forceinline__ void norm_body(const lgx_norm_args& a) {
     }
     if (a.xq) {
         __syncthreads();
-        quantize_row_from_lds<NT>(row, a.n, a.xq + (int64_t)b * a.n, a.xd + (int64_t)b * (a.n / 32));
+        quantize_row_from_lds<NT>(row, a.n, a.xq, a.xd, b, a.xq_t16 != 0);
     }
 }
 
@@ -1805,7 +1818,8 @@ __device__ __forceinline__ void attn_combine_quant_body(const lgx_attn_args& a) 
         const float f[4] = {row[4 * t], row[4 * t + 1], row[4 * t + 2], row[4 * t + 3]};
         uint16_t dh;
         const uint32_t qw = quantize4(f, dh);
-        *(uint32_t*)(a.xq + (int64_t)bh * D + 4 * t) = qw;
+        const int row = bh / a.hq, col = (bh - row * a.hq) * D + 4 * t;
+        *(uint32_t*)(a.xq + xq_off(row, col, a.hq * D, a.xq_t16 != 0)) = qw;
         if ((t & 7) == 0) a.xd[(int64_t)bh * (D / 32) + (t >> 3)] = dh;
     }
 }
@@ -1846,7 +1860,7 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_swiglu_quant(const lgx_s
     uint16_t dh;
     const uint32_t qw = quantize4(f, dh);
     if (on && a.xq) {
-        *(uint32_t*)(a.xq + (int64_t)b * a.inter + bl * 32 + 4 * j) = qw;
+        *(uint32_t*)(a.xq + xq_off(b, bl * 32 + 4 * j, a.inter, a.xq_t16 != 0)) = qw;
         if (j == 0) a.xd[(int64_t)b * nbl + bl] = dh;
     }
 }
@@ -2077,40 +2091,47 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_act_to_t16(const lgx_act
 }
 
 // ---------------------------------------------------------------------------
-// Large-M Q8_0 product (prefill).  Workgroup tile: 64 weight rows (4 row
-// tiles) x 128 activation rows (8 row tiles) over one group of up to
-// LGX_TG_RANGES ranges.  Four waves; wave (wn, wm) owns weight tiles 2wn,
-// 2wn+1 and activation tiles 4wm..4wm+3.  Per 64-column pair a wave issues
-// one MFMA i32_16x16x32_i8 per (block, weight tile, activation tile) with the
-// weight tile as A, so lane (r, c) of a result holds weight rows 4c..4c+3 of
-// the tile against activation row r; the epilogue runs the canonical chain
+// Tiled Q8_0 product (prefill; decode batches of 32 / 64 rows).  Workgroup
+// tile: 64 weight rows (4 row tiles) x 32*WM activation rows (2*WM row
+// tiles) over one group of a.grp aligned ranges (1, 2 or 4).  Four waves;
+// wave (wn, wm) owns weight tiles 2wn, 2wn+1 and activation tiles
+// WM*wm .. WM*wm + WM-1.  Per 64-column pair a wave issues one MFMA
+// i32_16x16x32_i8 per (block, weight tile, activation tile) with the weight
+// tile as A, so lane (r, c) of a result holds weight rows 4c..4c+3 of the
+// tile against activation row r; the epilogue runs the canonical chain
 // acc = fmaf((float)s, f32(dw) * f32(dx), acc) of each element.  When a
 // range ends its values fold into the group's subtree (a binary counter over
 // at most four ranges: earlier + later, as in the level-by-level tree) and
-// the group's values go to part[g].
+// the group's values go to part[g]: aligned groups of a power-of-two number
+// of ranges are subtrees of the canonical tree, so the tree over the groups
+// is the tree over all ranges.
 // Staging: two LDS stages of LGX_TG_S pairs filled by direct global->LDS
 // loads, 16-byte lanes for the T16 tiles and 4-byte lanes for the scale
 // pairs of a 64-column pair, which land pre-arranged: dw as [pair][64 rows]
-// (the four rows of a lane are one 16-byte read), dx as [pair][r][8 tiles]
-// (the four tiles of a wave are one 16-byte read).
+// (the four rows of a lane are one 16-byte read), dx as [pair][r][2*WM
+// tiles] (the WM tiles of a wave are one read).  Every operand of a stage is
+// read into registers before the next stage's loads are issued (the
+// compiler would otherwise wait for those loads before the reads).
 // Workgroup order: physical ids go round-robin over the 8 XCDs; each XCD
 // takes a contiguous run of logical tiles, which walk bands of 8 activation
 // tiles, n-tile by n-tile (activation tile fastest), so the tiles in flight
 // on one XCD share their operands through its L2.
 // ---------------------------------------------------------------------------
 #define LGX_TG_S 2
+template <int WM>
 struct TgSmem {
     uint4 w[4][LGX_TG_S][64];
-    uint4 x[8][LGX_TG_S][64];
+    uint4 x[2 * WM][LGX_TG_S][64];
     uint32_t dw[LGX_TG_S][64];
-    uint32_t dx[LGX_TG_S][128];
+    uint32_t dx[LGX_TG_S][16 * 2 * WM];
 };
 
-extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_gemm_tiled_args a) {
+template <int WM>
+__device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a) {
+    constexpr int MTILES = 2 * WM;
     // two stage buffers as two variables: a direct load into one is known
-    // not to alias reads of the other, so reads of the current stage do not
-    // wait for the next stage's loads
-    __shared__ TgSmem sm0, sm1;
+    // not to alias reads of the other
+    __shared__ TgSmem<WM> sm0, sm1;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int wn = wave & 1, wm = wave >> 1;
     const int r = lane & 15, c = lane >> 4;
@@ -2126,27 +2147,29 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_
     const int bsz = min(8, a.ntm - 8 * band);
     const int loc = rem - band * 8 * a.ntn;
     const int tn = loc / bsz, tm = 8 * band + (loc - (loc / bsz) * bsz);
-    const int tn0 = tn * 4, tm0 = tm * 8;
+    const int tn0 = tn * 4, tm0 = tm * MTILES;
 
     const int np = a.k >> 6, nb = a.k >> 5, nh = (a.k + 511) >> 9;
     const int ntw = a.n >> 4, ntx = (a.m + 15) >> 4;
-    const int pg0 = g * (LGX_TG_RANGES * LGX_Q8_RANGE_BLOCKS / 2);
-    const int pend = min(pg0 + LGX_TG_RANGES * LGX_Q8_RANGE_BLOCKS / 2, np);
+    const int gpairs = a.grp * (LGX_Q8_RANGE_BLOCKS / 2);
+    const int pg0 = g * gpairs;
+    const int pend = min(pg0 + gpairs, np);
     const int nst = (pend - pg0 + LGX_TG_S - 1) / LGX_TG_S;
     const v4i zero = {0, 0, 0, 0};
 
     // Direct loads of a stage (pairs pair0 .. pair0 + S - 1, clamped to the
     // group): uniform base + per-lane byte offset fixed over the stages.
     //   weights: 4 tiles x S pairs, units j = wave + 4i (tile j / S, pair j % S)
-    //   activations: 8 tiles x S pairs, likewise
+    //   activations: MTILES tiles x S pairs, likewise
     //   weight scale pairs: [s][64 rows], one 4-byte lane per row (waves < S)
-    //   activation scale pairs: [s][r][tile], wave instruction j = wave
+    //   activation scale pairs: [s][r][tile], wave instructions j = wave < WM
+    static_assert(LGX_TG_S == 2, "stage layout");
     const uint32_t off_t16 = lane * 16;
     const uint32_t off_dw = ((uint32_t)min(tn0 + (lane >> 4), ntw - 1) * nh * 256 + (lane & 15) * 16) * 2;
-    static_assert(LGX_TG_S == 2, "one activation scale instruction per wave");
-    const int dx_ml = (((wave & 1) * 64 + lane) & 7) * 16 + ((((wave & 1) * 64 + lane) & 127) >> 3);
+    const int dxp = (wave * 64 + lane) % (16 * MTILES);            // position within a pair
+    const int dx_ml = (dxp % MTILES) * 16 + dxp / MTILES;
     const uint32_t off_dx = (uint32_t)min(tm0 * 16 + dx_ml, a.m - 1) * nb * 2;
-    auto stage = [&](TgSmem& sm, int pair0) {
+    auto stage = [&](TgSmem<WM>& sm, int pair0) {
 #pragma unroll
         for (int i = 0; i < LGX_TG_S; ++i) {
             const int j = wave + 4 * i;
@@ -2156,7 +2179,7 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_
             __builtin_amdgcn_global_load_lds((const void*)(base + off_t16), (lds_void*)&sm.w[tile][s][0], 16, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < 2 * LGX_TG_S; ++i) {
+        for (int i = 0; i < MTILES * LGX_TG_S / 4; ++i) {
             const int j = wave + 4 * i;
             const int tile = j / LGX_TG_S, s = j - tile * LGX_TG_S;
             const int t = min(tm0 + tile, ntx - 1), p = min(pair0 + s, pend - 1);
@@ -2168,52 +2191,56 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_
             const char* base = (const char*)(a.wd + (b >> 4) * 256 + (b & 15));
             __builtin_amdgcn_global_load_lds((const void*)(base + off_dw), (lds_void*)&sm.dw[wave][0], 4, 0, 0);
         }
-        {
-            const int s = wave >> 1;
-            const char* base = (const char*)(a.xd + 2 * min(pair0 + s, pend - 1));
-            __builtin_amdgcn_global_load_lds((const void*)(base + off_dx),
-                                             (lds_void*)(&sm.dx[0][0] + wave * 64), 4, 0, 0);
+        if (wave < WM) {                          // 64 words per instruction, 16*MTILES per pair
+            const int s = (wave * 64 + lane) / (16 * MTILES);   // uniform unless WM == 1
+            const char* src = (const char*)(a.xd + 2 * min(pair0 + s, pend - 1)) + off_dx;
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(&sm.dx[0][0] + wave * 64), 4, 0, 0);
         }
     };
 
-    float acc[2][4][4], l0[2][4][4], l1[2][4][4];
+    float acc[2][WM][4], l0[2][WM][4], l1[2][WM][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < WM; ++j)
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[i][j][v] = l0[i][j][v] = l1[i][j][v] = 0.0f;
     int cnt = 0;
 
     // One stage: its products from `cur` while the next stage loads into `nxt`.
-    auto run = [&](int q, TgSmem& cur, TgSmem& nxt) {
+    auto run = [&](int q, TgSmem<WM>& cur, TgSmem<WM>& nxt) {
         __syncthreads();                          // stage q landed; stage q-1 fully read
-        // every operand of the stage into registers (per pair: two weight
-        // tiles, four activation tiles, the scale pairs of the lane's four
-        // weight rows per tile and of its activation row per tile), then the
-        // next stage's direct loads: issued after the stage's last LDS read,
-        // they overlap the products without the compiler waiting for them
-        uint4 A[LGX_TG_S][2], B[LGX_TG_S][4], DW[LGX_TG_S][2], DX[LGX_TG_S];
+        uint4 A[LGX_TG_S][2], B[LGX_TG_S][WM], DW[LGX_TG_S][2];
+        uint32_t DX[LGX_TG_S][WM];
 #pragma unroll
         for (int s = 0; s < LGX_TG_S; ++s) {
             A[s][0] = cur.w[2 * wn][s][lane];
             A[s][1] = cur.w[2 * wn + 1][s][lane];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) B[s][j] = cur.x[4 * wm + j][s][lane];
+            for (int j = 0; j < WM; ++j) B[s][j] = cur.x[WM * wm + j][s][lane];
             DW[s][0] = *(const uint4*)&cur.dw[s][(2 * wn) * 16 + 4 * c];
             DW[s][1] = *(const uint4*)&cur.dw[s][(2 * wn + 1) * 16 + 4 * c];
-            DX[s] = *(const uint4*)&cur.dx[s][r * 8 + 4 * wm];
+            const uint32_t* dxr = &cur.dx[s][r * MTILES + WM * wm];
+            if constexpr (WM == 4) {
+                const uint4 q4 = *(const uint4*)dxr;
+                DX[s][0] = q4.x; DX[s][1] = q4.y; DX[s][2] = q4.z; DX[s][3] = q4.w;
+            } else if constexpr (WM == 2) {
+                const uint2 q2 = *(const uint2*)dxr;
+                DX[s][0] = q2.x; DX[s][1] = q2.y;
+            } else {
+                DX[s][0] = dxr[0];
+            }
         }
         if (q + 1 < nst) stage(nxt, pg0 + LGX_TG_S * (q + 1));
 #pragma unroll
         for (int s = 0; s < LGX_TG_S; ++s) {
             if (pg0 + LGX_TG_S * q + s >= pend) continue;      // workgroup-uniform
-            const uint32_t dxw[4] = {DX[s].x, DX[s].y, DX[s].z, DX[s].w};
             // product u = (block, weight tile, activation tile); product u + 1
             // is issued before the epilogue of u, so the MFMA latency is
             // covered by that epilogue
+            constexpr int NU = 4 * WM;
             auto mf = [&](int u) -> v4i {
-                const int blk = u >> 3, i = (u >> 2) & 1, j = u & 3;
+                const int blk = u / (2 * WM), i = (u / WM) & 1, j = u % WM;
                 const long av = blk ? (long)(((uint64_t)A[s][i].w << 32) | A[s][i].z)
                                     : (long)(((uint64_t)A[s][i].y << 32) | A[s][i].x);
                 const long bv = blk ? (long)(((uint64_t)B[s][j].w << 32) | B[s][j].z)
@@ -2221,9 +2248,9 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_
                 return __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, zero, 0, 0, 0);
             };
             auto ep = [&](int u, const v4i& d) {
-                const int blk = u >> 3, i = (u >> 2) & 1, j = u & 3;
+                const int blk = u / (2 * WM), i = (u / WM) & 1, j = u % WM;
                 const uint32_t dww[4] = {DW[s][i].x, DW[s][i].y, DW[s][i].z, DW[s][i].w};
-                const float dx = h2f(blk ? dxw[j] >> 16 : dxw[j] & 0xffffu);
+                const float dx = h2f(blk ? DX[s][j] >> 16 : DX[s][j] & 0xffffu);
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const float dw = h2f(blk ? dww[v] >> 16 : dww[v] & 0xffffu);
@@ -2234,9 +2261,9 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_
             };
             v4i dcur = mf(0);
 #pragma unroll
-            for (int u = 0; u < 16; ++u) {
+            for (int u = 0; u < NU; ++u) {
                 v4i dnext = dcur;
-                if (u + 1 < 16) dnext = mf(u + 1);
+                if (u + 1 < NU) dnext = mf(u + 1);
                 __builtin_amdgcn_sched_barrier(0);
                 ep(u, dcur);
                 __builtin_amdgcn_sched_barrier(0);
@@ -2250,18 +2277,19 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_
             float* A0 = &acc[0][0][0];
             float* L0 = &l0[0][0][0];
             float* L1 = &l1[0][0][0];
+            constexpr int NE = 2 * WM * 4;
             if (cnt == 0 || cnt == 2) {
 #pragma unroll
-                for (int e = 0; e < 32; ++e) L0[e] = A0[e];
+                for (int e = 0; e < NE; ++e) L0[e] = A0[e];
             } else if (cnt == 1) {
 #pragma unroll
-                for (int e = 0; e < 32; ++e) L1[e] = L0[e] + A0[e];
+                for (int e = 0; e < NE; ++e) L1[e] = L0[e] + A0[e];
             } else {
 #pragma unroll
-                for (int e = 0; e < 32; ++e) L1[e] = L1[e] + (L0[e] + A0[e]);
+                for (int e = 0; e < NE; ++e) L1[e] = L1[e] + (L0[e] + A0[e]);
             }
 #pragma unroll
-            for (int e = 0; e < 32; ++e) A0[e] = 0.0f;
+            for (int e = 0; e < NE; ++e) A0[e] = 0.0f;
             ++cnt;
         }
     };
@@ -2278,8 +2306,8 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_
         if (t >= ntw) continue;
         const int n0 = t * 16 + 4 * c;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int m = (tm0 + 4 * wm + j) * 16 + r;
+        for (int j = 0; j < WM; ++j) {
+            const int m = (tm0 + WM * wm + j) * 16 + r;
             if (m >= a.m) continue;
             float f[4];
 #pragma unroll
@@ -2288,6 +2316,16 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_
             *(float4*)(a.part + ((int64_t)g * a.m + m) * a.n + n0) = make_float4(f[0], f[1], f[2], f[3]);
         }
     }
+}
+
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_gemm_tiled_args a) {
+    q8_tiled_body<4>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled64(const lgx_gemm_tiled_args a) {
+    q8_tiled_body<2>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled32(const lgx_gemm_tiled_args a) {
+    q8_tiled_body<1>(a);
 }
 
 // ---------------------------------------------------------------------------

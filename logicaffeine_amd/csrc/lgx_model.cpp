@@ -79,8 +79,7 @@ struct lgx_model {
     struct Prefill {
         int32_t chunk = 0;           // positions per sequence per chunk
         float* h = nullptr;          // [rows][H] residual stream
-        int8_t* xq = nullptr;        // [rows][kmax] Q8_0 activations, row-major
-        int8_t* xt = nullptr;        // the same in T16 tiles (the tiled product's operand)
+        int8_t* xt = nullptr;        // [rows16][kmax] Q8_0 activations in T16 tiles
         uint16_t* xd = nullptr;      // [rows][kmax / 32]
         float* q = nullptr;          // [rows][hq][d]
         float* part = nullptr;       // group partials of the products
@@ -159,7 +158,25 @@ lgx_status check_config(const lgx_qwen_config* c) {
 }
 
 
+// Decode products of m >= 33 rows go through the tiled product (32 activation
+// rows per workgroup, ranges grouped for a full grid; at 32 rows and below
+// the streaming kernels are as fast); their activations are written in T16
+// tiles by the producers (norm, attention merge, SwiGLU).
+bool dec_tiled(const lgx_model* md, int m) { return m >= 33 && !md->ctx->decode_streaming; }
+
+// Partials a product of W over m rows leaves for its consumer's tree.
+int parts(const lgx_model* md, const DevQ8& W, int m) {
+    if (!dec_tiled(md, m)) return nranges_of(W.m.k);
+    const Kern kern = tiled_kernel(md->ctx, m);
+    return tiled_groups(W.m.k, tiled_grp(md->ctx, kern, W.m.n, W.m.k, m));
+}
+
 lgx_status product(lgx_model* md, const DevQ8& W, int m, void* stream) {
+    if (dec_tiled(md, m)) {
+        const Kern kern = tiled_kernel(md->ctx, m);
+        return run_q8_tiled(md->ctx, &W.m, md->xq, md->xd, m, md->part, stream, kern,
+                            tiled_grp(md->ctx, kern, W.m.n, W.m.k, m));
+    }
     if (m == 1 && gemv_group_ok(md->ctx, W.m.k)) {
         const lgx_gemv_mat g = gemv_mat(&W.m, nullptr, md->xq, md->xd, md->part, 1);
         return run_gemv_group(md->ctx, &g, 1, stream);
@@ -179,6 +196,7 @@ lgx_status norm(lgx_model* md, int m, int n, int nr_part, bool with_part, float*
     a.xn = xn;
     a.xq = q8 ? md->xq : nullptr;
     a.xd = q8 ? md->xd : nullptr;
+    a.xq_t16 = q8 && dec_tiled(md, m);
     a.m = m;
     a.n = n;
     a.eps = md->c.rms_eps;
@@ -197,11 +215,12 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
     if ((st = launch(c, K_EMBED, dim3(B), dim3(256), ea, stream)) != LGX_OK) return st;
     for (int l = 0; l < cf.n_layers; ++l) {
         // norm (+ residual of the previous layer's down product) -> Q8
-        if ((st = norm(md, B, H, nranges_of(I), l > 0, nullptr, true, stream)) != LGX_OK) return st;
+        if ((st = norm(md, B, H, parts(md, md->dn[0], B), l > 0, nullptr, true, stream)) != LGX_OK)
+            return st;
         if ((st = product(md, md->qkv[l], B, stream)) != LGX_OK) return st;
         lgx_qkv_args qa{};
         qa.part = md->part;
-        qa.nr = nranges_of(H);
+        qa.nr = parts(md, md->qkv[l], B);
         qa.bias = md->bias[l];
         qa.cos_t = md->cos_t;
         qa.sin_t = md->sin_t;
@@ -236,6 +255,7 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
         aa.len_add = 1;
         aa.scale = (float)(1.0 / std::sqrt((double)d));
         aa.xq = md->xq;
+        aa.xq_t16 = dec_tiled(md, B);
         aa.xd = md->xd;
         if ((st = launch(c, (Kern)attn_kernel(d, hq / hkv), dim3(md->nchunk, B * hkv), dim3(256), aa,
                          stream)) != LGX_OK)
@@ -244,10 +264,11 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
                          dim3(B * hq), dim3(d), aa, stream)) != LGX_OK)
             return st;
         if ((st = product(md, md->o[l], B, stream)) != LGX_OK) return st;
-        if ((st = norm(md, B, H, nranges_of(hq * d), true, nullptr, true, stream)) != LGX_OK)
+        if ((st = norm(md, B, H, parts(md, md->o[l], B), true, nullptr, true, stream)) != LGX_OK)
             return st;
         if ((st = product(md, md->gu[l], B, stream)) != LGX_OK) return st;
-        lgx_swiglu_args sw{md->part, nranges_of(H), md->xq, md->xd, nullptr, B, I};
+        lgx_swiglu_args sw{md->part, parts(md, md->gu[l], B), md->xq, md->xd, nullptr, B, I,
+                           dec_tiled(md, B) ? 1 : 0};
         if ((st = launch(c, K_SWIGLU_QUANT, dim3(B, cdiv(I / 32, 32)), dim3(256), sw, stream)) !=
             LGX_OK)
             return st;
@@ -263,7 +284,7 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
     const int H = cf.hidden;
     lgx_status st;
     const bool tied = cf.tied_embedding != 0;
-    if ((st = norm(md, B, H, nranges_of(cf.intermediate), true, md->xn, !tied, stream,
+    if ((st = norm(md, B, H, parts(md, md->dn[0], B), true, md->xn, !tied, stream,
                    tied ? md->xt : nullptr)) != LGX_OK)
         return st;
     const float* lg;
@@ -278,7 +299,7 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
     } else {
         if ((st = product(md, md->lm, B, stream)) != LGX_OK) return st;
         lg = md->part;
-        nr = nranges_of(H);
+        nr = parts(md, md->lm, B);
     }
     md->last_nr = nr;
     md->last_B = B;
@@ -308,7 +329,7 @@ lgx_status prefill_alloc(lgx_model* md) {
     upd(H, I);
     lgx_model::Prefill& pf = md->pf;
     lgx_status st;
-    if ((st = dev_alloc(md, &pf.h, (size_t)rows * H)) || (st = dev_alloc(md, &pf.xq, (size_t)rows * kmax)) ||
+    if ((st = dev_alloc(md, &pf.h, (size_t)rows * H)) ||
         (st = dev_alloc(md, &pf.xt, (size_t)rows16 * kmax)) ||
         (st = dev_alloc(md, &pf.xd, (size_t)rows * kmax / 32)) ||
         (st = dev_alloc(md, &pf.q, (size_t)rows * hq * d)) || (st = dev_alloc(md, &pf.part, (size_t)part)) ||
@@ -318,11 +339,9 @@ lgx_status prefill_alloc(lgx_model* md) {
     return LGX_OK;
 }
 
-// Product of W over the chunk's M rows (Q8_0 in pf.xq/pf.xd): T16 copy of
-// the activations, then the tiled product's group partials into pf.part.
+// Product of W over the chunk's M rows (Q8_0 in T16 tiles pf.xt, scales
+// pf.xd, written so by the producers): group partials of 4 ranges into pf.part.
 lgx_status pf_product(lgx_model* md, const DevQ8& W, int M, void* stream) {
-    lgx_status st = act_to_t16(md->ctx, md->pf.xq, M, W.m.k, md->pf.xt, stream);
-    if (st != LGX_OK) return st;
     return run_q8_tiled(md->ctx, &W.m, md->pf.xt, md->pf.xd, M, md->pf.part, stream);
 }
 
@@ -332,8 +351,9 @@ lgx_status pf_norm(lgx_model* md, int M, int n, int nr, bool with_part, void* st
     a.nr = nr;
     a.h = md->pf.h;
     a.w = md->ones;
-    a.xq = md->pf.xq;
+    a.xq = md->pf.xt;
     a.xd = md->pf.xd;
+    a.xq_t16 = 1;
     a.m = M;
     a.n = n;
     a.eps = md->c.rms_eps;
@@ -397,7 +417,8 @@ lgx_status prefill_chunk(lgx_model* md, int B, int n, const int32_t* tokens, int
         aa.maxlen = cf.max_seq;
         aa.len_add = 1;
         aa.scale = (float)(1.0 / std::sqrt((double)d));
-        aa.xq = pf.xq;
+        aa.xq = pf.xt;
+        aa.xq_t16 = 1;
         aa.xd = pf.xd;
         aa.qpr = n;
         aa.ncg = ncg;
@@ -408,7 +429,7 @@ lgx_status prefill_chunk(lgx_model* md, int B, int n, const int32_t* tokens, int
         if ((st = pf_product(md, md->o[l], M, stream)) != LGX_OK) return st;
         if ((st = pf_norm(md, M, H, tiled_groups(hq * d), true, stream)) != LGX_OK) return st;
         if ((st = pf_product(md, md->gu[l], M, stream)) != LGX_OK) return st;
-        lgx_swiglu_args sw{pf.part, tiled_groups(H), pf.xq, pf.xd, nullptr, M, I};
+        lgx_swiglu_args sw{pf.part, tiled_groups(H), pf.xt, pf.xd, nullptr, M, I, 1};
         if ((st = launch(c, K_SWIGLU_QUANT, dim3(M, cdiv(I / 32, 32)), dim3(256), sw, stream)) != LGX_OK)
             return st;
         if ((st = pf_product(md, md->dn[l], M, stream)) != LGX_OK) return st;
@@ -576,7 +597,7 @@ lgx_status lgx_model_create(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t see
         upd(H, I);
         if (!cf.tied_embedding) upd(cf.vocab, H);
         if ((st = dev_alloc(m, &m->h, (size_t)B * H)) || (st = dev_alloc(m, &m->xn, (size_t)B * H)) ||
-            (st = dev_alloc(m, &m->xq, (size_t)B * kmax)) ||
+            (st = dev_alloc(m, &m->xq, (size_t)(B + 15) / 16 * 16 * kmax)) ||
             (st = dev_alloc(m, &m->xd, (size_t)B * kmax / 32)) ||
             (st = dev_alloc(m, &m->q, (size_t)B * hq * d)) || (st = dev_alloc(m, &m->part, (size_t)part)) ||
             (st = dev_alloc(m, &m->attn_part, (size_t)B * hq * m->nchunk * (d + 2))) ||

@@ -169,6 +169,45 @@ def test_chunked_prefill_equals_oracle(chunk):
     c.close()
 
 
+@pytest.mark.parametrize("name", ["tiny", "tiny_untied"])
+def test_wide_batch_decode_bit_exact(name, ctx):
+    """Batches of 33 or more sequences take the tiled products, whose
+    activations the norms, attention merge and SwiGLU write in T16 tiles:
+    40 sequences (a ragged last row tile) prefilled and decoded agree with
+    the oracle in tokens, logits and KV bits, graph replays included."""
+    from oracle import oracle as orc
+
+    cfg = dict(orc.qwen_config(name), max_batch=40, max_seq=64)
+    gm = lgx.Model(ctx, cfg, 5)
+    om = orc.Model(cfg, 5)
+    rng = np.random.default_rng(11)
+    B, P = 40, 21
+    prompt = rng.integers(0, cfg["vocab"], size=(B, P)).astype(np.int32)
+    tok = gm.prefill(ctx.to_device(prompt))
+    for p in range(P):
+        ref, lg = om.step(np.arange(B), prompt[:, p], want_logits=True)
+    assert np.array_equal(host(tok), ref)
+    assert np.array_equal(bits(host(gm.logits(B))), bits(lg))
+    for s in range(3):
+        gm.decode_step(tok)
+        ref, lg = om.step(np.arange(B), ref, want_logits=True)
+        assert np.array_equal(host(tok), ref), s
+        assert np.array_equal(bits(host(gm.logits(B))), bits(lg)), s
+    hist = ctx.torch.empty((3, B), dtype=ctx.torch.int32, device=ctx.dev)
+    gm.generate(tok, 3, hist)
+    for s in range(3):
+        ref = om.step(np.arange(B), ref)
+        assert np.array_equal(host(hist[s]), ref), s
+    L = P + 6
+    for layer in range(cfg["n_layers"]):
+        for b in (0, 17, 39):
+            for which in (0, 1):
+                assert np.array_equal(kv_dense(gm, cfg, layer, which, b, L),
+                                      om.kv(layer, which, b, L)), (layer, b, which)
+    gm.close()
+    om.close()
+
+
 def test_decode_uses_only_first_B_sequences(pair, ctx):
     """A step over B < max_batch leaves the other sequences' state alone."""
     cfg, gm, om = pair

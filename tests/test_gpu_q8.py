@@ -238,20 +238,23 @@ def test_tiled_gemm_bit_exact(ctx, orc, n, k, m):
     assert np.array_equal(y, orc.q8_gemm(qs, d, xq, xd))
 
 
-def test_tiled_gemm_small_m_forced(ctx, orc):
-    """LGX_GEMM_TILED_MIN=1 routes every m > 1 through the tiled product: a
-    single row, ragged row tiles and rows spanning workgroup tiles agree with
-    the oracle and with the streaming kernels."""
+@pytest.mark.parametrize("rows,grp", [(128, 0), (64, 0), (32, 0), (64, 1), (64, 2), (32, 4), (128, 1)])
+def test_tiled_gemm_small_m_forced(ctx, orc, rows, grp):
+    """LGX_GEMM_TILED_MIN=2 routes every m > 1 through the tiled product with
+    128, 64 or 32 activation rows per workgroup and 1, 2 or 4 ranges per
+    group (0: chosen by grid size): a ragged row tile, rows spanning
+    workgroup tiles and 9 ranges (groups of 4 + 4 + 1, 2 + 2 + 2 + 2 + 1, or
+    single ranges) agree with the oracle."""
     n, k = 1536, 8960
     qs, d = orc.gen_q8_matrix(3, 5, n, k)
     x = orc.gen_normal_f32(3, 6, (140, k))
     xq, xd = orc.quantize_q8_0(x)
     ref = orc.q8_gemm(qs, d, xq, xd)
-    c = _ctx_with_env(LGX_GEMM_TILED_MIN=2)
+    c = _ctx_with_env(LGX_GEMM_TILED_MIN=2, LGX_GEMM_TILED_ROWS=rows, LGX_GEMM_TILED_GRP=grp)
     try:
         W = c.q8_matrix(qs, d)
         gx, gd = c.to_device(xq), c.to_device(xd)
-        for m in (2, 15, 16, 17, 64, 140):
+        for m in (2, 15, 17, 32, 33, 64, 140):
             assert np.array_equal(host(c.q8_gemm(W, gx[:m].contiguous(), gd[:m].contiguous())),
                                   ref[:m]), m
     finally:
