@@ -1128,38 +1128,55 @@ __device__ __forceinline__ float lgx_expf(float x) {
     return p * __uint_as_float((uint32_t)(n + 127) << 23);
 }
 
+// p of lane J of the lane's 16-lane row (DPP row_newbcast: J is an immediate)
+template <int J>
+__device__ __forceinline__ float row_bcast(int v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0x150 + J, 0xf, 0xf, false));
+}
+template <int J>
+struct IdxC {
+    static constexpr int value = J;
+};
+template <int J, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (J < N) {
+        f(IdxC<J>{});
+        static_for<J + 1, N>(f);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Paged GQA decode attention, split over 256-token chunks.
 //
 // grid = (chunks, B * hkv), 256 threads: one workgroup per (sequence, KV
 // head, chunk) serves all GQ query heads of the group, so every K/V row is
 // read once per group.  Loads: thread t requests its token's whole K row
-// into registers, then the workgroup's direct global->LDS loads
-// (global_load_lds_dwordx4, 1 KiB per wave instruction) bring the chunk's V
-// pages into LDS in token order; both are in flight together and V lands
-// while the scores are computed (D = 64; at D = 128 V is streamed in phase
-// 3).  Phase 1: thread t runs the canonical score chain over d for the GQ
-// heads (query rows read as workgroup-uniform values).  Phase 2: per head
-// the chunk max (exact in any order), p_t = lgx_expf(s_t - m), and the
-// halving-tree sum of the 256 slots.  Phase 3: the canonical chain over the
-// chunk's tokens, o[i] = fmaf(p_t, V_t[i], o[i]), for every (head, i).
-// Partials (o_c, m_c, l_c) go to `part`; lgx_k_attn_combine merges the
-// chunks.  LDS: 2 KiB per head (+ 32 KiB of V at D = 64).
+// into registers; once it has landed, the workgroup's direct global->LDS
+// loads (global_load_lds_dwordx4, 1 KiB per wave instruction) bring the
+// first 32 KiB of the chunk's V rows into LDS in token order (the whole
+// chunk at D = 64, tokens 0..127 at D = 128; at D = 128 each thread also
+// loads 128 bytes of tokens 128..255 into registers), and V lands while the
+// scores are computed.  Phase 1: thread t runs the canonical score chain
+// over d for the GQ heads (query rows read as workgroup-uniform values).
+// Phase 2: per head the chunk max (exact in any order), p_t =
+// lgx_expf(s_t - m), and the halving-tree sum of the 256 slots.  Phase 3:
+// the canonical chain over the chunk's tokens, o[i] = fmaf(p_t, V_t[i],
+// o[i]), for every (head, i).  Partials (o_c, m_c, l_c) go to `part`;
+// lgx_k_attn_combine merges the chunks.  LDS: 32 KiB of V + 1088 bytes per
+// head.
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
-#define LGX_PV_VB 8
 
-// The chunk's V rows (n tokens of KV head g, pages pg_s) into v_s in token
-// order: wave instruction j moves bytes [1024 j, +1024) of the chunk, which
-// lie in page j / (D/32).  Every instruction is issued, so the compiler can
-// count them and wait for the K loads alone before the scores; one for a
-// page past the last token re-reads the chunk's first page (a cache hit)
-// into slots that are never used.
+// The chunk's first 32 KiB of V rows (KV head g, pages pg_s) into v_s in
+// token order: wave instruction j moves bytes [1024 j, +1024), which lie in
+// page j / (D/32).  Every instruction is issued, so the compiler can count
+// them; one for a page past the last token re-reads the chunk's first page
+// (a cache hit) into slots that are never used.
 template <int D>
 __device__ __forceinline__ void attn_stage_v(const lgx_attn_args& a, int g, int n,
                                              const int* pg_s, uint16_t* v_s, int wave, int lane) {
     constexpr int PER_PAGE = LGX_PAGE * D * 2 / 1024;   // wave instructions per page
-    constexpr int NJ = LGX_ATTN_CHUNK * D * 2 / 1024;   // per chunk
+    constexpr int NJ = 32768 / 1024;
 #pragma unroll
     for (int i = 0; i < NJ / 4; ++i) {
         const int j = wave + 4 * i;
@@ -1174,16 +1191,18 @@ __device__ __forceinline__ void attn_stage_v(const lgx_attn_args& a, int g, int 
 template <int D, int GQ>
 __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
     constexpr int C = LGX_ATTN_CHUNK;
-    // V through LDS at D = 64 (47 KiB with 7 heads: 3 workgroups per CU).
-    // At D = 128 the 64 KiB buffer would leave 2 workgroups per CU, fewer
-    // than the loads need in flight; there V is read from the pages directly.
-    constexpr bool VLDS = D == 64;
-    __shared__ __align__(16) uint16_t v_s[VLDS ? C * D : 8];
-    __shared__ __align__(16) float p_s[GQ][C];
-    __shared__ float t_s[GQ][C];
+    constexpr int VT = 32768 / (2 * D);          // tokens of V in LDS at once
+    constexpr int NVS = C / VT;                   // V stages: 1 (D = 64) or 2 (D = 128)
+    constexpr int CPR = D / 8;                    // 16-byte pieces per row
+    constexpr int NVB = NVS > 1 ? VT * CPR / 256 : 1;   // register pieces per thread
+    static_assert(NVS <= 2 && GQ <= 8, "chunk V in at most two 32 KiB stages, 8 heads");
+    __shared__ __align__(16) uint16_t v_s[VT * D];
+    // p rows padded by 16 floats: rows of neighbouring heads start 16 banks apart
+    __shared__ __align__(16) float p_s[GQ][C + 16];
     __shared__ float mx_s[GQ][4];
     __shared__ int pg_s[C / LGX_PAGE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = blockIdx.x, bg = blockIdx.y;
     const int b = bg / a.hkv, g = bg - b * a.hkv;
     const int L = min(a.seq_len[b] + a.len_add, a.maxlen);
@@ -1205,22 +1224,33 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
 #pragma unroll
     for (int h = 0; h < GQ; ++h) s[h] = 0.0f;
     const bool valid = tid < n;
-    uint4 kv[D / 8];
+    uint4 kv[CPR];
     {
         const uint4* kr = (const uint4*)(a.kpages +
                                          (((int64_t)pg_s[tid >> 4] * a.hkv + g) * LGX_PAGE + (tid & 15)) * D);
 #pragma unroll
-        for (int j = 0; j < D / 8; ++j) kv[j] = kr[j];
+        for (int j = 0; j < CPR; ++j) kv[j] = kr[j];
     }
-    if constexpr (VLDS) {
-        // the K row has arrived before V is requested: the compiler waits
-        // for every outstanding load before the first use of any of them
-        // once the LDS loads are in flight, so V's transfer overlaps the
-        // score chain only when it is requested after K is in registers
+    // the K row has arrived before V is requested: the compiler waits for
+    // every outstanding load before the first use of any of them once the
+    // LDS loads are in flight, so V's transfer overlaps the score chain only
+    // when it is requested after K is in registers
 #pragma unroll
-        for (int j = 0; j < D / 8; ++j)
-            asm volatile("" : "+v"(kv[j].x), "+v"(kv[j].y), "+v"(kv[j].z), "+v"(kv[j].w));
-        attn_stage_v<D>(a, g, n, pg_s, v_s, wave, lane);
+    for (int j = 0; j < CPR; ++j)
+        asm volatile("" : "+v"(kv[j].x), "+v"(kv[j].y), "+v"(kv[j].z), "+v"(kv[j].w));
+    attn_stage_v<D>(a, g, n, pg_s, v_s, wave, lane);
+    // D = 128: tokens VT.. of V, piece q = 256 i + tid of the second stage
+    // (coalesced: 16 lanes per row), stored to v_s after the first stage
+    // (rows past the chunk's end read a real page slot: pg_s is clamped)
+    u32x4 vb[NVB];
+    const bool two = NVS > 1 && n > VT;           // uniform in the workgroup
+    if constexpr (NVS > 1) {
+#pragma unroll
+        for (int i = 0; i < NVB; ++i) {
+            const int q = 256 * i + tid, tk = VT + q / CPR;
+            vb[i] = *(const u32x4*)(a.vpages + (((int64_t)pg_s[tk >> 4] * a.hkv + g) * LGX_PAGE + (tk & 15)) * D +
+                                    (q % CPR) * 8);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);           // keep every load ahead of the FMAs
     if (valid) {
@@ -1230,7 +1260,7 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
         const __attribute__((address_space(4))) float* qb =
             (const __attribute__((address_space(4))) float*)(a.q + ((int64_t)b * a.hq + h0) * D);
 #pragma unroll
-        for (int j = 0; j < D / 8; ++j) {
+        for (int j = 0; j < CPR; ++j) {
             const float kf[8] = {h2f(kv[j].x & 0xffffu), h2f(kv[j].x >> 16), h2f(kv[j].y & 0xffffu),
                                  h2f(kv[j].y >> 16),     h2f(kv[j].z & 0xffffu), h2f(kv[j].z >> 16),
                                  h2f(kv[j].w & 0xffffu), h2f(kv[j].w >> 16)};
@@ -1254,21 +1284,16 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
 #pragma unroll
     for (int h = 0; h < GQ; ++h) {
         const float m = fmaxf(fmaxf(mx_s[h][0], mx_s[h][1]), fmaxf(mx_s[h][2], mx_s[h][3]));
-        const float p = valid ? lgx_expf(s[h] - m) : 0.0f;
-        p_s[h][tid] = p;
-        t_s[h][tid] = p;
+        p_s[h][tid] = valid ? lgx_expf(s[h] - m) : 0.0f;
     }
-    if constexpr (VLDS) __builtin_amdgcn_s_waitcnt(0);   // this wave's V loads are in LDS
-    __syncthreads();                             // ... and every other wave's
-    if (tid < 128) {
-#pragma unroll
-        for (int h = 0; h < GQ; ++h) t_s[h][tid] = t_s[h][tid] + t_s[h][tid + 128];
-    }
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0);               // this wave's first-stage V is in LDS
+    __syncthreads();                             // ... and every other wave's, and p
     if (tid < 64) {
+        // levels 128 and 64 of the tree from p_s, the rest across lanes
         float l[GQ];
 #pragma unroll
-        for (int h = 0; h < GQ; ++h) l[h] = t_s[h][tid] + t_s[h][tid + 64];
+        for (int h = 0; h < GQ; ++h)
+            l[h] = (p_s[h][tid] + p_s[h][tid + 128]) + (p_s[h][tid + 64] + p_s[h][tid + 192]);
 #pragma unroll
         for (int s2 = 32; s2 >= 1; s2 >>= 1) {
 #pragma unroll
@@ -1284,20 +1309,19 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
             }
         }
     }
-    // phase 3: o_c[i] = chain_t fmaf(p_t, V_t[i], o).  D = 64: thread =
-    // (dimension pair, head group) reads its pair of each V row from LDS (a
-    // wave reads whole rows, conflict-free).  D = 128: one wave streams the
-    // V rows from the pages (below).  n is workgroup-uniform, so the loop
-    // bounds do not diverge.
-    constexpr int NP = D / 2;                     // dimension pairs
-    constexpr int NHG = 256 / NP;                 // head groups
-    constexpr int HPG = (GQ + NHG - 1) / NHG;     // heads per group
-    const int ip = tid % NP, hg = tid / NP;
-    float o[HPG][2];
+    // phase 3: o_c[i] = chain_t fmaf(p_t, V_t[i], o).  n is
+    // workgroup-uniform, so the loop bounds do not diverge.
+    if constexpr (D == 64) {
+        // thread = (dimension pair, head group) reads its pair of each V
+        // row from LDS (a wave reads whole rows, conflict-free), four
+        // tokens per step with p as one float4
+        constexpr int NP = D / 2;                 // dimension pairs
+        constexpr int NHG = 256 / NP;             // head groups
+        constexpr int HPG = (GQ + NHG - 1) / NHG; // heads per group
+        const int ip = tid % NP, hg = tid / NP;
+        float o[HPG][2];
 #pragma unroll
-    for (int k = 0; k < HPG; ++k) o[k][0] = o[k][1] = 0.0f;
-    if constexpr (VLDS) {
-        // four tokens per step, p as one float4
+        for (int k = 0; k < HPG; ++k) o[k][0] = o[k][1] = 0.0f;
         const uint32_t* vs = (const uint32_t*)v_s + ip;
         int t = 0;
         for (; t + 4 <= n; t += 4) {
@@ -1330,71 +1354,74 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
                 }
             }
         }
-    } else {
-        // One wave: lane = (dimension octet j, head slot hs), chains of heads
-        // hs and hs + 4 for 8 dimensions; each token's V row is one 16-byte
-        // load per lane (the four head slots share it), two batches of
-        // LGX_PV_VB tokens in flight.  The other waves are done.
-        constexpr int VB = LGX_PV_VB;
-        static_assert(D == 128 && GQ <= 8, "single-wave PV covers 128 dimensions, 8 heads");
-        if (wave != 0) return;
-        const int j = lane & 15, hs = lane >> 4;
-        const int hh[2] = {hs, hs + 4};
-        float acc[2][8];
 #pragma unroll
-        for (int k = 0; k < 2; ++k)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[k][e] = 0.0f;
-        const uint16_t* vbase = a.vpages + (int64_t)g * LGX_PAGE * D + 8 * j;
-        // token t's row (clamped to the last token: always a real page slot)
-        auto ld = [&](int tp, uint4 (&vv)[VB]) {
-#pragma unroll
-            for (int u = 0; u < VB; ++u) {
-                const int t = min(tp + u, n - 1);
-                vv[u] = *(const uint4*)(vbase + ((int64_t)pg_s[t >> 4] * a.hkv * LGX_PAGE + (t & 15)) * D);
+        for (int k = 0; k < HPG; ++k) {
+            const int h = hg + NHG * k;
+            if (h < GQ) {
+                float* pp = a.part + (((int64_t)b * a.hq + h0 + h) * a.nchunk + c) * (D + 2) + 2 * ip;
+                pp[0] = o[k][0];
+                pp[1] = o[k][1];
             }
+        }
+    } else {
+        // D = 128, all four waves: wave w = (head group hgp = w % HGN,
+        // dimension slice dq = w / HGN); 16-lane row rho is head 4 hgp + rho,
+        // lane k owns DL dimensions of the slice.  The row's p_t comes from
+        // lane t%16 of a 16-token register (DPP row_newbcast), V_t from LDS
+        // (a row reads 16 DL consecutive halves, the four rows the same ones).
+        constexpr int HGN = (GQ + 3) / 4;         // head groups of 4
+        constexpr int WPD = 4 / HGN;              // dimension slices
+        constexpr int DL = D / WPD / 16;          // dimensions per lane: 1, 2 or 4
+        const int hgp = wave % HGN, dq = wave / HGN;
+        const int rho = lane >> 4, k = lane & 15;
+        const int h = 4 * hgp + rho, hc = min(h, GQ - 1);
+        const int dcol = dq * (D / WPD) + DL * k;
+        float o[DL];
+#pragma unroll
+        for (int e = 0; e < DL; ++e) o[e] = 0.0f;
+        auto pv_token = [&](int tl, float pb) {  // tl: row of the V stage
+            float vf[DL];
+            if constexpr (DL == 4) {
+                const uint2 vv = *(const uint2*)(v_s + tl * D + dcol);
+                vf[0] = h2f(vv.x & 0xffffu);
+                vf[1] = h2f(vv.x >> 16);
+                vf[2] = h2f(vv.y & 0xffffu);
+                vf[3] = h2f(vv.y >> 16);
+            } else if constexpr (DL == 2) {
+                const uint32_t vv = *(const uint32_t*)(v_s + tl * D + dcol);
+                vf[0] = h2f(vv & 0xffffu);
+                vf[1] = h2f(vv >> 16);
+            } else {
+                vf[0] = h2f(v_s[tl * D + dcol]);
+            }
+#pragma unroll
+            for (int e = 0; e < DL; ++e) o[e] = fmaf(pb, vf[e], o[e]);
         };
-        auto use = [&](int tp, const uint4 (&vv)[VB]) {
-#pragma unroll
-            for (int u = 0; u < VB; ++u) {
-                if (tp + u < n) {
-                    const float ve[8] = {h2f(vv[u].x & 0xffffu), h2f(vv[u].x >> 16), h2f(vv[u].y & 0xffffu),
-                                         h2f(vv[u].y >> 16),     h2f(vv[u].z & 0xffffu), h2f(vv[u].z >> 16),
-                                         h2f(vv[u].w & 0xffffu), h2f(vv[u].w >> 16)};
-#pragma unroll
-                    for (int k = 0; k < 2; ++k) {
-                        const float pt = p_s[min(hh[k], GQ - 1)][tp + u];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) acc[k][e] = fmaf(pt, ve[e], acc[k][e]);
-                    }
+        auto pv_stage = [&](int tb) {            // tokens [tb, min(n, tb + VT)) from v_s
+            const int te = min(n, tb + VT);
+            for (int ts = tb; ts < te; ts += 16) {
+                const int pr = __builtin_bit_cast(int, p_s[hc][ts + k]);
+                if (ts + 16 <= te) {
+                    static_for<0, 16>([&](auto J) { pv_token(ts + J.value - tb, row_bcast<J.value>(pr)); });
+                } else {
+                    static_for<0, 16>([&](auto J) {
+                        if (ts + J.value < te) pv_token(ts + J.value - tb, row_bcast<J.value>(pr));
+                    });
                 }
             }
         };
-        uint4 va[VB], vb2[VB];
-        ld(0, va);
-        for (int tp = 0; tp < n; tp += 2 * VB) {
-            ld(tp + VB, vb2);
-            use(tp, va);
-            ld(tp + 2 * VB, va);
-            use(tp + VB, vb2);
-        }
+        pv_stage(0);
+        if (two) {
+            __syncthreads();                      // the first stage is fully read
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            if (hh[k] < GQ) {
-                float* pp = a.part + (((int64_t)b * a.hq + h0 + hh[k]) * a.nchunk + c) * (D + 2) + 8 * j;
-                *(float4*)pp = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
-                *(float4*)(pp + 4) = make_float4(acc[k][4], acc[k][5], acc[k][6], acc[k][7]);
-            }
+            for (int i = 0; i < NVB; ++i) *(u32x4*)(v_s + (256 * i + tid) * 8) = vb[i];
+            __syncthreads();
+            pv_stage(VT);
         }
-        return;
-    }
-#pragma unroll
-    for (int k = 0; k < HPG; ++k) {
-        const int h = hg + NHG * k;
         if (h < GQ) {
-            float* pp = a.part + (((int64_t)b * a.hq + h0 + h) * a.nchunk + c) * (D + 2) + 2 * ip;
-            pp[0] = o[k][0];
-            pp[1] = o[k][1];
+            float* pp = a.part + (((int64_t)b * a.hq + h0 + h) * a.nchunk + c) * (D + 2) + dcol;
+#pragma unroll
+            for (int e = 0; e < DL; ++e) pp[e] = o[e];
         }
     }
 }
@@ -2353,22 +2380,6 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled32(const lg
 //            comes from lane t%16 of a 16-token register (DPP row_newbcast).
 // ---------------------------------------------------------------------------
 #define PFA_QB 4
-// p of lane J of the lane's 16-lane row (DPP row_newbcast: J is an immediate)
-template <int J>
-__device__ __forceinline__ float row_bcast(int v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(v, 0x150 + J, 0xf, 0xf, false));
-}
-template <int J>
-struct IdxC {
-    static constexpr int value = J;
-};
-template <int J, int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (J < N) {
-        f(IdxC<J>{});
-        static_for<J + 1, N>(f);
-    }
-}
 template <int D>
 __device__ __forceinline__ int pfa_swz(int t) {
     return D == 128 ? (t & 15) : ((t >> 1) & 7);
