@@ -22,6 +22,11 @@ against the dense int8 peak): at these M the products are HBM- and
 epilogue-bound, far from the MFMA roofline.  `cpu_baseline` times the CPU oracle (a port: the reference has no
 CPU implementation of this path) on a bounded sample of the same step.
 
+`decode_attention`: the split-KV decode attention
+alone, B = 16, 12 query / 2 KV heads, head_dim 128, at L = 512, 4096, 32768
+and ragged lengths, per call against the HBM peak (K/V pages rotated past the
+Infinity Cache).
+
 The decode part (BASELINE.json configs 3 and 4) builds the seeded
 random-init Qwen2.5-0.5B- and 7B-shaped Q8_0 models on the device, prefills a
 random prompt for every sequence, and times the 64 greedy decode steps
@@ -241,6 +246,68 @@ def sustained_gemv(ctx, torch, iters=60):
             "GB_s": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
+ATTN_SHAPE = (16, 12, 2, 128)   # batch, query heads, KV heads, head_dim
+
+
+def attention_bench(ctx, torch, iters=50, seed=2):
+    """Config-2 decode attention over paged binary16 K/V in a random page
+    order: the split-KV chunk kernel and the chunk merge of one call, at
+    L = 512 / 4096 / 32768 and ragged lengths U[256, 32768].  The pages rotate
+    over enough copies (>= 2 x the Infinity Cache) that every call streams
+    them from HBM.  Algorithmic bytes per call: the attended K and V rows
+    (sum of L x hkv x d x 2 B x 2) plus q and the output.  Times are per
+    launch, from HIP events attached to each dispatch."""
+    B, hq, hkv, d = ATTN_SHAPE
+    chunk_k, merge_k = f"lgx_k_attn_chunk_d{d}_g{hq // hkv}", f"lgx_k_attn_combine_d{d}"
+    g = torch.Generator(device=ctx.dev)
+    g.manual_seed(seed)
+    ragged = torch.randint(256, 32769, (B,), generator=g, device=ctx.dev).tolist()
+    cases = [("L512", [512] * B), ("L4096", [4096] * B), ("L32768", [32768] * B),
+             ("ragged", ragged)]
+    res = {}
+    for name, lens in cases:
+        maxlen = max(lens)
+        maxp = -(-maxlen // 16)
+        npg = B * maxp
+        page_bytes = npg * hkv * 16 * d * 2
+        ncopy = max(1, -(-2 * MALL_BYTES // (2 * page_bytes)))
+        sets = []
+        for _ in range(ncopy):
+            k = torch.randn((npg, hkv, 16, d), generator=g, device=ctx.dev).half().view(torch.int16)
+            v = torch.randn((npg, hkv, 16, d), generator=g, device=ctx.dev).half().view(torch.int16)
+            pt = torch.randperm(npg, generator=g, device=ctx.dev).to(torch.int32).reshape(B, maxp)
+            sets.append((k, v, pt))
+        sl = torch.tensor(lens, dtype=torch.int32, device=ctx.dev)
+        q = torch.randn((B, hq, d), generator=g, device=ctx.dev)
+        o = torch.empty((B, hq, d), dtype=torch.float32, device=ctx.dev)
+        for i in range(3):
+            k, v, pt = sets[i % ncopy]
+            ctx.gqa_decode_attn(q, k, v, pt, sl, maxlen, out=o)
+        torch.cuda.synchronize()
+        ctx.kernel_timing(True)
+        for i in range(iters):
+            k, v, pt = sets[i % ncopy]
+            ctx.gqa_decode_attn(q, k, v, pt, sl, maxlen, out=o)
+        torch.cuda.synchronize()
+        ctx.kernel_timing(False)
+        (nc, tc), (nm, tm) = ctx.kernel_stats(chunk_k), ctx.kernel_stats(merge_k)
+        chunk_us, merge_us = tc / max(nc, 1) * 1e3, tm / max(nm, 1) * 1e3
+        kv = sum(lens) * hkv * d * 2 * 2
+        nbytes = kv + 2 * B * hq * d * 4
+        call_us = chunk_us + merge_us
+        res[name] = {
+            "kv_MiB": round(kv / 2**20, 1), "copies": ncopy,
+            "chunk_kernel_us": round(chunk_us, 2), "merge_us": round(merge_us, 2),
+            "GB_s": round(nbytes / call_us / 1e3, 1),
+            "frac": round(nbytes / call_us / 1e3 / HBM_PEAK_GBS, 4),
+            "chunk_kernel_GB_s": round(kv / chunk_us / 1e3, 1),
+        }
+        del sets, sl, q, o
+        torch.cuda.empty_cache()
+    return {"kernel": chunk_k, "shape": {"batch": B, "hq": hq, "hkv": hkv, "head_dim": d},
+            "unit": "GB/s", "peak": HBM_PEAK_GBS, "cases": res}
+
+
 DECODE_CONFIGS = {
     # BASELINE.json config 3 and 4: (shape, batch, prompt tokens, greedy steps)
     "config3": ("0.5b", 32, 2048, 64),
@@ -444,6 +511,11 @@ def main():
     print(f"[bench] sustained GEMV {SUSTAINED_SHAPE}: {sustained['us_per_launch']} us, "
           f"{sustained['GB_s']} GB/s", file=sys.stderr, flush=True)
     out["config"]["sustained_gemv_m1"] = sustained
+    attn = attention_bench(ctx, torch)
+    print("[bench] config-2 decode attention: " + ", ".join(
+        f"{k} {v['chunk_kernel_us'] + v['merge_us']:.1f} us {v['GB_s']} GB/s"
+        for k, v in attn["cases"].items()), file=sys.stderr, flush=True)
+    out["decode_attention"] = attn
     decode = {}
     for key in [k for k in args.decode.split(",") if k]:
         decode[key] = decode_bench(ctx, torch, key)

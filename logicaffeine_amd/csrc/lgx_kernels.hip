@@ -1429,41 +1429,50 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
 // Merge of the chunk partials of one (sequence, query head): M = max m_c,
 // w_c = lgx_expf(m_c - M), L = chain fmaf(w_c, l_c), O[i] = chain
 // fmaf(w_c, o_c[i]), out = O / L (0 for an empty sequence).  One workgroup of
-// D threads per (sequence, head); chunk values are loaded 8 at a time so
-// their loads overlap.
+// D threads per (sequence, head), called by every thread.  The maxima are
+// read with one load per thread and chunk stride D (the max is exact in any
+// order); w_c and l_c of up to 256 chunks at a time go to LDS, computed once
+// per chunk; thread i then runs both chains in chunk order, its o_c[i] loaded
+// 16 chunks at a time (the last group masked) so their loads overlap.
 template <int D>
 __device__ __forceinline__ float attn_merge(const lgx_attn_args& a, int bh) {
-    const int i = threadIdx.x;
+    constexpr int TCH = 256;                      // chunks per LDS tile
+    __shared__ float w_s[TCH], l_s[TCH], red_s[D / 64];
+    const int i = threadIdx.x, lane = i & 63, wave = i >> 6;
     const int qpr = max(a.qpr, 1);
     const int row = bh / a.hq, b = row / qpr;
     const int L = min(a.seq_len[b] + (row - b * qpr) + a.len_add, a.maxlen);
     const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
     const float* pp = a.part + (int64_t)bh * a.nchunk * (D + 2);
     float M = -__builtin_inff();
-    for (int c0 = 0; c0 < nc; c0 += 8) {
-        float mv[8];
+    for (int c = i; c < nc; c += D) M = fmaxf(M, pp[c * (D + 2) + D]);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) mv[u] = c0 + u < nc ? pp[(c0 + u) * (D + 2) + D] : -__builtin_inff();
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, shfl_xor_f(M, o));
+    if (lane == 0) red_s[wave] = M;
+    __syncthreads();
 #pragma unroll
-        for (int u = 0; u < 8; ++u) M = fmaxf(M, mv[u]);
-    }
+    for (int w = 0; w < D / 64; ++w) M = fmaxf(M, red_s[w]);
     float Ls = 0.0f, O = 0.0f;
-    for (int c0 = 0; c0 < nc; c0 += 8) {
-        float mv[8], lv[8], ov[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const bool on = c0 + u < nc;
-            const float* q = pp + (c0 + u) * (D + 2);
-            mv[u] = on ? q[D] : 0.0f;
-            lv[u] = on ? q[D + 1] : 0.0f;
-            ov[u] = on ? q[i] : 0.0f;
+    for (int c0 = 0; c0 < nc; c0 += TCH) {        // nc is uniform: every thread takes the barriers
+        const int cn = min(TCH, nc - c0);
+        __syncthreads();                          // the previous tile is consumed
+        for (int c = i; c < cn; c += D) {
+            const float* q = pp + (c0 + c) * (D + 2);
+            w_s[c] = lgx_expf(q[D] - M);
+            l_s[c] = q[D + 1];
         }
+        __syncthreads();
+        const float* po = pp + (int64_t)c0 * (D + 2) + i;
+        for (int c = 0; c < cn; c += 16) {
+            float ov[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            if (c0 + u < nc) {
-                const float w = lgx_expf(mv[u] - M);
-                Ls = fmaf(w, lv[u], Ls);
-                O = fmaf(w, ov[u], O);
+            for (int u = 0; u < 16; ++u) ov[u] = c + u < cn ? po[(c + u) * (D + 2)] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                if (c + u < cn) {                 // uniform
+                    Ls = fmaf(w_s[c + u], l_s[c + u], Ls);
+                    O = fmaf(w_s[c + u], ov[u], O);
+                }
             }
         }
     }
