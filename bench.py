@@ -48,7 +48,10 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 INT8_MFMA_PEAK_TOPS = 5000.0   # dense int8 MFMA, MI355X datasheet
-DOMINANT = ("lgx_k_q8_gemv_grp4", "lgx_k_q8_gemv_grp8", "lgx_k_q8_gemv_grp16")
+# the kernels the grouped M = 1 launch may use (LGX_GEMV=whole selects the
+# whole-K forms); the one with the most dispatches in the timed pass is reported
+DOMINANT = ("lgx_k_q8_gemv_grp4", "lgx_k_q8_gemv_grp8", "lgx_k_q8_gemv_grp16",
+            "lgx_k_q8_gemv_wg4", "lgx_k_q8_gemv_wg8", "lgx_k_q8_gemv_wg16")
 DOMINANT_USED = DOMINANT[2]
 # HBM bytes per dispatch of the grouped config-1 launch, from rocprofv3 --pmc
 # FETCH_SIZE and WRITE_SIZE passes of this script (--copy-calibration): the
@@ -460,6 +463,8 @@ def main():
 
     value = step_bytes(1) / (ms1_plain * 1e-3) / 1e9
     per_launch = gemv_launch_bytes()
+    if not gemv_ms:
+        raise SystemExit("bench: no dispatch of the grouped GEMV kernels was timed")
     achieved = per_launch / (gemv_ms * 1e-3) / 1e9
     out = {
         "metric": "Q8 GEMV HBM GB/s (% peak); batched Qwen decode tokens/sec on 1 MI355X",
