@@ -1379,30 +1379,27 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
         float o[DL];
 #pragma unroll
         for (int e = 0; e < DL; ++e) o[e] = 0.0f;
-        auto pv_token = [&](int tl, float pb) {  // tl: row of the V stage
-            float vf[DL];
-            if constexpr (DL == 4) {
-                const uint2 vv = *(const uint2*)(v_s + tl * D + dcol);
-                vf[0] = h2f(vv.x & 0xffffu);
-                vf[1] = h2f(vv.x >> 16);
-                vf[2] = h2f(vv.y & 0xffffu);
-                vf[3] = h2f(vv.y >> 16);
-            } else if constexpr (DL == 2) {
-                const uint32_t vv = *(const uint32_t*)(v_s + tl * D + dcol);
-                vf[0] = h2f(vv & 0xffffu);
-                vf[1] = h2f(vv >> 16);
-            } else {
-                vf[0] = h2f(v_s[tl * D + dcol]);
-            }
+        // a lane's DL halves of V row tl (as 2 words; DL <= 4)
+        auto v_load = [&](int tl) -> uint2 {
+            if constexpr (DL == 4) return *(const uint2*)(v_s + tl * D + dcol);
+            else if constexpr (DL == 2) return make_uint2(*(const uint32_t*)(v_s + tl * D + dcol), 0u);
+            else return make_uint2(v_s[tl * D + dcol], 0u);
+        };
+        auto pv_apply = [&](const uint2 vv, float pb) {
+            const float vf[4] = {h2f(vv.x & 0xffffu), h2f(vv.x >> 16), h2f(vv.y & 0xffffu), h2f(vv.y >> 16)};
 #pragma unroll
             for (int e = 0; e < DL; ++e) o[e] = fmaf(pb, vf[e], o[e]);
         };
+        auto pv_token = [&](int tl, float pb) { pv_apply(v_load(tl), pb); };   // tl: row of the V stage
         auto pv_stage = [&](int tb) {            // tokens [tb, min(n, tb + VT)) from v_s
             const int te = min(n, tb + VT);
             for (int ts = tb; ts < te; ts += 16) {
                 const int pr = __builtin_bit_cast(int, p_s[hc][ts + k]);
                 if (ts + 16 <= te) {
-                    static_for<0, 16>([&](auto J) { pv_token(ts + J.value - tb, row_bcast<J.value>(pr)); });
+                    // the 16 rows' reads issued together, then the chains
+                    uint2 vv[16];
+                    static_for<0, 16>([&](auto J) { vv[J.value] = v_load(ts + J.value - tb); });
+                    static_for<0, 16>([&](auto J) { pv_apply(vv[J.value], row_bcast<J.value>(pr)); });
                 } else {
                     static_for<0, 16>([&](auto J) {
                         if (ts + J.value < te) pv_token(ts + J.value - tb, row_bcast<J.value>(pr));
