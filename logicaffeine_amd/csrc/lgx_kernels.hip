@@ -1324,6 +1324,34 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
         for (int k = 0; k < HPG; ++k) o[k][0] = o[k][1] = 0.0f;
         const uint32_t* vs = (const uint32_t*)v_s + ip;
         int t = 0;
+        // 16 tokens per step: every read of the step (V pairs, p as float4)
+        // issued before the chains
+        for (; t + 16 <= n; t += 16) {
+            uint32_t vv[16];
+            float4 p4[HPG][4];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) vv[u] = vs[(t + u) * NP];
+#pragma unroll
+            for (int k = 0; k < HPG; ++k) {
+                const int h = min(hg + NHG * k, GQ - 1);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) p4[k][q] = *(const float4*)&p_s[h][t + 4 * q];
+            }
+#pragma unroll
+            for (int k = 0; k < HPG; ++k) {
+                if (hg + NHG * k < GQ) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float pt[4] = {p4[k][q].x, p4[k][q].y, p4[k][q].z, p4[k][q].w};
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            o[k][0] = fmaf(pt[u], h2f(vv[4 * q + u] & 0xffffu), o[k][0]);
+                            o[k][1] = fmaf(pt[u], h2f(vv[4 * q + u] >> 16), o[k][1]);
+                        }
+                    }
+                }
+            }
+        }
         for (; t + 4 <= n; t += 4) {
             uint32_t vv[4];
 #pragma unroll
