@@ -2579,23 +2579,23 @@ __device__ __forceinline__ void attn_prefill_body(const lgx_attn_args& a) {
     float o[DL];
 #pragma unroll
     for (int e = 0; e < DL; ++e) o[e] = 0.0f;
-    auto pv_token = [&](int t, float pb) {      // t: row of the stage tile
+    // a lane's DL halves of V row t of the stage tile (uint4: DL = 8; .xy: DL = 4)
+    auto v_load = [&](int t) -> uint4 {
         const int sw = pfa_swz<D>(t);
-        float vf[DL];
         if constexpr (D == 128) {
-            const uint4 vv = *(const uint4*)(kv_s + t * D + (k ^ sw) * 8);
-            const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                vf[2 * e] = h2f(w4[e] & 0xffffu);
-                vf[2 * e + 1] = h2f(w4[e] >> 16);
-            }
+            return *(const uint4*)(kv_s + t * D + (k ^ sw) * 8);
         } else {
             const uint2 vv = *(const uint2*)(kv_s + t * D + ((k >> 1) ^ sw) * 8 + (k & 1) * 4);
-            vf[0] = h2f(vv.x & 0xffffu);
-            vf[1] = h2f(vv.x >> 16);
-            vf[2] = h2f(vv.y & 0xffffu);
-            vf[3] = h2f(vv.y >> 16);
+            return make_uint4(vv.x, vv.y, 0u, 0u);
+        }
+    };
+    auto pv_apply = [&](const uint4 vv, float pb) {
+        const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+        float vf[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            vf[2 * e] = h2f(w4[e] & 0xffffu);
+            vf[2 * e + 1] = h2f(w4[e] >> 16);
         }
 #pragma unroll
         for (int e = 0; e < DL; ++e) o[e] = fmaf(pb, vf[e], o[e]);
@@ -2611,10 +2611,15 @@ __device__ __forceinline__ void attn_prefill_body(const lgx_attn_args& a) {
         for (int ts = tb; ts < te; ts += 16) {
             const int pr = __builtin_bit_cast(int, p_s[qp][hc][ts + k]);
             if (ts + 16 <= te) {
-                static_for<0, 16>([&](auto J) { pv_token(ts + J.value - tb, row_bcast<J.value>(pr)); });
+                // 8 rows' reads issued together, then their chains (twice)
+                uint4 va[8];
+                static_for<0, 8>([&](auto J) { va[J.value] = v_load(ts + J.value - tb); });
+                static_for<0, 8>([&](auto J) { pv_apply(va[J.value], row_bcast<J.value>(pr)); });
+                static_for<0, 8>([&](auto J) { va[J.value] = v_load(ts + 8 + J.value - tb); });
+                static_for<0, 8>([&](auto J) { pv_apply(va[J.value], row_bcast<8 + J.value>(pr)); });
             } else {
                 static_for<0, 16>([&](auto J) {
-                    if (ts + J.value < te) pv_token(ts + J.value - tb, row_bcast<J.value>(pr));
+                    if (ts + J.value < te) pv_apply(v_load(ts + J.value - tb), row_bcast<J.value>(pr));
                 });
             }
         }
