@@ -1259,17 +1259,23 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
         // read-only and scalar)
         const __attribute__((address_space(4))) float* qb =
             (const __attribute__((address_space(4))) float*)(a.q + ((int64_t)b * a.hq + h0) * D);
+        // at D = 128 the heads run in two passes over the K row (fewer query
+        // values live in scalar registers at once); each chain is unchanged
+        constexpr int HP = D == 128 ? (GQ + 1) / 2 : GQ;
+        static_for<0, (GQ + HP - 1) / HP>([&](auto P) {
+            constexpr int hlo = P.value * HP, hhi = hlo + HP < GQ ? hlo + HP : GQ;
 #pragma unroll
-        for (int j = 0; j < CPR; ++j) {
-            const float kf[8] = {h2f(kv[j].x & 0xffffu), h2f(kv[j].x >> 16), h2f(kv[j].y & 0xffffu),
-                                 h2f(kv[j].y >> 16),     h2f(kv[j].z & 0xffffu), h2f(kv[j].z >> 16),
-                                 h2f(kv[j].w & 0xffffu), h2f(kv[j].w >> 16)};
+            for (int j = 0; j < CPR; ++j) {
+                const float kf[8] = {h2f(kv[j].x & 0xffffu), h2f(kv[j].x >> 16), h2f(kv[j].y & 0xffffu),
+                                     h2f(kv[j].y >> 16),     h2f(kv[j].z & 0xffffu), h2f(kv[j].z >> 16),
+                                     h2f(kv[j].w & 0xffffu), h2f(kv[j].w >> 16)};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
+                for (int e = 0; e < 8; ++e) {
 #pragma unroll
-                for (int h = 0; h < GQ; ++h) s[h] = fmaf(qb[h * D + 8 * j + e], kf[e], s[h]);
+                    for (int h = hlo; h < hhi; ++h) s[h] = fmaf(qb[h * D + 8 * j + e], kf[e], s[h]);
+                }
             }
-        }
+        });
     }
     // phase 2: max, exp, halving-tree sum
 #pragma unroll
