@@ -1259,9 +1259,9 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
         // read-only and scalar)
         const __attribute__((address_space(4))) float* qb =
             (const __attribute__((address_space(4))) float*)(a.q + ((int64_t)b * a.hq + h0) * D);
-        // at D = 128 the heads run in two passes over the K row (fewer query
+        // the heads run in two passes over the K row (fewer query
         // values live in scalar registers at once); each chain is unchanged
-        constexpr int HP = D == 128 ? (GQ + 1) / 2 : GQ;
+        constexpr int HP = (GQ + 1) / 2;
         static_for<0, (GQ + HP - 1) / HP>([&](auto P) {
             constexpr int hlo = P.value * HP, hhi = hlo + HP < GQ ? hlo + HP : GQ;
 #pragma unroll
