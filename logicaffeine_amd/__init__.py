@@ -124,17 +124,17 @@ VALU_LANE_OPS_PEAK = 256 * 4 * 16 * 2.4e9
 def prefill_valu_ops(cfg: dict, B: int, P: int) -> float:
     """Essential VALU lane operations of the canonical prefill of B prompts of
     P tokens (rows B x (P - 1) through the batched chunks, the last position
-    through the decode step): 3 per (row, output, 32-block) of every Q8_0
-    product (cvt of the int32 block dot, scale product, chain FMA) and 1 per
-    attention FMA (score chain over d and PV chain over the attended tokens,
-    per query head).  The last layer of a batched chunk stops after its KV
-    append (QKV product only)."""
+    through the decode step): 2 per (row, output, 32-block) of every Q8_0
+    product (cvt of the int32 block dot, chain FMA; the scale products come
+    from a rank-1 f16 MFMA) and 1 per attention FMA (score chain over d and PV
+    chain over the attended tokens, per query head).  The last layer of a
+    batched chunk stops after its KV append (QKV product only)."""
     H, I, d = cfg["hidden"], cfg["inter"], cfg["head_dim"]
     hq, hkv, L, V = cfg["n_heads"], cfg["n_kv"], cfg["n_layers"], cfg["vocab"]
     qkv = (hq + 2 * hkv) * d * H / 32
     full = qkv + (H * hq * d + 2 * I * H + H * I) / 32
     rows = B * (P - 1)
-    gemm = 3.0 * (rows * ((L - 1) * full + qkv) + B * L * full)
+    gemm = 2.0 * (rows * ((L - 1) * full + qkv) + B * L * full)
     gemm += B * V * H * (1.0 if cfg["tied"] else 3.0 / 32)
     # attention: row at position p attends p + 1 tokens (2d FMAs per head each)
     att_rows = B * (P - 1) * P / 2.0            # sum over p < P - 1 of (p + 1)

@@ -23,6 +23,8 @@
 #include "lgx_kargs.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Streaming 128-bit load of weight data (read once per call: non-temporal).
@@ -2166,7 +2168,10 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_act_to_t16(const lgx_act
 // i32_16x16x32_i8 per (block, weight tile, activation tile) with the weight
 // tile as A, so lane (r, c) of a result holds weight rows 4c..4c+3 of the
 // tile against activation row r; the epilogue runs the canonical chain
-// acc = fmaf((float)s, f32(dw) * f32(dx), acc) of each element.  When a
+// acc = fmaf((float)s, f32(dw) * f32(dx), acc) of each element, the scale
+// products of a (block, weight tile, activation tile) coming from one rank-1
+// f16 MFMA (16x16x16) with the same lane layout, so the VALU does two
+// operations per element (convert, fma).  When a
 // range ends its values fold into the group's subtree (a binary counter over
 // at most four ranges: earlier + later, as in the level-by-level tree) and
 // the group's values go to part[g]: aligned groups of a power-of-two number
@@ -2223,6 +2228,7 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a) {
     const int pend = min(pg0 + gpairs, np);
     const int nst = (pend - pg0 + LGX_TG_S - 1) / LGX_TG_S;
     const v4i zero = {0, 0, 0, 0};
+    const v4f zerof = {0.0f, 0.0f, 0.0f, 0.0f};
 
     // Direct loads of a stage (pairs pair0 .. pair0 + S - 1, clamped to the
     // group): uniform base + per-lane byte offset fixed over the stages.
@@ -2277,16 +2283,18 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a) {
     // One stage: its products from `cur` while the next stage loads into `nxt`.
     auto run = [&](int q, TgSmem<WM>& cur, TgSmem<WM>& nxt) {
         __syncthreads();                          // stage q landed; stage q-1 fully read
-        uint4 A[LGX_TG_S][2], B[LGX_TG_S][WM], DW[LGX_TG_S][2];
-        uint32_t DX[LGX_TG_S][WM];
+        uint4 A[LGX_TG_S][2], B[LGX_TG_S][WM];
+        uint32_t DWR[LGX_TG_S][2], DX[LGX_TG_S][WM];
 #pragma unroll
         for (int s = 0; s < LGX_TG_S; ++s) {
             A[s][0] = cur.w[2 * wn][s][lane];
             A[s][1] = cur.w[2 * wn + 1][s][lane];
 #pragma unroll
             for (int j = 0; j < WM; ++j) B[s][j] = cur.x[WM * wm + j][s][lane];
-            DW[s][0] = *(const uint4*)&cur.dw[s][(2 * wn) * 16 + 4 * c];
-            DW[s][1] = *(const uint4*)&cur.dw[s][(2 * wn + 1) * 16 + 4 * c];
+            // weight scale pair of row r of tiles 2wn, 2wn+1 (lanes 16.. read
+            // the same rows; their values meet zeros in the scale product)
+            DWR[s][0] = cur.dw[s][(2 * wn) * 16 + r];
+            DWR[s][1] = cur.dw[s][(2 * wn + 1) * 16 + r];
             const uint32_t* dxr = &cur.dx[s][r * MTILES + WM * wm];
             if constexpr (WM == 4) {
                 const uint4 q4 = *(const uint4*)dxr;
@@ -2314,27 +2322,40 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a) {
                                     : (long)(((uint64_t)B[s][j].y << 32) | B[s][j].x);
                 return __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, zero, 0, 0, 0);
             };
-            auto ep = [&](int u, const v4i& d) {
+            // scale products dw[row 4c+v] x dx[row r] of product u as one
+            // rank-1 f16 MFMA with the same lane layout as the int8 result:
+            // A lanes 0..15 carry the weight scale pair (k = 0, 1), B lanes
+            // 0..15 this block's activation scale at k = blk and zeros
+            // elsewhere, so D = dw x dx + exact zeros.  f16 x f16 is exact in
+            // binary32 and the zeros make a -0 product +0, which is
+            // fmaf(dw, dx, +0) of the canonical epilogue.
+            auto sc = [&](int u) -> v4f {
                 const int blk = u / (2 * WM), i = (u / WM) & 1, j = u % WM;
-                const uint32_t dww[4] = {DW[s][i].x, DW[s][i].y, DW[s][i].z, DW[s][i].w};
-                const float dx = h2f(blk ? DX[s][j] >> 16 : DX[s][j] & 0xffffu);
+                const uint32_t bw = lane < 16 ? (blk ? DX[s][j] & 0xffff0000u : DX[s][j] & 0xffffu) : 0u;
+                const v4h av = __builtin_bit_cast(v4h, make_uint2(DWR[s][i], 0u));
+                const v4h bv = __builtin_bit_cast(v4h, make_uint2(bw, 0u));
+                return __builtin_amdgcn_mfma_f32_16x16x16f16(av, bv, zerof, 0, 0, 0);
+            };
+            auto ep = [&](int u, const v4i& d, const v4f& sp) {
+                const int i = (u / WM) & 1, j = u % WM;
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const float dw = h2f(blk ? dww[v] >> 16 : dww[v] & 0xffffu);
-                    // f16 x f16 is exact in binary32: fmaf(dw, dx, +0) is the
-                    // product (>= +0), one v_fma_mix from the binary16 halves
-                    acc[i][j][v] = fmaf((float)d[v], fmaf(dw, dx, 0.0f), acc[i][j][v]);
-                }
+                for (int v = 0; v < 4; ++v) acc[i][j][v] = fmaf((float)d[v], sp[v], acc[i][j][v]);
             };
             v4i dcur = mf(0);
+            v4f scur = sc(0);
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
                 v4i dnext = dcur;
-                if (u + 1 < NU) dnext = mf(u + 1);
+                v4f snext = scur;
+                if (u + 1 < NU) {
+                    dnext = mf(u + 1);
+                    snext = sc(u + 1);
+                }
                 __builtin_amdgcn_sched_barrier(0);
-                ep(u, dcur);
+                ep(u, dcur, scur);
                 __builtin_amdgcn_sched_barrier(0);
                 dcur = dnext;
+                scur = snext;
             }
         }
         const int done = LGX_TG_S * (q + 1);
