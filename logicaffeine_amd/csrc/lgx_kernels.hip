@@ -2324,15 +2324,19 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a) {
             };
             // scale products dw[row 4c+v] x dx[row r] of product u as one
             // rank-1 f16 MFMA with the same lane layout as the int8 result:
-            // A lanes 0..15 carry the weight scale pair (k = 0, 1), B lanes
-            // 0..15 this block's activation scale at k = blk and zeros
-            // elsewhere, so D = dw x dx + exact zeros.  f16 x f16 is exact in
-            // binary32 and the zeros make a -0 product +0, which is
-            // fmaf(dw, dx, +0) of the canonical epilogue.
+            // lanes 0..15 of A and B carry this block's weight and activation
+            // scales at k = blk, zeros elsewhere, so D = dw x dx + exact zeros.
+            // f16 x f16 is exact in binary32 and the zeros make a -0 product
+            // +0, which is fmaf(dw, dx, +0) of the canonical epilogue.
             auto sc = [&](int u) -> v4f {
                 const int blk = u / (2 * WM), i = (u / WM) & 1, j = u % WM;
-                const uint32_t bw = lane < 16 ? (blk ? DX[s][j] & 0xffff0000u : DX[s][j] & 0xffffu) : 0u;
-                const v4h av = __builtin_bit_cast(v4h, make_uint2(DWR[s][i], 0u));
+                // both operands keep only this block's half in lanes 0..15, so
+                // every other term is 0 x 0 (an infinite or NaN scale of the
+                // other block cannot leak in)
+                const uint32_t hm = blk ? 0xffff0000u : 0xffffu;
+                const uint32_t aw = lane < 16 ? DWR[s][i] & hm : 0u;
+                const uint32_t bw = lane < 16 ? DX[s][j] & hm : 0u;
+                const v4h av = __builtin_bit_cast(v4h, make_uint2(aw, 0u));
                 const v4h bv = __builtin_bit_cast(v4h, make_uint2(bw, 0u));
                 return __builtin_amdgcn_mfma_f32_16x16x16f16(av, bv, zerof, 0, 0, 0);
             };

@@ -238,6 +238,41 @@ def test_tiled_gemm_bit_exact(ctx, orc, n, k, m):
     assert np.array_equal(y, orc.q8_gemm(qs, d, xq, xd))
 
 
+@pytest.mark.parametrize("m,tiled_rows", [(1, 0), (16, 0), (64, 0), (140, 0), (64, 32)])
+def test_special_scales_bit_exact(ctx, orc, m, tiled_rows):
+    """Weight scales -0, the smallest binary16 denormal, the largest finite
+    value, +inf (rows 3: its products are +-inf or NaN) and NaN, and
+    activation scales that are denormal or zero, through the GEMV (m = 1),
+    the streaming products and the tiled product (m = 140, and m = 64 forced
+    through 32-row tiles): the outputs equal the oracle's, infinities and
+    NaNs in the same places.  The scale of the other block of a pair never
+    leaks into a block's scale product."""
+    n, k = 256, 2048
+    qs, d = orc.gen_q8_matrix(3, 9, n, k)
+    d = d.copy()
+    d[0, 0] = 0x8000                             # -0
+    d[1, 1] = 0x0001                             # smallest denormal
+    d[2, 2] = 0x7BFF                             # largest finite
+    d[3, 3] = 0x7C00                             # +inf (its pair-mate, block 2, is finite)
+    d[5, 4] = 0x7E00                             # NaN
+    d[6, 17] = 0x0200                            # denormal
+    x = orc.gen_normal_f32(3, 10, (m, k))
+    xq, xd = orc.quantize_q8_0(x)
+    xd = xd.copy()
+    xd[0, 7] = 0x0001                            # denormal activation scale
+    xd[m - 1, 8] = 0x0000                        # zero activation scale (nonzero quants)
+    ref = orc.q8_gemm(qs, d, xq, xd)
+    c = _ctx_with_env(LGX_GEMM_TILED_MIN=2, LGX_GEMM_TILED_ROWS=tiled_rows) if tiled_rows else ctx
+    try:
+        W = c.q8_matrix(qs, d)
+        y = host(c.q8_gemm(W, c.to_device(xq), c.to_device(xd)))
+    finally:
+        if c is not ctx:
+            c.close()
+    assert np.isinf(ref[:, 3]).any() and np.isnan(ref[:, 5]).all()
+    assert np.array_equal(y, ref, equal_nan=True)
+
+
 @pytest.mark.parametrize("rows,grp", [(128, 0), (64, 0), (32, 0), (64, 1), (64, 2), (32, 4), (128, 1)])
 def test_tiled_gemm_small_m_forced(ctx, orc, rows, grp):
     """LGX_GEMM_TILED_MIN=2 routes every m > 1 through the tiled product with
