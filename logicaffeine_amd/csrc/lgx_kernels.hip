@@ -960,25 +960,38 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
         }
     };
     float acc[MT][4];
+    // the LDS operands of unit i + 1 (activation slots and scales) are read
+    // while unit i's products run
+    auto ld_unit = [&](int pc, uint4 (&xv)[MT], float4 (&x0)[MT], float4 (&x1)[MT]) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            xv[mt] = xa_s[(mt * 16 + pc) * 64 + lane];
+            x0[mt] = *(const float4*)(dx_s + (2 * pc) * DXROWS + mt * 16 + 4 * c);
+            x1[mt] = *(const float4*)(dx_s + (2 * pc + 1) * DXROWS + mt * 16 + 4 * c);
+        }
+    };
     auto compute_batch = [&](int qb, const uint4 (&w)[PB], const uint32_t (&dw)[PB]) {
+        uint4 xvA[MT], xvB[MT];
+        float4 x0A[MT], x1A[MT], x0B[MT], x1B[MT];
+        ld_unit(min(PB * qb, last), xvA, x0A, x1A);
 #pragma unroll
         for (int i = 0; i < PB; ++i) {
             const int pi = PB * qb + i;
             const bool on = pi <= last;
-            const int pc = min(pi, last);
+            if (i + 1 < PB) ld_unit(min(pi + 1, last), xvB, x0B, x1B);
             const float dw0 = on ? h2f(dw[i] & 0xffffu) : 0.0f;
             const float dw1 = on ? h2f(dw[i] >> 16) : 0.0f;
             const long b0 = (long)(((uint64_t)w[i].y << 32) | w[i].x);
             const long b1 = (long)(((uint64_t)w[i].w << 32) | w[i].z);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                const uint4 xv = xa_s[(mt * 16 + pc) * 64 + lane];
+                const uint4 xv = xvA[mt];
                 const long a0 = (long)(((uint64_t)xv.y << 32) | xv.x);
                 const long a1 = (long)(((uint64_t)xv.w << 32) | xv.z);
                 const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, zero, 0, 0, 0);
                 const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, zero, 0, 0, 0);
-                const float4 x0 = *(const float4*)(dx_s + (2 * pc) * DXROWS + mt * 16 + 4 * c);
-                const float4 x1 = *(const float4*)(dx_s + (2 * pc + 1) * DXROWS + mt * 16 + 4 * c);
+                const float4 x0 = x0A[mt];
+                const float4 x1 = x1A[mt];
                 acc[mt][0] = fmaf((float)d0[0], dw0 * x0.x, acc[mt][0]);
                 acc[mt][1] = fmaf((float)d0[1], dw0 * x0.y, acc[mt][1]);
                 acc[mt][2] = fmaf((float)d0[2], dw0 * x0.z, acc[mt][2]);
@@ -991,6 +1004,12 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
             // keep each unit's MFMAs next to their epilogue: bounded live
             // ranges (occupancy) instead of all the batch's MFMA results
             __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                xvA[mt] = xvB[mt];
+                x0A[mt] = x0B[mt];
+                x1A[mt] = x1B[mt];
+            }
         }
     };
     auto store_tile = [&](int j) {
