@@ -63,7 +63,8 @@ def test_config2_ragged_long_bit_exact(ctx, orc):
     assert np.array_equal(out, orc.gqa_decode_attn(q, k, v, pt, np.asarray(lens, np.int32)))
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (28, 4, 128), (8, 8, 64), (8, 1, 128)])
+@pytest.mark.parametrize("hq,hkv,d", [(2 * g, 2, d) for d in (64, 128) for g in range(1, 9)]
+                         + [(28, 4, 128), (8, 8, 64), (8, 1, 128)])
 def test_head_layouts_bit_exact(ctx, orc, hq, hkv, d):
     B = 5
     lens = [1, 16, 255, 257, 1500]
