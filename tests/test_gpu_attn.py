@@ -140,6 +140,21 @@ def test_prefill_attn_bit_exact(ctx, orc, hq, hkv, d, ctx_len, P):
     assert np.array_equal(out, prefill_ref(orc, q, k, v, pt, ctx_len, P))
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("g", range(1, 9))
+def test_prefill_attn_head_groups_bit_exact(ctx, orc, g, d):
+    """Every head-group size the prefill kernels are built for, with one
+    fresh and one cached sequence whose rows cross a chunk boundary."""
+    hkv, ctx_len, P = 2, [0, 230], 35
+    B, hq = len(ctx_len), 2 * g
+    k, v, pt, maxp = make_cache(B, hkv, d, [c + P for c in ctx_len], seed=g * d)
+    q = orc.gen_normal_f32(5, g + d, (B * P, hq, d))
+    out = host(ctx.gqa_prefill_attn(ctx.to_device(q), ctx.to_device(k), ctx.to_device(v),
+                                    ctx.to_device(pt), ctx.to_device(np.asarray(ctx_len, np.int32)),
+                                    P, maxp * 16))
+    assert np.array_equal(out, prefill_ref(orc, q, k, v, pt, ctx_len, P))
+
+
 def test_prefill_attn_config4_shape_sampled(ctx, orc):
     """Config-4 head layout at a 4096-token context: 64 new rows after 4032
     cached tokens (17 chunks), checked on a sample of rows."""
