@@ -330,3 +330,34 @@ def test_generate_graph_replays_match_eager_and_oracle(name, ctx):
     assert e.value.status_name == "LGX_OUT_OF_BOUNDS"
     for m in (gg, ge, om):
         m.close()
+
+
+@pytest.mark.parametrize("env", [dict(LGX_GEMV_WGS="8"), dict(LGX_GEMV="whole", LGX_GEMV_WGS="8")])
+def test_single_sequence_decode_eight_wave_gemv(env):
+    """M = 1 decode steps with the eight-wave GEMV workgroups forced (the
+    grouped per-range kernels over Q8_0 and binary32 activations, then the
+    whole-K kernel) give the oracle's tokens."""
+    import os
+
+    from oracle import oracle as orc
+
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        c = lgx.Context(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k)
+            else:
+                os.environ[k] = v
+    cfg = orc.qwen_config("tiny_untied")
+    gm = lgx.Model(c, cfg, 41)
+    om = orc.Model(cfg, 41)
+    tok = np.array([5], np.int32)
+    dtok = c.to_device(tok)
+    for step in range(6):
+        gm.decode_step(dtok)
+        tok = om.step(np.arange(1), tok)
+        assert np.array_equal(host(dtok), tok), step
+    c.close()

@@ -207,7 +207,8 @@ def test_kernel_variants_agree(ctx, orc, n, k):
     ref = orc.q8_gemm(qs, d, xq, xd)
     for c in (ctx, _ctx_with_env(LGX_GEMV="dot4"), _ctx_with_env(LGX_GEMV="split"),
               _ctx_with_env(LGX_GEMV="whole"), _ctx_with_env(LGX_GEMV_WGS=4),
-              _ctx_with_env(LGX_GEMV_WGS=16), _ctx_with_env(LGX_WG_TARGET=3)):
+              _ctx_with_env(LGX_GEMV_WGS=8), _ctx_with_env(LGX_GEMV_WGS=16),
+              _ctx_with_env(LGX_WG_TARGET=3)):
         W = c.q8_matrix(qs, d)
         gx, gd = c.to_device(xq), c.to_device(xd)
         assert np.array_equal(host(c.q8q8_gemv(W, gx[0], gd[0])), ref[0])
@@ -357,6 +358,14 @@ def test_grouped_gemv_bit_exact(ctx, orc):
     for y, ref, W, x in zip(ys, refs, Ws, xs):
         assert np.array_equal(host(y), ref)
         assert np.array_equal(host(ctx.q8q8_gemv_quantize(W, x)), ref)
+    c8 = _ctx_with_env(LGX_GEMV_WGS=8)          # eight-wave workgroups
+    for (n, k), ref, i in zip(shapes, refs, range(len(shapes))):
+        qs, d = orc.gen_q8_matrix(4, 100 + i, n, k)
+        Ws[i] = c8.q8_matrix(qs, d)
+        xs[i] = c8.to_device(orc.gen_normal_f32(4, 200 + i, (1, k))[0])
+    for y, ref in zip(c8.q8q8_gemv_quantize_group(Ws, xs), refs):
+        assert np.array_equal(host(y), ref)
+    c8.close()
 
 
 def test_grouped_gemv_long_k_and_errors(ctx, orc):
