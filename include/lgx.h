@@ -97,6 +97,8 @@ void lgx_clear_error(void);
 
 /* Load `hsaco_path` (NULL: lgx_kernels.hsaco beside liblgx.so) on `device`. */
 lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out);
+/* Fails with LGX_INVALID_ARGUMENT (and frees nothing) while an lgx_model
+ * created on ctx has not been destroyed. */
 lgx_status lgx_ctx_destroy(lgx_ctx* ctx);
 /* Number of kernel launches made through `ctx` (AotNativeFn::call_count). */
 uint64_t lgx_ctx_launch_count(const lgx_ctx* ctx);
@@ -296,7 +298,11 @@ lgx_status lgx_model_destroy(lgx_model* m);
 lgx_status lgx_model_reset(lgx_model* m, void* stream);
 /* One greedy decode step for sequences 0..B-1: tokens[b] (device int32) is
  * the current token of sequence b, appended at position seq_len[b]; on return
- * (stream order) tokens[b] holds the argmax next token and seq_len[b] += 1. */
+ * (stream order) tokens[b] holds the argmax next token and seq_len[b] += 1.
+ * Sequence lengths are tracked on the host as well (seq_len changes only
+ * through these calls): a step that would take a sequence past max_seq fails
+ * with LGX_OUT_OF_BOUNDS before anything is launched; the same holds for
+ * lgx_qwen_generate (nsteps positions) and lgx_qwen_prefill (P positions). */
 lgx_status lgx_qwen_decode_step(lgx_model* m, int32_t B, int32_t* tokens, void* stream);
 /* Feeds prompt[b][0..P) (device int32 [B][P]) for sequences 0..B-1 at
  * positions seq_len[b]..+P, filling the KV cache; next[b] receives the

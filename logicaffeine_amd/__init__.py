@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liblgx.so")
@@ -228,9 +229,14 @@ class Context:
         h = C.c_void_p()
         _check(lib().lgx_ctx_create(device, hsaco.encode() if hsaco else None, C.byref(h)))
         self.handle = h
+        self._models = weakref.WeakSet()   # live Models built on this ctx
 
     def close(self) -> None:
+        """Destroy the ctx; Models still open on it are closed first
+        (lgx_ctx_destroy refuses a ctx that live models still use)."""
         if self.handle:
+            for m in list(self._models):
+                m.close()
             _check(lib().lgx_ctx_destroy(self.handle))
             self.handle = None
 
@@ -532,6 +538,7 @@ class Model:
         h = C.c_void_p()
         _check(lib().lgx_model_create(ctx.handle, C.byref(self.c), seed, C.byref(h)))
         self.handle = h
+        ctx._models.add(self)
 
     def close(self) -> None:
         if self.handle:

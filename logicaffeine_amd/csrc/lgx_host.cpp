@@ -97,6 +97,10 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
 lgx_status lgx_ctx_destroy(lgx_ctx* c) {
     return guarded(__func__, [&]() -> lgx_status {
         if (!valid_ctx(c)) return fail(LGX_INVALID_HANDLE, "invalid lgx_ctx handle");
+        const int live = c->live_models.load();
+        if (live > 0)
+            return fail(LGX_INVALID_ARGUMENT,
+                        "%d lgx_model handle(s) still use this ctx: destroy them first", live);
         (void)hipSetDevice(c->device);
         for (auto& t : c->timed) {
             (void)hipEventDestroy(t.start);

@@ -192,6 +192,7 @@ struct lgx_ctx {
     int ncu = 256;                // compute units of the device
     int wg_target = 512;
     std::atomic<uint64_t> launches{0};
+    std::atomic<int> live_models{0};  // lgx_model handles built on this ctx and not destroyed
     void* ws = nullptr;       // range partials
     size_t ws_bytes = 0;
     std::mutex ws_mu;

@@ -53,6 +53,9 @@ struct lgx_model {
     float *cos_t = nullptr, *sin_t = nullptr;
     int32_t* page_table = nullptr;
     int32_t* seq_len = nullptr;
+    // host shadow of seq_len: every call that advances the device lengths
+    // updates it, so max_seq is checked before anything is launched
+    std::vector<int32_t> len;
     // activations for max_batch rows
     float* h = nullptr;
     float* xn = nullptr;
@@ -66,6 +69,7 @@ struct lgx_model {
     int32_t last_nr = 1;       // partial count of the last lm_head
     int32_t last_B = 0;        // batch of the last lm_head
     std::vector<void*> allocs;
+    bool counted = false;      // holds one of ctx->live_models
     // recorded decode steps (lgx_qwen_generate), one per (B, tokens) pair
     struct StepGraph {
         int32_t B;
@@ -87,6 +91,7 @@ struct lgx_model {
     } pf;
 
     ~lgx_model() {
+        if (counted) ctx->live_models.fetch_sub(1);
         for (StepGraph& g : graphs) (void)hipGraphExecDestroy(g.exec);
         if (capture) (void)hipStreamDestroy(capture);
         for (void* p : allocs) (void)hipFree(p);
@@ -438,6 +443,20 @@ lgx_status prefill_chunk(lgx_model* md, int B, int n, const int32_t* tokens, int
     return launch(c, K_ADVANCE, dim3(cdiv(B, 64)), dim3(64), av, stream);
 }
 
+// Sequences 0..B-1 about to grow by `add` positions: every new position
+// must stay below max_seq (the kernels would clamp it and overwrite the last
+// KV slot).  Checked on the host shadow, before any launch.
+lgx_status check_growth(const lgx_model* md, int B, int64_t add) {
+    for (int b = 0; b < B; ++b)
+        if ((int64_t)md->len[b] + add > md->c.max_seq)
+            return fail(LGX_OUT_OF_BOUNDS, "sequence %d: %d + %lld positions exceed max_seq %d", b,
+                        md->len[b], (long long)add, md->c.max_seq);
+    return LGX_OK;
+}
+void grow(lgx_model* md, int B, int64_t add) {
+    for (int b = 0; b < B; ++b) md->len[b] += (int32_t)add;
+}
+
 constexpr size_t kGraphMax = 8;
 
 // The recorded decode step for (B, tokens): captured on the model's private
@@ -491,7 +510,10 @@ lgx_status lgx_model_create(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t see
         if ((st = check_config(cfg)) != LGX_OK) return st;
         auto* m = new lgx_model();
         m->ctx = c;
+        m->counted = true;
+        c->live_models.fetch_add(1);
         m->c = *cfg;
+        m->len.assign(cfg->max_batch, 0);
         m->seed = seed;
         const lgx_qwen_config& cf = *cfg;
         const int H = cf.hidden, I = cf.intermediate, d = cf.head_dim, hq = cf.n_heads,
@@ -631,7 +653,10 @@ lgx_status lgx_model_reset(lgx_model* m, void* stream) {
         lgx_status st = enter(m->ctx);
         if (st != LGX_OK) return st;
         lgx_advance_args a{m->seq_len, m->c.max_batch, 0, 0};
-        return launch(m->ctx, K_ADVANCE, dim3(cdiv(m->c.max_batch, 64)), dim3(64), a, stream);
+        if ((st = launch(m->ctx, K_ADVANCE, dim3(cdiv(m->c.max_batch, 64)), dim3(64), a, stream)) != LGX_OK)
+            return st;
+        std::fill(m->len.begin(), m->len.end(), 0);
+        return LGX_OK;
     });
 }
 
@@ -643,8 +668,11 @@ lgx_status lgx_qwen_decode_step(lgx_model* m, int32_t B, int32_t* tokens, void* 
         if (!tokens) return fail(LGX_NULL_POINTER, "NULL tokens");
         if (B <= 0 || B > m->c.max_batch)
             return fail(LGX_OUT_OF_BOUNDS, "B = %d outside [1, %d]", B, m->c.max_batch);
-        if ((st = layers(m, B, tokens, 1, stream)) != LGX_OK) return st;
-        return head(m, B, tokens, stream);
+        if ((st = check_growth(m, B, 1)) != LGX_OK) return st;
+        if ((st = layers(m, B, tokens, 1, stream)) != LGX_OK || (st = head(m, B, tokens, stream)) != LGX_OK)
+            return st;
+        grow(m, B, 1);
+        return LGX_OK;
     });
 }
 
@@ -659,6 +687,7 @@ lgx_status lgx_qwen_generate(lgx_model* m, int32_t B, int32_t* tokens, int32_t n
             return fail(LGX_OUT_OF_BOUNDS, "B = %d outside [1, %d]", B, m->c.max_batch);
         if (nsteps < 0) return fail(LGX_INVALID_ARGUMENT, "nsteps = %d", nsteps);
         if (nsteps == 0) return LGX_OK;
+        if ((st = check_growth(m, B, nsteps)) != LGX_OK) return st;
         hipGraphExec_t exec = nullptr;
         // per-kernel timing attaches events to each dispatch, which a graph
         // cannot hold: launch those steps eagerly
@@ -670,6 +699,7 @@ lgx_status lgx_qwen_generate(lgx_model* m, int32_t B, int32_t* tokens, int32_t n
                        (st = head(m, B, tokens, stream)) != LGX_OK) {
                 return st;
             }
+            grow(m, B, 1);
             if (history)
                 LGX_HIP(hipMemcpyAsync(history + (int64_t)s * B, tokens, (size_t)B * 4,
                                        hipMemcpyDeviceToDevice, (hipStream_t)stream));
@@ -702,6 +732,7 @@ lgx_status lgx_qwen_prefill(lgx_model* m, int32_t B, int32_t P, const int32_t* p
             if ((int64_t)smax + P > m->c.max_seq)
                 return fail(LGX_OUT_OF_BOUNDS, "prompt of %d tokens after %d exceeds max_seq %d", P,
                             smax, m->c.max_seq);
+            std::copy(sl.begin(), sl.end(), m->len.begin());
             if ((st = prefill_alloc(m)) != LGX_OK) return st;
             const int chunk = m->pf.chunk;
             for (int p0 = 0; p0 < P - 1; p0 += chunk) {
@@ -710,9 +741,13 @@ lgx_status lgx_qwen_prefill(lgx_model* m, int32_t B, int32_t P, const int32_t* p
                 if ((st = prefill_chunk(m, B, n, prompt + p0, P, ncg, stream)) != LGX_OK) return st;
             }
             // the last position through the decode step: its logits give `next`
-            if ((st = layers(m, B, prompt + (P - 1), P, stream)) != LGX_OK) return st;
-            return head(m, B, next, stream);
+            if ((st = layers(m, B, prompt + (P - 1), P, stream)) != LGX_OK ||
+                (st = head(m, B, next, stream)) != LGX_OK)
+                return st;
+            grow(m, B, P);
+            return LGX_OK;
         }
+        if ((st = check_growth(m, B, P)) != LGX_OK) return st;
         for (int p = 0; p < P; ++p) {
             if ((st = layers(m, B, prompt + p, P, stream)) != LGX_OK) return st;
             if (p + 1 < P) {
@@ -723,6 +758,7 @@ lgx_status lgx_qwen_prefill(lgx_model* m, int32_t B, int32_t P, const int32_t* p
                 return st;
             }
         }
+        grow(m, B, P);
         return LGX_OK;
     });
 }

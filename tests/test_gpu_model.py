@@ -360,4 +360,85 @@ def test_single_sequence_decode_eight_wave_gemv(env):
         gm.decode_step(dtok)
         tok = om.step(np.arange(1), tok)
         assert np.array_equal(host(dtok), tok), step
+    gm.close()
+    om.close()
+    c.close()
+
+
+def test_ctx_destroy_refused_while_a_model_lives():
+    """lgx_ctx_destroy of a ctx that a live model still uses fails (the model
+    would read the freed ctx); after lgx_model_destroy it succeeds.
+    Context.close() closes its live models first."""
+    from oracle import oracle as orc
+
+    c = lgx.Context(0)
+    gm = lgx.Model(c, orc.qwen_config("tiny"), 3)
+    st = lgx.lib().lgx_ctx_destroy(c.handle)
+    assert lgx.STATUS_NAMES[st] == "LGX_INVALID_ARGUMENT"
+    assert b"destroy them first" in lgx.lib().lgx_last_error()
+    gm.decode_step(c.to_device(np.array([1], np.int32)))    # the model still works
+    gm.close()
+    assert lgx.lib().lgx_ctx_destroy(c.handle) == 0
+    c.handle = None
+    c2 = lgx.Context(0)
+    gm2 = lgx.Model(c2, orc.qwen_config("tiny"), 3)
+    c2.close()                                  # closes gm2, then the ctx
+    assert gm2.handle is None and c2.handle is None
+
+
+def test_max_seq_bound_on_every_path():
+    """A call that would grow a sequence past max_seq fails with
+    LGX_OUT_OF_BOUNDS before launching anything, on every path: decode step,
+    generate, one-token prefill, batched prefill and serial prefill; the
+    device lengths stay unchanged, and calls that end exactly at max_seq
+    succeed."""
+    import os
+
+    from oracle import oracle as orc
+
+    cfg = dict(orc.qwen_config("tiny"), max_seq=40)
+    B = cfg["max_batch"]
+    old = os.environ.get("LGX_PREFILL")
+    os.environ["LGX_PREFILL"] = "serial"
+    try:
+        cs = lgx.Context(0)
+    finally:
+        if old is None:
+            os.environ.pop("LGX_PREFILL")
+        else:
+            os.environ["LGX_PREFILL"] = old
+    c = lgx.Context(0)
+    rng = np.random.default_rng(3)
+
+    def lens(gm):
+        return [int(x) for x in dev_array(gm, "seq_len", np.int32, (B,))]
+
+    def refused(fn):
+        with pytest.raises(lgx.LgxError) as e:
+            fn()
+        assert e.value.status_name == "LGX_OUT_OF_BOUNDS"
+
+    for cc in (c, cs):
+        gm = lgx.Model(cc, cfg, 9)
+        prompt = cc.to_device(rng.integers(0, cfg["vocab"], size=(B, 37)).astype(np.int32))
+        tok = gm.prefill(prompt)                                 # 37
+        gm.decode_step(tok)                                      # 38
+        refused(lambda: gm.generate(tok, 3))                     # 41 > 40
+        gm.generate(tok, 2)                                      # 40 == max_seq
+        assert lens(gm) == [40] * B
+        refused(lambda: gm.decode_step(tok))
+        refused(lambda: gm.decode_step(tok[:1]))
+        refused(lambda: gm.generate(tok, 1))
+        refused(lambda: gm.prefill(prompt[:, :1].contiguous()))  # the one-token path
+        refused(lambda: gm.prefill(prompt[:, :2].contiguous()))
+        assert lens(gm) == [40] * B
+        gm.reset()
+        gm.prefill(prompt[:1, :1].contiguous())                  # seq 0 only: 1
+        p40 = cc.to_device(rng.integers(0, cfg["vocab"], size=(B, 40)).astype(np.int32))
+        refused(lambda: gm.prefill(p40))                         # seq 0 would reach 41
+        assert lens(gm) == [1] + [0] * (B - 1)
+        gm.prefill(p40[:1, :39].contiguous())                   # 1 + 39 == max_seq
+        assert lens(gm) == [40] + [0] * (B - 1)
+        gm.close()
+    cs.close()
     c.close()

@@ -148,7 +148,8 @@ def test_shape_errors_and_launch_count(ctx, orc):
 
 def test_workspace_reuse_across_shapes(ctx, orc):
     """Regression: alternating multi-range shapes and batch sizes on one ctx
-    (scratch reused, arrival counters must stay zero between calls)."""
+    reuse (and grow) its range-partials workspace; every call still equals the
+    oracle, so no call reads partials another call left behind."""
     cases = []
     for n, k in ((1536, 8960), (8960, 1536), (32, 2112), (1536, 8960)):
         qs, d = orc.gen_q8_matrix(1, 60 + n + k, n, k)
