@@ -156,6 +156,21 @@ lgx_status lgx_q8q8_gemv_quantize_group(lgx_ctx* ctx, int32_t count, const lgx_q
 lgx_status lgx_q8_gemm(lgx_ctx* ctx, const lgx_q8_matrix* W, const int8_t* xq,
                        const uint16_t* xd, int32_t m, float* y, void* stream);
 
+/* Allocation-free lgx_q8_gemm.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops and harnesses that forbid hipMalloc).  Same arguments, same
+ * results bit for bit as lgx_q8_gemm, but the intermediate buffers (range
+ * partials, the T16 activation copy of the large-m path) live in a fixed
+ * device array of LGX_NOALLOC_SCRATCH_BYTES that the library holds on each
+ * device until the process ends; the call allocates nothing and never uses
+ * per-kernel timing events.  A product whose intermediates exceed the
+ * array fails with LGX_OUT_OF_BOUNDS.  All calls on one device share the
+ * array: calls that overlap on one device (two streams, two threads, two
+ * ctxs) race. */
+#define LGX_NOALLOC_SCRATCH_BYTES (32u << 20)
+lgx_status lgx_q8_gemm_noalloc(lgx_ctx* ctx, const lgx_q8_matrix* W, const int8_t* xq,
+                               const uint16_t* xd, int32_t m, float* y, void* stream);
+
 /* ---- paged GQA decode attention ---- */
 /* out[b][h][:] = softmax(q[b][h] . K_t / sqrt(d)) V_t over the first
  * seq_len[b] cached tokens of sequence b, for KV head h / (hq/hkv).

@@ -55,6 +55,7 @@ SIGNATURES = {
     "lgx_q8_gemv_f32": (C.c_int, [_P, _P, _P, _P, _P]),
     "lgx_q8q8_gemv": (C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     "lgx_q8_gemm": (C.c_int, [_P, _P, _P, _P, _I32, _P, _P]),
+    "lgx_q8_gemm_noalloc": (C.c_int, [_P, _P, _P, _P, _I32, _P, _P]),
     "lgx_q8q8_gemv_quantize": (C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     "lgx_q8q8_gemv_quantize_group": (C.c_int, [_P, _I32, _P, _P, _P, _P]),
     "lgx_q8_range_count": (_I32, [_I32]),
@@ -423,6 +424,14 @@ class Context:
         y = t.empty((m, W.n), dtype=t.float32, device=self.dev) if y is None else y
         _check(lib().lgx_q8_gemm(self.handle, W.cstruct, xq.data_ptr(), xd.data_ptr(), m,
                                  y.data_ptr(), self._s()))
+        return y
+
+    def q8_gemm_noalloc(self, W: Q8Matrix, xq, xd, y):
+        """lgx_q8_gemm_noalloc: the same product into the caller's y, with the
+        library's fixed device scratch instead of any allocation."""
+        m = xq.shape[0]
+        _check(lib().lgx_q8_gemm_noalloc(self.handle, W.cstruct, xq.data_ptr(), xd.data_ptr(), m,
+                                         y.data_ptr(), self._s()))
         return y
 
     # ---- decode-step glue ------------------------------------------------

@@ -49,14 +49,28 @@ def build_kernels() -> str:
 
 
 HOST_SOURCES = ["lgx_host.cpp", "lgx_glue.cpp", "lgx_model.cpp", "lgx_gen.cpp"]
+BUILD_DIR = os.path.join(HERE, "_build")
+
+
+def build_scratch() -> str:
+    """lgx_scratch.hip: host code plus a gfx950 code object holding only the
+    no-alloc entry point's device scratch array, registered with the HIP
+    runtime when liblgx.so loads."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    obj = os.path.join(BUILD_DIR, "lgx_scratch.o")
+    _run([os.path.join(ROCM, "bin", "hipcc"), "-c", "-fPIC", "-O2", "-std=c++17", f"--offload-arch={ARCH}",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-I", CSRC, "-o", obj, os.path.join(CSRC, "lgx_scratch.hip")])
+    return obj
 
 
 def build_host() -> str:
     srcs = [os.path.join(CSRC, s) for s in HOST_SOURCES]
+    scratch_obj = build_scratch()
     tmp = LIB + ".tmp"
     _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-ffp-contract=off", "-Wall", "-Wextra", "-pthread",
           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", "-I", CSRC,
-          "-o", tmp, *srcs, f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl"])
+          "-o", tmp, *srcs, scratch_obj, f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl"])
     os.replace(tmp, LIB)
     return LIB
 

@@ -53,9 +53,18 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
         if (e != hipSuccess)
             return fail(LGX_MODULE_LOAD_FAILED, "hipModuleLoad(%s): %s", path.c_str(),
                         hipGetErrorString(e));
+        // the allocation-free entry point's scratch on this device
+        void* scratch = nullptr;
+        e = lgxi_scratch_ptr(device, &scratch);
+        if (e != hipSuccess) {
+            (void)hipModuleUnload(mod);
+            return fail(LGX_HIP_ERROR, "hipGetSymbolAddress(scratch) on device %d: %s", device,
+                        hipGetErrorString(e));
+        }
         lgx_ctx* c = new lgx_ctx();
         c->device = device;
         c->module = mod;
+        c->scratch = scratch;
         c->arch = arch;
         const char* gv = getenv("LGX_GEMV");
         c->gemv_dot4 = gv && std::string(gv) == "dot4";
@@ -422,37 +431,70 @@ lgx_status lgx_gqa_prefill_attn(lgx_ctx* c, const float* q, const uint16_t* kpag
     });
 }
 
+// lgx_q8_gemm over the workspace `scratch` of `cap` bytes (nullptr: the
+// ctx's grow-on-demand workspace).
+static lgx_status q8_gemm_impl(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq,
+                               const uint16_t* xd, int32_t m, float* y, void* stream,
+                               void* scratch, size_t cap) {
+    lgx_status st = enter(c);
+    if (st != LGX_OK) return st;
+    if ((st = check_q8(W)) != LGX_OK) return st;
+    if (!xq || !xd || !y) return fail(LGX_NULL_POINTER, "NULL xq, xd or y");
+    if (m <= 0 || m > 65535 * 64) return fail(LGX_OUT_OF_BOUNDS, "m = %d out of range", m);
+    if (m == 1 && use_wg(c, W)) {
+        // the grouped GEMV applies the range tree in LDS: no workspace
+        lgx_gemv_mat g = gemv_mat(W, nullptr, xq, xd, y, 0);
+        return run_gemv_group(c, &g, 1, stream);
+    }
+    auto room = [&](size_t bytes, float** out) -> lgx_status {
+        if (!scratch) return ensure_ws(c, bytes, out);
+        if (bytes > cap)
+            return fail(LGX_OUT_OF_BOUNDS,
+                        "[%d x %d] product over m = %d needs %zu scratch bytes (limit %zu)", W->n,
+                        W->k, m, bytes, cap);
+        *out = (float*)scratch;
+        return LGX_OK;
+    };
+    if (m >= c->tiled_min) {
+        // T16 copy of the activations, then the group partials (straight
+        // into y when K is one group) and the tree over the groups
+        const Kern kern = tiled_kernel(c, m);
+        const int grp = tiled_grp(c, kern, W->n, W->k, m);
+        const int ng = tiled_groups(W->k, grp);
+        const size_t xbytes = ((size_t)cdiv(m, 16) * 16 * W->k + 255) / 256 * 256;
+        float* ws = nullptr;
+        if ((st = room(xbytes + (ng > 1 ? (size_t)ng * m * W->n * 4 : 0), &ws)) != LGX_OK)
+            return st;
+        int8_t* xt = (int8_t*)ws;
+        float* part = ng > 1 ? (float*)((char*)ws + xbytes) : y;
+        if ((st = act_to_t16(c, xq, m, W->k, xt, stream)) != LGX_OK ||
+            (st = run_q8_tiled(c, W, xt, xd, m, part, stream, kern, grp)) != LGX_OK || ng == 1)
+            return st;
+        lgx_combine_args ca{part, y, (int64_t)m * W->n, ng};
+        return launch(c, K_COMBINE, dim3(cdiv(ca.count, 256)), dim3(256), ca, stream);
+    }
+    const int nr = nranges_of(W->k);
+    float* part = nullptr;
+    if (nr > 1 && (st = room((size_t)nr * m * W->n * sizeof(float), &part)) != LGX_OK) return st;
+    return run_q8(c, gemm_kernel(c, m), W, nullptr, xq, xd, m, y, nullptr, stream, nullptr, nullptr,
+                  nullptr, part);
+}
+
 lgx_status lgx_q8_gemm(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq, const uint16_t* xd,
                        int32_t m, float* y, void* stream) {
+    return guarded(__func__, [&] { return q8_gemm_impl(c, W, xq, xd, m, y, stream, nullptr, 0); });
+}
+
+lgx_status lgx_q8_gemm_noalloc(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq,
+                               const uint16_t* xd, int32_t m, float* y, void* stream) {
     return guarded(__func__, [&]() -> lgx_status {
-        lgx_status st = enter(c);
-        if (st != LGX_OK) return st;
-        if ((st = check_q8(W)) != LGX_OK) return st;
-        if (!xq || !xd || !y) return fail(LGX_NULL_POINTER, "NULL xq, xd or y");
-        if (m <= 0 || m > 65535 * 64) return fail(LGX_OUT_OF_BOUNDS, "m = %d out of range", m);
-        if (m == 1 && use_wg(c, W)) {
-            lgx_gemv_mat g = gemv_mat(W, nullptr, xq, xd, y, 0);
-            return run_gemv_group(c, &g, 1, stream);
-        }
-        if (m >= c->tiled_min) {
-            // T16 copy of the activations, then the group partials (straight
-            // into y when K is one group) and the tree over the groups
-            const Kern kern = tiled_kernel(c, m);
-            const int grp = tiled_grp(c, kern, W->n, W->k, m);
-            const int ng = tiled_groups(W->k, grp);
-            const size_t xbytes = ((size_t)cdiv(m, 16) * 16 * W->k + 255) / 256 * 256;
-            float* ws = nullptr;
-            if ((st = ensure_ws(c, xbytes + (ng > 1 ? (size_t)ng * m * W->n * 4 : 0), &ws)) != LGX_OK)
-                return st;
-            int8_t* xt = (int8_t*)ws;
-            float* part = ng > 1 ? (float*)((char*)ws + xbytes) : y;
-            if ((st = act_to_t16(c, xq, m, W->k, xt, stream)) != LGX_OK ||
-                (st = run_q8_tiled(c, W, xt, xd, m, part, stream, kern, grp)) != LGX_OK || ng == 1)
-                return st;
-            lgx_combine_args ca{part, y, (int64_t)m * W->n, ng};
-            return launch(c, K_COMBINE, dim3(cdiv(ca.count, 256)), dim3(256), ca, stream);
-        }
-        return run_q8(c, gemm_kernel(c, m), W, nullptr, xq, xd, m, y, nullptr, stream);
+        if (!valid_ctx(c)) return fail(LGX_INVALID_HANDLE, "invalid lgx_ctx handle");
+        if (!c->scratch) return fail(LGX_HIP_ERROR, "no device scratch on device %d", c->device);
+        struct Untimed {
+            Untimed() { g_untimed = true; }
+            ~Untimed() { g_untimed = false; }
+        } untimed;
+        return q8_gemm_impl(c, W, xq, xd, m, y, stream, c->scratch, LGX_NOALLOC_SCRATCH_BYTES);
     });
 }
 

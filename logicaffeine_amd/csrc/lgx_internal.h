@@ -36,6 +36,9 @@ namespace lgxi {
 
 inline thread_local std::string g_last_error;
 inline thread_local bool g_has_error = false;
+// Set while an allocation-free entry point runs on this thread: its launches
+// never take timing events (creating them may allocate).
+inline thread_local bool g_untimed = false;
 
 inline lgx_status fail(lgx_status st, const char* fmt, ...) {
     char buf[1024];
@@ -195,6 +198,7 @@ struct lgx_ctx {
     std::atomic<int> live_models{0};  // lgx_model handles built on this ctx and not destroyed
     void* ws = nullptr;       // range partials
     size_t ws_bytes = 0;
+    void* scratch = nullptr;  // this device's LGX_NOALLOC_SCRATCH_BYTES array (lgx_scratch.hip)
     std::mutex ws_mu;
     // per-kernel device timing (lgx_ctx_set_kernel_timing): launches go
     // through hipExtModuleLaunchKernel with start/stop events attached to the
@@ -207,6 +211,10 @@ struct lgx_ctx {
     std::vector<Timed> timed;
     std::vector<hipEvent_t> event_pool;
 };
+
+// lgx_scratch.hip: device address of the fixed scratch array on `device`
+// (current), resolved once per device with hipGetSymbolAddress.
+extern "C" hipError_t lgxi_scratch_ptr(int device, void** out);
 
 namespace lgxi {
 
@@ -237,7 +245,7 @@ lgx_status launch(lgx_ctx* c, Kern k, dim3 grid, dim3 block, const Args& args, v
                   unsigned shmem = 0) {
     void* params[] = {(void*)&args};
     hipError_t e;
-    if (c->timing) {
+    if (c->timing && !g_untimed) {
         lgx_ctx::Timed t{k, nullptr, nullptr};
         if ((e = pooled_event(c, &t.start)) != hipSuccess || (e = pooled_event(c, &t.stop)) != hipSuccess)
             return fail(LGX_HIP_ERROR, "hipEventCreate: %s", hipGetErrorString(e));
@@ -332,7 +340,7 @@ inline Kern gemm_kernel(const lgx_ctx* c, int m) {
 inline lgx_status run_q8(lgx_ctx* c, Kern kern, const lgx_q8_matrix* W, const float* xf,
                   const int8_t* xq, const uint16_t* xd, int m, float* y, int32_t* dbg,
                   void* stream, int8_t* xq_out = nullptr, uint16_t* xd_out = nullptr,
-                  float* part_out = nullptr) {
+                  float* part_out = nullptr, float* part_ws = nullptr) {
     lgx_gemv_args a{};
     a.wt = W->qs;
     a.wd = W->d;
@@ -353,6 +361,8 @@ inline lgx_status run_q8(lgx_ctx* c, Kern kern, const lgx_q8_matrix* W, const fl
         // caller-owned partials [nranges][m][n]; no tree here
         a.part = part_out;
         a.y = part_out;
+    } else if (a.nranges > 1 && part_ws) {
+        a.part = part_ws;   // caller-provided room for nranges * m * n partials
     } else if (a.nranges > 1) {
         lgx_status st = ensure_ws(c, (size_t)a.nranges * m * W->n * sizeof(float), &a.part);
         if (st != LGX_OK) return st;

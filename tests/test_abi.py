@@ -62,6 +62,7 @@ def test_invalid_handle_and_null_pointer_paths():
     assert L.lgx_ctx_destroy(bogus) == 6
     assert L.lgx_quantize_q8_0(bogus, None, 1, 32, None, None, None) == 6
     assert L.lgx_q8_gemm(bogus, None, None, None, 1, None, None) == 6
+    assert L.lgx_q8_gemm_noalloc(bogus, None, None, None, 1, None, None) == 6
     assert L.lgx_q8q8_gemv(bogus, None, None, None, None, None, None) == 6
     assert L.lgx_q8_gemv_f32(bogus, None, None, None, None) == 6
     assert L.lgx_q8_repack_t16(bogus, None, None, 16, 64, None, None, None) == 6
