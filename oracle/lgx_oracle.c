@@ -15,6 +15,9 @@
 #include "lgx_oracle.h"
 
 #include <math.h>
+#ifdef __AVX2__
+#include <immintrin.h>
+#endif
 #include <stdlib.h>
 #include <string.h>
 
@@ -283,10 +286,32 @@ void orc_q8_gemv_f32(const int8_t* qs, const uint16_t* d, int32_t n, int32_t k,
     }
 }
 
-static inline int32_t block_dot(const int8_t* a, const int8_t* b) {
+/* orc_f16_to_f32 of every binary16 pattern, for the hot loops (filled once
+ * from orc_f16_to_f32 itself, so a lookup returns exactly its bits). */
+static float g_f16tab[65536];
+__attribute__((constructor)) static void fill_f16tab(void) {
+    for (uint32_t h = 0; h < 65536u; ++h) g_f16tab[h] = orc_f16_to_f32((uint16_t)h);
+}
+static inline float f16f(uint16_t h) { return g_f16tab[h]; }
+
+static inline int32_t block_dot(const int8_t* restrict a, const int8_t* restrict b) {
+#ifdef __AVX2__
+    /* the same exact integer sum: int8 -> int16, pairwise products summed
+     * into int32 lanes (|partial| <= 4 * 127^2, no overflow), then the lanes */
+    const __m256i a16lo = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)a));
+    const __m256i a16hi = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)(a + 16)));
+    const __m256i b16lo = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)b));
+    const __m256i b16hi = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)(b + 16)));
+    __m256i p = _mm256_add_epi32(_mm256_madd_epi16(a16lo, b16lo), _mm256_madd_epi16(a16hi, b16hi));
+    __m128i q = _mm_add_epi32(_mm256_castsi256_si128(p), _mm256_extracti128_si256(p, 1));
+    q = _mm_add_epi32(q, _mm_shuffle_epi32(q, 0x4e));
+    q = _mm_add_epi32(q, _mm_shuffle_epi32(q, 0xb1));
+    return _mm_cvtsi128_si32(q);
+#else
     int32_t s = 0;
     for (int i = 0; i < 32; ++i) s += (int32_t)a[i] * (int32_t)b[i];
     return s;
+#endif
 }
 
 /* Exact int32 block dot products s[row][b] of W with a Q8_0 activation. */
@@ -317,26 +342,63 @@ void orc_q8_gemm(const int8_t* qs, const uint16_t* d, int32_t n, int32_t k,
                  const int8_t* xq, const uint16_t* xd, int32_t m, float* y) {
     int32_t nb = k / 32;
     int32_t g = (nb + ORC_Q8_RANGE_BLOCKS - 1) / ORC_Q8_RANGE_BLOCKS;
-#pragma omp parallel for schedule(static)
-    for (int64_t idx = 0; idx < (int64_t)m * n; ++idx) {
-        int32_t mi = (int32_t)(idx / n), row = (int32_t)(idx % n);
+    float* dxf = (float*)malloc(sizeof(float) * (size_t)m * nb);
+    for (int64_t i = 0; i < (int64_t)m * nb; ++i) dxf[i] = f16f(xd[i]);
+    /* weight row outer, activation row inner: a thread keeps its weight row
+     * and its decoded scales in cache across all m rows; every output is the
+     * same chain as the one-row definition above */
+#pragma omp parallel
+    {
+        float* dwf = (float*)malloc(sizeof(float) * (size_t)nb);
         float part[1024];
-        const int8_t* w = qs + (int64_t)row * k;
-        const int8_t* a = xq + (int64_t)mi * k;
-        for (int32_t r = 0; r < g; ++r) {
-            float acc = 0.0f;
-            int32_t b1 = (r + 1) * ORC_Q8_RANGE_BLOCKS;
-            if (b1 > nb) b1 = nb;
-            for (int32_t b = r * ORC_Q8_RANGE_BLOCKS; b < b1; ++b) {
-                int32_t s = block_dot(w + (int64_t)b * 32, a + (int64_t)b * 32);
-                float dd = orc_f16_to_f32(d[(int64_t)row * nb + b]) *
-                           orc_f16_to_f32(xd[(int64_t)mi * nb + b]);
-                acc = fmaf((float)s, dd, acc);
+#pragma omp for schedule(static)
+        for (int32_t row = 0; row < n; ++row) {
+            const int8_t* w = qs + (int64_t)row * k;
+            for (int32_t b = 0; b < nb; ++b) dwf[b] = f16f(d[(int64_t)row * nb + b]);
+            int32_t mi = 0;
+            /* four activation rows at a time: four independent chains */
+            for (; mi + 4 <= m; mi += 4) {
+                float p4[4][1024 / ORC_Q8_RANGE_BLOCKS + 1];
+                for (int32_t r = 0; r < g; ++r) {
+                    float c0 = 0.0f, c1 = 0.0f, c2 = 0.0f, c3 = 0.0f;
+                    int32_t b1 = (r + 1) * ORC_Q8_RANGE_BLOCKS;
+                    if (b1 > nb) b1 = nb;
+                    for (int32_t b = r * ORC_Q8_RANGE_BLOCKS; b < b1; ++b) {
+                        const int8_t* wb = w + (int64_t)b * 32;
+                        const int8_t* ab = xq + (int64_t)mi * k + (int64_t)b * 32;
+                        const float* dxb = dxf + (int64_t)mi * nb + b;
+                        c0 = fmaf((float)block_dot(wb, ab), dwf[b] * dxb[0], c0);
+                        c1 = fmaf((float)block_dot(wb, ab + k), dwf[b] * dxb[nb], c1);
+                        c2 = fmaf((float)block_dot(wb, ab + 2 * (int64_t)k), dwf[b] * dxb[2 * nb], c2);
+                        c3 = fmaf((float)block_dot(wb, ab + 3 * (int64_t)k), dwf[b] * dxb[3 * nb], c3);
+                    }
+                    p4[0][r] = c0;
+                    p4[1][r] = c1;
+                    p4[2][r] = c2;
+                    p4[3][r] = c3;
+                }
+                for (int32_t u = 0; u < 4; ++u)
+                    y[(int64_t)(mi + u) * n + row] = orc_tree_sum(p4[u], g);
             }
-            part[r] = acc;
+            for (; mi < m; ++mi) {
+                const int8_t* a = xq + (int64_t)mi * k;
+                const float* dx = dxf + (int64_t)mi * nb;
+                for (int32_t r = 0; r < g; ++r) {
+                    float acc = 0.0f;
+                    int32_t b1 = (r + 1) * ORC_Q8_RANGE_BLOCKS;
+                    if (b1 > nb) b1 = nb;
+                    for (int32_t b = r * ORC_Q8_RANGE_BLOCKS; b < b1; ++b) {
+                        int32_t s = block_dot(w + (int64_t)b * 32, a + (int64_t)b * 32);
+                        acc = fmaf((float)s, dwf[b] * dx[b], acc);
+                    }
+                    part[r] = acc;
+                }
+                y[(int64_t)mi * n + row] = orc_tree_sum(part, g);
+            }
         }
-        y[(int64_t)mi * n + row] = orc_tree_sum(part, g);
+        free(dwf);
     }
+    free(dxf);
 }
 
 /* ------------------------------------------------------------------ */
@@ -389,21 +451,42 @@ void orc_gqa_decode_attn(const float* q, const uint16_t* kpages, const uint16_t*
         for (int32_t c = 0; c < nc; ++c) {
             int32_t t0 = c * ORC_ATTN_CHUNK, n = L - t0 < ORC_ATTN_CHUNK ? L - t0 : ORC_ATTN_CHUNK;
             float m = -INFINITY;
-            for (int32_t j = 0; j < n; ++j) {
+            /* score chains over i, four tokens' chains interleaved */
+            int32_t j = 0;
+            for (; j + 4 <= n; j += 4) {
+                const uint16_t* k0 = kv_row(kpages, page_table, b, maxp, t0 + j, g, hkv, d);
+                const uint16_t* k1 = kv_row(kpages, page_table, b, maxp, t0 + j + 1, g, hkv, d);
+                const uint16_t* k2 = kv_row(kpages, page_table, b, maxp, t0 + j + 2, g, hkv, d);
+                const uint16_t* k3 = kv_row(kpages, page_table, b, maxp, t0 + j + 3, g, hkv, d);
+                float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+                for (int32_t i = 0; i < d; ++i) {
+                    a0 = fmaf(qv[i], f16f(k0[i]), a0);
+                    a1 = fmaf(qv[i], f16f(k1[i]), a1);
+                    a2 = fmaf(qv[i], f16f(k2[i]), a2);
+                    a3 = fmaf(qv[i], f16f(k3[i]), a3);
+                }
+                s[j] = a0 * scale;
+                s[j + 1] = a1 * scale;
+                s[j + 2] = a2 * scale;
+                s[j + 3] = a3 * scale;
+            }
+            for (; j < n; ++j) {
                 const uint16_t* kr = kv_row(kpages, page_table, b, maxp, t0 + j, g, hkv, d);
                 float acc = 0.0f;
-                for (int32_t i = 0; i < d; ++i) acc = fmaf(qv[i], orc_f16_to_f32(kr[i]), acc);
+                for (int32_t i = 0; i < d; ++i) acc = fmaf(qv[i], f16f(kr[i]), acc);
                 s[j] = acc * scale;
-                if (s[j] > m) m = s[j];
             }
-            for (int32_t j = 0; j < ORC_ATTN_CHUNK; ++j) pbuf[j] = j < n ? orc_expf(s[j] - m) : 0.0f;
-            for (int32_t i = 0; i < d; ++i) {
-                float acc = 0.0f;
-                for (int32_t j = 0; j < n; ++j) {
-                    const uint16_t* vr = kv_row(vpages, page_table, b, maxp, t0 + j, g, hkv, d);
-                    acc = fmaf(pbuf[j], orc_f16_to_f32(vr[i]), acc);
-                }
-                oc[(int64_t)c * d + i] = acc;
+            for (j = 0; j < n; ++j)
+                if (s[j] > m) m = s[j];
+            for (j = 0; j < ORC_ATTN_CHUNK; ++j) pbuf[j] = j < n ? orc_expf(s[j] - m) : 0.0f;
+            /* PV: chain over tokens for each i (j outer, every i's chain
+             * advanced in token order) */
+            float* o = oc + (int64_t)c * d;
+            for (int32_t i = 0; i < d; ++i) o[i] = 0.0f;
+            for (j = 0; j < n; ++j) {
+                const uint16_t* vr = kv_row(vpages, page_table, b, maxp, t0 + j, g, hkv, d);
+                const float pj = pbuf[j];
+                for (int32_t i = 0; i < d; ++i) o[i] = fmaf(pj, f16f(vr[i]), o[i]);
             }
             mc[c] = m;
             lc[c] = orc_halving_sum(pbuf, ORC_ATTN_CHUNK);
@@ -756,3 +839,117 @@ void orc_model_step(orc_model* m, int32_t nseq, const int32_t* slots, const int3
     free(logits); free(h); free(xn); free(xq); free(xd); free(qkv); free(q); free(att);
     free(y); free(a); free(pt); free(lens);
 }
+
+/* Teacher-forced prefill of nseq sequences, P positions each: row s*P + j is
+ * token tokens[s*P + j] of slot slots[s] at position seq_len[slot] + j.
+ * Every layer runs its products over all nseq*P rows at once, appends the K/V
+ * of all rows, then lets row j attend to the first seq_len + j + 1 tokens of
+ * its slot.  Each row goes through exactly the operations orc_model_step
+ * applies to it (rows are independent in every product and glue step, and a
+ * row never reads cache slots past its own position), so the cache, next
+ * tokens, logits and hidden rows equal P calls of orc_model_step; the tests
+ * check that bit for bit.  Outputs are those of each slot's last position. */
+void orc_model_prefill(orc_model* m, int32_t nseq, const int32_t* slots, int32_t P,
+                       const int32_t* tokens, int32_t* next, float* hidden_out,
+                       float* logits_out) {
+    const orc_qwen_config* c = &m->c;
+    int32_t H = c->hidden, I = c->inter, d = c->head_dim, hq = c->n_heads, hkv = c->n_kv;
+    int32_t qn = m->qkv_n;
+    int64_t R = (int64_t)nseq * P;
+    int32_t kmax = H > I ? H : I;
+    if (hq * d > kmax) kmax = hq * d;
+    float* h = (float*)xmalloc(sizeof(float) * R * H);
+    float* xn = (float*)xmalloc(sizeof(float) * R * H);
+    int8_t* xq = (int8_t*)xmalloc((size_t)R * kmax);
+    uint16_t* xd = (uint16_t*)xmalloc((size_t)R * (kmax / 32) * 2);
+    float* qkv = (float*)xmalloc(sizeof(float) * R * qn);
+    float* q = (float*)xmalloc(sizeof(float) * R * hq * d);
+    float* att = (float*)xmalloc(sizeof(float) * R * hq * d);
+    float* y = (float*)xmalloc(sizeof(float) * R * (2 * I > H ? 2 * I : H));
+    float* a = (float*)xmalloc(sizeof(float) * R * I);
+    int32_t* pt = (int32_t*)xmalloc(sizeof(int32_t) * R * m->maxp);
+    int32_t* lens = (int32_t*)xmalloc(sizeof(int32_t) * R);
+    float scale = (float)(1.0 / sqrt((double)d));
+    for (int64_t r = 0; r < R; ++r) {
+        int32_t s = (int32_t)(r / P), j = (int32_t)(r % P);
+        for (int32_t k = 0; k < H; ++k)
+            h[r * H + k] = orc_f16_to_f32(m->emb[(int64_t)tokens[r] * H + k]);
+        memcpy(pt + r * m->maxp, m->page_table + (int64_t)slots[s] * m->maxp,
+               sizeof(int32_t) * m->maxp);
+        lens[r] = m->seq_len[slots[s]] + j + 1;
+    }
+    for (int32_t l = 0; l < c->n_layers; ++l) {
+        orc_rmsnorm(h, m->ones, (int32_t)R, H, c->eps, xn);
+        orc_quantize_q8_0(xn, R, H, xq, xd);
+        orc_q8_gemm(m->qkv_qs[l], m->qkv_d[l], qn, H, xq, xd, (int32_t)R, qkv);
+#pragma omp parallel for schedule(static)
+        for (int64_t i = 0; i < R; ++i) {
+            float* r = qkv + i * qn;
+            for (int32_t jj = 0; jj < qn; ++jj) r[jj] = r[jj] + m->bias[l][jj];
+            int32_t pos = lens[i] - 1;
+            orc_rope(r, hq + hkv, d, m->cos_t + (int64_t)pos * (d / 2),
+                     m->sin_t + (int64_t)pos * (d / 2));
+            memcpy(q + i * hq * d, r, sizeof(float) * hq * d);
+            int32_t b = slots[i / P];
+            for (int32_t g = 0; g < hkv; ++g) {
+                int32_t page = m->page_table[(int64_t)b * m->maxp + pos / ORC_PAGE];
+                int64_t off = (((int64_t)page * hkv + g) * ORC_PAGE + pos % ORC_PAGE) * d;
+                for (int32_t e = 0; e < d; ++e) {
+                    m->kc[l][off + e] = orc_f32_to_f16(r[(hq + g) * d + e]);
+                    m->vc[l][off + e] = orc_f32_to_f16(r[(hq + hkv + g) * d + e]);
+                }
+            }
+        }
+        orc_gqa_decode_attn(q, m->kc[l], m->vc[l], pt, lens, (int32_t)R, hq, hkv, d, m->maxp,
+                            scale, att);
+        orc_quantize_q8_0(att, R, hq * d, xq, xd);
+        orc_q8_gemm(m->o_qs[l], m->o_d[l], H, hq * d, xq, xd, (int32_t)R, y);
+        for (int64_t j = 0; j < R * H; ++j) h[j] = h[j] + y[j];
+        orc_rmsnorm(h, m->ones, (int32_t)R, H, c->eps, xn);
+        orc_quantize_q8_0(xn, R, H, xq, xd);
+        orc_q8_gemm(m->gu_qs[l], m->gu_d[l], 2 * I, H, xq, xd, (int32_t)R, y);
+        orc_swiglu(y, (int32_t)R, I, a);
+        orc_quantize_q8_0(a, R, I, xq, xd);
+        orc_q8_gemm(m->dn_qs[l], m->dn_d[l], H, I, xq, xd, (int32_t)R, y);
+        for (int64_t j = 0; j < R * H; ++j) h[j] = h[j] + y[j];
+    }
+    /* the head for each slot's last position only */
+    float* hl = (float*)xmalloc(sizeof(float) * (size_t)nseq * H);
+    for (int32_t s = 0; s < nseq; ++s)
+        memcpy(hl + (int64_t)s * H, h + ((int64_t)s * P + P - 1) * H, sizeof(float) * H);
+    orc_rmsnorm(hl, m->ones, nseq, H, c->eps, xn);
+    if (hidden_out) memcpy(hidden_out, xn, sizeof(float) * nseq * H);
+    float* logits = (float*)xmalloc(sizeof(float) * (size_t)nseq * c->vocab);
+    if (c->tied) {
+        orc_lm_head_f16(xn, nseq, m->emb, c->vocab, H, logits);
+    } else {
+        orc_quantize_q8_0(xn, nseq, H, xq, xd);
+        orc_q8_gemm(m->lm_qs, m->lm_d, c->vocab, H, xq, xd, nseq, logits);
+    }
+    for (int32_t s = 0; s < nseq; ++s) {
+        next[s] = orc_argmax(logits + (int64_t)s * c->vocab, c->vocab);
+        m->seq_len[slots[s]] += P;
+    }
+    if (logits_out) memcpy(logits_out, logits, sizeof(float) * (size_t)nseq * c->vocab);
+    free(logits); free(hl); free(h); free(xn); free(xq); free(xd); free(qkv); free(q);
+    free(att); free(y); free(a); free(pt); free(lens);
+}
+
+/* Writes cached K (kv = 0) or V (kv = 1) rows of slot b at layer l, tokens
+ * [0, n), from rows[n][hkv][d] (binary16): the inverse of orc_model_kv.  With
+ * orc_model_set_seq_len this loads a cache computed elsewhere (a device
+ * prefill the tests have checked bit for bit) so the CPU baseline can decode
+ * at the benchmark's context length without re-running the prompt. */
+void orc_model_load_kv(orc_model* m, int32_t layer, int32_t kv, int32_t b, int32_t n,
+                       const uint16_t* rows) {
+    int32_t hkv = m->c.n_kv, d = m->c.head_dim;
+    uint16_t* pages = kv ? m->vc[layer] : m->kc[layer];
+    for (int32_t t = 0; t < n; ++t)
+        for (int32_t g = 0; g < hkv; ++g) {
+            int32_t page = m->page_table[(int64_t)b * m->maxp + t / ORC_PAGE];
+            memcpy(pages + (((int64_t)page * hkv + g) * ORC_PAGE + t % ORC_PAGE) * d,
+                   rows + ((int64_t)t * hkv + g) * d, (size_t)d * 2);
+        }
+}
+
+void orc_model_set_seq_len(orc_model* m, int32_t slot, int32_t len) { m->seq_len[slot] = len; }

@@ -52,6 +52,12 @@
  *                    (tests/test_oracle_model.py) agrees within 1e-3 of the
  *                    logit scale, an interleaved-RoPE mutant does not; batch
  *                    and slot invariance
+ *   model prefill    equal bit for bit (tokens, logits, hidden rows, every
+ *                    cached K/V row) to P calls of the model step, over
+ *                    several chunks, ragged start lengths and 256-token
+ *                    attention-chunk boundaries (tests/test_oracle_model.py)
+ *   load_kv          round trip with orc_model_kv; decoding after a loaded
+ *                    cache equals decoding after the prefill that made it
  * None of these is "parity unpinned": each has the checks above, chosen so
  * that a dropped term, wrong sign or transposed operand fails one of them.
  */
@@ -135,6 +141,12 @@ void orc_model_kv(const orc_model* m, int32_t layer, int32_t kv, int32_t b, int3
                   uint16_t* out);
 void orc_model_step(orc_model* m, int32_t nseq, const int32_t* slots, const int32_t* tokens,
                     int32_t* next, float* hidden_out, float* logits_out);
+void orc_model_prefill(orc_model* m, int32_t nseq, const int32_t* slots, int32_t P,
+                       const int32_t* tokens, int32_t* next, float* hidden_out,
+                       float* logits_out);
+void orc_model_load_kv(orc_model* m, int32_t layer, int32_t kv, int32_t b, int32_t n,
+                       const uint16_t* rows);
+void orc_model_set_seq_len(orc_model* m, int32_t slot, int32_t len);
 
 #ifdef __cplusplus
 }

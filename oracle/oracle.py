@@ -82,6 +82,9 @@ def lib():
             "orc_model_tensor": (_P, [_P, _I32, _I32]),
             "orc_model_kv": (None, [_P, _I32, _I32, _I32, _I32, _P]),
             "orc_model_step": (None, [_P, _I32, _P, _P, _P, _P, _P]),
+            "orc_model_prefill": (None, [_P, _I32, _P, _I32, _P, _P, _P, _P]),
+            "orc_model_load_kv": (None, [_P, _I32, _I32, _I32, _I32, _P]),
+            "orc_model_set_seq_len": (None, [_P, _I32, _I32]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -415,6 +418,36 @@ class Model:
         if want_hidden:
             out.append(hid)
         return out[0] if len(out) == 1 else tuple(out)
+
+    def prefill(self, slots, tokens, want_logits=False, want_hidden=False):
+        """Teacher-forced prefill: tokens [nseq][P] for `slots`, all P
+        positions of every slot per layer in one batched pass; returns what
+        the P-th step call would (next tokens, logits, hidden rows)."""
+        slots = _c(slots, np.int32)
+        tokens = _c(tokens, np.int32)
+        nseq, P = tokens.shape
+        assert slots.size == nseq
+        nxt = np.empty(nseq, np.int32)
+        hid = np.empty((nseq, self.cfg["hidden"]), np.float32) if want_hidden else None
+        lg = np.empty((nseq, self.cfg["vocab"]), np.float32) if want_logits else None
+        lib().orc_model_prefill(self.h, nseq, _ptr(slots), P, _ptr(tokens), _ptr(nxt),
+                                _ptr(hid) if hid is not None else None,
+                                _ptr(lg) if lg is not None else None)
+        out = [nxt]
+        if want_logits:
+            out.append(lg)
+        if want_hidden:
+            out.append(hid)
+        return out[0] if len(out) == 1 else tuple(out)
+
+    def load_kv(self, layer: int, which: int, slot: int, rows) -> None:
+        """Write cached K (which 0) or V (1) rows [n][n_kv][head_dim] binary16
+        of `slot`, tokens 0..n-1 (the inverse of kv())."""
+        rows = _c(rows, np.uint16)
+        lib().orc_model_load_kv(self.h, layer, which, slot, rows.shape[0], _ptr(rows))
+
+    def set_seq_len(self, slot: int, n: int) -> None:
+        lib().orc_model_set_seq_len(self.h, slot, n)
 
 
 EMB_SIGMA = 0.002

@@ -390,3 +390,24 @@ def test_grouped_gemv_long_k_and_errors(ctx, orc):
     assert np.array_equal(host(cw.q8q8_gemv_quantize(Ww, gw)), ref)
     assert np.array_equal(host(cw.q8q8_gemv(Ww, cw.to_device(xq[0]), cw.to_device(xd[0]))), ref)
     cw.close()
+
+
+@pytest.mark.parametrize("n,k", [(37888, 3584), (3584, 18944), (152064, 3584)])
+def test_q8_gemm_7b_shapes_m64_streaming_and_tiled(ctx, orc, n, k):
+    """The config-4 (Qwen2.5-7B) products at the decode batch M = 64: the
+    fused gate|up [37888 x 3584], down [3584 x 18944] (19 ranges) and the
+    Q8_0 lm_head [152064 x 3584], the largest n in the system, through the
+    streaming kernel and through the 32-row tiled product the 7B decode uses,
+    against the oracle bit for bit."""
+    m = 64
+    qs, d = orc.gen_q8_matrix(4, 7000 + n % 1000 + k % 100, n, k)
+    x = orc.gen_normal_f32(4, 7100 + n % 1000, (m, k))
+    xq, xd = orc.quantize_q8_0(x)
+    ref = orc.q8_gemm(qs, d, xq, xd)
+    ct = _ctx_with_env(LGX_GEMM_TILED_MIN=33, LGX_GEMM_TILED_ROWS=32)
+    for c in (ctx, ct):
+        W = c.q8_matrix(qs, d)
+        y = host(c.q8_gemm(W, c.to_device(xq), c.to_device(xd)))
+        assert np.array_equal(y, ref), c is ct
+        del W
+    ct.close()

@@ -186,3 +186,63 @@ def test_model_batch_and_slot_invariance(orc):
     assert a.seq_len(0) == 8
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny_untied"])
+def test_prefill_equals_repeated_steps(orc, name):
+    """orc_model_prefill (all positions of a chunk per layer at once) equals
+    P calls of the already-pinned step bit for bit: next tokens, logits,
+    hidden rows and every cached K/V row, over two chunks per slot with
+    ragged start lengths, a 256-token attention-chunk boundary crossed
+    inside a chunk, and slots passed out of order."""
+    cfg = orc.qwen_config(name)
+    seed = 606
+    a, b = orc.Model(cfg, seed), orc.Model(cfg, seed)
+    rng = np.random.default_rng(7)
+    V = cfg["vocab"]
+    slots = np.array([2, 0], np.int32)
+    # chunk 1: slot 2 gets 250 tokens, slot 0 gets 250 (then both cross 256)
+    for P in (250, 19):
+        toks = rng.integers(0, V, size=(2, P)).astype(np.int32)
+        na, la, ha = a.prefill(slots, toks, want_logits=True, want_hidden=True)
+        for p in range(P):
+            nb, lb, hb = b.step(slots, toks[:, p], want_logits=True, want_hidden=True)
+        assert np.array_equal(na, nb)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        assert np.array_equal(ha.view(np.uint32), hb.view(np.uint32))
+    # a third slot starting later, alone
+    toks = rng.integers(0, V, size=(1, 7)).astype(np.int32)
+    assert np.array_equal(a.prefill([1], toks), [b.step([1], toks[:, p]) for p in range(7)][-1])
+    for s in (0, 1, 2, 3):
+        assert a.seq_len(s) == b.seq_len(s)
+    for layer in range(cfg["n_layers"]):
+        for s in (0, 1, 2):
+            n = a.seq_len(s)
+            for which in (0, 1):
+                assert np.array_equal(a.kv(layer, which, s, n), b.kv(layer, which, s, n))
+    a.close()
+    b.close()
+
+
+def test_load_kv_round_trip_and_decode(orc):
+    """A cache copied out of one model (kv) and loaded into another
+    (load_kv + set_seq_len) decodes exactly as the model that made it."""
+    cfg = orc.qwen_config("tiny")
+    a, b = orc.Model(cfg, 9), orc.Model(cfg, 9)
+    rng = np.random.default_rng(8)
+    toks = rng.integers(0, cfg["vocab"], size=(1, 40)).astype(np.int32)
+    nxt = a.prefill([3], toks)
+    for layer in range(cfg["n_layers"]):
+        for which in (0, 1):
+            rows = a.kv(layer, which, 3, 40)
+            b.load_kv(layer, which, 1, rows)
+            assert np.array_equal(b.kv(layer, which, 1, 40), rows)
+    b.set_seq_len(1, 40)
+    ta, tb = nxt.copy(), nxt.copy()
+    for _ in range(5):
+        ta, la = a.step([3], ta, want_logits=True)
+        tb, lb = b.step([1], tb, want_logits=True)
+        assert np.array_equal(ta, tb)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    a.close()
+    b.close()
