@@ -268,6 +268,23 @@ lgx_status lgx_lm_head_f16_t64(lgx_ctx* ctx, const float* x, const uint16_t* emb
  * gives 0); -0 and +0 compare equal. */
 lgx_status lgx_argmax(lgx_ctx* ctx, const float* logits, int32_t m, int32_t vocab, int32_t* out,
                       void* stream);
+/* Seeded top-k / top-p sampling: out[b] is drawn from row b of logits
+ * ([m][vocab] binary32).  Canonical rule (the CPU oracle restates it):
+ *   candidates  the top_k logits by value (ties: lower index first; NaN never
+ *               a candidate; -0 == +0), in that order j = 0, 1, ...
+ *   weights     e_j = expf((l_j - l_0) * (1/temperature)) (the library's
+ *               expf), c_j = c_{j-1} + e_j in binary32, c_{-1} = 0
+ *   nucleus     J = first j with c_j >= top_p * c_last
+ *   draw        x = element positions[b] of SplitMix64 stream b of `seed`
+ *               (the tensor generator's stream convention), u = (x >> 40) *
+ *               2^-24, token = candidate of the first j <= J with
+ *               c_j > u * c_J (J if none); no candidate at all gives 0.
+ * 1 <= top_k <= 64, 0 < top_p <= 1, temperature finite and > 0,
+ * vocab <= 262144.  The reference has no sampler; the seeded SplitMix64
+ * stream follows crates/logicaffeine_runtime/src/seed.rs:15-38. */
+lgx_status lgx_sample(lgx_ctx* ctx, const float* logits, int32_t m, int32_t vocab, int32_t top_k,
+                      float top_p, float temperature, uint64_t seed, const int32_t* positions,
+                      int32_t* out, void* stream);
 
 /* ---- random-init Qwen2-shaped Q8_0 model (batched greedy decode) ---- */
 /* Opaque model handle, created from a seed and freed explicitly, as the
@@ -341,6 +358,13 @@ lgx_status lgx_qwen_generate(lgx_model* m, int32_t B, int32_t* tokens, int32_t n
  * global ones). */
 lgx_status lgx_model_tensor(lgx_model* m, int32_t layer, int32_t which, const void** dev,
                             size_t* bytes);
+/* Token choice of every later decode step, generate and prefill of m:
+ * temperature 0 restores greedy argmax; otherwise the lgx_sample rule with
+ * stream b = sequence b and draw index = the position the step consumes
+ * (seq_len[b] before its += 1).  Drops the recorded HIP graphs (waits for
+ * the device if any exist). */
+lgx_status lgx_model_set_sampling(lgx_model* m, float temperature, int32_t top_k, float top_p,
+                                  uint64_t seed);
 /* out[B][vocab] = logits of the last decode/prefill step (binary32); B must
  * be that step's batch. */
 lgx_status lgx_qwen_logits(lgx_model* m, int32_t B, float* out, void* stream);

@@ -78,6 +78,9 @@ SIGNATURES = {
     "lgx_f16_repack_t64": (C.c_int, [_P, _P, _I32, _I32, _P, _P]),
     "lgx_lm_head_f16_t64": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _P, _P]),
     "lgx_argmax": (C.c_int, [_P, _P, _I32, _I32, _P, _P]),
+    "lgx_sample": (C.c_int, [_P, _P, _I32, _I32, _I32, C.c_float, C.c_float, C.c_uint64, _P, _P,
+                             _P]),
+    "lgx_model_set_sampling": (C.c_int, [_P, C.c_float, _I32, C.c_float, C.c_uint64]),
     "lgx_model_create": (C.c_int, [_P, _P, C.c_uint64, C.POINTER(_P)]),
     "lgx_model_destroy": (C.c_int, [_P]),
     "lgx_model_reset": (C.c_int, [_P, _P]),
@@ -526,6 +529,18 @@ class Context:
                                 self._s()))
         return out
 
+    def sample(self, logits, positions, top_k: int, top_p: float, temperature: float, seed: int,
+               out=None):
+        """lgx_sample: seeded top-k / top-p draw per row of logits [m][vocab];
+        positions (device int32 [m]) are the draw indices of the rows' streams."""
+        t = self.torch
+        m, vocab = logits.shape
+        out = t.empty(m, dtype=t.int32, device=self.dev) if out is None else out
+        _check(lib().lgx_sample(self.handle, logits.data_ptr(), m, vocab, top_k, top_p,
+                                temperature, seed, positions.data_ptr(), out.data_ptr(),
+                                self._s()))
+        return out
+
 
 def _ptr_or_none(tensor):
     return tensor.data_ptr() if tensor is not None else None
@@ -562,6 +577,12 @@ class Model:
 
     def reset(self) -> None:
         _check(lib().lgx_model_reset(self.handle, self.ctx._s()))
+
+    def set_sampling(self, temperature: float, top_k: int = 1, top_p: float = 1.0,
+                     seed: int = 0) -> None:
+        """Seeded top-k / top-p token choice for later steps (temperature 0:
+        greedy)."""
+        _check(lib().lgx_model_set_sampling(self.handle, temperature, top_k, top_p, seed))
 
     def decode_step(self, tokens) -> None:
         """tokens: device int32 [B], replaced in place by the next tokens."""

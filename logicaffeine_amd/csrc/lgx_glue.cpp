@@ -215,4 +215,21 @@ lgx_status lgx_argmax(lgx_ctx* c, const float* logits, int32_t m, int32_t vocab,
     });
 }
 
+lgx_status lgx_sample(lgx_ctx* c, const float* logits, int32_t m, int32_t vocab, int32_t top_k,
+                      float top_p, float temperature, uint64_t seed, const int32_t* positions,
+                      int32_t* out, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!logits || !positions || !out) return fail(LGX_NULL_POINTER, "NULL tensor");
+        if (m <= 0 || m > 65535) return fail(LGX_INVALID_ARGUMENT, "m = %d", m);
+        SampleParams sp;
+        if ((st = sample_check(top_k, top_p, temperature, vocab, &sp)) != LGX_OK) return st;
+        sp.seed = seed;
+        float* cand = nullptr;
+        if ((st = ensure_ws(c, sample_cand_bytes(m, vocab), &cand)) != LGX_OK) return st;
+        return launch_sample(c, sp, logits, 1, m, vocab, positions, out, nullptr, 0, cand, stream);
+    });
+}
+
 }  // extern "C"

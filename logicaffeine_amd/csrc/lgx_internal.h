@@ -119,7 +119,9 @@ enum Kern {
     K_GEMM_TILED32,
     K_PFA_D64_G1,    // + (gq - 1)
     K_PFA_D128_G1 = K_PFA_D64_G1 + 8,
-    K_COUNT = K_PFA_D128_G1 + 8
+    K_SAMPLE_PARTIAL = K_PFA_D128_G1 + 8,
+    K_SAMPLE_FINAL,
+    K_COUNT
 };
 inline const char* const kKernelNames[] = {
     "lgx_k_repack_t16", "lgx_k_quantize_q8_0", "lgx_k_q8q8_gemv",
@@ -148,6 +150,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_attn_prefill_d128_g1", "lgx_k_attn_prefill_d128_g2", "lgx_k_attn_prefill_d128_g3",
     "lgx_k_attn_prefill_d128_g4", "lgx_k_attn_prefill_d128_g5", "lgx_k_attn_prefill_d128_g6",
     "lgx_k_attn_prefill_d128_g7", "lgx_k_attn_prefill_d128_g8",
+    "lgx_k_sample_partial", "lgx_k_sample_final",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -307,6 +310,59 @@ inline int argmax_slices(int vocab) { return (vocab + LGX_ARGMAX_SLICE - 1) / LG
 inline lgx_status launch_argmax(lgx_ctx* c, const float* part, int nr, int m, int vocab,
                                 int32_t* tokens, int32_t* seq_len, int advance, void* cand,
                                 void* stream);
+
+// Seeded top-k / top-p draw of m rows of (range-partial) logits: slice
+// candidates (m * slices * LGX_SAMPLE_MAX_K keys in cand), then the per-row
+// draw; stream of row b is stream0 + b, draw index pos[b] (or seq_len[b]).
+struct SampleParams {
+    int32_t top_k = 0;      // 0: greedy (argmax)
+    float top_p = 1.0f;
+    float inv_temp = 1.0f;
+    uint64_t seed = 0;
+};
+inline lgx_status sample_check(int32_t top_k, float top_p, float temperature, int vocab,
+                               SampleParams* out) {
+    if (top_k < 1 || top_k > LGX_SAMPLE_MAX_K)
+        return fail(LGX_INVALID_ARGUMENT, "top_k = %d outside [1, %d]", top_k, LGX_SAMPLE_MAX_K);
+    if (!(top_p > 0.0f && top_p <= 1.0f))
+        return fail(LGX_INVALID_ARGUMENT, "top_p = %g outside (0, 1]", (double)top_p);
+    if (!(temperature > 0.0f) || !std::isfinite(temperature))
+        return fail(LGX_INVALID_ARGUMENT, "temperature = %g: need a finite value > 0",
+                    (double)temperature);
+    if (vocab <= 0 || vocab > 64 * LGX_ARGMAX_SLICE)
+        return fail(LGX_UNSUPPORTED, "vocab = %d outside [1, %d] for sampling", vocab,
+                    64 * LGX_ARGMAX_SLICE);
+    out->top_k = top_k;
+    out->top_p = top_p;
+    out->inv_temp = 1.0f / temperature;
+    return LGX_OK;
+}
+inline size_t sample_cand_bytes(int m, int vocab) {
+    return (size_t)m * argmax_slices(vocab) * LGX_SAMPLE_MAX_K * sizeof(uint64_t);
+}
+inline lgx_status launch_sample(lgx_ctx* c, const SampleParams& sp, const float* part, int nr,
+                                int m, int vocab, const int32_t* pos, int32_t* tokens,
+                                int32_t* seq_len, int advance, void* cand, void* stream) {
+    lgx_sample_args a{};
+    a.part = part;
+    a.nr = nr;
+    a.tokens = tokens;
+    a.seq_len = seq_len;
+    a.pos = pos;
+    a.cand = (uint64_t*)cand;
+    a.seed = sp.seed;
+    a.m = m;
+    a.vocab = vocab;
+    a.nslices = argmax_slices(vocab);
+    a.top_k = sp.top_k;
+    a.advance = advance;
+    a.stream0 = 0;
+    a.top_p = sp.top_p;
+    a.inv_temp = sp.inv_temp;
+    lgx_status st = launch(c, K_SAMPLE_PARTIAL, dim3(a.nslices, m), dim3(256), a, stream);
+    if (st != LGX_OK) return st;
+    return launch(c, K_SAMPLE_FINAL, dim3(m), dim3(64), a, stream);
+}
 
 inline lgx_status check_q8(const lgx_q8_matrix* W) {
     if (!W) return fail(LGX_NULL_POINTER, "W is NULL");

@@ -201,6 +201,27 @@ typedef struct {
     int32_t m, vocab, advance, nslices;
 } lgx_argmax_args;
 
+// Seeded top-k / top-p sampling of m rows of (range-partial) logits.
+// lgx_k_sample_partial: per 4096-logit slice, the slice's top_k keys
+// (value descending, index ascending; NaN never a candidate) into
+// cand[m][nslices][LGX_SAMPLE_MAX_K] (0 = empty).  lgx_k_sample_final: per
+// row the top_k keys of the slice lists, then the canonical draw (see
+// lgx_sample in lgx.h); tokens[b] = the drawn index, seq_len[b] += advance.
+// The draw index of row b is pos[b], or seq_len[b] before the advance when
+// pos is NULL; its SplitMix64 stream is `stream0 + b` of `seed`.
+#define LGX_SAMPLE_MAX_K 64
+typedef struct {
+    const float* part;     // [nr][m][vocab]
+    int32_t nr;
+    int32_t* tokens;
+    int32_t* seq_len;
+    const int32_t* pos;
+    uint64_t* cand;
+    uint64_t seed;
+    int32_t m, vocab, nslices, top_k, advance, stream0;
+    float top_p, inv_temp;
+} lgx_sample_args;
+
 // Large-M Q8_0 product (prefill): one workgroup per (64 weight rows, 128
 // activation rows, group of LGX_TG_RANGES ranges).  Activations in the T16
 // tile layout of the weights (row tiles of 16, 1 KiB per 64-column pair).

@@ -2151,6 +2151,155 @@ extern "C" __global__ __launch_bounds__(64) void lgx_k_argmax_final(const lgx_ar
     }
 }
 
+// ---------------------------------------------------------------------------
+// Seeded top-k / top-p sampling.  A logit x at vocabulary index v has the key
+//   (orderable bits of x, -0 taken as +0) << 32 | (0xffffffff - v)
+// so keys sort by value descending, then index ascending; NaN has no key
+// (0 marks an empty slot; every real key is larger).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t sample_key(float x, int v) {
+    if (x != x) return 0;
+    uint32_t u = __float_as_uint(x == 0.0f ? 0.0f : x);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)v);
+}
+__device__ __forceinline__ float key_value(uint64_t k) {
+    uint32_t u = (uint32_t)(k >> 32);
+    u = (u & 0x80000000u) ? (u & 0x7fffffffu) : ~u;
+    return __uint_as_float(u);
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)k, o, 64), hi = __shfl_xor((uint32_t)(k >> 32), o, 64);
+        const uint64_t ok = ((uint64_t)hi << 32) | lo;
+        k = ok > k ? ok : k;
+    }
+    return k;
+}
+
+// Slice (4096 logits) x row: each wave takes the top_k keys of its 1024
+// logits by rounds of wave maxima; thread 0 merges the four sorted lists.
+extern "C" __global__ __launch_bounds__(256) void lgx_k_sample_partial(const lgx_sample_args a) {
+    __shared__ uint64_t lst[4][LGX_SAMPLE_MAX_K];
+    const int sl = blockIdx.x, b = blockIdx.y, t = threadIdx.x, w = t >> 6, l = t & 63;
+    const int64_t stride = (int64_t)a.m * a.vocab;
+    const int v0 = sl * LGX_ARGMAX_SLICE + w * 1024 + l;
+    uint64_t k[16];
+#pragma unroll
+    for (int c = 0; c < 16; c += 4) {
+        bool on[4];
+        float x[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) on[e] = v0 + 64 * (c + e) < a.vocab;
+        tree_partials_n<4, 8>(a.part, a.nr, stride, (int64_t)b * a.vocab + v0 + 64 * c, 64, on, x);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) k[c + e] = on[e] ? sample_key(x[e], v0 + 64 * (c + e)) : 0;
+    }
+    uint64_t lm = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lm = k[i] > lm ? k[i] : lm;
+    for (int r = 0; r < a.top_k; ++r) {
+        const uint64_t best = wave_max_u64(lm);
+        if (l == 0) lst[w][r] = best;
+        if (best == 0) {
+            for (int q = r + 1 + l; q < a.top_k; q += 64) lst[w][q] = 0;
+            break;                                   // wave-uniform
+        }
+        if (lm == best) {                            // keys are unique: one lane
+            lm = 0;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                k[i] = k[i] == best ? 0 : k[i];
+                lm = k[i] > lm ? k[i] : lm;
+            }
+        }
+    }
+    __syncthreads();
+    if (t == 0) {
+        int h[4] = {0, 0, 0, 0};
+        uint64_t* out = a.cand + ((int64_t)b * a.nslices + sl) * LGX_SAMPLE_MAX_K;
+        for (int r = 0; r < a.top_k; ++r) {
+            int wi = 0;
+            uint64_t best = 0;
+            for (int q = 0; q < 4; ++q) {
+                const uint64_t c = h[q] < a.top_k ? lst[q][h[q]] : 0;
+                if (c > best) {
+                    best = c;
+                    wi = q;
+                }
+            }
+            out[r] = best;
+            if (best) ++h[wi];
+        }
+    }
+}
+
+__device__ __forceinline__ uint64_t sm_mix(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// Row b: the top_k keys of the slice lists (rounds of wave maxima over the
+// list heads), then on lane 0, in key order j = 0, 1, ...:
+//   e_j = lgx_expf((v_j - v_0) * inv_temp), c_j = c_{j-1} + e_j (c_{-1} = 0)
+//   J   = first j with c_j >= top_p * c_{n-1}
+//   u   = (x >> 40) * 2^-24, x = element pos of stream stream0 + b of seed
+//   pick the first j <= J with c_j > u * c_J (J if none)
+extern "C" __global__ __launch_bounds__(64) void lgx_k_sample_final(const lgx_sample_args a) {
+    __shared__ uint64_t top[LGX_SAMPLE_MAX_K];
+    const int b = blockIdx.x, l = threadIdx.x;
+    const uint64_t* lists = a.cand + (int64_t)b * a.nslices * LGX_SAMPLE_MAX_K;
+    int h = 0;
+    uint64_t head = l < a.nslices ? lists[(int64_t)l * LGX_SAMPLE_MAX_K] : 0;
+    int n = 0;
+    for (int r = 0; r < a.top_k; ++r) {
+        const uint64_t best = wave_max_u64(head);
+        if (best == 0) break;                        // wave-uniform
+        if (l == 0) top[r] = best;
+        n = r + 1;
+        if (head == best) {
+            ++h;
+            head = h < a.top_k ? lists[(int64_t)l * LGX_SAMPLE_MAX_K + h] : 0;
+        }
+    }
+    __syncthreads();
+    if (l != 0) return;
+    int tok = 0;
+    const int pos = a.pos ? a.pos[b] : a.seq_len[b];
+    if (n > 0) {
+        const float v0 = key_value(top[0]);
+        float c[LGX_SAMPLE_MAX_K];
+        float acc = 0.0f;
+        for (int j = 0; j < n; ++j) {
+            acc = acc + lgx_expf((key_value(top[j]) - v0) * a.inv_temp);
+            c[j] = acc;
+        }
+        const float thr = a.top_p * acc;
+        int J = n - 1;
+        for (int j = 0; j < n; ++j)
+            if (c[j] >= thr) {
+                J = j;
+                break;
+            }
+        const uint64_t sb = sm_mix(a.seed + 0x9E3779B97F4A7C15ull) ^
+                            sm_mix(((uint64_t)(a.stream0 + b) + 1ull) * 0xD1B54A32D192ED03ull);
+        const uint64_t x = sm_mix(sb + ((uint64_t)pos + 1ull) * 0x9E3779B97F4A7C15ull);
+        const float u = (float)(uint32_t)(x >> 40) * 0x1.0p-24f;
+        const float r = u * c[J];
+        int pick = J;
+        for (int j = 0; j <= J; ++j)
+            if (c[j] > r) {
+                pick = j;
+                break;
+            }
+        tok = (int)(0xffffffffu - (uint32_t)top[pick]);
+    }
+    a.tokens[b] = tok;
+    if (a.seq_len) a.seq_len[b] += a.advance;
+}
+
 extern "C" __global__ __launch_bounds__(64) void lgx_k_advance(const lgx_advance_args a) {
     const int b = blockIdx.x * 64 + threadIdx.x;
     if (b < a.m) a.seq_len[b] = (a.keep ? a.seq_len[b] : 0) + a.add;

@@ -66,6 +66,8 @@ struct lgx_model {
     float* attn_part = nullptr;
     float* logits = nullptr;
     float* cand = nullptr;     // argmax candidates [max_batch][slices] (value, index)
+    uint64_t* scand = nullptr; // sampling candidates [max_batch][slices][LGX_SAMPLE_MAX_K]
+    SampleParams samp;         // top_k 0: greedy
     int32_t last_nr = 1;       // partial count of the last lm_head
     int32_t last_B = 0;        // batch of the last lm_head
     std::vector<void*> allocs;
@@ -308,6 +310,9 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
     }
     md->last_nr = nr;
     md->last_B = B;
+    if (md->samp.top_k > 0)   // draw index: the position just consumed (seq_len before += 1)
+        return launch_sample(c, md->samp, lg, nr, B, cf.vocab, nullptr, next, md->seq_len, 1,
+                             md->scand, stream);
     return launch_argmax(c, lg, nr, B, cf.vocab, next, md->seq_len, 1, md->cand, stream);
 }
 
@@ -624,7 +629,9 @@ lgx_status lgx_model_create(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t see
             (st = dev_alloc(m, &m->q, (size_t)B * hq * d)) || (st = dev_alloc(m, &m->part, (size_t)part)) ||
             (st = dev_alloc(m, &m->attn_part, (size_t)B * hq * m->nchunk * (d + 2))) ||
             (st = dev_alloc(m, &m->logits, cf.tied_embedding ? (size_t)B * cf.vocab : 1)) ||
-            (st = dev_alloc(m, &m->cand, (size_t)B * argmax_slices(cf.vocab) * 2)))
+            (st = dev_alloc(m, &m->cand, (size_t)B * argmax_slices(cf.vocab) * 2)) ||
+            (cf.vocab <= 64 * LGX_ARGMAX_SLICE &&
+             (st = dev_alloc(m, &m->scand, sample_cand_bytes(B, cf.vocab) / 8))))
             return done(st);
         // staging no longer needed
         LGX_HIP(hipDeviceSynchronize());
@@ -818,6 +825,28 @@ lgx_status lgx_model_tensor(lgx_model* m, int32_t layer, int32_t which, const vo
             default:
                 return fail(LGX_INVALID_ARGUMENT, "unknown tensor id %d", which);
         }
+    });
+}
+
+lgx_status lgx_model_set_sampling(lgx_model* m, float temperature, int32_t top_k, float top_p,
+                                  uint64_t seed) {
+    return guarded(__func__, [&]() -> lgx_status {
+        if (!valid_model(m)) return fail(LGX_INVALID_HANDLE, "invalid lgx_model handle");
+        SampleParams sp;   // greedy
+        if (temperature != 0.0f) {
+            lgx_status st = sample_check(top_k, top_p, temperature, m->c.vocab, &sp);
+            if (st != LGX_OK) return st;
+            if (!m->scand) return fail(LGX_UNSUPPORTED, "no sampling buffer for this vocabulary");
+            sp.seed = seed;
+        }
+        // recorded steps hold the old head: drop them (after the device is
+        // done with any replay still in flight)
+        LGX_HIP(hipSetDevice(m->ctx->device));
+        if (!m->graphs.empty()) LGX_HIP(hipDeviceSynchronize());
+        for (lgx_model::StepGraph& g : m->graphs) (void)hipGraphExecDestroy(g.exec);
+        m->graphs.clear();
+        m->samp = sp;
+        return LGX_OK;
     });
 }
 

@@ -619,6 +619,81 @@ void orc_lm_head_f16(const float* x, int32_t m, const uint16_t* E, int32_t V, in
  *   L+6,7    Wdown Q8_0                                 [hidden][inter]
  *   L+8      qkv bias, binary32 N(0, 0.02)              [(hq+2hkv)d]
  * with L = 1000 + 16 * layer.  RMSNorm weights are 1.0. */
+/* ------------------------------------------------------------------ */
+/* Seeded top-k / top-p sampling                                       */
+/* ------------------------------------------------------------------ */
+/* Candidate order: value descending, then index ascending; NaN is never a
+ * candidate and -0 ranks as +0.  The key packs (orderable value bits, 2^32-1
+ * - index), so the order is the plain unsigned order of keys. */
+static uint64_t sample_key(float x, int32_t v) {
+    if (x != x) return 0;
+    uint32_t u = f2u(x == 0.0f ? 0.0f : x);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)v);
+}
+static float key_value(uint64_t k) {
+    uint32_t u = (uint32_t)(k >> 32);
+    u = (u & 0x80000000u) ? (u & 0x7fffffffu) : ~u;
+    return u2f(u);
+}
+static int key_desc(const void* a, const void* b) {
+    uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
+    return x < y ? 1 : x > y ? -1 : 0;
+}
+
+/* One row: the top_k candidates in order j = 0, 1, ...;
+ *   e_j = orc_expf((l_j - l_0) * (1/temperature)), c_j = c_{j-1} + e_j
+ *   J = first j with c_j >= top_p * c_{n-1}
+ *   u = (x >> 40) * 2^-24, x = element pos of SplitMix64 stream `stream` of
+ *       seed (orc_stream_base convention)
+ *   token = candidate of the first j <= J with c_j > u * c_J (J if none). */
+int32_t orc_sample_row(const float* logits, int32_t vocab, int32_t top_k, float top_p,
+                       float temperature, uint64_t seed, int32_t stream, int32_t pos) {
+    uint64_t* keys = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)(vocab > 0 ? vocab : 1));
+    int32_t nv = 0;
+    for (int32_t v = 0; v < vocab; ++v) {
+        uint64_t k = sample_key(logits[v], v);
+        if (k) keys[nv++] = k;
+    }
+    qsort(keys, (size_t)nv, sizeof(uint64_t), key_desc);
+    int32_t n = nv < top_k ? nv : top_k;
+    int32_t tok = 0;
+    if (n > 0) {
+        const float inv_temp = 1.0f / temperature;
+        const float v0 = key_value(keys[0]);
+        float c[64];
+        float acc = 0.0f;
+        for (int32_t j = 0; j < n; ++j) {
+            acc = acc + orc_expf((key_value(keys[j]) - v0) * inv_temp);
+            c[j] = acc;
+        }
+        const float thr = top_p * acc;
+        int32_t J = n - 1;
+        for (int32_t j = 0; j < n; ++j)
+            if (c[j] >= thr) { J = j; break; }
+        uint64_t x = stream_at(orc_stream_base(seed, (uint64_t)stream), (uint64_t)pos);
+        const float u = (float)(uint32_t)(x >> 40) * 0x1.0p-24f;
+        const float r = u * c[J];
+        int32_t pick = J;
+        for (int32_t j = 0; j <= J; ++j)
+            if (c[j] > r) { pick = j; break; }
+        tok = (int32_t)(0xffffffffu - (uint32_t)keys[pick]);
+    }
+    free(keys);
+    return tok;
+}
+
+/* m rows; row i uses stream streams[i] and draw index pos[i].  top_k in
+ * [1, 64]. */
+void orc_sample(const float* logits, int32_t m, int32_t vocab, int32_t top_k, float top_p,
+                float temperature, uint64_t seed, const int32_t* streams, const int32_t* pos,
+                int32_t* out) {
+#pragma omp parallel for schedule(dynamic)
+    for (int32_t i = 0; i < m; ++i)
+        out[i] = orc_sample_row(logits + (int64_t)i * vocab, vocab, top_k, top_p, temperature,
+                                seed, streams[i], pos[i]);
+}
+
 struct orc_model {
     orc_qwen_config c;
     uint64_t seed;
@@ -634,6 +709,9 @@ struct orc_model {
     uint16_t **kc, **vc;   /* per layer paged [max_batch*maxp][hkv][16][d] */
     int32_t* page_table;   /* identity: slot b page p -> b*maxp + p */
     int32_t* seq_len;
+    int32_t s_top_k;       /* 0: greedy argmax; else orc_sample_row with: */
+    float s_top_p, s_temp;
+    uint64_t s_seed;
 };
 
 static void* xmalloc(size_t n) {
@@ -832,7 +910,10 @@ void orc_model_step(orc_model* m, int32_t nseq, const int32_t* slots, const int3
         orc_q8_gemm(m->lm_qs, m->lm_d, c->vocab, H, xq, xd, B, logits);
     }
     for (int32_t i = 0; i < B; ++i) {
-        next[i] = orc_argmax(logits + (int64_t)i * c->vocab, c->vocab);
+        next[i] = m->s_top_k > 0
+                      ? orc_sample_row(logits + (int64_t)i * c->vocab, c->vocab, m->s_top_k,
+                                       m->s_top_p, m->s_temp, m->s_seed, slots[i], lens[i] - 1)
+                      : orc_argmax(logits + (int64_t)i * c->vocab, c->vocab);
         m->seq_len[slots[i]] = lens[i];
     }
     if (logits_out) memcpy(logits_out, logits, sizeof(float) * (size_t)B * c->vocab);
@@ -927,7 +1008,11 @@ void orc_model_prefill(orc_model* m, int32_t nseq, const int32_t* slots, int32_t
         orc_q8_gemm(m->lm_qs, m->lm_d, c->vocab, H, xq, xd, nseq, logits);
     }
     for (int32_t s = 0; s < nseq; ++s) {
-        next[s] = orc_argmax(logits + (int64_t)s * c->vocab, c->vocab);
+        next[s] = m->s_top_k > 0
+                      ? orc_sample_row(logits + (int64_t)s * c->vocab, c->vocab, m->s_top_k,
+                                       m->s_top_p, m->s_temp, m->s_seed, slots[s],
+                                       m->seq_len[slots[s]] + P - 1)
+                      : orc_argmax(logits + (int64_t)s * c->vocab, c->vocab);
         m->seq_len[slots[s]] += P;
     }
     if (logits_out) memcpy(logits_out, logits, sizeof(float) * (size_t)nseq * c->vocab);
@@ -953,3 +1038,13 @@ void orc_model_load_kv(orc_model* m, int32_t layer, int32_t kv, int32_t b, int32
 }
 
 void orc_model_set_seq_len(orc_model* m, int32_t slot, int32_t len) { m->seq_len[slot] = len; }
+
+/* Token choice of later steps and prefills: temperature 0 = greedy; else
+ * orc_sample_row with stream = slot and draw index = the consumed position. */
+void orc_model_set_sampling(orc_model* m, float temperature, int32_t top_k, float top_p,
+                            uint64_t seed) {
+    m->s_top_k = temperature != 0.0f ? top_k : 0;
+    m->s_temp = temperature;
+    m->s_top_p = top_p;
+    m->s_seed = seed;
+}

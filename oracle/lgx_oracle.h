@@ -58,6 +58,12 @@
  *                    attention-chunk boundaries (tests/test_oracle_model.py)
  *   load_kv          round trip with orc_model_kv; decoding after a loaded
  *                    cache equals decoding after the prefill that made it
+ *   sample           top_k = 1 and a tiny top_p give the argmax; equal
+ *                    logits pick only the lowest top_k indices, uniformly;
+ *                    NaN never drawn; the frequencies of 200k seeded draws
+ *                    match a float64 numpy statement of the top-k / nucleus
+ *                    distribution (tests/test_oracle_sample.py), and
+ *                    SplitMix64 draws follow the published vectors
  * None of these is "parity unpinned": each has the checks above, chosen so
  * that a dropped term, wrong sign or transposed operand fails one of them.
  */
@@ -147,6 +153,15 @@ void orc_model_prefill(orc_model* m, int32_t nseq, const int32_t* slots, int32_t
 void orc_model_load_kv(orc_model* m, int32_t layer, int32_t kv, int32_t b, int32_t n,
                        const uint16_t* rows);
 void orc_model_set_seq_len(orc_model* m, int32_t slot, int32_t len);
+void orc_model_set_sampling(orc_model* m, float temperature, int32_t top_k, float top_p,
+                            uint64_t seed);
+
+/* ---- seeded top-k / top-p sampling (the rule of lgx_sample) ---- */
+int32_t orc_sample_row(const float* logits, int32_t vocab, int32_t top_k, float top_p,
+                       float temperature, uint64_t seed, int32_t stream, int32_t pos);
+void orc_sample(const float* logits, int32_t m, int32_t vocab, int32_t top_k, float top_p,
+                float temperature, uint64_t seed, const int32_t* streams, const int32_t* pos,
+                int32_t* out);
 
 #ifdef __cplusplus
 }

@@ -85,6 +85,9 @@ def lib():
             "orc_model_prefill": (None, [_P, _I32, _P, _I32, _P, _P, _P, _P]),
             "orc_model_load_kv": (None, [_P, _I32, _I32, _I32, _I32, _P]),
             "orc_model_set_seq_len": (None, [_P, _I32, _I32]),
+            "orc_model_set_sampling": (None, [_P, C.c_float, _I32, C.c_float, C.c_uint64]),
+            "orc_sample": (None, [_P, _I32, _I32, _I32, C.c_float, C.c_float, C.c_uint64, _P,
+                                  _P, _P]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -349,6 +352,19 @@ def lm_head_f16(x, E):
     return out
 
 
+def sample(logits, top_k: int, top_p: float, temperature: float, seed: int, streams, pos):
+    """Seeded top-k / top-p draw per row of logits [m][vocab] (the rule of
+    lgx_sample); row i uses SplitMix64 stream streams[i] at index pos[i]."""
+    logits = _c(logits, np.float32)
+    m, vocab = logits.shape
+    streams = _c(np.broadcast_to(np.asarray(streams, np.int32), (m,)), np.int32)
+    pos = _c(np.broadcast_to(np.asarray(pos, np.int32), (m,)), np.int32)
+    out = np.empty(m, np.int32)
+    lib().orc_sample(_ptr(logits), m, vocab, top_k, top_p, temperature, seed, _ptr(streams),
+                     _ptr(pos), _ptr(out))
+    return out
+
+
 # ---- random-init Qwen2-shaped model ------------------------------------------
 
 class QwenConfigC(C.Structure):
@@ -448,6 +464,12 @@ class Model:
 
     def set_seq_len(self, slot: int, n: int) -> None:
         lib().orc_model_set_seq_len(self.h, slot, n)
+
+    def set_sampling(self, temperature: float, top_k: int = 1, top_p: float = 1.0,
+                     seed: int = 0) -> None:
+        """Seeded top-k / top-p token choice (temperature 0: greedy); stream =
+        slot, draw index = the consumed position."""
+        lib().orc_model_set_sampling(self.h, temperature, top_k, top_p, seed)
 
 
 EMB_SIGMA = 0.002
