@@ -12,15 +12,24 @@ Infinity Cache) that every step streams them from HBM.
 
 Headline `value`: algorithmic GB/s of the M = 1 step (weights + scales +
 activations + outputs, each counted once).  `roofline` is the dominant kernel
-(lgx_k_q8_gemv_grp16 for this group: the grouped launch itself), timed per launch by HIP
-events attached to its own dispatch (lgx_ctx_set_kernel_timing) on its
-stream, in a separate pass over the same steps.  Launches are queued behind a
-device-side sleep before the timed region opens, so the step time is the
-device's, not the Python loop's.  The M sweep (1, 8, 32, 64) is reported
-alongside, with its int8 MFMA utilisation (the M x N x K block-dot work
-against the dense int8 peak): at these M the products are HBM- and
-epilogue-bound, far from the MFMA roofline.  `cpu_baseline` times the CPU oracle (a port: the reference has no
-CPU implementation of this path) on a bounded sample of the same step.
+(lgx_k_q8_gemv_grp16 for this group: the step is that one launch), its
+average duration taken from HIP events around the K un-instrumented
+back-to-back launches of the timed region, on the stream they run on (so it
+can never exceed the step time; the per-dispatch event figure is reported
+beside it as a diagnostic).  Launches are queued behind a device-side sleep
+before the timed region opens, so the step time is the device's, not the
+Python loop's.
+
+`config0`: one Q8_0 GEMV [4864 x 896], binary32 x
+(lgx_q8_gemv_f32) and the int-dot form (lgx_q8q8_gemv_quantize: Q8_0 of x
+fused), per launch over > 512 MB of rotating weight copies.
+
+The M sweep (1, 8, 32, 64) is reported alongside, with its int8 MFMA
+utilisation (the M x N x K block-dot work against the dense int8 peak): at
+these M the products are HBM- and epilogue-bound, far from the MFMA
+roofline.  `cpu_baseline` times the CPU oracle (a port: the reference has no
+CPU implementation of this path) on a bounded sample of the same step, on all
+of its threads and on one.
 
 `decode_attention`: the split-KV decode attention
 alone, B = 16, 12 query / 2 KV heads, head_dim 128, at L = 512, 4096, 32768
@@ -178,8 +187,20 @@ def time_m(ctx, torch, sets, m, steps, warmup, per_launch=False):
     return ms, gemv_ms
 
 
+def cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds=12.0):
-    """The CPU oracle's canonical Q8 x Q8 step (quantise + 3 matmuls, M = 1)."""
+    """The CPU oracle's canonical Q8 x Q8 step (quantise + 3 matmuls, M = 1),
+    on all the oracle's OpenMP threads, then on one."""
     import numpy as np
 
     from oracle import oracle as orc
@@ -191,26 +212,91 @@ def cpu_baseline(seconds=12.0):
         d = (np.abs(rng.normal(0.0, 0.02, size=(n, k // 32))) / 127.0).astype(np.float16)
         x = rng.standard_normal((1, k)).astype(np.float32)
         mats.append((qs, d.view(np.uint16), x))
-    orc.q8_gemm(*mats[0][:2], *orc.quantize_q8_0(mats[0][2]))  # warm (threads, pages)
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        for qs, d, x in mats:
-            xq, xd = orc.quantize_q8_0(x)
-            orc.q8_gemm(qs, d, xq, xd)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+    def run(budget):
+        orc.q8_gemm(*mats[0][:2], *orc.quantize_q8_0(mats[0][2]))  # warm (threads, pages)
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            for qs, d, x in mats:
+                xq, xd = orc.quantize_q8_0(x)
+                orc.q8_gemm(qs, d, xq, xd)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return reps, el
+
+    threads = orc.max_threads()
+    reps, el = run(seconds)
+    orc.set_threads(1)
+    try:
+        reps1, el1 = run(seconds / 2)
+    finally:
+        orc.set_threads(threads)
     return {
         "value": round(step_bytes(1) * reps / el / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{reps} steps of config-1 M=1 (quantise + gate/up/down Q8xQ8, canonical "
-                  f"schedule, OpenMP) in {el:.1f} s",
+        "value_1core": round(step_bytes(1) * reps1 / el1 / 1e9, 3),
+        "cpu_model": cpu_model_name(),
+        "sample": f"config-1 M=1 steps (quantise + gate/up/down Q8xQ8, canonical schedule): "
+                  f"{reps} in {el:.1f} s on {threads} OpenMP threads, {reps1} in {el1:.1f} s "
+                  f"on 1",
     }
+
+
+CONFIG0_SHAPE = (4864, 896)
+
+
+def config0_bench(ctx, torch, launches=400, seed=0):
+    """One Q8_0 GEMV [4864 x 896] per launch (config 0): lgx_q8_gemv_f32
+    (binary32 x) and lgx_q8q8_gemv_quantize (x quantised to Q8_0 in the
+    prologue), over enough weight copies (> 2 x the 256 MB Infinity Cache)
+    that every launch streams from HBM; HIP events around the back-to-back
+    launches, queued behind a device-side sleep."""
+    import numpy as np
+
+    import logicaffeine_amd as lgx
+
+    n, k = CONFIG0_SHAPE
+    wbytes = q8_weight_bytes(n, k)
+    nbytes = wbytes + 4 * (k + n)
+    ncopy = -(-2 * MALL_BYTES // wbytes)
+    rng = np.random.default_rng(seed)
+    qs = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    d = (np.abs(rng.normal(0.0, 0.02, size=(n, k // 32))) / 127.0).astype(np.float16)
+    W0 = ctx.q8_matrix(qs, d.view(np.uint16))
+    Ws = [W0] + [lgx.Q8Matrix(W0.qs.clone(), W0.d.clone(), n, k) for _ in range(ncopy - 1)]
+    x = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(ctx.dev)
+    y = torch.empty(n, dtype=torch.float32, device=ctx.dev)
+    out = {"shape": [n, k], "bytes_per_launch": nbytes, "copies": ncopy,
+           "working_set_MB": round(ncopy * wbytes / 1e6, 1)}
+    for name, call, kern in (
+            ("f32", lambda W: ctx.q8_gemv_f32(W, x, y=y), "lgx_k_q8_gemv_f32"),
+            ("int_dot", lambda W: ctx.q8q8_gemv_quantize(W, x, y=y), "lgx_k_q8_gemv_grp4")):
+        for i in range(2 * ncopy):
+            call(Ws[i % ncopy])
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        call(Ws[0])
+        host_ms = (time.perf_counter() - t) * 1e3
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        queue_ahead(torch, 2.0 * host_ms * launches + 5.0)
+        e0.record()
+        for i in range(launches):
+            call(Ws[i % ncopy])
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / launches * 1e3
+        out[name] = {"kernel": kern, "us_per_launch": round(us, 3),
+                     "GB_s": round(nbytes / us / 1e3, 1),
+                     "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del Ws, W0
+    torch.cuda.empty_cache()
+    return out
 
 
 SUSTAINED_SHAPE = (152064, 3584)   # Qwen2.5-7B lm_head as a Q8_0 matrix (579 MB)
@@ -218,7 +304,8 @@ SUSTAINED_SHAPE = (152064, 3584)   # Qwen2.5-7B lm_head as a Q8_0 matrix (579 MB
 
 def sustained_gemv(ctx, torch, iters=60):
     """Fused-quantise M = 1 GEMV streaming one large Q8_0 matrix (two copies
-    alternate, > 2 x the Infinity Cache), per-launch dispatch-event time."""
+    alternate, > 2 x the Infinity Cache), HIP events around back-to-back
+    launches."""
     import numpy as np
 
     import logicaffeine_amd as lgx
@@ -235,13 +322,20 @@ def sustained_gemv(ctx, torch, iters=60):
         ctx.q8q8_gemv_quantize(Ws[i % 2], x, y=y)
     torch.cuda.synchronize()
     ctx.kernel_timing(True)
-    for i in range(iters):
-        ctx.q8q8_gemv_quantize(Ws[i % 2], x, y=y)
+    ctx.q8q8_gemv_quantize(Ws[0], x, y=y)
     torch.cuda.synchronize()
     ctx.kernel_timing(False)
-    stats = [(name, ctx.kernel_stats(name)) for name in DOMINANT]
-    name, (cnt, tot) = max(stats, key=lambda s: s[1][0])
-    us = tot / max(cnt, 1) * 1e3
+    name = max(DOMINANT, key=lambda nm: ctx.kernel_stats(nm)[0])
+    # back-to-back launches, HIP events around them
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    queue_ahead(torch, 1.0 * iters + 5.0)
+    e0.record()
+    for i in range(iters):
+        ctx.q8q8_gemv_quantize(Ws[i % 2], x, y=y)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / iters * 1e3
     nbytes = q8_weight_bytes(n, k) + 4 * (k + n)
     del Ws, W0
     torch.cuda.empty_cache()
@@ -318,7 +412,7 @@ DECODE_CONFIGS = {
 }
 
 
-def decode_bench(ctx, torch, key, seed=3):
+def decode_bench(ctx, torch, key, seed=3, with_cpu=True):
     """Prefill a random prompt per sequence, then time the greedy decode
     steps (each: the whole model for B sequences + argmax + KV append)."""
     import logicaffeine_amd as lgx
@@ -361,8 +455,20 @@ def decode_bench(ctx, torch, key, seed=3):
     ctxlen = P + 1 + (steps + 1) / 2.0        # mean attended tokens over the timed steps
     step_bytes_ = lgx.decode_step_bytes(cfg, B, ctxlen)
     gbs = step_bytes_ / (ms * 1e-3) / 1e9
+    # sequence 0's cache and current token, for the CPU baseline at this context
+    import numpy as np
+
+    ctx_now = P + 1 + steps + eager_steps
+    kv0 = None
+    if with_cpu:
+        maxp = -(-cfg["max_seq"] // 16)
+        pt = gm.tensor_bytes("page_table").view(np.int32).reshape(B, maxp)
+        kv0 = [[gm.kv_rows(layer, w, 0, ctx_now, pt) for w in (0, 1)]
+               for layer in range(cfg["n_layers"])]
+    tok0 = int(tok[0].item())
     gm.close()
     torch.cuda.empty_cache()
+    pf_int8 = lgx.prefill_int8_ops(cfg, B, P)
     out = {
         "model": f"random-init Qwen2.5-{shape.upper()}-shaped Q8_0 "
                  f"({'tied binary16' if cfg['tied'] else 'Q8_0'} lm_head)",
@@ -375,7 +481,11 @@ def decode_bench(ctx, torch, key, seed=3):
                     "roofline": {"bound": "valu", "achieved": round(pf_ops / prefill_s / 1e12, 2),
                                  "peak": round(lgx.VALU_LANE_OPS_PEAK / 1e12, 2),
                                  "unit": "T lane-op/s", "frac": round(pf_ops / prefill_s / lgx.VALU_LANE_OPS_PEAK, 4),
-                                 "ops": pf_ops}},
+                                 "ops": pf_ops},
+                    "mfma": {"int8_ops": pf_int8,
+                             "achieved_TOPS": round(pf_int8 / prefill_s / 1e12, 1),
+                             "peak_TOPS": INT8_MFMA_PEAK_TOPS,
+                             "utilisation": round(pf_int8 / prefill_s / 1e12 / INT8_MFMA_PEAK_TOPS, 4)}},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "bytes_per_step": int(step_bytes_),
@@ -384,36 +494,54 @@ def decode_bench(ctx, torch, key, seed=3):
     print(f"[bench] {key}: {out['tokens_per_s']} tok/s, {ms:.3f} ms/step (graph), "
           f"{eager_ms:.3f} ms/step (eager), {gbs:.0f} GB/s",
           file=sys.stderr, flush=True)
+    if with_cpu:
+        out["cpu_baseline"] = cpu_decode_baseline(key, cfg, seed, kv0, ctx_now, tok0)
     return out
 
 
-def cpu_decode_baseline(key, seconds=8.0):
-    """The CPU oracle model (a port; exact canonical arithmetic) on a bounded
-    sample: the same shape, one sequence, 8-token prompt, greedy steps until
-    `seconds` have passed."""
+def cpu_decode_baseline(key, cfg, seed, kv0, ctx_now, tok0, seconds=8.0):
+    """The CPU oracle model (a port; exact canonical arithmetic) decoding
+    sequence 0 of the benchmark at the benchmark's context: the device's
+    prefilled cache of that sequence (bit-identical to the oracle's, which the
+    GPU tests check) is loaded into the oracle, then greedy steps are timed
+    for `seconds` on all of its threads and for seconds / 2 on one."""
     import numpy as np
 
-    import logicaffeine_amd as lgx
     from oracle import oracle as orc
 
     shape = DECODE_CONFIGS[key][0]
-    cfg = lgx.qwen_shape(shape, 1, 64)
-    om = orc.Model(cfg, 3)
-    tok = np.arange(8, dtype=np.int32) * 7 + 1
-    for p in range(8):
-        nxt = om.step(np.zeros(1, np.int32), tok[p:p + 1])
-    t0 = time.perf_counter()
-    n = 0
-    while n < 48:
-        nxt = om.step(np.zeros(1, np.int32), nxt)
-        n += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    el = time.perf_counter() - t0
+    ocfg = dict(cfg, max_batch=1, max_seq=ctx_now + 64)
+    om = orc.Model(ocfg, seed)
+    for layer, (k, v) in enumerate(kv0):
+        om.load_kv(layer, 0, 0, k)
+        om.load_kv(layer, 1, 0, v)
+    om.set_seq_len(0, ctx_now)
+
+    def run(budget, cap):
+        nxt = np.array([tok0], np.int32)
+        t0 = time.perf_counter()
+        n = 0
+        while n < cap:
+            nxt = om.step(np.zeros(1, np.int32), nxt)
+            n += 1
+            if time.perf_counter() - t0 >= budget:
+                break
+        return n, time.perf_counter() - t0
+
+    threads = orc.max_threads()
+    n, el = run(seconds, 32)
+    om.set_seq_len(0, ctx_now)
+    orc.set_threads(1)
+    try:
+        n1, el1 = run(seconds / 2, 16)
+    finally:
+        orc.set_threads(threads)
     om.close()
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {"value": round(n / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{shape} shape, batch 1, 8-token prompt, {n} greedy steps in {el:.1f} s"}
+            "value_1core": round(n1 / el1, 4), "cpu_model": cpu_model_name(),
+            "sample": f"{shape} shape, sequence 0 of the batch at context {ctx_now} (device-"
+                      f"prefilled cache loaded into the oracle), batch 1: {n} greedy steps in "
+                      f"{el:.1f} s on {threads} threads, {n1} in {el1:.1f} s on 1"}
 
 
 def main():
@@ -465,7 +593,10 @@ def main():
     per_launch = gemv_launch_bytes()
     if not gemv_ms:
         raise SystemExit("bench: no dispatch of the grouped GEMV kernels was timed")
-    achieved = per_launch / (gemv_ms * 1e-3) / 1e9
+    # the step is one launch of the dominant kernel: its average duration is
+    # the un-instrumented back-to-back time of the timed region
+    launch_ms = ms1_plain
+    achieved = per_launch / (launch_ms * 1e-3) / 1e9
     out = {
         "metric": "Q8 GEMV HBM GB/s (% peak); batched Qwen decode tokens/sec on 1 MI355X",
         "value": round(value, 1),
@@ -496,10 +627,13 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": TRAFFIC_BYTES if DOMINANT_USED == "lgx_k_q8_gemv_grp16" else None,
-            "avg_launch_us": round(gemv_ms * 1e3, 3),
+            "avg_launch_us": round(launch_ms * 1e3, 3),
+            "timing": "HIP events around the timed region's back-to-back launches (one per step)",
+            "dispatch_event_us": round(gemv_ms * 1e3, 3),
             "bytes_per_launch": int(per_launch),
         },
     }
+    assert launch_ms <= ms1_plain
     del sets
     torch.cuda.empty_cache()
     if args.copy_calibration:
@@ -516,6 +650,11 @@ def main():
     print(f"[bench] sustained GEMV {SUSTAINED_SHAPE}: {sustained['us_per_launch']} us, "
           f"{sustained['GB_s']} GB/s", file=sys.stderr, flush=True)
     out["config"]["sustained_gemv_m1"] = sustained
+    c0 = config0_bench(ctx, torch)
+    print(f"[bench] config0 4864x896: f32 {c0['f32']['us_per_launch']} us "
+          f"{c0['f32']['GB_s']} GB/s, int-dot {c0['int_dot']['us_per_launch']} us "
+          f"{c0['int_dot']['GB_s']} GB/s", file=sys.stderr, flush=True)
+    out["config0"] = c0
     attn = attention_bench(ctx, torch)
     print("[bench] config-2 decode attention: " + ", ".join(
         f"{k} {v['chunk_kernel_us'] + v['merge_us']:.1f} us {v['GB_s']} GB/s"
@@ -523,9 +662,7 @@ def main():
     out["decode_attention"] = attn
     decode = {}
     for key in [k for k in args.decode.split(",") if k]:
-        decode[key] = decode_bench(ctx, torch, key)
-        if not args.no_cpu:
-            decode[key]["cpu_baseline"] = cpu_decode_baseline(key)
+        decode[key] = decode_bench(ctx, torch, key, with_cpu=not args.no_cpu)
     if decode:
         out["qwen_decode"] = decode
     if not args.no_cpu:

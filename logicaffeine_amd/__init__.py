@@ -126,6 +126,23 @@ def decode_step_bytes(cfg: dict, B: int, context: float) -> float:
 VALU_LANE_OPS_PEAK = 256 * 4 * 16 * 2.4e9
 
 
+def prefill_int8_ops(cfg: dict, B: int, P: int) -> float:
+    """int8 MFMA operations (2 per multiply-add) of the Q8_0 products of the
+    prefill of B prompts of P tokens: rows B x (P - 1) through the batched
+    chunks (the last layer of a chunk runs its QKV product only), the last
+    position of every prompt through the decode step, and the untied lm_head
+    for those B rows (the tied lm_head is a binary16 VALU chain)."""
+    H, I, d = cfg["hidden"], cfg["inter"], cfg["head_dim"]
+    hq, hkv, L, V = cfg["n_heads"], cfg["n_kv"], cfg["n_layers"], cfg["vocab"]
+    qkv = (hq + 2 * hkv) * d * H
+    full = qkv + H * hq * d + 2 * I * H + H * I
+    rows = B * (P - 1)
+    macs = rows * ((L - 1) * full + qkv) + B * L * full
+    if not cfg["tied"]:
+        macs += B * V * H
+    return 2.0 * macs
+
+
 def prefill_valu_ops(cfg: dict, B: int, P: int) -> float:
     """Essential VALU lane operations of the canonical prefill of B prompts of
     P tokens (rows B x (P - 1) through the batched chunks, the last position
@@ -630,6 +647,31 @@ class Model:
         _check_hip(C.CDLL("libamdhip64.so").hipMemcpy(
             out.ctypes.data_as(C.c_void_p), C.c_void_p(p), C.c_size_t(n), 2))
         return out
+
+
+    def kv_rows(self, layer: int, which: int, b: int, n: int, page_table=None):
+        """Host copy of the first n cached K (which 0) or V (1) rows of
+        sequence b at `layer`: binary16 [n][n_kv][head_dim] (gathered page by
+        page through the model's page table)."""
+        import numpy as np
+
+        cfg = self.cfg
+        hkv, d = cfg["n_kv"], cfg["head_dim"]
+        maxp = -(-cfg["max_seq"] // 16)
+        if page_table is None:
+            page_table = self.tensor_bytes("page_table").view(np.int32).reshape(
+                cfg["max_batch"], maxp)
+        p, _ = self.tensor_ptr("k_pages" if which == 0 else "v_pages", layer)
+        page_bytes = hkv * 16 * d * 2
+        npg = -(-n // 16)
+        buf = np.empty((npg, hkv, 16, d), np.uint16)
+        hip = C.CDLL("libamdhip64.so")
+        self.ctx.torch.cuda.current_stream(self.ctx.dev).synchronize()
+        for i in range(npg):
+            _check_hip(hip.hipMemcpy(buf[i].ctypes.data_as(C.c_void_p),
+                                     C.c_void_p(p + int(page_table[b, i]) * page_bytes),
+                                     C.c_size_t(page_bytes), 2))
+        return np.ascontiguousarray(buf.transpose(0, 2, 1, 3).reshape(npg * 16, hkv, d)[:n])
 
 
 def _check_hip(err: int) -> None:

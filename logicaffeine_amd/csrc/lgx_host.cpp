@@ -236,7 +236,9 @@ lgx_status lgx_q8q8_gemv(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq,
         if (st != LGX_OK) return st;
         if ((st = check_q8(W)) != LGX_OK) return st;
         if (!xq || !xd || !y) return fail(LGX_NULL_POINTER, "NULL xq, xd or y");
-        if (use_wg(c, W)) {
+        // the int32 block dots come from the v_dot4 GEMV (or the whole-K
+        // kernel); the grouped kernel keeps stores out of its load loop
+        if (use_wg(c, W) && (!dbg || c->gemv_whole)) {
             lgx_gemv_mat m = gemv_mat(W, nullptr, xq, xd, y, 0);
             m.dbg = dbg;
             return run_gemv_group(c, &m, 1, stream);

@@ -587,13 +587,43 @@ inline lgx_status run_gemv_group(lgx_ctx* c, const lgx_gemv_mat* mats, int count
     }
     int W = nrmax <= 4 ? 4 : nrmax <= 8 ? 8 : 16;
     if (c->gemv_wgs == 4 || c->gemv_wgs == 8 || c->gemv_wgs == 16) W = c->gemv_wgs;
+    // Tiles per workgroup: the smallest per-workgroup byte budget T for which
+    // the grid fits the device (ncu * 16 / W workgroups, each CU holding 16
+    // waves), tpw_i = clamp(T / tile bytes, 1, W / ranges): the bytes per
+    // workgroup are as even as whole tiles allow.
+    int tmax[LGX_GROUP_MAX], tpw[LGX_GROUP_MAX], nrg[LGX_GROUP_MAX];
+    double tb[LGX_GROUP_MAX];
+    std::vector<double> cand;
+    for (int i = 0; i < count; ++i) {
+        nrg[i] = (mats[i].k / 32 + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS;
+        tmax[i] = W / std::min(nrg[i], W);
+        tb[i] = 17.0 * mats[i].k;                      // 16 rows x k x 1.0625 B
+        for (int j = 1; j <= tmax[i]; ++j) cand.push_back(j * tb[i]);
+    }
+    std::sort(cand.begin(), cand.end());
+    const int64_t cap = (int64_t)c->ncu * (16 / W);
+    auto grid_for = [&](double T, int* tp) {
+        int64_t n = 0;
+        for (int i = 0; i < count; ++i) {
+            tp[i] = std::max(1, std::min(tmax[i], (int)(T / tb[i] + 1e-9)));
+            n += (mats[i].n / 16 + tp[i] - 1) / tp[i];
+        }
+        return n;
+    };
+    for (int i = 0; i < count; ++i) tpw[i] = tmax[i];
+    for (double T : cand) {
+        int tp[LGX_GROUP_MAX];
+        if (grid_for(T, tp) <= cap) {
+            std::copy(tp, tp + count, tpw);
+            break;
+        }
+    }
     for (int i = 0; i < count; ++i) {
         ga.mat[i] = mats[i];
-        const int nb = mats[i].k / 32, nr = (nb + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS;
-        const int tpw = W / std::min(nr, W);
+        ga.mat[i].pad = tpw[i];
         ga.tile0[i] = wgs;
-        wgs += (mats[i].n / 16 + tpw - 1) / tpw;
-        lds = std::max(lds, (size_t)mats[i].k + 4 * (size_t)nb + 64 * (size_t)tpw * nr);
+        wgs += (mats[i].n / 16 + tpw[i] - 1) / tpw[i];
+        lds = std::max(lds, (size_t)W * (1024 + 32 * 4) + 64 * (size_t)tpw[i] * nrg[i]);
     }
     ga.tile0[count] = wgs;
     const Kern k = xf ? (W == 16 ? K_GEMV_GRP16 : W == 8 ? K_GEMV_GRP8 : K_GEMV_GRP4)

@@ -675,139 +675,154 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_mfma_qx(const lg
 // ---------------------------------------------------------------------------
 // Grouped Q8 x Q8 GEMV (M = 1), ranges of a tile inside one workgroup.
 // A launch covers independent matrices (tile0 maps workgroups to matrices).
-// A workgroup of W waves (4, 8 or 16: the group's largest range count,
-// rounded up) serves tpw = W / min(ranges, W) row tiles of one matrix; wave (tile slot, range) requests all 16 of its range's 128-bit
-// T16 loads and scale words at once, multiplies on int8 MFMA with the
-// activation broadcast (D row = block dot of weight row r), and runs the
-// canonical fmaf chain of its range (lanes 0-15 hold row r); the pairwise
-// tree over the tile's ranges is applied in LDS -> y, or the chains are
-// stored as range partials.  Rows of more than W ranges take several
-// ranges per wave.  The activation (quantised to Q8_0 from binary32 by the
-// lgx_k_quantize_q8_0 rule, or copied) is staged in LDS in (pair, chunk)
-// order.  LDS (dynamic): k bytes, k/32 scales, tpw x ranges x 16 chains.
+// A workgroup of W waves (4, 8 or 16) serves tpw row tiles of one matrix
+// (mat.pad, chosen by the launcher to even out the bytes per workgroup, at
+// most W / min(ranges, W)); wave (tile slot, range) streams the 16 units of
+// its range (all GRP_WIN = 16 128-bit T16 loads in flight), multiplies on
+// int8 MFMA with the activation broadcast (D row = block dot of weight row
+// r), and runs the canonical fmaf chain of its range (lanes 0-15 hold row r);
+// the pairwise tree over the tile's ranges is applied in LDS -> y, or the
+// chains are stored as range partials.  Rows of more than W ranges take
+// several ranges per wave.
+// Each wave stages only its own range of the activation (Q8_0 of binary32
+// by the lgx_k_quantize_q8_0 rule, or a copy) in its own LDS slot, in (pair,
+// chunk) order: no workgroup barrier before the products, so every wave
+// starts as soon as its own data is in.  LDS (dynamic): W x (1 KiB quants +
+// 32 scales), then tpw x ranges x 16 chains.
 // ---------------------------------------------------------------------------
-// The activation loads are issued before the weight loads: the hardware
-// counts loads in issue order, so waiting for the activation then does not
-// also wait for the weights, and the range math can start as soon as each
-// weight unit arrives.  Every load is issued (addresses clamped), which keeps
-// the compiler's wait counts exact.  GRP_XB 16-byte slots per thread cover
-// k <= 8 * GRP_XB * threads (binary32) or k <= 16 * threads (Q8_0); the rest
-// (rows longer than the workgroup's range count) goes through a loop.
-#define GRP_XB 3
+#define GRP_WIN 16
+#define GRP_XSLOT (1024 + 32 * 4)
+
+// The range's activation, lane l holding the 16 values [16l, 16l + 16) of
+// the range (block l/2, half l%2): binary32 (4 x 16 bytes) or Q8_0 (16
+// quants + the block scale).
 template <bool XF>
-__device__ __forceinline__ void grp_x_issue(const lgx_gemv_mat& a, uint4 (&xr)[GRP_XB]) {
-    const int nb = a.k >> 5, np = a.k >> 6, tid = threadIdx.x, nt = blockDim.x;
+__device__ __forceinline__ void grp_x_load(const lgx_gemv_mat& a, const RangeInfo& ri, int lane,
+                                           uint4 (&xr)[4], uint32_t& xdr) {
+    const int bl = min(lane >> 1, ri.nbr - 1);     // lanes past the range re-read its last block
+    const int64_t e0 = (int64_t)(ri.b0 + bl) * 32 + 16 * (lane & 1);
     if constexpr (XF) {
 #pragma unroll
-        for (int u = 0; u < GRP_XB; ++u) {
-            const int sl = min(tid + u * nt, nb * 8 - 1);
-            xr[u] = *(const uint4*)(a.xf + (sl >> 3) * 32 + 4 * (sl & 7));
-        }
+        for (int u = 0; u < 4; ++u) xr[u] = *(const uint4*)(a.xf + e0 + 4 * u);
+        xdr = 0;
     } else {
-        const int s2 = min(tid, 4 * np - 1);
-        const int8_t* src = a.xq + (s2 >> 2) * 64 + 8 * (s2 & 3);
-        const uint2 lo = *(const uint2*)src;
-        const uint2 hi = *(const uint2*)(src + 32);
-        xr[0] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        xr[1].x = a.xd[min(tid, nb - 1)];
+        xr[0] = *(const uint4*)(a.xq + e0);
+        xdr = a.xd[ri.b0 + bl];
     }
 }
 
-// Q8_0 of the 32-block slot sl (8 lanes per block, whole groups) into the
-// LDS staging in (pair, chunk) order (+ the optional Q8_0 outputs).
-__device__ __forceinline__ void grp_quant_slot(const lgx_gemv_mat& a, int sl, const uint4& v,
-                                               int8_t* xs, float* dxs, bool emit) {
-    const int bl = sl >> 3, j = sl & 7;
-    const float f[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
-                        __uint_as_float(v.w)};
-    uint16_t dh;
-    const uint32_t qw = quantize4(f, dh);
-    *(uint32_t*)(xs + ((bl >> 1) * 4 + (j >> 1)) * 16 + (bl & 1) * 8 + 4 * (j & 1)) = qw;
-    if (j == 0) dxs[bl] = h2f(dh);
-    if (emit && a.xq_out) {
-        *(uint32_t*)(a.xq_out + bl * 32 + 4 * j) = qw;
-        if (j == 0) a.xd_out[bl] = dh;
-    }
-}
-
+// Q8_0 of the loaded values (two lanes per block) into the wave's LDS slot;
+// the matrix's first workgroup also writes Q8_0(x) out when asked.
 template <bool XF>
-__device__ __forceinline__ void grp_x_finish(const lgx_gemv_mat& a, int8_t* xs, float* dxs,
-                                             bool emit, const uint4 (&xr)[GRP_XB]) {
-    const int nb = a.k >> 5, np = a.k >> 6, tid = threadIdx.x, nt = blockDim.x;
+__device__ __forceinline__ void grp_x_stage(const lgx_gemv_mat& a, const RangeInfo& ri, int lane,
+                                            const uint4 (&xr)[4], uint32_t xdr, int8_t* xsw,
+                                            float* dxw, bool emit) {
+    const int bl = lane >> 1, h = lane & 1;
+    uint32_t q[4];
+    float dxv;
+    uint16_t dh = 0;
     if constexpr (XF) {
+        float f[16];
 #pragma unroll
-        for (int u = 0; u < GRP_XB; ++u) {
-            const int sl = tid + u * nt;
-            if (sl < nb * 8) grp_quant_slot(a, sl, xr[u], xs, dxs, emit);   // whole groups
+        for (int u = 0; u < 4; ++u) {
+            f[4 * u + 0] = __uint_as_float(xr[u].x);
+            f[4 * u + 1] = __uint_as_float(xr[u].y);
+            f[4 * u + 2] = __uint_as_float(xr[u].z);
+            f[4 * u + 3] = __uint_as_float(xr[u].w);
         }
-#pragma unroll 1
-        for (int sl = tid + GRP_XB * nt; sl < nb * 8; sl += nt)
-            grp_quant_slot(a, sl, *(const uint4*)(a.xf + (sl >> 3) * 32 + 4 * (sl & 7)), xs, dxs,
-                           emit);
+        float am = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) am = fmaxf(am, fabsf(f[e]));
+        am = fmaxf(am, shfl_xor_f(am, 1));
+        const float d = am / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            uint32_t qw = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float v = roundf(f[4 * u + e] * id);
+                v = fminf(fmaxf(v, -127.0f), 127.0f);
+                qw |= ((uint32_t)(int32_t)v & 0xffu) << (8 * e);
+            }
+            q[u] = qw;
+        }
+        dh = f2h(d);
+        dxv = h2f(dh);
     } else {
-        if (tid < 4 * np) *(uint4*)(xs + tid * 16) = xr[0];
-        if (tid < nb) dxs[tid] = h2f(xr[1].x);
-        for (int s2 = tid + nt; s2 < 4 * np; s2 += nt) {
-            const int8_t* src = a.xq + (s2 >> 2) * 64 + 8 * (s2 & 3);
-            const uint2 lo = *(const uint2*)src;
-            const uint2 hi = *(const uint2*)(src + 32);
-            *(uint4*)(xs + s2 * 16) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        q[0] = xr[0].x;
+        q[1] = xr[0].y;
+        q[2] = xr[0].z;
+        q[3] = xr[0].w;
+        dxv = h2f(xdr);
+    }
+    if (bl < ri.nbr) {
+        // chunks 2h and 2h + 1 of block bl: 8 bytes each in slot (pair, chunk)
+        int8_t* base = xsw + ((bl >> 1) * 4 + 2 * h) * 16 + (bl & 1) * 8;
+        *(uint2*)base = make_uint2(q[0], q[1]);
+        *(uint2*)(base + 16) = make_uint2(q[2], q[3]);
+        if (h == 0) dxw[bl] = dxv;
+        if constexpr (XF) {
+            if (emit && a.xq_out) {
+                *(uint4*)(a.xq_out + (int64_t)(ri.b0 + bl) * 32 + 16 * h) =
+                    make_uint4(q[0], q[1], q[2], q[3]);
+                if (h == 0) a.xd_out[ri.b0 + bl] = dh;
+            }
         }
-        for (int b = tid + nt; b < nb; b += nt) dxs[b] = h2f(a.xd[b]);
     }
 }
 
-// One wave's range: loads (issued by grp_issue) -> MFMA -> canonical chain.
-// Scales first, then the 16 weight units (clamped to the range's last pair),
-// so unit i's math waits only for the loads issued up to it.
-__device__ __forceinline__ void grp_issue(const lgx_gemv_mat& a, int t, const RangeInfo& ri,
-                                          int lane, uint4 (&w)[16], uint32_t (&dw)[16],
-                                          bool idle = false) {
-    const int np = a.k >> 6, nh = s16_nhalf(a.k), r = lane & 15;
-    uint32_t d0[8], d1[8];
-    load_scales_half(a.wd, t, 2 * ri.g, nh, r, d0);
-    load_scales_half(a.wd, t, min(2 * ri.g + 1, nh - 1), nh, r, d1);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        dw[i] = d0[i];
-        dw[8 + i] = d1[i];
-    }
-    __builtin_amdgcn_sched_barrier(0);            // issue order: scales, then weights
-    const uint4* wp = (const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64 + lane;
-    const int last = idle ? 0 : ri.npairs - 1;    // an idle wave re-reads one unit
-#pragma unroll
-    for (int i = 0; i < 16; ++i) w[i] = ld_stream(wp + min(i, last) * 64);
-    __builtin_amdgcn_sched_barrier(0);
-}
-
+// One wave's range: activation and scale loads, the first GRP_WIN weight
+// units, the activation staging, then per unit: the load GRP_WIN units
+// ahead, two MFMAs, the canonical chain step.
+template <bool XF>
 __device__ __forceinline__ float grp_range(const lgx_gemv_mat& a, int t, const RangeInfo& ri,
-                                           int lane, const int8_t* xs, const float* dxs,
-                                           const uint4 (&w)[16], const uint32_t (&dw)[16]) {
-    const int r = lane & 15, c = lane >> 4, nb = a.k >> 5;
+                                           int lane, int8_t* xsw, float* dxw, bool emit) {
+    const int np = a.k >> 6, nh = s16_nhalf(a.k);
+    const int r = lane & 15, c = lane >> 4;
+    uint4 xr[4];
+    uint32_t xdr;
+    grp_x_load<XF>(a, ri, lane, xr, xdr);
+    uint32_t dw[16];
+    {
+        uint32_t d0[8], d1[8];
+        load_scales_half(a.wd, t, 2 * ri.g, nh, r, d0);
+        load_scales_half(a.wd, t, min(2 * ri.g + 1, nh - 1), nh, r, d1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            dw[i] = d0[i];
+            dw[8 + i] = d1[i];
+        }
+    }
+    const uint4* wp = (const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64 + lane;
+    const int last = ri.npairs - 1;
+    uint4 w[16];
+#pragma unroll
+    for (int i = 0; i < GRP_WIN; ++i) w[i] = ld_stream(wp + min(i, last) * 64);
+    __builtin_amdgcn_sched_barrier(0);            // issue order: activation, scales, weights
+    grp_x_stage<XF>(a, ri, lane, xr, xdr, xsw, dxw, emit);
     const v4i zero = {0, 0, 0, 0};
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         if (i < ri.npairs) {                       // wave-uniform
-            const int p = ri.p0 + i;
-            const uint4 xv = *(const uint4*)(xs + (p * 4 + c) * 16);
+            if (i + GRP_WIN < 16) w[i + GRP_WIN] = ld_stream(wp + min(i + GRP_WIN, last) * 64);
+            const uint4 xv = *(const uint4*)(xsw + (i * 4 + c) * 16);
             const long a0 = (long)(((uint64_t)xv.y << 32) | xv.x);
             const long a1 = (long)(((uint64_t)xv.w << 32) | xv.z);
             const long b0 = (long)(((uint64_t)w[i].y << 32) | w[i].x);
             const long b1 = (long)(((uint64_t)w[i].w << 32) | w[i].z);
             const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, zero, 0, 0, 0);
             const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, zero, 0, 0, 0);
-            const float e0 = h2f(dw[i] & 0xffffu) * dxs[2 * p];
-            const float e1 = h2f(dw[i] >> 16) * dxs[2 * p + 1];
+            const float e0 = h2f(dw[i] & 0xffffu) * dxw[2 * i];
+            const float e1 = h2f(dw[i] >> 16) * dxw[2 * i + 1];
             acc = fmaf((float)d0[0], e0, acc);
             acc = fmaf((float)d1[0], e1, acc);
-            if (a.dbg && c == 0) {
-                a.dbg[(int64_t)(t * 16 + r) * nb + 2 * p] = d0[0];
-                a.dbg[(int64_t)(t * 16 + r) * nb + 2 * p + 1] = d1[0];
-            }
         }
         // unit i's MFMAs stay after unit i-1's chain step: one unit live at a
-        // time, each waiting only for its own weights
+        // time, each waiting only for its own weights (no stores in this
+        // loop: a store would share the load counter and make the waits
+        // conservative; the block-dot debug output is the dot4 kernel's)
         __builtin_amdgcn_sched_barrier(0);
     }
     return acc;
@@ -823,42 +838,23 @@ __device__ __forceinline__ void q8_gemv_grp_body(const lgx_gemv_group_args& ga) 
     const lgx_gemv_mat& a = ga.mat[g];
     const int k = a.k, nb = k >> 5;
     const int nr = (nb + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS;
-    const int nrs = min(nr, W), tpw = W / nrs;
+    const int nrs = min(nr, W);
+    const int tpw = a.pad > 0 ? a.pad : W / nrs;
     const int ntiles = a.n >> 4;
     const int tile_base = (bx - ga.tile0[g]) * tpw;
-    int8_t* xs = (int8_t*)lds_dyn;                 // k bytes, (pair, chunk) order
-    float* dxs = (float*)(lds_dyn + k);            // nb
-    float* ps = dxs + nb;                          // [tpw][nr][16]
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    int8_t* xsw = (int8_t*)lds_dyn + wave * GRP_XSLOT;   // this wave's activation slot
+    float* dxw = (float*)(xsw + 1024);
+    float* ps = (float*)(lds_dyn + W * GRP_XSLOT);        // [tpw][nr][16]
     const int ts = wave / nrs, rg = wave - ts * nrs;
     const int t = tile_base + ts;
     const bool on = ts < tpw && t < ntiles;
-
-    uint4 w[16];
-    uint32_t dw[16];
-    uint4 xr[GRP_XB];
-    const RangeInfo ri = range_info(rg, k);
-    grp_x_issue<XF>(a, xr);
-    __builtin_amdgcn_sched_barrier(0);            // activation loads first
-    // every wave issues its loads (an idle wave re-reads one unit of the
-    // first tile, a cache hit), so no branch hides them from the wait counts
-    grp_issue(a, on ? t : min(tile_base, ntiles - 1), ri, lane, w, dw, !on);
-    grp_x_finish<XF>(a, xs, dxs, bx == ga.tile0[g], xr);
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
+    const bool emit = bx == ga.tile0[g] && ts == 0;       // one wave per range writes Q8_0(x)
     if (on) {
-        float acc = grp_range(a, t, ri, lane, xs, dxs, w, dw);
-        if (lane < 16) {
-            if (a.part_out)
-                a.y[(int64_t)rg * a.n + t * 16 + lane] = acc;
-            else
-                ps[(ts * nr + rg) * 16 + lane] = acc;
-        }
 #pragma unroll 1
-        for (int rg2 = rg + W; rg2 < nr; rg2 += W) {   // rows of more than W ranges
-            const RangeInfo r2 = range_info(rg2, k);
-            grp_issue(a, t, r2, lane, w, dw);
-            acc = grp_range(a, t, r2, lane, xs, dxs, w, dw);
+        for (int rg2 = rg; rg2 < nr; rg2 += W) {           // rows of more than W ranges
+            const RangeInfo ri = range_info(rg2, k);
+            const float acc = grp_range<XF>(a, t, ri, lane, xsw, dxw, emit);
             if (lane < 16) {
                 if (a.part_out)
                     a.y[(int64_t)rg2 * a.n + t * 16 + lane] = acc;

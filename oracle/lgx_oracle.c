@@ -14,6 +14,8 @@
  */
 #include "lgx_oracle.h"
 
+#include <omp.h>
+
 #include <math.h>
 #ifdef __AVX2__
 #include <immintrin.h>
@@ -1038,6 +1040,10 @@ void orc_model_load_kv(orc_model* m, int32_t layer, int32_t kv, int32_t b, int32
 }
 
 void orc_model_set_seq_len(orc_model* m, int32_t slot, int32_t len) { m->seq_len[slot] = len; }
+
+/* OpenMP threads of later oracle calls (the CPU baseline times 1 and all). */
+void orc_set_threads(int32_t n) { omp_set_num_threads(n > 0 ? n : 1); }
+int32_t orc_max_threads(void) { return omp_get_max_threads(); }
 
 /* Token choice of later steps and prefills: temperature 0 = greedy; else
  * orc_sample_row with stream = slot and draw index = the consumed position. */

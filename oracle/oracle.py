@@ -86,6 +86,8 @@ def lib():
             "orc_model_load_kv": (None, [_P, _I32, _I32, _I32, _I32, _P]),
             "orc_model_set_seq_len": (None, [_P, _I32, _I32]),
             "orc_model_set_sampling": (None, [_P, C.c_float, _I32, C.c_float, C.c_uint64]),
+            "orc_set_threads": (None, [_I32]),
+            "orc_max_threads": (_I32, []),
             "orc_sample": (None, [_P, _I32, _I32, _I32, C.c_float, C.c_float, C.c_uint64, _P,
                                   _P, _P]),
         }
@@ -350,6 +352,15 @@ def lm_head_f16(x, E):
     out = np.empty((m, V), np.float32)
     lib().orc_lm_head_f16(_ptr(x), m, _ptr(E), V, h, _ptr(out))
     return out
+
+
+def set_threads(n: int) -> None:
+    """OpenMP threads of later oracle calls."""
+    lib().orc_set_threads(n)
+
+
+def max_threads() -> int:
+    return int(lib().orc_max_threads())
 
 
 def sample(logits, top_k: int, top_p: float, temperature: float, seed: int, streams, pos):
