@@ -65,7 +65,7 @@ typedef enum lgx_status {
     LGX_INVALID_ARGUMENT = 2,   /* LogosStatus::RefinementViolation: a contract on an argument */
     LGX_NULL_POINTER = 3,
     LGX_OUT_OF_BOUNDS = 4,
-    LGX_MODULE_LOAD_FAILED = 5, /* LogosStatus::DeserializationFailed: the code object */
+    LGX_MODULE_LOAD_FAILED = 5, /* LogosStatus::DeserializationFailed: the code object or a weight file */
     LGX_INVALID_HANDLE = 6,
     LGX_INTERNAL_PANIC = 8,     /* LogosStatus::ThreadPanic: a C++ exception caught at the ABI */
     LGX_OUT_OF_MEMORY = 9,      /* LogosStatus::MemoryExhausted */
@@ -316,16 +316,45 @@ enum {
     LGX_T_V_PAGES = 13,
     LGX_T_PAGE_TABLE = 14,/* int32 [max_batch][maxp], a seeded permutation */
     LGX_T_SEQ_LEN = 15,   /* int32 [max_batch] */
-    LGX_T_HIDDEN = 16     /* binary32 [max_batch][hidden]: last final-norm output */
+    LGX_T_HIDDEN = 16,    /* binary32 [max_batch][hidden]: last final-norm output */
+    LGX_T_ATTN_NORM = 17, /* binary32 [hidden] RMSNorm weight before attention */
+    LGX_T_FFN_NORM = 18,  /* binary32 [hidden] RMSNorm weight before the MLP */
+    LGX_T_OUT_NORM = 19   /* binary32 [hidden] final RMSNorm weight */
 };
 
 /* Generates every tensor from SplitMix64 streams of `seed` (quants uniform on
  * [-127, 127], scales |N(0, 0.02)|/127, qkv bias N(0, 0.02), embedding
  * N(0, emb_sigma), norm weights 1) and allocates the paged KV cache for
- * max_batch sequences of max_seq tokens.  Synchronous. */
+ * max_batch sequences of max_seq tokens.  Synchronous.  A model holds its
+ * RMSNorm weights per layer (1 here; a checkpoint's own values when loaded). */
 lgx_status lgx_model_create(lgx_ctx* ctx, const lgx_qwen_config* cfg, uint64_t seed,
                             lgx_model** out);
 lgx_status lgx_model_destroy(lgx_model* m);
+/* ---- Q8_0 checkpoints (GGUF) ----
+ * A Qwen2 model file in the GGUF container (versions 2 and 3, the llama.cpp
+ * format): metadata general.architecture = "qwen2", qwen2.block_count,
+ * .embedding_length, .feed_forward_length, .attention.head_count,
+ * .attention.head_count_kv (optional: .attention.key_length,
+ * .attention.layer_norm_rms_epsilon, .rope.freq_base); tensors
+ * token_embd.weight (F16), output_norm.weight (F32), output.weight (Q8_0;
+ * absent = tied embedding), and per layer N blk.N.attn_norm / ffn_norm
+ * (F32), attn_q / attn_k / attn_v / attn_output / ffn_gate / ffn_up /
+ * ffn_down .weight (Q8_0: blocks of a binary16 scale + 32 int8) and
+ * attn_q / attn_k / attn_v .bias (F32).  The query/key rows are taken in
+ * the file's (Hugging Face rotate-half) order.  No counterpart in the
+ * reference, which has no model format.
+ * lgx_gguf_config parses the file on the host (no device) and returns the
+ * model shape with max_batch / max_seq filled in; lgx_model_load_gguf builds
+ * the model from the file (synchronous; the file is read tensor by tensor).
+ * A file that is not GGUF or is truncated gives LGX_MODULE_LOAD_FAILED, a
+ * missing or misshapen tensor LGX_INVALID_ARGUMENT, another tensor type or
+ * architecture LGX_UNSUPPORTED. */
+lgx_status lgx_gguf_config(const char* path, int32_t max_batch, int32_t max_seq,
+                           lgx_qwen_config* out);
+lgx_status lgx_model_load_gguf(lgx_ctx* ctx, const char* path, int32_t max_batch,
+                               int32_t max_seq, lgx_model** out);
+/* The configuration a model was built with. */
+lgx_status lgx_model_config(const lgx_model* m, lgx_qwen_config* out);
 /* seq_len[:] = 0 (the KV cache is overwritten as sequences grow again). */
 lgx_status lgx_model_reset(lgx_model* m, void* stream);
 /* One greedy decode step for sequences 0..B-1: tokens[b] (device int32) is

@@ -82,6 +82,9 @@ SIGNATURES = {
                              _P]),
     "lgx_model_set_sampling": (C.c_int, [_P, C.c_float, _I32, C.c_float, C.c_uint64]),
     "lgx_model_create": (C.c_int, [_P, _P, C.c_uint64, C.POINTER(_P)]),
+    "lgx_gguf_config": (C.c_int, [C.c_char_p, _I32, _I32, _P]),
+    "lgx_model_load_gguf": (C.c_int, [_P, C.c_char_p, _I32, _I32, C.POINTER(_P)]),
+    "lgx_model_config": (C.c_int, [_P, _P]),
     "lgx_model_destroy": (C.c_int, [_P]),
     "lgx_model_reset": (C.c_int, [_P, _P]),
     "lgx_qwen_decode_step": (C.c_int, [_P, _I32, _P, _P]),
@@ -167,7 +170,8 @@ def prefill_valu_ops(cfg: dict, B: int, P: int) -> float:
 # Tensor ids of lgx_model_tensor.
 MODEL_TENSORS = {"emb": 0, "lm_q": 1, "lm_d": 2, "qkv_q": 3, "qkv_d": 4, "o_q": 5, "o_d": 6,
                  "gu_q": 7, "gu_d": 8, "dn_q": 9, "dn_d": 10, "bias": 11, "k_pages": 12,
-                 "v_pages": 13, "page_table": 14, "seq_len": 15, "hidden": 16}
+                 "v_pages": 13, "page_table": 14, "seq_len": 15, "hidden": 16,
+                 "attn_norm": 17, "ffn_norm": 18, "out_norm": 19}
 
 
 class LgxError(RuntimeError):
@@ -569,17 +573,29 @@ class Model:
     ``cfg`` uses the oracle's keys (n_layers, hidden, inter, n_heads, n_kv,
     head_dim, vocab, tied, max_batch, max_seq, eps, theta, emb_sigma)."""
 
-    def __init__(self, ctx: Context, cfg: dict, seed: int):
+    def __init__(self, ctx: Context, cfg: dict, seed: int, _handle=None):
         self.ctx = ctx
         self.cfg = dict(cfg)
         self.c = QwenConfigC(cfg["n_layers"], cfg["hidden"], cfg["inter"], cfg["n_heads"],
                              cfg["n_kv"], cfg["head_dim"], cfg["vocab"], cfg["tied"],
                              cfg["max_batch"], cfg["max_seq"], cfg["eps"], cfg["theta"],
                              cfg["emb_sigma"])
-        h = C.c_void_p()
-        _check(lib().lgx_model_create(ctx.handle, C.byref(self.c), seed, C.byref(h)))
-        self.handle = h
+        if _handle is None:
+            h = C.c_void_p()
+            _check(lib().lgx_model_create(ctx.handle, C.byref(self.c), seed, C.byref(h)))
+            _handle = h
+        self.handle = _handle
         ctx._models.add(self)
+
+    @classmethod
+    def load_gguf(cls, ctx: Context, path: str, max_batch: int, max_seq: int) -> "Model":
+        """lgx_model_load_gguf: the model of a Qwen2 Q8_0 GGUF file."""
+        h = C.c_void_p()
+        _check(lib().lgx_model_load_gguf(ctx.handle, path.encode(), max_batch, max_seq,
+                                         C.byref(h)))
+        c = QwenConfigC()
+        _check(lib().lgx_model_config(h, C.byref(c)))
+        return cls(ctx, _cfg_dict(c), 0, _handle=h)
 
     def close(self) -> None:
         if self.handle:
@@ -672,6 +688,20 @@ class Model:
                                      C.c_void_p(p + int(page_table[b, i]) * page_bytes),
                                      C.c_size_t(page_bytes), 2))
         return np.ascontiguousarray(buf.transpose(0, 2, 1, 3).reshape(npg * 16, hkv, d)[:n])
+
+
+def _cfg_dict(c) -> dict:
+    return dict(n_layers=c.n_layers, hidden=c.hidden, inter=c.intermediate, n_heads=c.n_heads,
+                n_kv=c.n_kv_heads, head_dim=c.head_dim, vocab=c.vocab, tied=c.tied_embedding,
+                max_batch=c.max_batch, max_seq=c.max_seq, eps=c.rms_eps, theta=c.rope_theta,
+                emb_sigma=c.emb_sigma)
+
+
+def gguf_config(path: str, max_batch: int, max_seq: int) -> dict:
+    """lgx_gguf_config: the model shape of a Qwen2 GGUF file (host only)."""
+    c = QwenConfigC()
+    _check(lib().lgx_gguf_config(path.encode(), max_batch, max_seq, C.byref(c)))
+    return _cfg_dict(c)
 
 
 def _check_hip(err: int) -> None:

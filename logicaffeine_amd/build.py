@@ -48,7 +48,7 @@ def build_kernels() -> str:
     return HSACO
 
 
-HOST_SOURCES = ["lgx_host.cpp", "lgx_glue.cpp", "lgx_model.cpp", "lgx_gen.cpp"]
+HOST_SOURCES = ["lgx_host.cpp", "lgx_glue.cpp", "lgx_model.cpp", "lgx_gen.cpp", "lgx_gguf.cpp"]
 BUILD_DIR = os.path.join(HERE, "_build")
 
 

@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "lgx_gen.h"
+#include "lgx_gguf.h"
 #include "lgx_internal.h"
 
 using namespace lgxi;
@@ -45,11 +46,12 @@ struct lgx_model {
     std::vector<DevQ8> qkv, o, gu, dn;
     DevQ8 lm;
     std::vector<float*> bias;
+    std::vector<float*> attn_norm, ffn_norm;   // RMSNorm weights per layer
+    float* out_norm = nullptr;                 // final RMSNorm weight
     std::vector<uint16_t*> kc, vc;
     uint16_t* emb = nullptr;
     uint16_t* emb_t64 = nullptr;   // tied lm_head: the embedding in T64 order
     float* xt = nullptr;           // tied lm_head: final-norm rows in T16 column order
-    float* ones = nullptr;
     float *cos_t = nullptr, *sin_t = nullptr;
     int32_t* page_table = nullptr;
     int32_t* seq_len = nullptr;
@@ -116,17 +118,99 @@ lgx_status dev_alloc(lgx_model* m, T** p, size_t count) {
     return LGX_OK;
 }
 
-// Generate a Q8_0 matrix on the host (streams s, s+1), upload it row-major
-// into the staging buffers and repack into the device tile layouts.
-lgx_status make_q8(lgx_model* m, uint64_t stream, int32_t n, int32_t k, DevQ8* out,
-                   int8_t* stage_q, uint16_t* stage_d, std::vector<int8_t>& hq,
+// Where a model's tensors come from: the seeded generator or a checkpoint
+// file.  Q8_0 matrices are row-major quants [n][k] + scales [n][k/32].
+enum { W_QKV, W_O, W_GU, W_DN, W_LM };
+enum { V_BIAS, V_ATTN_NORM, V_FFN_NORM, V_OUT_NORM };
+struct Source {
+    virtual ~Source() = default;
+    virtual lgx_status q8(int which, int layer, int32_t n, int32_t k, int8_t* qs, uint16_t* d) = 0;
+    virtual lgx_status vec(int which, int layer, int32_t n, float* out) = 0;
+    virtual lgx_status emb(int32_t V, int32_t H, uint16_t* out) = 0;
+};
+
+// The random-init model: SplitMix64 streams 1000 + 16 layer + {0,1: Wqkv;
+// 2,3: Wo; 4,5: Wgate|up; 6,7: Wdown; 8: qkv bias}, 1 embedding, 2/3 the
+// untied lm_head; norm weights 1.
+struct GenSource : Source {
+    uint64_t seed;
+    double emb_sigma;
+    GenSource(uint64_t s, double sig) : seed(s), emb_sigma(sig) {}
+    lgx_status q8(int which, int layer, int32_t n, int32_t k, int8_t* qs, uint16_t* d) override {
+        const uint64_t stream = which == W_LM ? 2 : 1000 + 16 * (uint64_t)layer + 2 * which;
+        lgxg::gen_i8(seed, stream, qs, (int64_t)n * k);
+        lgxg::gen_q8_scales(seed, stream + 1, d, (int64_t)n * (k / 32));
+        return LGX_OK;
+    }
+    lgx_status vec(int which, int layer, int32_t n, float* out) override {
+        if (which == V_BIAS)
+            lgxg::gen_normal_f32(seed, 1000 + 16 * (uint64_t)layer + 8, 0.02, out, n);
+        else
+            std::fill(out, out + n, 1.0f);
+        return LGX_OK;
+    }
+    lgx_status emb(int32_t V, int32_t H, uint16_t* out) override {
+        lgxg::gen_normal_f16(seed, 1, emb_sigma, out, (int64_t)V * H);
+        return LGX_OK;
+    }
+};
+
+// A Qwen2 GGUF file: the fused QKV rows are attn_q | attn_k | attn_v, the
+// fused gate|up rows ffn_gate | ffn_up.
+struct GgufSource : Source {
+    const lgxf::Gguf& g;
+    lgx_qwen_config c;
+    GgufSource(const lgxf::Gguf& gg, const lgx_qwen_config& cf) : g(gg), c(cf) {}
+    static std::string blk(int l, const char* t) { return "blk." + std::to_string(l) + "." + t; }
+    lgx_status q8(int which, int layer, int32_t n, int32_t k, int8_t* qs, uint16_t* d) override {
+        const int qd = c.n_heads * c.head_dim, kd = c.n_kv_heads * c.head_dim;
+        lgx_status st;
+        switch (which) {
+            case W_QKV:
+                if ((st = g.read_q8(blk(layer, "attn_q.weight"), qd, k, qs, d)) ||
+                    (st = g.read_q8(blk(layer, "attn_k.weight"), kd, k, qs + (int64_t)qd * k,
+                                    d + (int64_t)qd * (k / 32))))
+                    return st;
+                return g.read_q8(blk(layer, "attn_v.weight"), kd, k, qs + (int64_t)(qd + kd) * k,
+                                 d + (int64_t)(qd + kd) * (k / 32));
+            case W_O: return g.read_q8(blk(layer, "attn_output.weight"), n, k, qs, d);
+            case W_GU:
+                if ((st = g.read_q8(blk(layer, "ffn_gate.weight"), n / 2, k, qs, d))) return st;
+                return g.read_q8(blk(layer, "ffn_up.weight"), n / 2, k, qs + (int64_t)(n / 2) * k,
+                                 d + (int64_t)(n / 2) * (k / 32));
+            case W_DN: return g.read_q8(blk(layer, "ffn_down.weight"), n, k, qs, d);
+            default: return g.read_q8("output.weight", n, k, qs, d);
+        }
+    }
+    lgx_status vec(int which, int layer, int32_t n, float* out) override {
+        using lgxf::GGML_F32;
+        if (which == V_BIAS) {
+            const int qd = c.n_heads * c.head_dim, kd = c.n_kv_heads * c.head_dim;
+            lgx_status st;
+            if ((st = g.read_raw(blk(layer, "attn_q.bias"), GGML_F32, 1, qd, out)) ||
+                (st = g.read_raw(blk(layer, "attn_k.bias"), GGML_F32, 1, kd, out + qd)))
+                return st;
+            return g.read_raw(blk(layer, "attn_v.bias"), GGML_F32, 1, kd, out + qd + kd);
+        }
+        if (which == V_OUT_NORM) return g.read_raw("output_norm.weight", GGML_F32, 1, n, out);
+        return g.read_raw(blk(layer, which == V_ATTN_NORM ? "attn_norm.weight" : "ffn_norm.weight"),
+                          GGML_F32, 1, n, out);
+    }
+    lgx_status emb(int32_t V, int32_t H, uint16_t* out) override {
+        return g.read_raw("token_embd.weight", lgxf::GGML_F16, V, H, out);
+    }
+};
+
+// Take a Q8_0 matrix from the source, upload it row-major into the staging
+// buffers and repack into the device tile layouts.
+lgx_status make_q8(lgx_model* m, Source& src, int which, int layer, int32_t n, int32_t k,
+                   DevQ8* out, int8_t* stage_q, uint16_t* stage_d, std::vector<int8_t>& hq,
                    std::vector<uint16_t>& hd) {
     const int64_t nq = (int64_t)n * k, nd = (int64_t)n * (k / 32);
     hq.resize(nq);
     hd.resize(nd);
-    lgxg::gen_i8(m->seed, stream, hq.data(), nq);
-    lgxg::gen_q8_scales(m->seed, stream + 1, hd.data(), nd);
-    lgx_status st;
+    lgx_status st = src.q8(which, layer, n, k, hq.data(), hd.data());
+    if (st != LGX_OK) return st;
     if ((st = dev_alloc(m, &out->qs, (size_t)nq)) != LGX_OK) return st;
     if ((st = dev_alloc(m, &out->d, lgx_q8_scale_count(n, k))) != LGX_OK) return st;
     LGX_HIP(hipMemcpy(stage_q, hq.data(), nq, hipMemcpyHostToDevice));
@@ -192,14 +276,14 @@ lgx_status product(lgx_model* md, const DevQ8& W, int m, void* stream) {
                   stream, nullptr, nullptr, md->part);
 }
 
-lgx_status norm(lgx_model* md, int m, int n, int nr_part, bool with_part, float* xn, bool q8,
-                void* stream, float* xt = nullptr) {
+lgx_status norm(lgx_model* md, const float* w, int m, int n, int nr_part, bool with_part,
+                float* xn, bool q8, void* stream, float* xt = nullptr) {
     lgx_norm_args a{};
     a.xt = xt;
     a.part = with_part ? md->part : nullptr;
     a.nr = nr_part;
     a.h = md->h;
-    a.w = md->ones;
+    a.w = w;
     a.xn = xn;
     a.xq = q8 ? md->xq : nullptr;
     a.xd = q8 ? md->xd : nullptr;
@@ -222,7 +306,8 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
     if ((st = launch(c, K_EMBED, dim3(B), dim3(256), ea, stream)) != LGX_OK) return st;
     for (int l = 0; l < cf.n_layers; ++l) {
         // norm (+ residual of the previous layer's down product) -> Q8
-        if ((st = norm(md, B, H, parts(md, md->dn[0], B), l > 0, nullptr, true, stream)) != LGX_OK)
+        if ((st = norm(md, md->attn_norm[l], B, H, parts(md, md->dn[0], B), l > 0, nullptr, true,
+                       stream)) != LGX_OK)
             return st;
         if ((st = product(md, md->qkv[l], B, stream)) != LGX_OK) return st;
         lgx_qkv_args qa{};
@@ -271,7 +356,8 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
                          dim3(B * hq), dim3(d), aa, stream)) != LGX_OK)
             return st;
         if ((st = product(md, md->o[l], B, stream)) != LGX_OK) return st;
-        if ((st = norm(md, B, H, parts(md, md->o[l], B), true, nullptr, true, stream)) != LGX_OK)
+        if ((st = norm(md, md->ffn_norm[l], B, H, parts(md, md->o[l], B), true, nullptr, true,
+                       stream)) != LGX_OK)
             return st;
         if ((st = product(md, md->gu[l], B, stream)) != LGX_OK) return st;
         lgx_swiglu_args sw{md->part, parts(md, md->gu[l], B), md->xq, md->xd, nullptr, B, I,
@@ -291,7 +377,7 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
     const int H = cf.hidden;
     lgx_status st;
     const bool tied = cf.tied_embedding != 0;
-    if ((st = norm(md, B, H, parts(md, md->dn[0], B), true, md->xn, !tied, stream,
+    if ((st = norm(md, md->out_norm, B, H, parts(md, md->dn[0], B), true, md->xn, !tied, stream,
                    tied ? md->xt : nullptr)) != LGX_OK)
         return st;
     const float* lg;
@@ -355,12 +441,13 @@ lgx_status pf_product(lgx_model* md, const DevQ8& W, int M, void* stream) {
     return run_q8_tiled(md->ctx, &W.m, md->pf.xt, md->pf.xd, M, md->pf.part, stream);
 }
 
-lgx_status pf_norm(lgx_model* md, int M, int n, int nr, bool with_part, void* stream) {
+lgx_status pf_norm(lgx_model* md, const float* w, int M, int n, int nr, bool with_part,
+                   void* stream) {
     lgx_norm_args a{};
     a.part = with_part ? md->pf.part : nullptr;
     a.nr = nr;
     a.h = md->pf.h;
-    a.w = md->ones;
+    a.w = w;
     a.xq = md->pf.xt;
     a.xd = md->pf.xd;
     a.xq_t16 = 1;
@@ -387,7 +474,8 @@ lgx_status prefill_chunk(lgx_model* md, int B, int n, const int32_t* tokens, int
     lgx_embed_args ea{md->emb, tokens, pf.h, M, H, cf.vocab, stride, n};
     if ((st = launch(c, K_EMBED, dim3(M), dim3(256), ea, stream)) != LGX_OK) return st;
     for (int l = 0; l < cf.n_layers; ++l) {
-        if ((st = pf_norm(md, M, H, tiled_groups(I), l > 0, stream)) != LGX_OK) return st;
+        if ((st = pf_norm(md, md->attn_norm[l], M, H, tiled_groups(I), l > 0, stream)) != LGX_OK)
+            return st;
         if ((st = pf_product(md, md->qkv[l], M, stream)) != LGX_OK) return st;
         lgx_qkv_args qa{};
         qa.part = pf.part;
@@ -437,7 +525,8 @@ lgx_status prefill_chunk(lgx_model* md, int B, int n, const int32_t* tokens, int
                          dim3(M * hq), dim3(d), aa, stream)) != LGX_OK)
             return st;
         if ((st = pf_product(md, md->o[l], M, stream)) != LGX_OK) return st;
-        if ((st = pf_norm(md, M, H, tiled_groups(hq * d), true, stream)) != LGX_OK) return st;
+        if ((st = pf_norm(md, md->ffn_norm[l], M, H, tiled_groups(hq * d), true, stream)) != LGX_OK)
+            return st;
         if ((st = pf_product(md, md->gu[l], M, stream)) != LGX_OK) return st;
         lgx_swiglu_args sw{pf.part, tiled_groups(H), pf.xt, pf.xd, nullptr, M, I, 1};
         if ((st = launch(c, K_SWIGLU_QUANT, dim3(M, cdiv(I / 32, 32)), dim3(256), sw, stream)) != LGX_OK)
@@ -503,16 +592,14 @@ lgx_status step_graph(lgx_model* md, int B, int32_t* tokens, hipGraphExec_t* out
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-lgx_status lgx_model_create(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed,
-                            lgx_model** out) {
-    return guarded(__func__, [&]() -> lgx_status {
-        lgx_status st = enter(c);
-        if (st != LGX_OK) return st;
-        if (!cfg || !out) return fail(LGX_NULL_POINTER, "NULL config or out");
+// Allocate the model for *cfg and fill its tensors from src (ctx entered,
+// cfg checked).  `seed` also seeds the page-table permutation.
+lgx_status model_build(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed, Source& src,
+                       lgx_model** out) {
+        lgx_status st;
         *out = nullptr;
-        if ((st = check_config(cfg)) != LGX_OK) return st;
         auto* m = new lgx_model();
         m->ctx = c;
         m->counted = true;
@@ -551,16 +638,28 @@ lgx_status lgx_model_create(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t see
         m->vc.resize(L);
         const size_t kv_elems = (size_t)m->num_pages * hkv * LGX_PAGE * d;
         std::vector<float> hb(m->qkv_n);
+        m->attn_norm.resize(L);
+        m->ffn_norm.resize(L);
+        std::vector<float> hn(H);
+        // a host vector from the source into a new device buffer
+        auto put_vec = [&](int which, int l, int n, float** dst) -> lgx_status {
+            std::vector<float>& hv = which == V_BIAS ? hb : hn;
+            lgx_status s2 = src.vec(which, l, n, hv.data());
+            if (s2 != LGX_OK) return s2;
+            if ((s2 = dev_alloc(m, dst, n)) != LGX_OK) return s2;
+            LGX_HIP(hipMemcpy(*dst, hv.data(), (size_t)n * 4, hipMemcpyHostToDevice));
+            return LGX_OK;
+        };
         for (int l = 0; l < L; ++l) {
-            const uint64_t base = 1000 + 16 * (uint64_t)l;
-            if ((st = make_q8(m, base + 0, m->qkv_n, H, &m->qkv[l], stage_q, stage_d, hq8, hd16)) ||
-                (st = make_q8(m, base + 2, H, hq * d, &m->o[l], stage_q, stage_d, hq8, hd16)) ||
-                (st = make_q8(m, base + 4, 2 * I, H, &m->gu[l], stage_q, stage_d, hq8, hd16)) ||
-                (st = make_q8(m, base + 6, H, I, &m->dn[l], stage_q, stage_d, hq8, hd16)))
+            if ((st = make_q8(m, src, W_QKV, l, m->qkv_n, H, &m->qkv[l], stage_q, stage_d, hq8, hd16)) ||
+                (st = make_q8(m, src, W_O, l, H, hq * d, &m->o[l], stage_q, stage_d, hq8, hd16)) ||
+                (st = make_q8(m, src, W_GU, l, 2 * I, H, &m->gu[l], stage_q, stage_d, hq8, hd16)) ||
+                (st = make_q8(m, src, W_DN, l, H, I, &m->dn[l], stage_q, stage_d, hq8, hd16)))
                 return done(st);
-            lgxg::gen_normal_f32(seed, base + 8, 0.02, hb.data(), m->qkv_n);
-            if ((st = dev_alloc(m, &m->bias[l], m->qkv_n)) != LGX_OK) return done(st);
-            LGX_HIP(hipMemcpy(m->bias[l], hb.data(), m->qkv_n * 4, hipMemcpyHostToDevice));
+            if ((st = put_vec(V_BIAS, l, m->qkv_n, &m->bias[l])) ||
+                (st = put_vec(V_ATTN_NORM, l, H, &m->attn_norm[l])) ||
+                (st = put_vec(V_FFN_NORM, l, H, &m->ffn_norm[l])))
+                return done(st);
             if ((st = dev_alloc(m, &m->kc[l], kv_elems)) != LGX_OK ||
                 (st = dev_alloc(m, &m->vc[l], kv_elems)) != LGX_OK)
                 return done(st);
@@ -568,13 +667,14 @@ lgx_status lgx_model_create(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t see
             LGX_HIP(hipMemset(m->vc[l], 0, kv_elems * 2));
         }
         if (!cf.tied_embedding &&
-            (st = make_q8(m, 2, cf.vocab, H, &m->lm, stage_q, stage_d, hq8, hd16)) != LGX_OK)
+            (st = make_q8(m, src, W_LM, 0, cf.vocab, H, &m->lm, stage_q, stage_d, hq8, hd16)) != LGX_OK)
             return done(st);
+        if ((st = put_vec(V_OUT_NORM, 0, H, &m->out_norm)) != LGX_OK) return done(st);
         hq8.clear();
         hq8.shrink_to_fit();
         {
             std::vector<uint16_t> he((size_t)cf.vocab * H);
-            lgxg::gen_normal_f16(seed, 1, cf.emb_sigma, he.data(), (int64_t)he.size());
+            if ((st = src.emb(cf.vocab, H, he.data())) != LGX_OK) return done(st);
             if ((st = dev_alloc(m, &m->emb, he.size())) != LGX_OK) return done(st);
             LGX_HIP(hipMemcpy(m->emb, he.data(), he.size() * 2, hipMemcpyHostToDevice));
         }
@@ -589,10 +689,6 @@ lgx_status lgx_model_create(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t see
                 return done(st);
         }
         {
-            const int mx = std::max(H, I);
-            std::vector<float> one(mx, 1.0f);
-            if ((st = dev_alloc(m, &m->ones, mx)) != LGX_OK) return done(st);
-            LGX_HIP(hipMemcpy(m->ones, one.data(), mx * 4, hipMemcpyHostToDevice));
             std::vector<float> ct((size_t)cf.max_seq * (d / 2)), stb(ct.size());
             for (int p = 0; p < cf.max_seq; ++p)
                 for (int i = 0; i < d / 2; ++i) {
@@ -640,6 +736,64 @@ lgx_status lgx_model_create(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t see
             m->allocs.erase(std::find(m->allocs.begin(), m->allocs.end(), p));
         }
         return done(LGX_OK);
+}
+
+}  // namespace
+
+extern "C" {
+
+lgx_status lgx_model_create(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed,
+                            lgx_model** out) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!cfg || !out) return fail(LGX_NULL_POINTER, "NULL config or out");
+        *out = nullptr;
+        if ((st = check_config(cfg)) != LGX_OK) return st;
+        GenSource src(seed, cfg->emb_sigma);
+        return model_build(c, cfg, seed, src, out);
+    });
+}
+
+lgx_status lgx_gguf_config(const char* path, int32_t max_batch, int32_t max_seq,
+                           lgx_qwen_config* out) {
+    return guarded(__func__, [&]() -> lgx_status {
+        g_has_error = false;
+        if (!path || !out) return fail(LGX_NULL_POINTER, "NULL path or out");
+        if (max_batch <= 0 || max_seq <= 0)
+            return fail(LGX_INVALID_ARGUMENT, "max_batch %d, max_seq %d", max_batch, max_seq);
+        lgxf::Gguf g;
+        lgx_status st = g.open(path);
+        if (st != LGX_OK) return st;
+        return g.config(max_batch, max_seq, out);
+    });
+}
+
+lgx_status lgx_model_load_gguf(lgx_ctx* c, const char* path, int32_t max_batch, int32_t max_seq,
+                               lgx_model** out) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!path || !out) return fail(LGX_NULL_POINTER, "NULL path or out");
+        *out = nullptr;
+        if (max_batch <= 0 || max_seq <= 0)
+            return fail(LGX_INVALID_ARGUMENT, "max_batch %d, max_seq %d", max_batch, max_seq);
+        lgxf::Gguf g;
+        if ((st = g.open(path)) != LGX_OK) return st;
+        lgx_qwen_config cfg{};
+        if ((st = g.config(max_batch, max_seq, &cfg)) != LGX_OK) return st;
+        if ((st = check_config(&cfg)) != LGX_OK) return st;
+        GgufSource src(g, cfg);
+        return model_build(c, &cfg, 0, src, out);
+    });
+}
+
+lgx_status lgx_model_config(const lgx_model* m, lgx_qwen_config* out) {
+    return guarded(__func__, [&]() -> lgx_status {
+        if (!valid_model(m)) return fail(LGX_INVALID_HANDLE, "invalid lgx_model handle");
+        if (!out) return fail(LGX_NULL_POINTER, "NULL out");
+        *out = m->c;
+        return LGX_OK;
     });
 }
 
@@ -821,6 +975,13 @@ lgx_status lgx_model_tensor(lgx_model* m, int32_t layer, int32_t which, const vo
             case LGX_T_HIDDEN:
                 *dev = m->xn;
                 *bytes = (size_t)cf.max_batch * cf.hidden * 4;
+                return LGX_OK;
+            case LGX_T_ATTN_NORM:
+            case LGX_T_FFN_NORM:
+            case LGX_T_OUT_NORM:
+                *dev = which == LGX_T_ATTN_NORM ? m->attn_norm[layer]
+                       : which == LGX_T_FFN_NORM ? m->ffn_norm[layer] : m->out_norm;
+                *bytes = (size_t)cf.hidden * 4;
                 return LGX_OK;
             default:
                 return fail(LGX_INVALID_ARGUMENT, "unknown tensor id %d", which);

@@ -707,6 +707,8 @@ struct orc_model {
     uint16_t **qkv_d, **o_d, **gu_d, **dn_d;
     float** bias;
     float* ones;
+    float **attn_norm, **ffn_norm;   /* RMSNorm weights per layer (1 unless set) */
+    float* out_norm;
     float *cos_t, *sin_t;
     uint16_t **kc, **vc;   /* per layer paged [max_batch*maxp][hkv][16][d] */
     int32_t* page_table;   /* identity: slot b page p -> b*maxp + p */
@@ -779,6 +781,16 @@ orc_model* orc_model_create(const orc_qwen_config* cfg, uint64_t seed) {
     int32_t mx = H > I ? H : I;
     m->ones = (float*)xmalloc(sizeof(float) * mx);
     for (int32_t i = 0; i < mx; ++i) m->ones[i] = 1.0f;
+    m->attn_norm = (float**)calloc(nl, sizeof(void*));
+    m->ffn_norm = (float**)calloc(nl, sizeof(void*));
+    for (int32_t l = 0; l < nl; ++l) {
+        m->attn_norm[l] = (float*)xmalloc(sizeof(float) * H);
+        m->ffn_norm[l] = (float*)xmalloc(sizeof(float) * H);
+        memcpy(m->attn_norm[l], m->ones, sizeof(float) * H);
+        memcpy(m->ffn_norm[l], m->ones, sizeof(float) * H);
+    }
+    m->out_norm = (float*)xmalloc(sizeof(float) * H);
+    memcpy(m->out_norm, m->ones, sizeof(float) * H);
     m->cos_t = (float*)xmalloc(sizeof(float) * (size_t)c->max_seq * (d / 2));
     m->sin_t = (float*)xmalloc(sizeof(float) * (size_t)c->max_seq * (d / 2));
     orc_rope_tables(c->max_seq, d, c->theta, m->cos_t, m->sin_t);
@@ -798,6 +810,8 @@ void orc_model_destroy(orc_model* m) {
     free(m->qkv_qs); free(m->o_qs); free(m->gu_qs); free(m->dn_qs);
     free(m->qkv_d); free(m->o_d); free(m->gu_d); free(m->dn_d);
     free(m->bias); free(m->kc); free(m->vc);
+    for (int32_t l = 0; l < m->c.n_layers; ++l) { free(m->attn_norm[l]); free(m->ffn_norm[l]); }
+    free(m->attn_norm); free(m->ffn_norm); free(m->out_norm);
     free(m->emb); free(m->lm_qs); free(m->lm_d); free(m->ones);
     free(m->cos_t); free(m->sin_t); free(m->page_table); free(m->seq_len);
     free(m);
@@ -869,7 +883,7 @@ void orc_model_step(orc_model* m, int32_t nseq, const int32_t* slots, const int3
         lens[i] = m->seq_len[slots[i]] + 1;
     }
     for (int32_t l = 0; l < c->n_layers; ++l) {
-        orc_rmsnorm(h, m->ones, B, H, c->eps, xn);
+        orc_rmsnorm(h, m->attn_norm[l], B, H, c->eps, xn);
         orc_quantize_q8_0(xn, B, H, xq, xd);
         orc_q8_gemm(m->qkv_qs[l], m->qkv_d[l], qn, H, xq, xd, B, qkv);
         for (int32_t i = 0; i < B; ++i) {
@@ -894,7 +908,7 @@ void orc_model_step(orc_model* m, int32_t nseq, const int32_t* slots, const int3
         orc_quantize_q8_0(att, B, hq * d, xq, xd);
         orc_q8_gemm(m->o_qs[l], m->o_d[l], H, hq * d, xq, xd, B, y);
         for (int64_t j = 0; j < (int64_t)B * H; ++j) h[j] = h[j] + y[j];
-        orc_rmsnorm(h, m->ones, B, H, c->eps, xn);
+        orc_rmsnorm(h, m->ffn_norm[l], B, H, c->eps, xn);
         orc_quantize_q8_0(xn, B, H, xq, xd);
         orc_q8_gemm(m->gu_qs[l], m->gu_d[l], 2 * I, H, xq, xd, B, y);
         orc_swiglu(y, B, I, a);
@@ -902,7 +916,7 @@ void orc_model_step(orc_model* m, int32_t nseq, const int32_t* slots, const int3
         orc_q8_gemm(m->dn_qs[l], m->dn_d[l], H, I, xq, xd, B, y);
         for (int64_t j = 0; j < (int64_t)B * H; ++j) h[j] = h[j] + y[j];
     }
-    orc_rmsnorm(h, m->ones, B, H, c->eps, xn);
+    orc_rmsnorm(h, m->out_norm, B, H, c->eps, xn);
     if (hidden_out) memcpy(hidden_out, xn, sizeof(float) * B * H);
     float* logits = (float*)xmalloc(sizeof(float) * (size_t)B * c->vocab);
     if (c->tied) {
@@ -962,7 +976,7 @@ void orc_model_prefill(orc_model* m, int32_t nseq, const int32_t* slots, int32_t
         lens[r] = m->seq_len[slots[s]] + j + 1;
     }
     for (int32_t l = 0; l < c->n_layers; ++l) {
-        orc_rmsnorm(h, m->ones, (int32_t)R, H, c->eps, xn);
+        orc_rmsnorm(h, m->attn_norm[l], (int32_t)R, H, c->eps, xn);
         orc_quantize_q8_0(xn, R, H, xq, xd);
         orc_q8_gemm(m->qkv_qs[l], m->qkv_d[l], qn, H, xq, xd, (int32_t)R, qkv);
 #pragma omp parallel for schedule(static)
@@ -988,7 +1002,7 @@ void orc_model_prefill(orc_model* m, int32_t nseq, const int32_t* slots, int32_t
         orc_quantize_q8_0(att, R, hq * d, xq, xd);
         orc_q8_gemm(m->o_qs[l], m->o_d[l], H, hq * d, xq, xd, (int32_t)R, y);
         for (int64_t j = 0; j < R * H; ++j) h[j] = h[j] + y[j];
-        orc_rmsnorm(h, m->ones, (int32_t)R, H, c->eps, xn);
+        orc_rmsnorm(h, m->ffn_norm[l], (int32_t)R, H, c->eps, xn);
         orc_quantize_q8_0(xn, R, H, xq, xd);
         orc_q8_gemm(m->gu_qs[l], m->gu_d[l], 2 * I, H, xq, xd, (int32_t)R, y);
         orc_swiglu(y, (int32_t)R, I, a);
@@ -1000,7 +1014,7 @@ void orc_model_prefill(orc_model* m, int32_t nseq, const int32_t* slots, int32_t
     float* hl = (float*)xmalloc(sizeof(float) * (size_t)nseq * H);
     for (int32_t s = 0; s < nseq; ++s)
         memcpy(hl + (int64_t)s * H, h + ((int64_t)s * P + P - 1) * H, sizeof(float) * H);
-    orc_rmsnorm(hl, m->ones, nseq, H, c->eps, xn);
+    orc_rmsnorm(hl, m->out_norm, nseq, H, c->eps, xn);
     if (hidden_out) memcpy(hidden_out, xn, sizeof(float) * nseq * H);
     float* logits = (float*)xmalloc(sizeof(float) * (size_t)nseq * c->vocab);
     if (c->tied) {
@@ -1053,4 +1067,34 @@ void orc_model_set_sampling(orc_model* m, float temperature, int32_t top_k, floa
     m->s_temp = temperature;
     m->s_top_p = top_p;
     m->s_seed = seed;
+}
+
+/* Replace a model tensor (ids of orc_model_tensor, plus 12 attention norm,
+ * 13 MLP norm, 14 final norm weight) with `data` of the same size: the
+ * tests load a checkpoint's tensors into the oracle this way. */
+void orc_model_set_tensor(orc_model* m, int32_t layer, int32_t which, const void* data) {
+    const orc_qwen_config* c = &m->c;
+    int64_t H = c->hidden, I = c->inter, d = c->head_dim, hq = c->n_heads, V = c->vocab;
+    int64_t qn = m->qkv_n;
+    void* dst = NULL;
+    size_t n = 0;
+    switch (which) {
+        case 0: dst = m->emb; n = (size_t)(V * H * 2); break;
+        case 1: dst = m->lm_qs; n = (size_t)(V * H); break;
+        case 2: dst = m->lm_d; n = (size_t)(V * (H / 32) * 2); break;
+        case 3: dst = m->qkv_qs[layer]; n = (size_t)(qn * H); break;
+        case 4: dst = m->qkv_d[layer]; n = (size_t)(qn * (H / 32) * 2); break;
+        case 5: dst = m->o_qs[layer]; n = (size_t)(H * hq * d); break;
+        case 6: dst = m->o_d[layer]; n = (size_t)(H * (hq * d / 32) * 2); break;
+        case 7: dst = m->gu_qs[layer]; n = (size_t)(2 * I * H); break;
+        case 8: dst = m->gu_d[layer]; n = (size_t)(2 * I * (H / 32) * 2); break;
+        case 9: dst = m->dn_qs[layer]; n = (size_t)(H * I); break;
+        case 10: dst = m->dn_d[layer]; n = (size_t)(H * (I / 32) * 2); break;
+        case 11: dst = m->bias[layer]; n = (size_t)(qn * 4); break;
+        case 12: dst = m->attn_norm[layer]; n = (size_t)(H * 4); break;
+        case 13: dst = m->ffn_norm[layer]; n = (size_t)(H * 4); break;
+        case 14: dst = m->out_norm; n = (size_t)(H * 4); break;
+        default: return;
+    }
+    if (dst) memcpy(dst, data, n);
 }

@@ -87,6 +87,7 @@ def lib():
             "orc_model_set_seq_len": (None, [_P, _I32, _I32]),
             "orc_model_set_sampling": (None, [_P, C.c_float, _I32, C.c_float, C.c_uint64]),
             "orc_set_threads": (None, [_I32]),
+            "orc_model_set_tensor": (None, [_P, _I32, _I32, _P]),
             "orc_max_threads": (_I32, []),
             "orc_sample": (None, [_P, _I32, _I32, _I32, C.c_float, C.c_float, C.c_uint64, _P,
                                   _P, _P]),
@@ -386,7 +387,8 @@ class QwenConfigC(C.Structure):
 
 
 TENSORS = {"emb": 0, "lm_q": 1, "lm_d": 2, "qkv_q": 3, "qkv_d": 4, "o_q": 5, "o_d": 6,
-           "gu_q": 7, "gu_d": 8, "dn_q": 9, "dn_d": 10, "bias": 11}
+           "gu_q": 7, "gu_d": 8, "dn_q": 9, "dn_d": 10, "bias": 11, "attn_norm": 12,
+           "ffn_norm": 13, "out_norm": 14}
 
 
 class Model:
@@ -422,6 +424,20 @@ class Model:
         ptr = lib().orc_model_tensor(self.h, layer, TENSORS[name])
         n = int(np.prod(shape)) * np.dtype(dt).itemsize
         return np.frombuffer(C.string_at(ptr, n), dtype=dt).reshape(shape).copy()
+
+    def set_tensor(self, name: str, layer: int, data) -> None:
+        """Replace a tensor (the shapes and dtypes of tensor()) -- e.g. a
+        checkpoint's weights."""
+        want = self.tensor(name, layer) if name in self._shaped() else None
+        arr = np.ascontiguousarray(data)
+        if want is not None:
+            assert arr.shape == want.shape and arr.dtype == want.dtype, (name, arr.shape, arr.dtype)
+        lib().orc_model_set_tensor(self.h, layer, TENSORS[name], arr.ctypes.data_as(C.c_void_p))
+
+    @staticmethod
+    def _shaped():
+        return ("emb", "lm_q", "lm_d", "qkv_q", "qkv_d", "o_q", "o_d", "gu_q", "gu_d", "dn_q",
+                "dn_d", "bias")
 
     def kv(self, layer: int, which: int, slot: int, n: int) -> np.ndarray:
         c = self.cfg

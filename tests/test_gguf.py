@@ -1,0 +1,80 @@
+"""The GGUF reader on the host (no GPU): the test writer against the byte
+layout the format fixes, the model shape lgx_gguf_config derives, and the
+errors of malformed files."""
+import struct
+
+import numpy as np
+import pytest
+
+import logicaffeine_amd as lgx
+from tests import gguf_util as gg
+
+
+def test_writer_byte_layout(tmp_path):
+    """A one-entry, one-tensor file byte for byte as the format lays it out."""
+    p = tmp_path / "min.gguf"
+    gg.write_gguf(p, [("a", gg.T_U32, 7)], [("t", gg.GGML_F32, np.array([1.5, -2.0], np.float32))])
+    b = p.read_bytes()
+    want = (b"GGUF" + struct.pack("<IQQ", 3, 1, 1) +
+            struct.pack("<Q", 1) + b"a" + struct.pack("<II", 4, 7) +
+            struct.pack("<Q", 1) + b"t" + struct.pack("<IQIQ", 1, 2, 0, 0))
+    assert b[:len(want)] == want
+    assert len(b) % 32 == 8 and b[-8:] == struct.pack("<ff", 1.5, -2.0)
+    # a Q8_0 row: the scale bits then the 32 quants, per block
+    qs = np.arange(64, dtype=np.int8).reshape(1, 64) - 30
+    d = np.array([[0x3C00, 0x8001]], np.uint16)
+    raw = gg.q8_rows(qs, d)
+    assert raw[:2] == b"\x00\x3c" and raw[34:36] == b"\x01\x80"
+    assert raw[2:34] == qs[0, :32].tobytes() and raw[36:] == qs[0, 32:].tobytes()
+
+
+def _tiny(tied=True):
+    from oracle import oracle as orc
+
+    return dict(orc.qwen_config("tiny" if tied else "tiny_untied"), eps=1e-5, theta=50000.0)
+
+
+@pytest.mark.parametrize("tied", [True, False])
+def test_config_from_file(tmp_path, tied):
+    cfg = _tiny(tied)
+    p = tmp_path / "m.gguf"
+    gg.write_gguf(p, gg.qwen2_meta(cfg, alignment=64),
+                  gg.qwen2_tensors(cfg, gg.random_qwen2(cfg, 1)), alignment=64)
+    got = lgx.gguf_config(str(p), 3, 99)
+    for key in ("n_layers", "hidden", "inter", "n_heads", "n_kv", "head_dim", "vocab", "tied"):
+        assert got[key] == cfg[key], key
+    assert got["max_batch"] == 3 and got["max_seq"] == 99
+    assert got["eps"] == np.float32(1e-5) and got["theta"] == 50000.0
+
+
+def _err(path, *args):
+    with pytest.raises(lgx.LgxError) as e:
+        lgx.gguf_config(str(path), *(args or (1, 16)))
+    return e.value.status_name
+
+
+def test_malformed_files(tmp_path):
+    cfg = _tiny()
+    t = gg.random_qwen2(cfg, 2)
+    meta = gg.qwen2_meta(cfg)
+    assert _err(tmp_path / "absent.gguf") == "LGX_MODULE_LOAD_FAILED"
+    p = tmp_path / "bad.gguf"
+    gg.write_gguf(p, meta, gg.qwen2_tensors(cfg, t), magic=b"GGUX")
+    assert _err(p) == "LGX_MODULE_LOAD_FAILED"
+    gg.write_gguf(p, meta, gg.qwen2_tensors(cfg, t), version=1)
+    assert _err(p) == "LGX_UNSUPPORTED"
+    gg.write_gguf(p, meta, gg.qwen2_tensors(cfg, t))
+    p.write_bytes(p.read_bytes()[:200])                      # cut inside the metadata
+    assert _err(p) == "LGX_MODULE_LOAD_FAILED"
+    llama = [("general.architecture", gg.T_STRING, "llama")] + meta[1:]
+    gg.write_gguf(p, llama, gg.qwen2_tensors(cfg, t))
+    assert _err(p) == "LGX_UNSUPPORTED"
+    no_layers = [m for m in meta if m[0] != "qwen2.block_count"]
+    gg.write_gguf(p, no_layers, gg.qwen2_tensors(cfg, t))
+    assert _err(p) == "LGX_INVALID_ARGUMENT"
+    tens = gg.qwen2_tensors(cfg, t)
+    tens[0] = ("token_embd.weight", gg.GGML_F32, np.zeros((cfg["vocab"], cfg["hidden"]), np.float32))
+    gg.write_gguf(p, meta, tens)
+    assert _err(p) == "LGX_UNSUPPORTED"
+    gg.write_gguf(p, meta, gg.qwen2_tensors(cfg, t))
+    assert _err(p, 0, 16) == "LGX_INVALID_ARGUMENT"
