@@ -72,7 +72,7 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
         c->gemv_whole = gv && std::string(gv) == "whole";
         c->gemv_wgs = env_int("LGX_GEMV_WGS", 0);
         c->gemm_mt = env_int("LGX_GEMM_MT", 0);
-        c->tiled_min = env_int("LGX_GEMM_TILED_MIN", 128);
+        c->tiled_min = env_int("LGX_GEMM_TILED_MIN", 33);
         c->tiled_rows = env_int("LGX_GEMM_TILED_ROWS", 0);
         c->tiled_grp = env_int("LGX_GEMM_TILED_GRP", 0);
         if (c->tiled_grp != 1 && c->tiled_grp != 2 && c->tiled_grp != 4) c->tiled_grp = 0;

@@ -188,7 +188,7 @@ struct lgx_ctx {
     int gemv_wgs = 0;             // LGX_GEMV_WGS: M = 1 GEMV waves per workgroup (0: auto)
     bool gemv_whole = false;      // LGX_GEMV=whole: block dots through LDS, chains after
     int gemm_mt = 0;              // LGX_GEMM_MT: force the M > 1 m-tile width (0: by m)
-    int tiled_min = 128;          // LGX_GEMM_TILED_MIN: smallest m through the tiled product
+    int tiled_min = 33;           // LGX_GEMM_TILED_MIN: smallest m through the tiled product
     int tiled_rows = 0;           // LGX_GEMM_TILED_ROWS: force 128/64/32 activation rows per workgroup
     int tiled_grp = 0;            // LGX_GEMM_TILED_GRP: force 1/2/4 ranges per group
     bool decode_streaming = false; // LGX_DECODE_GEMM=streaming: decode products of m >= 17

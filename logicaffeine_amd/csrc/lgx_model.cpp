@@ -272,8 +272,14 @@ lgx_status product(lgx_model* md, const DevQ8& W, int m, void* stream) {
         const lgx_gemv_mat g = gemv_mat(&W.m, nullptr, md->xq, md->xd, md->part, 1);
         return run_gemv_group(md->ctx, &g, 1, stream);
     }
-    return run_q8(md->ctx, m == 1 ? K_GEMV_MFMA : gemm_kernel(md->ctx, m), &W.m, nullptr, md->xq, md->xd, m, md->part, nullptr,
-                  stream, nullptr, nullptr, md->part);
+    // decode batches of 17..32 rows: two 16-row m-groups (twice the
+    // workgroups of the 32-row kernel, half the activation staging each;
+    // the weight tile's second read hits L2)
+    const Kern k = m == 1 ? K_GEMV_MFMA
+                   : (m > 16 && m <= 32 && !md->ctx->gemm_mt) ? K_GEMM_MFMA16
+                                                              : gemm_kernel(md->ctx, m);
+    return run_q8(md->ctx, k, &W.m, nullptr, md->xq, md->xd, m, md->part, nullptr, stream, nullptr,
+                  nullptr, md->part);
 }
 
 lgx_status norm(lgx_model* md, const float* w, int m, int n, int nr_part, bool with_part,

@@ -169,3 +169,19 @@ def test_prefill_attn_config4_shape_sampled(ctx, orc):
     lens = np.array([ctx_len[r // P] + r % P + 1 for r in rows], np.int32)
     ref = orc.gqa_decode_attn(q[rows], k, v, pt[[r // P for r in rows]], lens)
     assert np.array_equal(out[rows], ref)
+
+
+def test_repeated_calls_changing_lengths_bit_exact(ctx, orc):
+    """Call after call with changing lengths (empty, one chunk, many chunks,
+    ragged) on one ctx (its workspace reused), for d = 64 and 128: the
+    oracle's bits each time, zeros for empty sequences."""
+    for d, hq, hkv in ((64, 14, 2), (128, 28, 4)):
+        for rep, lens in enumerate(([0, 1, 256, 257, 3000], [2049, 0, 5, 511, 4097],
+                                    [7, 7, 7, 7, 7])):
+            B = len(lens)
+            k, v, pt, _ = make_cache(B, hkv, d, [4097] * B, seed=d + rep)
+            q = orc.gen_normal_f32(5, 10 * d + rep, (B, hq, d))
+            out = run(ctx, q, k, v, pt, lens, max_seq_len=4097)
+            ref = orc.gqa_decode_attn(q, k, v, pt, np.asarray(lens, np.int32))
+            assert np.array_equal(out, ref), (d, rep)
+            assert np.all(out[np.asarray(lens) == 0] == 0.0)

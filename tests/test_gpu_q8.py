@@ -404,10 +404,10 @@ def test_q8_gemm_7b_shapes_m64_streaming_and_tiled(ctx, orc, n, k):
     x = orc.gen_normal_f32(4, 7100 + n % 1000, (m, k))
     xq, xd = orc.quantize_q8_0(x)
     ref = orc.q8_gemm(qs, d, xq, xd)
-    ct = _ctx_with_env(LGX_GEMM_TILED_MIN=33, LGX_GEMM_TILED_ROWS=32)
-    for c in (ctx, ct):
+    cs = _ctx_with_env(LGX_GEMM_TILED_MIN=100000)       # the streaming 64-row kernel
+    for c in (ctx, cs):                                 # ctx: the tiled product (m >= 33)
         W = c.q8_matrix(qs, d)
         y = host(c.q8_gemm(W, c.to_device(xq), c.to_device(xd)))
-        assert np.array_equal(y, ref), c is ct
+        assert np.array_equal(y, ref), c is cs
         del W
-    ct.close()
+    cs.close()

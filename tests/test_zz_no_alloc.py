@@ -55,9 +55,9 @@ def test_noalloc_rejects_oversized_scratch_and_runs_untimed(ctx, orc):
     import logicaffeine_amd as lgx
 
     t = ctx.torch
-    n = k = 8960                      # 9 ranges: 9 * 127 * 8960 * 4 B > 32 MiB
+    n = k = 8960                      # tiled product: 3 groups x 400 x 8960 x 4 B > 32 MiB
     W = ctx.q8_matrix(*orc.gen_q8_matrix(7, 501, n, k))
-    m = 127
+    m = 400
     gq = t.zeros((m, k), dtype=t.int8, device=ctx.dev)
     gd = t.zeros((m, k // 32), dtype=t.int16, device=ctx.dev)
     y = t.full((m, n), 7.0, dtype=t.float32, device=ctx.dev)
