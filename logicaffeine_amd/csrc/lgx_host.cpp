@@ -81,6 +81,8 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
         const char* pfv = getenv("LGX_PREFILL");
         c->prefill_serial = pfv && std::string(pfv) == "serial";
         c->prefill_chunk = env_int("LGX_PREFILL_CHUNK", 0);
+        c->decode_fuse = env_int("LGX_DECODE_FUSE", 1) != 0;
+        c->fuse_cols32 = env_int("LGX_FUSE_SWIGLU_COLS", 32) == 64 ? 2 : 1;
         int ncu = 0;
         if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) ==
                 hipSuccess &&

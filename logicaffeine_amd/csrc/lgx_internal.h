@@ -121,6 +121,8 @@ enum Kern {
     K_PFA_D128_G1 = K_PFA_D64_G1 + 8,
     K_SAMPLE_PARTIAL = K_PFA_D128_G1 + 8,
     K_SAMPLE_FINAL,
+    K_GEMM_MFMA16_QKV,
+    K_GEMM_MFMA16_SWIGLU,
     K_COUNT
 };
 inline const char* const kKernelNames[] = {
@@ -151,6 +153,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_attn_prefill_d128_g4", "lgx_k_attn_prefill_d128_g5", "lgx_k_attn_prefill_d128_g6",
     "lgx_k_attn_prefill_d128_g7", "lgx_k_attn_prefill_d128_g8",
     "lgx_k_sample_partial", "lgx_k_sample_final",
+    "lgx_k_q8_gemm_mfma16_qkv", "lgx_k_q8_gemm_mfma16_swiglu",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -193,6 +196,8 @@ struct lgx_ctx {
     int tiled_grp = 0;            // LGX_GEMM_TILED_GRP: force 1/2/4 ranges per group
     bool decode_streaming = false; // LGX_DECODE_GEMM=streaming: decode products of m >= 17
                                    // rows through the streaming kernels
+    bool decode_fuse = true;      // LGX_DECODE_FUSE=0: decode glue in kernels of its own
+    int fuse_cols32 = 1;          // LGX_FUSE_SWIGLU_COLS: SwiGLU columns per fused workgroup / 32
     bool prefill_serial = false;  // LGX_PREFILL=serial: prefill as P decode passes
     int prefill_chunk = 0;        // LGX_PREFILL_CHUNK: positions per prefill chunk (0: by batch)
     int ncu = 256;                // compute units of the device

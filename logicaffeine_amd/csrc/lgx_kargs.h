@@ -170,6 +170,24 @@ typedef struct {
     int32_t xq_t16;        // xq in T16 tiles instead of row-major
 } lgx_swiglu_args;
 
+// 16-row streaming product (K in one range, so each output is final in the
+// workgroup that computes it) with its consumer applied in the same
+// workgroup: the outputs of the workgroup's tiles go to LDS, then
+//   LGX_FUSE_QKV:    workgroup = one head of the qkv rows (d / 16 tiles,
+//                    tpw = d / 64): bias + RoPE + q_out and the binary16 K/V
+//                    append, as lgx_k_qkv_rope_append (q.part, q.nr unused);
+//   LGX_FUSE_SWIGLU: workgroup = 32 * cols32 SwiGLU columns c0..: the gate
+//                    tiles of those columns and the up tiles at inter + c0
+//                    (2 * cols32 tiles each, tpw = cols32); silu(g) * u and
+//                    its Q8_0, as lgx_k_swiglu_quant (s.part, s.nr unused).
+#define LGX_FUSE_QKV 1
+#define LGX_FUSE_SWIGLU 2
+typedef struct {
+    lgx_gemv_args g;
+    lgx_qkv_args q;
+    lgx_swiglu_args s;
+} lgx_gemm_fused_args;
+
 // logits[m][v] = canonical dot of binary32 x[m] with binary16 row E[v]
 // (1024-element ranges, pairwise tree).
 typedef struct {

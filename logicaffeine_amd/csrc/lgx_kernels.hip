@@ -909,15 +909,30 @@ extern "C" __global__ __launch_bounds__(1024) void lgx_k_q8_gemv_grpq16(const lg
 // D[m][n] (lane l = r + 16c holds n = r, m = 4c + v); the epilogue runs the
 // canonical chain acc = fmaf((float)D, dw*dx, acc).  Range partials go to
 // `part` (several ranges) and lgx_k_q8_combine applies the tree.
+//
+// FUSE (LGX_FUSE_QKV / LGX_FUSE_SWIGLU, MT = 1, one range): the tiles of a
+// workgroup are the columns its consumer needs (one qkv head; the gate and
+// up tiles of 32 * tpw SwiGLU columns), the chains land in LDS instead of
+// `y`, and the consumer runs on them after the stream (lgx_gemm_fused_args).
 // ---------------------------------------------------------------------------
-template <int MT, int W, int PB>
-__device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
+constexpr int FUSE_COLS = 128;        // LDS columns of a fused workgroup (d <= 128; 2 * 64)
+__device__ __forceinline__ void fused_qkv_post(const lgx_qkv_args& q, const float* out_s, int ld, int head,
+                               int m0, int mrows);
+__device__ __forceinline__ void fused_swiglu_post(const lgx_swiglu_args& s, const float* out_s, int ld, int cols,
+                                  int c0, int m0, int mrows);
+
+template <int MT, int W, int PB, int FUSE = 0>
+__device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a,
+                                               const lgx_gemm_fused_args* f = nullptr) {
     constexpr int XSLOTS = MT * 16 * 64;   // 16-byte A-operand slots
     constexpr int DXROWS = MT * 16;
     constexpr int NT = 64 * W;
     constexpr int NB = 16 / PB;            // batches per tile-range (16 pairs)
+    static_assert(FUSE == 0 || MT == 1, "fused consumers take 16-row m-groups");
+    constexpr int FLD = FUSE_COLS + 1;     // fused output row stride (floats)
     __shared__ __align__(16) uint4 xa_s[XSLOTS];
     __shared__ __align__(16) float dx_s[LGX_Q8_RANGE_BLOCKS * DXROWS];
+    __shared__ float out_s[FUSE ? 16 * FLD : 1];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const RangeInfo ri = range_info(blockIdx.y, a.k);
     const int nb = a.k >> 5, nh = s16_nhalf(a.k);
@@ -931,11 +946,22 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
     const int last = ri.npairs - 1;
     const int tbase = tg * W * a.tpw + wave;
     const v4i zero = {0, 0, 0, 0};
+    // weight tile of the wave's j-th tile; SwiGLU: logical tiles u < half are
+    // gate tiles of the workgroup's columns, the others the up tiles
+    const int half = W * a.tpw / 2;
+    auto tile_of = [&](int j) {
+        if constexpr (FUSE == LGX_FUSE_SWIGLU) {
+            const int u = wave + W * j;
+            return u < half ? tg * half + u : f->s.inter / 16 + tg * half + (u - half);
+        } else {
+            return tbase + W * j;
+        }
+    };
 
     // batch q of tile j: pairs [PB*(q % NB), +PB) of the range; scales of the
     // batch are 2*PB consecutive blocks of the S16 half-range (q*PB)/8
     auto load_batch = [&](int j, int qb, uint4 (&w)[PB], uint32_t (&dw)[PB]) {
-        const int t = min(tbase + W * j, a.ntiles - 1);
+        const int t = min(tile_of(j), a.ntiles - 1);
         const uint4* wp = (const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64 + lane;
 #pragma unroll
         for (int i = 0; i < PB; ++i) w[i] = ld_stream(wp + min(PB * qb + i, last) * 64);
@@ -1009,6 +1035,13 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
         }
     };
     auto store_tile = [&](int j) {
+        if constexpr (FUSE != 0) {
+            // logical column tile u of the workgroup: LDS row mm, column 16u + r
+            const int u = wave + W * j;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) out_s[(4 * c + v) * FLD + u * 16 + r] = acc[0][v];
+            return;
+        }
         const int t = tbase + W * j;
         if (t >= a.ntiles) return;
         const int col = t * 16 + r;
@@ -1090,6 +1123,13 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a) {
         if (q + 2 < nbat) load_batch((q + 2) / nbq, (q + 2) % nbq, wn, dn);
         run_batch(q + 1, wn2, dn2);
     }
+    if constexpr (FUSE == LGX_FUSE_QKV) {
+        __syncthreads();
+        fused_qkv_post(f->q, out_s, FLD, tg, m0, mrows);
+    } else if constexpr (FUSE == LGX_FUSE_SWIGLU) {
+        __syncthreads();
+        fused_swiglu_post(f->s, out_s, FLD, 16 * half, tg * 16 * half, m0, mrows);
+    }
 }
 
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16(const lgx_gemv_args a) {
@@ -1100,6 +1140,12 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma32(const lgx
 }
 extern "C" __global__ __launch_bounds__(512) void lgx_k_q8_gemm_mfma64(const lgx_gemv_args a) {
     q8_stream_body<4, 8, 4>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16_qkv(const lgx_gemm_fused_args a) {
+    q8_stream_body<1, 4, 8, LGX_FUSE_QKV>(a.g, &a);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16_swiglu(const lgx_gemm_fused_args a) {
+    q8_stream_body<1, 4, 8, LGX_FUSE_SWIGLU>(a.g, &a);
 }
 
 // ---------------------------------------------------------------------------
@@ -1946,6 +1992,76 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_swiglu_quant(const lgx_s
     if (on && a.xq) {
         *(uint32_t*)(a.xq + xq_off(b, bl * 32 + 4 * j, a.inter, a.xq_t16 != 0)) = qw;
         if (j == 0) a.xd[(int64_t)b * nbl + bl] = dh;
+    }
+}
+
+// Consumers of the fused 16-row products (lgx_gemm_fused_args), run by the
+// product's workgroup on its outputs in LDS (row mm of the m-group at
+// out_s[mm * ld]).  The same operations in the same order as
+// lgx_k_qkv_rope_append and lgx_k_swiglu_quant on a one-range product.
+__device__ __forceinline__ void fused_qkv_post(const lgx_qkv_args& q, const float* out_s, int ld, int head,
+                               int m0, int mrows) {
+    const int d = q.d, half = d / 2;
+    const int qpr = max(q.qpr, 1);
+    const bool rot = head < q.hq + q.hkv;   // q and k heads rotate, v heads are copied
+    const int per = rot ? half : d;
+    const float* bias = q.bias ? q.bias + head * d : nullptr;
+    for (int e = threadIdx.x; e < mrows * per; e += blockDim.x) {
+        const int mm = e / per, i = e - mm * per;
+        const int b = m0 + mm, bs = b / qpr;
+        const int pos = min(max(q.seq_len[bs] + (b - bs * qpr), 0), q.max_seq - 1);
+        const int page =
+            min(max(q.page_table[(int64_t)bs * q.maxp + pos / LGX_PAGE], 0), q.num_pages - 1);
+        const int slot = pos % LGX_PAGE;
+        const float* row = out_s + mm * ld;
+        if (rot) {
+            const float x0 = bias ? row[i] + bias[i] : row[i];
+            const float x1 = bias ? row[i + half] + bias[i + half] : row[i + half];
+            const float c = q.cos_t[(int64_t)pos * half + i], sn = q.sin_t[(int64_t)pos * half + i];
+            const float t0 = x0 * c, t1 = x1 * sn, t2 = x1 * c, t3 = x0 * sn;
+            const float y0 = t0 - t1, y1 = t2 + t3;
+            if (head < q.hq) {
+                float* qo = q.q_out + ((int64_t)b * q.hq + head) * d;
+                qo[i] = y0;
+                qo[i + half] = y1;
+            } else {
+                uint16_t* kd = q.kpages + (((int64_t)page * q.hkv + (head - q.hq)) * LGX_PAGE + slot) * d;
+                kd[i] = f2h(y0);
+                kd[i + half] = f2h(y1);
+            }
+        } else {
+            const int g = head - q.hq - q.hkv;
+            uint16_t* vd = q.vpages + (((int64_t)page * q.hkv + g) * LGX_PAGE + slot) * d;
+            vd[i] = f2h(bias ? row[i] + bias[i] : row[i]);
+        }
+    }
+}
+
+// Gate columns at out_s[mm * ld + cc], up at out_s[mm * ld + cols + cc],
+// cc < cols; output columns c0 + cc.  8 lanes per 32-block, the 8 lanes of a
+// block always active together.
+__device__ __forceinline__ void fused_swiglu_post(const lgx_swiglu_args& s, const float* out_s, int ld, int cols,
+                                  int c0, int m0, int mrows) {
+    const int nbl = cols / 32, j = threadIdx.x & 7;
+    for (int e = threadIdx.x >> 3; e < 16 * nbl; e += blockDim.x >> 3) {
+        const int mm = e / nbl, bl = e - mm * nbl;
+        const bool on = mm < mrows;
+        const float* row = out_s + mm * ld + bl * 32 + 4 * j;
+        float f[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) f[k] = on ? lgx_silu(row[k]) * row[cols + k] : 0.0f;
+        const int64_t m = m0 + mm;
+        const int col = c0 + bl * 32 + 4 * j;
+        if (on && s.y) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) s.y[m * s.inter + col + k] = f[k];
+        }
+        uint16_t dh;
+        const uint32_t qw = quantize4(f, dh);
+        if (on && s.xq) {
+            *(uint32_t*)(s.xq + xq_off(m, col, s.inter, s.xq_t16 != 0)) = qw;
+            if (j == 0) s.xd[m * (s.inter / 32) + col / 32] = dh;
+        }
     }
 }
 

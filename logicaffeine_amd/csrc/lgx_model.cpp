@@ -63,6 +63,8 @@ struct lgx_model {
     float* xn = nullptr;
     int8_t* xq = nullptr;
     uint16_t* xd = nullptr;
+    int8_t* sq = nullptr;          // fused SwiGLU output (Q8_0 [max_batch][inter]): the
+    uint16_t* sd = nullptr;        // gate|up product still reads xq while it is written
     float* q = nullptr;
     float* part = nullptr;
     float* attn_part = nullptr;
@@ -262,14 +264,19 @@ int parts(const lgx_model* md, const DevQ8& W, int m) {
     return tiled_groups(W.m.k, tiled_grp(md->ctx, kern, W.m.n, W.m.k, m));
 }
 
-lgx_status product(lgx_model* md, const DevQ8& W, int m, void* stream) {
+lgx_status product(lgx_model* md, const DevQ8& W, int m, void* stream,
+                   const int8_t* xq = nullptr, const uint16_t* xd = nullptr) {
+    if (!xq) {
+        xq = md->xq;
+        xd = md->xd;
+    }
     if (dec_tiled(md, m)) {
         const Kern kern = tiled_kernel(md->ctx, m);
-        return run_q8_tiled(md->ctx, &W.m, md->xq, md->xd, m, md->part, stream, kern,
+        return run_q8_tiled(md->ctx, &W.m, xq, xd, m, md->part, stream, kern,
                             tiled_grp(md->ctx, kern, W.m.n, W.m.k, m));
     }
     if (m == 1 && gemv_group_ok(md->ctx, W.m.k)) {
-        const lgx_gemv_mat g = gemv_mat(&W.m, nullptr, md->xq, md->xd, md->part, 1);
+        const lgx_gemv_mat g = gemv_mat(&W.m, nullptr, xq, xd, md->part, 1);
         return run_gemv_group(md->ctx, &g, 1, stream);
     }
     // decode batches of 17..32 rows: two 16-row m-groups (twice the
@@ -278,8 +285,34 @@ lgx_status product(lgx_model* md, const DevQ8& W, int m, void* stream) {
     const Kern k = m == 1 ? K_GEMV_MFMA
                    : (m > 16 && m <= 32 && !md->ctx->gemm_mt) ? K_GEMM_MFMA16
                                                               : gemm_kernel(md->ctx, m);
-    return run_q8(md->ctx, k, &W.m, nullptr, md->xq, md->xd, m, md->part, nullptr, stream, nullptr,
+    return run_q8(md->ctx, k, &W.m, nullptr, xq, xd, m, md->part, nullptr, stream, nullptr,
                   nullptr, md->part);
+}
+
+// Decode products whose consumer runs in the product's own workgroups
+// (lgx_k_q8_gemm_mfma16_qkv / _swiglu): 2+ rows on the streaming kernels
+// and K in one range, so every output is final where it is computed.
+bool fused(const lgx_model* md, int m) {
+    const lgx_ctx* c = md->ctx;
+    return c->decode_fuse && m > 1 && !dec_tiled(md, m) && nranges_of(md->c.hidden) == 1 &&
+           (c->gemm_mt == 0 || c->gemm_mt == 16);
+}
+
+lgx_status run_fused(lgx_model* md, Kern kern, const DevQ8& W, int m, int tpw, int ngroups,
+                     lgx_gemm_fused_args& f, void* stream) {
+    lgx_gemv_args& a = f.g;
+    a.wt = W.m.qs;
+    a.wd = W.m.d;
+    a.xq = md->xq;
+    a.xd = md->xd;
+    a.n = W.m.n;
+    a.k = W.m.k;
+    a.m = m;
+    a.ntiles = W.m.n / 16;
+    a.nranges = 1;
+    a.nmgroups = (int)cdiv(m, 16);
+    a.tpw = tpw;
+    return launch(md->ctx, kern, dim3(ngroups * a.nmgroups), dim3(256), f, stream);
 }
 
 lgx_status norm(lgx_model* md, const float* w, int m, int n, int nr_part, bool with_part,
@@ -315,7 +348,6 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
         if ((st = norm(md, md->attn_norm[l], B, H, parts(md, md->dn[0], B), l > 0, nullptr, true,
                        stream)) != LGX_OK)
             return st;
-        if ((st = product(md, md->qkv[l], B, stream)) != LGX_OK) return st;
         lgx_qkv_args qa{};
         qa.part = md->part;
         qa.nr = parts(md, md->qkv[l], B);
@@ -334,7 +366,19 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
         qa.maxp = md->maxp;
         qa.num_pages = md->num_pages;
         qa.max_seq = cf.max_seq;
-        if ((st = launch(c, K_QKV_ROPE_APPEND, dim3(B), dim3(LGX_GLUE_NT), qa, stream)) != LGX_OK) return st;
+        if (fused(md, B)) {
+            // one workgroup per (head, 16-row m-group)
+            lgx_gemm_fused_args f{};
+            f.q = qa;
+            if ((st = run_fused(md, K_GEMM_MFMA16_QKV, md->qkv[l], B, d / 64, hq + 2 * hkv, f,
+                                stream)) != LGX_OK)
+                return st;
+        } else {
+            if ((st = product(md, md->qkv[l], B, stream)) != LGX_OK) return st;
+            if ((st = launch(c, K_QKV_ROPE_APPEND, dim3(B), dim3(LGX_GLUE_NT), qa, stream)) !=
+                LGX_OK)
+                return st;
+        }
         lgx_attn_args aa{};
         aa.q = md->q;
         aa.kpages = md->kc[l];
@@ -365,6 +409,17 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
         if ((st = norm(md, md->ffn_norm[l], B, H, parts(md, md->o[l], B), true, nullptr, true,
                        stream)) != LGX_OK)
             return st;
+        if (fused(md, B) && I % (32 * c->fuse_cols32) == 0) {
+            // one workgroup per (32 * cols32 SwiGLU columns, m-group); the Q8_0
+            // output goes to sq / sd, which the down product reads
+            lgx_gemm_fused_args f{};
+            f.s = lgx_swiglu_args{nullptr, 1, md->sq, md->sd, nullptr, B, I, 0};
+            if ((st = run_fused(md, K_GEMM_MFMA16_SWIGLU, md->gu[l], B, c->fuse_cols32,
+                                I / (32 * c->fuse_cols32), f, stream)) != LGX_OK)
+                return st;
+            if ((st = product(md, md->dn[l], B, stream, md->sq, md->sd)) != LGX_OK) return st;
+            continue;
+        }
         if ((st = product(md, md->gu[l], B, stream)) != LGX_OK) return st;
         lgx_swiglu_args sw{md->part, parts(md, md->gu[l], B), md->xq, md->xd, nullptr, B, I,
                            dec_tiled(md, B) ? 1 : 0};
@@ -728,6 +783,8 @@ lgx_status model_build(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed, So
         if ((st = dev_alloc(m, &m->h, (size_t)B * H)) || (st = dev_alloc(m, &m->xn, (size_t)B * H)) ||
             (st = dev_alloc(m, &m->xq, (size_t)(B + 15) / 16 * 16 * kmax)) ||
             (st = dev_alloc(m, &m->xd, (size_t)B * kmax / 32)) ||
+            (st = dev_alloc(m, &m->sq, (size_t)B * I)) ||
+            (st = dev_alloc(m, &m->sd, (size_t)B * I / 32)) ||
             (st = dev_alloc(m, &m->q, (size_t)B * hq * d)) || (st = dev_alloc(m, &m->part, (size_t)part)) ||
             (st = dev_alloc(m, &m->attn_part, (size_t)B * hq * m->nchunk * (d + 2))) ||
             (st = dev_alloc(m, &m->logits, cf.tied_embedding ? (size_t)B * cf.vocab : 1)) ||

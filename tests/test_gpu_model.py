@@ -442,3 +442,67 @@ def test_max_seq_bound_on_every_path():
         gm.close()
     cs.close()
     c.close()
+
+
+def _ctx_with(env):
+    import os
+
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        return lgx.Context(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("env", [{}, dict(LGX_FUSE_SWIGLU_COLS="64"), dict(LGX_DECODE_FUSE="0")])
+@pytest.mark.parametrize("name", ["tiny", "tiny_untied"])
+def test_fused_decode_consumers_bit_exact(name, env):
+    """Decode batches of 2..32 rows run RoPE + KV append inside the qkv
+    product's workgroups (one per head and 16-row m-group) and SwiGLU + Q8_0
+    inside the gate|up product's (32 or 64 columns each); with the fusion off
+    they run as kernels of their own.  Every form leaves the oracle's tokens,
+    logits and KV bits: 24 rows (a second, partial m-group), 3 rows, and one
+    row (the grouped GEMV), graph replays included."""
+    from oracle import oracle as orc
+
+    c = _ctx_with(env)
+    cfg = dict(orc.qwen_config(name), max_batch=24, max_seq=64)
+    gm = lgx.Model(c, cfg, 77)
+    om = orc.Model(cfg, 77)
+    rng = np.random.default_rng(5)
+    B = 24
+    tok = rng.integers(0, cfg["vocab"], size=B).astype(np.int32)
+    ref = tok.copy()
+    dtok = c.to_device(tok)
+    for s in range(4):
+        gm.decode_step(dtok)
+        ref, lg = om.step(np.arange(B), ref, want_logits=True)
+        assert np.array_equal(host(dtok), ref), s
+        assert np.array_equal(bits(host(gm.logits(B))), bits(lg)), s
+    hist = c.torch.empty((3, B), dtype=c.torch.int32, device=c.dev)
+    gm.generate(dtok, 3, hist)
+    for s in range(3):
+        ref = om.step(np.arange(B), ref)
+        assert np.array_equal(host(hist[s]), ref), s
+    for nb in (3, 1):
+        t = c.to_device(ref[:nb].copy())
+        for s in range(2):
+            gm.decode_step(t)
+            r, lg = om.step(np.arange(nb), (ref[:nb] if s == 0 else r), want_logits=True)
+            assert np.array_equal(host(t), r), (nb, s)
+            assert np.array_equal(bits(host(gm.logits(nb))), bits(lg)), (nb, s)
+    lens = [int(x) for x in dev_array(gm, "seq_len", np.int32, (B,))]
+    assert lens == [11, 9, 9] + [7] * 21
+    for layer in range(cfg["n_layers"]):
+        for b in (0, 2, 5, 23):
+            for which in (0, 1):
+                assert np.array_equal(kv_dense(gm, cfg, layer, which, b, lens[b]),
+                                      om.kv(layer, which, b, lens[b])), (layer, b, which)
+    gm.close()
+    om.close()
+    c.close()
