@@ -123,6 +123,7 @@ enum Kern {
     K_SAMPLE_FINAL,
     K_GEMM_MFMA16_QKV,
     K_GEMM_MFMA16_SWIGLU,
+    K_NORM_W,
     K_COUNT
 };
 inline const char* const kKernelNames[] = {
@@ -153,7 +154,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_attn_prefill_d128_g4", "lgx_k_attn_prefill_d128_g5", "lgx_k_attn_prefill_d128_g6",
     "lgx_k_attn_prefill_d128_g7", "lgx_k_attn_prefill_d128_g8",
     "lgx_k_sample_partial", "lgx_k_sample_final",
-    "lgx_k_q8_gemm_mfma16_qkv", "lgx_k_q8_gemm_mfma16_swiglu",
+    "lgx_k_q8_gemm_mfma16_qkv", "lgx_k_q8_gemm_mfma16_swiglu", "lgx_k_add_rmsnorm_quant_w",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -198,6 +199,7 @@ struct lgx_ctx {
                                    // rows through the streaming kernels
     bool decode_fuse = true;      // LGX_DECODE_FUSE=0: decode glue in kernels of its own
     int fuse_cols32 = 1;          // LGX_FUSE_SWIGLU_COLS: SwiGLU columns per fused workgroup / 32
+    int norm_waves = 1;           // LGX_NORM_WAVES: rows (waves) per workgroup of the wave norm (0: off)
     bool prefill_serial = false;  // LGX_PREFILL=serial: prefill as P decode passes
     int prefill_chunk = 0;        // LGX_PREFILL_CHUNK: positions per prefill chunk (0: by batch)
     int ncu = 256;                // compute units of the device
@@ -303,6 +305,12 @@ inline unsigned cdiv(int64_t a, int64_t b);
 // row fits them (n % 4 == 0, n <= 4096, nr <= 20), else the general one.
 inline lgx_status launch_norm(lgx_ctx* c, const lgx_norm_args& a, void* stream) {
     const int nr = a.part ? a.nr : 1;
+    // one wave per row for many short rows (prefill); a small batch (decode)
+    // runs faster spread over the 512-thread kernel's waves
+    if (c->norm_waves > 0 && a.m >= 64 && a.n % 4 == 0 && a.n <= 1024 && nr <= 8 &&
+        (!a.xq || a.n % 32 == 0))
+        return launch(c, K_NORM_W, dim3(cdiv(a.m, c->norm_waves)), dim3(64 * c->norm_waves), a,
+                      stream, 0u);
     if (a.n % 4 == 0 && a.n <= 4096 && nr <= 20)
         return launch(c, nr <= 8 ? K_NORM4_R8 : K_NORM4_R20, dim3(a.m), dim3(512), a, stream, 0u);
     return launch(c, K_ADD_RMSNORM_QUANT, dim3(a.m), dim3(LGX_GLUE_NT), a, stream, 0u);

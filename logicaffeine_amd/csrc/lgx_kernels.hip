@@ -47,6 +47,9 @@ __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(
 // Q8_0 of one 32-block held by 8 consecutive lanes (4 values each): the
 // lgx_k_quantize_q8_0 rule.  Returns the packed quants of this lane's four
 // values and the binary16 scale.
+__device__ __forceinline__ float4 add4(const float4& x, const float4& y) {
+    return make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+}
 __device__ __forceinline__ uint32_t quantize4(const float (&f)[4], uint16_t& dh) {
     float am = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
     am = fmaxf(am, shfl_xor_f(am, 1));
@@ -1697,9 +1700,6 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_embed(const lgx_embed_ar
 // level-by-level tree; at the end the pending subtrees fold from the
 // smallest (latest) up: T = L[hi] + (... + L[lo]).  j is a compile-time
 // constant in the unrolled loop, so every L index is static.
-__device__ __forceinline__ float4 add4(const float4& x, const float4& y) {
-    return make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
-}
 template <int R>
 __device__ __forceinline__ float4 tree_stream4(const float4 (&p)[R], int nr) {
     float4 L[6];
@@ -1864,6 +1864,106 @@ extern "C" __global__ __launch_bounds__(512) void lgx_k_add_rmsnorm_quant4_r8(co
 }
 extern "C" __global__ __launch_bounds__(512) void lgx_k_add_rmsnorm_quant4_r20(const lgx_norm_args a) {
     norm_body<512, 2, 20>(a);
+}
+
+// The same residual combine + RMSNorm (+ Q8_0) with one wave per row, for
+// n <= 1024 (n % 4 == 0) and nr <= 8: lane l owns the float4 slots l + 64k
+// (elements 256k + 4l .. + 3), requests h and every partial of them at once,
+// and the halving tree runs in registers (levels >= 256 across k, 128 .. 4
+// across lanes, 2 and 1 inside the float4), so no LDS and no barrier.  The
+// 8 lanes of a 32-element block hold it whole: Q8_0 straight from registers.
+extern "C" __global__ __launch_bounds__(256) void lgx_k_add_rmsnorm_quant_w(const lgx_norm_args a) {
+    constexpr int KS = 4, R = 8;
+    const int lane = threadIdx.x & 63;
+    const int b = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (b >= a.m) return;                    // whole waves only; no barrier below
+    const int n4 = a.n >> 2;
+    float4* hr = (float4*)(a.h + (int64_t)b * a.n);
+    float4 x4[KS];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) x4[k] = hr[min(lane + 64 * k, n4 - 1)];
+    if (a.part) {
+        float4 pv[KS][R];
+        const int64_t stride = (int64_t)a.m * n4;
+        const float4* pb = (const float4*)a.part + (int64_t)b * n4;
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+                pv[k][j] = j < a.nr ? pb[j * stride + min(lane + 64 * k, n4 - 1)]
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            float px[R], py[R], pz[R], pw[R];
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                px[j] = pv[k][j].x;
+                py[j] = pv[k][j].y;
+                pz[j] = pv[k][j].z;
+                pw[j] = pv[k][j].w;
+            }
+            x4[k].x = x4[k].x + tree_sum_r<R>(px, a.nr);
+            x4[k].y = x4[k].y + tree_sum_r<R>(py, a.nr);
+            x4[k].z = x4[k].z + tree_sum_r<R>(pz, a.nr);
+            x4[k].w = x4[k].w + tree_sum_r<R>(pw, a.nr);
+            if (lane + 64 * k < n4) hr[lane + 64 * k] = x4[k];
+        }
+    }
+    float v[KS][4];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+        const bool on = lane + 64 * k < n4;  // zero past n
+        v[k][0] = on ? x4[k].x * x4[k].x : 0.0f;
+        v[k][1] = on ? x4[k].y * x4[k].y : 0.0f;
+        v[k][2] = on ? x4[k].z * x4[k].z : 0.0f;
+        v[k][3] = on ? x4[k].w * x4[k].w : 0.0f;
+    }
+    int n2 = 4;
+    while (n2 < a.n) n2 <<= 1;
+    // slot i += slot i + sl for i < sl, sl = n2/2 .. 1; element i = 256k + 4 lane + e
+    for (int sl = n2 >> 1; sl >= 256; sl >>= 1) {
+        const int ks = sl >> 8;
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+            if (k < ks) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[k][e] = v[k][e] + v[k + ks][e];
+            }
+    }
+    for (int sl = min(n2 >> 1, 128); sl >= 4; sl >>= 1) {
+        const int dl = sl >> 2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[0][e] = v[0][e] + __shfl_down(v[0][e], dl, 64);
+    }
+    if (n2 >= 4) {
+        v[0][0] = v[0][0] + v[0][2];
+        v[0][1] = v[0][1] + v[0][3];
+        v[0][0] = v[0][0] + v[0][1];
+    }
+    const float ssq = __shfl(v[0][0], 0, 64);
+    const float ms = ssq / (float)a.n;
+    const float r = 1.0f / sqrtf(ms + a.eps);
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+        const int s = lane + 64 * k;
+        const bool on = s < n4;
+        const float4 w4 = ((const float4*)a.w)[min(s, n4 - 1)];
+        float y[4] = {(x4[k].x * r) * w4.x, (x4[k].y * r) * w4.y, (x4[k].z * r) * w4.z,
+                      (x4[k].w * r) * w4.w};
+        if (on && a.xn) *(float4*)(a.xn + (int64_t)b * a.n + 4 * s) = make_float4(y[0], y[1], y[2], y[3]);
+        if (on && a.xt) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a.xt[((int64_t)(b >> 4) * a.n + 4 * s + e) * 16 + (b & 15)] = y[e];
+        }
+        if (a.xq && 256 * k < a.n) {         // whole 8-lane blocks (n % 32 == 0 with Q8_0)
+            uint16_t dh;
+            const uint32_t qw = quantize4(y, dh);
+            if (on) {
+                *(uint32_t*)(a.xq + xq_off(b, 4 * s, a.n, a.xq_t16 != 0)) = qw;
+                if ((lane & 7) == 0) a.xd[(int64_t)b * (a.n / 32) + (s >> 3)] = dh;
+            }
+        }
+    }
 }
 
 // QKV combine + bias + RoPE + paged KV append.  One workgroup of 1024

@@ -28,7 +28,8 @@ def test_embed_gathers_binary16_rows(ctx, orc):
     assert np.array_equal(bits(out), bits(want))
 
 
-@pytest.mark.parametrize("m,n", [(1, 64), (3, 256), (5, 896), (2, 1000), (4, 3584), (2, 8192)])
+@pytest.mark.parametrize("m,n", [(1, 64), (3, 256), (5, 896), (32, 896), (96, 896), (64, 1024),
+                                 (70, 960), (2, 1000), (65, 1000), (4, 3584), (2, 8192)])
 def test_rmsnorm_quant_bit_exact(ctx, orc, m, n):
     rng = np.random.default_rng(n + m)
     x = (rng.standard_normal((m, n)) * rng.uniform(0.01, 30, size=(m, 1))).astype(np.float32)
@@ -59,13 +60,15 @@ def _tree_rows(part):
                     np.float32).reshape(m, n)
 
 
-@pytest.mark.parametrize("m,n,nr", [(3, 896, 1), (4, 896, 5), (2, 3584, 4), (5, 3584, 19),
+@pytest.mark.parametrize("m,n,nr", [(3, 896, 1), (4, 896, 5), (80, 896, 5), (64, 896, 8), (66, 256, 8),
+                                    (64, 1024, 3), (71, 64, 2), (64, 1000, 1), (2, 3584, 4), (5, 3584, 19),
                                     (2, 4096, 8), (2, 4096, 20), (2, 3584, 21), (1, 8192, 32),
                                     (2, 1000, 9), (1, 4096, 13)])
 def test_add_rmsnorm_quant_bit_exact(ctx, orc, m, n, nr):
-    """Residual form: h += tree of the range partials (the float4-slot
-    kernels for n % 4 == 0, n <= 4096, nr <= 20; the general kernel past
-    those), written back, then the RMSNorm + Q8_0 of the new h."""
+    """Residual form: h += tree of the range partials (one wave per row for
+    64+ rows of n % 4 == 0, n <= 1024, nr <= 8; the float4-slot kernels for
+    n <= 4096, nr <= 20; the general kernel past those), written back, then
+    the RMSNorm + Q8_0 of the new h."""
     rng = np.random.default_rng(m * 7 + n + nr)
     part = rng.standard_normal((nr, m, n)).astype(np.float32)
     h = (rng.standard_normal((m, n)) * 3).astype(np.float32)

@@ -464,10 +464,11 @@ def _ctx_with(env):
 def test_fused_decode_consumers_bit_exact(name, env):
     """Decode batches of 2..32 rows run RoPE + KV append inside the qkv
     product's workgroups (one per head and 16-row m-group) and SwiGLU + Q8_0
-    inside the gate|up product's (32 or 64 columns each); with the fusion off
-    they run as kernels of their own.  Every form leaves the oracle's tokens,
-    logits and KV bits: 24 rows (a second, partial m-group), 3 rows, and one
-    row (the grouped GEMV), graph replays included."""
+    inside the gate|up product's (32 or 64 columns each); with the fusion
+    off they run as kernels of their own.  Every form leaves the oracle's
+    tokens, logits, hidden state and KV bits: 24 rows (a second, partial
+    m-group), 3 rows, and one row (the grouped GEMV), graph replays
+    included."""
     from oracle import oracle as orc
 
     c = _ctx_with(env)
@@ -493,9 +494,12 @@ def test_fused_decode_consumers_bit_exact(name, env):
         t = c.to_device(ref[:nb].copy())
         for s in range(2):
             gm.decode_step(t)
-            r, lg = om.step(np.arange(nb), (ref[:nb] if s == 0 else r), want_logits=True)
+            r, lg, hid = om.step(np.arange(nb), (ref[:nb] if s == 0 else r), want_logits=True,
+                                 want_hidden=True)
             assert np.array_equal(host(t), r), (nb, s)
             assert np.array_equal(bits(host(gm.logits(nb))), bits(lg)), (nb, s)
+            assert np.array_equal(bits(dev_array(gm, "hidden", np.float32, (B, cfg["hidden"]))[:nb]),
+                                  bits(hid)), (nb, s)
     lens = [int(x) for x in dev_array(gm, "seq_len", np.int32, (B,))]
     assert lens == [11, 9, 9] + [7] * 21
     for layer in range(cfg["n_layers"]):
