@@ -1343,14 +1343,25 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
             }
         });
     }
-    // phase 2: max, exp, halving-tree sum
+    // phase 2: max, exp, halving-tree sum.  The wave maxima of the heads
+    // advance level by level together (independent shuffles in flight at
+    // once, not one chain per head)
+    {
+        float mw[GQ];
 #pragma unroll
-    for (int h = 0; h < GQ; ++h) {
-        s[h] = valid ? s[h] * a.scale : -__builtin_inff();
-        float m = s[h];
+        for (int h = 0; h < GQ; ++h) {
+            s[h] = valid ? s[h] * a.scale : -__builtin_inff();
+            mw[h] = s[h];
+        }
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, shfl_xor_f(m, o));
-        if (lane == 0) mx_s[h][wave] = m;
+        for (int o = 32; o >= 1; o >>= 1) {
+#pragma unroll
+            for (int h = 0; h < GQ; ++h) mw[h] = fmaxf(mw[h], shfl_xor_f(mw[h], o));
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int h = 0; h < GQ; ++h) mx_s[h][wave] = mw[h];
+        }
     }
     __syncthreads();
 #pragma unroll
@@ -1534,13 +1545,51 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
 template <int D>
 __device__ __forceinline__ float attn_merge(const lgx_attn_args& a, int bh) {
     constexpr int TCH = 256;                      // chunks per LDS tile
+    constexpr int FC = 16;                        // chunk count of the one-round path
     __shared__ float w_s[TCH], l_s[TCH], red_s[D / 64];
     const int i = threadIdx.x, lane = i & 63, wave = i >> 6;
     const int qpr = max(a.qpr, 1);
     const int row = bh / a.hq, b = row / qpr;
+    const float* pp = a.part + (int64_t)bh * a.nchunk * (D + 2);
+    if (a.nchunk <= FC) {
+        // every partial this thread may need (chunk i's m and l, o_c[i] of
+        // every chunk) requested together with the length; chunks at or past
+        // nc are never used
+        float mc = -__builtin_inff(), lc = 0.0f, ov[FC];
+        if (i < a.nchunk) {
+            mc = pp[i * (D + 2) + D];
+            lc = pp[i * (D + 2) + D + 1];
+        }
+#pragma unroll
+        for (int c = 0; c < FC; ++c) ov[c] = c < a.nchunk ? pp[c * (D + 2) + i] : 0.0f;
+        const int L = min(a.seq_len[b] + (row - b * qpr) + a.len_add, a.maxlen);
+        const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
+        float M = i < nc ? mc : -__builtin_inff();
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, shfl_xor_f(M, o));
+        if constexpr (D > 64) {
+            if (lane == 0) red_s[wave] = M;
+            __syncthreads();
+#pragma unroll
+            for (int w = 0; w < D / 64; ++w) M = fmaxf(M, red_s[w]);
+        }
+        if (i < nc) {
+            w_s[i] = lgx_expf(mc - M);
+            l_s[i] = lc;
+        }
+        __syncthreads();
+        float Ls = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int c = 0; c < FC; ++c) {
+            if (c < nc) {                         // uniform
+                Ls = fmaf(w_s[c], l_s[c], Ls);
+                O = fmaf(w_s[c], ov[c], O);
+            }
+        }
+        return nc > 0 ? O / Ls : 0.0f;
+    }
     const int L = min(a.seq_len[b] + (row - b * qpr) + a.len_add, a.maxlen);
     const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
-    const float* pp = a.part + (int64_t)bh * a.nchunk * (D + 2);
     float M = -__builtin_inff();
     for (int c = i; c < nc; c += D) M = fmaxf(M, pp[c * (D + 2) + D]);
 #pragma unroll
@@ -2954,32 +3003,51 @@ __device__ __forceinline__ void attn_prefill_body(const lgx_attn_args& a) {
     stage(a.vpages, 0);
 
     // ---- softmax, within the wave: max, p to LDS, halving tree (levels
-    // 128 and 64 in-lane, the rest across lanes) ----
+    // 128 and 64 in-lane, the rest across lanes); the wave's heads advance
+    // each shuffle level together ----
+    {
+        float mm[HW], l[HW];
 #pragma unroll
-    for (int hh = 0; hh < HW; ++hh) {
-        const int h = 4 * hg + hh;
-        float mm = -__builtin_inff();
+        for (int hh = 0; hh < HW; ++hh) {
+            mm[hh] = -__builtin_inff();
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            sc[hh][u] = lane + 64 * u < nq ? sc[hh][u] : -__builtin_inff();
-            mm = fmaxf(mm, sc[hh][u]);
+            for (int u = 0; u < 4; ++u) {
+                sc[hh][u] = lane + 64 * u < nq ? sc[hh][u] : -__builtin_inff();
+                mm[hh] = fmaxf(mm[hh], sc[hh][u]);
+            }
         }
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) mm = fmaxf(mm, shfl_xor_f(mm, o));
-        float p[4];
+        for (int o = 32; o >= 1; o >>= 1) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) p[u] = lane + 64 * u < nq ? lgx_expf(sc[hh][u] - mm) : 0.0f;
-        if (h < GQ) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) p_s[qp][h][lane + 64 * u] = p[u];
+            for (int hh = 0; hh < HW; ++hh) mm[hh] = fmaxf(mm[hh], shfl_xor_f(mm[hh], o));
         }
-        float l = (p[0] + p[2]) + (p[1] + p[3]);  // levels 128 and 64
 #pragma unroll
-        for (int s2 = 32; s2 >= 1; s2 >>= 1) l = l + __shfl_down(l, s2, 64);
-        if (lane == 0 && h < GQ && nq > 0) {
-            float* pp = a.part + (((int64_t)row * a.hq + g * GQ + h) * a.nchunk + c) * (D + 2);
-            pp[D] = mm;
-            pp[D + 1] = l;
+        for (int hh = 0; hh < HW; ++hh) {
+            const int h = 4 * hg + hh;
+            float p[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) p[u] = lane + 64 * u < nq ? lgx_expf(sc[hh][u] - mm[hh]) : 0.0f;
+            if (h < GQ) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) p_s[qp][h][lane + 64 * u] = p[u];
+            }
+            l[hh] = (p[0] + p[2]) + (p[1] + p[3]);  // levels 128 and 64
+        }
+#pragma unroll
+        for (int s2 = 32; s2 >= 1; s2 >>= 1) {
+#pragma unroll
+            for (int hh = 0; hh < HW; ++hh) l[hh] = l[hh] + __shfl_down(l[hh], s2, 64);
+        }
+        if (lane == 0 && nq > 0) {
+#pragma unroll
+            for (int hh = 0; hh < HW; ++hh) {
+                const int h = 4 * hg + hh;
+                if (h < GQ) {
+                    float* pp = a.part + (((int64_t)row * a.hq + g * GQ + h) * a.nchunk + c) * (D + 2);
+                    pp[D] = mm[hh];
+                    pp[D + 1] = l[hh];
+                }
+            }
         }
     }
 
