@@ -47,7 +47,10 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
         if (arch != "gfx950")
             return fail(LGX_UNSUPPORTED, "device %d is %s; lgx kernels are built for gfx950",
                         device, arch.c_str());
-        std::string path = hsaco_path ? std::string(hsaco_path) : default_hsaco_path();
+        const char* env_path = getenv("LGX_HSACO");
+        std::string path = hsaco_path             ? std::string(hsaco_path)
+                           : env_path && *env_path ? std::string(env_path)
+                                                   : default_hsaco_path();
         hipModule_t mod = nullptr;
         e = hipModuleLoad(&mod, path.c_str());
         if (e != hipSuccess)

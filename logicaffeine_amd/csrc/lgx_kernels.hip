@@ -44,6 +44,42 @@ __device__ __forceinline__ uint16_t f2h(float f) {
 __device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, 64); }
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
+// DPP lane moves for the wave reductions (VALU operations, where a shuffle
+// is an LDS round trip): quad_perm [1,0,3,2] (0xB1) and [2,3,0,1] (0x4E),
+// row_half_mirror (0x141: lane i <- 7 - i of its 8), row_mirror (0x140:
+// lane i <- 15 - i of its 16), row_shl:S (0x100 + S: lane i <- lane i + S of
+// its 16-lane row).  A lane without a source keeps its own value.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    const int x = __builtin_bit_cast(int, v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(x, x, CTRL, 0xf, 0xf, false));
+}
+// Maximum over each aligned group of 8 lanes, in every lane of the group
+// (fmaxf is order-free, so any pairing gives the same value).
+__device__ __forceinline__ float max8(float m) {
+    m = fmaxf(m, dpp_f<0xB1>(m));
+    m = fmaxf(m, dpp_f<0x4E>(m));
+    return fmaxf(m, dpp_f<0x141>(m));
+}
+// Maximum over the wave, in every lane.
+__device__ __forceinline__ float wave_max(float m) {
+    m = max8(m);
+    m = fmaxf(m, dpp_f<0x140>(m));
+    m = fmaxf(m, shfl_xor_f(m, 16));
+    return fmaxf(m, shfl_xor_f(m, 32));
+}
+// The halving tree over the wave's 64 slots, lane i += lane i + s for
+// s = 32, 16, ..., 1 (the same pairs and order as the shuffle form); the
+// sum is lane 0's.
+__device__ __forceinline__ float wave_tree_sum(float l) {
+    l = l + __shfl_down(l, 32, 64);
+    l = l + __shfl_down(l, 16, 64);
+    l = l + dpp_f<0x108>(l);
+    l = l + dpp_f<0x104>(l);
+    l = l + dpp_f<0x102>(l);
+    return l + dpp_f<0x101>(l);
+}
+
 // Q8_0 of one 32-block held by 8 consecutive lanes (4 values each): the
 // lgx_k_quantize_q8_0 rule.  Returns the packed quants of this lane's four
 // values and the binary16 scale.
@@ -52,9 +88,7 @@ __device__ __forceinline__ float4 add4(const float4& x, const float4& y) {
 }
 __device__ __forceinline__ uint32_t quantize4(const float (&f)[4], uint16_t& dh) {
     float am = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
-    am = fmaxf(am, shfl_xor_f(am, 1));
-    am = fmaxf(am, shfl_xor_f(am, 2));
-    am = fmaxf(am, shfl_xor_f(am, 4));
+    am = max8(am);
     const float d = am / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     uint32_t qw = 0;
@@ -246,9 +280,7 @@ __device__ __forceinline__ void quantize_blocks_to_lds(const lgx_gemv_args& a, i
         const int b = blo + bl;
         const float4 v = *(const float4*)(a.xf + (int64_t)b * 32 + 4 * j);
         float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        am = fmaxf(am, shfl_xor_f(am, 1));
-        am = fmaxf(am, shfl_xor_f(am, 2));
-        am = fmaxf(am, shfl_xor_f(am, 4));
+        am = max8(am);
         const float d = am / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         const float f[4] = {v.x, v.y, v.z, v.w};
@@ -736,7 +768,7 @@ __device__ __forceinline__ void grp_x_stage(const lgx_gemv_mat& a, const RangeIn
         float am = 0.0f;
 #pragma unroll
         for (int e = 0; e < 16; ++e) am = fmaxf(am, fabsf(f[e]));
-        am = fmaxf(am, shfl_xor_f(am, 1));
+        am = fmaxf(am, dpp_f<0xB1>(am));
         const float d = am / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
 #pragma unroll
@@ -1291,6 +1323,20 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
     for (int h = 0; h < GQ; ++h) s[h] = 0.0f;
     const bool valid = tid < n;
     uint4 kv[CPR];
+#ifndef LGX_ATTN_VREG
+#define LGX_ATTN_VREG 0
+#endif
+    constexpr bool VREG = D == 64 && LGX_ATTN_VREG;
+    uint4 vr[VREG ? CPR : 1];
+    if constexpr (VREG) {
+        const int64_t row = (((int64_t)pg_s[tid >> 4] * a.hkv + g) * LGX_PAGE + (tid & 15)) * D;
+        const uint4* kr = (const uint4*)(a.kpages + row);
+        const uint4* vp = (const uint4*)(a.vpages + row);
+#pragma unroll
+        for (int j = 0; j < CPR; ++j) kv[j] = kr[j];
+#pragma unroll
+        for (int j = 0; j < CPR; ++j) vr[j] = vp[j];
+    } else {
     {
         const uint4* kr = (const uint4*)(a.kpages +
                                          (((int64_t)pg_s[tid >> 4] * a.hkv + g) * LGX_PAGE + (tid & 15)) * D);
@@ -1305,6 +1351,7 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
     for (int j = 0; j < CPR; ++j)
         asm volatile("" : "+v"(kv[j].x), "+v"(kv[j].y), "+v"(kv[j].z), "+v"(kv[j].w));
     attn_stage_v<D>(a, g, n, pg_s, v_s, wave, lane);
+    }
     // D = 128: tokens VT.. of V, piece q = 256 i + tid of the second stage
     // (coalesced: 16 lanes per row), stored to v_s after the first stage
     // (rows past the chunk's end read a real page slot: pg_s is clamped)
@@ -1354,10 +1401,7 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
             mw[h] = s[h];
         }
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-#pragma unroll
-            for (int h = 0; h < GQ; ++h) mw[h] = fmaxf(mw[h], shfl_xor_f(mw[h], o));
-        }
+        for (int h = 0; h < GQ; ++h) mw[h] = wave_max(mw[h]);
         if (lane == 0) {
 #pragma unroll
             for (int h = 0; h < GQ; ++h) mx_s[h][wave] = mw[h];
@@ -1369,26 +1413,27 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
         const float m = fmaxf(fmaxf(mx_s[h][0], mx_s[h][1]), fmaxf(mx_s[h][2], mx_s[h][3]));
         p_s[h][tid] = valid ? lgx_expf(s[h] - m) : 0.0f;
     }
+    if constexpr (VREG) {
+#pragma unroll
+        for (int j = 0; j < CPR; ++j) ((uint4*)v_s)[tid * CPR + j] = vr[j];
+    }
     __builtin_amdgcn_s_waitcnt(0);               // this wave's first-stage V is in LDS
     __syncthreads();                             // ... and every other wave's, and p
-    if (tid < 64) {
-        // levels 128 and 64 of the tree from p_s, the rest across lanes
-        float l[GQ];
+    {
+        // head h's sum on wave h % 4: levels 128 and 64 of the tree from
+        // p_s, the rest across lanes
 #pragma unroll
-        for (int h = 0; h < GQ; ++h)
-            l[h] = (p_s[h][tid] + p_s[h][tid + 128]) + (p_s[h][tid + 64] + p_s[h][tid + 192]);
-#pragma unroll
-        for (int s2 = 32; s2 >= 1; s2 >>= 1) {
-#pragma unroll
-            for (int h = 0; h < GQ; ++h) l[h] = l[h] + __shfl_down(l[h], s2, 64);
-        }
-        if (tid == 0) {
-#pragma unroll
-            for (int h = 0; h < GQ; ++h) {
-                const float m = fmaxf(fmaxf(mx_s[h][0], mx_s[h][1]), fmaxf(mx_s[h][2], mx_s[h][3]));
-                float* pp = a.part + (((int64_t)b * a.hq + h0 + h) * a.nchunk + c) * (D + 2);
-                pp[D] = m;
-                pp[D + 1] = l[h];
+        for (int h0w = 0; h0w < GQ; h0w += 4) {
+            const int h = h0w + wave;
+            if (h < GQ) {
+                float l = (p_s[h][lane] + p_s[h][lane + 128]) + (p_s[h][lane + 64] + p_s[h][lane + 192]);
+                l = wave_tree_sum(l);
+                if (lane == 0) {
+                    const float m = fmaxf(fmaxf(mx_s[h][0], mx_s[h][1]), fmaxf(mx_s[h][2], mx_s[h][3]));
+                    float* pp = a.part + (((int64_t)b * a.hq + h0 + h) * a.nchunk + c) * (D + 2);
+                    pp[D] = m;
+                    pp[D + 1] = l;
+                }
             }
         }
     }
@@ -1564,9 +1609,7 @@ __device__ __forceinline__ float attn_merge(const lgx_attn_args& a, int bh) {
         for (int c = 0; c < FC; ++c) ov[c] = c < a.nchunk ? pp[c * (D + 2) + i] : 0.0f;
         const int L = min(a.seq_len[b] + (row - b * qpr) + a.len_add, a.maxlen);
         const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
-        float M = i < nc ? mc : -__builtin_inff();
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, shfl_xor_f(M, o));
+        float M = wave_max(i < nc ? mc : -__builtin_inff());
         if constexpr (D > 64) {
             if (lane == 0) red_s[wave] = M;
             __syncthreads();
@@ -1592,8 +1635,7 @@ __device__ __forceinline__ float attn_merge(const lgx_attn_args& a, int bh) {
     const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
     float M = -__builtin_inff();
     for (int c = i; c < nc; c += D) M = fmaxf(M, pp[c * (D + 2) + D]);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, shfl_xor_f(M, o));
+    M = wave_max(M);
     if (lane == 0) red_s[wave] = M;
     __syncthreads();
 #pragma unroll
@@ -1879,9 +1921,7 @@ __device__ __forceinline__ void norm_body(const lgx_norm_args& a) {
     }
     float Ssq = 0.0f;
     if (t < 64) {
-        Ssq = red[t];
-#pragma unroll
-        for (int sl = 32; sl >= 1; sl >>= 1) Ssq = Ssq + __shfl_down(Ssq, sl, 64);
+        Ssq = wave_tree_sum(red[t]);
     }
     __syncthreads();
     if (t == 0) red[0] = Ssq;
@@ -3017,10 +3057,7 @@ __device__ __forceinline__ void attn_prefill_body(const lgx_attn_args& a) {
             }
         }
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-#pragma unroll
-            for (int hh = 0; hh < HW; ++hh) mm[hh] = fmaxf(mm[hh], shfl_xor_f(mm[hh], o));
-        }
+        for (int hh = 0; hh < HW; ++hh) mm[hh] = wave_max(mm[hh]);
 #pragma unroll
         for (int hh = 0; hh < HW; ++hh) {
             const int h = 4 * hg + hh;
@@ -3034,10 +3071,7 @@ __device__ __forceinline__ void attn_prefill_body(const lgx_attn_args& a) {
             l[hh] = (p[0] + p[2]) + (p[1] + p[3]);  // levels 128 and 64
         }
 #pragma unroll
-        for (int s2 = 32; s2 >= 1; s2 >>= 1) {
-#pragma unroll
-            for (int hh = 0; hh < HW; ++hh) l[hh] = l[hh] + __shfl_down(l[hh], s2, 64);
-        }
+        for (int hh = 0; hh < HW; ++hh) l[hh] = wave_tree_sum(l[hh]);
         if (lane == 0 && nq > 0) {
 #pragma unroll
             for (int hh = 0; hh < HW; ++hh) {
