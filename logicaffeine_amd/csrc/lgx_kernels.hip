@@ -951,8 +951,17 @@ extern "C" __global__ __launch_bounds__(1024) void lgx_k_q8_gemv_grpq16(const lg
 // `y`, and the consumer runs on them after the stream (lgx_gemm_fused_args).
 // ---------------------------------------------------------------------------
 constexpr int FUSE_COLS = 128;        // LDS columns of a fused workgroup (d <= 128; 2 * 64)
-__device__ __forceinline__ void fused_qkv_post(const lgx_qkv_args& q, const float* out_s, int ld, int head,
-                               int m0, int mrows);
+constexpr int QKV_PE = 8;             // qkv consumer elements per thread: 16 rows x d <= 128 / 256
+struct QkvPrep {
+    int pos[QKV_PE], page[QKV_PE];
+    float b0[QKV_PE], b1[QKV_PE], c[QKV_PE], sn[QKV_PE];
+};
+__device__ __forceinline__ void fused_qkv_prep1(const lgx_qkv_args& q, int head, int m0, int mrows,
+                                                QkvPrep& p);
+__device__ __forceinline__ void fused_qkv_prep2(const lgx_qkv_args& q, int head, int m0, int mrows,
+                                                QkvPrep& p);
+__device__ __forceinline__ void fused_qkv_post(const lgx_qkv_args& q, const float* out_s, int ld,
+                                               int head, int m0, int mrows, const QkvPrep& p);
 __device__ __forceinline__ void fused_swiglu_post(const lgx_swiglu_args& s, const float* out_s, int ld, int cols,
                                   int c0, int m0, int mrows);
 
@@ -1098,7 +1107,10 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a,
 
     uint4 wn[PB], wn2[PB];
     uint32_t dn[PB], dn2[PB];
+    QkvPrep qp;
+    if constexpr (FUSE == LGX_FUSE_QKV) fused_qkv_prep1(f->q, tg, m0, mrows, qp);
     load_batch(0, 0, wn, dn);
+    if constexpr (FUSE == LGX_FUSE_QKV) fused_qkv_prep2(f->q, tg, m0, mrows, qp);
     // stage the activation range: every load of a thread is requested before
     // the first LDS store (one L2 round trip, not one per slot)
     {
@@ -1160,7 +1172,7 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a,
     }
     if constexpr (FUSE == LGX_FUSE_QKV) {
         __syncthreads();
-        fused_qkv_post(f->q, out_s, FLD, tg, m0, mrows);
+        fused_qkv_post(f->q, out_s, FLD, tg, m0, mrows, qp);
     } else if constexpr (FUSE == LGX_FUSE_SWIGLU) {
         __syncthreads();
         fused_swiglu_post(f->s, out_s, FLD, 16 * half, tg * 16 * half, m0, mrows);
@@ -1841,6 +1853,11 @@ __device__ __forceinline__ void norm_body(const lgx_norm_args& a) {
     bool on[KV];
 #pragma unroll
     for (int k = 0; k < KV; ++k) on[k] = t + NT * k < a.n;
+    // the weights of this thread's elements, requested with the row (a load
+    // after the barriers below would be one more memory round at the end)
+    float wk[KV];
+#pragma unroll
+    for (int k = 0; k < KV; ++k) wk[k] = on[k] ? a.w[t + NT * k] : 0.0f;
     float v[KV];
     if constexpr (S > 0) {
         const int n4 = a.n >> 2;
@@ -1932,7 +1949,7 @@ __device__ __forceinline__ void norm_body(const lgx_norm_args& a) {
     for (int k = 0; k < KV; ++k) {
         if (on[k]) {
             const int i = t + NT * k;
-            const float y = (row[i] * r) * a.w[i];
+            const float y = (row[i] * r) * wk[k];
             row[i] = y;
             if (a.xn) a.xn[(int64_t)b * a.n + i] = y;
             if (a.xt) a.xt[((int64_t)(b >> 4) * a.n + i) * 16 + (b & 15)] = y;
@@ -2188,25 +2205,62 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_swiglu_quant(const lgx_s
 // product's workgroup on its outputs in LDS (row mm of the m-group at
 // out_s[mm * ld]).  The same operations in the same order as
 // lgx_k_qkv_rope_append and lgx_k_swiglu_quant on a one-range product.
-__device__ __forceinline__ void fused_qkv_post(const lgx_qkv_args& q, const float* out_s, int ld, int head,
-                               int m0, int mrows) {
+// The qkv consumer's loads do not depend on the product, so they are made
+// before it (QkvPrep): stage 1, first in the kernel, the length of each
+// element's sequence and its bias; stage 2, after the first weight loads are
+// issued, the position's cos / sin and page entry.  vmcnt counts in issue
+// order, so waiting for stage 1 does not wait for the weight loads behind it.
+__device__ __forceinline__ void fused_qkv_prep1(const lgx_qkv_args& q, int head, int m0, int mrows,
+                                                QkvPrep& p) {
+    const int d = q.d, half = d / 2, qpr = max(q.qpr, 1);
+    const int per = head < q.hq + q.hkv ? half : d;
+    const float* bias = q.bias ? q.bias + head * d : nullptr;
+#pragma unroll
+    for (int j = 0; j < QKV_PE; ++j) {
+        const int e = threadIdx.x + 256 * j, mm = e / per, i = e - mm * per;
+        const bool on = mm < mrows;
+        p.pos[j] = on ? q.seq_len[(m0 + mm) / qpr] : 0;
+        p.b0[j] = on && bias ? bias[i] : 0.0f;
+        p.b1[j] = on && bias && per == half ? bias[i + half] : 0.0f;
+    }
+}
+__device__ __forceinline__ void fused_qkv_prep2(const lgx_qkv_args& q, int head, int m0, int mrows,
+                                                QkvPrep& p) {
+    const int d = q.d, half = d / 2, qpr = max(q.qpr, 1);
+    const bool rot = head < q.hq + q.hkv;
+    const int per = rot ? half : d;
+#pragma unroll
+    for (int j = 0; j < QKV_PE; ++j) {
+        const int e = threadIdx.x + 256 * j, mm = e / per, i = e - mm * per;
+        const bool on = mm < mrows;
+        const int b = m0 + mm, bs = b / qpr;
+        const int pos = min(max(p.pos[j] + (b - bs * qpr), 0), q.max_seq - 1);
+        p.pos[j] = pos;
+        p.page[j] = on ? q.page_table[(int64_t)bs * q.maxp + pos / LGX_PAGE] : 0;
+        p.c[j] = on && rot ? q.cos_t[(int64_t)pos * half + i] : 0.0f;
+        p.sn[j] = on && rot ? q.sin_t[(int64_t)pos * half + i] : 0.0f;
+    }
+}
+// Element e = threadIdx.x + 256 j of the head's rows: pair (i, i + d/2) of
+// a q / k head, value i of a v head.
+__device__ __forceinline__ void fused_qkv_post(const lgx_qkv_args& q, const float* out_s, int ld,
+                                               int head, int m0, int mrows, const QkvPrep& p) {
     const int d = q.d, half = d / 2;
-    const int qpr = max(q.qpr, 1);
     const bool rot = head < q.hq + q.hkv;   // q and k heads rotate, v heads are copied
     const int per = rot ? half : d;
-    const float* bias = q.bias ? q.bias + head * d : nullptr;
-    for (int e = threadIdx.x; e < mrows * per; e += blockDim.x) {
-        const int mm = e / per, i = e - mm * per;
-        const int b = m0 + mm, bs = b / qpr;
-        const int pos = min(max(q.seq_len[bs] + (b - bs * qpr), 0), q.max_seq - 1);
-        const int page =
-            min(max(q.page_table[(int64_t)bs * q.maxp + pos / LGX_PAGE], 0), q.num_pages - 1);
-        const int slot = pos % LGX_PAGE;
+    const bool bias = q.bias != nullptr;
+#pragma unroll
+    for (int j = 0; j < QKV_PE; ++j) {
+        const int e = threadIdx.x + 256 * j, mm = e / per, i = e - mm * per;
+        if (mm >= mrows) continue;
+        const int b = m0 + mm;
+        const int page = min(max(p.page[j], 0), q.num_pages - 1);
+        const int slot = p.pos[j] % LGX_PAGE;
         const float* row = out_s + mm * ld;
         if (rot) {
-            const float x0 = bias ? row[i] + bias[i] : row[i];
-            const float x1 = bias ? row[i + half] + bias[i + half] : row[i + half];
-            const float c = q.cos_t[(int64_t)pos * half + i], sn = q.sin_t[(int64_t)pos * half + i];
+            const float x0 = bias ? row[i] + p.b0[j] : row[i];
+            const float x1 = bias ? row[i + half] + p.b1[j] : row[i + half];
+            const float c = p.c[j], sn = p.sn[j];
             const float t0 = x0 * c, t1 = x1 * sn, t2 = x1 * c, t3 = x0 * sn;
             const float y0 = t0 - t1, y1 = t2 + t3;
             if (head < q.hq) {
@@ -2221,7 +2275,7 @@ __device__ __forceinline__ void fused_qkv_post(const lgx_qkv_args& q, const floa
         } else {
             const int g = head - q.hq - q.hkv;
             uint16_t* vd = q.vpages + (((int64_t)page * q.hkv + g) * LGX_PAGE + slot) * d;
-            vd[i] = f2h(bias ? row[i] + bias[i] : row[i]);
+            vd[i] = f2h(bias ? row[i] + p.b0[j] : row[i]);
         }
     }
 }
