@@ -1109,6 +1109,13 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a,
     uint32_t dn[PB], dn2[PB];
     QkvPrep qp;
     if constexpr (FUSE == LGX_FUSE_QKV) fused_qkv_prep1(f->q, tg, m0, mrows, qp);
+    // batches of the range that hold pairs (the last range may be short);
+    // the first is requested before the activations are staged, the second
+    // right after the staging loads (before their data is waited for), so a
+    // short stream (two batches: the small decode products) waits for one
+    // memory round, not two
+    const int nbq = min(NB, (ri.npairs + PB - 1) / PB);
+    const int nbat = nbq * a.tpw;
     load_batch(0, 0, wn, dn);
     if constexpr (FUSE == LGX_FUSE_QKV) fused_qkv_prep2(f->q, tg, m0, mrows, qp);
     // stage the activation range: every load of a thread is requested before
@@ -1122,12 +1129,16 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a,
             const int mt = s >> 10, pl = (s >> 6) & 15, l = s & 63;
             const int rr = l & 15, cc = l >> 4;
             const int m = m0 + mt * 16 + rr;
-            lo[k] = hi[k] = make_uint2(0, 0);
-            if (m < a.m && pl < ri.npairs) {
-                const int8_t* src = a.xq + (int64_t)m * a.k + (ri.p0 + pl) * 64 + 8 * cc;
-                lo[k] = *(const uint2*)src;
-                hi[k] = *(const uint2*)(src + 32);
-            }
+            // unconditional loads at clamped addresses, masked to zero after:
+            // a load under a branch makes the compiler wait for every load
+            // in flight (the weight batches included) where the paths join
+            const bool on = m < a.m && pl < ri.npairs;
+            const int8_t* src = a.xq + (int64_t)min(m, a.m - 1) * a.k +
+                                (ri.p0 + min(pl, ri.npairs - 1)) * 64 + 8 * cc;
+            const uint2 l2 = *(const uint2*)src, h2 = *(const uint2*)(src + 32);
+            const uint32_t keep = 0u - (uint32_t)on;
+            lo[k] = make_uint2(l2.x & keep, l2.y & keep);
+            hi[k] = make_uint2(h2.x & keep, h2.y & keep);
         }
         constexpr int DS = LGX_Q8_RANGE_BLOCKS * DXROWS / NT;   // scales per thread
         uint16_t dh[DS];
@@ -1135,8 +1146,16 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a,
         for (int k = 0; k < DS; ++k) {
             const int s = threadIdx.x + k * NT;
             const int b = s / DXROWS, m = s - b * DXROWS;
-            dh[k] = (m < mrows && b < ri.nbr) ? a.xd[(int64_t)(m0 + m) * nb + ri.b0 + b] : (uint16_t)0;
+            const uint16_t v = a.xd[(int64_t)(m0 + min(m, mrows - 1)) * nb + ri.b0 + min(b, ri.nbr - 1)];
+            // a mask, not a select: the compiler turns a select of a load into
+            // a branch around it, with a wait for every load at the join
+            dh[k] = v & (uint16_t)(0u - (uint32_t)(m < mrows && b < ri.nbr));
         }
+        // unconditional (indices clamped inside): under a branch, the join
+        // would wait for every load in flight; and nothing that consumes the
+        // staging loads is scheduled above it
+        load_batch(1 / nbq, 1 % nbq, wn2, dn2);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k = 0; k < XS; ++k)
             xa_s[threadIdx.x + k * NT] = make_uint4(lo[k].x, lo[k].y, hi[k].x, hi[k].y);
@@ -1144,9 +1163,6 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a,
         for (int k = 0; k < DS; ++k) dx_s[threadIdx.x + k * NT] = h2f(dh[k]);
     }
     __syncthreads();
-    // batches of the range that hold pairs (the last range may be short)
-    const int nbq = min(NB, (ri.npairs + PB - 1) / PB);
-    const int nbat = nbq * a.tpw;
     // batch q of the wave's stream: zero the chains at a tile's first batch,
     // store them after its last
     auto run_batch = [&](int q, const uint4 (&w)[PB], const uint32_t (&dw)[PB]) {
@@ -1160,15 +1176,16 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a,
         compute_batch(qb, w, dw);
         if (qb == nbq - 1) store_tile(q / nbq);
     };
-    // two buffers in turn (no register copies): batch q + 1 is requested
-    // before batch q is consumed
+    // two buffers in turn (no register copies): batch q + 1 is in flight
+    // while batch q is consumed, and batch q + 2 is requested into q's
+    // buffer as soon as q is done
 #pragma unroll 1
     for (int q = 0; q < nbat; q += 2) {
-        if (q + 1 < nbat) load_batch((q + 1) / nbq, (q + 1) % nbq, wn2, dn2);
         run_batch(q, wn, dn);
-        if (q + 1 >= nbat) break;
         if (q + 2 < nbat) load_batch((q + 2) / nbq, (q + 2) % nbq, wn, dn);
+        if (q + 1 >= nbat) break;
         run_batch(q + 1, wn2, dn2);
+        if (q + 3 < nbat) load_batch((q + 3) / nbq, (q + 3) % nbq, wn2, dn2);
     }
     if constexpr (FUSE == LGX_FUSE_QKV) {
         __syncthreads();
@@ -2203,13 +2220,15 @@ __device__ __forceinline__ void fused_qkv_prep1(const lgx_qkv_args& q, int head,
     const int d = q.d, half = d / 2, qpr = max(q.qpr, 1);
     const int per = head < q.hq + q.hkv ? half : d;
     const float* bias = q.bias ? q.bias + head * d : nullptr;
+    // every load unconditional at a valid address (rows past the m-group's
+    // read its last row; their values are never used): a load under a
+    // per-lane branch makes the compiler wait for all loads at the join
 #pragma unroll
     for (int j = 0; j < QKV_PE; ++j) {
         const int e = threadIdx.x + 256 * j, mm = e / per, i = e - mm * per;
-        const bool on = mm < mrows;
-        p.pos[j] = on ? q.seq_len[(m0 + mm) / qpr] : 0;
-        p.b0[j] = on && bias ? bias[i] : 0.0f;
-        p.b1[j] = on && bias && per == half ? bias[i + half] : 0.0f;
+        p.pos[j] = q.seq_len[(m0 + min(mm, mrows - 1)) / qpr];
+        p.b0[j] = bias ? bias[i] : 0.0f;
+        p.b1[j] = bias && per == half ? bias[i + half] : 0.0f;
     }
 }
 __device__ __forceinline__ void fused_qkv_prep2(const lgx_qkv_args& q, int head, int m0, int mrows,
@@ -2220,13 +2239,12 @@ __device__ __forceinline__ void fused_qkv_prep2(const lgx_qkv_args& q, int head,
 #pragma unroll
     for (int j = 0; j < QKV_PE; ++j) {
         const int e = threadIdx.x + 256 * j, mm = e / per, i = e - mm * per;
-        const bool on = mm < mrows;
-        const int b = m0 + mm, bs = b / qpr;
+        const int b = m0 + min(mm, mrows - 1), bs = b / qpr;
         const int pos = min(max(p.pos[j] + (b - bs * qpr), 0), q.max_seq - 1);
         p.pos[j] = pos;
-        p.page[j] = on ? q.page_table[(int64_t)bs * q.maxp + pos / LGX_PAGE] : 0;
-        p.c[j] = on && rot ? q.cos_t[(int64_t)pos * half + i] : 0.0f;
-        p.sn[j] = on && rot ? q.sin_t[(int64_t)pos * half + i] : 0.0f;
+        p.page[j] = q.page_table[(int64_t)bs * q.maxp + pos / LGX_PAGE];
+        p.c[j] = rot ? q.cos_t[(int64_t)pos * half + i] : 0.0f;
+        p.sn[j] = rot ? q.sin_t[(int64_t)pos * half + i] : 0.0f;
     }
 }
 // Element e = threadIdx.x + 256 j of the head's rows: pair (i, i + d/2) of
