@@ -1617,13 +1617,13 @@ __device__ __forceinline__ float attn_merge(const lgx_attn_args& a, int bh) {
         // every partial this thread may need (chunk i's m and l, o_c[i] of
         // every chunk) requested together with the length; chunks at or past
         // nc are never used
-        float mc = -__builtin_inff(), lc = 0.0f, ov[FC];
-        if (i < a.nchunk) {
-            mc = pp[i * (D + 2) + D];
-            lc = pp[i * (D + 2) + D + 1];
-        }
+        // (unconditional loads at clamped chunk indices: a load under a
+        // branch makes the compiler wait for every load where paths join)
+        const int ic = min(i, a.nchunk - 1);
+        const float mc = pp[ic * (D + 2) + D], lc = pp[ic * (D + 2) + D + 1];
+        float ov[FC];
 #pragma unroll
-        for (int c = 0; c < FC; ++c) ov[c] = c < a.nchunk ? pp[c * (D + 2) + i] : 0.0f;
+        for (int c = 0; c < FC; ++c) ov[c] = pp[min(c, a.nchunk - 1) * (D + 2) + i];
         const int L = min(a.seq_len[b] + (row - b * qpr) + a.len_add, a.maxlen);
         const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
         float M = wave_max(i < nc ? mc : -__builtin_inff());
@@ -1862,7 +1862,8 @@ __device__ __forceinline__ void norm_body(const lgx_norm_args& a) {
     // after the barriers below would be one more memory round at the end)
     float wk[KV];
 #pragma unroll
-    for (int k = 0; k < KV; ++k) wk[k] = on[k] ? a.w[t + NT * k] : 0.0f;
+    for (int k = 0; k < KV; ++k)
+        if (NT * k < a.n) wk[k] = a.w[min(t + NT * k, a.n - 1)];   // uniform test, clamped index
     float v[KV];
     if constexpr (S > 0) {
         const int n4 = a.n >> 2;
