@@ -114,10 +114,11 @@ def run_step(ctx, sets, i, acts, m):
                                      [acts[name][0][0] for name, _, _ in SHAPES],
                                      [acts[name][3][0] for name, _, _ in SHAPES])
         return
-    for name, n, k in SHAPES:
-        x, xq, xd, y, part = acts[name]
-        ctx.quantize_q8_0(x, xq, xd)
-        ctx.q8_gemm(W[name], xq, xd, y=y)
+    # quantisation, products and range trees of the three matrices in three
+    # launches of the grouped M > 1 product
+    ctx.q8_gemm_quantize_group([W[name] for name, _, _ in SHAPES],
+                               [acts[name][0] for name, _, _ in SHAPES],
+                               [acts[name][3] for name, _, _ in SHAPES])
 
 
 def make_acts(ctx, torch, m):

@@ -58,6 +58,7 @@ SIGNATURES = {
     "lgx_q8_gemm_noalloc": (C.c_int, [_P, _P, _P, _P, _I32, _P, _P]),
     "lgx_q8q8_gemv_quantize": (C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     "lgx_q8q8_gemv_quantize_group": (C.c_int, [_P, _I32, _P, _P, _P, _P]),
+    "lgx_q8_gemm_quantize_group": (C.c_int, [_P, _I32, _P, _P, _I32, _P, _P]),
     "lgx_q8_range_count": (_I32, [_I32]),
     "lgx_q8q8_gemv_quantize_partials": (C.c_int, [_P, _P, _P, _P, _P, _P, _P]),
     "lgx_q8_gemm_partials": (C.c_int, [_P, _P, _P, _P, _I32, _P, _P]),
@@ -382,6 +383,22 @@ class Context:
         xp = (C.c_void_p * n)(*[x.data_ptr() for x in xs])
         yp = (C.c_void_p * n)(*[y.data_ptr() for y in ys])
         _check(lib().lgx_q8q8_gemv_quantize_group(self.handle, n, arr, xp, yp, self._s()))
+        return ys
+
+    def q8_gemm_quantize_group(self, Ws, xs, ys=None):
+        """ys[i] = Q8_0(xs[i]) Ws[i]^T for up to 8 matrices (xs[i]: [m][k_i]
+        binary32, the same m for all) in three launches."""
+        t = self.torch
+        n = len(Ws)
+        m = xs[0].shape[0] if xs[0].dim() == 2 else 1
+        for x, W in zip(xs, Ws):
+            if (x.shape[0] if x.dim() == 2 else 1) != m or x.shape[-1] != W.k or not x.is_contiguous():
+                raise ValueError("every x must be a contiguous [m][k] of its matrix")
+        ys = [t.empty((m, W.n), dtype=t.float32, device=self.dev) for W in Ws] if ys is None else ys
+        arr = (Q8MatrixC * n)(*[W._c for W in Ws])
+        xp = (C.c_void_p * n)(*[x.data_ptr() for x in xs])
+        yp = (C.c_void_p * n)(*[y.data_ptr() for y in ys])
+        _check(lib().lgx_q8_gemm_quantize_group(self.handle, n, arr, xp, m, yp, self._s()))
         return ys
 
     def q8q8_gemv_quantize_partials(self, W: Q8Matrix, x, part=None):

@@ -488,6 +488,172 @@ static lgx_status q8_gemm_impl(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t*
                   nullptr, part);
 }
 
+lgx_status lgx_q8_gemm_quantize_group(lgx_ctx* c, int32_t count, const lgx_q8_matrix* W,
+                                      const float* const* x, int32_t m, float* const* y,
+                                      void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!W || !x || !y) return fail(LGX_NULL_POINTER, "NULL W, x or y array");
+        if (count < 1 || count > LGX_MGROUP_MAX)
+            return fail(LGX_OUT_OF_BOUNDS, "count = %d (1..%d)", count, LGX_MGROUP_MAX);
+        if (m <= 0 || m > 65535 * 64) return fail(LGX_OUT_OF_BOUNDS, "m = %d out of range", m);
+        for (int i = 0; i < count; ++i) {
+            if ((st = check_q8(&W[i])) != LGX_OK) return st;
+            if (!x[i] || !y[i]) return fail(LGX_NULL_POINTER, "NULL x[%d] or y[%d]", i, i);
+        }
+        if (m == 1) {
+            lgx_gemv_mat mats[LGX_GROUP_MAX];
+            for (int i = 0; i < count; ++i) {
+                if (!gemv_group_ok(c, W[i].k))
+                    return fail(LGX_UNSUPPORTED, "W[%d].k = %d too long for a grouped GEMV", i,
+                                W[i].k);
+                mats[i] = gemv_mat(&W[i], x[i], nullptr, nullptr, y[i], 0);
+            }
+            std::stable_sort(mats, mats + count, [](const lgx_gemv_mat& a, const lgx_gemv_mat& b) {
+                return a.k > b.k;
+            });
+            return run_gemv_group(c, mats, count, stream);
+        }
+        const bool tiled = m >= c->tiled_min;
+        const Kern tk = tiled_kernel(c, m);
+        const int trows = tk == K_GEMM_TILED ? 128 : tk == K_GEMM_TILED64 ? 64 : 32;
+        // ranges per group of the tiled products: from the tiles of all the
+        // matrices together (one launch fills the device)
+        int grp = 1;
+        if (tiled) {
+            if (c->tiled_grp) {
+                grp = c->tiled_grp;
+            } else {
+                for (grp = 4; grp > 1; grp >>= 1) {
+                    int64_t wgs = 0;
+                    for (int i = 0; i < count; ++i)
+                        wgs += (int64_t)cdiv(W[i].n, LGX_TG_N) * cdiv(m, trows) * tiled_groups(W[i].k, grp);
+                    if (wgs >= 4LL * c->ncu) break;
+                }
+            }
+        }
+        // workspace: per matrix the Q8_0 activations (T16 tiles padded to 16
+        // rows on the tiled path), their scales, and partials when there are
+        // several ranges / groups; 256-byte aligned pieces
+        auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+        size_t xq_b[LGX_MGROUP_MAX], xd_b[LGX_MGROUP_MAX], pt_b[LGX_MGROUP_MAX];
+        int nparts[LGX_MGROUP_MAX];
+        size_t total = 0;
+        for (int i = 0; i < count; ++i) {
+            const int k = W[i].k, n = W[i].n;
+            xq_b[i] = al((size_t)(tiled ? cdiv(m, 16) * 16 : m) * k);
+            xd_b[i] = al((size_t)m * (k / 32) * 2);
+            nparts[i] = tiled ? tiled_groups(k, grp) : nranges_of(k);
+            pt_b[i] = nparts[i] > 1 ? al((size_t)nparts[i] * m * n * sizeof(float)) : 0;
+            total += xq_b[i] + xd_b[i] + pt_b[i];
+        }
+        float* ws = nullptr;
+        if ((st = ensure_ws(c, total, &ws)) != LGX_OK) return st;
+        char* wp = (char*)ws;
+        int8_t* xq[LGX_MGROUP_MAX];
+        uint16_t* xd[LGX_MGROUP_MAX];
+        float* part[LGX_MGROUP_MAX];
+        for (int i = 0; i < count; ++i) {
+            xq[i] = (int8_t*)wp;
+            wp += xq_b[i];
+            xd[i] = (uint16_t*)wp;
+            wp += xd_b[i];
+            part[i] = pt_b[i] ? (float*)wp : y[i];
+            wp += pt_b[i];
+        }
+        // 1. Q8_0 of every activation matrix
+        lgx_quant_group_args qa{};
+        qa.m = m;
+        qa.count = count;
+        qa.t16 = tiled ? 1 : 0;
+        qa.blk0[0] = 0;
+        for (int i = 0; i < count; ++i) {
+            qa.x[i] = x[i];
+            qa.xq[i] = xq[i];
+            qa.xd[i] = xd[i];
+            qa.k[i] = W[i].k;
+            qa.blk0[i + 1] = qa.blk0[i] + (int64_t)m * (W[i].k / 32);
+        }
+        if ((st = launch(c, K_QUANT_GROUP, dim3(cdiv(qa.blk0[count] * 8, 256)), dim3(256), qa,
+                         stream)) != LGX_OK)
+            return st;
+        // 2. the products
+        if (tiled) {
+            lgx_tiled_group_args ta{};
+            ta.count = count;
+            ta.wg0[0] = 0;
+            for (int i = 0; i < count; ++i) {
+                lgx_gemm_tiled_args& a = ta.mat[i];
+                a.wt = W[i].qs;
+                a.wd = W[i].d;
+                a.xt = xq[i];
+                a.xd = xd[i];
+                a.part = part[i];
+                a.n = W[i].n;
+                a.k = W[i].k;
+                a.m = m;
+                a.grp = grp;
+                a.ngroups = tiled_groups(W[i].k, grp);
+                a.ntn = (int)cdiv(W[i].n, LGX_TG_N);
+                a.ntm = (int)cdiv(m, trows);
+                const int64_t wgs = (int64_t)a.ntn * a.ntm * a.ngroups;
+                const int64_t end = ta.wg0[i] + (wgs + 7) / 8 * 8;
+                if (end > INT32_MAX) return fail(LGX_OUT_OF_BOUNDS, "grouped product too large");
+                ta.wg0[i + 1] = (int32_t)end;
+            }
+            const Kern gk = tk == K_GEMM_TILED   ? K_GEMM_TILED_GROUP
+                            : tk == K_GEMM_TILED64 ? K_GEMM_TILED64_GROUP
+                                                   : K_GEMM_TILED32_GROUP;
+            if ((st = launch(c, gk, dim3(ta.wg0[count]), dim3(256), ta, stream)) != LGX_OK) return st;
+        } else {
+            lgx_stream_group_args sa{};
+            sa.count = count;
+            sa.wg0[0] = 0;
+            for (int i = 0; i < count; ++i) {
+                lgx_gemv_args& a = sa.mat[i];
+                a.wt = W[i].qs;
+                a.wd = W[i].d;
+                a.xq = xq[i];
+                a.xd = xd[i];
+                a.y = y[i];
+                a.part = part[i];
+                a.n = W[i].n;
+                a.k = W[i].k;
+                a.m = m;
+                a.ntiles = W[i].n / 16;
+                a.nranges = nranges_of(W[i].k);
+                a.nmgroups = (int)cdiv(m, 16);
+                const int64_t tasks = (int64_t)a.ntiles * a.nranges * a.nmgroups;
+                const int64_t tpw = (tasks + 4LL * c->wg_target - 1) / (4LL * c->wg_target);
+                a.tpw = (int)(tpw < 1 ? 1 : tpw > 64 ? 64 : tpw);
+                sa.gx[i] = (int)(cdiv(a.ntiles, 4LL * a.tpw) * a.nmgroups);
+                const int64_t end = sa.wg0[i] + (int64_t)sa.gx[i] * a.nranges;
+                if (end > INT32_MAX) return fail(LGX_OUT_OF_BOUNDS, "grouped product too large");
+                sa.wg0[i + 1] = (int32_t)end;
+            }
+            if ((st = launch(c, K_GEMM_MFMA16_GROUP, dim3(sa.wg0[count]), dim3(256), sa, stream)) !=
+                LGX_OK)
+                return st;
+        }
+        // 3. the trees of the products with several ranges / groups
+        lgx_combine_group_args ca{};
+        int nc = 0;
+        ca.el0[0] = 0;
+        for (int i = 0; i < count; ++i) {
+            if (nparts[i] <= 1) continue;
+            ca.part[nc] = part[i];
+            ca.y[nc] = y[i];
+            ca.nr[nc] = nparts[i];
+            ca.el0[nc + 1] = ca.el0[nc] + (int64_t)m * W[i].n;
+            ++nc;
+        }
+        ca.count = nc;
+        if (nc == 0) return LGX_OK;
+        return launch(c, K_COMBINE_GROUP, dim3(cdiv(ca.el0[nc], 256)), dim3(256), ca, stream);
+    });
+}
+
 lgx_status lgx_q8_gemm(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq, const uint16_t* xd,
                        int32_t m, float* y, void* stream) {
     return guarded(__func__, [&] { return q8_gemm_impl(c, W, xq, xd, m, y, stream, nullptr, 0); });

@@ -259,6 +259,46 @@ typedef struct {
     int32_t grp;           // ranges per group: 1, 2 or 4 (ngroups = ceil(nranges / grp))
 } lgx_gemm_tiled_args;
 
+// Grouped M > 1 products (lgx_q8_gemm_quantize_group): up to
+// LGX_MGROUP_MAX independent matrices, m rows each, in three launches.
+#define LGX_MGROUP_MAX 8
+// Q8_0 of every x[g] ([m][k[g]] binary32) -> xq[g] (row-major, or T16 tiles
+// when t16) and xd[g] [m][k/32]; 8 lanes per 32-block, blocks numbered over
+// the matrices (blk0[g] = first block of matrix g).
+typedef struct {
+    const float* x[LGX_MGROUP_MAX];
+    int8_t* xq[LGX_MGROUP_MAX];
+    uint16_t* xd[LGX_MGROUP_MAX];
+    int32_t k[LGX_MGROUP_MAX];
+    int64_t blk0[LGX_MGROUP_MAX + 1];
+    int32_t m, count, t16;
+} lgx_quant_group_args;
+// The tiled product of every matrix in one launch: matrix g takes
+// workgroups wg0[g] .. wg0[g+1]-1 (a multiple of 8 from the start, so each
+// keeps its XCD-aware order; the padding workgroups exit).
+typedef struct {
+    lgx_gemm_tiled_args mat[LGX_MGROUP_MAX];
+    int32_t wg0[LGX_MGROUP_MAX + 1];
+    int32_t count;
+} lgx_tiled_group_args;
+// The 16-row streaming product of every matrix in one launch: matrix g
+// takes workgroups wg0[g] .. as its own (gx[g] x nranges) grid, x fastest.
+typedef struct {
+    lgx_gemv_args mat[LGX_MGROUP_MAX];
+    int32_t wg0[LGX_MGROUP_MAX + 1];
+    int32_t gx[LGX_MGROUP_MAX];
+    int32_t count;
+} lgx_stream_group_args;
+// y[g][i] = tree over part[g][0..nr[g]) at element i (count m*n of matrix
+// g); elements numbered over the matrices from el0[g].
+typedef struct {
+    const float* part[LGX_MGROUP_MAX];
+    float* y[LGX_MGROUP_MAX];
+    int32_t nr[LGX_MGROUP_MAX];
+    int64_t el0[LGX_MGROUP_MAX + 1];
+    int32_t count;
+} lgx_combine_group_args;
+
 // Row-major int8 [rows][k] -> T16 tiles of ceil(rows/16) * 16 rows, the rows
 // past `rows` zero.
 typedef struct {

@@ -966,8 +966,8 @@ __device__ __forceinline__ void fused_swiglu_post(const lgx_swiglu_args& s, cons
                                   int c0, int m0, int mrows);
 
 template <int MT, int W, int PB, int FUSE = 0>
-__device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a,
-                                               const lgx_gemm_fused_args* f = nullptr) {
+__device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a, const lgx_gemm_fused_args* f,
+                                               int bx, int by) {
     constexpr int XSLOTS = MT * 16 * 64;   // 16-byte A-operand slots
     constexpr int DXROWS = MT * 16;
     constexpr int NT = 64 * W;
@@ -978,11 +978,11 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a,
     __shared__ __align__(16) float dx_s[LGX_Q8_RANGE_BLOCKS * DXROWS];
     __shared__ float out_s[FUSE ? 16 * FLD : 1];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const RangeInfo ri = range_info(blockIdx.y, a.k);
+    const RangeInfo ri = range_info(by, a.k);
     const int nb = a.k >> 5, nh = s16_nhalf(a.k);
     // m-group fastest along x: the groups of one set of row tiles run
     // together and share the weight stream through L2 / MALL
-    const int mg = blockIdx.x % a.nmgroups, tg = blockIdx.x / a.nmgroups;
+    const int mg = bx % a.nmgroups, tg = bx / a.nmgroups;
     const int m0 = mg * DXROWS;
     const int mrows = min(DXROWS, a.m - m0);
     const int r = lane & 15, c = lane >> 4;
@@ -1197,19 +1197,28 @@ __device__ __forceinline__ void q8_stream_body(const lgx_gemv_args& a,
 }
 
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16(const lgx_gemv_args a) {
-    q8_stream_body<1, 4, 8>(a);
+    q8_stream_body<1, 4, 8>(a, nullptr, blockIdx.x, blockIdx.y);
 }
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma32(const lgx_gemv_args a) {
-    q8_stream_body<2, 4, 8>(a);
+    q8_stream_body<2, 4, 8>(a, nullptr, blockIdx.x, blockIdx.y);
 }
 extern "C" __global__ __launch_bounds__(512) void lgx_k_q8_gemm_mfma64(const lgx_gemv_args a) {
-    q8_stream_body<4, 8, 4>(a);
+    q8_stream_body<4, 8, 4>(a, nullptr, blockIdx.x, blockIdx.y);
 }
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16_qkv(const lgx_gemm_fused_args a) {
-    q8_stream_body<1, 4, 8, LGX_FUSE_QKV>(a.g, &a);
+    q8_stream_body<1, 4, 8, LGX_FUSE_QKV>(a.g, &a, blockIdx.x, blockIdx.y);
 }
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16_swiglu(const lgx_gemm_fused_args a) {
-    q8_stream_body<1, 4, 8, LGX_FUSE_SWIGLU>(a.g, &a);
+    q8_stream_body<1, 4, 8, LGX_FUSE_SWIGLU>(a.g, &a, blockIdx.x, blockIdx.y);
+}
+// Grouped 16-row streaming products (lgx_stream_group_args): workgroup ->
+// (matrix, its own block coordinates).
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16_group(const lgx_stream_group_args a) {
+    const int bid = blockIdx.x;
+    int g = 0;
+    while (g + 1 < a.count && bid >= a.wg0[g + 1]) ++g;
+    const int local = bid - a.wg0[g];
+    q8_stream_body<1, 4, 8>(a.mat[g], nullptr, local % a.gx[g], local / a.gx[g]);
 }
 
 // ---------------------------------------------------------------------------
@@ -2729,7 +2738,7 @@ struct TgSmem {
 };
 
 template <int WM>
-__device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a) {
+__device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a, const int P) {
     constexpr int MTILES = 2 * WM;
     // two stage buffers as two variables: a direct load into one is known
     // not to alias reads of the other
@@ -2739,7 +2748,7 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a) {
     const int r = lane & 15, c = lane >> 4;
     // XCD-aware logical id, then (group, band of 8 activation tiles, n tile)
     const int T = a.ntn * a.ntm * a.ngroups;
-    const int P = blockIdx.x, xcd = P & 7, slot = P >> 3;
+    const int xcd = P & 7, slot = P >> 3;
     const int q8 = T >> 3, r8 = T & 7;
     const int id = xcd * q8 + min(xcd, r8) + slot;
     const int per_g = a.ntn * a.ntm;
@@ -2941,13 +2950,67 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a) {
 }
 
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled(const lgx_gemm_tiled_args a) {
-    q8_tiled_body<4>(a);
+    q8_tiled_body<4>(a, blockIdx.x);
 }
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled64(const lgx_gemm_tiled_args a) {
-    q8_tiled_body<2>(a);
+    q8_tiled_body<2>(a, blockIdx.x);
 }
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled32(const lgx_gemm_tiled_args a) {
-    q8_tiled_body<1>(a);
+    q8_tiled_body<1>(a, blockIdx.x);
+}
+// Grouped tiled products (lgx_tiled_group_args): each matrix's workgroups
+// start at a multiple of 8, so the hardware XCD of a workgroup is its
+// within-matrix id's & 7, as the XCD-aware order assumes.
+template <int WM>
+__device__ __forceinline__ void q8_tiled_group_body(const lgx_tiled_group_args& a) {
+    const int bid = blockIdx.x;
+    int g = 0;
+    while (g + 1 < a.count && bid >= a.wg0[g + 1]) ++g;
+    const int P = bid - a.wg0[g];
+    const lgx_gemm_tiled_args& m = a.mat[g];
+    if (P >= m.ntn * m.ntm * m.ngroups) return;   // padding to a multiple of 8
+    q8_tiled_body<WM>(m, P);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled_group(const lgx_tiled_group_args a) {
+    q8_tiled_group_body<4>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled64_group(const lgx_tiled_group_args a) {
+    q8_tiled_group_body<2>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled32_group(const lgx_tiled_group_args a) {
+    q8_tiled_group_body<1>(a);
+}
+
+// Q8_0 of several activation matrices in one launch (lgx_quant_group_args):
+// 8 lanes per 32-block, the lgx_k_quantize_q8_0 rule (quantize4).
+extern "C" __global__ __launch_bounds__(256) void lgx_k_quantize_group(const lgx_quant_group_args a) {
+    const int64_t blk = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+    if (blk >= a.blk0[a.count]) return;           // whole 8-lane groups
+    int g = 0;
+    while (g + 1 < a.count && blk >= a.blk0[g + 1]) ++g;
+    const int k = a.k[g], nbk = k >> 5, j = threadIdx.x & 7;
+    const int64_t local = blk - a.blk0[g];
+    const int64_t row = local / nbk;
+    const int bl = (int)(local - row * nbk);
+    const float4 v = *(const float4*)(a.x[g] + row * k + bl * 32 + 4 * j);
+    const float f[4] = {v.x, v.y, v.z, v.w};
+    uint16_t dh;
+    const uint32_t qw = quantize4(f, dh);
+    *(uint32_t*)(a.xq[g] + xq_off(row, bl * 32 + 4 * j, k, a.t16 != 0)) = qw;
+    if (j == 0) a.xd[g][row * nbk + bl] = dh;
+}
+
+// Range / group trees of several products in one launch (lgx_combine_group_args).
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_combine_group(const lgx_combine_group_args a) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.el0[a.count]) return;
+    int g = 0;
+    while (g + 1 < a.count && i >= a.el0[g + 1]) ++g;
+    const int64_t cnt = a.el0[g + 1] - a.el0[g], e = i - a.el0[g];
+    float p[LGX_MAX_RANGES];
+#pragma unroll
+    for (int j = 0; j < LGX_MAX_RANGES; ++j) p[j] = j < a.nr[g] ? a.part[g][j * cnt + e] : 0.0f;
+    a.y[g][e] = tree_sum(p, a.nr[g]);
 }
 
 // ---------------------------------------------------------------------------

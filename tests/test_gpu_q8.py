@@ -21,6 +21,10 @@ def u16(t):
     return host(t).view(np.uint16)
 
 
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
 def config0(orc):
     qs, d = orc.gen_q8_matrix(0, 0, 4864, 896)
     x = orc.gen_normal_f32(0, 2, (896,))
@@ -411,3 +415,54 @@ def test_q8_gemm_7b_shapes_m64_streaming_and_tiled(ctx, orc, n, k):
         assert np.array_equal(y, ref), c is cs
         del W
     cs.close()
+
+
+@pytest.mark.parametrize("m", [2, 8, 17, 32, 33, 64, 100])
+def test_grouped_gemm_bit_exact(ctx, orc, m):
+    """lgx_q8_gemm_quantize_group: the quantisation of every activation
+    matrix, the products and the range trees of several matrices in three
+    launches (streaming 16-row kernels below 33 rows, tiled from 33), each
+    output bit-identical to the oracle's Q8_0 + canonical product: config 1's
+    gate / up / down, a single tile of one 64-column pair, a K of two ranges
+    (the second partial), a ragged last row tile."""
+    shapes = [(8960, 1536), (8960, 1536), (1536, 8960), (48, 64), (80, 1088)]
+    Ws, xs, refs = [], [], []
+    for i, (n, k) in enumerate(shapes):
+        qs, d = orc.gen_q8_matrix(7, 300 + i, n, k)
+        x = orc.gen_normal_f32(7, 400 + i + m, (m, k))
+        xq, xd = orc.quantize_q8_0(x)
+        Ws.append(ctx.q8_matrix(qs, d))
+        xs.append(ctx.to_device(x))
+        refs.append(orc.q8_gemm(qs, d, xq, xd))
+    before = ctx.launch_count
+    ys = ctx.q8_gemm_quantize_group(Ws, xs)
+    assert ctx.launch_count - before in (2, 3)
+    for i, (y, ref) in enumerate(zip(ys, refs)):
+        assert np.array_equal(bits(host(y)), bits(ref)), (m, shapes[i])
+    # a group of one and a repeat with other inputs (stale workspace)
+    y1 = ctx.q8_gemm_quantize_group([Ws[4]], [xs[4]])[0]
+    assert np.array_equal(bits(host(y1)), bits(refs[4]))
+    x2 = orc.gen_normal_f32(7, 999, (m, 1536))
+    xq2, xd2 = orc.quantize_q8_0(x2)
+    qs0, d0 = orc.gen_q8_matrix(7, 300, 8960, 1536)
+    y2 = ctx.q8_gemm_quantize_group([Ws[0]], [ctx.to_device(x2)])[0]
+    assert np.array_equal(bits(host(y2)), bits(orc.q8_gemm(qs0, d0, xq2, xd2)))
+
+
+def test_grouped_gemm_m1_and_errors(ctx, orc):
+    """m = 1 is the grouped GEMV; bad counts, row counts and shapes are
+    refused before anything runs."""
+    qs, d = orc.gen_q8_matrix(8, 1, 256, 512)
+    x = orc.gen_normal_f32(8, 2, (1, 512))
+    xq, xd = orc.quantize_q8_0(x)
+    W = ctx.q8_matrix(qs, d)
+    gx = ctx.to_device(x)
+    before = ctx.launch_count
+    y = ctx.q8_gemm_quantize_group([W], [gx])[0]
+    assert ctx.launch_count == before + 1
+    assert np.array_equal(bits(host(y)), bits(orc.q8_gemm(qs, d, xq, xd)))
+    with pytest.raises(lgx.LgxError) as e:
+        ctx.q8_gemm_quantize_group([W] * 9, [gx] * 9)
+    assert e.value.status_name == "LGX_OUT_OF_BOUNDS"
+    with pytest.raises(ValueError):
+        ctx.q8_gemm_quantize_group([W], [ctx.to_device(orc.gen_normal_f32(8, 3, (2, 256)))])
