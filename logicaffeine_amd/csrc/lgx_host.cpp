@@ -518,18 +518,20 @@ lgx_status lgx_q8_gemm_quantize_group(lgx_ctx* c, int32_t count, const lgx_q8_ma
         const bool tiled = m >= c->tiled_min;
         const Kern tk = tiled_kernel(c, m);
         const int trows = tk == K_GEMM_TILED ? 128 : tk == K_GEMM_TILED64 ? 64 : 32;
-        // ranges per group of the tiled products: from the tiles of all the
-        // matrices together (one launch fills the device)
+        // ranges per group of the tiled products: 2, or 1 when that leaves
+        // fewer than two workgroups per compute unit over all the matrices
+        // together.  Groups of 4 make the long-K matrix's workgroups the
+        // launch's tail (config 1 at M = 64: 41 us against 32 us per step)
         int grp = 1;
         if (tiled) {
             if (c->tiled_grp) {
                 grp = c->tiled_grp;
             } else {
-                for (grp = 4; grp > 1; grp >>= 1) {
+                for (grp = 2; grp > 1; grp >>= 1) {
                     int64_t wgs = 0;
                     for (int i = 0; i < count; ++i)
                         wgs += (int64_t)cdiv(W[i].n, LGX_TG_N) * cdiv(m, trows) * tiled_groups(W[i].k, grp);
-                    if (wgs >= 4LL * c->ncu) break;
+                    if (wgs >= 2LL * c->ncu) break;
                 }
             }
         }
@@ -607,6 +609,9 @@ lgx_status lgx_q8_gemm_quantize_group(lgx_ctx* c, int32_t count, const lgx_q8_ma
                                                    : K_GEMM_TILED32_GROUP;
             if ((st = launch(c, gk, dim3(ta.wg0[count]), dim3(256), ta, stream)) != LGX_OK) return st;
         } else {
+            // 16-row m-groups (several workgroups per weight tile, the
+            // later reads from L2), or 32 rows for 17..32 when forced
+            const int mrows = c->gemm_mt == 32 && m > 16 && m <= 32 ? 32 : 16;
             lgx_stream_group_args sa{};
             sa.count = count;
             sa.wg0[0] = 0;
@@ -623,7 +628,7 @@ lgx_status lgx_q8_gemm_quantize_group(lgx_ctx* c, int32_t count, const lgx_q8_ma
                 a.m = m;
                 a.ntiles = W[i].n / 16;
                 a.nranges = nranges_of(W[i].k);
-                a.nmgroups = (int)cdiv(m, 16);
+                a.nmgroups = (int)cdiv(m, mrows);
                 const int64_t tasks = (int64_t)a.ntiles * a.nranges * a.nmgroups;
                 const int64_t tpw = (tasks + 4LL * c->wg_target - 1) / (4LL * c->wg_target);
                 a.tpw = (int)(tpw < 1 ? 1 : tpw > 64 ? 64 : tpw);
@@ -632,8 +637,8 @@ lgx_status lgx_q8_gemm_quantize_group(lgx_ctx* c, int32_t count, const lgx_q8_ma
                 if (end > INT32_MAX) return fail(LGX_OUT_OF_BOUNDS, "grouped product too large");
                 sa.wg0[i + 1] = (int32_t)end;
             }
-            if ((st = launch(c, K_GEMM_MFMA16_GROUP, dim3(sa.wg0[count]), dim3(256), sa, stream)) !=
-                LGX_OK)
+            if ((st = launch(c, mrows == 32 ? K_GEMM_MFMA32_GROUP : K_GEMM_MFMA16_GROUP,
+                             dim3(sa.wg0[count]), dim3(256), sa, stream)) != LGX_OK)
                 return st;
         }
         // 3. the trees of the products with several ranges / groups

@@ -1213,12 +1213,19 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16_swiglu(co
 }
 // Grouped 16-row streaming products (lgx_stream_group_args): workgroup ->
 // (matrix, its own block coordinates).
-extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16_group(const lgx_stream_group_args a) {
+template <int MT>
+__device__ __forceinline__ void q8_stream_group_body(const lgx_stream_group_args& a) {
     const int bid = blockIdx.x;
     int g = 0;
     while (g + 1 < a.count && bid >= a.wg0[g + 1]) ++g;
     const int local = bid - a.wg0[g];
-    q8_stream_body<1, 4, 8>(a.mat[g], nullptr, local % a.gx[g], local / a.gx[g]);
+    q8_stream_body<MT, 4, 8>(a.mat[g], nullptr, local % a.gx[g], local / a.gx[g]);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16_group(const lgx_stream_group_args a) {
+    q8_stream_group_body<1>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma32_group(const lgx_stream_group_args a) {
+    q8_stream_group_body<2>(a);
 }
 
 // ---------------------------------------------------------------------------
