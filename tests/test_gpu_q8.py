@@ -417,11 +417,11 @@ def test_q8_gemm_7b_shapes_m64_streaming_and_tiled(ctx, orc, n, k):
     cs.close()
 
 
-@pytest.mark.parametrize("m", [2, 8, 17, 32, 33, 64, 100])
+@pytest.mark.parametrize("m", [2, 8, 16, 17, 32, 33, 64, 100])
 def test_grouped_gemm_bit_exact(ctx, orc, m):
     """lgx_q8_gemm_quantize_group: the quantisation of every activation
     matrix, the products and the range trees of several matrices in three
-    launches (streaming 16-row kernels below 33 rows, tiled from 33), each
+    launches (streaming 16-row kernels below 17 rows, tiled from 17), each
     output bit-identical to the oracle's Q8_0 + canonical product: config 1's
     gate / up / down, a single tile of one 64-column pair, a K of two ranges
     (the second partial), a ragged last row tile."""
