@@ -33,6 +33,17 @@ __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Raw buffer descriptors (stride 0, range checked in bytes): a load at or
+// past num_records returns zeros and touches no memory.  Word 3 is the gfx9
+// raw-buffer format (32-bit data format, no swizzle).
+#define LGX_BUF_DWORD3 0x00020000
+// The same non-temporal 128-bit load through a buffer descriptor (cache
+// policy 2: nt).
+__device__ __forceinline__ uint4 ld_buf_stream(__amdgpu_buffer_rsrc_t r, int off) {
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float h2f(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
@@ -719,11 +730,13 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemv_mfma_qx(const lg
 // the pairwise tree over the tile's ranges is applied in LDS -> y, or the
 // chains are stored as range partials.  Rows of more than W ranges take
 // several ranges per wave.
-// Each wave stages only its own range of the activation (Q8_0 of binary32
-// by the lgx_k_quantize_q8_0 rule, or a copy) in its own LDS slot, in (pair,
-// chunk) order: no workgroup barrier before the products, so every wave
-// starts as soon as its own data is in.  LDS (dynamic): W x (1 KiB quants +
-// 32 scales), then tpw x ranges x 16 chains.
+// The activation is staged in LDS as Q8_0 (of binary32 by the
+// lgx_k_quantize_q8_0 rule, or a copy) in (pair, chunk) order.  With several
+// tiles per workgroup, the tile-slot-0 wave of each range stages it once for
+// all of them (slot = range) behind one workgroup barrier, issued after
+// every wave's weight loads; with one tile per workgroup each wave stages
+// its own range in its own slot, with no barrier before the products.  LDS
+// (dynamic): W x (1 KiB quants + 32 scales), then tpw x ranges x 16 chains.
 // ---------------------------------------------------------------------------
 #define GRP_WIN 16
 #define GRP_XSLOT (1024 + 32 * 4)
@@ -807,50 +820,63 @@ __device__ __forceinline__ void grp_x_stage(const lgx_gemv_mat& a, const RangeIn
     }
 }
 
-// One wave's range: activation and scale loads, the first GRP_WIN weight
-// units, the activation staging, then per unit: the load GRP_WIN units
-// ahead, two MFMAs, the canonical chain step.
-template <bool XF>
-__device__ __forceinline__ float grp_range(const lgx_gemv_mat& a, int t, const RangeInfo& ri,
-                                           int lane, int8_t* xsw, float* dxw, bool emit) {
-    const int np = a.k >> 6, nh = s16_nhalf(a.k);
-    const int r = lane & 15, c = lane >> 4;
+// One wave's range, in two halves around the workgroup barrier of the
+// shared staging.  grp_issue: the activation loads (only in a wave that
+// stages the range), the scale loads and all GRP_WIN weight units, in that
+// issue order; grp_chain: per unit, two MFMAs and the canonical chain step
+// over the staged activation (quants xs, block scales dx).
+struct GrpRegs {
     uint4 xr[4];
     uint32_t xdr;
-    grp_x_load<XF>(a, ri, lane, xr, xdr);
     uint32_t dw[16];
+    uint4 w[16];
+};
+
+template <bool XF>
+__device__ __forceinline__ void grp_issue(const lgx_gemv_mat& a, int t, const RangeInfo& ri,
+                                          int lane, bool stage, GrpRegs& R) {
+    const int np = a.k >> 6, nh = s16_nhalf(a.k);
+    const int r = lane & 15;
+    if (stage) grp_x_load<XF>(a, ri, lane, R.xr, R.xdr);   // wave-uniform
     {
         uint32_t d0[8], d1[8];
         load_scales_half(a.wd, t, 2 * ri.g, nh, r, d0);
         load_scales_half(a.wd, t, min(2 * ri.g + 1, nh - 1), nh, r, d1);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            dw[i] = d0[i];
-            dw[8 + i] = d1[i];
+            R.dw[i] = d0[i];
+            R.dw[8 + i] = d1[i];
         }
     }
-    const uint4* wp = (const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64 + lane;
-    const int last = ri.npairs - 1;
-    uint4 w[16];
+    // the range's units through a buffer descriptor of npairs KiB: all 16
+    // loads are issued (the wait counts stay exact), and those past the
+    // range fall outside the descriptor, so they read zeros without any
+    // memory access
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const uint4*)a.wt + ((int64_t)t * np + ri.p0) * 64), 0, ri.npairs * 1024,
+        LGX_BUF_DWORD3);
 #pragma unroll
-    for (int i = 0; i < GRP_WIN; ++i) w[i] = ld_stream(wp + min(i, last) * 64);
+    for (int i = 0; i < GRP_WIN; ++i) R.w[i] = ld_buf_stream(wr, (i * 64 + lane) * 16);
     __builtin_amdgcn_sched_barrier(0);            // issue order: activation, scales, weights
-    grp_x_stage<XF>(a, ri, lane, xr, xdr, xsw, dxw, emit);
+}
+
+__device__ __forceinline__ float grp_chain(const RangeInfo& ri, int lane, const GrpRegs& R,
+                                           const int8_t* xs, const float* dx) {
+    const int c = lane >> 4;
     const v4i zero = {0, 0, 0, 0};
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         if (i < ri.npairs) {                       // wave-uniform
-            if (i + GRP_WIN < 16) w[i + GRP_WIN] = ld_stream(wp + min(i + GRP_WIN, last) * 64);
-            const uint4 xv = *(const uint4*)(xsw + (i * 4 + c) * 16);
+            const uint4 xv = *(const uint4*)(xs + (i * 4 + c) * 16);
             const long a0 = (long)(((uint64_t)xv.y << 32) | xv.x);
             const long a1 = (long)(((uint64_t)xv.w << 32) | xv.z);
-            const long b0 = (long)(((uint64_t)w[i].y << 32) | w[i].x);
-            const long b1 = (long)(((uint64_t)w[i].w << 32) | w[i].z);
+            const long b0 = (long)(((uint64_t)R.w[i].y << 32) | R.w[i].x);
+            const long b1 = (long)(((uint64_t)R.w[i].w << 32) | R.w[i].z);
             const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, zero, 0, 0, 0);
             const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, zero, 0, 0, 0);
-            const float e0 = h2f(dw[i] & 0xffffu) * dxw[2 * i];
-            const float e1 = h2f(dw[i] >> 16) * dxw[2 * i + 1];
+            const float e0 = h2f(R.dw[i] & 0xffffu) * dx[2 * i];
+            const float e1 = h2f(R.dw[i] >> 16) * dx[2 * i + 1];
             acc = fmaf((float)d0[0], e0, acc);
             acc = fmaf((float)d1[0], e1, acc);
         }
@@ -863,33 +889,109 @@ __device__ __forceinline__ float grp_range(const lgx_gemv_mat& a, int t, const R
     return acc;
 }
 
+// The fields of ga.mat[g] in two wide scalar loads issued together (one
+// round trip; field by field, the compiler waits on each load at its first
+// use).  The pointers go back to the global address space.
+__device__ __forceinline__ lgx_gemv_mat grp_mat(const lgx_gemv_group_args& ga, int g) {
+    static_assert(sizeof(lgx_gemv_mat) == 88, "lgx_gemv_mat layout");
+    typedef int v16i_t __attribute__((ext_vector_type(16)));
+    typedef int v8i_t __attribute__((ext_vector_type(8)));
+    // 64 + 32 bytes from the 88-byte record: the last 8 bytes read belong to
+    // the next record or to tile0, inside the argument block either way
+    const int* src = (const int*)&ga.mat[g];
+    const v16i_t lo = *(const v16i_t*)src;
+    const v8i_t hi = *(const v8i_t*)(src + 16);
+    asm volatile("" ::"s"(lo), "s"(hi));
+    auto p64 = [&](int i) {
+        const uint32_t l = (uint32_t)(i < 16 ? lo[i] : hi[i - 16]);
+        const uint32_t h = (uint32_t)(i + 1 < 16 ? lo[i + 1] : hi[i + 1 - 16]);
+        return ((uint64_t)h << 32) | l;
+    };
+#define LGX_GLOBAL_PTR(T, v) ((T*)(__attribute__((address_space(1))) T*)(v))
+    lgx_gemv_mat a;
+    a.wt = LGX_GLOBAL_PTR(const int8_t, p64(0));
+    a.wd = LGX_GLOBAL_PTR(const uint16_t, p64(2));
+    a.xf = LGX_GLOBAL_PTR(const float, p64(4));
+    a.xq = LGX_GLOBAL_PTR(const int8_t, p64(6));
+    a.xd = LGX_GLOBAL_PTR(const uint16_t, p64(8));
+    a.y = LGX_GLOBAL_PTR(float, p64(10));
+    a.xq_out = LGX_GLOBAL_PTR(int8_t, p64(12));
+    a.xd_out = LGX_GLOBAL_PTR(uint16_t, p64(14));
+    a.dbg = LGX_GLOBAL_PTR(int32_t, p64(16));
+#undef LGX_GLOBAL_PTR
+    a.n = hi[2];
+    a.k = hi[3];
+    a.part_out = hi[4];
+    a.pad = hi[5];
+    return a;
+}
+
 template <int W, bool XF>
 __device__ __forceinline__ void q8_gemv_grp_body(const lgx_gemv_group_args& ga) {
     extern __shared__ __align__(16) uint8_t lds_dyn[];
     const int bx = blockIdx.x;
-    int g = 0;
-#pragma unroll 1
-    while (g + 1 < ga.count && bx >= ga.tile0[g + 1]) ++g;
-    const lgx_gemv_mat& a = ga.mat[g];
+    // matrix of this workgroup and its first workgroup: tile0 ascends, so g
+    // counts the starts at or below bx (all read in one scalar round trip)
+    int g = 0, t0 = 0;
+#pragma unroll
+    for (int j = 1; j < LGX_GROUP_MAX; ++j) {
+        const bool in = j < ga.count && bx >= ga.tile0[j];
+        g += in ? 1 : 0;
+        t0 = in ? ga.tile0[j] : t0;
+    }
+    const lgx_gemv_mat a = grp_mat(ga, g);
     const int k = a.k, nb = k >> 5;
     const int nr = (nb + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS;
     const int nrs = min(nr, W);
-    const int tpw = a.pad > 0 ? a.pad : W / nrs;
+    const int tpw = a.pad;                                // >= 1, set by the launcher
     const int ntiles = a.n >> 4;
-    const int tile_base = (bx - ga.tile0[g]) * tpw;
+    const int tile_base = (bx - t0) * tpw;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    int8_t* xsw = (int8_t*)lds_dyn + wave * GRP_XSLOT;   // this wave's activation slot
-    float* dxw = (float*)(xsw + 1024);
     float* ps = (float*)(lds_dyn + W * GRP_XSLOT);        // [tpw][nr][16]
-    const int ts = wave / nrs, rg = wave - ts * nrs;
+    // wave / nrs without an integer division: wave < 16 and nrs <= 16, so
+    // (wave + 1/2) / nrs stays at least 1/32 away from an integer, far more
+    // than the error of the reciprocal
+    const int ts = __builtin_amdgcn_readfirstlane(
+        (int)(((float)wave + 0.5f) * __builtin_amdgcn_rcpf((float)nrs)));
+    const int rg = wave - ts * nrs;
     const int t = tile_base + ts;
     const bool on = ts < tpw && t < ntiles;
-    const bool emit = bx == ga.tile0[g] && ts == 0;       // one wave per range writes Q8_0(x)
-    if (on) {
+    const bool emit = bx == t0 && ts == 0;                // one wave per range writes Q8_0(x)
+    if (tpw > 1) {
+        // several tiles per workgroup (so at most W / 2 ranges per row, one
+        // per wave): the tile-slot-0 wave of each range stages it once, in
+        // slot rg, for every tile of the workgroup
+        const RangeInfo ri = range_info(rg, k);
+        int8_t* xs = (int8_t*)lds_dyn + rg * GRP_XSLOT;
+        float* dx = (float*)(xs + 1024);
+        GrpRegs R;
+        if (on) {
+            grp_issue<XF>(a, t, ri, lane, ts == 0, R);
+            if (ts == 0) grp_x_stage<XF>(a, ri, lane, R.xr, R.xdr, xs, dx, emit);
+        }
+        __syncthreads();
+        if (on) {
+            const float acc = grp_chain(ri, lane, R, xs, dx);
+            if (lane < 16) {
+                if (a.part_out)
+                    a.y[(int64_t)rg * a.n + t * 16 + lane] = acc;
+                else
+                    ps[(ts * nr + rg) * 16 + lane] = acc;
+            }
+        }
+    } else if (on) {
+        // one tile per workgroup: each wave stages its own range in its own
+        // slot (no barrier before the products); rows of more than W ranges
+        // take several ranges per wave
+        int8_t* xs = (int8_t*)lds_dyn + wave * GRP_XSLOT;
+        float* dx = (float*)(xs + 1024);
 #pragma unroll 1
-        for (int rg2 = rg; rg2 < nr; rg2 += W) {           // rows of more than W ranges
+        for (int rg2 = rg; rg2 < nr; rg2 += W) {
             const RangeInfo ri = range_info(rg2, k);
-            const float acc = grp_range<XF>(a, t, ri, lane, xsw, dxw, emit);
+            GrpRegs R;
+            grp_issue<XF>(a, t, ri, lane, true, R);
+            grp_x_stage<XF>(a, ri, lane, R.xr, R.xdr, xs, dx, emit);
+            const float acc = grp_chain(ri, lane, R, xs, dx);
             if (lane < 16) {
                 if (a.part_out)
                     a.y[(int64_t)rg2 * a.n + t * 16 + lane] = acc;
