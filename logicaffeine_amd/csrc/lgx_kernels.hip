@@ -201,6 +201,38 @@ __device__ __forceinline__ float tree_sum(float (&p)[LGX_MAX_RANGES], int g) {
     }
     return p[0];
 }
+template <int R>
+__device__ __forceinline__ float tree_sum_r(float (&p)[R], int g) {
+#pragma unroll
+    for (int s = 1; s < R; s <<= 1) {
+#pragma unroll
+        for (int i = 0; i + s < R; i += 2 * s)
+            if (i + s < g) p[i] = p[i] + p[i + s];
+    }
+    return p[0];
+}
+
+// The same tree over the nr (1 <= nr <= LGX_MAX_RANGES, wave-uniform)
+// values get(0), ..., get(nr - 1), over the smallest power-of-two width R
+// that holds them.  The R reads are unconditional, at indices clamped to
+// nr - 1 (the extra values never enter the sum): reads under per-index
+// branches would each wait at their join.
+template <int R, class F>
+__device__ __forceinline__ float tree_read_r(int nr, F get) {
+    float p[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) p[j] = get(min(j, nr - 1));
+    return tree_sum_r<R>(p, nr);
+}
+template <class F>
+__device__ __forceinline__ float tree_read(int nr, F get) {
+    static_assert(LGX_MAX_RANGES == 32, "tree_read widths");
+    if (nr <= 2) return tree_read_r<2>(nr, get);
+    if (nr <= 4) return tree_read_r<4>(nr, get);
+    if (nr <= 8) return tree_read_r<8>(nr, get);
+    if (nr <= 16) return tree_read_r<16>(nr, get);
+    return tree_read_r<32>(nr, get);
+}
 
 // Exact int32 sum of the four k-chunk partials of two blocks.  Lane l = r+16c
 // holds s0 (block 2p) and s1 (block 2p+1) for its chunk c.  Two VALU lane
@@ -545,10 +577,7 @@ __device__ __forceinline__ void q8_gemv_wg_body(const lgx_gemv_group_args& ga) {
         const int qt = tid >> 4, qr = tid & 15;
         const int tq = tile_base + qt;
         if (tq < ntiles) {
-            float p[LGX_MAX_RANGES];
-#pragma unroll
-            for (int j = 0; j < LGX_MAX_RANGES; ++j) p[j] = j < nr ? ps[(qt * nr + j) * 16 + qr] : 0.0f;
-            a.y[tq * 16 + qr] = tree_sum(p, nr);
+            a.y[tq * 16 + qr] = tree_read(nr, [&](int j) { return ps[(qt * nr + j) * 16 + qr]; });
         }
     }
 }
@@ -1005,10 +1034,8 @@ __device__ __forceinline__ void q8_gemv_grp_body(const lgx_gemv_group_args& ga) 
     if (tid < tpw * 16) {
         const int qt = tid >> 4, qr = tid & 15;
         if (tile_base + qt < ntiles) {
-            float p[LGX_MAX_RANGES];
-#pragma unroll
-            for (int j = 0; j < LGX_MAX_RANGES; ++j) p[j] = j < nr ? ps[(qt * nr + j) * 16 + qr] : 0.0f;
-            a.y[(tile_base + qt) * 16 + qr] = tree_sum(p, nr);
+            a.y[(tile_base + qt) * 16 + qr] =
+                tree_read(nr, [&](int j) { return ps[(qt * nr + j) * 16 + qr]; });
         }
     }
 }
@@ -1336,10 +1363,7 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma32_group(con
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_combine(const lgx_combine_args a) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= a.count) return;
-    float p[LGX_MAX_RANGES];
-#pragma unroll
-    for (int j = 0; j < LGX_MAX_RANGES; ++j) p[j] = j < a.nranges ? a.part[j * a.count + i] : 0.0f;
-    a.y[i] = tree_sum(p, a.nranges);
+    a.y[i] = tree_read(a.nranges, [&](int j) { return a.part[j * a.count + i]; });
 }
 
 // ---------------------------------------------------------------------------
@@ -1852,10 +1876,7 @@ __device__ __forceinline__ float lgx_silu(float g) {
 // tree over nr partials of element i (stride = elements per partial)
 __device__ __forceinline__ float tree_partials(const float* part, int nr, int64_t stride,
                                                int64_t i) {
-    float p[LGX_MAX_RANGES];
-#pragma unroll
-    for (int j = 0; j < LGX_MAX_RANGES; ++j) p[j] = j < nr ? part[j * stride + i] : 0.0f;
-    return tree_sum(p, nr);
+    return tree_read(nr, [&](int j) { return part[j * stride + i]; });
 }
 
 // Byte offset of element (row m, column i) of an m x k int8 activation held
@@ -1889,16 +1910,6 @@ __device__ __forceinline__ void quantize_row_from_lds(const float* row, int n, i
 
 // Canonical tree over the nr (<= R) range partials of NE elements i0,
 // i0 + di, ... of one thread, with every load issued before the first add.
-template <int R>
-__device__ __forceinline__ float tree_sum_r(float (&p)[R], int g) {
-#pragma unroll
-    for (int s = 1; s < R; s <<= 1) {
-#pragma unroll
-        for (int i = 0; i + s < R; i += 2 * s)
-            if (i + s < g) p[i] = p[i] + p[i + s];
-    }
-    return p[0];
-}
 template <int NE, int R>
 __device__ __forceinline__ void tree_partials_n(const float* part, int nr, int64_t stride,
                                                 int64_t i0, int64_t di, const bool (&on)[NE],
@@ -3116,10 +3127,8 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_combine_group(const l
     int g = 0;
     while (g + 1 < a.count && i >= a.el0[g + 1]) ++g;
     const int64_t cnt = a.el0[g + 1] - a.el0[g], e = i - a.el0[g];
-    float p[LGX_MAX_RANGES];
-#pragma unroll
-    for (int j = 0; j < LGX_MAX_RANGES; ++j) p[j] = j < a.nr[g] ? a.part[g][j * cnt + e] : 0.0f;
-    a.y[g][e] = tree_sum(p, a.nr[g]);
+    const float* pg = a.part[g];
+    a.y[g][e] = tree_read(a.nr[g], [&](int j) { return pg[j * cnt + e]; });
 }
 
 // ---------------------------------------------------------------------------
