@@ -1908,20 +1908,43 @@ __device__ __forceinline__ void quantize_row_from_lds(const float* row, int n, i
     }
 }
 
-// Canonical tree over the nr (<= R) range partials of NE elements i0,
-// i0 + di, ... of one thread, with every load issued before the first add.
+// Canonical tree over the nr (1 <= nr <= R, wave-uniform) range partials of
+// NE elements i0, i0 + di, ... of one thread (0 where on[e] is false), with
+// every load issued before the first add.  The loads are unconditional over
+// the smallest power-of-two width W >= nr: partial indices clamped to
+// nr - 1, and an element that is off reads element 0 (always present) and
+// is dropped at the end; loads under per-element branches would each wait
+// at their join.
+template <int NE, int W>
+__device__ __forceinline__ void tree_partials_w(const float* part, int nr, int64_t stride,
+                                                int64_t i0, int64_t di, const bool (&on)[NE],
+                                                float (&out)[NE]) {
+    float p[NE][W];
+#pragma unroll
+    for (int j = 0; j < W; ++j)
+#pragma unroll
+        for (int e = 0; e < NE; ++e)
+            p[e][j] = part[min(j, nr - 1) * stride + (on[e] ? i0 + e * di : 0)];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) out[e] = on[e] ? tree_sum_r<W>(p[e], nr) : 0.0f;
+}
 template <int NE, int R>
 __device__ __forceinline__ void tree_partials_n(const float* part, int nr, int64_t stride,
                                                 int64_t i0, int64_t di, const bool (&on)[NE],
                                                 float (&out)[NE]) {
-    float p[NE][R];
-#pragma unroll
-    for (int j = 0; j < R; ++j)
-#pragma unroll
-        for (int e = 0; e < NE; ++e)
-            p[e][j] = (j < nr && on[e]) ? part[j * stride + i0 + e * di] : 0.0f;
-#pragma unroll
-    for (int e = 0; e < NE; ++e) out[e] = tree_sum_r<R>(p[e], nr);
+    static_assert(R == 8 || R == 32, "tree_partials_n widths");
+    if (nr <= 1)
+        tree_partials_w<NE, 1>(part, nr, stride, i0, di, on, out);
+    else if (nr <= 2)
+        tree_partials_w<NE, 2>(part, nr, stride, i0, di, on, out);
+    else if (nr <= 4)
+        tree_partials_w<NE, 4>(part, nr, stride, i0, di, on, out);
+    else if (R == 8 || nr <= 8)
+        tree_partials_w<NE, 8>(part, nr, stride, i0, di, on, out);
+    else if (nr <= 16)
+        tree_partials_w<NE, (R > 16 ? 16 : R)>(part, nr, stride, i0, di, on, out);
+    else
+        tree_partials_w<NE, R>(part, nr, stride, i0, di, on, out);
 }
 
 extern "C" __global__ __launch_bounds__(256) void lgx_k_embed(const lgx_embed_args a) {
@@ -2131,8 +2154,7 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_add_rmsnorm_quant_w(cons
         for (int j = 0; j < R; ++j)
 #pragma unroll
             for (int k = 0; k < KS; ++k)
-                pv[k][j] = j < a.nr ? pb[j * stride + min(lane + 64 * k, n4 - 1)]
-                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                pv[k][j] = pb[min(j, a.nr - 1) * stride + min(lane + 64 * k, n4 - 1)];
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
             float px[R], py[R], pz[R], pw[R];
