@@ -276,6 +276,29 @@ lgx_status lgx_f16_repack_t64(lgx_ctx* ctx, const uint16_t* src, int32_t rows, i
  * scalar cache.  h % 64 == 0, h <= 1024, m <= 64. */
 lgx_status lgx_lm_head_f16_t64(lgx_ctx* ctx, const float* x, const uint16_t* emb_t64, int32_t m,
                                int32_t h, int32_t vocab, float* logits, void* stream);
+/* Per-row constants of a binary16 embedding [vocab][h] for
+ * lgx_lm_head_argmax_f16: rowc[v] = (upper bound of sum_k |emb[v][k]|, upper
+ * bound of the same sum over its subnormal entries), +inf in both for a row
+ * with a non-finite entry; rowc holds 2 * vocab floats.  h <= 1024.
+ * No counterpart in the reference: the precomputation of the certified
+ * greedy lm_head below. */
+lgx_status lgx_lm_head_rowconst(lgx_ctx* ctx, const uint16_t* emb, int32_t vocab, int32_t h,
+                                float* rowc, void* stream);
+/* out[i] = lgx_argmax of row i of lgx_lm_head_f16(x, emb) -- the same token,
+ * bit for bit -- without the full logits: binary16 MFMA logits with a
+ * rigorous error bound per (row, vocabulary row), then the exact chain only
+ * for the vocabulary rows whose bound reaches the largest lower bound (all
+ * rows of a slice with more than 8 of them, all rows of an x row that is not
+ * finite or outside [2^-60, 2^60] in magnitude).  emb: row-major [vocab][h];
+ * emb_t64 its lgx_f16_repack_t64 form; rowc from lgx_lm_head_rowconst.
+ * bounds (nullable, [m][vocab][2]): the scaled approximation and its bound,
+ * for verification.  m <= 32, h % 64 == 0, h <= 1024, vocab <= 655360.
+ * No counterpart in the reference: the same pick as lgx_lm_head_f16 followed
+ * by lgx_argmax, for greedy decode of a tied-embedding model. */
+lgx_status lgx_lm_head_argmax_f16(lgx_ctx* ctx, const float* x, const uint16_t* emb,
+                                  const uint16_t* emb_t64, const float* rowc, int32_t m,
+                                  int32_t h, int32_t vocab, int32_t* out, float* bounds,
+                                  void* stream);
 /* out[i] = first index of the maximum of logits[i][:], NaN skipped (all NaN
  * gives 0); -0 and +0 compare equal. */
 lgx_status lgx_argmax(lgx_ctx* ctx, const float* logits, int32_t m, int32_t vocab, int32_t* out,

@@ -78,6 +78,8 @@ SIGNATURES = {
     "lgx_f16_t64_count": (C.c_int64, [_I32, _I32]),
     "lgx_f16_repack_t64": (C.c_int, [_P, _P, _I32, _I32, _P, _P]),
     "lgx_lm_head_f16_t64": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _P, _P]),
+    "lgx_lm_head_rowconst": (C.c_int, [_P, _P, _I32, _I32, _P, _P]),
+    "lgx_lm_head_argmax_f16": (C.c_int, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P]),
     "lgx_argmax": (C.c_int, [_P, _P, _I32, _I32, _P, _P]),
     "lgx_sample": (C.c_int, [_P, _P, _I32, _I32, _I32, C.c_float, C.c_float, C.c_uint64, _P, _P,
                              _P]),
@@ -558,6 +560,31 @@ class Context:
         _check(lib().lgx_lm_head_f16_t64(self.handle, x.data_ptr(), emb_t64.data_ptr(), m, h,
                                          vocab, out.data_ptr(), self._s()))
         return out
+
+    def lm_head_rowconst(self, emb):
+        """Per-row constants of a binary16 embedding (int16 bits [vocab][h]) for
+        lm_head_argmax_f16: float32 [vocab][2]."""
+        t = self.torch
+        vocab, h = emb.shape
+        out = t.empty((vocab, 2), dtype=t.float32, device=self.dev)
+        _check(lib().lgx_lm_head_rowconst(self.handle, emb.data_ptr(), vocab, h, out.data_ptr(),
+                                          self._s()))
+        return out
+
+    def lm_head_argmax_f16(self, x, emb, emb_t64, rowc, out=None, bounds: bool = False):
+        """Certified greedy token of the tied lm_head (the token of
+        argmax(lm_head_f16(x, emb))); with bounds=True also the [m][vocab][2]
+        scaled approximations and their bounds."""
+        t = self.torch
+        m, h = x.shape
+        vocab = emb.shape[0]
+        out = t.empty(m, dtype=t.int32, device=self.dev) if out is None else out
+        bd = t.empty((m, vocab, 2), dtype=t.float32, device=self.dev) if bounds else None
+        _check(lib().lgx_lm_head_argmax_f16(self.handle, x.data_ptr(), emb.data_ptr(),
+                                            emb_t64.data_ptr(), rowc.data_ptr(), m, h, vocab,
+                                            out.data_ptr(), bd.data_ptr() if bd is not None else None,
+                                            self._s()))
+        return (out, bd) if bounds else out
 
     def argmax(self, logits, out=None):
         t = self.torch

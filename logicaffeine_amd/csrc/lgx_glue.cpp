@@ -215,6 +215,39 @@ lgx_status lgx_argmax(lgx_ctx* c, const float* logits, int32_t m, int32_t vocab,
     });
 }
 
+lgx_status lgx_lm_head_rowconst(lgx_ctx* c, const uint16_t* emb, int32_t vocab, int32_t h,
+                                float* rowc, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!emb || !rowc) return fail(LGX_NULL_POINTER, "NULL tensor");
+        if (vocab <= 0 || h <= 0 || h > LGX_LMC_MAXH)
+            return fail(LGX_INVALID_ARGUMENT, "vocab %d, h %d (h <= %d)", vocab, h, LGX_LMC_MAXH);
+        return launch_lm_rowconst(c, emb, vocab, h, rowc, stream);
+    });
+}
+
+lgx_status lgx_lm_head_argmax_f16(lgx_ctx* c, const float* x, const uint16_t* emb,
+                                  const uint16_t* emb_t64, const float* rowc, int32_t m,
+                                  int32_t h, int32_t vocab, int32_t* out, float* bounds,
+                                  void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!x || !emb || !emb_t64 || !rowc || !out) return fail(LGX_NULL_POINTER, "NULL tensor");
+        if (m <= 0 || m > LGX_LMC_MAXB || vocab <= 0 || h <= 0 || h % 64 || h > LGX_LMC_MAXH ||
+            lm_cert_slices(vocab) > 1024)
+            return fail(LGX_UNSUPPORTED, "m %d (<= %d), vocab %d (<= 655360), h %d (h %% 64 == 0, h <= %d)",
+                        m, LGX_LMC_MAXB, vocab, h, LGX_LMC_MAXH);
+        float* ws = nullptr;
+        if ((st = ensure_ws(c, (size_t)m * lm_cert_slices(vocab) * sizeof(lgx_lmc_summary), &ws)) !=
+            LGX_OK)
+            return st;
+        return launch_lm_cert(c, x, emb, emb_t64, rowc, m, h, vocab, (lgx_lmc_summary*)ws, bounds,
+                              out, nullptr, 0, stream);
+    });
+}
+
 lgx_status lgx_sample(lgx_ctx* c, const float* logits, int32_t m, int32_t vocab, int32_t top_k,
                       float top_p, float temperature, uint64_t seed, const int32_t* positions,
                       int32_t* out, void* stream) {

@@ -131,6 +131,9 @@ enum Kern {
     K_GEMM_TILED32_GROUP,
     K_QUANT_GROUP,
     K_COMBINE_GROUP,
+    K_LM_ROWCONST,
+    K_LM_CERT,
+    K_LM_PICK,
     K_COUNT
 };
 inline const char* const kKernelNames[] = {
@@ -164,6 +167,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_q8_gemm_mfma16_qkv", "lgx_k_q8_gemm_mfma16_swiglu", "lgx_k_add_rmsnorm_quant_w",
     "lgx_k_q8_gemm_mfma16_group", "lgx_k_q8_gemm_mfma32_group", "lgx_k_q8_gemm_tiled_group", "lgx_k_q8_gemm_tiled64_group",
     "lgx_k_q8_gemm_tiled32_group", "lgx_k_quantize_group", "lgx_k_q8_combine_group",
+    "lgx_k_lm_rowconst", "lgx_k_lm_cert", "lgx_k_lm_pick",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -209,6 +213,7 @@ struct lgx_ctx {
     bool decode_fuse = true;      // LGX_DECODE_FUSE=0: decode glue in kernels of its own
     int fuse_cols32 = 1;          // LGX_FUSE_SWIGLU_COLS: SwiGLU columns per fused workgroup / 32
     int norm_waves = 1;           // LGX_NORM_WAVES: rows (waves) per workgroup of the wave norm (0: off)
+    bool lm_cert = true;          // LGX_LM_CERT=0: greedy tied lm_head through the full logits
     bool prefill_serial = false;  // LGX_PREFILL=serial: prefill as P decode passes
     int prefill_chunk = 0;        // LGX_PREFILL_CHUNK: positions per prefill chunk (0: by batch)
     int ncu = 256;                // compute units of the device
@@ -325,6 +330,28 @@ inline lgx_status launch_norm(lgx_ctx* c, const lgx_norm_args& a, void* stream) 
     return launch(c, K_ADD_RMSNORM_QUANT, dim3(a.m), dim3(LGX_GLUE_NT), a, stream, 0u);
 }
 inline int argmax_slices(int vocab) { return (vocab + LGX_ARGMAX_SLICE - 1) / LGX_ARGMAX_SLICE; }
+
+// Certified greedy token of a tied binary16 lm_head (m <= LGX_LMC_MAXB rows
+// of x [m][h], h % 64 == 0, h <= LGX_LMC_MAXH): summaries of the slices
+// into summ (m * lm_cert_slices(vocab) records), then the per-row pick
+// (+ seq_len advance).
+inline int lm_cert_slices(int vocab) { return cdiv(cdiv(vocab, 64), LGX_LMC_GROUPS); }
+inline lgx_status launch_lm_cert(lgx_ctx* c, const float* x, const uint16_t* emb,
+                                 const uint16_t* emb_t64, const float* rowc, int m, int h,
+                                 int vocab, lgx_lmc_summary* summ, float* dbg, int32_t* tokens,
+                                 int32_t* seq_len, int advance, void* stream) {
+    const int ns = lm_cert_slices(vocab);
+    lgx_lmc_args a{x, emb_t64, rowc, summ, dbg, m, h, vocab, ns};
+    lgx_status st = launch(c, K_LM_CERT, dim3(ns), dim3(64 * LGX_LMC_GROUPS), a, stream);
+    if (st != LGX_OK) return st;
+    lgx_lmp_args p{x, emb, summ, tokens, seq_len, m, h, vocab, ns, advance};
+    return launch(c, K_LM_PICK, dim3(m), dim3(256), p, stream);
+}
+inline lgx_status launch_lm_rowconst(lgx_ctx* c, const uint16_t* emb, int vocab, int h,
+                                     float* rowc, void* stream) {
+    lgx_lmrc_args a{emb, rowc, vocab, h};
+    return launch(c, K_LM_ROWCONST, dim3(cdiv(vocab, 4)), dim3(256), a, stream);
+}
 
 // Greedy token of m rows of (range-partial) logits: candidates per slice,
 // then the per-row pick (+ seq_len advance).  cand holds m * slices floats

@@ -205,6 +205,49 @@ typedef struct {
     int32_t rows, h;
 } lgx_t64_args;
 
+// Certified greedy token of a tied binary16 lm_head (lgx_k_lm_cert, then
+// lgx_k_lm_pick).  Per (row b, slice of LGX_LMC_ROWS vocabulary rows) the
+// first kernel leaves a summary: L, the largest lower bound of a scaled
+// logit in the slice; Umax, the largest upper bound; cnt, the number of rows
+// whose upper bound reaches L (their bounds and indices in U/v when cnt <=
+// LGX_LMC_CAND; LGX_LMC_EXACT when row b needs exact chains everywhere).
+#define LGX_LMC_GROUPS 10                      // 64-row groups (waves) per workgroup
+#define LGX_LMC_ROWS (64 * LGX_LMC_GROUPS)      // vocabulary rows per slice
+#define LGX_LMC_MAXB 32
+#define LGX_LMC_MAXH 1024
+#define LGX_LMC_CAND 8
+#define LGX_LMC_EXACT 0x7fffffff
+typedef struct {
+    float L, Umax;
+    int32_t cnt, pad;
+    float U[LGX_LMC_CAND];
+    int32_t v[LGX_LMC_CAND];
+} lgx_lmc_summary;
+typedef struct {
+    const float* x;            // [m][h] binary32 rows
+    const uint16_t* emb_t64;   // the binary16 embedding in T64 order
+    const float* rowc;         // [vocab][2] (lgx_k_lm_rowconst)
+    lgx_lmc_summary* summ;     // [m][nslices]
+    float* dbg;                // nullable: [m][vocab][2] scaled approximation, bound
+    int32_t m, h, vocab, nslices;
+} lgx_lmc_args;
+typedef struct {
+    const float* x;            // [m][h]
+    const uint16_t* emb;       // [vocab][h] row-major binary16
+    const lgx_lmc_summary* summ;
+    int32_t* tokens;           // [m]
+    int32_t* seq_len;          // nullable: += advance
+    int32_t m, h, vocab, nslices, advance;
+} lgx_lmp_args;
+// Per-row constants of a binary16 embedding: rowc[v] = (upper bound of
+// sum_k |e[v][k]|, upper bound of the same sum over the subnormal entries);
+// +inf in both when the row has a non-finite entry.
+typedef struct {
+    const uint16_t* emb;       // [vocab][h]
+    float* rowc;               // [vocab][2]
+    int32_t vocab, h;
+} lgx_lmrc_args;
+
 // next[b] = first index of the max of tree(part[.][b][:]) (NaN skipped);
 // then tokens[b] = next[b] and seq_len[b] += advance.  Two launches through
 // per-slice candidates cand_v/cand_i [m][nslices].

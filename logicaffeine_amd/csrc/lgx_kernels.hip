@@ -2665,6 +2665,402 @@ extern "C" __global__ __launch_bounds__(64) void lgx_k_argmax_final(const lgx_ar
 }
 
 // ---------------------------------------------------------------------------
+// Certified greedy token of a tied binary16 lm_head: the token of lgx_argmax
+// over the canonical logits z[b][v] (sequential fmaf chain over k of
+// x[b][k] * e[v][k]) without computing every chain.
+//
+// lgx_k_lm_cert (workgroup = slice of LGX_LMC_GROUPS 64-row groups, one wave
+// per group): row b of x is scaled by s = 2^p (max |x| s in [2^14, 2^15)),
+// y = x s, split as y ~ h + l with h = f16(y), l = f16(y - h); binary16
+// MFMAs (f32 accumulation) give T = sum_k (h + l) e and A = sum_k |h| |e|
+// per (v, b).  With S = sum_k |e| and D = the same sum over subnormal e
+// (per row, lgx_k_lm_rowconst), |s z - T| <= eps = CA A + CS S + CD D,
+// taking: the chain's own rounding (gamma_H <= 1024 u / (1 - 1024 u)), the
+// split's residual |y - h - l| <= 2^-22 |h| + 2^-24, binary16 inputs
+// flushed to zero or not (2^-14 per flushed input, the subnormal e part
+// through D with |h| <= 2^15), and an MFMA accumulation error of at most
+// 2^-9 of the sum of the absolute terms (the sequential round-to-nearest
+// bound for 2048 terms is 2^-13).  eps is then widened for the binary32
+// arithmetic of the bound itself.  The summary of (b, slice): the largest
+// lower bound L = T - eps, the largest upper bound U = T + eps, and the
+// rows whose U reaches L.
+//
+// lgx_k_lm_pick (workgroup = row b): L(b) = max over slices; a row v can be
+// the first maximum only if U(v) >= L(b) (otherwise s z_v <= U(v) < L(v')
+// <= s z_v' for some v').  Those rows get the exact chain (rows of a slice
+// holding more than LGX_LMC_CAND of them, or of a row b whose x is not
+// finite or outside [2^-60, 2^60] in magnitude: every row of the slice, or
+// of the vocabulary); the token is the first maximum of the exact values
+// (NaN skipped, none gives 0), then seq_len[b] += advance.
+// ---------------------------------------------------------------------------
+// binary16 per staged row: h columns, zeros up to the last column of the
+// up-to-two k-steps past h that the 3-slot ring runs, and 8 of bank spread
+#define LGX_LMC_XS (LGX_LMC_MAXH + 64 + 8)
+#define LGX_LMC_CA 2.02e-3f
+#define LGX_LMC_CS 2.45e-4f
+#define LGX_LMC_CD 32900.0f
+
+// Upper bounds of sum |e| and of its subnormal part per row (exact fp64
+// sums: binary16 magnitudes are multiples of 2^-24 below 2^16, so 1024 of
+// them sum exactly in 53 bits), rounded up to binary32; +inf for a row with
+// a non-finite entry.  One wave per row.
+__device__ __forceinline__ float f64_to_f32_up(double d) {
+    float f = (float)d;
+    if ((double)f < d) f = __uint_as_float(__float_as_uint(f) + 1u);   // d >= 0
+    return f;
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_lm_rowconst(const lgx_lmrc_args a) {
+    const int lane = threadIdx.x & 63;
+    const int v = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (v >= a.vocab) return;                   // whole waves; no barrier below
+    const uint16_t* er = a.emb + (int64_t)v * a.h;
+    double s = 0.0, d = 0.0;
+    int bad = 0;
+    for (int k = lane; k < a.h; k += 64) {
+        const uint32_t mag = er[k] & 0x7fffu;
+        bad |= mag >= 0x7c00u ? 1 : 0;
+        const double f = (double)h2f(mag);
+        s += f;
+        if (mag < 0x0400u) d += f;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        s += __shfl_xor(s, o, 64);
+        d += __shfl_xor(d, o, 64);
+        bad |= __shfl_xor(bad, o, 64);
+    }
+    if (lane == 0) {
+        const float inf = __builtin_inff();
+        ((float2*)a.rowc)[v] = bad ? make_float2(inf, inf) : make_float2(f64_to_f32_up(s), f64_to_f32_up(d));
+    }
+}
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ v8h as_v8h(uint4 u) { return __builtin_bit_cast(v8h, u); }
+__device__ __forceinline__ uint4 abs_h8(uint4 u) {
+    return make_uint4(u.x & 0x7fff7fffu, u.y & 0x7fff7fffu, u.z & 0x7fff7fffu, u.w & 0x7fff7fffu);
+}
+
+extern "C" __global__ __launch_bounds__(64 * LGX_LMC_GROUPS) void lgx_k_lm_cert(const lgx_lmc_args a) {
+    // rows of the scaled, split x (binary16 bits), [b][k] with a padded row
+    // stride: an MFMA B operand (16 rows x 8 columns) is one conflict-free read
+    __shared__ __align__(16) uint16_t xh[LGX_LMC_MAXB * LGX_LMC_XS];
+    __shared__ __align__(16) uint16_t xl[LGX_LMC_MAXB * LGX_LMC_XS];
+    __shared__ float2 rc[LGX_LMC_GROUPS][64];
+    __shared__ float lmx[LGX_LMC_GROUPS][LGX_LMC_MAXB], umx[LGX_LMC_GROUPS][LGX_LMC_MAXB];
+    __shared__ float lwg[LGX_LMC_MAXB], uwg[LGX_LMC_MAXB];
+    __shared__ int ccnt[LGX_LMC_MAXB], rexact[LGX_LMC_MAXB];
+    __shared__ float cu[LGX_LMC_MAXB][LGX_LMC_CAND];
+    __shared__ int cv[LGX_LMC_MAXB][LGX_LMC_CAND];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, c = lane >> 4;
+    const int ngroups = (a.vocab + 63) >> 6;
+    const int g = blockIdx.x * LGX_LMC_GROUPS + w;
+    const bool gon = g < ngroups;                          // wave-uniform
+    const int ncg = a.h >> 3, ns = a.h >> 5;
+    // the group's T64 units (ncg KiB); k-step s, q-block q of lane (r, c):
+    // unit 4s + c, position 16q + r (row 16q + r, columns 32s + 8c ..).
+    // Past the group (and for a wave without a group) the loads fall outside
+    // the descriptor: zeros, no memory access.
+    const __amdgpu_buffer_rsrc_t er = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.emb_t64 + (int64_t)min(g, ngroups - 1) * ncg * 512), 0, gon ? ncg * 1024 : 0,
+        LGX_BUF_DWORD3);
+    // k-steps in flight: a ring of three (the step in use and two ahead)
+    uint4 wa[3][4];
+    auto ld = [&](int s, uint4 (&dst)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dst[q] = ld_buf_stream(er, ((4 * s + c) * 64 + 16 * q + r) * 16);
+    };
+    ld(0, wa[0]);
+    ld(1, wa[1]);
+    // per-row constants of the group's rows
+    {
+        const int v = min(64 * g + lane, a.vocab - 1);
+        const float2 q = ((const float2*)a.rowc)[v];
+        rc[w][lane] = q;
+    }
+    // stage x: wave w takes rows w, w + GROUPS, ...; lane holds columns
+    // 8(lane + 64 i) .. + 7 (i < 3: the h <= 1024 columns and the zeros
+    // after them)
+    for (int b = w; b < LGX_LMC_MAXB; b += LGX_LMC_GROUPS) {
+        const bool brow = b < a.m;                         // wave-uniform
+        const float* xr = a.x + (int64_t)min(b, a.m - 1) * a.h;
+        float xv[3][8];
+        float mx = 0.0f;
+        int bad = 0;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int k8 = lane + 64 * i;
+            const bool on = brow && 8 * k8 < a.h;
+            const float4* p = (const float4*)(xr + min(8 * k8, a.h - 8));
+            const float4 u0 = p[0], u1 = p[1];
+            const float t[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                xv[i][e] = on ? t[e] : 0.0f;
+                const float ax = fabsf(xv[i][e]);
+                bad |= !(ax <= 3.4028234663852886e38f) ? 1 : 0;   // NaN or inf
+                mx = fmaxf(mx, ax);
+            }
+        }
+        mx = wave_max(mx);
+        const bool anybad = __ballot(bad) != 0;
+        const bool exact = anybad || !(mx >= 0x1p-60f) || mx > 0x1p60f;
+        // mx = f 2^ex with f in [0.5, 1) (mx normal when not exact)
+        const int ex = (int)((__float_as_uint(mx) >> 23) & 0xffu) - 126;
+        const int p = exact ? 0 : 15 - ex;                  // mx 2^p in [2^14, 2^15)
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int k8 = lane + 64 * i;
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                uint32_t hp[2], lp[2];
+#pragma unroll
+                for (int f = 0; f < 2; ++f) {
+                    const float y = exact ? 0.0f : ldexpf(xv[i][e + f], p);
+                    const uint16_t hb = f2h(y);
+                    hp[f] = hb;
+                    lp[f] = f2h(y - h2f(hb));
+                }
+                hw[e / 2] = hp[0] | (hp[1] << 16);
+                lw[e / 2] = lp[0] | (lp[1] << 16);
+            }
+            // columns [h, XS) are zero: steps past h read them
+            if (8 * k8 + 8 <= LGX_LMC_XS) {
+                *(uint4*)&xh[b * LGX_LMC_XS + 8 * k8] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+                *(uint4*)&xl[b * LGX_LMC_XS + 8 * k8] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            }
+        }
+        if (lane == 0) rexact[b] = brow && exact ? 1 : 0;
+    }
+    __syncthreads();
+
+    // products: T[q][t] (h and l passes) and A[q][t] (|h| |e|), batch tile t
+    // of rows 16t .. 16t + 15
+    const int nt = a.m > 16 ? 2 : 1;
+    const v4f zf = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f T[4][2], A[4][2];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) T[q][t] = A[q][t] = zf;
+    auto step = [&](int s, int slot) {
+        uint4 cur[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) cur[q] = wa[slot][q];
+        ld(s + 2, wa[(slot + 2) % 3]);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (t < nt) {                                   // workgroup-uniform
+                const int xo = (16 * t + r) * LGX_LMC_XS + 32 * s + 8 * c;
+                const uint4 bh = *(const uint4*)&xh[xo];
+                const uint4 bl = *(const uint4*)&xl[xo];
+                const uint4 ba = abs_h8(bh);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    T[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_v8h(cur[q]), as_v8h(bh), T[q][t], 0, 0, 0);
+                    T[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_v8h(cur[q]), as_v8h(bl), T[q][t], 0, 0, 0);
+                    A[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_v8h(abs_h8(cur[q])), as_v8h(ba), A[q][t], 0, 0, 0);
+                }
+            }
+        }
+    };
+#pragma unroll 1
+    for (int s0 = 0; s0 < ns; s0 += 3) {
+        // steps past ns multiply zeros (loads past the group, zero columns)
+        step(s0, 0);
+        step(s0 + 1, 1);
+        step(s0 + 2, 2);
+    }
+
+    // bounds of element (q, t, e): vocabulary row 64g + 16q + 4c + e, batch
+    // row 16t + r
+    auto bounds = [&](int q, int t, int e, float& lo, float& hi) {
+        const float2 k2 = rc[w][16 * q + 4 * c + e];
+        const float tv = T[q][t][e];
+        float eps = LGX_LMC_CA * A[q][t][e] + LGX_LMC_CS * k2.x + LGX_LMC_CD * k2.y;
+        eps = eps * (1.0f + 0x1p-18f) + fabsf(tv) * 0x1p-21f;
+        lo = tv - eps;
+        hi = tv + eps;
+        const int v = 64 * g + 16 * q + 4 * c + e;
+        if (!gon || v >= a.vocab) lo = hi = -__builtin_inff();
+    };
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        if (t < nt) {
+            float lm = -__builtin_inff(), um = -__builtin_inff();
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float lo, hi;
+                    bounds(q, t, e, lo, hi);
+                    lm = fmaxf(lm, lo);
+                    um = fmaxf(um, hi);
+                    const int b = 16 * t + r, v = 64 * g + 16 * q + 4 * c + e;
+                    if (a.dbg && b < a.m && gon && v < a.vocab) {
+                        float* dp = a.dbg + ((int64_t)b * a.vocab + v) * 2;
+                        dp[0] = T[q][t][e];
+                        dp[1] = hi - T[q][t][e];
+                    }
+                }
+            lm = fmaxf(lm, shfl_xor_f(lm, 16));
+            lm = fmaxf(lm, shfl_xor_f(lm, 32));
+            um = fmaxf(um, shfl_xor_f(um, 16));
+            um = fmaxf(um, shfl_xor_f(um, 32));
+            if (c == 0) {
+                lmx[w][16 * t + r] = lm;
+                umx[w][16 * t + r] = um;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < LGX_LMC_MAXB) {
+        float lm = -__builtin_inff(), um = -__builtin_inff();
+        if (tid < 16 * nt) {
+#pragma unroll
+            for (int j = 0; j < LGX_LMC_GROUPS; ++j) {
+                lm = fmaxf(lm, lmx[j][tid]);
+                um = fmaxf(um, umx[j][tid]);
+            }
+        }
+        lwg[tid] = lm;
+        uwg[tid] = um;
+        ccnt[tid] = 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        if (t < nt) {
+            const int b = 16 * t + r;
+            const float lb = lwg[b];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float lo, hi;
+                    bounds(q, t, e, lo, hi);
+                    if (hi >= lb && hi > -__builtin_inff()) {
+                        const int slot = atomicAdd(&ccnt[b], 1);
+                        if (slot < LGX_LMC_CAND) {
+                            cu[b][slot] = hi;
+                            cv[b][slot] = 64 * g + 16 * q + 4 * c + e;
+                        }
+                    }
+                }
+        }
+    }
+    __syncthreads();
+    if (tid < a.m) {
+        lgx_lmc_summary* o = a.summ + (int64_t)tid * a.nslices + blockIdx.x;
+        const int n = ccnt[tid];
+        o->L = lwg[tid];
+        o->Umax = uwg[tid];
+        o->cnt = rexact[tid] ? LGX_LMC_EXACT : n;
+        o->pad = 0;
+#pragma unroll
+        for (int i = 0; i < LGX_LMC_CAND; ++i) {
+            o->U[i] = i < n ? cu[tid][i] : -__builtin_inff();
+            o->v[i] = i < n ? cv[tid][i] : 0x7fffffff;
+        }
+    }
+}
+
+// The canonical chain of vocabulary row v against the staged row xs.
+__device__ __forceinline__ float lm_chain(const float* xs, const uint16_t* emb, int v, int h) {
+    const uint4* er = (const uint4*)(emb + (int64_t)v * h);
+    float acc = 0.0f;
+#pragma unroll 2
+    for (int j = 0; j < (h >> 3); ++j) {
+        const uint4 e = er[j];
+        const float* xj = xs + 8 * j;
+        acc = fmaf(xj[0], h2f(e.x & 0xffffu), acc);
+        acc = fmaf(xj[1], h2f(e.x >> 16), acc);
+        acc = fmaf(xj[2], h2f(e.y & 0xffffu), acc);
+        acc = fmaf(xj[3], h2f(e.y >> 16), acc);
+        acc = fmaf(xj[4], h2f(e.z & 0xffffu), acc);
+        acc = fmaf(xj[5], h2f(e.z >> 16), acc);
+        acc = fmaf(xj[6], h2f(e.w & 0xffffu), acc);
+        acc = fmaf(xj[7], h2f(e.w >> 16), acc);
+    }
+    return acc;
+}
+
+#define LGX_LMP_MAXSL 1024
+extern "C" __global__ __launch_bounds__(256) void lgx_k_lm_pick(const lgx_lmp_args a) {
+    __shared__ float xs[LGX_LMC_MAXH];
+    __shared__ float rl[256];
+    __shared__ int dense[LGX_LMP_MAXSL];
+    __shared__ int ndense, exact_row;
+    __shared__ float bvs[4];
+    __shared__ int bis[4];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const lgx_lmc_summary* sm = a.summ + (int64_t)b * a.nslices;
+    for (int k = tid; k < a.h; k += 256) xs[k] = a.x[(int64_t)b * a.h + k];
+    float lm = -__builtin_inff();
+    for (int s = tid; s < a.nslices; s += 256) lm = fmaxf(lm, sm[s].L);
+    rl[tid] = lm;
+    if (tid == 0) {
+        ndense = 0;
+        exact_row = sm[0].cnt == LGX_LMC_EXACT ? 1 : 0;
+    }
+    __syncthreads();
+    float L = -__builtin_inff();
+    for (int j = 0; j < 256; ++j) L = fmaxf(L, rl[j]);
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+    auto take = [&](int v) {
+        const float z = lm_chain(xs, a.emb, v, a.h);
+        if (z == z) better(bv, bi, z, v);
+    };
+    if (!exact_row) {
+        // the listed rows whose bound reaches L; slices with more rows than
+        // listed go to the dense pass
+        for (int s = tid; s < a.nslices; s += 256) {
+            const lgx_lmc_summary& o = sm[s];
+            if (!(o.Umax >= L)) continue;
+            if (o.cnt > LGX_LMC_CAND) {
+                dense[atomicAdd(&ndense, 1)] = s;
+                continue;
+            }
+            for (int i = 0; i < o.cnt; ++i)
+                if (o.U[i] >= L) take(o.v[i]);
+        }
+    }
+    __syncthreads();
+    // dense pass: every row of the listed slices (of every slice for an
+    // exact row)
+    const int nd = exact_row ? a.nslices : ndense;
+    for (int i = 0; i < nd; ++i) {
+        const int s = exact_row ? i : dense[i];
+        const int v0 = s * LGX_LMC_ROWS;
+        const int v1 = min(v0 + LGX_LMC_ROWS, a.vocab);
+        for (int v = v0 + tid; v < v1; v += 256) take(v);
+    }
+    // first maximum over the threads
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = shfl_xor_f(bv, o);
+        const int oi = __shfl_xor(bi, o, 64);
+        better(bv, bi, ov, oi);
+    }
+    if (lane == 0) {
+        bvs[w] = bv;
+        bis[w] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float fv = bvs[0];
+        int fi = bis[0];
+        for (int j = 1; j < 4; ++j) better(fv, fi, bvs[j], bis[j]);
+        a.tokens[b] = fi == 0x7fffffff ? 0 : fi;
+        if (a.seq_len) a.seq_len[b] += a.advance;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Seeded top-k / top-p sampling.  A logit x at vocabulary index v has the key
 //   (orderable bits of x, -0 taken as +0) << 32 | (0xffffffff - v)
 // so keys sort by value descending, then index ascending; NaN has no key

@@ -52,6 +52,11 @@ struct lgx_model {
     uint16_t* emb = nullptr;
     uint16_t* emb_t64 = nullptr;   // tied lm_head: the embedding in T64 order
     float* xt = nullptr;           // tied lm_head: final-norm rows in T16 column order
+    // certified greedy lm_head (tied): per-row embedding constants, slice
+    // summaries, and whether the embedding is finite (the path's condition)
+    float* lm_rowc = nullptr;
+    lgx_lmc_summary* lm_summ = nullptr;
+    bool lm_cert_ok = false;
     float *cos_t = nullptr, *sin_t = nullptr;
     int32_t* page_table = nullptr;
     int32_t* seq_len = nullptr;
@@ -74,6 +79,7 @@ struct lgx_model {
     SampleParams samp;         // top_k 0: greedy
     int32_t last_nr = 1;       // partial count of the last lm_head
     int32_t last_B = 0;        // batch of the last lm_head
+    bool last_cert = false;    // the last lm_head left no logits (certified greedy pick)
     std::vector<void*> allocs;
     bool counted = false;      // holds one of ctx->live_models
     // recorded decode steps (lgx_qwen_generate), one per (B, tokens) pair
@@ -81,6 +87,7 @@ struct lgx_model {
         int32_t B;
         int32_t* tokens;
         int32_t last_nr;
+        bool last_cert;
         hipGraphExec_t exec;
     };
     std::vector<StepGraph> graphs;
@@ -441,6 +448,15 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
     if ((st = norm(md, md->out_norm, B, H, parts(md, md->dn[0], B), true, md->xn, !tied, stream,
                    tied ? md->xt : nullptr)) != LGX_OK)
         return st;
+    if (tied && md->lm_cert_ok && md->ctx->lm_cert && md->samp.top_k == 0 && B <= LGX_LMC_MAXB) {
+        // greedy: the certified pick from the final-norm rows (xn), no logits
+        md->last_nr = 1;
+        md->last_B = B;
+        md->last_cert = true;
+        return launch_lm_cert(c, md->xn, md->emb, md->emb_t64, md->lm_rowc, B, H, cf.vocab,
+                              md->lm_summ, nullptr, next, md->seq_len, 1, stream);
+    }
+    md->last_cert = false;
     const float* lg;
     int nr;
     if (tied) {
@@ -621,6 +637,7 @@ lgx_status step_graph(lgx_model* md, int B, int32_t* tokens, hipGraphExec_t* out
     for (const lgx_model::StepGraph& g : md->graphs)
         if (g.B == B && g.tokens == tokens) {
             md->last_nr = g.last_nr;
+            md->last_cert = g.last_cert;
             md->last_B = B;
             *out = g.exec;
             return LGX_OK;
@@ -646,7 +663,7 @@ lgx_status step_graph(lgx_model* md, int B, int32_t* tokens, hipGraphExec_t* out
     (void)hipGraphDestroy(graph);
     if (ei != hipSuccess)
         return fail(LGX_HIP_ERROR, "hipGraphInstantiate: %s", hipGetErrorString(ei));
-    md->graphs.push_back({B, tokens, md->last_nr, exec});
+    md->graphs.push_back({B, tokens, md->last_nr, md->last_cert, exec});
     *out = exec;
     return LGX_OK;
 }
@@ -748,6 +765,20 @@ lgx_status model_build(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed, So
             if ((st = launch(c, K_REPACK_F16_T64, dim3(cdiv(nt / 8, 256)), dim3(256), ta, nullptr)) !=
                 LGX_OK)
                 return done(st);
+            // the certified greedy lm_head: row constants, and the path only
+            // for a finite embedding (a non-finite row has +inf constants)
+            if (H % 64 == 0 && H <= LGX_LMC_MAXH && lm_cert_slices(cf.vocab) <= 1024) {
+                if ((st = dev_alloc(m, &m->lm_rowc, (size_t)cf.vocab * 2)) != LGX_OK ||
+                    (st = dev_alloc(m, &m->lm_summ,
+                                    (size_t)std::min(B, LGX_LMC_MAXB) * lm_cert_slices(cf.vocab))) !=
+                        LGX_OK ||
+                    (st = launch_lm_rowconst(c, m->emb, cf.vocab, H, m->lm_rowc, nullptr)) != LGX_OK)
+                    return done(st);
+                std::vector<float> rc((size_t)cf.vocab * 2);
+                LGX_HIP(hipMemcpy(rc.data(), m->lm_rowc, rc.size() * sizeof(float),
+                                  hipMemcpyDeviceToHost));
+                m->lm_cert_ok = std::all_of(rc.begin(), rc.end(), [](float f) { return std::isfinite(f); });
+            }
         }
         {
             std::vector<float> ct((size_t)cf.max_seq * (d / 2)), stb(ct.size());
@@ -1084,6 +1115,14 @@ lgx_status lgx_qwen_logits(lgx_model* m, int32_t B, float* out, void* stream) {
             return fail(LGX_INVALID_ARGUMENT, "B = %d, but the last step ran %d sequences", B,
                         m->last_B);
         const int64_t count = (int64_t)B * m->c.vocab;
+        if (m->last_cert) {
+            // the certified pick left no logits: the exact lm_head of the
+            // step's final-norm rows (still in xt) first
+            lgx_lmhead_args la{m->xt, m->emb_t64, m->logits, B, m->c.hidden, m->c.vocab};
+            if ((st = launch(m->ctx, K_LM_HEAD_T64, dim3(cdiv(m->c.vocab, 64), cdiv(B, 16)),
+                             dim3(64), la, stream)) != LGX_OK)
+                return st;
+        }
         lgx_combine_args ca{m->c.tied_embedding ? m->logits : m->part, out, count, m->last_nr};
         return launch(m->ctx, K_COMBINE, dim3(cdiv(count, 256)), dim3(256), ca, stream);
     });

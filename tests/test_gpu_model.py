@@ -459,7 +459,8 @@ def _ctx_with(env):
                 os.environ[k] = v
 
 
-@pytest.mark.parametrize("env", [{}, dict(LGX_FUSE_SWIGLU_COLS="64"), dict(LGX_DECODE_FUSE="0")])
+@pytest.mark.parametrize("env", [{}, dict(LGX_FUSE_SWIGLU_COLS="64"), dict(LGX_DECODE_FUSE="0"),
+                                 dict(LGX_LM_CERT="0")])
 @pytest.mark.parametrize("name", ["tiny", "tiny_untied"])
 def test_fused_decode_consumers_bit_exact(name, env):
     """Decode batches of 2..32 rows run RoPE + KV append inside the qkv
