@@ -277,9 +277,10 @@ lgx_status lgx_f16_repack_t64(lgx_ctx* ctx, const uint16_t* src, int32_t rows, i
 lgx_status lgx_lm_head_f16_t64(lgx_ctx* ctx, const float* x, const uint16_t* emb_t64, int32_t m,
                                int32_t h, int32_t vocab, float* logits, void* stream);
 /* Per-row constants of a binary16 embedding [vocab][h] for
- * lgx_lm_head_argmax_f16: rowc[v] = (upper bound of sum_k |emb[v][k]|, upper
- * bound of the same sum over its subnormal entries), +inf in both for a row
- * with a non-finite entry; rowc holds 2 * vocab floats.  h <= 1024.
+ * lgx_lm_head_argmax_f16: rowc[v] = upper bounds of (sum_k |emb[v][k]|, the
+ * same sum over its subnormal entries, ||emb[v]||_2), then 0; +inf in the
+ * first three for a row with a non-finite entry; rowc holds 4 * vocab
+ * floats.  h <= 1024.
  * No counterpart in the reference: the precomputation of the certified
  * greedy lm_head below. */
 lgx_status lgx_lm_head_rowconst(lgx_ctx* ctx, const uint16_t* emb, int32_t vocab, int32_t h,

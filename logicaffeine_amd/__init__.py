@@ -563,10 +563,10 @@ class Context:
 
     def lm_head_rowconst(self, emb):
         """Per-row constants of a binary16 embedding (int16 bits [vocab][h]) for
-        lm_head_argmax_f16: float32 [vocab][2]."""
+        lm_head_argmax_f16: float32 [vocab][4]."""
         t = self.torch
         vocab, h = emb.shape
-        out = t.empty((vocab, 2), dtype=t.float32, device=self.dev)
+        out = t.empty((vocab, 4), dtype=t.float32, device=self.dev)
         _check(lib().lgx_lm_head_rowconst(self.handle, emb.data_ptr(), vocab, h, out.data_ptr(),
                                           self._s()))
         return out

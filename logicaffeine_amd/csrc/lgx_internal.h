@@ -345,7 +345,7 @@ inline lgx_status launch_lm_cert(lgx_ctx* c, const float* x, const uint16_t* emb
     lgx_status st = launch(c, K_LM_CERT, dim3(ns), dim3(64 * LGX_LMC_GROUPS), a, stream);
     if (st != LGX_OK) return st;
     lgx_lmp_args p{x, emb, summ, tokens, seq_len, m, h, vocab, ns, advance};
-    return launch(c, K_LM_PICK, dim3(m), dim3(256), p, stream);
+    return launch(c, K_LM_PICK, dim3(m), dim3(512), p, stream);
 }
 inline lgx_status launch_lm_rowconst(lgx_ctx* c, const uint16_t* emb, int vocab, int h,
                                      float* rowc, void* stream) {

@@ -226,7 +226,7 @@ typedef struct {
 typedef struct {
     const float* x;            // [m][h] binary32 rows
     const uint16_t* emb_t64;   // the binary16 embedding in T64 order
-    const float* rowc;         // [vocab][2] (lgx_k_lm_rowconst)
+    const float* rowc;         // [vocab][4] (lgx_k_lm_rowconst)
     lgx_lmc_summary* summ;     // [m][nslices]
     float* dbg;                // nullable: [m][vocab][2] scaled approximation, bound
     int32_t m, h, vocab, nslices;
@@ -239,12 +239,12 @@ typedef struct {
     int32_t* seq_len;          // nullable: += advance
     int32_t m, h, vocab, nslices, advance;
 } lgx_lmp_args;
-// Per-row constants of a binary16 embedding: rowc[v] = (upper bound of
-// sum_k |e[v][k]|, upper bound of the same sum over the subnormal entries);
-// +inf in both when the row has a non-finite entry.
+// Per-row constants of a binary16 embedding: rowc[v] = upper bounds of
+// (sum_k |e[v][k]|, the same sum over the subnormal entries, ||e[v]||_2),
+// then 0; +inf in the first three when the row has a non-finite entry.
 typedef struct {
     const uint16_t* emb;       // [vocab][h]
-    float* rowc;               // [vocab][2]
+    float* rowc;               // [vocab][4]
     int32_t vocab, h;
 } lgx_lmrc_args;
 

@@ -2671,19 +2671,23 @@ extern "C" __global__ __launch_bounds__(64) void lgx_k_argmax_final(const lgx_ar
 //
 // lgx_k_lm_cert (workgroup = slice of LGX_LMC_GROUPS 64-row groups, one wave
 // per group): row b of x is scaled by s = 2^p (max |x| s in [2^14, 2^15)),
-// y = x s, split as y ~ h + l with h = f16(y), l = f16(y - h); binary16
-// MFMAs (f32 accumulation) give T = sum_k (h + l) e and A = sum_k |h| |e|
-// per (v, b).  With S = sum_k |e| and D = the same sum over subnormal e
-// (per row, lgx_k_lm_rowconst), |s z - T| <= eps = CA A + CS S + CD D,
-// taking: the chain's own rounding (gamma_H <= 1024 u / (1 - 1024 u)), the
-// split's residual |y - h - l| <= 2^-22 |h| + 2^-24, binary16 inputs
-// flushed to zero or not (2^-14 per flushed input, the subnormal e part
-// through D with |h| <= 2^15), and an MFMA accumulation error of at most
-// 2^-9 of the sum of the absolute terms (the sequential round-to-nearest
-// bound for 2048 terms is 2^-13).  eps is then widened for the binary32
-// arithmetic of the bound itself.  The summary of (b, slice): the largest
-// lower bound L = T - eps, the largest upper bound U = T + eps, and the
-// rows whose U reaches L.
+// y = x s and h = f16(y); binary16 MFMAs (f32 accumulation) give
+// T = sum_k h e per (v, b).  With S = sum_k |e|, D = the same sum over the
+// subnormal e, N >= ||e||_2 (per row, lgx_k_lm_rowconst) and H >= ||h||_2
+// (per row of x), |s z - T| <= eps = CA H N + CS S + CD D, taking:
+//   - the MFMA accumulation: at most 2^-9 of sum |h| |e| (the sequential
+//     round-to-nearest bound for 1024 terms is 2^-14), and sum |h| |e| <=
+//     ||h|| ||e|| (Cauchy-Schwarz);
+//   - the rounding y -> h: |y - h| <= 2^-11 |h| + 2^-25;
+//   - binary16 inputs flushed to zero or not: 2^-14 per flushed h, the
+//     subnormal e through D with |h| <= 2^15;
+//   - the chain's own rounding: gamma_H = 1024 u / (1 - 1024 u), u = 2^-24,
+//     times sum |y| |e|;
+// so CA = 2^-9 + 2^-11 + gamma_H (1 + 2^-11), CS = 2^-14 + 2^-25 (+ the
+// chain's share), CD = 2^15, each rounded up; eps is then widened for the
+// binary32 arithmetic of the bound itself.  The summary of (b, slice): the
+// largest lower bound L = T - eps, the largest upper bound U = T + eps, and
+// the rows whose U reaches L.
 //
 // lgx_k_lm_pick (workgroup = row b): L(b) = max over slices; a row v can be
 // the first maximum only if U(v) >= L(b) (otherwise s z_v <= U(v) < L(v')
@@ -2694,16 +2698,18 @@ extern "C" __global__ __launch_bounds__(64) void lgx_k_argmax_final(const lgx_ar
 // (NaN skipped, none gives 0), then seq_len[b] += advance.
 // ---------------------------------------------------------------------------
 // binary16 per staged row: h columns, zeros up to the last column of the
-// up-to-two k-steps past h that the 3-slot ring runs, and 8 of bank spread
-#define LGX_LMC_XS (LGX_LMC_MAXH + 64 + 8)
-#define LGX_LMC_CA 2.02e-3f
-#define LGX_LMC_CS 2.45e-4f
-#define LGX_LMC_CD 32900.0f
+// k-steps past h that the prefetch ring runs, and 8 of bank spread
+#define LGX_LMC_XS (LGX_LMC_MAXH + 96 + 8)
+#define LGX_LMC_CA 2.51e-3f
+#define LGX_LMC_CS 6.3e-5f
+#define LGX_LMC_CD 32800.0f
 
-// Upper bounds of sum |e| and of its subnormal part per row (exact fp64
-// sums: binary16 magnitudes are multiples of 2^-24 below 2^16, so 1024 of
-// them sum exactly in 53 bits), rounded up to binary32; +inf for a row with
-// a non-finite entry.  One wave per row.
+// Upper bounds per row: rowc[v] = (sum_k |e|, the same over subnormal e,
+// ||e||_2, 0).  The sums of magnitudes are exact in fp64 (binary16
+// magnitudes are multiples of 2^-24 below 2^16: 1024 of them need 50 bits);
+// the sum of squares has relative error below 2^-42 and is widened before
+// the square root.  Each is rounded up to binary32; +inf for a row with a
+// non-finite entry.  One wave per row.
 __device__ __forceinline__ float f64_to_f32_up(double d) {
     float f = (float)d;
     if ((double)f < d) f = __uint_as_float(__float_as_uint(f) + 1u);   // d >= 0
@@ -2714,39 +2720,42 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_lm_rowconst(const lgx_lm
     const int v = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (v >= a.vocab) return;                   // whole waves; no barrier below
     const uint16_t* er = a.emb + (int64_t)v * a.h;
-    double s = 0.0, d = 0.0;
+    double s = 0.0, d = 0.0, q = 0.0;
     int bad = 0;
     for (int k = lane; k < a.h; k += 64) {
         const uint32_t mag = er[k] & 0x7fffu;
         bad |= mag >= 0x7c00u ? 1 : 0;
         const double f = (double)h2f(mag);
         s += f;
+        q += f * f;
         if (mag < 0x0400u) d += f;
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         s += __shfl_xor(s, o, 64);
         d += __shfl_xor(d, o, 64);
+        q += __shfl_xor(q, o, 64);
         bad |= __shfl_xor(bad, o, 64);
     }
     if (lane == 0) {
         const float inf = __builtin_inff();
-        ((float2*)a.rowc)[v] = bad ? make_float2(inf, inf) : make_float2(f64_to_f32_up(s), f64_to_f32_up(d));
+        ((float4*)a.rowc)[v] = bad ? make_float4(inf, inf, inf, 0.0f)
+                                   : make_float4(f64_to_f32_up(s), f64_to_f32_up(d),
+                                                 f64_to_f32_up(sqrt(q * (1.0 + 0x1p-40)) * (1.0 + 0x1p-40)),
+                                                 0.0f);
     }
 }
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ v8h as_v8h(uint4 u) { return __builtin_bit_cast(v8h, u); }
-__device__ __forceinline__ uint4 abs_h8(uint4 u) {
-    return make_uint4(u.x & 0x7fff7fffu, u.y & 0x7fff7fffu, u.z & 0x7fff7fffu, u.w & 0x7fff7fffu);
-}
 
+#define LGX_LMC_RING 4                  // k-steps in flight: the one in use and three ahead
 extern "C" __global__ __launch_bounds__(64 * LGX_LMC_GROUPS) void lgx_k_lm_cert(const lgx_lmc_args a) {
-    // rows of the scaled, split x (binary16 bits), [b][k] with a padded row
-    // stride: an MFMA B operand (16 rows x 8 columns) is one conflict-free read
+    // rows of the scaled x (binary16 bits), [b][k] with a padded row stride:
+    // an MFMA B operand (16 rows x 8 columns) is one conflict-free read
     __shared__ __align__(16) uint16_t xh[LGX_LMC_MAXB * LGX_LMC_XS];
-    __shared__ __align__(16) uint16_t xl[LGX_LMC_MAXB * LGX_LMC_XS];
-    __shared__ float2 rc[LGX_LMC_GROUPS][64];
+    __shared__ float4 rc[LGX_LMC_GROUPS][64];
+    __shared__ float hn[LGX_LMC_MAXB];
     __shared__ float lmx[LGX_LMC_GROUPS][LGX_LMC_MAXB], umx[LGX_LMC_GROUPS][LGX_LMC_MAXB];
     __shared__ float lwg[LGX_LMC_MAXB], uwg[LGX_LMC_MAXB];
     __shared__ int ccnt[LGX_LMC_MAXB], rexact[LGX_LMC_MAXB];
@@ -2766,20 +2775,15 @@ extern "C" __global__ __launch_bounds__(64 * LGX_LMC_GROUPS) void lgx_k_lm_cert(
     const __amdgpu_buffer_rsrc_t er = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(a.emb_t64 + (int64_t)min(g, ngroups - 1) * ncg * 512), 0, gon ? ncg * 1024 : 0,
         LGX_BUF_DWORD3);
-    // k-steps in flight: a ring of three (the step in use and two ahead)
-    uint4 wa[3][4];
+    uint4 wa[LGX_LMC_RING][4];
     auto ld = [&](int s, uint4 (&dst)[4]) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) dst[q] = ld_buf_stream(er, ((4 * s + c) * 64 + 16 * q + r) * 16);
     };
-    ld(0, wa[0]);
-    ld(1, wa[1]);
+#pragma unroll
+    for (int i = 0; i < LGX_LMC_RING - 1; ++i) ld(i, wa[i]);
     // per-row constants of the group's rows
-    {
-        const int v = min(64 * g + lane, a.vocab - 1);
-        const float2 q = ((const float2*)a.rowc)[v];
-        rc[w][lane] = q;
-    }
+    rc[w][lane] = ((const float4*)a.rowc)[min(64 * g + lane, a.vocab - 1)];
     // stage x: wave w takes rows w, w + GROUPS, ...; lane holds columns
     // 8(lane + 64 i) .. + 7 (i < 3: the h <= 1024 columns and the zeros
     // after them)
@@ -2810,77 +2814,74 @@ extern "C" __global__ __launch_bounds__(64 * LGX_LMC_GROUPS) void lgx_k_lm_cert(
         // mx = f 2^ex with f in [0.5, 1) (mx normal when not exact)
         const int ex = (int)((__float_as_uint(mx) >> 23) & 0xffu) - 126;
         const int p = exact ? 0 : 15 - ex;                  // mx 2^p in [2^14, 2^15)
+        double sq = 0.0;
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
             const int k8 = lane + 64 * i;
-            uint32_t hw[4], lw[4];
+            uint32_t hw[4];
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
-                uint32_t hp[2], lp[2];
+                uint32_t hp[2];
 #pragma unroll
                 for (int f = 0; f < 2; ++f) {
                     const float y = exact ? 0.0f : ldexpf(xv[i][e + f], p);
                     const uint16_t hb = f2h(y);
+                    const double hd = (double)h2f(hb);
+                    sq += hd * hd;
                     hp[f] = hb;
-                    lp[f] = f2h(y - h2f(hb));
                 }
                 hw[e / 2] = hp[0] | (hp[1] << 16);
-                lw[e / 2] = lp[0] | (lp[1] << 16);
             }
             // columns [h, XS) are zero: steps past h read them
-            if (8 * k8 + 8 <= LGX_LMC_XS) {
+            if (8 * k8 + 8 <= LGX_LMC_XS)
                 *(uint4*)&xh[b * LGX_LMC_XS + 8 * k8] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-                *(uint4*)&xl[b * LGX_LMC_XS + 8 * k8] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-            }
         }
-        if (lane == 0) rexact[b] = brow && exact ? 1 : 0;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
+        if (lane == 0) {
+            rexact[b] = brow && exact ? 1 : 0;
+            // ||h||_2 rounded up (the fp64 sum of squares is within 2^-42)
+            hn[b] = f64_to_f32_up(sqrt(sq * (1.0 + 0x1p-40)) * (1.0 + 0x1p-40));
+        }
     }
     __syncthreads();
 
-    // products: T[q][t] (h and l passes) and A[q][t] (|h| |e|), batch tile t
-    // of rows 16t .. 16t + 15
+    // T[q][t] of batch tile t (rows 16t .. 16t + 15)
     const int nt = a.m > 16 ? 2 : 1;
     const v4f zf = {0.0f, 0.0f, 0.0f, 0.0f};
-    v4f T[4][2], A[4][2];
+    v4f T[4][2];
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) T[q][t] = A[q][t] = zf;
+        for (int t = 0; t < 2; ++t) T[q][t] = zf;
     auto step = [&](int s, int slot) {
         uint4 cur[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) cur[q] = wa[slot][q];
-        ld(s + 2, wa[(slot + 2) % 3]);
+        ld(s + LGX_LMC_RING - 1, wa[(slot + LGX_LMC_RING - 1) % LGX_LMC_RING]);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             if (t < nt) {                                   // workgroup-uniform
-                const int xo = (16 * t + r) * LGX_LMC_XS + 32 * s + 8 * c;
-                const uint4 bh = *(const uint4*)&xh[xo];
-                const uint4 bl = *(const uint4*)&xl[xo];
-                const uint4 ba = abs_h8(bh);
+                const uint4 bh = *(const uint4*)&xh[(16 * t + r) * LGX_LMC_XS + 32 * s + 8 * c];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < 4; ++q)
                     T[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_v8h(cur[q]), as_v8h(bh), T[q][t], 0, 0, 0);
-                    T[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_v8h(cur[q]), as_v8h(bl), T[q][t], 0, 0, 0);
-                    A[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_v8h(abs_h8(cur[q])), as_v8h(ba), A[q][t], 0, 0, 0);
-                }
             }
         }
     };
 #pragma unroll 1
-    for (int s0 = 0; s0 < ns; s0 += 3) {
+    for (int s0 = 0; s0 < ns; s0 += LGX_LMC_RING) {
         // steps past ns multiply zeros (loads past the group, zero columns)
-        step(s0, 0);
-        step(s0 + 1, 1);
-        step(s0 + 2, 2);
+#pragma unroll
+        for (int i = 0; i < LGX_LMC_RING; ++i) step(s0 + i, i);
     }
 
     // bounds of element (q, t, e): vocabulary row 64g + 16q + 4c + e, batch
     // row 16t + r
-    auto bounds = [&](int q, int t, int e, float& lo, float& hi) {
-        const float2 k2 = rc[w][16 * q + 4 * c + e];
+    auto bounds = [&](int q, int t, int e, float& lo, float& hi, float& eps) {
+        const float4 k4 = rc[w][16 * q + 4 * c + e];
         const float tv = T[q][t][e];
-        float eps = LGX_LMC_CA * A[q][t][e] + LGX_LMC_CS * k2.x + LGX_LMC_CD * k2.y;
+        eps = LGX_LMC_CA * (hn[16 * t + r] * k4.z) + LGX_LMC_CS * k4.x + LGX_LMC_CD * k4.y;
         eps = eps * (1.0f + 0x1p-18f) + fabsf(tv) * 0x1p-21f;
         lo = tv - eps;
         hi = tv + eps;
@@ -2895,15 +2896,15 @@ extern "C" __global__ __launch_bounds__(64 * LGX_LMC_GROUPS) void lgx_k_lm_cert(
             for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float lo, hi;
-                    bounds(q, t, e, lo, hi);
+                    float lo, hi, eps;
+                    bounds(q, t, e, lo, hi, eps);
                     lm = fmaxf(lm, lo);
                     um = fmaxf(um, hi);
                     const int b = 16 * t + r, v = 64 * g + 16 * q + 4 * c + e;
                     if (a.dbg && b < a.m && gon && v < a.vocab) {
                         float* dp = a.dbg + ((int64_t)b * a.vocab + v) * 2;
                         dp[0] = T[q][t][e];
-                        dp[1] = hi - T[q][t][e];
+                        dp[1] = eps;
                     }
                 }
             lm = fmaxf(lm, shfl_xor_f(lm, 16));
@@ -2940,8 +2941,8 @@ extern "C" __global__ __launch_bounds__(64 * LGX_LMC_GROUPS) void lgx_k_lm_cert(
             for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float lo, hi;
-                    bounds(q, t, e, lo, hi);
+                    float lo, hi, eps;
+                    bounds(q, t, e, lo, hi, eps);
                     if (hi >= lb && hi > -__builtin_inff()) {
                         const int slot = atomicAdd(&ccnt[b], 1);
                         if (slot < LGX_LMC_CAND) {
@@ -2968,76 +2969,167 @@ extern "C" __global__ __launch_bounds__(64 * LGX_LMC_GROUPS) void lgx_k_lm_cert(
     }
 }
 
-// The canonical chain of vocabulary row v against the staged row xs.
-__device__ __forceinline__ float lm_chain(const float* xs, const uint16_t* emb, int v, int h) {
+// The canonical chain of vocabulary row v against the staged row xs, with
+// the row itself staged in es (binary32): the wave loads it (one memory
+// round), lane 0 chains it, 32 columns per batch of 16-byte LDS reads.
+__device__ __forceinline__ float lm_chain_wave(const float* xs, float* es, const uint16_t* emb, int v,
+                                               int h, int lane) {
     const uint4* er = (const uint4*)(emb + (int64_t)v * h);
-    float acc = 0.0f;
-#pragma unroll 2
-    for (int j = 0; j < (h >> 3); ++j) {
+    for (int j = lane; j < (h >> 3); j += 64) {
         const uint4 e = er[j];
-        const float* xj = xs + 8 * j;
-        acc = fmaf(xj[0], h2f(e.x & 0xffffu), acc);
-        acc = fmaf(xj[1], h2f(e.x >> 16), acc);
-        acc = fmaf(xj[2], h2f(e.y & 0xffffu), acc);
-        acc = fmaf(xj[3], h2f(e.y >> 16), acc);
-        acc = fmaf(xj[4], h2f(e.z & 0xffffu), acc);
-        acc = fmaf(xj[5], h2f(e.z >> 16), acc);
-        acc = fmaf(xj[6], h2f(e.w & 0xffffu), acc);
-        acc = fmaf(xj[7], h2f(e.w >> 16), acc);
+        float4* d = (float4*)(es + 8 * j);
+        d[0] = make_float4(h2f(e.x & 0xffffu), h2f(e.x >> 16), h2f(e.y & 0xffffu), h2f(e.y >> 16));
+        d[1] = make_float4(h2f(e.z & 0xffffu), h2f(e.z >> 16), h2f(e.w & 0xffffu), h2f(e.w >> 16));
+    }
+    float acc = 0.0f;
+    if (lane == 0) {
+        for (int k0 = 0; k0 < h; k0 += 32) {
+            float4 xa[8], ea[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                xa[i] = *(const float4*)(xs + k0 + 4 * i);
+                ea[i] = *(const float4*)(es + k0 + 4 * i);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                acc = fmaf(xa[i].x, ea[i].x, acc);
+                acc = fmaf(xa[i].y, ea[i].y, acc);
+                acc = fmaf(xa[i].z, ea[i].z, acc);
+                acc = fmaf(xa[i].w, ea[i].w, acc);
+            }
+        }
+    }
+    return acc;
+}
+
+// The canonical chains of 64 consecutive rows v0 + lane (rows >= v1 idle):
+// each lane streams its own row in 64-column blocks, one block ahead.
+__device__ __forceinline__ float lm_chain_lanes(const float* xs, const uint16_t* emb, int v, int h) {
+    const uint4* er = (const uint4*)(emb + (int64_t)v * h);
+    const int nb = h >> 6;
+    uint4 cur[8], nxt[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cur[j] = er[j];
+    float acc = 0.0f;
+    for (int kb = 0; kb < nb; ++kb) {
+        const int kn = min(kb + 1, nb - 1);                 // the last block re-reads itself
+#pragma unroll
+        for (int j = 0; j < 8; ++j) nxt[j] = er[8 * kn + j];
+        const float* xk = xs + 64 * kb;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint4 e = cur[j];
+            acc = fmaf(xk[8 * j + 0], h2f(e.x & 0xffffu), acc);
+            acc = fmaf(xk[8 * j + 1], h2f(e.x >> 16), acc);
+            acc = fmaf(xk[8 * j + 2], h2f(e.y & 0xffffu), acc);
+            acc = fmaf(xk[8 * j + 3], h2f(e.y >> 16), acc);
+            acc = fmaf(xk[8 * j + 4], h2f(e.z & 0xffffu), acc);
+            acc = fmaf(xk[8 * j + 5], h2f(e.z >> 16), acc);
+            acc = fmaf(xk[8 * j + 6], h2f(e.w & 0xffffu), acc);
+            acc = fmaf(xk[8 * j + 7], h2f(e.w >> 16), acc);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) cur[j] = nxt[j];
     }
     return acc;
 }
 
 #define LGX_LMP_MAXSL 1024
-extern "C" __global__ __launch_bounds__(256) void lgx_k_lm_pick(const lgx_lmp_args a) {
-    __shared__ float xs[LGX_LMC_MAXH];
-    __shared__ float rl[256];
+#define LGX_LMP_MAXC 2048
+#define LGX_LMP_WAVES 8
+extern "C" __global__ __launch_bounds__(64 * LGX_LMP_WAVES) void lgx_k_lm_pick(const lgx_lmp_args a) {
+    constexpr int NT = 64 * LGX_LMP_WAVES;
+    __shared__ __align__(16) float xs[LGX_LMC_MAXH];
+    __shared__ __align__(16) float es[LGX_LMP_WAVES][LGX_LMC_MAXH];
+    __shared__ float rl[LGX_LMP_WAVES];
+    __shared__ int cand[LGX_LMP_MAXC];
     __shared__ int dense[LGX_LMP_MAXSL];
-    __shared__ int ndense, exact_row;
-    __shared__ float bvs[4];
-    __shared__ int bis[4];
+    __shared__ int ncand, ndense, exact_row;
+    __shared__ float bvs[LGX_LMP_WAVES];
+    __shared__ int bis[LGX_LMP_WAVES];
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const lgx_lmc_summary* sm = a.summ + (int64_t)b * a.nslices;
-    for (int k = tid; k < a.h; k += 256) xs[k] = a.x[(int64_t)b * a.h + k];
+    for (int k = tid; k < a.h; k += NT) xs[k] = a.x[(int64_t)b * a.h + k];
+    // the records of this thread's slices (nslices <= 2 NT) in one memory
+    // round: {L, Umax, cnt, pad}, U[0..7], v[0..7]
+    static_assert(sizeof(lgx_lmc_summary) == 80 && LGX_LMC_CAND == 8, "record layout");
+    uint4 rec[2][5];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint4* rp = (const uint4*)(sm + min(tid + NT * i, a.nslices - 1));
+#pragma unroll
+        for (int j = 0; j < 5; ++j) rec[i][j] = rp[j];
+    }
     float lm = -__builtin_inff();
-    for (int s = tid; s < a.nslices; s += 256) lm = fmaxf(lm, sm[s].L);
-    rl[tid] = lm;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        if (tid + NT * i < a.nslices) lm = fmaxf(lm, __uint_as_float(rec[i][0].x));
+    lm = wave_max(lm);
+    if (lane == 0) rl[w] = lm;
     if (tid == 0) {
+        ncand = 0;
         ndense = 0;
-        exact_row = sm[0].cnt == LGX_LMC_EXACT ? 1 : 0;
+        exact_row = (int)rec[0][0].z == LGX_LMC_EXACT ? 1 : 0;   // slice 0's record
     }
     __syncthreads();
-    float L = -__builtin_inff();
-    for (int j = 0; j < 256; ++j) L = fmaxf(L, rl[j]);
-    float bv = -__builtin_inff();
-    int bi = 0x7fffffff;
-    auto take = [&](int v) {
-        const float z = lm_chain(xs, a.emb, v, a.h);
-        if (z == z) better(bv, bi, z, v);
-    };
+    float L = rl[0];
+#pragma unroll
+    for (int j = 1; j < LGX_LMP_WAVES; ++j) L = fmaxf(L, rl[j]);
     if (!exact_row) {
         // the listed rows whose bound reaches L; slices with more rows than
         // listed go to the dense pass
-        for (int s = tid; s < a.nslices; s += 256) {
-            const lgx_lmc_summary& o = sm[s];
-            if (!(o.Umax >= L)) continue;
-            if (o.cnt > LGX_LMC_CAND) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int s = tid + NT * i;
+            const float umax = __uint_as_float(rec[i][0].y);
+            const int cnt = (int)rec[i][0].z;
+            if (s >= a.nslices || !(umax >= L)) continue;
+            if (cnt > LGX_LMC_CAND) {
                 dense[atomicAdd(&ndense, 1)] = s;
                 continue;
             }
-            for (int i = 0; i < o.cnt; ++i)
-                if (o.U[i] >= L) take(o.v[i]);
+            const uint32_t uu[8] = {rec[i][1].x, rec[i][1].y, rec[i][1].z, rec[i][1].w,
+                                    rec[i][2].x, rec[i][2].y, rec[i][2].z, rec[i][2].w};
+            const uint32_t vv[8] = {rec[i][3].x, rec[i][3].y, rec[i][3].z, rec[i][3].w,
+                                    rec[i][4].x, rec[i][4].y, rec[i][4].z, rec[i][4].w};
+            bool full = false;
+#pragma unroll
+            for (int j = 0; j < LGX_LMC_CAND; ++j)
+                if (j < cnt && __uint_as_float(uu[j]) >= L) {
+                    const int k = atomicAdd(&ncand, 1);
+                    if (k < LGX_LMP_MAXC)
+                        cand[k] = (int)vv[j];
+                    else
+                        full = true;                // (a row listed twice is harmless)
+                }
+            if (full) dense[atomicAdd(&ndense, 1)] = s;
         }
     }
     __syncthreads();
-    // dense pass: every row of the listed slices (of every slice for an
-    // exact row)
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+    auto take = [&](float z, int v) {
+        if (z == z) better(bv, bi, z, v);
+    };
+    // sparse: one candidate per wave at a time
+    const int nc = min(ncand, LGX_LMP_MAXC);
+    for (int i = w; i < nc; i += LGX_LMP_WAVES) {
+        const int v = cand[i];
+        const float z = lm_chain_wave(xs, es[w], a.emb, v, a.h, lane);
+        if (lane == 0) take(z, v);
+    }
+    // dense: every row of the listed slices (of every slice for an exact
+    // row), one row per lane
     const int nd = exact_row ? a.nslices : ndense;
     for (int i = 0; i < nd; ++i) {
         const int s = exact_row ? i : dense[i];
         const int v0 = s * LGX_LMC_ROWS;
         const int v1 = min(v0 + LGX_LMC_ROWS, a.vocab);
-        for (int v = v0 + tid; v < v1; v += 256) take(v);
+        for (int vb = v0 + 64 * w; vb < v1; vb += NT) {       // wave-uniform
+            const int v = vb + lane;
+            const float z = lm_chain_lanes(xs, a.emb, min(v, v1 - 1), a.h);
+            if (v < v1) take(z, v);
+        }
     }
     // first maximum over the threads
 #pragma unroll
@@ -3054,7 +3146,7 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_lm_pick(const lgx_lmp_ar
     if (tid == 0) {
         float fv = bvs[0];
         int fi = bis[0];
-        for (int j = 1; j < 4; ++j) better(fv, fi, bvs[j], bis[j]);
+        for (int j = 1; j < LGX_LMP_WAVES; ++j) better(fv, fi, bvs[j], bis[j]);
         a.tokens[b] = fi == 0x7fffffff ? 0 : fi;
         if (a.seq_len) a.seq_len[b] += a.advance;
     }

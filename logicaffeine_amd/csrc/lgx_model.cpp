@@ -768,13 +768,13 @@ lgx_status model_build(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed, So
             // the certified greedy lm_head: row constants, and the path only
             // for a finite embedding (a non-finite row has +inf constants)
             if (H % 64 == 0 && H <= LGX_LMC_MAXH && lm_cert_slices(cf.vocab) <= 1024) {
-                if ((st = dev_alloc(m, &m->lm_rowc, (size_t)cf.vocab * 2)) != LGX_OK ||
+                if ((st = dev_alloc(m, &m->lm_rowc, (size_t)cf.vocab * 4)) != LGX_OK ||
                     (st = dev_alloc(m, &m->lm_summ,
                                     (size_t)std::min(B, LGX_LMC_MAXB) * lm_cert_slices(cf.vocab))) !=
                         LGX_OK ||
                     (st = launch_lm_rowconst(c, m->emb, cf.vocab, H, m->lm_rowc, nullptr)) != LGX_OK)
                     return done(st);
-                std::vector<float> rc((size_t)cf.vocab * 2);
+                std::vector<float> rc((size_t)cf.vocab * 4);
                 LGX_HIP(hipMemcpy(rc.data(), m->lm_rowc, rc.size() * sizeof(float),
                                   hipMemcpyDeviceToHost));
                 m->lm_cert_ok = std::all_of(rc.begin(), rc.end(), [](float f) { return std::isfinite(f); });

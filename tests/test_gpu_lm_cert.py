@@ -82,8 +82,8 @@ def test_certified_token_small_vocab_against_oracle(ctx, orc):
 def test_bound_holds_with_margin(ctx):
     """|s z - T| <= eps for every (row, vocabulary row) of the certified rows
     (z the exact chain, s the row's power-of-two scale), with a wide margin:
-    the bound allows an MFMA accumulation error 16x the sequential
-    round-to-nearest one."""
+    the bound allows an MFMA accumulation error 32x the sequential
+    round-to-nearest one, over Cauchy-Schwarz."""
     m, h, vocab = 32, 896, 151936
     E = emb_device(ctx, vocab, h, seed=5)
     Et = ctx.f16_repack_t64(E)
@@ -108,6 +108,7 @@ def test_bound_holds_with_margin(ctx):
         worst = max(worst, float(np.max(err / eps)))
         checked += 1
     assert checked >= 25
+    print(f"bound check: {checked} rows, largest |s z - T| / eps = {worst:.3e}")
     assert worst < 0.25, worst
 
 
@@ -157,7 +158,7 @@ def test_rowconst_bounds(ctx, orc):
     Ef = np.abs(orc.f16_to_f32(E).astype(np.float64))
     for v in range(vocab):
         if v in (5, 6):
-            assert np.isinf(rc[v, 0]) and np.isinf(rc[v, 1])
+            assert np.all(np.isinf(rc[v, :3]))
             continue
         s = Ef[v].sum()
         d = Ef[v][(E[v] & 0x7fff) < 0x0400].sum()
@@ -165,6 +166,9 @@ def test_rowconst_bounds(ctx, orc):
             assert float(got) >= exact
             assert float(got) == float(np.float32(exact)) or \
                 float(got) == float(np.nextafter(np.float32(exact), np.float32(np.inf)))
+        n2 = np.sqrt(np.sum(Ef[v] ** 2))             # the norm: above, by a few ulp at most
+        assert n2 <= float(rc[v, 2]) <= n2 * (1 + 2.0 ** -21)
+        assert rc[v, 3] == 0.0
 
 
 def test_certified_argument_errors(ctx):
