@@ -66,7 +66,7 @@ DOMINANT_USED = DOMINANT[2]
 # FETCH_SIZE and WRITE_SIZE passes of this script (--copy-calibration): the
 # counters scaled by what they read for a plain 256 MiB device copy (FETCH_SIZE
 # x 2.0, WRITE_SIZE x 1.0); profiles/q8_gemv_grouped_config1.md.
-TRAFFIC_BYTES = (21691.8 * 2.0 + 76.0) * 1024
+TRAFFIC_BYTES = (21710.5 * 2.0 + 76.0) * 1024
 MALL_BYTES = 256 << 20
 SHAPES = (("gate", 8960, 1536), ("up", 8960, 1536), ("down", 1536, 8960))
 
