@@ -212,6 +212,7 @@ struct lgx_ctx {
                                    // rows through the streaming kernels
     bool decode_fuse = true;      // LGX_DECODE_FUSE=0: decode glue in kernels of its own
     int fuse_cols32 = 1;          // LGX_FUSE_SWIGLU_COLS: SwiGLU columns per fused workgroup / 32
+    bool tiled_swiglu = true;     // LGX_TILED_SWIGLU=0: tiled gate|up products leave their outputs to lgx_k_swiglu_quant
     int norm_waves = 1;           // LGX_NORM_WAVES: rows (waves) per workgroup of the wave norm (0: off)
     bool lm_cert = true;          // LGX_LM_CERT=0: greedy tied lm_head through the full logits
     bool prefill_serial = false;  // LGX_PREFILL=serial: prefill as P decode passes
@@ -496,11 +497,14 @@ inline lgx_status run_q8(lgx_ctx* c, Kern kern, const lgx_q8_matrix* W, const fl
 // Tiled product: activations in T16 tiles (ceil(m/16) of them), group
 // partials part[ceil(nr / grp)][m][n] (canonical subtrees of grp aligned
 // ranges, grp in {1, 2, 4}).  Activation rows per workgroup: 128
-// (K_GEMM_TILED), 64 or 32.
+// (K_GEMM_TILED), 64 or 32.  With swiglu = I (W the [gate; up] matrix of
+// 2I rows, I % 32 == 0, one group) the SwiGLU + Q8_0 of the outputs goes to
+// sq (T16) / sd instead of part.
 inline int tiled_groups(int k, int grp = LGX_TG_RANGES) { return (nranges_of(k) + grp - 1) / grp; }
 inline lgx_status run_q8_tiled(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xt,
                                const uint16_t* xd, int m, float* part, void* stream,
-                               Kern kern = K_GEMM_TILED, int grp = LGX_TG_RANGES) {
+                               Kern kern = K_GEMM_TILED, int grp = LGX_TG_RANGES,
+                               int swiglu = 0, int8_t* sq = nullptr, uint16_t* sd = nullptr) {
     const int mrows = kern == K_GEMM_TILED ? 128 : kern == K_GEMM_TILED64 ? 64 : 32;
     lgx_gemm_tiled_args a{};
     a.wt = W->qs;
@@ -513,6 +517,14 @@ inline lgx_status run_q8_tiled(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t*
     a.m = m;
     a.grp = grp;
     a.ngroups = tiled_groups(W->k, grp);
+    if (swiglu) {
+        if (swiglu % 32 || W->n != 2 * swiglu || a.ngroups != 1 || !sq || !sd)
+            return fail(LGX_INVALID_ARGUMENT, "tiled SwiGLU product: n %d, I %d, %d groups", W->n,
+                        swiglu, a.ngroups);
+        a.swiglu = swiglu;
+        a.sq = sq;
+        a.sd = sd;
+    }
     a.ntn = (int)cdiv(W->n, LGX_TG_N);
     a.ntm = (int)cdiv(m, mrows);
     const int64_t wgs = (int64_t)a.ntn * a.ntm * a.ngroups;

@@ -287,7 +287,11 @@ typedef struct {
 // activation rows, group of LGX_TG_RANGES ranges).  Activations in the T16
 // tile layout of the weights (row tiles of 16, 1 KiB per 64-column pair).
 // part[g][m][n] = canonical tree over the ranges of group g, so the tree
-// over the groups is the tree over all ranges.
+// over the groups is the tree over all ranges.  With swiglu = I > 0 (a
+// gate|up matrix of n = 2I rows, gate rows first, in one group) the outputs
+// are not stored: the workgroup runs SwiGLU + Q8_0 on them and writes the
+// quants in T16 tiles to sq ([ceil(m/16)][I/64][64][16]) and the scales to
+// sd ([m][I/32]), the lgx_k_swiglu_quant operations.
 #define LGX_TG_RANGES 4
 #define LGX_TG_N 64
 #define LGX_TG_M 128
@@ -297,9 +301,12 @@ typedef struct {
     const int8_t* xt;      // T16 activations [ceil(m/16)][k/64][64][16]
     const uint16_t* xd;    // activation scales [m][k/32]
     float* part;           // [ngroups][m][n]
+    int8_t* sq;            // swiglu: T16 quants of the SwiGLU outputs
+    uint16_t* sd;          // swiglu: their scales
     int32_t n, k, m, ngroups;
     int32_t ntn, ntm;      // workgroup tiles along n and m
     int32_t grp;           // ranges per group: 1, 2 or 4 (ngroups = ceil(nranges / grp))
+    int32_t swiglu;        // I of a fused SwiGLU consumer, else 0
 } lgx_gemm_tiled_args;
 
 // Grouped M > 1 products (lgx_q8_gemm_quantize_group): up to

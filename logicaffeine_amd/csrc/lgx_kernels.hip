@@ -91,15 +91,17 @@ __device__ __forceinline__ float wave_tree_sum(float l) {
     return l + dpp_f<0x101>(l);
 }
 
-// Q8_0 of one 32-block held by 8 consecutive lanes (4 values each): the
-// lgx_k_quantize_q8_0 rule.  Returns the packed quants of this lane's four
-// values and the binary16 scale.
 __device__ __forceinline__ float4 add4(const float4& x, const float4& y) {
     return make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
 }
-__device__ __forceinline__ uint32_t quantize4(const float (&f)[4], uint16_t& dh) {
-    float am = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
-    am = max8(am);
+// Largest |f| of a lane's four values (the block maximum is the fmaxf of
+// these over the block's lanes, in any order).
+__device__ __forceinline__ float absmax4(const float (&f)[4]) {
+    return fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
+}
+// The lgx_k_quantize_q8_0 rule for four values of a 32-block whose largest
+// |value| is am: the packed quants and the binary16 scale.
+__device__ __forceinline__ uint32_t quantize4_am(const float (&f)[4], float am, uint16_t& dh) {
     const float d = am / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     uint32_t qw = 0;
@@ -111,6 +113,10 @@ __device__ __forceinline__ uint32_t quantize4(const float (&f)[4], uint16_t& dh)
     }
     dh = f2h(d);
     return qw;
+}
+// Q8_0 of one 32-block held by 8 consecutive lanes (4 values each).
+__device__ __forceinline__ uint32_t quantize4(const float (&f)[4], uint16_t& dh) {
+    return quantize4_am(f, max8(absmax4(f)), dh);
 }
 
 // ---------------------------------------------------------------------------
@@ -3345,7 +3351,9 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_act_to_t16(const lgx_act
 // at most four ranges: earlier + later, as in the level-by-level tree) and
 // the group's values go to part[g]: aligned groups of a power-of-two number
 // of ranges are subtrees of the canonical tree, so the tree over the groups
-// is the tree over all ranges.
+// is the tree over all ranges.  A gate|up product in one group can instead
+// finish with SwiGLU + Q8_0 in the workgroup (a.swiglu): its tile slots then
+// pair each gate tile with the up tile of the same columns.
 // Staging: two LDS stages of LGX_TG_S pairs filled by direct global->LDS
 // loads, 16-byte lanes for the T16 tiles and 4-byte lanes for the scale
 // pairs of a 64-column pair, which land pre-arranged: dw as [pair][64 rows]
@@ -3392,6 +3400,14 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a, cons
 
     const int np = a.k >> 6, nb = a.k >> 5, nh = (a.k + 511) >> 9;
     const int ntw = a.n >> 4, ntx = (a.m + 15) >> 4;
+    // Weight row tile of the workgroup's tile slot s (0..3).  With the SwiGLU
+    // consumer, slot 2w is the gate tile and slot 2w + 1 the up tile of the
+    // same 16 columns 32 tn + 16 w (gate rows [0, I), up rows [I, 2I)), so
+    // wave (w, .) holds both factors of its outputs.
+    const int swi = a.swiglu;
+    auto wtile = [&](int s) {
+        return swi ? (s & 1) * (swi >> 4) + 2 * tn + (s >> 1) : min(tn0 + s, ntw - 1);
+    };
     const int gpairs = a.grp * (LGX_Q8_RANGE_BLOCKS / 2);
     const int pg0 = g * gpairs;
     const int pend = min(pg0 + gpairs, np);
@@ -3407,7 +3423,7 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a, cons
     //   activation scale pairs: [s][r][tile], wave instructions j = wave < WM
     static_assert(LGX_TG_S == 2, "stage layout");
     const uint32_t off_t16 = lane * 16;
-    const uint32_t off_dw = ((uint32_t)min(tn0 + (lane >> 4), ntw - 1) * nh * 256 + (lane & 15) * 16) * 2;
+    const uint32_t off_dw = ((uint32_t)wtile(lane >> 4) * nh * 256 + (lane & 15) * 16) * 2;
     const int dxp = (wave * 64 + lane) % (16 * MTILES);            // position within a pair
     const int dx_ml = (dxp % MTILES) * 16 + dxp / MTILES;
     const uint32_t off_dx = (uint32_t)min(tm0 * 16 + dx_ml, a.m - 1) * nb * 2;
@@ -3416,7 +3432,7 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a, cons
         for (int i = 0; i < LGX_TG_S; ++i) {
             const int j = wave + 4 * i;
             const int tile = j / LGX_TG_S, s = j - tile * LGX_TG_S;
-            const int t = min(tn0 + tile, ntw - 1), p = min(pair0 + s, pend - 1);
+            const int t = wtile(tile), p = min(pair0 + s, pend - 1);
             const char* base = (const char*)a.wt + ((int64_t)t * np + p) * 1024;
             __builtin_amdgcn_global_load_lds((const void*)(base + off_t16), (lds_void*)&sm.w[tile][s][0], 16, 0, 0);
         }
@@ -3561,6 +3577,39 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a, cons
         run(q, sm0, sm1);
         if (q + 1 < nst) run(q + 1, sm1, sm0);
     }
+    // the group's value of element (i, j, v)
+    auto fin = [&](int i, int j, int v) {
+        return cnt == 1 ? l0[i][j][v] : cnt == 3 ? l1[i][j][v] + l0[i][j][v] : l1[i][j][v];
+    };
+    if (swi) {
+        // SwiGLU + Q8_0 (the lgx_k_swiglu_quant operations on a one-group
+        // product): lane (r, c) of wave (w, wm) holds columns 32 tn + 16 w +
+        // 4c .. +3 of activation row r of each tile j; the 32-block of a row
+        // is its four lanes c in both waves w, whose maxima meet in LDS
+        __shared__ float qm_s[2][WM][16][2];
+        const int nbl = swi >> 5;
+        float f[WM][4], am[WM];
+#pragma unroll
+        for (int j = 0; j < WM; ++j) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) f[j][v] = lgx_silu(fin(0, j, v)) * fin(1, j, v);
+            am[j] = absmax4(f[j]);
+            am[j] = fmaxf(am[j], shfl_xor_f(am[j], 16));
+            am[j] = fmaxf(am[j], shfl_xor_f(am[j], 32));
+            if (c == 0) qm_s[wm][j][r][wn] = am[j];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < WM; ++j) {
+            const int m = (tm0 + WM * wm + j) * 16 + r;
+            uint16_t dh;
+            const uint32_t qw = quantize4_am(f[j], fmaxf(qm_s[wm][j][r][0], qm_s[wm][j][r][1]), dh);
+            if (m >= a.m) continue;
+            *(uint32_t*)(a.sq + t16_off(m, 32 * tn + 16 * wn + 4 * c, swi)) = qw;
+            if (wn == 0 && c == 0) a.sd[(int64_t)m * nbl + tn] = dh;
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int t = tn0 + 2 * wn + i;
@@ -3572,8 +3621,7 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a, cons
             if (m >= a.m) continue;
             float f[4];
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
-                f[v] = cnt == 1 ? l0[i][j][v] : cnt == 3 ? l1[i][j][v] + l0[i][j][v] : l1[i][j][v];
+            for (int v = 0; v < 4; ++v) f[v] = fin(i, j, v);
             *(float4*)(a.part + ((int64_t)g * a.m + m) * a.n + n0) = make_float4(f[0], f[1], f[2], f[3]);
         }
     }

@@ -68,8 +68,8 @@ struct lgx_model {
     float* xn = nullptr;
     int8_t* xq = nullptr;
     uint16_t* xd = nullptr;
-    int8_t* sq = nullptr;          // fused SwiGLU output (Q8_0 [max_batch][inter]): the
-    uint16_t* sd = nullptr;        // gate|up product still reads xq while it is written
+    int8_t* sq = nullptr;          // fused SwiGLU output (Q8_0 [max_batch][inter], T16 tiles
+    uint16_t* sd = nullptr;        // for the tiled products): the gate|up product still reads xq
     float* q = nullptr;
     float* part = nullptr;
     float* attn_part = nullptr;
@@ -101,6 +101,8 @@ struct lgx_model {
         float* q = nullptr;          // [rows][hq][d]
         float* part = nullptr;       // group partials of the products
         float* attn_part = nullptr;  // [rows][hq][nchunk][d + 2]
+        int8_t* sq = nullptr;        // [rows16][I] SwiGLU Q8_0 in T16 tiles (fused gate|up)
+        uint16_t* sd = nullptr;      // [rows][I / 32]
     } pf;
 
     ~lgx_model() {
@@ -296,6 +298,14 @@ lgx_status product(lgx_model* md, const DevQ8& W, int m, void* stream,
                   nullptr, md->part);
 }
 
+// Tiled gate|up products that finish with SwiGLU + Q8_0 in their own
+// workgroups (into sq / sd): the whole reduction in one range group.
+bool tiled_swiglu(const lgx_model* md, int m) {
+    const lgx_ctx* c = md->ctx;
+    return c->tiled_swiglu && dec_tiled(md, m) && md->c.intermediate % 32 == 0 &&
+           parts(md, md->gu[0], m) == 1;
+}
+
 // Decode products whose consumer runs in the product's own workgroups
 // (lgx_k_q8_gemm_mfma16_qkv / _swiglu): 2+ rows on the streaming kernels
 // and K in one range, so every output is final where it is computed.
@@ -427,6 +437,15 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
             if ((st = product(md, md->dn[l], B, stream, md->sq, md->sd)) != LGX_OK) return st;
             continue;
         }
+        if (tiled_swiglu(md, B)) {
+            const Kern kern = tiled_kernel(c, B);
+            const DevQ8& W = md->gu[l];
+            if ((st = run_q8_tiled(c, &W.m, md->xq, md->xd, B, md->part, stream, kern,
+                                   tiled_grp(c, kern, W.m.n, W.m.k, B), I, md->sq, md->sd)) != LGX_OK)
+                return st;
+            if ((st = product(md, md->dn[l], B, stream, md->sq, md->sd)) != LGX_OK) return st;
+            continue;
+        }
         if ((st = product(md, md->gu[l], B, stream)) != LGX_OK) return st;
         lgx_swiglu_args sw{md->part, parts(md, md->gu[l], B), md->xq, md->xd, nullptr, B, I,
                            dec_tiled(md, B) ? 1 : 0};
@@ -506,7 +525,8 @@ lgx_status prefill_alloc(lgx_model* md) {
         (st = dev_alloc(md, &pf.xt, (size_t)rows16 * kmax)) ||
         (st = dev_alloc(md, &pf.xd, (size_t)rows * kmax / 32)) ||
         (st = dev_alloc(md, &pf.q, (size_t)rows * hq * d)) || (st = dev_alloc(md, &pf.part, (size_t)part)) ||
-        (st = dev_alloc(md, &pf.attn_part, (size_t)rows * hq * md->nchunk * (d + 2))))
+        (st = dev_alloc(md, &pf.attn_part, (size_t)rows * hq * md->nchunk * (d + 2))) ||
+        (st = dev_alloc(md, &pf.sq, (size_t)rows16 * I)) || (st = dev_alloc(md, &pf.sd, (size_t)rows * I / 32)))
         return st;
     pf.chunk = chunk;
     return LGX_OK;
@@ -604,6 +624,14 @@ lgx_status prefill_chunk(lgx_model* md, int B, int n, const int32_t* tokens, int
         if ((st = pf_product(md, md->o[l], M, stream)) != LGX_OK) return st;
         if ((st = pf_norm(md, md->ffn_norm[l], M, H, tiled_groups(hq * d), true, stream)) != LGX_OK)
             return st;
+        if (c->tiled_swiglu && I % 32 == 0 && tiled_groups(H) == 1) {
+            // SwiGLU + Q8_0 in the gate|up product's workgroups, into pf.sq / pf.sd
+            if ((st = run_q8_tiled(c, &md->gu[l].m, pf.xt, pf.xd, M, pf.part, stream, K_GEMM_TILED,
+                                   LGX_TG_RANGES, I, pf.sq, pf.sd)) != LGX_OK ||
+                (st = run_q8_tiled(c, &md->dn[l].m, pf.sq, pf.sd, M, pf.part, stream)) != LGX_OK)
+                return st;
+            continue;
+        }
         if ((st = pf_product(md, md->gu[l], M, stream)) != LGX_OK) return st;
         lgx_swiglu_args sw{pf.part, tiled_groups(H), pf.xt, pf.xd, nullptr, M, I, 1};
         if ((st = launch(c, K_SWIGLU_QUANT, dim3(M, cdiv(I / 32, 32)), dim3(256), sw, stream)) != LGX_OK)
@@ -814,7 +842,7 @@ lgx_status model_build(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed, So
         if ((st = dev_alloc(m, &m->h, (size_t)B * H)) || (st = dev_alloc(m, &m->xn, (size_t)B * H)) ||
             (st = dev_alloc(m, &m->xq, (size_t)(B + 15) / 16 * 16 * kmax)) ||
             (st = dev_alloc(m, &m->xd, (size_t)B * kmax / 32)) ||
-            (st = dev_alloc(m, &m->sq, (size_t)B * I)) ||
+            (st = dev_alloc(m, &m->sq, (size_t)(B + 15) / 16 * 16 * I)) ||
             (st = dev_alloc(m, &m->sd, (size_t)B * I / 32)) ||
             (st = dev_alloc(m, &m->q, (size_t)B * hq * d)) || (st = dev_alloc(m, &m->part, (size_t)part)) ||
             (st = dev_alloc(m, &m->attn_part, (size_t)B * hq * m->nchunk * (d + 2))) ||

@@ -120,24 +120,16 @@ def test_prefill_then_decode_bit_exact(pair, ctx):
                 assert np.array_equal(got, om.kv(layer, which, b, int(lens[b]))), (layer, b, which)
 
 
-@pytest.mark.parametrize("chunk", [48, 16])
-def test_chunked_prefill_equals_oracle(chunk):
+@pytest.mark.parametrize("chunk,env", [(48, {}), (16, {}), (48, dict(LGX_TILED_SWIGLU="0"))])
+def test_chunked_prefill_equals_oracle(chunk, env):
     """The batched prefill in several chunks (positions per chunk forced
     small: chunk boundaries inside and across 256-token attention chunks,
-    ragged starting lengths) leaves the oracle's tokens, logits and KV bits."""
-    import os
-
+    ragged starting lengths) leaves the oracle's tokens, logits and KV bits,
+    with SwiGLU + Q8_0 inside the gate|up product (default) or in a kernel of
+    its own."""
     from oracle import oracle as orc
 
-    old = os.environ.get("LGX_PREFILL_CHUNK")
-    os.environ["LGX_PREFILL_CHUNK"] = str(chunk)
-    try:
-        c = lgx.Context(0)
-    finally:
-        if old is None:
-            os.environ.pop("LGX_PREFILL_CHUNK")
-        else:
-            os.environ["LGX_PREFILL_CHUNK"] = old
+    c = _ctx_with(dict(env, LGX_PREFILL_CHUNK=str(chunk)))
     cfg = orc.qwen_config("tiny_untied")
     gm = lgx.Model(c, cfg, 31)
     om = orc.Model(cfg, 31)
@@ -169,14 +161,18 @@ def test_chunked_prefill_equals_oracle(chunk):
     c.close()
 
 
+@pytest.mark.parametrize("env", [{}, dict(LGX_TILED_SWIGLU="0")])
 @pytest.mark.parametrize("name", ["tiny", "tiny_untied"])
-def test_wide_batch_decode_bit_exact(name, ctx):
+def test_wide_batch_decode_bit_exact(name, env):
     """Batches of 33 or more sequences take the tiled products, whose
     activations the norms, attention merge and SwiGLU write in T16 tiles:
     40 sequences (a ragged last row tile) prefilled and decoded agree with
-    the oracle in tokens, logits and KV bits, graph replays included."""
+    the oracle in tokens, logits and KV bits, graph replays included.  The
+    gate|up product runs SwiGLU + Q8_0 in its own workgroups (default) or
+    leaves its outputs to the SwiGLU kernel (LGX_TILED_SWIGLU=0)."""
     from oracle import oracle as orc
 
+    ctx = _ctx_with(env)
     cfg = dict(orc.qwen_config(name), max_batch=40, max_seq=64)
     gm = lgx.Model(ctx, cfg, 5)
     om = orc.Model(cfg, 5)
@@ -206,6 +202,7 @@ def test_wide_batch_decode_bit_exact(name, ctx):
                                       om.kv(layer, which, b, L)), (layer, b, which)
     gm.close()
     om.close()
+    ctx.close()
 
 
 def test_decode_uses_only_first_B_sequences(pair, ctx):
