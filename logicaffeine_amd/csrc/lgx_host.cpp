@@ -79,6 +79,7 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
         c->tiled_rows = env_int("LGX_GEMM_TILED_ROWS", 0);
         c->tiled_grp = env_int("LGX_GEMM_TILED_GRP", 0);
         if (c->tiled_grp != 1 && c->tiled_grp != 2 && c->tiled_grp != 4) c->tiled_grp = 0;
+        c->tiled_wpc = std::max(1, env_int("LGX_GEMM_TILED_WPC", 4));
         const char* dg = getenv("LGX_DECODE_GEMM");
         c->decode_streaming = dg && std::string(dg) == "streaming";
         const char* pfv = getenv("LGX_PREFILL");

@@ -208,6 +208,7 @@ struct lgx_ctx {
     int tiled_min = 33;           // LGX_GEMM_TILED_MIN: smallest m through the tiled product
     int tiled_rows = 0;           // LGX_GEMM_TILED_ROWS: force 128/64/32 activation rows per workgroup
     int tiled_grp = 0;            // LGX_GEMM_TILED_GRP: force 1/2/4 ranges per group
+    int tiled_wpc = 4;            // LGX_GEMM_TILED_WPC: workgroups per CU the automatic group choice keeps
     bool decode_streaming = false; // LGX_DECODE_GEMM=streaming: decode products of m >= 17
                                    // rows through the streaming kernels
     bool decode_fuse = true;      // LGX_DECODE_FUSE=0: decode glue in kernels of its own
@@ -545,7 +546,7 @@ inline int tiled_grp(const lgx_ctx* c, Kern kern, int n, int k, int m) {
     const int mrows = kern == K_GEMM_TILED ? 128 : kern == K_GEMM_TILED64 ? 64 : 32;
     const int64_t tiles = (int64_t)cdiv(n, LGX_TG_N) * cdiv(m, mrows);
     for (int grp = 4; grp > 1; grp >>= 1)
-        if (tiles * tiled_groups(k, grp) >= 4LL * c->ncu) return grp;
+        if (tiles * tiled_groups(k, grp) >= (int64_t)c->tiled_wpc * c->ncu) return grp;
     return 1;
 }
 

@@ -1750,56 +1750,72 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
 // D threads per (sequence, head), called by every thread.  The maxima are
 // read with one load per thread and chunk stride D (the max is exact in any
 // order); w_c and l_c of up to 256 chunks at a time go to LDS, computed once
-// per chunk; thread i then runs both chains in chunk order, its o_c[i] loaded
-// 16 chunks at a time (the last group masked) so their loads overlap.
+// per chunk; thread i then runs both chains in chunk order.  Up to 32 chunks,
+// every partial a thread needs is requested at once (one memory round); past
+// that its o_c[i] are loaded 16 chunks at a time, the next 16 in flight while
+// the current 16 enter the chains.
+//
+// One memory round for up to FC (<= D) chunks: every partial this thread may
+// need (chunk i's m and l, o_c[i] of every chunk) requested together with
+// the length; chunks at or past nc are never used (unconditional loads at
+// clamped chunk indices: a load under a branch makes the compiler wait for
+// every load where paths join).
+template <int D, int FC>
+__device__ __forceinline__ float attn_merge_one_round(const lgx_attn_args& a, const float* pp, int row,
+                                                      int b, int qpr, float* w_s, float* l_s,
+                                                      float* red_s) {
+    const int i = threadIdx.x, lane = i & 63, wave = i >> 6;
+    const int ic = min(i, a.nchunk - 1);
+    const float mc = pp[ic * (D + 2) + D], lc = pp[ic * (D + 2) + D + 1];
+    float ov[FC];
+#pragma unroll
+    for (int c = 0; c < FC; ++c) ov[c] = pp[min(c, a.nchunk - 1) * (D + 2) + i];
+    const int L = min(a.seq_len[b] + (row - b * qpr) + a.len_add, a.maxlen);
+    const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
+    float M = wave_max(i < nc ? mc : -__builtin_inff());
+    if constexpr (D > 64) {
+        if (lane == 0) red_s[wave] = M;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < D / 64; ++w) M = fmaxf(M, red_s[w]);
+    }
+    if (i < nc) {
+        w_s[i] = lgx_expf(mc - M);
+        l_s[i] = lc;
+    }
+    __syncthreads();
+    float Ls = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int c = 0; c < FC; ++c) {
+        if (c < nc) {                             // uniform
+            Ls = fmaf(w_s[c], l_s[c], Ls);
+            O = fmaf(w_s[c], ov[c], O);
+        }
+    }
+    return nc > 0 ? O / Ls : 0.0f;
+}
+
 template <int D>
 __device__ __forceinline__ float attn_merge(const lgx_attn_args& a, int bh) {
     constexpr int TCH = 256;                      // chunks per LDS tile
-    constexpr int FC = 16;                        // chunk count of the one-round path
     __shared__ float w_s[TCH], l_s[TCH], red_s[D / 64];
     const int i = threadIdx.x, lane = i & 63, wave = i >> 6;
     const int qpr = max(a.qpr, 1);
     const int row = bh / a.hq, b = row / qpr;
     const float* pp = a.part + (int64_t)bh * a.nchunk * (D + 2);
-    if (a.nchunk <= FC) {
-        // every partial this thread may need (chunk i's m and l, o_c[i] of
-        // every chunk) requested together with the length; chunks at or past
-        // nc are never used
-        // (unconditional loads at clamped chunk indices: a load under a
-        // branch makes the compiler wait for every load where paths join)
-        const int ic = min(i, a.nchunk - 1);
-        const float mc = pp[ic * (D + 2) + D], lc = pp[ic * (D + 2) + D + 1];
-        float ov[FC];
+    if (a.nchunk <= 16) return attn_merge_one_round<D, 16>(a, pp, row, b, qpr, w_s, l_s, red_s);
+    if (a.nchunk <= 32) return attn_merge_one_round<D, 32>(a, pp, row, b, qpr, w_s, l_s, red_s);
+    // chunk i's m and l and the first 16 o_c[i] requested with the length
+    // (clamped chunk indices; values past nc are never used)
+    const int ic = min(i, a.nchunk - 1);
+    const float mc = pp[ic * (D + 2) + D], lc = pp[ic * (D + 2) + D + 1];
+    float ov[16], on[16];
 #pragma unroll
-        for (int c = 0; c < FC; ++c) ov[c] = pp[min(c, a.nchunk - 1) * (D + 2) + i];
-        const int L = min(a.seq_len[b] + (row - b * qpr) + a.len_add, a.maxlen);
-        const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
-        float M = wave_max(i < nc ? mc : -__builtin_inff());
-        if constexpr (D > 64) {
-            if (lane == 0) red_s[wave] = M;
-            __syncthreads();
-#pragma unroll
-            for (int w = 0; w < D / 64; ++w) M = fmaxf(M, red_s[w]);
-        }
-        if (i < nc) {
-            w_s[i] = lgx_expf(mc - M);
-            l_s[i] = lc;
-        }
-        __syncthreads();
-        float Ls = 0.0f, O = 0.0f;
-#pragma unroll
-        for (int c = 0; c < FC; ++c) {
-            if (c < nc) {                         // uniform
-                Ls = fmaf(w_s[c], l_s[c], Ls);
-                O = fmaf(w_s[c], ov[c], O);
-            }
-        }
-        return nc > 0 ? O / Ls : 0.0f;
-    }
+    for (int u = 0; u < 16; ++u) ov[u] = pp[min(u, a.nchunk - 1) * (D + 2) + i];
     const int L = min(a.seq_len[b] + (row - b * qpr) + a.len_add, a.maxlen);
     const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
-    float M = -__builtin_inff();
-    for (int c = i; c < nc; c += D) M = fmaxf(M, pp[c * (D + 2) + D]);
+    float M = i < nc ? mc : -__builtin_inff();
+    for (int c = i + D; c < nc; c += D) M = fmaxf(M, pp[c * (D + 2) + D]);
     M = wave_max(M);
     if (lane == 0) red_s[wave] = M;
     __syncthreads();
@@ -1809,17 +1825,29 @@ __device__ __forceinline__ float attn_merge(const lgx_attn_args& a, int bh) {
     for (int c0 = 0; c0 < nc; c0 += TCH) {        // nc is uniform: every thread takes the barriers
         const int cn = min(TCH, nc - c0);
         __syncthreads();                          // the previous tile is consumed
-        for (int c = i; c < cn; c += D) {
+        int c = i;
+        if (c0 == 0 && i < cn) {                  // chunk i from the registers
+            w_s[i] = lgx_expf(mc - M);
+            l_s[i] = lc;
+            c += D;
+        }
+        for (; c < cn; c += D) {
             const float* q = pp + (c0 + c) * (D + 2);
             w_s[c] = lgx_expf(q[D] - M);
             l_s[c] = q[D + 1];
         }
         __syncthreads();
         const float* po = pp + (int64_t)c0 * (D + 2) + i;
-        for (int c = 0; c < cn; c += 16) {
-            float ov[16];
+        // o_c[i] 16 chunks at a time, the next 16 requested before the
+        // current 16 enter the chains (unconditional loads at clamped chunk
+        // indices; the values past cn are never used)
+        if (c0 > 0) {
 #pragma unroll
-            for (int u = 0; u < 16; ++u) ov[u] = c + u < cn ? po[(c + u) * (D + 2)] : 0.0f;
+            for (int u = 0; u < 16; ++u) ov[u] = po[min(u, cn - 1) * (D + 2)];
+        }
+        for (int c = 0; c < cn; c += 16) {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) on[u] = po[min(c + 16 + u, cn - 1) * (D + 2)];
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
                 if (c + u < cn) {                 // uniform
@@ -1827,6 +1855,8 @@ __device__ __forceinline__ float attn_merge(const lgx_attn_args& a, int bh) {
                     O = fmaf(w_s[c + u], ov[u], O);
                 }
             }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) ov[u] = on[u];
         }
     }
     return nc > 0 ? O / Ls : 0.0f;

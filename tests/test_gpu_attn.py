@@ -63,6 +63,20 @@ def test_config2_ragged_long_bit_exact(ctx, orc):
     assert np.array_equal(out, orc.gqa_decode_attn(q, k, v, pt, np.asarray(lens, np.int32)))
 
 
+@pytest.mark.parametrize("d,hq", [(64, 14), (128, 12)])
+def test_very_long_context_merge_bit_exact(ctx, orc, d, hq):
+    """Contexts past 64 Ki tokens (more than 256 chunks: the merge runs
+    several LDS tiles, and more chunks than threads), next to a short one
+    and an empty one in the same call."""
+    B, hkv = 3, 2
+    lens = [70000, 3000, 0]
+    k, v, pt, _ = make_cache(B, hkv, d, lens, seed=d + 7)
+    q = orc.gen_normal_f32(2, 40 + d, (B, hq, d))
+    out = run(ctx, q, k, v, pt, lens)
+    assert np.array_equal(out, orc.gqa_decode_attn(q, k, v, pt, np.asarray(lens, np.int32)))
+    assert np.all(out[2] == 0.0)
+
+
 @pytest.mark.parametrize("hq,hkv,d", [(2 * g, 2, d) for d in (64, 128) for g in range(1, 9)]
                          + [(28, 4, 128), (8, 8, 64), (8, 1, 128)])
 def test_head_layouts_bit_exact(ctx, orc, hq, hkv, d):
