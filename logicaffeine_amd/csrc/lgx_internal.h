@@ -134,6 +134,7 @@ enum Kern {
     K_LM_ROWCONST,
     K_LM_CERT,
     K_LM_PICK,
+    K_NORM4S_R8,
     K_COUNT
 };
 inline const char* const kKernelNames[] = {
@@ -167,7 +168,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_q8_gemm_mfma16_qkv", "lgx_k_q8_gemm_mfma16_swiglu", "lgx_k_add_rmsnorm_quant_w",
     "lgx_k_q8_gemm_mfma16_group", "lgx_k_q8_gemm_mfma32_group", "lgx_k_q8_gemm_tiled_group", "lgx_k_q8_gemm_tiled64_group",
     "lgx_k_q8_gemm_tiled32_group", "lgx_k_quantize_group", "lgx_k_q8_combine_group",
-    "lgx_k_lm_rowconst", "lgx_k_lm_cert", "lgx_k_lm_pick",
+    "lgx_k_lm_rowconst", "lgx_k_lm_cert", "lgx_k_lm_pick", "lgx_k_add_rmsnorm_quant4s_r8",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -327,8 +328,12 @@ inline lgx_status launch_norm(lgx_ctx* c, const lgx_norm_args& a, void* stream) 
         (!a.xq || a.n % 32 == 0))
         return launch(c, K_NORM_W, dim3(cdiv(a.m, c->norm_waves)), dim3(64 * c->norm_waves), a,
                       stream, 0u);
-    if (a.n % 4 == 0 && a.n <= 4096 && nr <= 20)
-        return launch(c, nr <= 8 ? K_NORM4_R8 : K_NORM4_R20, dim3(a.m), dim3(512), a, stream, 0u);
+    // float4 slots through buffer descriptors: the partials' byte span must
+    // stay below 2^31
+    const bool span_ok = !a.part || ((int64_t)(nr - 1) * a.m * a.n + a.n) * 4 < (1LL << 31);
+    if (a.n % 4 == 0 && a.n <= 4096 && nr <= 20 && span_ok)
+        return launch(c, nr > 8 ? K_NORM4_R20 : a.n <= 2048 ? K_NORM4S_R8 : K_NORM4_R8, dim3(a.m),
+                      dim3(512), a, stream, 0u);
     return launch(c, K_ADD_RMSNORM_QUANT, dim3(a.m), dim3(LGX_GLUE_NT), a, stream, 0u);
 }
 inline int argmax_slices(int vocab) { return (vocab + LGX_ARGMAX_SLICE - 1) / LGX_ARGMAX_SLICE; }

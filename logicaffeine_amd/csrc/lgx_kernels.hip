@@ -2054,22 +2054,36 @@ __device__ __forceinline__ void norm_body(const lgx_norm_args& a) {
         if (NT * k < a.n) wk[k] = a.w[min(t + NT * k, a.n - 1)];   // uniform test, clamped index
     float v[KV];
     if constexpr (S > 0) {
+        // h and the partials through buffer descriptors: every load is
+        // issued (the wait counts stay exact), and those of slots past the
+        // row or ranges past nr fall outside the descriptor, so they read
+        // zeros without a memory access (the launcher keeps the partials'
+        // byte span below 2^31)
         const int n4 = a.n >> 2;
+        constexpr uint32_t OOB = 0x80000000u;
+        const __amdgpu_buffer_rsrc_t hrs =
+            __builtin_amdgcn_make_buffer_rsrc((void*)hr, 0, a.n * 4, LGX_BUF_DWORD3);
         float4 x4[S];
 #pragma unroll
         for (int k = 0; k < S; ++k)
-            x4[k] = *(const float4*)(hr + 4 * min(t + NT * k, n4 - 1));
+            x4[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   hrs, t + NT * k < n4 ? 16u * (t + NT * k) : OOB, 0, 0));
         if (a.part) {
-            // every load issued (range index clamped), consumed in order
+            // every load issued, consumed in order
             float4 pv[S][R];
             const int64_t stride = (int64_t)a.m * a.n;
-            const float* pb = a.part + (int64_t)b * a.n;
+            const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(a.part + (int64_t)b * a.n), 0, (int)(((a.nr - 1) * stride + a.n) * 4),
+                LGX_BUF_DWORD3);
 #pragma unroll
             for (int j = 0; j < R; ++j)
 #pragma unroll
-                for (int k = 0; k < S; ++k)
-                    pv[k][j] = *(const float4*)(pb + min(j, a.nr - 1) * stride +
-                                                4 * min(t + NT * k, n4 - 1));
+                for (int k = 0; k < S; ++k) {
+                    const uint32_t off = j < a.nr && t + NT * k < n4
+                                             ? (uint32_t)((j * stride + 4 * (t + NT * k)) * 4)
+                                             : OOB;
+                    pv[k][j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, 0));
+                }
 #pragma unroll
             for (int k = 0; k < S; ++k) {
                 x4[k] = add4(x4[k], tree_stream4<R>(pv[k], a.nr));
@@ -2158,7 +2172,11 @@ __device__ __forceinline__ void norm_body(const lgx_norm_args& a) {
 extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_add_rmsnorm_quant(const lgx_norm_args a) {
     norm_body<LGX_GLUE_NT, 0, 1>(a);
 }
-// n % 4 == 0, n <= 4096: 512 threads, two float4 slots each, nr <= 8 / 20
+// n % 4 == 0, n <= 4096: 512 threads, two float4 slots each, nr <= 8 / 20;
+// n <= 2048: one slot each
+extern "C" __global__ __launch_bounds__(512) void lgx_k_add_rmsnorm_quant4s_r8(const lgx_norm_args a) {
+    norm_body<512, 1, 8>(a);
+}
 extern "C" __global__ __launch_bounds__(512) void lgx_k_add_rmsnorm_quant4_r8(const lgx_norm_args a) {
     norm_body<512, 2, 8>(a);
 }

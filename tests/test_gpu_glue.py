@@ -63,12 +63,14 @@ def _tree_rows(part):
 @pytest.mark.parametrize("m,n,nr", [(3, 896, 1), (4, 896, 5), (80, 896, 5), (64, 896, 8), (66, 256, 8),
                                     (64, 1024, 3), (71, 64, 2), (64, 1000, 1), (2, 3584, 4), (5, 3584, 19),
                                     (2, 4096, 8), (2, 4096, 20), (2, 3584, 21), (1, 8192, 32),
-                                    (2, 1000, 9), (1, 4096, 13)])
+                                    (2, 1000, 9), (1, 4096, 13), (3, 1000, 4), (2, 2048, 6),
+                                    (2, 2052, 3)])
 def test_add_rmsnorm_quant_bit_exact(ctx, orc, m, n, nr):
     """Residual form: h += tree of the range partials (one wave per row for
     64+ rows of n % 4 == 0, n <= 1024, nr <= 8; the float4-slot kernels for
-    n <= 4096, nr <= 20; the general kernel past those), written back, then
-    the RMSNorm + Q8_0 of the new h."""
+    n <= 4096, nr <= 20, one slot per thread up to n = 2048 and nr = 8; the
+    general kernel past those), written back, then the RMSNorm + Q8_0 of the
+    new h."""
     rng = np.random.default_rng(m * 7 + n + nr)
     part = rng.standard_normal((nr, m, n)).astype(np.float32)
     h = (rng.standard_normal((m, n)) * 3).astype(np.float32)
