@@ -1755,21 +1755,33 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
 // that its o_c[i] are loaded 16 chunks at a time, the next 16 in flight while
 // the current 16 enter the chains.
 //
+// Loads of the partials pp[(c, j)] = pp[c * (D + 2) + j] of chunks c < nch
+// through a buffer descriptor: every load is issued (no load under a branch,
+// whose join would wait for every load in flight), and those of chunks at or
+// past nch read zeros without a memory access.
+template <int D>
+struct MergeRd {
+    __amdgpu_buffer_rsrc_t r;
+    __device__ MergeRd(const float* pp, int nch)
+        : r(__builtin_amdgcn_make_buffer_rsrc((void*)pp, 0, nch * (D + 2) * 4, LGX_BUF_DWORD3)) {}
+    __device__ float operator()(int c, int j) const {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (c * (D + 2) + j) * 4, 0, 0));
+    }
+};
+
 // One memory round for up to FC (<= D) chunks: every partial this thread may
 // need (chunk i's m and l, o_c[i] of every chunk) requested together with
-// the length; chunks at or past nc are never used (unconditional loads at
-// clamped chunk indices: a load under a branch makes the compiler wait for
-// every load where paths join).
+// the length; chunks at or past nc are never used.
 template <int D, int FC>
 __device__ __forceinline__ float attn_merge_one_round(const lgx_attn_args& a, const float* pp, int row,
                                                       int b, int qpr, float* w_s, float* l_s,
                                                       float* red_s) {
     const int i = threadIdx.x, lane = i & 63, wave = i >> 6;
-    const int ic = min(i, a.nchunk - 1);
-    const float mc = pp[ic * (D + 2) + D], lc = pp[ic * (D + 2) + D + 1];
+    const MergeRd<D> rd(pp, a.nchunk);
+    const float mc = rd(i, D), lc = rd(i, D + 1);
     float ov[FC];
 #pragma unroll
-    for (int c = 0; c < FC; ++c) ov[c] = pp[min(c, a.nchunk - 1) * (D + 2) + i];
+    for (int c = 0; c < FC; ++c) ov[c] = rd(c, i);
     const int L = min(a.seq_len[b] + (row - b * qpr) + a.len_add, a.maxlen);
     const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
     float M = wave_max(i < nc ? mc : -__builtin_inff());
@@ -1806,12 +1818,12 @@ __device__ __forceinline__ float attn_merge(const lgx_attn_args& a, int bh) {
     if (a.nchunk <= 16) return attn_merge_one_round<D, 16>(a, pp, row, b, qpr, w_s, l_s, red_s);
     if (a.nchunk <= 32) return attn_merge_one_round<D, 32>(a, pp, row, b, qpr, w_s, l_s, red_s);
     // chunk i's m and l and the first 16 o_c[i] requested with the length
-    // (clamped chunk indices; values past nc are never used)
-    const int ic = min(i, a.nchunk - 1);
-    const float mc = pp[ic * (D + 2) + D], lc = pp[ic * (D + 2) + D + 1];
+    // (values past nc are never used)
+    const MergeRd<D> rd0(pp, a.nchunk);
+    const float mc = rd0(i, D), lc = rd0(i, D + 1);
     float ov[16], on[16];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) ov[u] = pp[min(u, a.nchunk - 1) * (D + 2) + i];
+    for (int u = 0; u < 16; ++u) ov[u] = rd0(u, i);
     const int L = min(a.seq_len[b] + (row - b * qpr) + a.len_add, a.maxlen);
     const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
     float M = i < nc ? mc : -__builtin_inff();
@@ -1837,17 +1849,16 @@ __device__ __forceinline__ float attn_merge(const lgx_attn_args& a, int bh) {
             l_s[c] = q[D + 1];
         }
         __syncthreads();
-        const float* po = pp + (int64_t)c0 * (D + 2) + i;
         // o_c[i] 16 chunks at a time, the next 16 requested before the
-        // current 16 enter the chains (unconditional loads at clamped chunk
-        // indices; the values past cn are never used)
+        // current 16 enter the chains (the values past cn are never used)
+        const MergeRd<D> rd(pp + (int64_t)c0 * (D + 2), cn);
         if (c0 > 0) {
 #pragma unroll
-            for (int u = 0; u < 16; ++u) ov[u] = po[min(u, cn - 1) * (D + 2)];
+            for (int u = 0; u < 16; ++u) ov[u] = rd(u, i);
         }
         for (int c = 0; c < cn; c += 16) {
 #pragma unroll
-            for (int u = 0; u < 16; ++u) on[u] = po[min(c + 16 + u, cn - 1) * (D + 2)];
+            for (int u = 0; u < 16; ++u) on[u] = rd(c + 16 + u, i);
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
                 if (c + u < cn) {                 // uniform
