@@ -90,6 +90,7 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
         c->tiled_swiglu = env_int("LGX_TILED_SWIGLU", 1) != 0;
         c->norm_waves = std::min(std::max(env_int("LGX_NORM_WAVES", 1), 0), 4);
         c->lm_cert = env_int("LGX_LM_CERT", 1) != 0;
+        c->tiled_s4 = env_int("LGX_TILED_S4", 1) != 0;
         int ncu = 0;
         if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) ==
                 hipSuccess &&

@@ -135,6 +135,8 @@ enum Kern {
     K_LM_CERT,
     K_LM_PICK,
     K_NORM4S_R8,
+    K_GEMM_TILED64_S4,
+    K_GEMM_TILED32_S4,
     K_COUNT
 };
 inline const char* const kKernelNames[] = {
@@ -169,6 +171,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_q8_gemm_mfma16_group", "lgx_k_q8_gemm_mfma32_group", "lgx_k_q8_gemm_tiled_group", "lgx_k_q8_gemm_tiled64_group",
     "lgx_k_q8_gemm_tiled32_group", "lgx_k_quantize_group", "lgx_k_q8_combine_group",
     "lgx_k_lm_rowconst", "lgx_k_lm_cert", "lgx_k_lm_pick", "lgx_k_add_rmsnorm_quant4s_r8",
+    "lgx_k_q8_gemm_tiled64s4", "lgx_k_q8_gemm_tiled32s4",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -217,6 +220,7 @@ struct lgx_ctx {
     bool tiled_swiglu = true;     // LGX_TILED_SWIGLU=0: tiled gate|up products leave their outputs to lgx_k_swiglu_quant
     int norm_waves = 1;           // LGX_NORM_WAVES: rows (waves) per workgroup of the wave norm (0: off)
     bool lm_cert = true;          // LGX_LM_CERT=0: greedy tied lm_head through the full logits
+    bool tiled_s4 = true;         // LGX_TILED_S4=0: tiled products always in stages of 2 pairs
     bool prefill_serial = false;  // LGX_PREFILL=serial: prefill as P decode passes
     int prefill_chunk = 0;        // LGX_PREFILL_CHUNK: positions per prefill chunk (0: by batch)
     int ncu = 256;                // compute units of the device
@@ -535,6 +539,14 @@ inline lgx_status run_q8_tiled(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t*
     a.ntm = (int)cdiv(m, mrows);
     const int64_t wgs = (int64_t)a.ntn * a.ntm * a.ngroups;
     if (wgs > INT32_MAX) return fail(LGX_OUT_OF_BOUNDS, "tiled product of %lld workgroups", (long long)wgs);
+    // a grid of at most two workgroups per compute unit runs in stages of 4
+    // pairs: half the dependent memory rounds per workgroup (config-4 o_proj,
+    // 448 workgroups: 8.8 against 10.1 us; at 576 workgroups, three share some
+    // compute units and the 2-pair stages are faster: 11.9 against 12.8 us)
+    if (c->tiled_s4 && wgs <= 2 * (int64_t)c->ncu) {
+        if (kern == K_GEMM_TILED32) kern = K_GEMM_TILED32_S4;
+        else if (kern == K_GEMM_TILED64) kern = K_GEMM_TILED64_S4;
+    }
     return launch(c, kern, dim3((unsigned)wgs), dim3(256), a, stream);
 }
 // Tiled kernel for m rows: 128 activation rows per workgroup from m >= 128,

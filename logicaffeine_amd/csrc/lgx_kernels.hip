@@ -3425,21 +3425,22 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_act_to_t16(const lgx_act
 // tiles, n-tile by n-tile (activation tile fastest), so the tiles in flight
 // on one XCD share their operands through its L2.
 // ---------------------------------------------------------------------------
-#define LGX_TG_S 2
-template <int WM>
+// S pairs per stage: 2, or 4 for grids of at most two workgroups per compute
+// unit (half the stages, so half the dependent memory rounds)
+template <int WM, int S>
 struct TgSmem {
-    uint4 w[4][LGX_TG_S][64];
-    uint4 x[2 * WM][LGX_TG_S][64];
-    uint32_t dw[LGX_TG_S][64];
-    uint32_t dx[LGX_TG_S][16 * 2 * WM];
+    uint4 w[4][S][64];
+    uint4 x[2 * WM][S][64];
+    uint32_t dw[S][64];
+    uint32_t dx[S][16 * 2 * WM];
 };
 
-template <int WM>
+template <int WM, int S = 2>
 __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a, const int P) {
     constexpr int MTILES = 2 * WM;
     // two stage buffers as two variables: a direct load into one is known
     // not to alias reads of the other
-    __shared__ TgSmem<WM> sm0, sm1;
+    __shared__ TgSmem<WM, S> sm0, sm1;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int wn = wave & 1, wm = wave >> 1;
     const int r = lane & 15, c = lane >> 4;
@@ -3470,7 +3471,7 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a, cons
     const int gpairs = a.grp * (LGX_Q8_RANGE_BLOCKS / 2);
     const int pg0 = g * gpairs;
     const int pend = min(pg0 + gpairs, np);
-    const int nst = (pend - pg0 + LGX_TG_S - 1) / LGX_TG_S;
+    const int nst = (pend - pg0 + S - 1) / S;
     const v4i zero = {0, 0, 0, 0};
     const v4f zerof = {0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -3480,35 +3481,35 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a, cons
     //   activations: MTILES tiles x S pairs, likewise
     //   weight scale pairs: [s][64 rows], one 4-byte lane per row (waves < S)
     //   activation scale pairs: [s][r][tile], wave instructions j = wave < WM
-    static_assert(LGX_TG_S == 2, "stage layout");
+    static_assert((S == 2 || S == 4) && WM * S <= 8, "stage layout: scale loads on at most four waves");
     const uint32_t off_t16 = lane * 16;
     const uint32_t off_dw = ((uint32_t)wtile(lane >> 4) * nh * 256 + (lane & 15) * 16) * 2;
     const int dxp = (wave * 64 + lane) % (16 * MTILES);            // position within a pair
     const int dx_ml = (dxp % MTILES) * 16 + dxp / MTILES;
     const uint32_t off_dx = (uint32_t)min(tm0 * 16 + dx_ml, a.m - 1) * nb * 2;
-    auto stage = [&](TgSmem<WM>& sm, int pair0) {
+    auto stage = [&](TgSmem<WM, S>& sm, int pair0) {
 #pragma unroll
-        for (int i = 0; i < LGX_TG_S; ++i) {
+        for (int i = 0; i < S; ++i) {
             const int j = wave + 4 * i;
-            const int tile = j / LGX_TG_S, s = j - tile * LGX_TG_S;
+            const int tile = j / S, s = j - tile * S;
             const int t = wtile(tile), p = min(pair0 + s, pend - 1);
             const char* base = (const char*)a.wt + ((int64_t)t * np + p) * 1024;
             __builtin_amdgcn_global_load_lds((const void*)(base + off_t16), (lds_void*)&sm.w[tile][s][0], 16, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < MTILES * LGX_TG_S / 4; ++i) {
+        for (int i = 0; i < MTILES * S / 4; ++i) {
             const int j = wave + 4 * i;
-            const int tile = j / LGX_TG_S, s = j - tile * LGX_TG_S;
+            const int tile = j / S, s = j - tile * S;
             const int t = min(tm0 + tile, ntx - 1), p = min(pair0 + s, pend - 1);
             const char* base = (const char*)a.xt + ((int64_t)t * np + p) * 1024;
             __builtin_amdgcn_global_load_lds((const void*)(base + off_t16), (lds_void*)&sm.x[tile][s][0], 16, 0, 0);
         }
-        if (wave < LGX_TG_S) {
+        if (wave < S) {
             const int b = 2 * min(pair0 + wave, pend - 1);
             const char* base = (const char*)(a.wd + (b >> 4) * 256 + (b & 15));
             __builtin_amdgcn_global_load_lds((const void*)(base + off_dw), (lds_void*)&sm.dw[wave][0], 4, 0, 0);
         }
-        if (wave < WM) {                          // 64 words per instruction, 16*MTILES per pair
+        if (wave < WM * S / 2) {                  // 64 words per instruction, 16*MTILES per pair
             const int s = (wave * 64 + lane) / (16 * MTILES);   // uniform unless WM == 1
             const char* src = (const char*)(a.xd + 2 * min(pair0 + s, pend - 1)) + off_dx;
             __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(&sm.dx[0][0] + wave * 64), 4, 0, 0);
@@ -3525,12 +3526,12 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a, cons
     int cnt = 0;
 
     // One stage: its products from `cur` while the next stage loads into `nxt`.
-    auto run = [&](int q, TgSmem<WM>& cur, TgSmem<WM>& nxt) {
+    auto run = [&](int q, TgSmem<WM, S>& cur, TgSmem<WM, S>& nxt) {
         __syncthreads();                          // stage q landed; stage q-1 fully read
-        uint4 A[LGX_TG_S][2], B[LGX_TG_S][WM];
-        uint32_t DWR[LGX_TG_S][2], DX[LGX_TG_S][WM];
+        uint4 A[S][2], B[S][WM];
+        uint32_t DWR[S][2], DX[S][WM];
 #pragma unroll
-        for (int s = 0; s < LGX_TG_S; ++s) {
+        for (int s = 0; s < S; ++s) {
             A[s][0] = cur.w[2 * wn][s][lane];
             A[s][1] = cur.w[2 * wn + 1][s][lane];
 #pragma unroll
@@ -3550,10 +3551,10 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a, cons
                 DX[s][0] = dxr[0];
             }
         }
-        if (q + 1 < nst) stage(nxt, pg0 + LGX_TG_S * (q + 1));
+        if (q + 1 < nst) stage(nxt, pg0 + S * (q + 1));
 #pragma unroll
-        for (int s = 0; s < LGX_TG_S; ++s) {
-            if (pg0 + LGX_TG_S * q + s >= pend) continue;      // workgroup-uniform
+        for (int s = 0; s < S; ++s) {
+            if (pg0 + S * q + s >= pend) continue;      // workgroup-uniform
             // product u = (block, weight tile, activation tile); product u + 1
             // is issued before the epilogue of u, so the MFMA latency is
             // covered by that epilogue
@@ -3606,7 +3607,7 @@ __device__ __forceinline__ void q8_tiled_body(const lgx_gemm_tiled_args& a, cons
                 scur = snext;
             }
         }
-        const int done = LGX_TG_S * (q + 1);
+        const int done = S * (q + 1);
         if (done % (LGX_Q8_RANGE_BLOCKS / 2) == 0 || q == nst - 1) {
             // range end: fold into the group's subtree (cnt is uniform: one
             // branch per fold)
@@ -3694,6 +3695,12 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled64(const lg
 }
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled32(const lgx_gemm_tiled_args a) {
     q8_tiled_body<1>(a, blockIdx.x);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled64s4(const lgx_gemm_tiled_args a) {
+    q8_tiled_body<2, 4>(a, blockIdx.x);
+}
+extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_tiled32s4(const lgx_gemm_tiled_args a) {
+    q8_tiled_body<1, 4>(a, blockIdx.x);
 }
 // Grouped tiled products (lgx_tiled_group_args): each matrix's workgroups
 // start at a multiple of 8, so the hardware XCD of a workgroup is its

@@ -302,6 +302,30 @@ def test_tiled_gemm_small_m_forced(ctx, orc, rows, grp):
         c.close()
 
 
+@pytest.mark.parametrize("n,k", [(3584, 3584), (1024, 896), (512, 2112), (64, 192), (2048, 18944)])
+@pytest.mark.parametrize("rows", [32, 64])
+def test_tiled_gemm_stage_sizes_agree(orc, n, k, rows):
+    """Grids of at most two workgroups per compute unit run in stages of 4
+    pairs, larger ones in stages of 2 (LGX_TILED_S4=0: always 2).  Both
+    stage sizes give the oracle's bits at 32 and 64 activation rows per
+    workgroup: whole ranges (3584), a range of 14 pairs ending mid-stage
+    (896), 33 pairs (2112), 3 pairs (192) and 19 ranges in groups (18944)."""
+    qs, d = orc.gen_q8_matrix(5, n + k, n, k)
+    x = orc.gen_normal_f32(5, rows, (64, k))
+    xq, xd = orc.quantize_q8_0(x)
+    ref = orc.q8_gemm(qs, d, xq, xd)
+    for s4 in (1, 0):
+        c = _ctx_with_env(LGX_GEMM_TILED_MIN=2, LGX_GEMM_TILED_ROWS=rows, LGX_TILED_S4=s4)
+        try:
+            W = c.q8_matrix(qs, d)
+            gx, gd = c.to_device(xq), c.to_device(xd)
+            for m in (33, 64):
+                assert np.array_equal(host(c.q8_gemm(W, gx[:m].contiguous(), gd[:m].contiguous())),
+                                      ref[:m]), (s4, m)
+        finally:
+            c.close()
+
+
 @pytest.mark.parametrize("n,k", [(4864, 896), (1536, 8960)])
 def test_partials_then_combine_equal_full_product(ctx, orc, n, k):
     """Range partials + lgx_q8_range_combine == the one-call product, and each
