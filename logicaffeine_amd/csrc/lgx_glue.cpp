@@ -122,7 +122,7 @@ lgx_status lgx_rope_kv_append(lgx_ctx* c, const float* qkv, const float* bias, c
         a.maxp = maxp;
         a.num_pages = num_pages;
         a.max_seq = max_seq;
-        return launch(c, K_QKV_ROPE_APPEND, dim3(B), dim3(LGX_GLUE_NT), a, stream);
+        return launch_qkv_rope(c, a, B, stream);
     });
 }
 

@@ -567,6 +567,14 @@ inline int tiled_grp(const lgx_ctx* c, Kern kern, int n, int k, int m) {
     return 1;
 }
 
+// Tree + bias + RoPE + K/V append over `rows` rows: 256 rotation pairs per
+// workgroup along y.
+inline lgx_status launch_qkv_rope(lgx_ctx* c, const lgx_qkv_args& a, int rows, void* stream) {
+    const int64_t pairs = (int64_t)(a.hq + 2 * a.hkv) * (a.d / 2);
+    return launch(c, K_QKV_ROPE_APPEND, dim3((unsigned)rows, (unsigned)cdiv(pairs, 256)), dim3(256), a,
+                  stream);
+}
+
 // Row-major int8 activations [m][k] -> T16 tiles at dst (ceil(m/16)*16*k bytes).
 inline lgx_status act_to_t16(lgx_ctx* c, const int8_t* xq, int m, int k, int8_t* dst, void* stream) {
     lgx_act_t16_args a{xq, dst, m, k};

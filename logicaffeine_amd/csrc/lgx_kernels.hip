@@ -2296,52 +2296,35 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_add_rmsnorm_quant_w(cons
 
 // QKV combine + bias + RoPE + paged KV append.  One workgroup of 1024
 // threads per sequence.
-#define LGX_QKV_MAX 8192
-extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_qkv_rope_append(const lgx_qkv_args a) {
-    constexpr int NT = LGX_GLUE_NT, KV = LGX_QKV_MAX / NT;
-    __shared__ float row[LGX_QKV_MAX];
-    // workgroup = row b of the product (sequence bs, its query j)
+// Tree + bias + RoPE + binary16 K/V append.  grid = (rows of the product,
+// ceil(pairs / 256)), 256 threads: thread t of workgroup y owns rotation
+// pair p = 256 y + t, i.e. elements (i, i + d/2) of head p / (d/2) of the
+// row (q and k heads rotated, v heads copied), whatever d.  The position's
+// values (length, then page and cos/sin) are requested first, with the
+// pair's partials, so the two dependent rounds they need overlap the
+// partials' round.
+extern "C" __global__ __launch_bounds__(256) void lgx_k_qkv_rope_append(const lgx_qkv_args a) {
+    // workgroup row b of the product (sequence bs, its query j)
     const int b = blockIdx.x, t = threadIdx.x;
     const int qpr = max(a.qpr, 1), bs = b / qpr;
     const int d = a.d, half = d / 2;
-    const int nq = (a.hq + 2 * a.hkv) * d;
-    bool on[KV];
-    float v[KV];
-#pragma unroll
-    for (int k = 0; k < KV; ++k) {
-        on[k] = t + NT * k < nq;
-        v[k] = 0.0f;
-    }
-    // qkv partials: K = hidden <= 8192, so at most 8 ranges
-#pragma unroll
-    for (int k = 0; k < KV; k += 4) {
-        if (on[k]) {
-            const bool o4[4] = {on[k], on[k + 1], on[k + 2], on[k + 3]};
-            float u4[4];
-            tree_partials_n<4, 8>(a.part, a.nr, (int64_t)a.m * nq, (int64_t)b * nq + t + NT * k, NT,
-                                  o4, u4);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[k + e] = u4[e];
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < KV; ++k) {
-        if (on[k]) {
-            const int i = t + NT * k;
-            row[i] = a.bias ? v[k] + a.bias[i] : v[k];
-        }
-    }
-    __syncthreads();
+    const int nh = a.hq + 2 * a.hkv, nq = nh * d, np = nh * half;
+    const int p = blockIdx.y * 256 + t;
+    const int pc = min(p, np - 1), hh = pc / half, i = pc - hh * half;
     const int pos = min(max(a.seq_len[bs] + (b - bs * qpr), 0), a.max_seq - 1);
-    const float* cr = a.cos_t + (int64_t)pos * half;
-    const float* sr = a.sin_t + (int64_t)pos * half;
     const int page = min(max(a.page_table[(int64_t)bs * a.maxp + pos / LGX_PAGE], 0), a.num_pages - 1);
+    const float c = a.cos_t[(int64_t)pos * half + i], sn = a.sin_t[(int64_t)pos * half + i];
+    const int64_t e0 = (int64_t)b * nq + hh * d + i, stride = (int64_t)a.m * nq;
+    float x0 = tree_read(a.nr, [&](int j) { return a.part[j * stride + e0]; });
+    float x1 = tree_read(a.nr, [&](int j) { return a.part[j * stride + e0 + half]; });
+    if (a.bias) {
+        x0 = x0 + a.bias[hh * d + i];
+        x1 = x1 + a.bias[hh * d + i + half];
+    }
+    if (p >= np) return;
     const int slot = pos % LGX_PAGE;
-    // rotate q heads and k heads: pair (i, i + d/2) of head hh
-    for (int e = t; e < (a.hq + a.hkv) * half; e += NT) {
-        const int hh = e / half, i = e - hh * half;
-        const float x0 = row[hh * d + i], x1 = row[hh * d + i + half];
-        const float c = cr[i], sn = sr[i];
+    if (hh < a.hq + a.hkv) {
+        // rotate-half pair of a q or k head, each product rounded on its own
         const float t0 = x0 * c, t1 = x1 * sn, t2 = x1 * c, t3 = x0 * sn;
         const float y0 = t0 - t1, y1 = t2 + t3;
         if (hh < a.hq) {
@@ -2354,11 +2337,11 @@ extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_qkv_rope_append(
             kd[i] = f2h(y0);
             kd[i + half] = f2h(y1);
         }
-    }
-    for (int e = t; e < a.hkv * d; e += NT) {
-        const int g = e / d, i = e - g * d;
+    } else {
+        const int g = hh - a.hq - a.hkv;
         uint16_t* vd = a.vpages + (((int64_t)page * a.hkv + g) * LGX_PAGE + slot) * d;
-        vd[i] = f2h(row[(a.hq + a.hkv) * d + e]);
+        vd[i] = f2h(x0);
+        vd[i + half] = f2h(x1);
     }
 }
 

@@ -410,7 +410,7 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
                 return st;
         } else {
             if ((st = product(md, md->qkv[l], B, stream)) != LGX_OK) return st;
-            if ((st = launch(c, K_QKV_ROPE_APPEND, dim3(B), dim3(LGX_GLUE_NT), qa, stream)) !=
+            if ((st = launch_qkv_rope(c, qa, B, stream)) !=
                 LGX_OK)
                 return st;
         }
@@ -610,7 +610,7 @@ lgx_status prefill_chunk(lgx_model* md, int B, int n, const int32_t* tokens, int
         qa.num_pages = md->num_pages;
         qa.max_seq = cf.max_seq;
         qa.qpr = n;
-        if ((st = launch(c, K_QKV_ROPE_APPEND, dim3(M), dim3(LGX_GLUE_NT), qa, stream)) != LGX_OK)
+        if ((st = launch_qkv_rope(c, qa, M, stream)) != LGX_OK)
             return st;
         if (l == cf.n_layers - 1) break;
         lgx_attn_args aa{};
