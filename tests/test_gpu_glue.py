@@ -88,7 +88,11 @@ def test_add_rmsnorm_quant_bit_exact(ctx, orc, m, n, nr):
         assert np.array_equal(host(xd).view(np.uint16), rd)
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (28, 4, 128), (12, 2, 128), (4, 4, 64)])
+# a workgroup holds 256 rotation pairs of a row: d = 96 and 40 put parts of
+# several heads (and the v heads' copies) in one workgroup, 32/8/128 fills
+# 12 workgroups exactly
+@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (28, 4, 128), (12, 2, 128), (4, 4, 64),
+                                      (6, 2, 96), (3, 1, 40), (32, 8, 128)])
 def test_rope_kv_append_bit_exact(ctx, orc, hq, hkv, d):
     rng = np.random.default_rng(hq * 1000 + d)
     B, max_seq = 5, 700
