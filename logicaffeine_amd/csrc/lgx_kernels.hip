@@ -2051,7 +2051,7 @@ template <int NT, int S, int R>
 __device__ __forceinline__ void norm_body(const lgx_norm_args& a) {
     constexpr int KV = LGX_NORM_MAX / NT;
     __shared__ __align__(16) float row[LGX_NORM_MAX];
-    __shared__ float red[NT];
+    __shared__ float red[NT + 1];   // + the sum of squares
     const int b = blockIdx.x, t = threadIdx.x;
     float* hr = a.h + (int64_t)b * a.n;
     bool on[KV];
@@ -2150,19 +2150,25 @@ __device__ __forceinline__ void norm_body(const lgx_norm_args& a) {
     }
     red[t] = v[0];
     __syncthreads();
-#pragma unroll
-    for (int sl = NT / 2; sl >= 64; sl >>= 1) {
-        if (t < sl) red[t] = red[t] + red[t + sl];
-        __syncthreads();
-    }
-    float Ssq = 0.0f;
+    // levels NT/2 .. 64 across waves, evaluated by wave 0 alone from one
+    // LDS round: lane l reads the NT/64 slots l + 64 j and folds them with
+    // the same pairs in the same order (slot l + 64 j at level s joins
+    // l + 64 j + s), then the lane levels by shuffles
     if (t < 64) {
-        Ssq = wave_tree_sum(red[t]);
+        constexpr int NS = NT / 64;
+        float q[NS];
+#pragma unroll
+        for (int j = 0; j < NS; ++j) q[j] = red[t + 64 * j];
+#pragma unroll
+        for (int s = NS / 2; s >= 1; s >>= 1) {
+#pragma unroll
+            for (int j = 0; j < s; ++j) q[j] = q[j] + q[j + s];
+        }
+        const float Ssq = wave_tree_sum(q[0]);
+        if (t == 0) red[NT] = Ssq;
     }
     __syncthreads();
-    if (t == 0) red[0] = Ssq;
-    __syncthreads();
-    const float ms = red[0] / (float)a.n;
+    const float ms = red[NT] / (float)a.n;
     const float r = 1.0f / sqrtf(ms + a.eps);
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
