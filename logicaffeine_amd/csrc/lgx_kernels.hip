@@ -2186,19 +2186,125 @@ __device__ __forceinline__ void norm_body(const lgx_norm_args& a) {
     }
 }
 
+// Residual combine + RMSNorm (+ Q8_0) on float4 slots held in registers
+// throughout: one workgroup of NT threads per row, thread t owns slots
+// t + NT k (k < S; slot q = elements 4q .. 4q + 3; n % 4 == 0, n <= 4 NT S,
+// nr <= R).  h, the partials and the weights are requested together; the
+// sum of squares is the canonical halving tree over the elements (zero
+// padded to a power of two), evaluated as element strides >= 4 NT across
+// the thread's slots, 256 .. 2 NT across waves (every wave folds them from
+// one LDS round, so the workgroup takes a single barrier), 128 .. 4 across
+// lanes, 2 and 1 inside the float4 -- the same pairs in the same order (a
+// stride at or past the padded width only adds zeros, exactly).  y = (x r) w
+// per element and Q8_0 per 32-block from registers (8 consecutive lanes).
+template <int NT, int S, int R>
+__device__ __forceinline__ void norm4_body(const lgx_norm_args& a) {
+    constexpr int NW = NT / 64;
+    __shared__ float4 sq_s[NT];
+    const int b = blockIdx.x, t = threadIdx.x, lane = t & 63;
+    float* hr = a.h + (int64_t)b * a.n;
+    const int n4 = a.n >> 2;
+    float4 w4[S];
+#pragma unroll
+    for (int k = 0; k < S; ++k) w4[k] = ((const float4*)a.w)[min(t + NT * k, n4 - 1)];
+    // h and the partials through buffer descriptors: every load is issued
+    // (the wait counts stay exact), and those of slots past the row or ranges
+    // past nr fall outside the descriptor, so they read zeros without a
+    // memory access (the launcher keeps the partials' byte span below 2^31)
+    constexpr uint32_t OOB = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t hrs = __builtin_amdgcn_make_buffer_rsrc((void*)hr, 0, a.n * 4, LGX_BUF_DWORD3);
+    float4 x4[S];
+#pragma unroll
+    for (int k = 0; k < S; ++k)
+        x4[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               hrs, t + NT * k < n4 ? 16u * (t + NT * k) : OOB, 0, 0));
+    if (a.part) {
+        float4 pv[S][R];
+        const int64_t stride = (int64_t)a.m * a.n;
+        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(a.part + (int64_t)b * a.n), 0, (int)(((a.nr - 1) * stride + a.n) * 4), LGX_BUF_DWORD3);
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+#pragma unroll
+            for (int k = 0; k < S; ++k) {
+                const uint32_t off = j < a.nr && t + NT * k < n4 ? (uint32_t)((j * stride + 4 * (t + NT * k)) * 4)
+                                                                 : OOB;
+                pv[k][j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, 0));
+            }
+#pragma unroll
+        for (int k = 0; k < S; ++k) {
+            x4[k] = add4(x4[k], tree_stream4<R>(pv[k], a.nr));
+            if (t + NT * k < n4) *(float4*)(hr + 4 * (t + NT * k)) = x4[k];
+        }
+    }
+    // squares (zero past n; slots past the row read zeros above)
+    float4 v[S];
+#pragma unroll
+    for (int k = 0; k < S; ++k)
+        v[k] = make_float4(x4[k].x * x4[k].x, x4[k].y * x4[k].y, x4[k].z * x4[k].z, x4[k].w * x4[k].w);
+    static_assert(S == 1 || S == 2, "n <= 8 NT: one stride at most inside the thread");
+    int n2 = 4;
+    while (n2 < a.n) n2 <<= 1;
+    if constexpr (S == 2) {
+        if (n2 > 4 * NT) v[0] = add4(v[0], v[1]);          // stride 4 NT (n2 = 8 NT)
+    }
+    sq_s[t] = v[0];
+    __syncthreads();
+    float4 q[NW];
+#pragma unroll
+    for (int j = 0; j < NW; ++j) q[j] = sq_s[lane + 64 * j];
+#pragma unroll
+    for (int s = NW / 2; s >= 1; s >>= 1) {                  // strides 256 s across waves
+#pragma unroll
+        for (int j = 0; j < s; ++j) q[j] = add4(q[j], q[j + s]);
+    }
+    float e[4] = {q[0].x, q[0].y, q[0].z, q[0].w};
+#pragma unroll
+    for (int dl = 32; dl >= 1; dl >>= 1) {                  // strides 4 dl across lanes
+#pragma unroll
+        for (int c = 0; c < 4; ++c) e[c] = e[c] + __shfl_down(e[c], dl, 64);
+    }
+    e[0] = e[0] + e[2];
+    e[1] = e[1] + e[3];
+    e[0] = e[0] + e[1];
+    const float ssq = __shfl(e[0], 0, 64);
+    const float ms = ssq / (float)a.n;
+    const float r = 1.0f / sqrtf(ms + a.eps);
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+        const int sl = t + NT * k;
+        const bool on = sl < n4;
+        const float y[4] = {(x4[k].x * r) * w4[k].x, (x4[k].y * r) * w4[k].y, (x4[k].z * r) * w4[k].z,
+                            (x4[k].w * r) * w4[k].w};
+        if (on && a.xn) *(float4*)(a.xn + (int64_t)b * a.n + 4 * sl) = make_float4(y[0], y[1], y[2], y[3]);
+        if (on && a.xt) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a.xt[((int64_t)(b >> 4) * a.n + 4 * sl + c) * 16 + (b & 15)] = y[c];
+        }
+        if (a.xq && 4 * NT * k < a.n) {      // uniform; whole 8-lane blocks (n % 32 == 0 with Q8_0)
+            uint16_t dh;
+            const uint32_t qw = quantize4(y, dh);
+            if (on) {
+                *(uint32_t*)(a.xq + xq_off(b, 4 * sl, a.n, a.xq_t16 != 0)) = qw;
+                if ((lane & 7) == 0) a.xd[(int64_t)b * (a.n / 32) + (sl >> 3)] = dh;
+            }
+        }
+    }
+}
+
 extern "C" __global__ __launch_bounds__(LGX_GLUE_NT) void lgx_k_add_rmsnorm_quant(const lgx_norm_args a) {
     norm_body<LGX_GLUE_NT, 0, 1>(a);
 }
 // n % 4 == 0, n <= 4096: 512 threads, two float4 slots each, nr <= 8 / 20;
 // n <= 2048: one slot each
 extern "C" __global__ __launch_bounds__(512) void lgx_k_add_rmsnorm_quant4s_r8(const lgx_norm_args a) {
-    norm_body<512, 1, 8>(a);
+    norm4_body<512, 1, 8>(a);
 }
 extern "C" __global__ __launch_bounds__(512) void lgx_k_add_rmsnorm_quant4_r8(const lgx_norm_args a) {
-    norm_body<512, 2, 8>(a);
+    norm4_body<512, 2, 8>(a);
 }
 extern "C" __global__ __launch_bounds__(512) void lgx_k_add_rmsnorm_quant4_r20(const lgx_norm_args a) {
-    norm_body<512, 2, 20>(a);
+    norm4_body<512, 2, 20>(a);
 }
 
 // The same residual combine + RMSNorm (+ Q8_0) with one wave per row, for
