@@ -1490,12 +1490,22 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
     if (t0 >= L) return;                          // whole workgroup: chunk past the end
     const int n = min(C, L - t0);
     const int h0 = g * GQ;
-    if (tid < C / LGX_PAGE) {
-        int pg = 0;
-        if (t0 + tid * LGX_PAGE < L) pg = a.page_table[(int64_t)b * a.maxp + t0 / LGX_PAGE + tid];
-        pg_s[tid] = min(max(pg, 0), a.num_pages - 1);
+    // D = 64: every thread looks up its own token's page (the last token's
+    // past the end: a real slot, never used), so no LDS round and no barrier
+    // stand before the K loads; D = 128 shares the chunk's 16 entries in LDS
+    int pgt = 0;
+    if constexpr (D == 64) {
+        pgt = a.page_table[(int64_t)b * a.maxp + (t0 + min(tid, n - 1)) / LGX_PAGE];
+        pgt = min(max(pgt, 0), a.num_pages - 1);
+    } else {
+        if (tid < C / LGX_PAGE) {
+            int pg = 0;
+            if (t0 + tid * LGX_PAGE < L) pg = a.page_table[(int64_t)b * a.maxp + t0 / LGX_PAGE + tid];
+            pg_s[tid] = min(max(pg, 0), a.num_pages - 1);
+        }
+        __syncthreads();
+        pgt = pg_s[tid >> 4];
     }
-    __syncthreads();
 
     // phase 1: scores.  Thread t owns token t; its whole K row is requested
     // before the first use so all of its loads are in flight together (the
@@ -1506,8 +1516,7 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
     const bool valid = tid < n;
     uint4 kv[CPR];
     {
-        const uint4* kr = (const uint4*)(a.kpages +
-                                         (((int64_t)pg_s[tid >> 4] * a.hkv + g) * LGX_PAGE + (tid & 15)) * D);
+        const uint4* kr = (const uint4*)(a.kpages + (((int64_t)pgt * a.hkv + g) * LGX_PAGE + (tid & 15)) * D);
 #pragma unroll
         for (int j = 0; j < CPR; ++j) kv[j] = kr[j];
     }
@@ -1518,7 +1527,20 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
 #pragma unroll
     for (int j = 0; j < CPR; ++j)
         asm volatile("" : "+v"(kv[j].x), "+v"(kv[j].y), "+v"(kv[j].z), "+v"(kv[j].w));
-    attn_stage_v<D>(a, g, n, pg_s, v_s, wave, lane);
+    if constexpr (D == 64) {
+        // the whole chunk's V (32 KiB): wave w moves its own tokens
+        // 64 w .. 64 w + 63 (wave instructions 8 w .. 8 w + 7, two per page),
+        // the page of instruction i taken from lane 16 (i / 2)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int j = 8 * wave + i;
+            const int pg = __builtin_amdgcn_readlane(pgt, 16 * (i >> 1));
+            const uint16_t* src = a.vpages + ((int64_t)pg * a.hkv + g) * LGX_PAGE * D + (i & 1) * 512 + lane * 8;
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(v_s + j * 512), 16, 0, 0);
+        }
+    } else {
+        attn_stage_v<D>(a, g, n, pg_s, v_s, wave, lane);
+    }
     // D = 128: tokens VT.. of V, piece q = 256 i + tid of the second stage
     // (coalesced: 16 lanes per row), stored to v_s after the first stage
     // (rows past the chunk's end read a real page slot: pg_s is clamped)
