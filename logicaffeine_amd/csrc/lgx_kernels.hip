@@ -1425,8 +1425,10 @@ __device__ __forceinline__ void static_for(F&& f) {
 //
 // grid = (chunks, B * hkv), 256 threads: one workgroup per (sequence, KV
 // head, chunk) serves all GQ query heads of the group, so every K/V row is
-// read once per group.  Loads: thread t requests its token's whole K row
-// into registers; once it has landed, the workgroup's direct global->LDS
+// read once per group.  Pages: at D = 64 thread t looks up its own token's
+// page (no LDS round or barrier before the K loads), at D = 128 the chunk's
+// 16 entries go through LDS.  Loads: thread t requests its token's whole K
+// row into registers; once it has landed, the workgroup's direct global->LDS
 // loads (global_load_lds_dwordx4, 1 KiB per wave instruction) bring the
 // first 32 KiB of the chunk's V rows into LDS in token order (the whole
 // chunk at D = 64, tokens 0..127 at D = 128; at D = 128 each thread also
