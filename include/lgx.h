@@ -420,7 +420,9 @@ lgx_status lgx_qwen_prefill(lgx_model* m, int32_t B, int32_t P, const int32_t* p
 lgx_status lgx_qwen_generate(lgx_model* m, int32_t B, int32_t* tokens, int32_t nsteps,
                              int32_t* history, void* stream);
 /* Device pointer and size in bytes of a model tensor (layer ignored for the
- * global ones). */
+ * global ones), for reading.  The model keeps derived copies of some tensors
+ * (a tied embedding's T64 copy and row constants, built once), so writes
+ * through this pointer are not supported. */
 lgx_status lgx_model_tensor(lgx_model* m, int32_t layer, int32_t which, const void** dev,
                             size_t* bytes);
 /* Token choice of every later decode step, generate and prefill of m:

@@ -153,7 +153,55 @@ lgx_status Gguf::open(const char* p) {
     if (here < 0) return fail(LGX_MODULE_LOAD_FAILED, "%s: ftello failed", p);
     data_start = ((uint64_t)here + alignment - 1) / alignment * alignment;
     if (fseeko(f, 0, SEEK_END) != 0) return fail(LGX_MODULE_LOAD_FAILED, "%s: seek failed", p);
-    file_size = (uint64_t)ftello(f);
+    const off_t end = ftello(f);
+    if (end < 0) return fail(LGX_MODULE_LOAD_FAILED, "%s: ftello failed", p);
+    file_size = (uint64_t)end;
+    return check_extents();
+}
+
+// Bytes of a tensor of `elems` values of `type` (0 for a type not read here).
+static uint64_t tensor_bytes(uint32_t type, uint64_t elems) {
+    switch (type) {
+        case GGML_F32: return elems * 4;
+        case GGML_F16: return elems * 2;
+        case GGML_Q8_0: return elems / 32 * 34;
+        default: return 0;
+    }
+}
+
+// Element count of a tensor's dims, or false when a dim is 0 or the product
+// exceeds 2^48 (far above any model tensor; keeps every byte count below
+// 2^54 with no overflow).
+static bool tensor_elems(const TensorInfo& t, uint64_t* out) {
+    uint64_t n = 1;
+    for (uint64_t d : t.dims) {
+        if (d == 0 || d > (1ull << 48) || __builtin_mul_overflow(n, d, &n) || n > (1ull << 48))
+            return false;
+    }
+    *out = n;
+    return true;
+}
+
+// Every tensor of a type this reader knows lies inside the data section:
+// offset + bytes <= file_size - data_start, compared without wrap-around.
+lgx_status Gguf::check_extents() const {
+    if (data_start > file_size)
+        return fail(LGX_MODULE_LOAD_FAILED, "%s: no data section", path.c_str());
+    const uint64_t room = file_size - data_start;
+    for (const auto& kv : tensors) {
+        const TensorInfo& t = kv.second;
+        uint64_t elems = 0;
+        if (!tensor_elems(t, &elems))
+            return fail(LGX_MODULE_LOAD_FAILED, "%s: tensor %s has invalid dims", path.c_str(),
+                        t.name.c_str());
+        if (t.type == GGML_Q8_0 && t.dims[0] % 32 != 0)
+            return fail(LGX_MODULE_LOAD_FAILED, "%s: Q8_0 tensor %s has a row of %llu values",
+                        path.c_str(), t.name.c_str(), (unsigned long long)t.dims[0]);
+        const uint64_t nbytes = tensor_bytes(t.type, elems);
+        if (nbytes > room || t.offset > room - nbytes)
+            return fail(LGX_MODULE_LOAD_FAILED, "%s: tensor %s runs past the end of the file",
+                        path.c_str(), t.name.c_str());
+    }
     return LGX_OK;
 }
 
@@ -171,22 +219,14 @@ const TensorInfo* Gguf::tensor(const std::string& name) const {
     return it == tensors.end() ? nullptr : &it->second;
 }
 
-// Bytes of a tensor of `elems` values of `type`.
-static uint64_t tensor_bytes(uint32_t type, uint64_t elems) {
-    switch (type) {
-        case GGML_F32: return elems * 4;
-        case GGML_F16: return elems * 2;
-        case GGML_Q8_0: return elems / 32 * 34;
-        default: return 0;
-    }
-}
-
 // The tensor `name` with shape rows x cols (dims[0] = cols) and `type`,
 // positioned for reading.
 lgx_status Gguf::seek(const std::string& name, uint32_t type, int64_t rows, int64_t cols) const {
     const TensorInfo* t = tensor(name);
     if (!t) return fail(LGX_INVALID_ARGUMENT, "%s: tensor %s missing", path.c_str(), name.c_str());
-    int64_t d0 = (int64_t)t->dims[0], rest = 1;
+    // open() checked the dims (product <= 2^48) and the extent of the tensor
+    const int64_t d0 = (int64_t)t->dims[0];
+    int64_t rest = 1;
     for (size_t i = 1; i < t->dims.size(); ++i) rest *= (int64_t)t->dims[i];
     if (t->type != type)
         return fail(LGX_UNSUPPORTED, "%s: tensor %s has ggml type %u (expected %u)", path.c_str(),
@@ -195,10 +235,6 @@ lgx_status Gguf::seek(const std::string& name, uint32_t type, int64_t rows, int6
         return fail(LGX_INVALID_ARGUMENT, "%s: tensor %s is %lld x %lld (expected %lld x %lld)",
                     path.c_str(), name.c_str(), (long long)rest, (long long)d0, (long long)rows,
                     (long long)cols);
-    const uint64_t nbytes = tensor_bytes(type, (uint64_t)rows * cols);
-    if (data_start + t->offset + nbytes > file_size)
-        return fail(LGX_MODULE_LOAD_FAILED, "%s: tensor %s runs past the end of the file",
-                    path.c_str(), name.c_str());
     if (fseeko(f, (off_t)(data_start + t->offset), SEEK_SET) != 0)
         return fail(LGX_MODULE_LOAD_FAILED, "%s: seek to %s failed", path.c_str(), name.c_str());
     return LGX_OK;
@@ -258,6 +294,15 @@ lgx_status Gguf::config(int32_t max_batch, int32_t max_seq, lgx_qwen_config* cfg
     if (num("attention.layer_norm_rms_epsilon", &eps) != LGX_OK) eps = 1e-6;
     if (num("rope.freq_base", &theta) != LGX_OK) theta = 1e6;
     g_has_error = false;
+    // every number in range before the int32 conversions
+    auto in = [](double v, double lo, double hi) { return v >= lo && v <= hi && v == (double)(int64_t)v; };
+    if (!in(L, 1, 4096) || !in(H, 1, 1 << 20) || !in(I, 1, 1 << 22) || !in(hq, 1, 4096) ||
+        !in(hkv, 1, 4096))
+        return fail(LGX_INVALID_ARGUMENT, "%s: model shape out of range (layers %g, hidden %g, "
+                    "ffn %g, heads %g / %g)", path.c_str(), L, H, I, hq, hkv);
+    if (!(eps > 0.0 && eps < 1.0) || !(theta > 0.0 && theta < 1e30))
+        return fail(LGX_INVALID_ARGUMENT, "%s: rms epsilon %g or rope base %g out of range",
+                    path.c_str(), eps, theta);
     const TensorInfo* emb = tensor("token_embd.weight");
     if (!emb || emb->dims.size() != 2)
         return fail(LGX_INVALID_ARGUMENT, "%s: token_embd.weight missing", path.c_str());
@@ -269,8 +314,15 @@ lgx_status Gguf::config(int32_t max_batch, int32_t max_seq, lgx_qwen_config* cfg
     c.n_kv_heads = (int32_t)hkv;
     c.head_dim = c.n_heads > 0 ? c.hidden / c.n_heads : 0;
     double kl;
-    if (num("attention.key_length", &kl) == LGX_OK) c.head_dim = (int32_t)kl;
+    if (num("attention.key_length", &kl) == LGX_OK) {
+        if (!in(kl, 1, 4096))
+            return fail(LGX_INVALID_ARGUMENT, "%s: key length %g out of range", path.c_str(), kl);
+        c.head_dim = (int32_t)kl;
+    }
     g_has_error = false;
+    if (emb->dims[1] > 0x7fffffffull)
+        return fail(LGX_INVALID_ARGUMENT, "%s: vocabulary of %llu rows", path.c_str(),
+                    (unsigned long long)emb->dims[1]);
     c.vocab = (int32_t)emb->dims[1];
     c.tied_embedding = tensor("output.weight") ? 0 : 1;
     c.max_batch = max_batch;

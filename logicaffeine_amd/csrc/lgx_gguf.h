@@ -47,6 +47,7 @@ struct Gguf {
                         void* out) const;
 
   private:
+    lgx_status check_extents() const;
     lgx_status seek(const std::string& name, uint32_t type, int64_t rows, int64_t cols) const;
 };
 

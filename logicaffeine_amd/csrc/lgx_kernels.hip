@@ -3069,6 +3069,12 @@ extern "C" __global__ __launch_bounds__(64 * LGX_LMC_GROUPS) void lgx_k_lm_cert(
         eps = eps * (1.0f + 0x1p-18f) + fabsf(tv) * 0x1p-21f;
         lo = tv - eps;
         hi = tv + eps;
+        // A row with a non-finite entry has infinite constants; its T can be
+        // NaN (an inf or NaN entry against a column of x that rounds to 0 in
+        // binary16: 0 x inf in the MFMA) and inf - inf is NaN.  A NaN bound
+        // certifies nothing: the row stays a candidate for its exact chain.
+        if (hi != hi) hi = __builtin_inff();
+        if (lo != lo) lo = -__builtin_inff();
         const int v = 64 * g + 16 * q + 4 * c + e;
         if (!gon || v >= a.vocab) lo = hi = -__builtin_inff();
     };

@@ -206,6 +206,8 @@ void orc_gen_q8_scales(uint64_t seed, uint64_t stream, uint16_t* out, int64_t n)
  * binary16(d) (RNE) while q uses the binary32 id. */
 void orc_quantize_q8_0(const float* x, int64_t m, int32_t k, int8_t* qs, uint16_t* d) {
     int32_t nb = k / 32;
+    /* blocks are independent: rows split over the threads */
+#pragma omp parallel for schedule(static) if (m * (int64_t)k >= 65536)
     for (int64_t r = 0; r < m; ++r) {
         for (int32_t b = 0; b < nb; ++b) {
             const float* xb = x + r * k + (int64_t)b * 32;
@@ -333,6 +335,124 @@ float orc_tree_sum(float* p, int32_t g) {
     return g > 0 ? p[0] : 0.0f;
 }
 
+#if defined(__x86_64__) && defined(__GNUC__)
+/* AVX-512 VNNI form of orc_q8_gemm for 16+ activation rows (chosen at run
+ * time when the host has it): the same exact int32 block dots and the same
+ * binary32 chain and tree per output, with 16 activation rows in the 16
+ * lanes of a vector.  vpdpbusd multiplies unsigned by signed bytes, so the
+ * activation bytes enter as x + 128 (x ^ 0x80) and each block dot starts
+ * from -128 * sum(w) of its weight block: sum (x + 128) w - 128 sum w =
+ * sum x w, exact in int32 (no saturation: |sum (x + 128) w| <= 32*255*128).
+ * Per lane the chain is acc = fmaf((float)s_b, dw_b * dx_b, acc), b
+ * ascending inside a range, then orc_tree_sum's pairwise tree over the
+ * ranges -- the scalar path's operations on the same values. */
+#define ORC_VNNI_ROWS 4       /* weight rows sharing one load of activations */
+#define ORC_VNNI_GROUPS 16    /* 16-row activation groups per cache tile */
+__attribute__((target("avx512f,avx512bw,avx512vnni")))
+static void q8_gemm_vnni(const int8_t* qs, const uint16_t* d, int32_t n, int32_t k,
+                         const int8_t* xq, const uint16_t* xd, int32_t m, float* y) {
+    const int32_t nb = k / 32, g = (nb + ORC_Q8_RANGE_BLOCKS - 1) / ORC_Q8_RANGE_BLOCKS;
+    const int32_t ng = (m + 15) / 16;
+    /* activations as [group][block][dword j][16 lanes] of x ^ 0x80, scales
+     * as [group][block][16 lanes] binary32; rows past m hold x = 0, d = 0 */
+    uint32_t* xu = (uint32_t*)aligned_alloc(64, (size_t)ng * nb * 8 * 64);
+    float* dxf = (float*)aligned_alloc(64, (size_t)ng * nb * 64);
+    if (!xu || !dxf) abort();
+#pragma omp parallel for schedule(static)
+    for (int64_t gb = 0; gb < (int64_t)ng * nb; ++gb) {
+        const int32_t grp = (int32_t)(gb / nb), b = (int32_t)(gb % nb);
+        for (int32_t lane = 0; lane < 16; ++lane) {
+            const int32_t row = grp * 16 + lane;
+            for (int32_t j = 0; j < 8; ++j) {
+                uint32_t v = 0u;
+                if (row < m) memcpy(&v, xq + (int64_t)row * k + (int64_t)b * 32 + 4 * j, 4);
+                xu[(gb * 8 + j) * 16 + lane] = v ^ 0x80808080u;
+            }
+            dxf[gb * 16 + lane] = row < m ? f16f(xd[(int64_t)row * nb + b]) : 0.0f;
+        }
+    }
+    const int32_t nrb = (n + ORC_VNNI_ROWS - 1) / ORC_VNNI_ROWS;
+#pragma omp parallel
+    {
+        float* part = (float*)aligned_alloc(64, (size_t)ORC_VNNI_ROWS * g * 64);
+        int32_t* wc = (int32_t*)malloc(sizeof(int32_t) * ORC_VNNI_ROWS * nb);
+        float* dw = (float*)malloc(sizeof(float) * ORC_VNNI_ROWS * nb);
+        if (!part || !wc || !dw) abort();
+        for (int32_t g0 = 0; g0 < ng; g0 += ORC_VNNI_GROUPS) {
+            const int32_t g1 = g0 + ORC_VNNI_GROUPS < ng ? g0 + ORC_VNNI_GROUPS : ng;
+#pragma omp for schedule(dynamic, 4)
+            for (int32_t rb = 0; rb < nrb; ++rb) {
+                const int8_t* w[ORC_VNNI_ROWS];
+                for (int32_t u = 0; u < ORC_VNNI_ROWS; ++u) {
+                    int32_t row = rb * ORC_VNNI_ROWS + u;
+                    if (row > n - 1) row = n - 1;       /* tail: a repeated row, not stored */
+                    w[u] = qs + (int64_t)row * k;
+                    for (int32_t b = 0; b < nb; ++b) {
+                        int32_t s = 0;
+                        for (int32_t i = 0; i < 32; ++i) s += w[u][b * 32 + i];
+                        wc[u * nb + b] = -128 * s;
+                        dw[u * nb + b] = f16f(d[(int64_t)row * nb + b]);
+                    }
+                }
+                for (int32_t grp = g0; grp < g1; ++grp) {
+                    for (int32_t r = 0; r < g; ++r) {
+                        __m512 acc[ORC_VNNI_ROWS];
+                        for (int32_t u = 0; u < ORC_VNNI_ROWS; ++u) acc[u] = _mm512_setzero_ps();
+                        int32_t b1 = (r + 1) * ORC_Q8_RANGE_BLOCKS;
+                        if (b1 > nb) b1 = nb;
+                        for (int32_t b = r * ORC_Q8_RANGE_BLOCKS; b < b1; ++b) {
+                            const int64_t gb = (int64_t)grp * nb + b;
+                            const __m512i* xv = (const __m512i*)(xu + gb * 8 * 16);
+                            const __m512 dx = _mm512_load_ps(dxf + gb * 16);
+                            for (int32_t u = 0; u < ORC_VNNI_ROWS; ++u) {
+                                const int32_t* wb = (const int32_t*)(w[u] + (int64_t)b * 32);
+                                __m512i s = _mm512_set1_epi32(wc[u * nb + b]);
+                                for (int32_t j = 0; j < 8; ++j) {
+                                    int32_t wd;
+                                    memcpy(&wd, wb + j, 4);
+                                    s = _mm512_dpbusd_epi32(s, _mm512_load_si512(xv + j),
+                                                            _mm512_set1_epi32(wd));
+                                }
+                                const __m512 dd = _mm512_mul_ps(_mm512_set1_ps(dw[u * nb + b]), dx);
+                                acc[u] = _mm512_fmadd_ps(_mm512_cvtepi32_ps(s), dd, acc[u]);
+                            }
+                        }
+                        for (int32_t u = 0; u < ORC_VNNI_ROWS; ++u)
+                            _mm512_store_ps(part + ((int64_t)u * g + r) * 16, acc[u]);
+                    }
+                    for (int32_t u = 0; u < ORC_VNNI_ROWS; ++u) {
+                        const int32_t row = rb * ORC_VNNI_ROWS + u;
+                        if (row >= n) break;
+                        float* p = part + (int64_t)u * g * 16;
+                        /* orc_tree_sum over the ranges, lane by lane */
+                        for (int32_t s = 1; s < g; s <<= 1)
+                            for (int32_t i = 0; i + s < g; i += 2 * s)
+                                _mm512_store_ps(p + i * 16, _mm512_add_ps(_mm512_load_ps(p + i * 16),
+                                                                          _mm512_load_ps(p + (i + s) * 16)));
+                        for (int32_t lane = 0; lane < 16; ++lane) {
+                            const int32_t mi = grp * 16 + lane;
+                            if (mi < m) y[(int64_t)mi * n + row] = p[lane];
+                        }
+                    }
+                }
+            }
+        }
+        free(part); free(wc); free(dw);
+    }
+    free(xu); free(dxf);
+}
+
+static int vnni_ok(void) {
+    static int ok = -1;
+    if (ok < 0) {
+        __builtin_cpu_init();
+        ok = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+             __builtin_cpu_supports("avx512vnni") && getenv("ORC_NO_VNNI") == NULL;
+    }
+    return ok;
+}
+#endif
+
 /* Canonical Q8 x Q8 product, the schedule every device kernel follows:
  *   s_b  = sum_i qw[32b+i] * qx[32b+i]            (int32, exact)
  *   dd_b = f32(dw_b) * f32(dx_b)                  (exact: 11x11-bit product)
@@ -344,6 +464,12 @@ void orc_q8_gemm(const int8_t* qs, const uint16_t* d, int32_t n, int32_t k,
                  const int8_t* xq, const uint16_t* xd, int32_t m, float* y) {
     int32_t nb = k / 32;
     int32_t g = (nb + ORC_Q8_RANGE_BLOCKS - 1) / ORC_Q8_RANGE_BLOCKS;
+#if defined(__x86_64__) && defined(__GNUC__)
+    if (m >= 16 && nb > 0 && vnni_ok()) {
+        q8_gemm_vnni(qs, d, n, k, xq, xd, m, y);
+        return;
+    }
+#endif
     float* dxf = (float*)malloc(sizeof(float) * (size_t)m * nb);
     for (int64_t i = 0; i < (int64_t)m * nb; ++i) dxf[i] = f16f(xd[i]);
     /* weight row outer, activation row inner: a thread keeps its weight row
@@ -434,11 +560,190 @@ float orc_halving_sum(float* p, int32_t n) {
  *   M = max m_c, w_c = orc_expf(m_c - M),
  *   L = chain_c fmaf(w_c, l_c, L), O[i] = chain_c fmaf(w_c, o_c[i], O[i]),
  *   out[i] = O[i] / L (0 for an empty sequence). */
+#if defined(__x86_64__) && defined(__GNUC__)
+/* 16 x 16 binary32 transpose: r[j] holds row j on entry, column j on exit
+ * (unpacks inside 128-bit lanes, then lane shuffles). */
+__attribute__((target("avx512f")))
+static inline void tr16x16(__m512 r[16]) {
+    __m512 t[16], u[16];
+    for (int i = 0; i < 8; ++i) {
+        t[2 * i] = _mm512_unpacklo_ps(r[2 * i], r[2 * i + 1]);
+        t[2 * i + 1] = _mm512_unpackhi_ps(r[2 * i], r[2 * i + 1]);
+    }
+    for (int i = 0; i < 4; ++i) {      /* u[4i + c]: column 4L + c of rows 4i..4i+3 in lane L */
+        const __m512d a = _mm512_castps_pd(t[4 * i]), b = _mm512_castps_pd(t[4 * i + 2]);
+        const __m512d c = _mm512_castps_pd(t[4 * i + 1]), e = _mm512_castps_pd(t[4 * i + 3]);
+        u[4 * i] = _mm512_castpd_ps(_mm512_unpacklo_pd(a, b));
+        u[4 * i + 1] = _mm512_castpd_ps(_mm512_unpackhi_pd(a, b));
+        u[4 * i + 2] = _mm512_castpd_ps(_mm512_unpacklo_pd(c, e));
+        u[4 * i + 3] = _mm512_castpd_ps(_mm512_unpackhi_pd(c, e));
+    }
+    for (int k = 0; k < 4; ++k) {
+        const __m512 v0 = _mm512_shuffle_f32x4(u[k], u[4 + k], 0x88);
+        const __m512 v1 = _mm512_shuffle_f32x4(u[k], u[4 + k], 0xdd);
+        const __m512 w0 = _mm512_shuffle_f32x4(u[8 + k], u[12 + k], 0x88);
+        const __m512 w1 = _mm512_shuffle_f32x4(u[8 + k], u[12 + k], 0xdd);
+        r[k] = _mm512_shuffle_f32x4(v0, w0, 0x88);
+        r[8 + k] = _mm512_shuffle_f32x4(v0, w0, 0xdd);
+        r[4 + k] = _mm512_shuffle_f32x4(v1, w1, 0x88);
+        r[12 + k] = _mm512_shuffle_f32x4(v1, w1, 0xdd);
+    }
+}
+
+/* orc_expf on 16 lanes: the same operations lane by lane (NaN passes
+ * through, the two range limits are blends after the polynomial). */
+__attribute__((target("avx512f")))
+static inline __m512 expf16(__m512 x) {
+    const __m512 nf = _mm512_sub_ps(_mm512_add_ps(_mm512_mul_ps(x, _mm512_set1_ps(1.44269504088896341f)),
+                                                  _mm512_set1_ps(12582912.0f)),
+                                    _mm512_set1_ps(12582912.0f));
+    __m512 r = _mm512_fnmadd_ps(nf, _mm512_set1_ps(0.693145751953125f), x);
+    r = _mm512_fnmadd_ps(nf, _mm512_set1_ps(1.42860682030941723e-06f), r);
+    __m512 p = _mm512_set1_ps(1.98412698412698413e-04f);
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(1.38888888888888889e-03f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(8.33333333333333333e-03f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(4.16666666666666667e-02f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(1.66666666666666667e-01f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(0.5f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(1.0f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(1.0f));
+    __m512i n = _mm512_cvttps_epi32(nf);
+    const __mmask16 big = _mm512_cmpgt_epi32_mask(n, _mm512_set1_epi32(127));
+    p = _mm512_mask_mul_ps(p, big, p, _mm512_set1_ps(2.0f));
+    n = _mm512_mask_sub_epi32(n, big, n, _mm512_set1_epi32(1));
+    __m512 y = _mm512_mul_ps(p, _mm512_castsi512_ps(_mm512_slli_epi32(
+                                    _mm512_add_epi32(n, _mm512_set1_epi32(127)), 23)));
+    y = _mm512_mask_blend_ps(_mm512_cmp_ps_mask(x, _mm512_set1_ps(-87.33f), _CMP_LT_OQ), y,
+                             _mm512_setzero_ps());
+    y = _mm512_mask_blend_ps(_mm512_cmp_ps_mask(x, _mm512_set1_ps(88.72f), _CMP_GT_OQ), y,
+                             _mm512_set1_ps(INFINITY));
+    return _mm512_mask_blend_ps(_mm512_cmp_ps_mask(x, x, _CMP_UNORD_Q), y, x);
+}
+
+/* AVX-512 form of orc_gqa_decode_attn for one (sequence b, KV head g) and
+ * its gq query heads: the same per-head operations, 16 tokens (scores) or 16
+ * dimensions (PV) in the lanes of a vector.  Score lane t runs the chain
+ * fmaf(q[i], K_t[i], acc) over i ascending from +0, then * scale; PV lane i
+ * runs fmaf(p_t, V_t[i], acc) over t ascending from +0; the binary16 rows are
+ * widened with vcvtph2ps (exact: the cache holds no signalling NaN, its
+ * values come from RNE conversions).  Softmax, the halving sums and the
+ * chunk merge are the scalar code's. */
+__attribute__((target("avx512f")))
+static void attn_bg_avx512(const float* q, const uint16_t* kpages, const uint16_t* vpages,
+                           const int32_t* page_table, int32_t b, int32_t g, int32_t L,
+                           int32_t hq, int32_t hkv, int32_t d, int32_t maxp, float scale,
+                           float* out, float* vf, float* sbuf, float* oc, float* mc, float* lc) {
+    const int32_t gq = hq / hkv, nd = d / 16;
+    const int32_t nc = (L + ORC_ATTN_CHUNK - 1) / ORC_ATTN_CHUNK;
+    for (int32_t c = 0; c < nc; ++c) {
+        const int32_t t0 = c * ORC_ATTN_CHUNK;
+        const int32_t n = L - t0 < ORC_ATTN_CHUNK ? L - t0 : ORC_ATTN_CHUNK;
+        /* scores: sbuf[hh][t] */
+        for (int32_t tb = 0; tb * 16 < n; ++tb) {
+            const int32_t nv = n - 16 * tb < 16 ? n - 16 * tb : 16;
+            __m512 a[8];
+            for (int32_t hh = 0; hh < gq; ++hh) a[hh] = _mm512_setzero_ps();
+            for (int32_t ib = 0; ib < nd; ++ib) {
+                __m512 r[16];
+                for (int32_t j = 0; j < 16; ++j)
+                    r[j] = j < nv ? _mm512_cvtph_ps(_mm256_loadu_si256((const __m256i*)(
+                                        kv_row(kpages, page_table, b, maxp, t0 + 16 * tb + j, g, hkv, d) +
+                                        16 * ib)))
+                                  : _mm512_setzero_ps();
+                tr16x16(r);
+                for (int32_t i = 0; i < 16; ++i)
+                    for (int32_t hh = 0; hh < gq; ++hh) {
+                        const float qi = q[((int64_t)b * hq + g * gq + hh) * d + 16 * ib + i];
+                        a[hh] = _mm512_fmadd_ps(_mm512_set1_ps(qi), r[i], a[hh]);
+                    }
+            }
+            for (int32_t hh = 0; hh < gq; ++hh)
+                _mm512_storeu_ps(sbuf + hh * ORC_ATTN_CHUNK + 16 * tb,
+                                 _mm512_mul_ps(a[hh], _mm512_set1_ps(scale)));
+        }
+        /* V rows of the chunk as binary32 */
+        for (int32_t t = 0; t < n; ++t) {
+            const uint16_t* vr = kv_row(vpages, page_table, b, maxp, t0 + t, g, hkv, d);
+            for (int32_t ib = 0; ib < nd; ++ib)
+                _mm512_storeu_ps(vf + (int64_t)t * d + 16 * ib,
+                                 _mm512_cvtph_ps(_mm256_loadu_si256((const __m256i*)(vr + 16 * ib))));
+        }
+        for (int32_t hh = 0; hh < gq; ++hh) {
+            float* s = sbuf + hh * ORC_ATTN_CHUNK;
+            float m = -INFINITY;
+            for (int32_t j = 0; j < n; ++j)
+                if (s[j] > m) m = s[j];
+            for (int32_t j = 0; j < ORC_ATTN_CHUNK; j += 16) {
+                const __m512 e = expf16(_mm512_sub_ps(_mm512_loadu_ps(s + j), _mm512_set1_ps(m)));
+                const __mmask16 live = j + 16 <= n ? (__mmask16)0xffff
+                                     : j >= n ? (__mmask16)0 : (__mmask16)((1u << (n - j)) - 1u);
+                _mm512_storeu_ps(s + j, _mm512_maskz_mov_ps(live, e));
+            }
+            __m512 o[8];
+            for (int32_t ib = 0; ib < nd; ++ib) o[ib] = _mm512_setzero_ps();
+            for (int32_t t = 0; t < n; ++t) {
+                const __m512 p = _mm512_set1_ps(s[t]);
+                for (int32_t ib = 0; ib < nd; ++ib)
+                    o[ib] = _mm512_fmadd_ps(p, _mm512_loadu_ps(vf + (int64_t)t * d + 16 * ib), o[ib]);
+            }
+            float* oo = oc + ((int64_t)hh * nc + c) * d;
+            for (int32_t ib = 0; ib < nd; ++ib) _mm512_storeu_ps(oo + 16 * ib, o[ib]);
+            mc[hh * nc + c] = m;
+            lc[hh * nc + c] = orc_halving_sum(s, ORC_ATTN_CHUNK);
+        }
+    }
+    for (int32_t hh = 0; hh < gq; ++hh) {
+        const int64_t bh = (int64_t)b * hq + g * gq + hh;
+        float M = -INFINITY;
+        for (int32_t c = 0; c < nc; ++c) if (mc[hh * nc + c] > M) M = mc[hh * nc + c];
+        float Ls = 0.0f;
+        for (int32_t c = 0; c < nc; ++c) Ls = fmaf(orc_expf(mc[hh * nc + c] - M), lc[hh * nc + c], Ls);
+        for (int32_t i = 0; i < d; ++i) {
+            float O = 0.0f;
+            for (int32_t c = 0; c < nc; ++c)
+                O = fmaf(orc_expf(mc[hh * nc + c] - M), oc[((int64_t)hh * nc + c) * d + i], O);
+            out[bh * d + i] = nc > 0 ? O / Ls : 0.0f;
+        }
+    }
+}
+#endif
+
 void orc_gqa_decode_attn(const float* q, const uint16_t* kpages, const uint16_t* vpages,
                          const int32_t* page_table, const int32_t* seq_len, int32_t B,
                          int32_t hq, int32_t hkv, int32_t d, int32_t maxp, float scale,
                          float* out) {
     int32_t gq = hq / hkv;
+#if defined(__x86_64__) && defined(__GNUC__)
+    /* the vector form works on (sequence, KV head) tasks: taken when there
+     * are enough of them for the threads (prefill rows, large batches) */
+    if (vnni_ok() && d % 16 == 0 && d <= 128 && gq <= 8 &&
+        (int64_t)B * hkv >= 4 * (int64_t)omp_get_max_threads()) {
+#pragma omp parallel
+        {
+            float* vf = (float*)malloc(sizeof(float) * ORC_ATTN_CHUNK * d);
+            float* sbuf = (float*)malloc(sizeof(float) * 8 * ORC_ATTN_CHUNK);
+            int32_t cap = 0;
+            float *oc = NULL, *mc = NULL, *lc = NULL;
+#pragma omp for schedule(dynamic)
+            for (int64_t bg = 0; bg < (int64_t)B * hkv; ++bg) {
+                const int32_t b = (int32_t)(bg / hkv), g = (int32_t)(bg % hkv);
+                const int32_t L = seq_len[b];
+                const int32_t nc = (L + ORC_ATTN_CHUNK - 1) / ORC_ATTN_CHUNK;
+                if (nc > cap) {
+                    cap = nc;
+                    free(oc); free(mc); free(lc);
+                    oc = (float*)malloc(sizeof(float) * (size_t)gq * cap * d);
+                    mc = (float*)malloc(sizeof(float) * (size_t)gq * cap);
+                    lc = (float*)malloc(sizeof(float) * (size_t)gq * cap);
+                }
+                attn_bg_avx512(q, kpages, vpages, page_table, b, g, L, hq, hkv, d, maxp, scale, out,
+                               vf, sbuf, oc, mc, lc);
+            }
+            free(vf); free(sbuf); free(oc); free(mc); free(lc);
+        }
+        return;
+    }
+#endif
 #pragma omp parallel for schedule(dynamic)
     for (int64_t bh = 0; bh < (int64_t)B * hq; ++bh) {
         int32_t b = (int32_t)(bh / hq), h = (int32_t)(bh % hq), g = h / gq;
@@ -531,15 +836,20 @@ static int32_t pow2_at_least(int32_t n) {
  * past h), ms = S / h, r = 1 / sqrtf(ms + eps), y_i = (x_i * r) * w_i. */
 void orc_rmsnorm(const float* x, const float* w, int32_t m, int32_t h, float eps, float* y) {
     int32_t n2 = pow2_at_least(h);
-    float* t = (float*)malloc(sizeof(float) * n2);
-    for (int32_t r = 0; r < m; ++r) {
-        const float* xr = x + (int64_t)r * h;
-        for (int32_t i = 0; i < n2; ++i) t[i] = i < h ? xr[i] * xr[i] : 0.0f;
-        float ms = orc_halving_sum(t, n2) / (float)h;
-        float rr = 1.0f / sqrtf(ms + eps);
-        for (int32_t i = 0; i < h; ++i) y[(int64_t)r * h + i] = (xr[i] * rr) * w[i];
+    /* rows are independent: split over the threads, one scratch row each */
+#pragma omp parallel if (m >= 64)
+    {
+        float* t = (float*)malloc(sizeof(float) * n2);
+#pragma omp for schedule(static)
+        for (int32_t r = 0; r < m; ++r) {
+            const float* xr = x + (int64_t)r * h;
+            for (int32_t i = 0; i < n2; ++i) t[i] = i < h ? xr[i] * xr[i] : 0.0f;
+            float ms = orc_halving_sum(t, n2) / (float)h;
+            float rr = 1.0f / sqrtf(ms + eps);
+            for (int32_t i = 0; i < h; ++i) y[(int64_t)r * h + i] = (xr[i] * rr) * w[i];
+        }
+        free(t);
     }
-    free(t);
 }
 
 /* RoPE tables: angle = pos * theta^(-2i/d) in binary64, rounded to binary32
@@ -570,6 +880,7 @@ void orc_rope(float* x, int32_t nheads, int32_t d, const float* cos_row, const f
 
 /* a_i = silu(g_i) * u_i for gu = [gate(0..I) | up(0..I)]. */
 void orc_swiglu(const float* gu, int32_t m, int32_t inter, float* a) {
+#pragma omp parallel for schedule(static) if (m >= 16)
     for (int32_t r = 0; r < m; ++r)
         for (int32_t i = 0; i < inter; ++i)
             a[(int64_t)r * inter + i] = orc_silu(gu[(int64_t)r * 2 * inter + i]) *

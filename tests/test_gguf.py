@@ -78,3 +78,34 @@ def test_malformed_files(tmp_path):
     assert _err(p) == "LGX_UNSUPPORTED"
     gg.write_gguf(p, meta, gg.qwen2_tensors(cfg, t))
     assert _err(p, 0, 16) == "LGX_INVALID_ARGUMENT"
+
+
+def _patch_info(p, name, ndims, field, value):
+    """Overwrite a field of tensor `name`'s info in file p: "dim0" or
+    "offset" (little-endian u64)."""
+    b = bytearray(p.read_bytes())
+    key = struct.pack("<Q", len(name)) + name.encode()
+    at = b.find(key) + len(key) + 4                      # after n_dims
+    pos = at if field == "dim0" else at + 8 * ndims + 4
+    b[pos:pos + 8] = struct.pack("<Q", value)
+    p.write_bytes(bytes(b))
+
+
+def test_corrupt_tensor_extents(tmp_path):
+    """Offsets or dims that would overflow the size arithmetic are refused
+    when the file is opened, before any tensor is read."""
+    cfg = _tiny()
+    t = gg.random_qwen2(cfg, 3)
+    meta = gg.qwen2_meta(cfg)
+    p = tmp_path / "c.gguf"
+    for field, value in [("offset", 2**64 - 16), ("offset", 2**63), ("dim0", 2**62),
+                         ("dim0", 0), ("offset", 10**9)]:
+        gg.write_gguf(p, meta, gg.qwen2_tensors(cfg, t))
+        assert lgx.gguf_config(str(p), 1, 16)["hidden"] == cfg["hidden"]
+        _patch_info(p, "output_norm.weight", 1, field, value)
+        assert _err(p) == "LGX_MODULE_LOAD_FAILED", (field, value)
+    # a shape number past int32 in the metadata
+    big = [(k, gg.T_U64 if k == "qwen2.embedding_length" else ty,
+            2**40 if k == "qwen2.embedding_length" else v) for k, ty, v in meta]
+    gg.write_gguf(p, big, gg.qwen2_tensors(cfg, t))
+    assert _err(p) == "LGX_INVALID_ARGUMENT"

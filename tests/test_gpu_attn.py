@@ -43,7 +43,7 @@ def test_golden_fixture(ctx, orc, golden):
     assert np.all(np.abs(out - f64) <= 2e-3 * (np.abs(f64) + 1e-2))
 
 
-@pytest.mark.parametrize("L", [512, 4096])
+@pytest.mark.parametrize("L", [512, 4096, 32768])
 def test_config2_uniform_bit_exact(ctx, orc, L):
     B, hq, hkv, d = 16, 12, 2, 128
     lens = [L] * B
@@ -54,7 +54,9 @@ def test_config2_uniform_bit_exact(ctx, orc, L):
 
 
 def test_config2_ragged_long_bit_exact(ctx, orc):
-    B, hq, hkv, d = 4, 12, 2, 128
+    """Config 2's ragged variant at its batch of 16: lengths uniform in
+    [256, 32768], the first at the maximum."""
+    B, hq, hkv, d = 16, 12, 2, 128
     lens = list(orc.gen_below_i32(2, 30, 32768 - 256 + 1, (B,)) + 256)
     lens[0] = 32768
     k, v, pt, _ = make_cache(B, hkv, d, lens, seed=3)

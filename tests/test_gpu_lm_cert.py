@@ -183,3 +183,35 @@ def test_certified_argument_errors(ctx):
         ctx.lm_head_argmax_f16(t.zeros((2, 96), dtype=t.float32, device=ctx.dev),
                                t.zeros((100, 96), dtype=t.int16, device=ctx.dev), Et, rc)
     assert e.value.status_name == "LGX_UNSUPPORTED"
+
+
+def test_certified_token_with_non_finite_embedding_rows(ctx, orc):
+    """Embedding rows holding +inf, -inf or NaN at a column where x is
+    nonzero but far below its largest entry (|x_k| < 2^-40 max|x|, so the
+    binary16 copy of x holds 0 there and the MFMA forms 0 x inf = NaN): the
+    exact chain gives +inf, -inf or NaN for those rows, and the certified
+    token must still be the full logits' argmax (the +inf row when x_k > 0)."""
+    rng = np.random.default_rng(11)
+    m, h, vocab = 6, 256, 1300
+    E = orc.f32_to_f16((rng.standard_normal((vocab, h)) * 0.05).astype(np.float32))
+    k0, k1 = 5, 77
+    E[101, k0] = 0x7c00            # +inf
+    E[702, k0] = 0xfc00            # -inf
+    E[903, k0] = 0x7e00            # NaN
+    E[1250, k1] = 0x7c00           # +inf at another column
+    x = rng.standard_normal((m, h)).astype(np.float32)
+    x[0, k0] = 1e-30               # +inf row wins
+    x[1, k0] = -1e-30              # row 101 -inf, row 702 +inf: 702 wins
+    x[2, k0] = 0.0                 # 0 x inf = NaN: those rows are skipped
+    x[3, k0] = 1e-30
+    x[3, k1] = 1e-30               # two +inf rows: the first (101) wins
+    x[4, k0] = 2.5                 # an ordinary value at the column
+    x[5, k1] = -1e-30
+    Ed = ctx.to_device(E)
+    Et = ctx.f16_repack_t64(Ed)
+    got = host(ctx.lm_head_argmax_f16(ctx.to_device(x), Ed, Et, ctx.lm_head_rowconst(Ed)))
+    want = full_tokens(ctx, ctx.to_device(x), Et, vocab)
+    lg = orc.lm_head_f16(x, E)
+    assert list(want) == [orc.argmax(r) for r in lg]
+    assert list(got) == list(want)
+    assert got[0] == 101 and got[1] == 702 and got[3] == 101

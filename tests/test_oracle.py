@@ -234,3 +234,29 @@ def test_s16_scale_layout_formula(orc):
     # padding past nb is zero, and every scale appears exactly once
     assert s[((0 * nh + 1) * 16 + 3) * 16 + 12] == 0
     assert np.array_equal(np.sort(s[s != 0]), np.sort(d.ravel()))
+
+
+def test_q8_gemm_wide_path_matches_row_path(orc, golden):
+    """16+ activation rows take the oracle's vector path (AVX-512 VNNI, when
+    the host has it); one row at a time takes the scalar path.  Both must give
+    the same bits, scale specials (inf, NaN, -0, subnormal, max) included,
+    and the wide path must meet the independent float64 golden bound."""
+    rng = np.random.default_rng(5)
+    for n, k, m in [(37, 96, 17), (100, 3584, 40), (16, 18944, 33), (5, 64, 300)]:
+        qs = rng.integers(-128, 128, size=(n, k)).astype(np.int8)
+        d = orc.f32_to_f16((np.abs(rng.standard_normal((n, k // 32))) * 0.02 / 127).astype(np.float32))
+        xq = rng.integers(-128, 128, size=(m, k)).astype(np.int8)
+        xd = orc.f32_to_f16(rng.random((m, k // 32)).astype(np.float32))
+        specials = np.array([0x7c00, 0xfc00, 0x7e00, 0x8000, 0x0001, 0x7bff], np.uint16)
+        d.flat[rng.integers(0, d.size, 6)] = specials
+        xd.flat[rng.integers(0, xd.size, 6)] = specials
+        y = orc.q8_gemm(qs, d, xq, xd)
+        rows = np.stack([orc.q8_gemm(qs, d, xq[i:i + 1], xd[i:i + 1])[0] for i in range(m)])
+        assert np.array_equal(y.view(np.uint32), rows.view(np.uint32)), (n, k, m)
+    qs, d = golden["ranges_qs"], golden["ranges_d"]
+    reps = -(-16 // golden["ranges_xq"].shape[0])
+    xq = np.tile(golden["ranges_xq"], (reps, 1))
+    xd = np.tile(golden["ranges_xd"], (reps, 1))
+    ref = np.tile(golden["ranges_y_q8q8"], (reps, 1))
+    absum = np.tile(golden["ranges_y_q8q8_abs"], (reps, 1))
+    assert _q8_bound_ok(orc.q8_gemm(qs, d, xq, xd), ref, absum)

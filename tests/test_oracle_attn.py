@@ -84,3 +84,30 @@ def test_halving_sum_order(orc):
     # level s=128 pairs (0,128): 1e8+1 == 1e8; then (0,1): 0.  Left to right gives 1.
     assert orc.halving_sum(p) == 0.0
     assert orc.halving_sum(np.ones(256, np.float32)) == 256.0
+
+
+def test_wide_path_matches_per_sequence_path(orc, golden):
+    """Many (sequence, KV head) tasks take the oracle's vector path (AVX-512,
+    when the host has it); one sequence at a time takes the scalar path.
+    Same bits for ragged lengths (empty, one token, partial chunks, several
+    chunks), d = 64 and 128 and group sizes 1 to 7; the golden fixture
+    repeated over many sequences meets its float64 reference."""
+    rng = np.random.default_rng(6)
+    for hq, hkv, d in [(14, 2, 64), (28, 4, 128), (8, 8, 64), (12, 2, 128)]:
+        B = max(8, 192 // hkv)
+        lens = rng.integers(0, 700, size=B).astype(np.int32)
+        lens[:4] = [0, 1, 256, 513]
+        maxp = -(-int(lens.max()) // 16)
+        k, v, pt = _cache(orc, B, hkv, d, maxp, seed=hq + d)
+        q = orc.gen_normal_f32(9, hq + d, (B, hq, d))
+        out = orc.gqa_decode_attn(q, k, v, pt, lens)
+        for b in range(B):
+            one = orc.gqa_decode_attn(q[b:b + 1], k, v, pt[b:b + 1], lens[b:b + 1])
+            assert np.array_equal(out[b].view(np.uint32), one[0].view(np.uint32)), (hq, d, b)
+    gB = golden["attn_q"].shape[0]
+    reps = -(-96 // gB)
+    q = np.tile(golden["attn_q"], (reps, 1, 1))
+    pt = np.tile(golden["attn_pt"], (reps, 1))
+    lens = np.tile(golden["attn_lens"], reps)
+    out = orc.gqa_decode_attn(q, golden["attn_k"], golden["attn_v"], pt, lens)
+    assert close(out, np.tile(golden["attn_out"], (reps, 1, 1)))
