@@ -87,15 +87,54 @@ def gemv_launch_bytes():
     return step_bytes(1)
 
 
-def build_sets(ctx, torch, nsets, seed=1):
+_SM_GAMMA = 0x9E3779B97F4A7C15
+
+
+def _sm_mix(z):
+    """SplitMix64 finaliser on a numpy uint64 array (wrapping arithmetic)."""
     import numpy as np
 
-    rng = np.random.default_rng(seed)
-    base = {}
-    for name, n, k in SHAPES:
-        qs = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
-        d = (np.abs(rng.normal(0.0, 0.02, size=(n, k // 32))) / 127.0).astype(np.float16)
-        base[name] = ctx.q8_matrix(qs, d.view(np.uint16))
+    z = np.asarray(z, np.uint64)
+    z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def splitmix_stream(seed, stream, n):
+    """Elements 0..n-1 of SplitMix64 stream `stream` of `seed`: element i is
+    mix(base + (i + 1) * gamma), base = mix(seed + gamma) ^
+    mix((stream + 1) * 0xD1B54A32D192ED03) -- the generator convention of the
+    model's tensors (after crates/logicaffeine_runtime/src/seed.rs)."""
+    import numpy as np
+
+    with np.errstate(over="ignore"):
+        base = (_sm_mix(np.uint64((seed + _SM_GAMMA) % 2**64)) ^
+                _sm_mix(np.uint64(((stream + 1) * 0xD1B54A32D192ED03) % 2**64)))
+        i = np.arange(1, n + 1, dtype=np.uint64)
+        return _sm_mix(base + i * np.uint64(_SM_GAMMA))
+
+
+def config1_inputs(seed=1):
+    """Config 1's Q8_0 weights from the seed-1 SplitMix64 streams, one stream
+    pair per matrix: quants uniform on [-127, 127] by the multiply-high map
+    of the top 32 bits, scales |N(0, 0.02)| / 127 by Box-Muller (binary64)
+    on draws 2i and 2i + 1, rounded to binary16.  Host arrays, shared by the
+    GPU leg and the CPU baseline."""
+    import numpy as np
+
+    out = {}
+    for j, (name, n, k) in enumerate(SHAPES):
+        u = splitmix_stream(seed, 10 + 2 * j, n * k)
+        qs = ((((u >> np.uint64(32)) * np.uint64(255)) >> np.uint64(32)).astype(np.int32) - 127)
+        qs = qs.astype(np.int8).reshape(n, k)
+        z = splitmix_normal_f32(seed, 11 + 2 * j, (n * (k // 32),)).astype(np.float64)
+        d = (np.abs(0.02 * z) / 127.0).astype(np.float32).astype(np.float16).view(np.uint16)
+        out[name] = (qs, d.reshape(n, k // 32))
+    return out
+
+
+def build_sets(ctx, torch, nsets, inputs):
+    base = {name: ctx.q8_matrix(*inputs[name]) for name, _, _ in SHAPES}
     import logicaffeine_amd as lgx
 
     sets = [base]
@@ -121,12 +160,24 @@ def run_step(ctx, sets, i, acts, m):
                                [acts[name][3] for name, _, _ in SHAPES])
 
 
+def splitmix_normal_f32(seed, stream, shape):
+    """N(0, 1) binary32 values by Box-Muller (binary64) on draws 2i, 2i + 1 of
+    a SplitMix64 stream."""
+    import numpy as np
+
+    n = int(np.prod(shape))
+    u = splitmix_stream(seed, stream, 2 * n)
+    u1 = ((u[0::2] >> np.uint64(11)) + np.uint64(1)).astype(np.float64) * 2.0**-53
+    u2 = (u[1::2] >> np.uint64(11)).astype(np.float64) * 2.0**-53
+    return (np.sqrt(-2.0 * np.log(u1)) * np.cos(6.283185307179586 * u2)).astype(np.float32).reshape(shape)
+
+
 def make_acts(ctx, torch, m):
+    """The step's activations: rows of the seed-1 streams 20, 21, 22 (the
+    CPU baseline's x is row 0 of the same streams)."""
     acts = {}
-    g = torch.Generator(device=ctx.dev)
-    g.manual_seed(1234 + m)
-    for name, n, k in SHAPES:
-        x = torch.randn((m, k), generator=g, device=ctx.dev, dtype=torch.float32)
+    for j, (name, n, k) in enumerate(SHAPES):
+        x = ctx.to_device(splitmix_normal_f32(1, 20 + j, (m, k)))
         xq = torch.empty((m, k), dtype=torch.int8, device=ctx.dev)
         xd = torch.empty((m, k // 32), dtype=torch.int16, device=ctx.dev)
         y = torch.empty((m, n), dtype=torch.float32, device=ctx.dev)
@@ -199,27 +250,26 @@ def cpu_model_name():
     return "unknown"
 
 
-def cpu_baseline(seconds=12.0):
-    """The CPU oracle's canonical Q8 x Q8 step (quantise + 3 matmuls, M = 1),
-    on all the oracle's OpenMP threads, then on one."""
+def cpu_baseline(inputs, seconds=12.0, copies=4):
+    """The CPU oracle's canonical Q8 x Q8 step (quantise + 3 matmuls, M = 1)
+    on the GPU leg's seed-1 weights, rotating over `copies` copies of them
+    (176 MB, past the host's last-level cache, so the weights stream from
+    DRAM as the GPU leg's stream from HBM), on all the oracle's OpenMP
+    threads, then on one."""
     import numpy as np
 
     from oracle import oracle as orc
 
-    rng = np.random.default_rng(7)
-    mats = []
-    for _, n, k in SHAPES:
-        qs = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
-        d = (np.abs(rng.normal(0.0, 0.02, size=(n, k // 32))) / 127.0).astype(np.float16)
-        x = rng.standard_normal((1, k)).astype(np.float32)
-        mats.append((qs, d.view(np.uint16), x))
+    xs = {name: splitmix_normal_f32(1, 20 + j, (1, k)) for j, (name, _, k) in enumerate(SHAPES)}
+    sets = [[(inputs[name][0].copy(), inputs[name][1].copy(), xs[name]) for name, _, _ in SHAPES]
+            for _ in range(copies)]
 
     def run(budget):
-        orc.q8_gemm(*mats[0][:2], *orc.quantize_q8_0(mats[0][2]))  # warm (threads, pages)
+        orc.q8_gemm(*sets[0][0][:2], *orc.quantize_q8_0(sets[0][0][2]))  # warm (threads, pages)
         t0 = time.perf_counter()
         reps = 0
         while True:
-            for qs, d, x in mats:
+            for qs, d, x in sets[reps % copies]:
                 xq, xd = orc.quantize_q8_0(x)
                 orc.q8_gemm(qs, d, xq, xd)
             reps += 1
@@ -241,7 +291,9 @@ def cpu_baseline(seconds=12.0):
         "kind": "port",
         "value_1core": round(step_bytes(1) * reps1 / el1 / 1e9, 3),
         "cpu_model": cpu_model_name(),
-        "sample": f"config-1 M=1 steps (quantise + gate/up/down Q8xQ8, canonical schedule): "
+        "sample": f"config-1 M=1 steps (quantise + gate/up/down Q8xQ8, canonical schedule) on "
+                  f"the seed-1 SplitMix64 weights, {copies} copies rotating "
+                  f"({copies * sum(q8_weight_bytes(n, k) for _, n, k in SHAPES) / 1e6:.0f} MB): "
                   f"{reps} in {el:.1f} s on {threads} OpenMP threads, {reps1} in {el1:.1f} s "
                   f"on 1",
     }
@@ -342,6 +394,66 @@ def sustained_gemv(ctx, torch, iters=60):
     torch.cuda.empty_cache()
     return {"shape": [n, k], "kernel": name, "us_per_launch": round(us, 2),
             "GB_s": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def kernel_probe_config4(torch, iters=20):
+    """The config-4 decode step's two dominant kernels alone, at the shapes the
+    step runs them (for counter passes, which cannot run beside the resident
+    27 GB model): the tiled Q8 product at M = 64 with 64 activation rows per
+    workgroup (lgx_k_q8_gemm_tiled64) for gate|up [37888 x 3584] and down
+    [3584 x 18944], and the d = 128 decode attention chunk kernel
+    (lgx_k_attn_chunk_d128_g7) at B = 64, 28 / 4 heads, context 4128.  Weights
+    and K/V pages rotate over two copies (> the Infinity Cache per pass).
+    Returns per-launch times from HIP events attached to each dispatch."""
+    import numpy as np
+
+    import logicaffeine_amd as lgx
+
+    os.environ["LGX_GEMM_TILED_ROWS"] = "64"
+    ctx = lgx.Context(0)
+    rng = np.random.default_rng(4)
+    out = {}
+    m = 64
+    for name, n, k in (("gate_up", 37888, 3584), ("down", 3584, 18944)):
+        qs = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+        d = (np.abs(rng.normal(0.0, 0.02, size=(n, k // 32))) / 127.0).astype(np.float16)
+        W0 = ctx.q8_matrix(qs, d.view(np.uint16))
+        Ws = [W0, lgx.Q8Matrix(W0.qs.clone(), W0.d.clone(), n, k)]
+        xq = ctx.to_device(rng.integers(-127, 128, size=(m, k), dtype=np.int8))
+        xd = ctx.to_device((np.abs(rng.normal(0.0, 0.01, size=(m, k // 32)))).astype(np.float16).view(np.uint16))
+        y = torch.empty((m, n), dtype=torch.float32, device=ctx.dev)
+        ctx.kernel_timing(True)
+        for i in range(iters):
+            ctx.q8_gemm(Ws[i % 2], xq, xd, y=y)
+        torch.cuda.synchronize()
+        ctx.kernel_timing(False)
+        cnt, tot = ctx.kernel_stats("lgx_k_q8_gemm_tiled64")
+        nbytes = q8_weight_bytes(n, k) + m * k * (1 + 2 / 32) + 4 * m * n
+        us = tot / max(cnt, 1) * 1e3
+        out[name] = {"shape": [n, k], "m": m, "kernel": "lgx_k_q8_gemm_tiled64", "launches": cnt,
+                     "us_per_launch": round(us, 2), "GB_s": round(nbytes / us / 1e3, 1)}
+        del Ws, W0
+        torch.cuda.empty_cache()
+    B, hq, hkv, dh, L = 64, 28, 4, 128, 4128
+    maxp = -(-L // 16)
+    pages = [torch.randn((B * maxp, hkv, 16, dh), device=ctx.dev).to(torch.float16).view(torch.int16)
+             for _ in range(4)]
+    pt = torch.randperm(B * maxp, device=ctx.dev).to(torch.int32).reshape(B, maxp)
+    lens = torch.full((B,), L, dtype=torch.int32, device=ctx.dev)
+    q = torch.randn((B, hq, dh), device=ctx.dev)
+    ctx.kernel_timing(True)
+    for i in range(iters):
+        ctx.gqa_decode_attn(q, pages[2 * (i % 2)], pages[2 * (i % 2) + 1], pt, lens, L)
+    torch.cuda.synchronize()
+    ctx.kernel_timing(False)
+    cnt, tot = ctx.kernel_stats("lgx_k_attn_chunk_d128_g7")
+    us = tot / max(cnt, 1) * 1e3
+    kv = B * L * hkv * dh * 2 * 2
+    out["attention"] = {"shape": {"batch": B, "hq": hq, "hkv": hkv, "head_dim": dh, "context": L},
+                        "kernel": "lgx_k_attn_chunk_d128_g7", "launches": cnt,
+                        "us_per_launch": round(us, 2), "GB_s": round(kv / us / 1e3, 1)}
+    ctx.close()
+    return out
 
 
 ATTN_SHAPE = (16, 12, 2, 128)   # BASELINE.json config 2: batch, query heads, KV heads, head_dim
@@ -467,6 +579,7 @@ def decode_bench(ctx, torch, key, seed=3, with_cpu=True):
         kv0 = [[gm.kv_rows(layer, w, 0, ctx_now, pt) for w in (0, 1)]
                for layer in range(cfg["n_layers"])]
     tok0 = int(tok[0].item())
+    prompt0 = prompt[0].cpu().numpy()
     gm.close()
     torch.cuda.empty_cache()
     pf_int8 = lgx.prefill_int8_ops(cfg, B, P)
@@ -496,13 +609,19 @@ def decode_bench(ctx, torch, key, seed=3, with_cpu=True):
           f"{eager_ms:.3f} ms/step (eager), {gbs:.0f} GB/s",
           file=sys.stderr, flush=True)
     if with_cpu:
-        out["cpu_baseline"] = cpu_decode_baseline(key, cfg, seed, kv0, ctx_now, tok0)
+        out["cpu_baseline"] = cpu_decode_baseline(key, cfg, seed, kv0, ctx_now, tok0, prompt0)
     return out
 
 
-def cpu_decode_baseline(key, cfg, seed, kv0, ctx_now, tok0, seconds=8.0):
-    """The CPU oracle model (a port; exact canonical arithmetic) decoding
-    sequence 0 of the benchmark at the benchmark's context: the device's
+# prompt tokens of sequence 0 the CPU oracle prefills for its prefill figure
+PREFILL_SAMPLE = {"config3": 1024, "config4": 512}
+
+
+def cpu_decode_baseline(key, cfg, seed, kv0, ctx_now, tok0, prompt0, seconds=8.0):
+    """The CPU oracle model (a port; exact canonical arithmetic) on sequence 0
+    of the benchmark.  Prefill: the first tokens of its prompt, timed on all
+    of the oracle's threads (a bounded sample: PREFILL_SAMPLE tokens) and on
+    one (an eighth of them).  Decode at the benchmark's context: the device's
     prefilled cache of that sequence (bit-identical to the oracle's, which the
     GPU tests check) is loaded into the oracle, then greedy steps are timed
     for `seconds` on all of its threads and for seconds / 2 on one."""
@@ -513,6 +632,21 @@ def cpu_decode_baseline(key, cfg, seed, kv0, ctx_now, tok0, seconds=8.0):
     shape = DECODE_CONFIGS[key][0]
     ocfg = dict(cfg, max_batch=1, max_seq=ctx_now + 64)
     om = orc.Model(ocfg, seed)
+    threads = orc.max_threads()
+    npf = PREFILL_SAMPLE[key]
+
+    def prefill(n):
+        om.set_seq_len(0, 0)
+        t0 = time.perf_counter()
+        om.prefill([0], np.ascontiguousarray(prompt0[None, :n], np.int32))
+        return time.perf_counter() - t0
+
+    pf_el = prefill(npf)
+    orc.set_threads(1)
+    try:
+        pf_el1 = prefill(npf // 8)
+    finally:
+        orc.set_threads(threads)
     for layer, (k, v) in enumerate(kv0):
         om.load_kv(layer, 0, 0, k)
         om.load_kv(layer, 1, 0, v)
@@ -529,7 +663,6 @@ def cpu_decode_baseline(key, cfg, seed, kv0, ctx_now, tok0, seconds=8.0):
                 break
         return n, time.perf_counter() - t0
 
-    threads = orc.max_threads()
     n, el = run(seconds, 32)
     om.set_seq_len(0, ctx_now)
     orc.set_threads(1)
@@ -542,7 +675,12 @@ def cpu_decode_baseline(key, cfg, seed, kv0, ctx_now, tok0, seconds=8.0):
             "value_1core": round(n1 / el1, 4), "cpu_model": cpu_model_name(),
             "sample": f"{shape} shape, sequence 0 of the batch at context {ctx_now} (device-"
                       f"prefilled cache loaded into the oracle), batch 1: {n} greedy steps in "
-                      f"{el:.1f} s on {threads} threads, {n1} in {el1:.1f} s on 1"}
+                      f"{el:.1f} s on {threads} threads, {n1} in {el1:.1f} s on 1",
+            "prefill": {"value": round(npf / pf_el, 2), "unit": "tokens/s", "cores": threads,
+                        "value_1core": round((npf // 8) / pf_el1, 3),
+                        "sample": f"the first {npf} prompt tokens of sequence 0 prefilled by the "
+                                  f"oracle (batched over positions) in {pf_el:.1f} s on {threads} "
+                                  f"threads; {npf // 8} in {pf_el1:.1f} s on 1"}}
 
 
 def main():
@@ -554,6 +692,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--decode", default="config3,config4",
                     help="decode configs to run (comma list; empty for none)")
+    ap.add_argument("--kernel-probe", action="store_true",
+                    help="only run the config-4 decode's tiled product and attention kernels "
+                         "standalone (for counter passes) and print their timings")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 4 plain 256 MiB device copies (HBM counter calibration)")
     args = ap.parse_args()
@@ -566,10 +707,14 @@ def main():
 
     import logicaffeine_amd as lgx
 
+    if args.kernel_probe:
+        print(json.dumps({"config4_kernels": kernel_probe_config4(torch)}), flush=True)
+        return
     ctx = lgx.Context(0)
     set_bytes = sum(q8_weight_bytes(n, k) for _, n, k in SHAPES)
     nsets = max(2, -(-2 * MALL_BYTES // set_bytes))
-    sets = build_sets(ctx, torch, nsets)
+    inputs = config1_inputs(1)
+    sets = build_sets(ctx, torch, nsets, inputs)
     print(f"[bench] {nsets} weight sets x {set_bytes / 1e6:.1f} MB rotating", file=sys.stderr,
           flush=True)
 
@@ -610,7 +755,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (int8 U[-127,127], d=|N(0,0.02)|/127 f16, x~N(0,1) f32)",
+        "data": "synthetic, seed-1 SplitMix64 streams (int8 U[-127,127], d=|N(0,0.02)|/127 f16, "
+                "x~N(0,1) f32)",
         "config": {
             "workload": "config1 Qwen2.5-1.5B MLP Q8_0 gate/up [8960x1536] + down [1536x8960], "
                         "M=1 (one grouped launch: fused quantise + whole-K Q8xQ8 GEMV of the "
@@ -667,7 +813,7 @@ def main():
     if decode:
         out["qwen_decode"] = decode
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(inputs, args.cpu_seconds)
     ctx.close()
     print(json.dumps(out), flush=True)
 
