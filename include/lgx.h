@@ -261,8 +261,10 @@ lgx_status lgx_rope_kv_append(lgx_ctx* ctx, const float* qkv, const float* bias,
  * silu(g) = g / (1 + exp(-g)); a (binary32) and/or Q8_0(a) written. */
 lgx_status lgx_swiglu_quant(lgx_ctx* ctx, const float* gu, int32_t m, int32_t inter, float* y,
                             int8_t* xq, uint16_t* xd, void* stream);
-/* logits[m][v] = sequential fmaf chain over k of x[m][k] * emb[v][k]
- * (binary16 tied embedding); h % 64 == 0, h <= 1024. */
+/* logits[m][v] = canonical dot of x[m] with emb[v] (binary16 tied
+ * embedding): a sequential fmaf chain over each 1024-column range of k, then
+ * the pairwise tree over the ranges (one range, the chain itself, for
+ * h <= 1024); h % 64 == 0, h <= 8192. */
 lgx_status lgx_lm_head_f16(lgx_ctx* ctx, const float* x, const uint16_t* emb, int32_t m,
                            int32_t h, int32_t vocab, float* logits, void* stream);
 /* Binary16 rows [rows][h] -> T64 order: 1 KiB units (g, j), lane l of a
@@ -273,7 +275,7 @@ lgx_status lgx_f16_repack_t64(lgx_ctx* ctx, const uint16_t* src, int32_t rows, i
                               uint16_t* dst, void* stream);
 /* lgx_lm_head_f16 over a T64 embedding (same logits, bit for bit): one
  * whole-1 KiB wave load per 64 rows x 8 columns, activations through the
- * scalar cache.  h % 64 == 0, h <= 1024, m <= 64. */
+ * scalar cache.  h % 64 == 0, h <= 8192, m <= 64. */
 lgx_status lgx_lm_head_f16_t64(lgx_ctx* ctx, const float* x, const uint16_t* emb_t64, int32_t m,
                                int32_t h, int32_t vocab, float* logits, void* stream);
 /* Per-row constants of a binary16 embedding [vocab][h] for
@@ -331,7 +333,9 @@ typedef struct lgx_model lgx_model;
 
 typedef struct {
     int32_t n_layers, hidden, intermediate, n_heads, n_kv_heads, head_dim, vocab;
-    int32_t tied_embedding; /* 1: logits from the binary16 embedding (exact chain) */
+    int32_t tied_embedding; /* 1: logits from the binary16 embedding (the
+                               lgx_lm_head_f16 dot: 1024-column range chains
+                               and their tree) */
     int32_t max_batch, max_seq;
     float rms_eps;          /* 1e-6 */
     double rope_theta;      /* 1e6 */

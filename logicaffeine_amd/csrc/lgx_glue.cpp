@@ -12,7 +12,7 @@
 using namespace lgxi;
 
 namespace {
-constexpr int kNormMax = 8192, kQkvMax = 8192, kLmMaxH = 1024, kLmMaxM = 64;
+constexpr int kNormMax = 8192, kQkvMax = 8192, kLmMaxH = 8192, kLmMaxM = 64;
 }
 
 extern "C" {
@@ -150,12 +150,24 @@ lgx_status lgx_lm_head_f16(lgx_ctx* c, const float* x, const uint16_t* emb, int3
         if (m <= 0 || vocab <= 0 || h <= 0 || h % 64 || h > kLmMaxH)
             return fail(LGX_UNSUPPORTED, "m %d, vocab %d, h %d (h %% 64 == 0, h <= %d)", m, vocab,
                         h, kLmMaxH);
+        // one chain per 1024-column range; more than one range: the range
+        // partials in the workspace, then the pairwise tree into logits
+        const int nr = (h + 1023) / 1024;
         for (int r0 = 0; r0 < m; r0 += kLmMaxM) {
-            lgx_lmhead_args a{x + (int64_t)r0 * h, emb, logits + (int64_t)r0 * vocab,
-                              std::min(kLmMaxM, m - r0), h, vocab};
-            if ((st = launch(c, K_LM_HEAD_F16, dim3(cdiv(vocab, 256)), dim3(256), a, stream)) !=
+            const int mm = std::min(kLmMaxM, m - r0);
+            float* out = logits + (int64_t)r0 * vocab;
+            float* part = out;
+            if (nr > 1 && (st = ensure_ws(c, (size_t)nr * mm * vocab * sizeof(float), &part)) != LGX_OK)
+                return st;
+            lgx_lmhead_args a{x + (int64_t)r0 * h, emb, part, mm, h, vocab};
+            if ((st = launch(c, K_LM_HEAD_F16, dim3(cdiv(vocab, 256), nr), dim3(256), a, stream)) !=
                 LGX_OK)
                 return st;
+            if (nr > 1) {
+                lgx_combine_args ca{part, out, (int64_t)mm * vocab, nr};
+                if ((st = launch(c, K_COMBINE, dim3(cdiv(ca.count, 256)), dim3(256), ca, stream)) != LGX_OK)
+                    return st;
+            }
         }
         return LGX_OK;
     });
@@ -189,16 +201,25 @@ lgx_status lgx_lm_head_f16_t64(lgx_ctx* c, const float* x, const uint16_t* emb_t
         if (m <= 0 || m > kLmMaxM || vocab <= 0 || h <= 0 || h % 64 || h > kLmMaxH)
             return fail(LGX_UNSUPPORTED, "m %d (<= %d), vocab %d, h %d (h %% 64 == 0, h <= %d)",
                         m, kLmMaxM, vocab, h, kLmMaxH);
-        // the activation in T16 column order, in the workspace
-        const int mc = (m + 15) / 16;
+        // the activation in T16 column order in the workspace, followed there
+        // by the range partials when h holds more than one 1024-column range
+        const int mc = (m + 15) / 16, nr = (h + 1023) / 1024;
+        const size_t nxt = (size_t)mc * 16 * h;
         float* xt = nullptr;
-        if ((st = ensure_ws(c, (size_t)mc * 16 * h * sizeof(float), &xt)) != LGX_OK) return st;
+        if ((st = ensure_ws(c, (nxt + (nr > 1 ? (size_t)nr * m * vocab : 0)) * sizeof(float), &xt)) !=
+            LGX_OK)
+            return st;
         lgx_t64_args ta{x, xt, m, h};
         if ((st = launch(c, K_ROWS_TO_T16, dim3(cdiv((int64_t)m * h, 256)), dim3(256), ta,
                          stream)) != LGX_OK)
             return st;
-        lgx_lmhead_args a{xt, emb_t64, logits, m, h, vocab};
-        return launch(c, K_LM_HEAD_T64, dim3(cdiv(vocab, 64), mc), dim3(64), a, stream);
+        float* part = nr > 1 ? xt + nxt : logits;
+        lgx_lmhead_args a{xt, emb_t64, part, m, h, vocab};
+        if ((st = launch(c, K_LM_HEAD_T64, dim3(cdiv(vocab, 64), mc, nr), dim3(64), a, stream)) != LGX_OK)
+            return st;
+        if (nr == 1) return LGX_OK;
+        lgx_combine_args ca{part, logits, (int64_t)m * vocab, nr};
+        return launch(c, K_COMBINE, dim3(cdiv(ca.count, 256)), dim3(256), ca, stream);
     });
 }
 

@@ -2663,10 +2663,14 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_lm_head_f16(const lgx_lm
     const int t = threadIdx.x;
     const int v0 = blockIdx.x * 256;
     const int v = v0 + t;
+    // range blockIdx.y: columns [1024 y, min(h, 1024 y + 1024)), its chain
+    // to range partial y ([ranges][m][vocab]; one range for h <= 1024)
+    const int kb = blockIdx.y * 1024, ke = min(a.h, kb + 1024);
+    float* lg = a.logits + (int64_t)blockIdx.y * a.m * a.vocab;
     float acc[LGX_LM_MAXM];
 #pragma unroll
     for (int r = 0; r < LGX_LM_MAXM; ++r) acc[r] = 0.0f;
-    for (int k0 = 0; k0 < a.h; k0 += 64) {
+    for (int k0 = kb; k0 < ke; k0 += 64) {
         __syncthreads();
         for (int s2 = t; s2 < 256 * 32; s2 += 256) {
             const int rr = s2 >> 5, cc = s2 & 31;
@@ -2698,7 +2702,7 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_lm_head_f16(const lgx_lm
     if (v >= a.vocab) return;
 #pragma unroll
     for (int r = 0; r < LGX_LM_MAXM; ++r)
-        if (r < a.m) a.logits[(int64_t)r * a.vocab + v] = acc[r];
+        if (r < a.m) lg[(int64_t)r * a.vocab + v] = acc[r];
 }
 
 // Binary16 rows in T64 order: unit (g, j) = 1 KiB, lane l holds columns
@@ -2728,10 +2732,12 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_rows_to_t16(const lgx_t6
     ((float*)a.dst)[((int64_t)(row >> 4) * a.h + col) * 16 + (row & 15)] = ((const float*)a.src)[i];
 }
 
-// Tied binary16 lm_head over T64 rows (h <= 1024: one canonical range, the
-// logit is the sequential fmaf chain over the columns).  One wave per (64
-// vocabulary rows, 16 activation rows): lane l owns vocabulary row 64g + l
-// and keeps 16 chains.  The activation comes in T16 column order, so the 16
+// Tied binary16 lm_head over T64 rows: the canonical chain of one
+// 1024-column range per blockIdx.z (the sequential fmaf chain over the
+// range's columns) into range partial z ([ranges][m][vocab], the consumers
+// apply the pairwise tree; h <= 1024 is one range, the logit itself).  One
+// wave per (64 vocabulary rows, 16 activation rows, range): lane l owns
+// vocabulary row 64g + l and keeps 16 chains.  The activation comes in T16 column order, so the 16
 // values of one column are one 64-byte scalar load into SGPRs (wave-uniform,
 // no LDS traffic) feeding 16 independent chains; the binary16 units stream
 // in as whole 1 KiB wave loads, LGX_LMT_PF units ahead.
@@ -2741,6 +2747,8 @@ extern "C" __global__ __launch_bounds__(64) void lgx_k_lm_head_t64(const lgx_lmh
     const int g = blockIdx.x, lane = threadIdx.x;
     const int m0 = blockIdx.y * 16, nm = min(16, a.m - m0);
     const int ncg = a.h >> 3;
+    // the range's units (8 columns each): [128 z, min(ncg, 128 z + 128))
+    const int jb = blockIdx.z * 128, je = min(ncg, jb + 128);
     const uint4* ep = (const uint4*)a.emb + (int64_t)g * ncg * 64 + lane;
     const cfloat_p xt = (cfloat_p)(a.x + (int64_t)blockIdx.y * a.h * 16);
     float acc[16];
@@ -2751,13 +2759,13 @@ extern "C" __global__ __launch_bounds__(64) void lgx_k_lm_head_t64(const lgx_lmh
     // compiler's wait counts stay exact
     uint4 e[LGX_LMT_PF];
 #pragma unroll
-    for (int u = 0; u < LGX_LMT_PF; ++u) e[u] = ep[u * 64];
-    for (int j0 = 0; j0 < ncg; j0 += LGX_LMT_PF) {
+    for (int u = 0; u < LGX_LMT_PF; ++u) e[u] = ep[(jb + u) * 64];
+    for (int j0 = jb; j0 < je; j0 += LGX_LMT_PF) {
 #pragma unroll
         for (int u = 0; u < LGX_LMT_PF; ++u) {
             const int j = j0 + u;
             const uint4 cur = e[u];
-            e[u] = ep[min(j + LGX_LMT_PF, ncg - 1) * 64];
+            e[u] = ep[min(j + LGX_LMT_PF, je - 1) * 64];
             const float ev[8] = {h2f(cur.x & 0xffffu), h2f(cur.x >> 16), h2f(cur.y & 0xffffu),
                                  h2f(cur.y >> 16),     h2f(cur.z & 0xffffu), h2f(cur.z >> 16),
                                  h2f(cur.w & 0xffffu), h2f(cur.w >> 16)};
@@ -2771,9 +2779,10 @@ extern "C" __global__ __launch_bounds__(64) void lgx_k_lm_head_t64(const lgx_lmh
     }
     const int v = 64 * g + lane;
     if (v >= a.vocab) return;
+    float* lg = a.logits + (int64_t)blockIdx.z * a.m * a.vocab;
 #pragma unroll
     for (int r = 0; r < 16; ++r)
-        if (r < nm) a.logits[(int64_t)(m0 + r) * a.vocab + v] = acc[r];
+        if (r < nm) lg[(int64_t)(m0 + r) * a.vocab + v] = acc[r];
 }
 
 // Greedy token, in two launches.  Partial: workgroup (slice, row) takes the

@@ -252,8 +252,6 @@ lgx_status check_config(const lgx_qwen_config* c) {
     if (H > 8192 || (hq + 2 * hkv) * d > 8192 || hq * d > 8192 || I > 32768)
         return fail(LGX_UNSUPPORTED, "hidden %d / qkv %d / intermediate %d too large", H,
                     (hq + 2 * hkv) * d, I);
-    if (c->tied_embedding && H > 1024)
-        return fail(LGX_UNSUPPORTED, "tied binary16 lm_head needs hidden <= 1024 (got %d)", H);
     if (!c->tied_embedding && c->vocab % 16)
         return fail(LGX_UNSUPPORTED, "untied Q8_0 lm_head needs vocab %% 16 == 0");
     return LGX_OK;
@@ -496,12 +494,14 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
     const float* lg;
     int nr;
     if (tied) {
+        // one chain per 1024-column range of the hidden size: range partials
+        // [nr][B][vocab], the argmax / draw applies the tree
+        nr = nranges_of(H);
         lgx_lmhead_args la{md->xt, md->emb_t64, md->logits, B, H, cf.vocab};
-        if ((st = launch(c, K_LM_HEAD_T64, dim3(cdiv(cf.vocab, 64), cdiv(B, 16)), dim3(64), la,
+        if ((st = launch(c, K_LM_HEAD_T64, dim3(cdiv(cf.vocab, 64), cdiv(B, 16), nr), dim3(64), la,
                          stream)) != LGX_OK)
             return st;
         lg = md->logits;
-        nr = 1;
     } else {
         if ((st = product(md, md->lm, B, stream)) != LGX_OK) return st;
         lg = md->part;
@@ -863,7 +863,8 @@ lgx_status model_build(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed, So
             (st = dev_alloc(m, &m->sd, (size_t)B * I / 32)) ||
             (st = dev_alloc(m, &m->q, (size_t)B * hq * d)) || (st = dev_alloc(m, &m->part, (size_t)part)) ||
             (st = dev_alloc(m, &m->attn_part, (size_t)B * hq * m->nchunk * (d + 2))) ||
-            (st = dev_alloc(m, &m->logits, cf.tied_embedding ? (size_t)B * cf.vocab : 1)) ||
+            (st = dev_alloc(m, &m->logits,
+                            cf.tied_embedding ? (size_t)nranges_of(H) * B * cf.vocab : 1)) ||
             (st = dev_alloc(m, &m->cand, (size_t)B * argmax_slices(cf.vocab) * 2)) ||
             (cf.vocab <= 64 * LGX_ARGMAX_SLICE &&
              (st = dev_alloc(m, &m->scand, sample_cand_bytes(B, cf.vocab) / 8))))
@@ -1164,7 +1165,7 @@ lgx_status lgx_qwen_logits(lgx_model* m, int32_t B, float* out, void* stream) {
             // the certified pick left no logits: the exact lm_head of the
             // step's final-norm rows (still in xt) first
             lgx_lmhead_args la{m->xt, m->emb_t64, m->logits, B, m->c.hidden, m->c.vocab};
-            if ((st = launch(m->ctx, K_LM_HEAD_T64, dim3(cdiv(m->c.vocab, 64), cdiv(B, 16)),
+            if ((st = launch(m->ctx, K_LM_HEAD_T64, dim3(cdiv(m->c.vocab, 64), cdiv(B, 16), 1),
                              dim3(64), la, stream)) != LGX_OK)
                 return st;
         }

@@ -149,8 +149,11 @@ def test_swiglu_quant_bit_exact(ctx, orc, m, inter):
 
 
 @pytest.mark.parametrize("m,h,vocab", [(1, 64, 300), (5, 256, 1000), (64, 896, 2048),
-                                       (70, 896, 1000)])
+                                       (70, 896, 1000), (3, 1536, 700), (65, 2048, 300),
+                                       (2, 8192, 130)])
 def test_lm_head_f16_bit_exact(ctx, orc, m, h, vocab):
+    """Chains per 1024-column range and the pairwise tree over the ranges
+    (h > 1024: range partials, then the tree) equal the oracle's logits."""
     rng = np.random.default_rng(m * h + vocab)
     x = rng.standard_normal((m, h)).astype(np.float32)
     E = orc.f32_to_f16((rng.standard_normal((vocab, h)) * 0.02).astype(np.float32))
@@ -159,7 +162,8 @@ def test_lm_head_f16_bit_exact(ctx, orc, m, h, vocab):
 
 
 @pytest.mark.parametrize("m,h,vocab", [(1, 64, 300), (5, 256, 1000), (17, 896, 2048),
-                                       (64, 1024, 4160), (32, 896, 151936)])
+                                       (64, 1024, 4160), (32, 896, 151936), (5, 1536, 1000),
+                                       (20, 3072, 700), (2, 8192, 130)])
 def test_lm_head_f16_t64_bit_exact(ctx, orc, m, h, vocab):
     """The T64 path (repacked embedding, activations in SGPRs) gives the
     oracle's logits bit for bit, including a ragged last row group and a
@@ -218,8 +222,8 @@ def test_glue_argument_errors(ctx):
     t = ctx.torch
     x = t.zeros((2, 64), dtype=t.float32, device=ctx.dev)
     with pytest.raises(lgx.LgxError) as e:
-        ctx.lm_head_f16(t.zeros((1, 1088), dtype=t.float32, device=ctx.dev),
-                        t.zeros((4, 1088), dtype=t.int16, device=ctx.dev))
+        ctx.lm_head_f16(t.zeros((1, 8256), dtype=t.float32, device=ctx.dev),    # h > 8192
+                        t.zeros((4, 8256), dtype=t.int16, device=ctx.dev))
     assert e.value.status_name == "LGX_UNSUPPORTED"
     with pytest.raises(lgx.LgxError) as e:          # m > 64 on the T64 path
         ctx.lm_head_f16_t64(t.zeros((65, 64), dtype=t.float32, device=ctx.dev),

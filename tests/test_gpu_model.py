@@ -224,7 +224,7 @@ def test_model_argument_errors(ctx):
     from oracle import oracle as orc
 
     cfg = dict(orc.qwen_config("tiny"))
-    for bad in (dict(head_dim=96), dict(n_heads=20, n_kv=2), dict(hidden=2048),
+    for bad in (dict(head_dim=96), dict(n_heads=20, n_kv=2), dict(hidden=16384),
                 dict(hidden=200)):
         with pytest.raises(lgx.LgxError):
             lgx.Model(ctx, dict(cfg, **bad), 1)
@@ -508,3 +508,44 @@ def test_fused_decode_consumers_bit_exact(name, env):
     gm.close()
     om.close()
     c.close()
+
+
+@pytest.mark.parametrize("hidden", [1536, 2048])
+def test_tied_model_hidden_above_1024(ctx, hidden):
+    """A tied binary16 embedding with hidden > 1024 (the Qwen2.5-1.5B / 3B
+    widths): the lm_head runs one chain per 1024-column range and the
+    argmax, the seeded draw and the logits entry point apply the pairwise
+    tree over them (the certified pick covers hidden <= 1024 only).  Tokens
+    and logits equal the oracle's through prefill, greedy decode, graph
+    replays and sampled decode."""
+    from oracle import oracle as orc
+
+    cfg = dict(orc.qwen_config("tiny"), n_layers=2, hidden=hidden, inter=512, n_heads=hidden // 128,
+               n_kv=2, head_dim=128, vocab=1000, tied=1, max_batch=4, max_seq=64)
+    gm = lgx.Model(ctx, cfg, 17)
+    om = orc.Model(cfg, 17)
+    rng = np.random.default_rng(hidden)
+    B, P = 4, 9
+    prompt = rng.integers(0, cfg["vocab"], size=(B, P)).astype(np.int32)
+    tok = gm.prefill(ctx.to_device(prompt))
+    ref, lg = om.prefill(np.arange(B), prompt, want_logits=True)
+    assert np.array_equal(host(tok), ref)
+    assert np.array_equal(bits(host(gm.logits(B))), bits(lg))
+    for s in range(4):
+        gm.decode_step(tok)
+        ref, lg = om.step(np.arange(B), ref, want_logits=True)
+        assert np.array_equal(host(tok), ref), s
+        assert np.array_equal(bits(host(gm.logits(B))), bits(lg)), s
+    hist = ctx.torch.empty((3, B), dtype=ctx.torch.int32, device=ctx.dev)
+    gm.generate(tok, 3, hist)
+    for s in range(3):
+        ref = om.step(np.arange(B), ref)
+        assert np.array_equal(host(hist[s]), ref), s
+    gm.set_sampling(0.8, top_k=20, top_p=0.9, seed=5)
+    om.set_sampling(0.8, top_k=20, top_p=0.9, seed=5)
+    for s in range(4):
+        gm.decode_step(tok)
+        ref = om.step(np.arange(B), ref)
+        assert np.array_equal(host(tok), ref), ("sampled", s)
+    gm.close()
+    om.close()
