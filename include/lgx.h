@@ -359,7 +359,9 @@ enum {
     LGX_T_HIDDEN = 16,    /* binary32 [max_batch][hidden]: last final-norm output */
     LGX_T_ATTN_NORM = 17, /* binary32 [hidden] RMSNorm weight before attention */
     LGX_T_FFN_NORM = 18,  /* binary32 [hidden] RMSNorm weight before the MLP */
-    LGX_T_OUT_NORM = 19   /* binary32 [hidden] final RMSNorm weight */
+    LGX_T_OUT_NORM = 19,  /* binary32 [hidden] final RMSNorm weight */
+    LGX_T_EMB_Q = 20,     /* Q8_0 embedding quants (a checkpoint's Q8_0 token_embd), T16 */
+    LGX_T_EMB_D = 21      /* Q8_0 embedding scales, S16 */
 };
 
 /* Generates every tensor from SplitMix64 streams of `seed` (quants uniform on
@@ -376,13 +378,17 @@ lgx_status lgx_model_destroy(lgx_model* m);
  * .embedding_length, .feed_forward_length, .attention.head_count,
  * .attention.head_count_kv (optional: .attention.key_length,
  * .attention.layer_norm_rms_epsilon, .rope.freq_base); tensors
- * token_embd.weight (F16), output_norm.weight (F32), output.weight (Q8_0;
- * absent = tied embedding), and per layer N blk.N.attn_norm / ffn_norm
+ * token_embd.weight (F16 or Q8_0), output_norm.weight (F32), output.weight
+ * (Q8_0; absent = tied embedding), and per layer N blk.N.attn_norm / ffn_norm
  * (F32), attn_q / attn_k / attn_v / attn_output / ffn_gate / ffn_up /
  * ffn_down .weight (Q8_0: blocks of a binary16 scale + 32 int8) and
  * attn_q / attn_k / attn_v .bias (F32).  The query/key rows are taken in
- * the file's (Hugging Face rotate-half) order.  No counterpart in the
- * reference, which has no model format.
+ * the file's (Hugging Face rotate-half) order.  A Q8_0 token_embd
+ * (vocab % 16 == 0) is gathered as f32(d) * q per element, and a tied model
+ * with it takes its logits from the Q8 product of the Q8_0 final-norm rows
+ * with that matrix, as an untied Q8_0 output.weight would (a binary16
+ * token_embd keeps the binary16 lm_head).  No counterpart in the reference,
+ * which has no model format.
  * lgx_gguf_config parses the file on the host (no device) and returns the
  * model shape with max_batch / max_seq filled in; lgx_model_load_gguf builds
  * the model from the file (synchronous; the file is read tensor by tensor).

@@ -174,7 +174,7 @@ def prefill_valu_ops(cfg: dict, B: int, P: int) -> float:
 MODEL_TENSORS = {"emb": 0, "lm_q": 1, "lm_d": 2, "qkv_q": 3, "qkv_d": 4, "o_q": 5, "o_d": 6,
                  "gu_q": 7, "gu_d": 8, "dn_q": 9, "dn_d": 10, "bias": 11, "k_pages": 12,
                  "v_pages": 13, "page_table": 14, "seq_len": 15, "hidden": 16,
-                 "attn_norm": 17, "ffn_norm": 18, "out_norm": 19}
+                 "attn_norm": 17, "ffn_norm": 18, "out_norm": 19, "emb_q": 20, "emb_d": 21}
 
 
 class LgxError(RuntimeError):

@@ -9,7 +9,8 @@
 //   tensor infos: name, n_dims u32, dims u64[n_dims] (dims[0] the row length),
 //     ggml type u32, offset u64 (from the data section),
 //   padding to general.alignment (default 32), then the data section.
-// Tensor types read here: F32 (0), F16 (1) and Q8_0 (8): blocks of 32
+// Tensor types read here: F32 (0), F16 (1) and Q8_0 (8; also for
+// token_embd, as llama.cpp's Q8_0 conversion stores it): blocks of 32
 // values stored as a binary16 scale d followed by 32 int8 quants (34 bytes),
 // the same block as the Q8_0 format the kernels use, so a row of Q8_0 blocks
 // splits into the row-major quants/scales that lgx_q8_repack_t16 takes.
@@ -333,8 +334,8 @@ lgx_status Gguf::config(int32_t max_batch, int32_t max_seq, lgx_qwen_config* cfg
     if ((int64_t)emb->dims[0] != c.hidden)
         return fail(LGX_INVALID_ARGUMENT, "%s: token_embd row length %llu, hidden %d", path.c_str(),
                     (unsigned long long)emb->dims[0], c.hidden);
-    if (emb->type != GGML_F16)
-        return fail(LGX_UNSUPPORTED, "%s: token_embd.weight has ggml type %u (F16 is read)",
+    if (emb->type != GGML_F16 && emb->type != GGML_Q8_0)
+        return fail(LGX_UNSUPPORTED, "%s: token_embd.weight has ggml type %u (F16 and Q8_0 are read)",
                     path.c_str(), emb->type);
     *cfg = c;
     return LGX_OK;

@@ -137,6 +137,7 @@ enum Kern {
     K_NORM4S_R8,
     K_GEMM_TILED64_S4,
     K_GEMM_TILED32_S4,
+    K_EMBED_Q8,
     K_COUNT
 };
 inline const char* const kKernelNames[] = {
@@ -171,7 +172,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_q8_gemm_mfma16_group", "lgx_k_q8_gemm_mfma32_group", "lgx_k_q8_gemm_tiled_group", "lgx_k_q8_gemm_tiled64_group",
     "lgx_k_q8_gemm_tiled32_group", "lgx_k_quantize_group", "lgx_k_q8_combine_group",
     "lgx_k_lm_rowconst", "lgx_k_lm_cert", "lgx_k_lm_pick", "lgx_k_add_rmsnorm_quant4s_r8",
-    "lgx_k_q8_gemm_tiled64s4", "lgx_k_q8_gemm_tiled32s4",
+    "lgx_k_q8_gemm_tiled64s4", "lgx_k_q8_gemm_tiled32s4", "lgx_k_embed_q8",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,

@@ -115,6 +115,16 @@ typedef struct {
     int32_t m, n, vocab, tokens_stride;
     int32_t qpr;           // rows per sequence (0 or 1: one)
 } lgx_embed_args;
+// Gather of a Q8_0 embedding [vocab][n] in T16 / S16 tiles: h[r][i] =
+// f32(d) * q of the token's element i (binary32, exact).
+typedef struct {
+    const int8_t* wt;      // T16 quants
+    const uint16_t* wd;    // S16 scales
+    const int32_t* tokens;
+    float* h;              // [m][n]
+    int32_t m, n, vocab, tokens_stride;
+    int32_t qpr;
+} lgx_embed_q8_args;
 
 // seq_len[b] = (keep ? seq_len[b] : 0) + add for b < m
 typedef struct {

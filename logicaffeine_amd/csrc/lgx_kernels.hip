@@ -2025,6 +2025,23 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_embed(const lgx_embed_ar
     for (int i = threadIdx.x; i < a.n; i += 256) a.h[(int64_t)row * a.n + i] = h2f(er[i]);
 }
 
+// Q8_0 embedding rows (a checkpoint's token_embd stored as Q8_0): element i
+// of token v is f32(d[v][i/32]) * q[v][i], read from the T16 quant tiles
+// (byte 8(i%64 >= 32) + i%8 of lane v%16 + 16 (i%32)/8 in unit (v/16, i/64))
+// and the S16 scale tiles.
+extern "C" __global__ __launch_bounds__(256) void lgx_k_embed_q8(const lgx_embed_q8_args a) {
+    const int row = blockIdx.x, qpr = max(a.qpr, 1), b = row / qpr;
+    const int tok = min(max(a.tokens[(int64_t)b * a.tokens_stride + (row - b * qpr)], 0), a.vocab - 1);
+    const int np = a.n >> 6, nh = s16_nhalf(a.n), t = tok >> 4, r = tok & 15;
+    for (int i = threadIdx.x; i < a.n; i += 256) {
+        const int kk = i & 63, half = kk >> 5, c = (kk & 31) >> 3;
+        const int8_t q = a.wt[((int64_t)t * np + (i >> 6)) * 1024 + (r + 16 * c) * 16 + 8 * half + (kk & 7)];
+        const int bl = i >> 5;
+        const uint16_t d = a.wd[(((int64_t)t * nh + (bl >> 4)) * 16 + r) * 16 + (bl & 15)];
+        a.h[(int64_t)row * a.n + i] = h2f(d) * (float)q;
+    }
+}
+
 // The canonical pairwise tree over nr (<= R) values, evaluated as they
 // arrive in index order: after value j the pending subtrees are the set bits
 // of j + 1 (L[k] holds one of 2^k values), merged earlier + later as in the

@@ -50,6 +50,11 @@ struct lgx_model {
     float* out_norm = nullptr;                 // final RMSNorm weight
     std::vector<uint16_t*> kc, vc;
     uint16_t* emb = nullptr;
+    // a checkpoint's Q8_0 token embedding (T16 / S16 tiles): the gather
+    // dequantises it, and a tied model's lm_head is the Q8 product with it
+    // (lm then describes the same tiles); emb stays null
+    bool emb_q8 = false;
+    DevQ8 embq;
     uint16_t* emb_t64 = nullptr;   // tied lm_head: the embedding in T64 order
     float* xt = nullptr;           // tied lm_head: final-norm rows in T16 column order
     // certified greedy lm_head (tied): per-row embedding constants, slice
@@ -131,13 +136,15 @@ lgx_status dev_alloc(lgx_model* m, T** p, size_t count) {
 
 // Where a model's tensors come from: the seeded generator or a checkpoint
 // file.  Q8_0 matrices are row-major quants [n][k] + scales [n][k/32].
-enum { W_QKV, W_O, W_GU, W_DN, W_LM };
+enum { W_QKV, W_O, W_GU, W_DN, W_LM, W_EMB };
 enum { V_BIAS, V_ATTN_NORM, V_FFN_NORM, V_OUT_NORM };
 struct Source {
     virtual ~Source() = default;
     virtual lgx_status q8(int which, int layer, int32_t n, int32_t k, int8_t* qs, uint16_t* d) = 0;
     virtual lgx_status vec(int which, int layer, int32_t n, float* out) = 0;
     virtual lgx_status emb(int32_t V, int32_t H, uint16_t* out) = 0;
+    // the embedding comes as a Q8_0 matrix (q8(W_EMB, ...)) instead of binary16
+    virtual bool emb_is_q8() const { return false; }
 };
 
 // The random-init model: SplitMix64 streams 1000 + 16 layer + {0,1: Wqkv;
@@ -190,6 +197,7 @@ struct GgufSource : Source {
                 return g.read_q8(blk(layer, "ffn_up.weight"), n / 2, k, qs + (int64_t)(n / 2) * k,
                                  d + (int64_t)(n / 2) * (k / 32));
             case W_DN: return g.read_q8(blk(layer, "ffn_down.weight"), n, k, qs, d);
+            case W_EMB: return g.read_q8("token_embd.weight", n, k, qs, d);
             default: return g.read_q8("output.weight", n, k, qs, d);
         }
     }
@@ -209,6 +217,10 @@ struct GgufSource : Source {
     }
     lgx_status emb(int32_t V, int32_t H, uint16_t* out) override {
         return g.read_raw("token_embd.weight", lgxf::GGML_F16, V, H, out);
+    }
+    bool emb_is_q8() const override {
+        const lgxf::TensorInfo* t = g.tensor("token_embd.weight");
+        return t && t->type == lgxf::GGML_Q8_0;
     }
 };
 
@@ -238,6 +250,22 @@ lgx_status make_q8(lgx_model* m, Source& src, int which, int layer, int32_t n, i
     out->m = lgx_q8_matrix{out->qs, out->d, n, k, LGX_Q8_T16};
     return LGX_OK;
 }
+
+// Embedding rows of m tokens (row r = b * qpr + j takes tokens[b * stride + j])
+// into h [m][hidden]: binary16 rows widened, or Q8_0 rows dequantised.
+lgx_status embed(lgx_model* md, const int32_t* tokens, int stride, int qpr, float* h, int m,
+                 void* stream) {
+    const lgx_qwen_config& cf = md->c;
+    if (md->emb_q8) {
+        lgx_embed_q8_args a{md->embq.qs, md->embq.d, tokens, h, m, cf.hidden, cf.vocab, stride, qpr};
+        return launch(md->ctx, K_EMBED_Q8, dim3(m), dim3(256), a, stream);
+    }
+    lgx_embed_args a{md->emb, tokens, h, m, cf.hidden, cf.vocab, stride, qpr};
+    return launch(md->ctx, K_EMBED, dim3(m), dim3(256), a, stream);
+}
+
+// The binary16 lm_head of a tied embedding (else the Q8 product with lm).
+bool f16_head(const lgx_model* md) { return md->c.tied_embedding && !md->emb_q8; }
 
 lgx_status check_config(const lgx_qwen_config* c) {
     const int hq = c->n_heads, hkv = c->n_kv_heads, d = c->head_dim, H = c->hidden,
@@ -374,8 +402,7 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
     const int H = cf.hidden, I = cf.intermediate, d = cf.head_dim, hq = cf.n_heads,
               hkv = cf.n_kv_heads;
     lgx_status st;
-    lgx_embed_args ea{md->emb, tokens, md->h, B, H, cf.vocab, tokens_stride, 1};
-    if ((st = launch(c, K_EMBED, dim3(B), dim3(256), ea, stream)) != LGX_OK) return st;
+    if ((st = embed(md, tokens, tokens_stride, 1, md->h, B, stream)) != LGX_OK) return st;
     for (int l = 0; l < cf.n_layers; ++l) {
         // norm (+ residual of the previous layer's down product) -> Q8
         if ((st = norm(md, md->attn_norm[l], B, H, parts(md, md->dn[0], B), l > 0, nullptr, true,
@@ -478,7 +505,7 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
     const lgx_qwen_config& cf = md->c;
     const int H = cf.hidden;
     lgx_status st;
-    const bool tied = cf.tied_embedding != 0;
+    const bool tied = f16_head(md);
     if ((st = norm(md, md->out_norm, B, H, parts(md, md->dn[0], B), true, md->xn, !tied, stream,
                    tied ? md->xt : nullptr)) != LGX_OK)
         return st;
@@ -585,8 +612,7 @@ lgx_status prefill_chunk(lgx_model* md, int B, int n, const int32_t* tokens, int
     const int M = B * n;
     lgx_model::Prefill& pf = md->pf;
     lgx_status st;
-    lgx_embed_args ea{md->emb, tokens, pf.h, M, H, cf.vocab, stride, n};
-    if ((st = launch(c, K_EMBED, dim3(M), dim3(256), ea, stream)) != LGX_OK) return st;
+    if ((st = embed(md, tokens, stride, n, pf.h, M, stream)) != LGX_OK) return st;
     for (int l = 0; l < cf.n_layers; ++l) {
         if ((st = pf_norm(md, md->attn_norm[l], M, H, tiled_groups(I), l > 0, stream)) != LGX_OK)
             return st;
@@ -745,7 +771,7 @@ lgx_status model_build(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed, So
         // staging for the row-major upload of the largest Q8 matrix
         int64_t big = std::max<int64_t>({(int64_t)m->qkv_n * H, (int64_t)H * hq * d,
                                          (int64_t)2 * I * H, (int64_t)H * I,
-                                         cf.tied_embedding ? 0 : (int64_t)cf.vocab * H});
+                                         (!cf.tied_embedding || src.emb_is_q8()) ? (int64_t)cf.vocab * H : 0});
         int8_t* stage_q = nullptr;
         uint16_t* stage_d = nullptr;
         if ((st = dev_alloc(m, &stage_q, (size_t)big)) != LGX_OK) return done(st);
@@ -792,16 +818,25 @@ lgx_status model_build(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed, So
         if (!cf.tied_embedding &&
             (st = make_q8(m, src, W_LM, 0, cf.vocab, H, &m->lm, stage_q, stage_d, hq8, hd16)) != LGX_OK)
             return done(st);
+        if (src.emb_is_q8()) {
+            if (cf.vocab % 16)
+                return done(fail(LGX_UNSUPPORTED, "Q8_0 embedding needs vocab %% 16 == 0 (got %d)", cf.vocab));
+            if ((st = make_q8(m, src, W_EMB, 0, cf.vocab, H, &m->embq, stage_q, stage_d, hq8, hd16)) !=
+                LGX_OK)
+                return done(st);
+            m->emb_q8 = true;
+            if (cf.tied_embedding) m->lm = m->embq;
+        }
         if ((st = put_vec(V_OUT_NORM, 0, H, &m->out_norm)) != LGX_OK) return done(st);
         hq8.clear();
         hq8.shrink_to_fit();
-        {
+        if (!m->emb_q8) {
             std::vector<uint16_t> he((size_t)cf.vocab * H);
             if ((st = src.emb(cf.vocab, H, he.data())) != LGX_OK) return done(st);
             if ((st = dev_alloc(m, &m->emb, he.size())) != LGX_OK) return done(st);
             LGX_HIP(hipMemcpy(m->emb, he.data(), he.size() * 2, hipMemcpyHostToDevice));
         }
-        if (cf.tied_embedding) {
+        if (f16_head(m)) {
             const int64_t nt = lgx_f16_t64_count(cf.vocab, H);
             if ((st = dev_alloc(m, &m->emb_t64, (size_t)nt)) != LGX_OK ||
                 (st = dev_alloc(m, &m->xt, (size_t)cdiv(B, 16) * 16 * H)) != LGX_OK)
@@ -855,7 +890,7 @@ lgx_status model_build(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed, So
         upd(H, hq * d);
         upd(2 * I, H);
         upd(H, I);
-        if (!cf.tied_embedding) upd(cf.vocab, H);
+        if (!f16_head(m)) upd(cf.vocab, H);
         if ((st = dev_alloc(m, &m->h, (size_t)B * H)) || (st = dev_alloc(m, &m->xn, (size_t)B * H)) ||
             (st = dev_alloc(m, &m->xq, (size_t)(B + 15) / 16 * 16 * kmax)) ||
             (st = dev_alloc(m, &m->xd, (size_t)B * kmax / 32)) ||
@@ -864,7 +899,7 @@ lgx_status model_build(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed, So
             (st = dev_alloc(m, &m->q, (size_t)B * hq * d)) || (st = dev_alloc(m, &m->part, (size_t)part)) ||
             (st = dev_alloc(m, &m->attn_part, (size_t)B * hq * m->nchunk * (d + 2))) ||
             (st = dev_alloc(m, &m->logits,
-                            cf.tied_embedding ? (size_t)nranges_of(H) * B * cf.vocab : 1)) ||
+                            f16_head(m) ? (size_t)nranges_of(H) * B * cf.vocab : 1)) ||
             (st = dev_alloc(m, &m->cand, (size_t)B * argmax_slices(cf.vocab) * 2)) ||
             (cf.vocab <= 64 * LGX_ARGMAX_SLICE &&
              (st = dev_alloc(m, &m->scand, sample_cand_bytes(B, cf.vocab) / 8))))
@@ -1079,9 +1114,12 @@ lgx_status lgx_model_tensor(lgx_model* m, int32_t layer, int32_t which, const vo
         };
         switch (which) {
             case LGX_T_EMB:
+                if (m->emb_q8) return fail(LGX_INVALID_ARGUMENT, "the embedding is Q8_0 (LGX_T_EMB_Q / _D)");
                 *dev = m->emb;
                 *bytes = (size_t)cf.vocab * cf.hidden * 2;
                 return LGX_OK;
+            case LGX_T_EMB_Q: return q8(m->embq, false);
+            case LGX_T_EMB_D: return q8(m->embq, true);
             case LGX_T_LM_Q: return q8(m->lm, false);
             case LGX_T_LM_D: return q8(m->lm, true);
             case LGX_T_QKV_Q: return q8(m->qkv[layer], false);
@@ -1169,7 +1207,7 @@ lgx_status lgx_qwen_logits(lgx_model* m, int32_t B, float* out, void* stream) {
                              dim3(64), la, stream)) != LGX_OK)
                 return st;
         }
-        lgx_combine_args ca{m->c.tied_embedding ? m->logits : m->part, out, count, m->last_nr};
+        lgx_combine_args ca{f16_head(m) ? m->logits : m->part, out, count, m->last_nr};
         return launch(m->ctx, K_COMBINE, dim3(cdiv(count, 256)), dim3(256), ca, stream);
     });
 }

@@ -1012,6 +1012,8 @@ struct orc_model {
     uint64_t seed;
     int32_t qkv_n, maxp;
     uint16_t* emb;
+    int8_t* emb_qs;        /* a Q8_0 embedding (orc_model_set_emb_q8), else NULL */
+    uint16_t* emb_d;
     int8_t* lm_qs;
     uint16_t* lm_d;
     int8_t **qkv_qs, **o_qs, **gu_qs, **dn_qs;
@@ -1028,6 +1030,15 @@ struct orc_model {
     float s_top_p, s_temp;
     uint64_t s_seed;
 };
+
+/* Element k of token v's embedding row: binary16 widened, or Q8_0
+ * f32(d) * q (exact). */
+static inline float emb_value(const orc_model* m, int32_t v, int32_t k) {
+    const int64_t H = m->c.hidden;
+    if (m->emb_qs)
+        return f16f(m->emb_d[(int64_t)v * (H / 32) + k / 32]) * (float)m->emb_qs[(int64_t)v * H + k];
+    return orc_f16_to_f32(m->emb[(int64_t)v * H + k]);
+}
 
 static void* xmalloc(size_t n) {
     void* p = malloc(n ? n : 1);
@@ -1123,7 +1134,7 @@ void orc_model_destroy(orc_model* m) {
     free(m->bias); free(m->kc); free(m->vc);
     for (int32_t l = 0; l < m->c.n_layers; ++l) { free(m->attn_norm[l]); free(m->ffn_norm[l]); }
     free(m->attn_norm); free(m->ffn_norm); free(m->out_norm);
-    free(m->emb); free(m->lm_qs); free(m->lm_d); free(m->ones);
+    free(m->emb); free(m->emb_qs); free(m->emb_d); free(m->lm_qs); free(m->lm_d); free(m->ones);
     free(m->cos_t); free(m->sin_t); free(m->page_table); free(m->seq_len);
     free(m);
 }
@@ -1188,7 +1199,7 @@ void orc_model_step(orc_model* m, int32_t nseq, const int32_t* slots, const int3
     float scale = (float)(1.0 / sqrt((double)d));
     for (int32_t i = 0; i < B; ++i) {
         for (int32_t k = 0; k < H; ++k)
-            h[(int64_t)i * H + k] = orc_f16_to_f32(m->emb[(int64_t)tokens[i] * H + k]);
+            h[(int64_t)i * H + k] = emb_value(m, tokens[i], k);
         memcpy(pt + (int64_t)i * m->maxp, m->page_table + (int64_t)slots[i] * m->maxp,
                sizeof(int32_t) * m->maxp);
         lens[i] = m->seq_len[slots[i]] + 1;
@@ -1230,11 +1241,12 @@ void orc_model_step(orc_model* m, int32_t nseq, const int32_t* slots, const int3
     orc_rmsnorm(h, m->out_norm, B, H, c->eps, xn);
     if (hidden_out) memcpy(hidden_out, xn, sizeof(float) * B * H);
     float* logits = (float*)xmalloc(sizeof(float) * (size_t)B * c->vocab);
-    if (c->tied) {
+    if (c->tied && !m->emb_qs) {
         orc_lm_head_f16(xn, B, m->emb, c->vocab, H, logits);
     } else {
         orc_quantize_q8_0(xn, B, H, xq, xd);
-        orc_q8_gemm(m->lm_qs, m->lm_d, c->vocab, H, xq, xd, B, logits);
+        orc_q8_gemm(c->tied ? m->emb_qs : m->lm_qs, c->tied ? m->emb_d : m->lm_d, c->vocab, H,
+                    xq, xd, B, logits);
     }
     for (int32_t i = 0; i < B; ++i) {
         next[i] = m->s_top_k > 0
@@ -1281,7 +1293,7 @@ void orc_model_prefill(orc_model* m, int32_t nseq, const int32_t* slots, int32_t
     for (int64_t r = 0; r < R; ++r) {
         int32_t s = (int32_t)(r / P), j = (int32_t)(r % P);
         for (int32_t k = 0; k < H; ++k)
-            h[r * H + k] = orc_f16_to_f32(m->emb[(int64_t)tokens[r] * H + k]);
+            h[r * H + k] = emb_value(m, tokens[r], k);
         memcpy(pt + r * m->maxp, m->page_table + (int64_t)slots[s] * m->maxp,
                sizeof(int32_t) * m->maxp);
         lens[r] = m->seq_len[slots[s]] + j + 1;
@@ -1328,11 +1340,12 @@ void orc_model_prefill(orc_model* m, int32_t nseq, const int32_t* slots, int32_t
     orc_rmsnorm(hl, m->out_norm, nseq, H, c->eps, xn);
     if (hidden_out) memcpy(hidden_out, xn, sizeof(float) * nseq * H);
     float* logits = (float*)xmalloc(sizeof(float) * (size_t)nseq * c->vocab);
-    if (c->tied) {
+    if (c->tied && !m->emb_qs) {
         orc_lm_head_f16(xn, nseq, m->emb, c->vocab, H, logits);
     } else {
         orc_quantize_q8_0(xn, nseq, H, xq, xd);
-        orc_q8_gemm(m->lm_qs, m->lm_d, c->vocab, H, xq, xd, nseq, logits);
+        orc_q8_gemm(c->tied ? m->emb_qs : m->lm_qs, c->tied ? m->emb_d : m->lm_d, c->vocab, H,
+                    xq, xd, nseq, logits);
     }
     for (int32_t s = 0; s < nseq; ++s) {
         next[s] = m->s_top_k > 0
@@ -1383,6 +1396,21 @@ void orc_model_set_sampling(orc_model* m, float temperature, int32_t top_k, floa
 /* Replace a model tensor (ids of orc_model_tensor, plus 12 attention norm,
  * 13 MLP norm, 14 final norm weight) with `data` of the same size: the
  * tests load a checkpoint's tensors into the oracle this way. */
+/* A Q8_0 embedding [vocab][hidden] (row-major quants + scales [vocab][hidden/32])
+ * in place of the binary16 one: element k of token v is
+ * f32(d[v][k/32]) * q[v][k] (exact in binary32), and a tied model's logits
+ * become the canonical Q8 product of the Q8_0 final-norm rows with it (the
+ * untied lm_head's operations with this matrix). */
+void orc_model_set_emb_q8(orc_model* m, const int8_t* qs, const uint16_t* d) {
+    const int64_t V = m->c.vocab, H = m->c.hidden;
+    free(m->emb_qs);
+    free(m->emb_d);
+    m->emb_qs = (int8_t*)xmalloc((size_t)(V * H));
+    m->emb_d = (uint16_t*)xmalloc((size_t)(V * (H / 32)) * 2);
+    memcpy(m->emb_qs, qs, (size_t)(V * H));
+    memcpy(m->emb_d, d, (size_t)(V * (H / 32)) * 2);
+}
+
 void orc_model_set_tensor(orc_model* m, int32_t layer, int32_t which, const void* data) {
     const orc_qwen_config* c = &m->c;
     int64_t H = c->hidden, I = c->inter, d = c->head_dim, hq = c->n_heads, V = c->vocab;

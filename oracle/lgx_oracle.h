@@ -156,6 +156,7 @@ void orc_model_set_seq_len(orc_model* m, int32_t slot, int32_t len);
 void orc_model_set_sampling(orc_model* m, float temperature, int32_t top_k, float top_p,
                             uint64_t seed);
 void orc_model_set_tensor(orc_model* m, int32_t layer, int32_t which, const void* data);
+void orc_model_set_emb_q8(orc_model* m, const int8_t* qs, const uint16_t* d);
 void orc_set_threads(int32_t n);
 int32_t orc_max_threads(void);
 

@@ -88,6 +88,7 @@ def lib():
             "orc_model_set_sampling": (None, [_P, C.c_float, _I32, C.c_float, C.c_uint64]),
             "orc_set_threads": (None, [_I32]),
             "orc_model_set_tensor": (None, [_P, _I32, _I32, _P]),
+            "orc_model_set_emb_q8": (None, [_P, _P, _P]),
             "orc_max_threads": (_I32, []),
             "orc_sample": (None, [_P, _I32, _I32, _I32, C.c_float, C.c_float, C.c_uint64, _P,
                                   _P, _P]),
@@ -433,6 +434,16 @@ class Model:
         if want is not None:
             assert arr.shape == want.shape and arr.dtype == want.dtype, (name, arr.shape, arr.dtype)
         lib().orc_model_set_tensor(self.h, layer, TENSORS[name], arr.ctypes.data_as(C.c_void_p))
+
+    def set_emb_q8(self, qs, d) -> None:
+        """A Q8_0 embedding (row-major quants [vocab][hidden] int8, scales
+        [vocab][hidden/32] binary16 bits): gathered as f32(d) * q, and the
+        tied lm_head becomes the Q8 product with it."""
+        c = self.cfg
+        qs = _c(qs, np.int8)
+        d = _c(d, np.uint16)
+        assert qs.shape == (c["vocab"], c["hidden"]) and d.shape == (c["vocab"], c["hidden"] // 32)
+        lib().orc_model_set_emb_q8(self.h, _ptr(qs), _ptr(d))
 
     @staticmethod
     def _shaped():

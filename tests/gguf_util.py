@@ -104,8 +104,9 @@ def qwen2_tensors(cfg, t):
     (rows gate | up), dn, bias and the norm weights)."""
     H, I, d = cfg["hidden"], cfg["inter"], cfg["head_dim"]
     qd, kd = cfg["n_heads"] * d, cfg["n_kv"] * d
-    out = [("token_embd.weight", GGML_F16, t["emb"]),
-           ("output_norm.weight", GGML_F32, t["out_norm"])]
+    emb = ("token_embd.weight", GGML_Q8_0, (t["emb_q"], t["emb_d"])) if "emb_q" in t else \
+        ("token_embd.weight", GGML_F16, t["emb"])
+    out = [emb, ("output_norm.weight", GGML_F32, t["out_norm"])]
     if not cfg["tied"]:
         out.append(("output.weight", GGML_Q8_0, (t["lm_q"], t["lm_d"])))
     for l in range(cfg["n_layers"]):
@@ -130,9 +131,10 @@ def qwen2_tensors(cfg, t):
     return out
 
 
-def random_qwen2(cfg, seed):
+def random_qwen2(cfg, seed, emb_q8=False):
     """Random tensors of a Qwen2 model (numpy PCG64): Q8_0 quants and scales,
-    biases, norm weights in [0.5, 1.5), a binary16 embedding."""
+    biases, norm weights in [0.5, 1.5), a binary16 embedding (or, emb_q8, a
+    Q8_0 one as llama.cpp's Q8_0 files store token_embd)."""
     rng = np.random.default_rng(seed)
     H, I, d, V = cfg["hidden"], cfg["inter"], cfg["head_dim"], cfg["vocab"]
     qn = (cfg["n_heads"] + 2 * cfg["n_kv"]) * d
@@ -144,6 +146,8 @@ def random_qwen2(cfg, seed):
 
     t = {"emb": rng.normal(0, 0.002, size=(V, H)).astype(np.float16).view(np.uint16),
          "out_norm": rng.uniform(0.5, 1.5, H).astype(np.float32)}
+    if emb_q8:
+        t["emb_q"], t["emb_d"] = q8(V, H)
     if not cfg["tied"]:
         t["lm_q"], t["lm_d"] = q8(V, H)
     for l in range(cfg["n_layers"]):
@@ -160,6 +164,8 @@ def random_qwen2(cfg, seed):
 def load_into_oracle(om, cfg, t):
     """Set the oracle model's tensors to the dict `t` (random_qwen2 layout)."""
     om.set_tensor("emb", 0, t["emb"])
+    if "emb_q" in t:
+        om.set_emb_q8(t["emb_q"], t["emb_d"])
     om.set_tensor("out_norm", 0, t["out_norm"])
     if not cfg["tied"]:
         om.set_tensor("lm_q", 0, t["lm_q"])

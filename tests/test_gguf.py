@@ -72,6 +72,9 @@ def test_malformed_files(tmp_path):
     no_layers = [m for m in meta if m[0] != "qwen2.block_count"]
     gg.write_gguf(p, no_layers, gg.qwen2_tensors(cfg, t))
     assert _err(p) == "LGX_INVALID_ARGUMENT"
+    tq = gg.random_qwen2(dict(cfg, vocab=1008), 2, emb_q8=True)     # a Q8_0 token_embd is read
+    gg.write_gguf(p, gg.qwen2_meta(dict(cfg, vocab=1008)), gg.qwen2_tensors(dict(cfg, vocab=1008), tq))
+    assert lgx.gguf_config(str(p), 1, 16)["vocab"] == 1008
     tens = gg.qwen2_tensors(cfg, t)
     tens[0] = ("token_embd.weight", gg.GGML_F32, np.zeros((cfg["vocab"], cfg["hidden"]), np.float32))
     gg.write_gguf(p, meta, tens)

@@ -33,12 +33,23 @@ def _cfg(name, **kw):
     return dict(orc.qwen_config(name), **kw)
 
 
-@pytest.mark.parametrize("name", ["tiny", "tiny_untied"])
-def test_loaded_checkpoint_decodes_like_oracle(ctx, tmp_path, name):
+H1536 = dict(hidden=1536, n_heads=12, n_kv=2, head_dim=128, inter=512)
+
+
+@pytest.mark.parametrize("name,emb_q8,kw", [
+    ("tiny", False, {}), ("tiny_untied", False, {}),
+    ("tiny", True, dict(vocab=1008)), ("tiny_untied", True, {}),
+    ("tiny", False, H1536), ("tiny", True, dict(H1536, vocab=1008))],
+    ids=["tied", "untied", "tied-q8emb", "untied-q8emb", "tied-h1536", "tied-h1536-q8emb"])
+def test_loaded_checkpoint_decodes_like_oracle(ctx, tmp_path, name, emb_q8, kw):
+    """Binary16 or Q8_0 token_embd (llama.cpp's Q8_0 files store it as
+    Q8_0: the gather dequantises, a tied model's lm_head is the Q8 product
+    with it), hidden <= 1024 and 1536 (two ranges in the tied binary16
+    lm_head)."""
     from oracle import oracle as orc
 
-    cfg = _cfg(name, eps=1e-5, theta=20000.0)
-    t = gg.random_qwen2(cfg, 17)
+    cfg = _cfg(name, eps=1e-5, theta=20000.0, **kw)
+    t = gg.random_qwen2(cfg, 17, emb_q8=emb_q8)
     path = tmp_path / "model.gguf"
     gg.write_gguf(path, gg.qwen2_meta(cfg), gg.qwen2_tensors(cfg, t))
     gm = lgx.Model.load_gguf(ctx, str(path), cfg["max_batch"], cfg["max_seq"])
@@ -56,6 +67,13 @@ def test_loaded_checkpoint_decodes_like_oracle(ctx, tmp_path, name):
         for nm in ("attn_norm", "ffn_norm"):
             assert np.array_equal(gm.tensor_bytes(nm, l).view(np.float32), t[(nm, l)])
     assert np.array_equal(gm.tensor_bytes("out_norm").view(np.float32), t["out_norm"])
+    if emb_q8:
+        V = cfg["vocab"]
+        assert np.array_equal(gm.tensor_bytes("emb_q").view(np.int8), orc.q8_repack_t16(t["emb_q"]))
+        assert np.array_equal(gm.tensor_bytes("emb_d").view(np.uint16),
+                              orc.q8_repack_s16(t["emb_d"], V, H))
+        with pytest.raises(lgx.LgxError):
+            gm.tensor_bytes("emb")
     om = orc.Model(gm.cfg, 0)
     gg.load_into_oracle(om, cfg, t)
     B = cfg["max_batch"]

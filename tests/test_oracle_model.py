@@ -246,3 +246,43 @@ def test_load_kv_round_trip_and_decode(orc):
         assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
     a.close()
     b.close()
+
+
+def test_q8_embedding_gather_and_tied_head(orc):
+    """orc_model_set_emb_q8: the gather is f32(d) * q per element (checked on
+    the hidden rows of a zero-layer-like comparison: the same model with the
+    binary16 embedding set to a Q8_0 matrix whose dequantised values are
+    binary16-exact gives the same hidden rows), and the tied model's logits
+    with a Q8_0 embedding equal an untied model's whose lm_head is that
+    matrix."""
+    import numpy as np
+
+    cfg_t = dict(orc.qwen_config("tiny"), vocab=1008, max_batch=2, max_seq=32)
+    cfg_u = dict(cfg_t, tied=0)
+    rng = np.random.default_rng(4)
+    V, H = cfg_t["vocab"], cfg_t["hidden"]
+    # quants times power-of-two scales: f32(d) * q is exact in binary16 too
+    qs = rng.integers(-127, 128, size=(V, H), dtype=np.int8)
+    d = orc.f32_to_f16(np.full((V, H // 32), 2.0 ** -14, np.float32))
+    emb16 = orc.f32_to_f16(qs.astype(np.float32) * np.float32(2.0 ** -14))
+    a = orc.Model(cfg_t, 9)
+    b = orc.Model(cfg_t, 9)
+    a.set_emb_q8(qs, d)
+    b.set_tensor("emb", 0, emb16)
+    toks = np.array([3, 999], np.int32)
+    _, ha = a.step([0, 1], toks, want_hidden=True)
+    _, hb = b.step([0, 1], toks, want_hidden=True)
+    assert np.array_equal(ha.view(np.uint32), hb.view(np.uint32))
+    # tied Q8_0 head == untied head with the same matrix (general scales)
+    d2 = orc.f32_to_f16((np.abs(rng.standard_normal((V, H // 32))) * 0.02 / 127).astype(np.float32))
+    t = orc.Model(cfg_t, 9)
+    u = orc.Model(cfg_u, 9)
+    t.set_emb_q8(qs, d2)
+    u.set_emb_q8(qs, d2)
+    u.set_tensor("lm_q", 0, qs)
+    u.set_tensor("lm_d", 0, d2)
+    nt, lt = t.step([0, 1], toks, want_logits=True)
+    nu, lu = u.step([0, 1], toks, want_logits=True)
+    assert np.array_equal(lt.view(np.uint32), lu.view(np.uint32)) and np.array_equal(nt, nu)
+    for m in (a, b, t, u):
+        m.close()
