@@ -212,6 +212,16 @@ lgx_status lgx_gqa_prefill_attn(lgx_ctx* ctx, const float* q, const uint16_t* kp
                                 const int32_t* seq_len, int32_t B, int32_t P, int32_t hq,
                                 int32_t hkv, int32_t d, int32_t maxp, int32_t num_pages,
                                 int32_t max_seq_len, float* out, void* stream);
+/* lgx_gqa_prefill_attn's causal attention on binary16 MFMA (flash
+ * attention: online softmax over 64-token tiles, q scaled by 1/sqrt(d) and
+ * rounded to binary16, P in binary16, binary32 accumulation): not the
+ * canonical schedule; within 2e-3 of it.  Same arguments; the fast prefill
+ * mode's attention.  No counterpart in the reference. */
+lgx_status lgx_gqa_prefill_attn_fast(lgx_ctx* ctx, const float* q, const uint16_t* kpages,
+                                     const uint16_t* vpages, const int32_t* page_table,
+                                     const int32_t* seq_len, int32_t B, int32_t P, int32_t hq,
+                                     int32_t hkv, int32_t d, int32_t maxp, int32_t num_pages,
+                                     int32_t max_seq_len, float* out, void* stream);
 
 /* ---- range partials (for consumers that fuse the range tree) ---- */
 /* Number of canonical 32-block ranges of K = the partial count of a product. */
@@ -442,6 +452,18 @@ lgx_status lgx_model_tensor(lgx_model* m, int32_t layer, int32_t which, const vo
  * the device if any exist). */
 lgx_status lgx_model_set_sampling(lgx_model* m, float temperature, int32_t top_k, float top_p,
                                   uint64_t seed);
+/* Prefill modes of lgx_qwen_prefill.  LGX_PREFILL_EXACT (the default): every
+ * prompt position runs the decode step's canonical schedule, so the cache,
+ * tokens and logits equal the CPU oracle's bit for bit.  LGX_PREFILL_FAST:
+ * the prompt positions before the last attend through
+ * lgx_gqa_prefill_attn_fast (binary16 MFMA flash attention, within 2e-3 of
+ * the canonical attention); the products, norms and the last position stay
+ * exact, so the cache differs from the exact one by that attention error
+ * and every decode step after it is exact given the cache.  Under
+ * LGX_PREFILL=serial (every position through the decode step) the mode has
+ * no effect.  No counterpart in the reference. */
+enum { LGX_PREFILL_EXACT = 0, LGX_PREFILL_FAST = 1 };
+lgx_status lgx_model_set_prefill_mode(lgx_model* m, int32_t mode);
 /* out[B][vocab] = logits of the last decode/prefill step (binary32); B must
  * be that step's batch. */
 lgx_status lgx_qwen_logits(lgx_model* m, int32_t B, float* out, void* stream);

@@ -67,6 +67,8 @@ SIGNATURES = {
                                       _I32, _I32, _P, _P]),
     "lgx_gqa_prefill_attn": (C.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32,
                                        _I32, _I32, _I32, _P, _P]),
+    "lgx_gqa_prefill_attn_fast": (C.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
+                                            _I32, _I32, _I32, _I32, _P, _P]),
     "lgx_embed_f16": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _P, _P]),
     "lgx_rmsnorm_quant": (C.c_int, [_P, _P, _P, _I32, _I32, C.c_float, _P, _P, _P, _P]),
     "lgx_add_rmsnorm_quant": (C.c_int, [_P, _P, _I32, _P, _P, _I32, _I32, C.c_float, _P, _P, _P,
@@ -84,6 +86,7 @@ SIGNATURES = {
     "lgx_sample": (C.c_int, [_P, _P, _I32, _I32, _I32, C.c_float, C.c_float, C.c_uint64, _P, _P,
                              _P]),
     "lgx_model_set_sampling": (C.c_int, [_P, C.c_float, _I32, C.c_float, C.c_uint64]),
+    "lgx_model_set_prefill_mode": (C.c_int, [_P, _I32]),
     "lgx_model_create": (C.c_int, [_P, _P, C.c_uint64, C.POINTER(_P)]),
     "lgx_gguf_config": (C.c_int, [C.c_char_p, _I32, _I32, _P]),
     "lgx_model_load_gguf": (C.c_int, [_P, C.c_char_p, _I32, _I32, C.POINTER(_P)]),
@@ -444,9 +447,10 @@ class Context:
         return out
 
     def gqa_prefill_attn(self, q, kpages, vpages, page_table, seq_len, P: int, max_seq_len: int,
-                         out=None):
+                         out=None, fast: bool = False):
         """q [B*P][hq][d] f32: row b*P + j is the query at position seq_len[b] + j
-        (causal over the first seq_len[b] + j + 1 cached tokens)."""
+        (causal over the first seq_len[b] + j + 1 cached tokens).  fast: the
+        binary16 MFMA flash attention (within 2e-3 of the canonical result)."""
         t = self.torch
         rows, hq, d = q.shape
         B = seq_len.numel()
@@ -455,10 +459,10 @@ class Context:
         num_pages, hkv = kpages.shape[0], kpages.shape[1]
         maxp = page_table.shape[1]
         out = t.empty((rows, hq, d), dtype=t.float32, device=self.dev) if out is None else out
-        _check(lib().lgx_gqa_prefill_attn(self.handle, q.data_ptr(), kpages.data_ptr(),
-                                          vpages.data_ptr(), page_table.data_ptr(),
-                                          seq_len.data_ptr(), B, P, hq, hkv, d, maxp, num_pages,
-                                          max_seq_len, out.data_ptr(), self._s()))
+        fn = lib().lgx_gqa_prefill_attn_fast if fast else lib().lgx_gqa_prefill_attn
+        _check(fn(self.handle, q.data_ptr(), kpages.data_ptr(), vpages.data_ptr(),
+                  page_table.data_ptr(), seq_len.data_ptr(), B, P, hq, hkv, d, maxp, num_pages,
+                  max_seq_len, out.data_ptr(), self._s()))
         return out
 
     def q8_gemm(self, W: Q8Matrix, xq, xd, y=None):
@@ -660,6 +664,11 @@ class Model:
         """Seeded top-k / top-p token choice for later steps (temperature 0:
         greedy)."""
         _check(lib().lgx_model_set_sampling(self.handle, temperature, top_k, top_p, seed))
+
+    def set_prefill_mode(self, fast: bool) -> None:
+        """fast: later prefills attend through the binary16 MFMA flash
+        attention (LGX_PREFILL_FAST); otherwise the exact canonical schedule."""
+        _check(lib().lgx_model_set_prefill_mode(self.handle, 1 if fast else 0))
 
     def decode_step(self, tokens) -> None:
         """tokens: device int32 [B], replaced in place by the next tokens."""

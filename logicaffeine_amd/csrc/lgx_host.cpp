@@ -443,6 +443,45 @@ lgx_status lgx_gqa_prefill_attn(lgx_ctx* c, const float* q, const uint16_t* kpag
     });
 }
 
+lgx_status lgx_gqa_prefill_attn_fast(lgx_ctx* c, const float* q, const uint16_t* kpages,
+                                     const uint16_t* vpages, const int32_t* page_table,
+                                     const int32_t* seq_len, int32_t B, int32_t P, int32_t hq,
+                                     int32_t hkv, int32_t d, int32_t maxp, int32_t num_pages,
+                                     int32_t max_seq_len, float* out, void* stream) {
+    return guarded(__func__, [&]() -> lgx_status {
+        lgx_status st = enter(c);
+        if (st != LGX_OK) return st;
+        if (!q || !kpages || !vpages || !page_table || !seq_len || !out)
+            return fail(LGX_NULL_POINTER, "NULL tensor pointer");
+        if (B <= 0 || P <= 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0 || maxp <= 0 || num_pages <= 0)
+            return fail(LGX_INVALID_ARGUMENT, "B=%d P=%d hq=%d hkv=%d maxp=%d num_pages=%d", B, P, hq,
+                        hkv, maxp, num_pages);
+        if ((d != 64 && d != 128) || hq / hkv > 8)
+            return fail(LGX_UNSUPPORTED, "head_dim %d / %d query heads per KV head", d, hq / hkv);
+        if (max_seq_len <= 0 || max_seq_len > maxp * LGX_PAGE)
+            return fail(LGX_OUT_OF_BOUNDS, "max_seq_len %d outside (0, %d]", max_seq_len,
+                        maxp * LGX_PAGE);
+        if ((int64_t)B * P * hq > INT32_MAX) return fail(LGX_OUT_OF_BOUNDS, "B*P*hq too large");
+        lgx_attn_args a{};
+        a.q = q;
+        a.kpages = kpages;
+        a.vpages = vpages;
+        a.page_table = page_table;
+        a.seq_len = seq_len;
+        a.out = out;
+        a.B = B;
+        a.hq = hq;
+        a.hkv = hkv;
+        a.maxp = maxp;
+        a.num_pages = num_pages;
+        a.maxlen = max_seq_len;
+        a.len_add = 1;
+        a.qpr = P;
+        a.scale = (float)(1.0 / std::sqrt((double)d));
+        return launch_prefill_attn_fast(c, a, d, stream);
+    });
+}
+
 // lgx_q8_gemm over the workspace `scratch` of `cap` bytes (nullptr: the
 // ctx's grow-on-demand workspace).
 static lgx_status q8_gemm_impl(lgx_ctx* c, const lgx_q8_matrix* W, const int8_t* xq,

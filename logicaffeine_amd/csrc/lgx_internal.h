@@ -138,7 +138,9 @@ enum Kern {
     K_GEMM_TILED64_S4,
     K_GEMM_TILED32_S4,
     K_EMBED_Q8,
-    K_COUNT
+    K_FPA_D64_G1,    // + (gq - 1): fast (binary16 MFMA) prefill attention
+    K_FPA_D128_G1 = K_FPA_D64_G1 + 8,
+    K_COUNT = K_FPA_D128_G1 + 8
 };
 inline const char* const kKernelNames[] = {
     "lgx_k_repack_t16", "lgx_k_quantize_q8_0", "lgx_k_q8q8_gemv",
@@ -173,6 +175,12 @@ inline const char* const kKernelNames[] = {
     "lgx_k_q8_gemm_tiled32_group", "lgx_k_quantize_group", "lgx_k_q8_combine_group",
     "lgx_k_lm_rowconst", "lgx_k_lm_cert", "lgx_k_lm_pick", "lgx_k_add_rmsnorm_quant4s_r8",
     "lgx_k_q8_gemm_tiled64s4", "lgx_k_q8_gemm_tiled32s4", "lgx_k_embed_q8",
+    "lgx_k_attn_prefill_fast_d64_g1", "lgx_k_attn_prefill_fast_d64_g2", "lgx_k_attn_prefill_fast_d64_g3",
+    "lgx_k_attn_prefill_fast_d64_g4", "lgx_k_attn_prefill_fast_d64_g5", "lgx_k_attn_prefill_fast_d64_g6",
+    "lgx_k_attn_prefill_fast_d64_g7", "lgx_k_attn_prefill_fast_d64_g8",
+    "lgx_k_attn_prefill_fast_d128_g1", "lgx_k_attn_prefill_fast_d128_g2", "lgx_k_attn_prefill_fast_d128_g3",
+    "lgx_k_attn_prefill_fast_d128_g4", "lgx_k_attn_prefill_fast_d128_g5", "lgx_k_attn_prefill_fast_d128_g6",
+    "lgx_k_attn_prefill_fast_d128_g7", "lgx_k_attn_prefill_fast_d128_g8",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -585,6 +593,18 @@ inline lgx_status act_to_t16(lgx_ctx* c, const int8_t* xq, int m, int k, int8_t*
 
 // Launch of the prefill attention over B sequences x a.qpr query rows:
 // one workgroup per (sequence, KV head, chunk of the grid, block of 4 rows).
+// Fast prefill attention (binary16 MFMA flash attention, not the canonical
+// schedule): one workgroup of gq waves per (sequence, KV head, 16 query
+// positions); writes out (binary32) and / or xq / xd (Q8_0).
+inline lgx_status launch_prefill_attn_fast(lgx_ctx* c, const lgx_attn_args& a, int d, void* stream) {
+    const int gq = a.hq / a.hkv;
+    if (gq < 1 || gq > 8 || (d != 64 && d != 128)) return fail(LGX_UNSUPPORTED, "fast prefill attention shape");
+    const int k = (d == 64 ? K_FPA_D64_G1 : K_FPA_D128_G1) + gq - 1;
+    const int64_t wgs = (int64_t)a.B * a.hkv * ((std::max(a.qpr, 1) + 15) / 16);
+    if (wgs > INT32_MAX) return fail(LGX_OUT_OF_BOUNDS, "fast prefill attention grid");
+    if (wgs == 0) return LGX_OK;
+    return launch(c, (Kern)k, dim3((unsigned)wgs), dim3(64 * gq), a, stream);
+}
 inline lgx_status launch_prefill_attn(lgx_ctx* c, const lgx_attn_args& a, int d, void* stream) {
     const int k = prefill_attn_kernel(d, a.hq / a.hkv);
     const int64_t wgs = (int64_t)a.B * a.hkv * a.ncg * ((std::max(a.qpr, 1) + 3) / 4);

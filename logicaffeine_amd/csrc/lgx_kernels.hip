@@ -4182,3 +4182,194 @@ LGX_PFA_KERNELS(128, 5)
 LGX_PFA_KERNELS(128, 6)
 LGX_PFA_KERNELS(128, 7)
 LGX_PFA_KERNELS(128, 8)
+
+// ---------------------------------------------------------------------------
+// Fast prefill attention (opt-in; not the canonical schedule): causal GQA
+// flash attention on binary16 MFMA, within 2e-3 of the canonical attention
+// (the tests check it against the oracle).  Workgroup =
+// (sequence b, KV head g, FPA_Q query positions j0 ..), one wave per query
+// head of the group.  Scores are formed transposed, S^T[token][query] =
+// K . Q^T with v_mfma_f32_16x16x32_f16 (A: 16 K rows x 32 dimensions from
+// LDS; B: the 16 query columns' dimensions in registers, scaled by
+// 1/sqrt(d) before their binary16 rounding), so lane l holds tokens
+// 4 (l/16) + v of query column l % 16.  The online softmax keeps the running
+// maximum and sum per query column (the same in the column's four lanes;
+// the sum adds the binary16-rounded weights, so constant V comes out as V);
+// P^T in binary16 is then directly the B operand of the PV product
+// O^T[dim][query] += V^T . P^T (v_mfma_f32_16x16x16_f16, A from a transposed
+// LDS copy of V).  Tiles of FPA_T tokens pass through LDS once for all the
+// group's heads; tokens past the block's last length read as zeros.  Output
+// rows: binary32 to `out` and / or Q8_0 (the canonical quantisation rule) to
+// xq / xd in row-major or T16 order.
+// ---------------------------------------------------------------------------
+#define FPA_Q 16
+#define FPA_T 64
+template <int D, int GQ>
+__device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
+    constexpr int CH = D / 8;                 // 16-byte pieces per row
+    constexpr int VS = FPA_T + 4;             // V^T row stride (halves): rows 8 bytes apart in the banks
+    constexpr int NKS = D / 32;               // k-steps of the score product
+    constexpr int NT = 64 * GQ;
+    __shared__ __align__(16) uint16_t k_s[FPA_T * D];     // [token][piece ^ (token % CH)]
+    __shared__ __align__(16) uint16_t vt_s[D * VS];       // [dim][token]
+    __shared__ int pg_s[FPA_T / LGX_PAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int qpr = max(a.qpr, 1), nqb = (qpr + FPA_Q - 1) / FPA_Q;
+    const int bg = blockIdx.x / nqb, qb = blockIdx.x - bg * nqb;
+    const int b = bg / a.hkv, g = bg - b * a.hkv;
+    const int j0 = qb * FPA_Q;
+    const int sl = a.seq_len[b];
+    const int h = g * GQ + w;
+    const int qc = lane & 15, kg = lane >> 4;
+    const int jq = j0 + qc;
+    const bool qvalid = jq < qpr;
+    const int Lq = qvalid ? min(max(sl + jq + a.len_add, 0), a.maxlen) : 0;
+    const int jl = min(j0 + FPA_Q, qpr) - 1;
+    const int Lmax = min(max(sl + jl + a.len_add, 0), a.maxlen);   // workgroup-uniform
+    const int row = b * qpr + min(jq, qpr - 1);
+    v8h qv[NKS];
+    {
+        const float* qr = a.q + ((int64_t)row * a.hq + h) * D;
+#pragma unroll
+        for (int s = 0; s < NKS; ++s) {
+            const float4 x0 = *(const float4*)(qr + 32 * s + 8 * kg);
+            const float4 x1 = *(const float4*)(qr + 32 * s + 8 * kg + 4);
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qv[s][e] = (_Float16)(xs[e] * a.scale);
+        }
+    }
+    float m = -__builtin_inff(), l = 0.0f;
+    v4f o[D / 16];
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) o[i] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    const int ntile = (Lmax + FPA_T - 1) / FPA_T;
+    for (int tt = 0; tt < ntile; ++tt) {
+        const int t0 = tt * FPA_T;
+        __syncthreads();                          // the previous tile is fully read
+        if (tid < FPA_T / LGX_PAGE) {
+            int pg = 0;
+            if (t0 + tid * LGX_PAGE < Lmax) pg = a.page_table[(int64_t)b * a.maxp + t0 / LGX_PAGE + tid];
+            pg_s[tid] = min(max(pg, 0), a.num_pages - 1);
+        }
+        __syncthreads();
+        for (int p = tid; p < FPA_T * CH; p += NT) {
+            const int t = p / CH, c = p - t * CH;
+            const int64_t off = (((int64_t)pg_s[t >> 4] * a.hkv + g) * LGX_PAGE + (t & 15)) * D + c * 8;
+            const bool on = t0 + t < Lmax;
+            uint4 kk = *(const uint4*)(a.kpages + off), vv = *(const uint4*)(a.vpages + off);
+            if (!on) kk = vv = make_uint4(0u, 0u, 0u, 0u);
+            *(uint4*)(k_s + t * D + (c ^ (t & (CH - 1))) * 8) = kk;
+            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vt_s[(c * 8 + 2 * e) * VS + t] = (uint16_t)(vw[e] & 0xffffu);
+                vt_s[(c * 8 + 2 * e + 1) * VS + t] = (uint16_t)(vw[e] >> 16);
+            }
+        }
+        __syncthreads();
+        // S^T of the tile's four 16-token sub-tiles
+        v4f st[FPA_T / 16];
+#pragma unroll
+        for (int u = 0; u < FPA_T / 16; ++u) {
+            v4f acc = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+            const int tr = 16 * u + qc;           // the K row of this lane's A operand
+#pragma unroll
+            for (int s = 0; s < NKS; ++s) {
+                const int c = 4 * s + kg;
+                const v8h kv = as_v8h(*(const uint4*)(k_s + tr * D + (c ^ (tr & (CH - 1))) * 8));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qv[s], acc, 0, 0, 0);
+            }
+            st[u] = acc;
+        }
+        float mt = -__builtin_inff();
+#pragma unroll
+        for (int u = 0; u < FPA_T / 16; ++u)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float sv = t0 + 16 * u + 4 * kg + v < Lq ? st[u][v] : -__builtin_inff();
+                st[u][v] = sv;
+                mt = fmaxf(mt, sv);
+            }
+        mt = fmaxf(mt, shfl_xor_f(mt, 16));
+        mt = fmaxf(mt, shfl_xor_f(mt, 32));
+        const float mn = fmaxf(m, mt);
+        const bool none = mn == -__builtin_inff();          // nothing attended yet
+        const float alpha = none ? 1.0f : __expf(m - mn);
+        float ps = 0.0f;
+        v4h pt[FPA_T / 16];
+#pragma unroll
+        for (int u = 0; u < FPA_T / 16; ++u)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float pv = st[u][v] == -__builtin_inff() ? 0.0f : __expf(st[u][v] - mn);
+                pt[u][v] = (_Float16)pv;
+                ps += (float)pt[u][v];            // the weights the PV product uses
+            }
+        ps += shfl_xor_f(ps, 16);
+        ps += shfl_xor_f(ps, 32);
+        l = l * alpha + ps;
+        m = mn;
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i) o[i] *= alpha;
+#pragma unroll
+        for (int u = 0; u < FPA_T / 16; ++u)
+#pragma unroll
+            for (int i = 0; i < D / 16; ++i) {
+                const uint2 vw = *(const uint2*)(vt_s + (16 * i + qc) * VS + 16 * u + 4 * kg);
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, vw), pt[u], o[i], 0, 0, 0);
+            }
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) o[i] *= inv;
+    if (a.out && qvalid) {
+        float* orow = a.out + ((int64_t)row * a.hq + h) * D;
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i)
+            *(float4*)(orow + 16 * i + 4 * kg) = make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
+    }
+    if (a.xq) {
+        // block j (dimensions 32 j ..) of query column qc: o[2j] and o[2j+1]
+        // in the column's four lanes, 8 values each
+#pragma unroll
+        for (int j = 0; j < D / 32; ++j) {
+            const float f0[4] = {o[2 * j][0], o[2 * j][1], o[2 * j][2], o[2 * j][3]};
+            const float f1[4] = {o[2 * j + 1][0], o[2 * j + 1][1], o[2 * j + 1][2], o[2 * j + 1][3]};
+            float am = fmaxf(absmax4(f0), absmax4(f1));
+            am = fmaxf(am, shfl_xor_f(am, 16));
+            am = fmaxf(am, shfl_xor_f(am, 32));
+            uint16_t dh;
+            const uint32_t q0 = quantize4_am(f0, am, dh), q1 = quantize4_am(f1, am, dh);
+            if (qvalid) {
+                const int col = h * D + 32 * j + 4 * kg;
+                *(uint32_t*)(a.xq + xq_off(row, col, a.hq * D, a.xq_t16 != 0)) = q0;
+                *(uint32_t*)(a.xq + xq_off(row, col + 16, a.hq * D, a.xq_t16 != 0)) = q1;
+                if (kg == 0) a.xd[(int64_t)row * (a.hq * D / 32) + h * (D / 32) + j] = dh;
+            }
+        }
+    }
+}
+
+#define LGX_FPA_KERNELS(D, G)                                                                     \
+    extern "C" __global__ __launch_bounds__(64 * G) void lgx_k_attn_prefill_fast_d##D##_g##G(     \
+        const lgx_attn_args a) {                                                                 \
+        attn_prefill_fast_body<D, G>(a);                                                         \
+    }
+LGX_FPA_KERNELS(64, 1)
+LGX_FPA_KERNELS(64, 2)
+LGX_FPA_KERNELS(64, 3)
+LGX_FPA_KERNELS(64, 4)
+LGX_FPA_KERNELS(64, 5)
+LGX_FPA_KERNELS(64, 6)
+LGX_FPA_KERNELS(64, 7)
+LGX_FPA_KERNELS(64, 8)
+LGX_FPA_KERNELS(128, 1)
+LGX_FPA_KERNELS(128, 2)
+LGX_FPA_KERNELS(128, 3)
+LGX_FPA_KERNELS(128, 4)
+LGX_FPA_KERNELS(128, 5)
+LGX_FPA_KERNELS(128, 6)
+LGX_FPA_KERNELS(128, 7)
+LGX_FPA_KERNELS(128, 8)

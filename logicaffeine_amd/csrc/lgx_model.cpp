@@ -85,6 +85,7 @@ struct lgx_model {
     int32_t last_nr = 1;       // partial count of the last lm_head
     int32_t last_B = 0;        // batch of the last lm_head
     bool last_cert = false;    // the last lm_head left no logits (certified greedy pick)
+    bool fast_prefill = false; // lgx_model_set_prefill_mode: binary16 MFMA prefill attention
     std::vector<void*> allocs;
     bool counted = false;      // holds one of ctx->live_models
     // recorded decode steps (lgx_qwen_generate), one per (B, tokens) pair
@@ -660,10 +661,14 @@ lgx_status prefill_chunk(lgx_model* md, int B, int n, const int32_t* tokens, int
         aa.xd = pf.xd;
         aa.qpr = n;
         aa.ncg = ncg;
-        if ((st = launch_prefill_attn(c, aa, d, stream)) != LGX_OK) return st;
-        if ((st = launch(c, d == 64 ? K_ATTN_COMBINE_QUANT_D64 : K_ATTN_COMBINE_QUANT_D128,
-                         dim3(M * hq), dim3(d), aa, stream)) != LGX_OK)
+        if (md->fast_prefill) {
+            // binary16 MFMA flash attention straight to the Q8_0 T16 rows
+            if ((st = launch_prefill_attn_fast(c, aa, d, stream)) != LGX_OK) return st;
+        } else if ((st = launch_prefill_attn(c, aa, d, stream)) != LGX_OK ||
+                   (st = launch(c, d == 64 ? K_ATTN_COMBINE_QUANT_D64 : K_ATTN_COMBINE_QUANT_D128,
+                                dim3(M * hq), dim3(d), aa, stream)) != LGX_OK) {
             return st;
+        }
         if ((st = pf_product(md, md->o[l], M, stream)) != LGX_OK) return st;
         if ((st = pf_norm(md, md->ffn_norm[l], M, H, tiled_groups(hq * d), true, stream)) != LGX_OK)
             return st;
@@ -1185,6 +1190,16 @@ lgx_status lgx_model_set_sampling(lgx_model* m, float temperature, int32_t top_k
         for (lgx_model::StepGraph& g : m->graphs) (void)hipGraphExecDestroy(g.exec);
         m->graphs.clear();
         m->samp = sp;
+        return LGX_OK;
+    });
+}
+
+lgx_status lgx_model_set_prefill_mode(lgx_model* m, int32_t mode) {
+    return guarded(__func__, [&]() -> lgx_status {
+        if (!valid_model(m)) return fail(LGX_INVALID_HANDLE, "invalid lgx_model handle");
+        if (mode != LGX_PREFILL_EXACT && mode != LGX_PREFILL_FAST)
+            return fail(LGX_INVALID_ARGUMENT, "prefill mode %d", mode);
+        m->fast_prefill = mode == LGX_PREFILL_FAST;
         return LGX_OK;
     });
 }
