@@ -57,6 +57,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 INT8_MFMA_PEAK_TOPS = 5000.0   # dense int8 MFMA, MI355X datasheet
+F16_MFMA_PEAK_TFLOPS = 2500.0  # dense binary16 MFMA, MI355X datasheet
 # the kernels the grouped M = 1 launch may use (LGX_GEMV=whole selects the
 # whole-K forms); the one with the most dispatches in the timed pass is reported
 DOMINANT = ("lgx_k_q8_gemv_grp4", "lgx_k_q8_gemv_grp8", "lgx_k_q8_gemv_grp16",
@@ -580,9 +581,25 @@ def decode_bench(ctx, torch, key, seed=3, with_cpu=True):
                for layer in range(cfg["n_layers"])]
     tok0 = int(tok[0].item())
     prompt0 = prompt[0].cpu().numpy()
+    # the same prompts again through the opt-in fast prefill (binary16 MFMA
+    # flash attention; products, norms and the last position exact)
+    gm.reset()
+    gm.set_prefill_mode(True)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    gm.prefill(prompt)
+    torch.cuda.synchronize()
+    fast_s = time.perf_counter() - t
+    print(f"[bench] {key}: fast prefill {B}x{P} in {fast_s:.2f} s ({B * P / fast_s:.0f} tok/s)",
+          file=sys.stderr, flush=True)
     gm.close()
     torch.cuda.empty_cache()
     pf_int8 = lgx.prefill_int8_ops(cfg, B, P)
+    pf_f16 = lgx.prefill_fast_attn_flops(cfg, B, P)
+    # MFMA busy fraction if the pipes ran at their dense peaks: int8 product
+    # operations at the int8 peak plus the flash attention's binary16 flops
+    # at the binary16 peak
+    mfma_frac = (pf_int8 / (INT8_MFMA_PEAK_TOPS * 1e12) + pf_f16 / (F16_MFMA_PEAK_TFLOPS * 1e12)) / fast_s
     out = {
         "model": f"random-init Qwen2.5-{shape.upper()}-shaped Q8_0 "
                  f"({'tied binary16' if cfg['tied'] else 'Q8_0'} lm_head)",
@@ -600,6 +617,14 @@ def decode_bench(ctx, torch, key, seed=3, with_cpu=True):
                              "achieved_TOPS": round(pf_int8 / prefill_s / 1e12, 1),
                              "peak_TOPS": INT8_MFMA_PEAK_TOPS,
                              "utilisation": round(pf_int8 / prefill_s / 1e12 / INT8_MFMA_PEAK_TOPS, 4)}},
+        "prefill_fast_s": round(fast_s, 2),
+        "prefill_fast": {"tokens_per_s": round(B * P / fast_s, 1),
+                         "mode": "LGX_PREFILL_FAST: binary16 MFMA causal flash attention "
+                                 "(within 2e-3), products and the last position exact",
+                         "mfma": {"int8_ops": pf_int8, "f16_flops": pf_f16,
+                                  "int8_peak_TOPS": INT8_MFMA_PEAK_TOPS,
+                                  "f16_peak_TFLOPS": F16_MFMA_PEAK_TFLOPS,
+                                  "utilisation": round(mfma_frac, 4)}},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "bytes_per_step": int(step_bytes_),

@@ -152,6 +152,16 @@ def prefill_int8_ops(cfg: dict, B: int, P: int) -> float:
     return 2.0 * macs
 
 
+def prefill_fast_attn_flops(cfg: dict, B: int, P: int) -> float:
+    """binary16 MFMA flops of the fast prefill's causal attention: 2 d per
+    (query head, attended token) for the scores and 2 d for the PV product,
+    over the batched rows B x (P - 1) of layers 0 .. L - 2 (the row at
+    position p attends p + 1 tokens)."""
+    d, hq, L = cfg["head_dim"], cfg["n_heads"], cfg["n_layers"]
+    att_rows = B * (P - 1) * P / 2.0
+    return 4.0 * d * hq * att_rows * (L - 1)
+
+
 def prefill_valu_ops(cfg: dict, B: int, P: int) -> float:
     """Essential VALU lane operations of the canonical prefill of B prompts of
     P tokens (rows B x (P - 1) through the batched chunks, the last position

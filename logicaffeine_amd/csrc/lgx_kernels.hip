@@ -1737,15 +1737,24 @@ __device__ __forceinline__ void attn_chunk_body(const lgx_attn_args& a) {
         auto pv_stage = [&](int tb) {            // tokens [tb, min(n, tb + VT)) from v_s
             const int te = min(n, tb + VT);
             for (int ts = tb; ts < te; ts += 16) {
-                const int pr = __builtin_bit_cast(int, p_s[hc][ts + k]);
+                // p of the 16 tokens: four 16-byte reads at one address per
+                // 16-lane row (LDS broadcast), no VALU work per token
+                float pt[16];
+                static_for<0, 4>([&](auto Q) {
+                    const float4 p4 = *(const float4*)&p_s[hc][ts + 4 * Q.value];
+                    pt[4 * Q.value] = p4.x;
+                    pt[4 * Q.value + 1] = p4.y;
+                    pt[4 * Q.value + 2] = p4.z;
+                    pt[4 * Q.value + 3] = p4.w;
+                });
                 if (ts + 16 <= te) {
                     // the 16 rows' reads issued together, then the chains
                     uint2 vv[16];
                     static_for<0, 16>([&](auto J) { vv[J.value] = v_load(ts + J.value - tb); });
-                    static_for<0, 16>([&](auto J) { pv_apply(vv[J.value], row_bcast<J.value>(pr)); });
+                    static_for<0, 16>([&](auto J) { pv_apply(vv[J.value], pt[J.value]); });
                 } else {
                     static_for<0, 16>([&](auto J) {
-                        if (ts + J.value < te) pv_token(ts + J.value - tb, row_bcast<J.value>(pr));
+                        if (ts + J.value < te) pv_token(ts + J.value - tb, pt[J.value]);
                     });
                 }
             }
@@ -4139,17 +4148,26 @@ __device__ __forceinline__ void attn_prefill_body(const lgx_attn_args& a) {
         __syncthreads();                          // V stage kap has landed
         const int tb = kap * TOK, te = min(nq, tb + TOK);   // uniform in the wave
         for (int ts = tb; ts < te; ts += 16) {
-            const int pr = __builtin_bit_cast(int, p_s[qp][hc][ts + k]);
+            // p of the 16 tokens: four 16-byte reads at one address per
+            // 16-lane row (LDS broadcast)
+            float pt[16];
+            static_for<0, 4>([&](auto Q) {
+                const float4 p4 = *(const float4*)&p_s[qp][hc][ts + 4 * Q.value];
+                pt[4 * Q.value] = p4.x;
+                pt[4 * Q.value + 1] = p4.y;
+                pt[4 * Q.value + 2] = p4.z;
+                pt[4 * Q.value + 3] = p4.w;
+            });
             if (ts + 16 <= te) {
                 // 8 rows' reads issued together, then their chains (twice)
                 uint4 va[8];
                 static_for<0, 8>([&](auto J) { va[J.value] = v_load(ts + J.value - tb); });
-                static_for<0, 8>([&](auto J) { pv_apply(va[J.value], row_bcast<J.value>(pr)); });
+                static_for<0, 8>([&](auto J) { pv_apply(va[J.value], pt[J.value]); });
                 static_for<0, 8>([&](auto J) { va[J.value] = v_load(ts + 8 + J.value - tb); });
-                static_for<0, 8>([&](auto J) { pv_apply(va[J.value], row_bcast<8 + J.value>(pr)); });
+                static_for<0, 8>([&](auto J) { pv_apply(va[J.value], pt[8 + J.value]); });
             } else {
                 static_for<0, 16>([&](auto J) {
-                    if (ts + J.value < te) pv_apply(v_load(ts + J.value - tb), row_bcast<J.value>(pr));
+                    if (ts + J.value < te) pv_apply(v_load(ts + J.value - tb), pt[J.value]);
                 });
             }
         }
