@@ -455,13 +455,18 @@ lgx_status lgx_model_set_sampling(lgx_model* m, float temperature, int32_t top_k
 /* Prefill modes of lgx_qwen_prefill.  LGX_PREFILL_EXACT (the default): every
  * prompt position runs the decode step's canonical schedule, so the cache,
  * tokens and logits equal the CPU oracle's bit for bit.  LGX_PREFILL_FAST:
- * the prompt positions before the last attend through
- * lgx_gqa_prefill_attn_fast (binary16 MFMA flash attention, within 2e-3 of
- * the canonical attention); the products, norms and the last position stay
- * exact, so the cache differs from the exact one by that attention error
- * and every decode step after it is exact given the cache.  Under
- * LGX_PREFILL=serial (every position through the decode step) the mode has
- * no effect.  No counterpart in the reference. */
+ * the prompt positions before the last run in binary16: each layer's Q8_0
+ * weights dequantised to binary16 (RNE of d * q), the norm, attention and
+ * SwiGLU outputs rounded to binary16, every product a binary16 GEMM with
+ * binary32 accumulation (hipBLASLt), the attention that of
+ * lgx_gqa_prefill_attn_fast; the norms, RoPE, KV append and SwiGLU keep
+ * their exact operations on those inputs.  The cache so left differs from
+ * the exact one by rounding (the Q8_0 activation quantisation above all);
+ * the last prompt position runs the exact decode step, so its token and
+ * logits, and every decode step after, are exact given the cache.  One
+ * layer of binary16 weights and a binary16 operand buffer are allocated on
+ * the first fast prefill.  Under LGX_PREFILL=serial (every position through
+ * the decode step) the mode has no effect.  No counterpart in the reference. */
 enum { LGX_PREFILL_EXACT = 0, LGX_PREFILL_FAST = 1 };
 lgx_status lgx_model_set_prefill_mode(lgx_model* m, int32_t mode);
 /* out[B][vocab] = logits of the last decode/prefill step (binary32); B must

@@ -152,14 +152,24 @@ def prefill_int8_ops(cfg: dict, B: int, P: int) -> float:
     return 2.0 * macs
 
 
-def prefill_fast_attn_flops(cfg: dict, B: int, P: int) -> float:
-    """binary16 MFMA flops of the fast prefill's causal attention: 2 d per
-    (query head, attended token) for the scores and 2 d for the PV product,
-    over the batched rows B x (P - 1) of layers 0 .. L - 2 (the row at
-    position p attends p + 1 tokens)."""
-    d, hq, L = cfg["head_dim"], cfg["n_heads"], cfg["n_layers"]
+def prefill_fast_flops(cfg: dict, B: int, P: int) -> tuple:
+    """MFMA work of the fast prefill of B prompts of P tokens: (binary16
+    flops, int8 operations).  binary16: the GEMMs of the batched rows
+    B x (P - 1) (2 per multiply-add; the last layer of a chunk runs its qkv
+    GEMM only) and the causal attention of layers 0 .. L - 2 (2 d per query
+    head and attended token for the scores, 2 d for PV; the row at position
+    p attends p + 1 tokens).  int8: the last position of every prompt
+    through the exact decode step (and the untied Q8_0 lm_head)."""
+    H, I, d = cfg["hidden"], cfg["inter"], cfg["head_dim"]
+    hq, hkv, L, V = cfg["n_heads"], cfg["n_kv"], cfg["n_layers"], cfg["vocab"]
+    qkv = (hq + 2 * hkv) * d * H
+    full = qkv + H * hq * d + 2 * I * H + H * I
+    rows = B * (P - 1)
+    gemm = 2.0 * rows * ((L - 1) * full + qkv)
     att_rows = B * (P - 1) * P / 2.0
-    return 4.0 * d * hq * att_rows * (L - 1)
+    attn = 4.0 * d * hq * att_rows * (L - 1)
+    int8 = 2.0 * B * (L * full + (0 if cfg["tied"] else V * H))
+    return gemm + attn, int8
 
 
 def prefill_valu_ops(cfg: dict, B: int, P: int) -> float:

@@ -48,7 +48,8 @@ def build_kernels() -> str:
     return HSACO
 
 
-HOST_SOURCES = ["lgx_host.cpp", "lgx_glue.cpp", "lgx_model.cpp", "lgx_gen.cpp", "lgx_gguf.cpp"]
+HOST_SOURCES = ["lgx_host.cpp", "lgx_glue.cpp", "lgx_model.cpp", "lgx_gen.cpp", "lgx_gguf.cpp",
+                "lgx_f16gemm.cpp"]
 BUILD_DIR = os.path.join(HERE, "_build")
 
 
@@ -70,7 +71,7 @@ def build_host() -> str:
     tmp = LIB + ".tmp"
     _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-ffp-contract=off", "-Wall", "-Wextra", "-pthread",
           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", "-I", CSRC,
-          "-o", tmp, *srcs, scratch_obj, f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl"])
+          "-o", tmp, *srcs, scratch_obj, f"-L{ROCM}/lib", "-lamdhip64", "-lhipblaslt", f"-Wl,-rpath,{ROCM}/lib", "-ldl"])
     os.replace(tmp, LIB)
     return LIB
 

@@ -138,6 +138,8 @@ enum Kern {
     K_GEMM_TILED64_S4,
     K_GEMM_TILED32_S4,
     K_EMBED_Q8,
+    K_DEQUANT_F16,
+    K_SWIGLU_F16,
     K_FPA_D64_G1,    // + (gq - 1): fast (binary16 MFMA) prefill attention
     K_FPA_D128_G1 = K_FPA_D64_G1 + 8,
     K_COUNT = K_FPA_D128_G1 + 8
@@ -174,7 +176,8 @@ inline const char* const kKernelNames[] = {
     "lgx_k_q8_gemm_mfma16_group", "lgx_k_q8_gemm_mfma32_group", "lgx_k_q8_gemm_tiled_group", "lgx_k_q8_gemm_tiled64_group",
     "lgx_k_q8_gemm_tiled32_group", "lgx_k_quantize_group", "lgx_k_q8_combine_group",
     "lgx_k_lm_rowconst", "lgx_k_lm_cert", "lgx_k_lm_pick", "lgx_k_add_rmsnorm_quant4s_r8",
-    "lgx_k_q8_gemm_tiled64s4", "lgx_k_q8_gemm_tiled32s4", "lgx_k_embed_q8",
+    "lgx_k_q8_gemm_tiled64s4", "lgx_k_q8_gemm_tiled32s4", "lgx_k_embed_q8", "lgx_k_dequant_f16",
+    "lgx_k_swiglu_f16",
     "lgx_k_attn_prefill_fast_d64_g1", "lgx_k_attn_prefill_fast_d64_g2", "lgx_k_attn_prefill_fast_d64_g3",
     "lgx_k_attn_prefill_fast_d64_g4", "lgx_k_attn_prefill_fast_d64_g5", "lgx_k_attn_prefill_fast_d64_g6",
     "lgx_k_attn_prefill_fast_d64_g7", "lgx_k_attn_prefill_fast_d64_g8",
@@ -251,6 +254,17 @@ struct lgx_ctx {
     std::vector<Timed> timed;
     std::vector<hipEvent_t> event_pool;
 };
+
+// lgx_f16gemm.cpp: the fast prefill's plain binary16 GEMM (hipBLASLt),
+// y[m][n] = x[m][k] . w[n][k]^T, both binary16 row-major, y binary32 or
+// (y16) binary16.
+namespace lgxi {
+struct F16Gemm;
+lgx_status f16gemm_create(F16Gemm** out);
+void f16gemm_destroy(F16Gemm* g);
+lgx_status f16gemm_run(F16Gemm* g, const uint16_t* w, const uint16_t* x, void* y, bool y16, int m,
+                       int n, int k, void* stream);
+}  // namespace lgxi
 
 // lgx_scratch.hip: device address of the fixed scratch array on `device`
 // (current), resolved once per device with hipGetSymbolAddress.

@@ -102,6 +102,7 @@ typedef struct {
     int32_t qpr;
     int32_t ncg;               // prefill: chunks covered by the grid
     int32_t xq_t16;            // combine+quantise: xq in T16 tiles instead of row-major
+    uint16_t* out16;           // fast prefill attention: binary16 out rows [rows][hq*d] (nullable)
 } lgx_attn_args;
 
 #define LGX_PAGE 16
@@ -126,6 +127,15 @@ typedef struct {
     int32_t qpr;
 } lgx_embed_q8_args;
 
+// Q8_0 matrix (T16 quants, S16 scales) to binary16 row-major [n][k]:
+// out[r][c] = RNE_f16(f32(d[r][c/32]) * q[r][c]).
+typedef struct {
+    const int8_t* wt;
+    const uint16_t* wd;
+    uint16_t* out;
+    int32_t n, k;
+} lgx_dequant_args;
+
 // seq_len[b] = (keep ? seq_len[b] : 0) + add for b < m
 typedef struct {
     int32_t* seq_len;
@@ -148,6 +158,7 @@ typedef struct {
     float eps;
     float* xt;
     int32_t xq_t16;        // xq in T16 tiles (the tiled product's operand) instead of row-major
+    uint16_t* x16;         // binary16 y [m][n] (nullable; the fast prefill's GEMM operand)
 } lgx_norm_args;
 
 // qkv = tree(part) (+ bias, nullable); RoPE on the q and k heads at position seq_len[b];
@@ -179,6 +190,14 @@ typedef struct {
     int32_t m, inter;
     int32_t xq_t16;        // xq in T16 tiles instead of row-major
 } lgx_swiglu_args;
+
+// Fast prefill SwiGLU: y[r][i] = RNE_f16(silu(g) * u), g = gu[r][i],
+// u = gu[r][inter + i], all binary16 ([m][2 inter] -> [m][inter]).
+typedef struct {
+    const uint16_t* gu;
+    uint16_t* y;
+    int32_t m, inter;
+} lgx_swiglu16_args;
 
 // 16-row streaming product (K in one range, so each output is final in the
 // workgroup that computes it) with its consumer applied in the same

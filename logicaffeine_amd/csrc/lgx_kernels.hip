@@ -2227,6 +2227,7 @@ __device__ __forceinline__ void norm_body(const lgx_norm_args& a) {
             const float y = (row[i] * r) * wk[k];
             row[i] = y;
             if (a.xn) a.xn[(int64_t)b * a.n + i] = y;
+            if (a.x16) a.x16[(int64_t)b * a.n + i] = f2h(y);
             if (a.xt) a.xt[((int64_t)(b >> 4) * a.n + i) * 16 + (b & 15)] = y;
         }
     }
@@ -2327,6 +2328,9 @@ __device__ __forceinline__ void norm4_body(const lgx_norm_args& a) {
         const float y[4] = {(x4[k].x * r) * w4[k].x, (x4[k].y * r) * w4[k].y, (x4[k].z * r) * w4[k].z,
                             (x4[k].w * r) * w4[k].w};
         if (on && a.xn) *(float4*)(a.xn + (int64_t)b * a.n + 4 * sl) = make_float4(y[0], y[1], y[2], y[3]);
+        if (on && a.x16)
+            *(uint2*)(a.x16 + (int64_t)b * a.n + 4 * sl) =
+                make_uint2(f2h(y[0]) | ((uint32_t)f2h(y[1]) << 16), f2h(y[2]) | ((uint32_t)f2h(y[3]) << 16));
         if (on && a.xt) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) a.xt[((int64_t)(b >> 4) * a.n + 4 * sl + c) * 16 + (b & 15)] = y[c];
@@ -2441,6 +2445,9 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_add_rmsnorm_quant_w(cons
         float y[4] = {(x4[k].x * r) * w4.x, (x4[k].y * r) * w4.y, (x4[k].z * r) * w4.z,
                       (x4[k].w * r) * w4.w};
         if (on && a.xn) *(float4*)(a.xn + (int64_t)b * a.n + 4 * s) = make_float4(y[0], y[1], y[2], y[3]);
+        if (on && a.x16)
+            *(uint2*)(a.x16 + (int64_t)b * a.n + 4 * s) =
+                make_uint2(f2h(y[0]) | ((uint32_t)f2h(y[1]) << 16), f2h(y[2]) | ((uint32_t)f2h(y[3]) << 16));
         if (on && a.xt) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) a.xt[((int64_t)(b >> 4) * a.n + 4 * s + e) * 16 + (b & 15)] = y[e];
@@ -2566,6 +2573,27 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_swiglu_quant(const lgx_s
         *(uint32_t*)(a.xq + xq_off(b, bl * 32 + 4 * j, a.inter, a.xq_t16 != 0)) = qw;
         if (j == 0) a.xd[(int64_t)b * nbl + bl] = dh;
     }
+}
+
+// The fast prefill's SwiGLU on a binary16 gate|up GEMM output: thread per 8
+// consecutive outputs of a row (16-byte loads of gate and up, one store).
+extern "C" __global__ __launch_bounds__(256) void lgx_k_swiglu_f16(const lgx_swiglu16_args a) {
+    const int i8 = a.inter >> 3;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (int64_t)a.m * i8) return;
+    const int64_t r = t / i8;
+    const int i = (int)(t - r * i8) * 8;
+    const uint16_t* g = a.gu + r * 2 * a.inter + i;
+    const uint4 gv = *(const uint4*)g, uv = *(const uint4*)(g + a.inter);
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float f0 = lgx_silu(h2f(gw[e] & 0xffffu)) * h2f(uw[e] & 0xffffu);
+        const float f1 = lgx_silu(h2f(gw[e] >> 16)) * h2f(uw[e] >> 16);
+        o[e] = f2h(f0) | ((uint32_t)f2h(f1) << 16);
+    }
+    *(uint4*)(a.y + r * a.inter + i) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 // Consumers of the fused 16-row products (lgx_gemm_fused_args), run by the
@@ -3554,6 +3582,33 @@ extern "C" __global__ __launch_bounds__(256) void lgx_k_act_to_t16(const lgx_act
 }
 
 // ---------------------------------------------------------------------------
+// Q8_0 matrix in T16 / S16 tiles to binary16 row-major (the fast prefill's
+// GEMM operand): thread per 8 consecutive columns of a row, i.e. one 8-byte
+// piece of a T16 lane slot (columns 64p + 32 half + 8 c .. +7 of row 16 t + r
+// sit at byte ((t np + p) 64 + r + 16 c) 16 + 8 half of the tiles).
+// ---------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(256) void lgx_k_dequant_f16(const lgx_dequant_args a) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int k8 = a.k >> 3;
+    if (i >= (int64_t)a.n * k8) return;
+    const int row = (int)(i / k8), col = (int)(i - (int64_t)row * k8) * 8;
+    const int np = a.k >> 6, nh = s16_nhalf(a.k);
+    const int t = row >> 4, r = row & 15, p = col >> 6, half = (col >> 5) & 1, c = (col >> 3) & 3;
+    const uint2 q8 = *(const uint2*)(a.wt + (((int64_t)t * np + p) * 64 + r + 16 * c) * 16 + 8 * half);
+    const int b = col >> 5;
+    const float d = h2f(a.wd[(((int64_t)t * nh + (b >> 4)) * 16 + r) * 16 + (b & 15)]);
+    const uint32_t w[2] = {q8.x, q8.y};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int8_t lo = (int8_t)((w[e >> 1] >> (16 * (e & 1))) & 0xff);
+        const int8_t hi = (int8_t)((w[e >> 1] >> (16 * (e & 1) + 8)) & 0xff);
+        o[e] = f2h(d * (float)lo) | ((uint32_t)f2h(d * (float)hi) << 16);
+    }
+    *(uint4*)(a.out + (int64_t)row * a.k + col) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// ---------------------------------------------------------------------------
 // Tiled Q8_0 product (prefill; decode batches of 32 / 64 rows).  Workgroup
 // tile: 64 weight rows (4 row tiles) x 32*WM activation rows (2*WM row
 // tiles) over one group of a.grp aligned ranges (1, 2 or 4).  Four waves;
@@ -4347,6 +4402,14 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
 #pragma unroll
         for (int i = 0; i < D / 16; ++i)
             *(float4*)(orow + 16 * i + 4 * kg) = make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
+    }
+    if (a.out16 && qvalid) {
+        uint16_t* orow = a.out16 + ((int64_t)row * a.hq + h) * D;
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i)
+            *(uint2*)(orow + 16 * i + 4 * kg) =
+                make_uint2(f2h(o[i][0]) | ((uint32_t)f2h(o[i][1]) << 16),
+                           f2h(o[i][2]) | ((uint32_t)f2h(o[i][3]) << 16));
     }
     if (a.xq) {
         // block j (dimensions 32 j ..) of query column qc: o[2j] and o[2j+1]

@@ -85,7 +85,8 @@ struct lgx_model {
     int32_t last_nr = 1;       // partial count of the last lm_head
     int32_t last_B = 0;        // batch of the last lm_head
     bool last_cert = false;    // the last lm_head left no logits (certified greedy pick)
-    bool fast_prefill = false; // lgx_model_set_prefill_mode: binary16 MFMA prefill attention
+    bool fast_prefill = false; // lgx_model_set_prefill_mode: binary16 prefill
+    F16Gemm* f16 = nullptr;    // fast prefill: binary16 GEMM plans and workspace
     std::vector<void*> allocs;
     bool counted = false;      // holds one of ctx->live_models
     // recorded decode steps (lgx_qwen_generate), one per (B, tokens) pair
@@ -109,10 +110,17 @@ struct lgx_model {
         float* attn_part = nullptr;  // [rows][hq][nchunk][d + 2]
         int8_t* sq = nullptr;        // [rows16][I] SwiGLU Q8_0 in T16 tiles (fused gate|up)
         uint16_t* sd = nullptr;      // [rows][I / 32]
+        // fast prefill (allocated on its first use): every layer's weights
+        // in binary16 (per layer qkv, o, gate|up, down, row-major), the GEMM
+        // operand rows and the gate|up output rows
+        uint16_t* w16 = nullptr;
+        uint16_t* x16 = nullptr;     // [rows][kmax] binary16
+        uint16_t* gu16 = nullptr;    // [rows][2 I] binary16
     } pf;
 
     ~lgx_model() {
         if (counted) ctx->live_models.fetch_sub(1);
+        if (f16) f16gemm_destroy(f16);
         for (StepGraph& g : graphs) (void)hipGraphExecDestroy(g.exec);
         if (capture) (void)hipStreamDestroy(capture);
         for (void* p : allocs) (void)hipFree(p);
@@ -599,6 +607,136 @@ lgx_status pf_norm(lgx_model* md, const float* w, int M, int n, int nr, bool wit
     return launch_norm(md->ctx, a, stream);
 }
 
+// binary16 weights of one layer: qkv, o, gate|up, down, row-major
+int64_t layer_w16(const lgx_model* md) {
+    const lgx_qwen_config& cf = md->c;
+    const int64_t H = cf.hidden, I = cf.intermediate, hd = (int64_t)cf.n_heads * cf.head_dim;
+    return md->qkv_n * H + H * hd + 2 * I * H + H * I;
+}
+
+lgx_status dequant16(lgx_model* md, const DevQ8& W, uint16_t* out, void* stream) {
+    lgx_dequant_args a{W.m.qs, W.m.d, out, W.m.n, W.m.k};
+    const int64_t threads = (int64_t)W.m.n * (W.m.k / 8);
+    return launch(md->ctx, K_DEQUANT_F16, dim3((unsigned)cdiv(threads, 256)), dim3(256), a, stream);
+}
+
+// The fast prefill's buffers, on its first use: every layer's weights in
+// binary16 (dequantised here, once: the weights never change), the
+// binary16 GEMM operand rows and the gate|up output rows.
+lgx_status prefill_fast_alloc(lgx_model* md, void* stream) {
+    lgx_model::Prefill& pf = md->pf;
+    if (pf.w16) return LGX_OK;
+    const lgx_qwen_config& cf = md->c;
+    const int64_t H = cf.hidden, I = cf.intermediate, hd = (int64_t)cf.n_heads * cf.head_dim;
+    const int64_t rows = (int64_t)cf.max_batch * pf.chunk;
+    const int64_t kmax = std::max({H, I, hd}), lw = layer_w16(md);
+    uint16_t *w16 = nullptr, *x16 = nullptr, *gu16 = nullptr;
+    lgx_status st;
+    if ((st = dev_alloc(md, &w16, (size_t)(lw * cf.n_layers))) ||
+        (st = dev_alloc(md, &x16, (size_t)(rows * kmax))) ||
+        (st = dev_alloc(md, &gu16, (size_t)(rows * 2 * I))))
+        return st;
+    for (int l = 0; l < cf.n_layers; ++l) {
+        uint16_t* w = w16 + lw * l;
+        if ((st = dequant16(md, md->qkv[l], w, stream)) != LGX_OK ||
+            (st = dequant16(md, md->o[l], w + md->qkv_n * H, stream)) != LGX_OK ||
+            (st = dequant16(md, md->gu[l], w + md->qkv_n * H + H * hd, stream)) != LGX_OK ||
+            (st = dequant16(md, md->dn[l], w + md->qkv_n * H + H * hd + 2 * I * H, stream)) != LGX_OK)
+            return st;
+    }
+    if (!md->f16 && (st = f16gemm_create(&md->f16)) != LGX_OK) return st;
+    pf.w16 = w16;
+    pf.x16 = x16;
+    pf.gu16 = gu16;
+    return LGX_OK;
+}
+
+// prefill_chunk in the fast mode: every product a binary16 GEMM (the
+// dequantised weights, binary16 activations, binary32 accumulation; binary32
+// outputs, binary16 for gate|up), the norms and RoPE / KV append as in the
+// exact chunk on one-range outputs, SwiGLU on binary16, the attention
+// lgx_gqa_prefill_attn_fast's kernel.
+lgx_status prefill_chunk_fast(lgx_model* md, int B, int n, const int32_t* tokens, int stride,
+                              void* stream) {
+    lgx_ctx* c = md->ctx;
+    const lgx_qwen_config& cf = md->c;
+    const int H = cf.hidden, I = cf.intermediate, d = cf.head_dim, hq = cf.n_heads,
+              hkv = cf.n_kv_heads;
+    const int M = B * n;
+    lgx_model::Prefill& pf = md->pf;
+    lgx_status st;
+    auto norm16 = [&](const float* w, bool with_part) {
+        lgx_norm_args a{};
+        a.part = with_part ? pf.part : nullptr;
+        a.nr = 1;
+        a.h = pf.h;
+        a.w = w;
+        a.x16 = pf.x16;
+        a.m = M;
+        a.n = H;
+        a.eps = cf.rms_eps;
+        return launch_norm(c, a, stream);
+    };
+    if ((st = embed(md, tokens, stride, n, pf.h, M, stream)) != LGX_OK) return st;
+    for (int l = 0; l < cf.n_layers; ++l) {
+        const uint16_t* wq = pf.w16 + layer_w16(md) * l;
+        const uint16_t* wo = wq + (int64_t)md->qkv_n * H;
+        const uint16_t* wg = wo + (int64_t)H * hq * d;
+        const uint16_t* wd = wg + (int64_t)2 * I * H;
+        if ((st = norm16(md->attn_norm[l], l > 0)) != LGX_OK ||
+            (st = f16gemm_run(md->f16, wq, pf.x16, pf.part, false, M, md->qkv_n, H, stream)) != LGX_OK)
+            return st;
+        lgx_qkv_args qa{};
+        qa.part = pf.part;
+        qa.nr = 1;
+        qa.bias = md->bias[l];
+        qa.cos_t = md->cos_t;
+        qa.sin_t = md->sin_t;
+        qa.seq_len = md->seq_len;
+        qa.page_table = md->page_table;
+        qa.kpages = md->kc[l];
+        qa.vpages = md->vc[l];
+        qa.q_out = pf.q;
+        qa.m = M;
+        qa.hq = hq;
+        qa.hkv = hkv;
+        qa.d = d;
+        qa.maxp = md->maxp;
+        qa.num_pages = md->num_pages;
+        qa.max_seq = cf.max_seq;
+        qa.qpr = n;
+        if ((st = launch_qkv_rope(c, qa, M, stream)) != LGX_OK) return st;
+        if (l == cf.n_layers - 1) break;
+        lgx_attn_args aa{};
+        aa.q = pf.q;
+        aa.kpages = md->kc[l];
+        aa.vpages = md->vc[l];
+        aa.page_table = md->page_table;
+        aa.seq_len = md->seq_len;
+        aa.B = B;
+        aa.hq = hq;
+        aa.hkv = hkv;
+        aa.maxp = md->maxp;
+        aa.num_pages = md->num_pages;
+        aa.maxlen = cf.max_seq;
+        aa.len_add = 1;
+        aa.scale = (float)(1.0 / std::sqrt((double)d));
+        aa.qpr = n;
+        aa.out16 = pf.x16;
+        lgx_swiglu16_args sw{pf.gu16, pf.x16, M, I};
+        if ((st = launch_prefill_attn_fast(c, aa, d, stream)) != LGX_OK ||
+            (st = f16gemm_run(md->f16, wo, pf.x16, pf.part, false, M, H, hq * d, stream)) != LGX_OK ||
+            (st = norm16(md->ffn_norm[l], true)) != LGX_OK ||
+            (st = f16gemm_run(md->f16, wg, pf.x16, pf.gu16, true, M, 2 * I, H, stream)) != LGX_OK ||
+            (st = launch(c, K_SWIGLU_F16, dim3((unsigned)cdiv((int64_t)M * (I / 8), 256)), dim3(256), sw,
+                         stream)) != LGX_OK ||
+            (st = f16gemm_run(md->f16, wd, pf.x16, pf.part, false, M, H, I, stream)) != LGX_OK)
+            return st;
+    }
+    lgx_advance_args av{md->seq_len, B, n, 1};
+    return launch(c, K_ADVANCE, dim3(cdiv(B, 64)), dim3(64), av, stream);
+}
+
 // One chunk: positions seq_len[b] + j (j < n) of the B sequences, tokens
 // tokens[b * stride + j]; ncg chunks of 256 cached tokens bound the
 // attention grid.  Leaves seq_len[b] += n.  The last layer stops after its
@@ -661,14 +799,10 @@ lgx_status prefill_chunk(lgx_model* md, int B, int n, const int32_t* tokens, int
         aa.xd = pf.xd;
         aa.qpr = n;
         aa.ncg = ncg;
-        if (md->fast_prefill) {
-            // binary16 MFMA flash attention straight to the Q8_0 T16 rows
-            if ((st = launch_prefill_attn_fast(c, aa, d, stream)) != LGX_OK) return st;
-        } else if ((st = launch_prefill_attn(c, aa, d, stream)) != LGX_OK ||
-                   (st = launch(c, d == 64 ? K_ATTN_COMBINE_QUANT_D64 : K_ATTN_COMBINE_QUANT_D128,
-                                dim3(M * hq), dim3(d), aa, stream)) != LGX_OK) {
+        if ((st = launch_prefill_attn(c, aa, d, stream)) != LGX_OK ||
+            (st = launch(c, d == 64 ? K_ATTN_COMBINE_QUANT_D64 : K_ATTN_COMBINE_QUANT_D128,
+                         dim3(M * hq), dim3(d), aa, stream)) != LGX_OK)
             return st;
-        }
         if ((st = pf_product(md, md->o[l], M, stream)) != LGX_OK) return st;
         if ((st = pf_norm(md, md->ffn_norm[l], M, H, tiled_groups(hq * d), true, stream)) != LGX_OK)
             return st;
@@ -1075,11 +1209,14 @@ lgx_status lgx_qwen_prefill(lgx_model* m, int32_t B, int32_t P, const int32_t* p
                             smax, m->c.max_seq);
             std::copy(sl.begin(), sl.end(), m->len.begin());
             if ((st = prefill_alloc(m)) != LGX_OK) return st;
+            if (m->fast_prefill && (st = prefill_fast_alloc(m, stream)) != LGX_OK) return st;
             const int chunk = m->pf.chunk;
             for (int p0 = 0; p0 < P - 1; p0 += chunk) {
                 const int n = std::min(chunk, P - 1 - p0);
                 const int ncg = (int)cdiv(std::min(smax + p0 + n, m->c.max_seq), LGX_ATTN_CHUNK);
-                if ((st = prefill_chunk(m, B, n, prompt + p0, P, ncg, stream)) != LGX_OK) return st;
+                st = m->fast_prefill ? prefill_chunk_fast(m, B, n, prompt + p0, P, stream)
+                                     : prefill_chunk(m, B, n, prompt + p0, P, ncg, stream);
+                if (st != LGX_OK) return st;
             }
             // the last position through the decode step: its logits give `next`
             if ((st = layers(m, B, prompt + (P - 1), P, stream)) != LGX_OK ||

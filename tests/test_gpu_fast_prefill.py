@@ -7,11 +7,13 @@
   not a multiple of 16, every head group 1..8, d 64 and 128), config 4's head
   layout at a 4096-token context, and closed forms (constant V gives V; a
   single cached token gives its V row exactly).
-* A model prefilled in fast mode: the cache it leaves, loaded into the
-  oracle, gives the device's next token, logits and last-position K/V bit
-  for bit, and the greedy decode steps after it stay bit-exact (the decode
-  step is exact given the cache).  Layer 0's cache, which no attention
-  precedes, equals the exact prefill's.
+* A model prefilled in fast mode (binary16 GEMMs on dequantised weights,
+  binary16 activations, the fast attention): the cache it leaves, loaded
+  into the oracle, gives the device's next token, logits and last-position
+  K/V bit for bit, and the greedy decode steps after it stay bit-exact (the
+  decode step is exact given the cache).  The fast cache stays within a few
+  percent (relative L2) of the exact prefill's at layer 0 and at the last
+  layer.
 """
 import numpy as np
 import pytest
@@ -148,16 +150,19 @@ def test_fast_prefill_model_then_decode_bit_exact(ctx, name, B, P, steps):
     except Exception:
         gm.close()
         raise
-    for b in range(B):
-        for w in (0, 1):
-            assert np.array_equal(kv[0][b][w], exact_l0[b][w]), (b, w)
-    # the fast cache stays close to the exact one at the last layer
+    # the fast cache stays close to the exact one (layer 0: the binary16
+    # qkv product against the exact Q8_0 one; the last layer: every layer's
+    # rounding)
+    def rel(a, e):
+        a = a.view(np.float16).astype(np.float64)
+        e = e.view(np.float16).astype(np.float64)
+        return np.linalg.norm(a - e) / np.linalg.norm(e)
+
     for w in (0, 1):
-        a = kv[nl - 1][0][w].view(np.float16).astype(np.float64)
-        e = exact_top[w].view(np.float16).astype(np.float64)
-        rel = np.linalg.norm(a - e) / np.linalg.norm(e)
-        print(f"last layer {'KV'[w]}: relative L2 distance fast vs exact {rel:.2e}")
-        assert rel <= 0.05, w
+        r0 = max(rel(kv[0][b][w], exact_l0[b][w]) for b in range(B))
+        rl = rel(kv[nl - 1][0][w], exact_top[w])
+        print(f"{'KV'[w]}: relative L2 distance fast vs exact: layer 0 {r0:.2e}, last layer {rl:.2e}")
+        assert r0 <= 0.02 and rl <= 0.1, w
     om = orc.Model(cfg, seed)
     try:
         for layer in range(nl):
