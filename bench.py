@@ -581,8 +581,8 @@ def decode_bench(ctx, torch, key, seed=3, with_cpu=True):
                for layer in range(cfg["n_layers"])]
     tok0 = int(tok[0].item())
     prompt0 = prompt[0].cpu().numpy()
-    # the same prompts again through the opt-in fast prefill (binary16 MFMA
-    # flash attention; products, norms and the last position exact)
+    # the same prompts again through the opt-in fast prefill (binary16 GEMMs
+    # and flash attention; the last position exact)
     gm.reset()
     gm.set_prefill_mode(True)
     torch.cuda.synchronize()
@@ -710,6 +710,60 @@ def cpu_decode_baseline(key, cfg, seed, kv0, ctx_now, tok0, prompt0, seconds=8.0
                                   f"threads; {npf // 8} in {pf_el1:.1f} s on 1"}}
 
 
+def decode_trace(torch, key, seed=3):
+    """The decode benchmark's model and prompts, the exact prefill, then only
+    graph-replayed greedy steps (one recording replay + `steps`): under a
+    kernel trace, every dispatch after the last prefill kernel belongs to a
+    graph-replayed step."""
+    import logicaffeine_amd as lgx
+
+    shape, B, P, steps = DECODE_CONFIGS[key]
+    ctx = lgx.Context(0)
+    cfg = lgx.qwen_shape(shape, B, P + 1 + steps + min(8, steps))
+    gm = lgx.Model(ctx, cfg, seed)
+    g = torch.Generator(device=ctx.dev)
+    g.manual_seed(seed)
+    prompt = torch.randint(0, cfg["vocab"], (B, P), generator=g, device=ctx.dev,
+                           dtype=torch.int32)
+    tok = gm.prefill(prompt)
+    gm.generate(tok, 1)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    gm.generate(tok, steps)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    gm.close()
+    return {"workload": f"{key} decode B={B}, {P}-token prompts", "graph_steps": steps + 1,
+            "ms_per_step": round(ms, 4), "tokens_per_s": round(B / (ms * 1e-3), 1)}
+
+
+def prefill_probe(torch, mode, key="config4", seed=3):
+    """One prefill of the decode benchmark's prompts (config 4: 64 x 4096) in
+    the given mode (exact | fast), alone, for kernel traces of the prefill."""
+    import logicaffeine_amd as lgx
+
+    shape, B, P, steps = DECODE_CONFIGS[key]
+    ctx = lgx.Context(0)
+    cfg = lgx.qwen_shape(shape, B, P + 1 + steps + min(8, steps))
+    gm = lgx.Model(ctx, cfg, seed)
+    g = torch.Generator(device=ctx.dev)
+    g.manual_seed(seed)
+    prompt = torch.randint(0, cfg["vocab"], (B, P), generator=g, device=ctx.dev,
+                           dtype=torch.int32)
+    gm.set_prefill_mode(mode == "fast")
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    gm.prefill(prompt)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t
+    gm.close()
+    return {"mode": mode, "workload": f"{key} prefill {B}x{P}", "seconds": round(el, 3),
+            "tokens_per_s": round(B * P / el, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -722,6 +776,13 @@ def main():
     ap.add_argument("--kernel-probe", action="store_true",
                     help="only run the config-4 decode's tiled product and attention kernels "
                          "standalone (for counter passes) and print their timings")
+    ap.add_argument("--prefill-probe", choices=["exact", "fast"],
+                    help="only run one prefill of --probe-config in that mode and print its "
+                         "time (for kernel traces of the prefill)")
+    ap.add_argument("--probe-config", default="config4", choices=sorted(DECODE_CONFIGS))
+    ap.add_argument("--decode-trace", choices=sorted(DECODE_CONFIGS),
+                    help="only run that config's prefill and graph-replayed decode steps "
+                         "(for kernel traces of the decode step)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 4 plain 256 MiB device copies (HBM counter calibration)")
     args = ap.parse_args()
@@ -736,6 +797,13 @@ def main():
 
     if args.kernel_probe:
         print(json.dumps({"config4_kernels": kernel_probe_config4(torch)}), flush=True)
+        return
+    if args.prefill_probe:
+        print(json.dumps({"prefill_probe": prefill_probe(torch, args.prefill_probe,
+                                                         args.probe_config)}), flush=True)
+        return
+    if args.decode_trace:
+        print(json.dumps({"decode_trace": decode_trace(torch, args.decode_trace)}), flush=True)
         return
     ctx = lgx.Context(0)
     set_bytes = sum(q8_weight_bytes(n, k) for _, n, k in SHAPES)
