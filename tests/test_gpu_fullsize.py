@@ -14,6 +14,9 @@
   layer) must equal the device's -- the same operations the device's batched
   prefill applies to that row.  Both sequences then decode 64 steps in the
   oracle beside the device batch, tokens and logits compared at every step.
+* Config 4 through the opt-in fast prefill: the caches of sequences 0 and 63
+  loaded into the oracle give the device's next token, logits and last K/V
+  row bit for bit, and 64 greedy steps after it stay bit-exact.
 * The tiled product through the lgx_q8_gemm entry point at M = 8192 (one
   prefill chunk) for the 7B gate|up and down shapes, sampled rows against
   the oracle (rows are independent in the canonical product).
@@ -122,6 +125,60 @@ def test_config4_bench_workload_prompt4096_batch64(ctx):
         for which in (0, 1):
             assert np.array_equal(gm.kv_rows(layer, which, 0, P + steps, page_table=pt),
                                   om.kv(layer, which, 0, P + steps)), (layer, which)
+    gm.close()
+    om.close()
+
+
+@pytest.mark.timeout(900)
+def test_config4_fast_prefill_then_64_decode_steps_bit_exact(ctx):
+    """Config 4 through the opt-in fast prefill (binary16 GEMMs and flash
+    attention): sequences 0 and 63's caches (positions 0..4094, all 28
+    layers), loaded into the oracle, give the device's next token, logits and
+    last-position K/V bit for bit, then 64 greedy steps of both, tokens and
+    logits, bit for bit."""
+    from oracle import oracle as orc
+
+    t0 = time.perf_counter()
+    P, B, steps, seed = 4096, 64, 64, 4
+    cfg = dict(orc.qwen_config("7b"), max_batch=B, max_seq=P + steps)
+    V, nl = cfg["vocab"], cfg["n_layers"]
+    rng = np.random.default_rng(4097)
+    prompt = rng.integers(0, V, size=(B, P)).astype(np.int32)
+    gm = lgx.Model(ctx, cfg, seed)
+    gm.set_prefill_mode(True)
+    tok = gm.prefill(ctx.to_device(prompt))
+    dev_next = host(tok)
+    dev_logits = host(gm.logits(B))
+    pt = gm.tensor_bytes("page_table").view(np.int32).reshape(B, -1)
+    _log("device fast prefill done", t0)
+    seqs = [0, 63]
+    kv = {b: [[gm.kv_rows(layer, w, b, P, page_table=pt) for w in (0, 1)] for layer in range(nl)]
+          for b in seqs}
+    om = orc.Model(dict(cfg, max_batch=2), seed)
+    for slot, b in enumerate(seqs):
+        for layer in range(nl):
+            for w in (0, 1):
+                om.load_kv(layer, w, slot, kv[b][layer][w][:P - 1])
+        om.set_seq_len(slot, P - 1)
+    ref, lg = om.step([0, 1], prompt[seqs, P - 1], want_logits=True)
+    assert np.array_equal(dev_next[seqs], ref)
+    assert np.array_equal(bits(dev_logits[seqs]), bits(lg))
+    for slot, b in enumerate(seqs):
+        for layer in range(nl):
+            for w in (0, 1):
+                assert np.array_equal(om.kv(layer, w, slot, P)[P - 1], kv[b][layer][w][P - 1]), (b, layer, w)
+    _log("last prompt position equal at every layer", t0)
+    del kv
+    hist = []
+    for s in range(steps):
+        gm.decode_step(tok)
+        ref, lg = om.step([0, 1], ref, want_logits=True)
+        got = host(tok)
+        assert np.array_equal(got[seqs], ref), f"step {s}: tokens {got[seqs]} vs {ref}"
+        assert np.array_equal(bits(host(gm.logits(B))[seqs]), bits(lg)), f"step {s}: logits"
+        hist.append(ref.copy())
+    assert len(np.unique(np.stack(hist))) >= 8
+    _log(f"{steps} decode steps equal in tokens and logits", t0)
     gm.close()
     om.close()
 
