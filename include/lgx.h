@@ -463,10 +463,13 @@ lgx_status lgx_model_set_sampling(lgx_model* m, float temperature, int32_t top_k
  * their exact operations on those inputs.  The cache so left differs from
  * the exact one by rounding (the Q8_0 activation quantisation above all);
  * the last prompt position runs the exact decode step, so its token and
- * logits, and every decode step after, are exact given the cache.  One
- * layer of binary16 weights and a binary16 operand buffer are allocated on
- * the first fast prefill.  Under LGX_PREFILL=serial (every position through
- * the decode step) the mode has no effect.  No counterpart in the reference. */
+ * logits, and every decode step after, are exact given the cache.  Setting
+ * LGX_PREFILL_FAST does the mode's one-time work before it returns
+ * (synchronising the device): the prefill buffers, every layer's weights
+ * in binary16 (2 bytes per weight, kept until lgx_model_destroy), the GEMM
+ * library and its plans for chunks of max_batch sequences.  Under
+ * LGX_PREFILL=serial (every position through the decode step) the mode has
+ * no effect.  No counterpart in the reference. */
 enum { LGX_PREFILL_EXACT = 0, LGX_PREFILL_FAST = 1 };
 lgx_status lgx_model_set_prefill_mode(lgx_model* m, int32_t mode);
 /* out[B][vocab] = logits of the last decode/prefill step (binary32); B must

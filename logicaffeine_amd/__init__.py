@@ -686,8 +686,10 @@ class Model:
         _check(lib().lgx_model_set_sampling(self.handle, temperature, top_k, top_p, seed))
 
     def set_prefill_mode(self, fast: bool) -> None:
-        """fast: later prefills attend through the binary16 MFMA flash
-        attention (LGX_PREFILL_FAST); otherwise the exact canonical schedule."""
+        """fast: later prefills run in binary16 (LGX_PREFILL_FAST: binary16
+        GEMMs and flash attention, the last position exact); the call does the
+        mode's one-time work (binary16 weights, GEMM plans) and synchronises.
+        Otherwise the exact canonical schedule."""
         _check(lib().lgx_model_set_prefill_mode(self.handle, 1 if fast else 0))
 
     def decode_step(self, tokens) -> None:

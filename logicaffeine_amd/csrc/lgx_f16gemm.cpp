@@ -145,8 +145,8 @@ static lgx_status make_plan(F16Gemm* g, const uint16_t* w, const uint16_t* x, vo
     return LGX_OK;
 }
 
-lgx_status f16gemm_run(F16Gemm* g, const uint16_t* w, const uint16_t* x, void* y, bool y16, int m,
-                       int n, int k, void* stream) {
+static lgx_status get_plan(F16Gemm* g, const uint16_t* w, const uint16_t* x, void* y, bool y16, int m,
+                           int n, int k, void* stream, const F16Gemm::Plan** out) {
     if (m <= 0 || n <= 0 || k <= 0) return fail(LGX_INVALID_ARGUMENT, "GEMM m=%d n=%d k=%d", m, n, k);
     auto key = std::make_tuple(m, n, k, y16);
     auto it = g->plans.find(key);
@@ -162,7 +162,22 @@ lgx_status f16gemm_run(F16Gemm* g, const uint16_t* w, const uint16_t* x, void* y
         }
         it = g->plans.emplace(key, p).first;
     }
-    const F16Gemm::Plan& p = it->second;
+    *out = &it->second;
+    return LGX_OK;
+}
+
+lgx_status f16gemm_prepare(F16Gemm* g, const uint16_t* w, const uint16_t* x, void* y, bool y16, int m,
+                           int n, int k, void* stream) {
+    const F16Gemm::Plan* p = nullptr;
+    return get_plan(g, w, x, y, y16, m, n, k, stream, &p);
+}
+
+lgx_status f16gemm_run(F16Gemm* g, const uint16_t* w, const uint16_t* x, void* y, bool y16, int m,
+                       int n, int k, void* stream) {
+    const F16Gemm::Plan* pp = nullptr;
+    const lgx_status st = get_plan(g, w, x, y, y16, m, n, k, stream, &pp);
+    if (st != LGX_OK) return st;
+    const F16Gemm::Plan& p = *pp;
     const float alpha = 1.0f, beta = 0.0f;
     LGX_BLAS(hipblasLtMatmul(g->h, p.desc, &alpha, w, p.a, x, p.b, &beta, y, p.c, y, p.c, &p.algo, g->ws,
                              kWorkspace, (hipStream_t)stream));

@@ -264,6 +264,9 @@ lgx_status f16gemm_create(F16Gemm** out);
 void f16gemm_destroy(F16Gemm* g);
 lgx_status f16gemm_run(F16Gemm* g, const uint16_t* w, const uint16_t* x, void* y, bool y16, int m,
                        int n, int k, void* stream);
+// the plan of that shape made now (hipBLASLt's heuristic query), nothing run
+lgx_status f16gemm_prepare(F16Gemm* g, const uint16_t* w, const uint16_t* x, void* y, bool y16, int m,
+                           int n, int k, void* stream);
 }  // namespace lgxi
 
 // lgx_scratch.hip: device address of the fixed scratch array on `device`

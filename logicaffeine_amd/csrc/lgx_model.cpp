@@ -1337,6 +1337,24 @@ lgx_status lgx_model_set_prefill_mode(lgx_model* m, int32_t mode) {
         if (mode != LGX_PREFILL_EXACT && mode != LGX_PREFILL_FAST)
             return fail(LGX_INVALID_ARGUMENT, "prefill mode %d", mode);
         m->fast_prefill = mode == LGX_PREFILL_FAST;
+        if (!m->fast_prefill || m->ctx->prefill_serial) return LGX_OK;
+        // the fast mode's one-time work, here rather than in the first
+        // prefill: buffers, every layer's weights in binary16, the GEMM
+        // library and its plans for full chunks of max_batch sequences
+        lgx_status st = enter(m->ctx);
+        if (st != LGX_OK) return st;
+        if ((st = prefill_alloc(m)) != LGX_OK || (st = prefill_fast_alloc(m, nullptr)) != LGX_OK)
+            return st;
+        const lgx_qwen_config& cf = m->c;
+        const int M = cf.max_batch * m->pf.chunk, H = cf.hidden, I = cf.intermediate,
+                  hd = cf.n_heads * cf.head_dim;
+        const uint16_t* w = m->pf.w16;
+        if ((st = f16gemm_prepare(m->f16, w, m->pf.x16, m->pf.part, false, M, m->qkv_n, H, nullptr)) ||
+            (st = f16gemm_prepare(m->f16, w, m->pf.x16, m->pf.part, false, M, H, hd, nullptr)) ||
+            (st = f16gemm_prepare(m->f16, w, m->pf.x16, m->pf.gu16, true, M, 2 * I, H, nullptr)) ||
+            (st = f16gemm_prepare(m->f16, w, m->pf.x16, m->pf.part, false, M, H, I, nullptr)))
+            return st;
+        LGX_HIP(hipDeviceSynchronize());
         return LGX_OK;
     });
 }
