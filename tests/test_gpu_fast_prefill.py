@@ -13,7 +13,8 @@
   K/V bit for bit, and the greedy decode steps after it stay bit-exact (the
   decode step is exact given the cache).  The fast cache stays within a few
   percent (relative L2) of the exact prefill's at layer 0 and at the last
-  layer.
+  layer.  The same on top of cached context of ragged lengths, and for a
+  GGUF checkpoint with a Q8_0 embedding and norm weights != 1.
 """
 import numpy as np
 import pytest
@@ -183,6 +184,87 @@ def test_fast_prefill_model_then_decode_bit_exact(ctx, name, B, P, steps):
             ref, lg = om.step(np.arange(B), ref, want_logits=True)
             assert np.array_equal(host(tok), ref), f"step {s}"
             assert np.array_equal(bits(host(gm.logits(B))), bits(lg)), f"step {s}"
+    finally:
+        om.close()
+        gm.close()
+
+
+def _load_device_cache(gm, om, cfg, seqs, lens):
+    """The device's cache of sequences `seqs` (first lens[i] positions) into
+    oracle slots 0.. and their lengths."""
+    nl = cfg["n_layers"]
+    for slot, (b, L) in enumerate(zip(seqs, lens)):
+        for layer in range(nl):
+            for w in (0, 1):
+                om.load_kv(layer, w, slot, gm.kv_rows(layer, w, b, L))
+        om.set_seq_len(slot, L)
+
+
+def test_fast_prefill_after_cached_context_ragged(ctx):
+    """A fast prefill on top of cached context of different lengths (two
+    sequences with 100 exact-prefilled positions, two fresh): the oracle,
+    given the device's cache up to the last prompt position, reproduces the
+    next tokens and logits, then 12 greedy steps, bit for bit."""
+    from oracle import oracle as orc
+
+    cfg = dict(orc.qwen_config("tiny"), max_seq=320)
+    B, seed = cfg["max_batch"], 31
+    rng = np.random.default_rng(8)
+    p1 = rng.integers(0, cfg["vocab"], size=(2, 100)).astype(np.int32)
+    p2 = rng.integers(0, cfg["vocab"], size=(B, 150)).astype(np.int32)
+    gm = lgx.Model(ctx, cfg, seed)
+    om = orc.Model(cfg, seed)
+    try:
+        gm.prefill(ctx.to_device(p1))                     # exact: sequences 0, 1
+        gm.set_prefill_mode(True)
+        tok = gm.prefill(ctx.to_device(p2))               # fast, on 100 / 100 / 0 / 0 cached
+        nxt, lg_dev = host(tok), host(gm.logits(B))
+        lens = [100 + 149, 100 + 149, 149, 149]
+        _load_device_cache(gm, om, cfg, range(B), lens)
+        ref, lg = om.step(np.arange(B), p2[:, -1], want_logits=True)
+        assert np.array_equal(nxt, ref)
+        assert np.array_equal(bits(lg_dev), bits(lg))
+        for s in range(12):
+            gm.decode_step(tok)
+            ref, lg = om.step(np.arange(B), ref, want_logits=True)
+            assert np.array_equal(host(tok), ref), s
+            assert np.array_equal(bits(host(gm.logits(B))), bits(lg)), s
+    finally:
+        om.close()
+        gm.close()
+
+
+def test_fast_prefill_gguf_checkpoint_then_decode(ctx, tmp_path):
+    """A checkpoint with a Q8_0 token embedding, norm weights != 1 and a
+    tied hidden-1536 shape (two lm_head ranges) through the fast prefill:
+    the device cache in the oracle (given the same tensors) reproduces the
+    next tokens, logits and 10 greedy steps bit for bit."""
+    from oracle import oracle as orc
+    from tests import gguf_util as gg
+
+    cfg = dict(orc.qwen_config("tiny"), eps=1e-5, theta=20000.0, hidden=1536, n_heads=12,
+               n_kv=2, head_dim=128, inter=512, vocab=1008)
+    t = gg.random_qwen2(cfg, 23, emb_q8=True)
+    path = tmp_path / "model.gguf"
+    gg.write_gguf(path, gg.qwen2_meta(cfg), gg.qwen2_tensors(cfg, t))
+    gm = lgx.Model.load_gguf(ctx, str(path), cfg["max_batch"], cfg["max_seq"])
+    om = orc.Model(gm.cfg, 0)
+    try:
+        gg.load_into_oracle(om, cfg, t)
+        B, P = cfg["max_batch"], 90
+        prompt = np.random.default_rng(5).integers(0, cfg["vocab"], size=(B, P)).astype(np.int32)
+        gm.set_prefill_mode(True)
+        tok = gm.prefill(ctx.to_device(prompt))
+        nxt, lg_dev = host(tok), host(gm.logits(B))
+        _load_device_cache(gm, om, gm.cfg, range(B), [P - 1] * B)
+        ref, lg = om.step(np.arange(B), prompt[:, -1], want_logits=True)
+        assert np.array_equal(nxt, ref)
+        assert np.array_equal(bits(lg_dev), bits(lg))
+        for s in range(10):
+            gm.decode_step(tok)
+            ref, lg = om.step(np.arange(B), ref, want_logits=True)
+            assert np.array_equal(host(tok), ref), s
+            assert np.array_equal(bits(host(gm.logits(B))), bits(lg)), s
     finally:
         om.close()
         gm.close()
