@@ -655,8 +655,8 @@ lgx_status lgx_q8_gemm_quantize_group(lgx_ctx* c, int32_t count, const lgx_q8_ma
             if ((st = launch(c, gk, dim3(ta.wg0[count]), dim3(256), ta, stream)) != LGX_OK) return st;
         } else {
             // 16-row m-groups (several workgroups per weight tile, the
-            // later reads from L2), or 32 rows for 17..32 when forced
-            const int mrows = c->gemm_mt == 32 && m > 16 && m <= 32 ? 32 : 16;
+            // later reads from L2); 17 rows and more take the tiled path
+            const int mrows = 16;
             lgx_stream_group_args sa{};
             sa.count = count;
             sa.wg0[0] = 0;
@@ -682,7 +682,7 @@ lgx_status lgx_q8_gemm_quantize_group(lgx_ctx* c, int32_t count, const lgx_q8_ma
                 if (end > INT32_MAX) return fail(LGX_OUT_OF_BOUNDS, "grouped product too large");
                 sa.wg0[i + 1] = (int32_t)end;
             }
-            if ((st = launch(c, mrows == 32 ? K_GEMM_MFMA32_GROUP : K_GEMM_MFMA16_GROUP,
+            if ((st = launch(c, K_GEMM_MFMA16_GROUP,
                              dim3(sa.wg0[count]), dim3(256), sa, stream)) != LGX_OK)
                 return st;
         }

@@ -125,7 +125,6 @@ enum Kern {
     K_GEMM_MFMA16_SWIGLU,
     K_NORM_W,
     K_GEMM_MFMA16_GROUP,
-    K_GEMM_MFMA32_GROUP,
     K_GEMM_TILED_GROUP,
     K_GEMM_TILED64_GROUP,
     K_GEMM_TILED32_GROUP,
@@ -173,7 +172,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_attn_prefill_d128_g7", "lgx_k_attn_prefill_d128_g8",
     "lgx_k_sample_partial", "lgx_k_sample_final",
     "lgx_k_q8_gemm_mfma16_qkv", "lgx_k_q8_gemm_mfma16_swiglu", "lgx_k_add_rmsnorm_quant_w",
-    "lgx_k_q8_gemm_mfma16_group", "lgx_k_q8_gemm_mfma32_group", "lgx_k_q8_gemm_tiled_group", "lgx_k_q8_gemm_tiled64_group",
+    "lgx_k_q8_gemm_mfma16_group", "lgx_k_q8_gemm_tiled_group", "lgx_k_q8_gemm_tiled64_group",
     "lgx_k_q8_gemm_tiled32_group", "lgx_k_quantize_group", "lgx_k_q8_combine_group",
     "lgx_k_lm_rowconst", "lgx_k_lm_cert", "lgx_k_lm_pick", "lgx_k_add_rmsnorm_quant4s_r8",
     "lgx_k_q8_gemm_tiled64s4", "lgx_k_q8_gemm_tiled32s4", "lgx_k_embed_q8", "lgx_k_dequant_f16",

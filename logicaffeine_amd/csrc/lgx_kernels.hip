@@ -1359,9 +1359,6 @@ __device__ __forceinline__ void q8_stream_group_body(const lgx_stream_group_args
 extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma16_group(const lgx_stream_group_args a) {
     q8_stream_group_body<1>(a);
 }
-extern "C" __global__ __launch_bounds__(256) void lgx_k_q8_gemm_mfma32_group(const lgx_stream_group_args a) {
-    q8_stream_group_body<2>(a);
-}
 
 // ---------------------------------------------------------------------------
 // Range combine: y[i] = canonical pairwise tree over the range partials.

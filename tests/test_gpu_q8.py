@@ -473,6 +473,28 @@ def test_grouped_gemm_bit_exact(ctx, orc, m):
     assert np.array_equal(bits(host(y2)), bits(orc.q8_gemm(qs0, d0, xq2, xd2)))
 
 
+@pytest.mark.parametrize("m,env", [(160, {}), (64, dict(LGX_GEMM_TILED_ROWS="64"))],
+                         ids=["tiled128-rows", "tiled64-rows"])
+def test_grouped_gemm_other_kernel_forms(orc, m, env):
+    """The grouped product's other tiled forms: 128-row tiles (m >= 128) and
+    64-row tiles (forced), each output bit-identical to the oracle."""
+    c = _ctx_with_env(**env)
+    shapes = [(8960, 1536), (1536, 8960), (80, 1088)]
+    Ws, xs, refs = [], [], []
+    for i, (n, k) in enumerate(shapes):
+        qs, d = orc.gen_q8_matrix(7, 500 + i, n, k)
+        x = orc.gen_normal_f32(7, 600 + i + m, (m, k))
+        xq, xd = orc.quantize_q8_0(x)
+        Ws.append(c.q8_matrix(qs, d))
+        xs.append(c.to_device(x))
+        refs.append(orc.q8_gemm(qs, d, xq, xd))
+    ys = c.q8_gemm_quantize_group(Ws, xs)
+    for i, (y, ref) in enumerate(zip(ys, refs)):
+        assert np.array_equal(bits(host(y)), bits(ref)), (m, shapes[i])
+    del Ws, xs, ys
+    c.close()
+
+
 def test_grouped_gemm_m1_and_errors(ctx, orc):
     """m = 1 is the grouped GEMV; bad counts, row counts and shapes are
     refused before anything runs."""
