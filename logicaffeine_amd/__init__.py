@@ -241,7 +241,7 @@ def lib() -> C.CDLL:
 def _check(status: int) -> None:
     if status != 0:
         msg = lib().lgx_last_error()
-        raise LgxError(status, msg.decode() if msg else "(no message)")
+        raise LgxError(status, msg.decode(errors="replace") if msg else "(no message)")
 
 
 def _stream(torch, device):

@@ -33,6 +33,18 @@ using namespace lgxi;
 namespace lgxf {
 
 namespace {
+// A string read from the file, as it appears in an error message: printable
+// ASCII only (other bytes as '?'), at most 64 characters.
+std::string shown(const std::string& s) {
+    std::string o;
+    for (size_t i = 0; i < s.size() && i < 64; ++i) {
+        const unsigned char ch = (unsigned char)s[i];
+        o += ch >= 0x20 && ch < 0x7f ? (char)ch : '?';
+    }
+    if (s.size() > 64) o += "...";
+    return o;
+}
+
 enum : uint32_t {
     GT_U8 = 0, GT_I8, GT_U16, GT_I16, GT_U32, GT_I32, GT_F32, GT_BOOL, GT_STRING, GT_ARRAY,
     GT_U64, GT_I64, GT_F64
@@ -133,7 +145,7 @@ lgx_status Gguf::open(const char* p) {
         Meta m;
         if (!r.ok || !read_value(r, type, m))
             return fail(LGX_MODULE_LOAD_FAILED, "%s: bad metadata entry %llu (%s)", p,
-                        (unsigned long long)i, key.c_str());
+                        (unsigned long long)i, shown(key).c_str());
         meta[key] = m;
     }
     for (uint64_t i = 0; i < nt; ++i) {
@@ -194,14 +206,14 @@ lgx_status Gguf::check_extents() const {
         uint64_t elems = 0;
         if (!tensor_elems(t, &elems))
             return fail(LGX_MODULE_LOAD_FAILED, "%s: tensor %s has invalid dims", path.c_str(),
-                        t.name.c_str());
+                        shown(t.name).c_str());
         if (t.type == GGML_Q8_0 && t.dims[0] % 32 != 0)
             return fail(LGX_MODULE_LOAD_FAILED, "%s: Q8_0 tensor %s has a row of %llu values",
-                        path.c_str(), t.name.c_str(), (unsigned long long)t.dims[0]);
+                        path.c_str(), shown(t.name).c_str(), (unsigned long long)t.dims[0]);
         const uint64_t nbytes = tensor_bytes(t.type, elems);
         if (nbytes > room || t.offset > room - nbytes)
             return fail(LGX_MODULE_LOAD_FAILED, "%s: tensor %s runs past the end of the file",
-                        path.c_str(), t.name.c_str());
+                        path.c_str(), shown(t.name).c_str());
     }
     return LGX_OK;
 }
@@ -224,33 +236,36 @@ const TensorInfo* Gguf::tensor(const std::string& name) const {
 // positioned for reading.
 lgx_status Gguf::seek(const std::string& name, uint32_t type, int64_t rows, int64_t cols) const {
     const TensorInfo* t = tensor(name);
-    if (!t) return fail(LGX_INVALID_ARGUMENT, "%s: tensor %s missing", path.c_str(), name.c_str());
+    if (!t)
+        return fail(LGX_INVALID_ARGUMENT, "%s: tensor %s missing", path.c_str(), shown(name).c_str());
     // open() checked the dims (product <= 2^48) and the extent of the tensor
     const int64_t d0 = (int64_t)t->dims[0];
     int64_t rest = 1;
     for (size_t i = 1; i < t->dims.size(); ++i) rest *= (int64_t)t->dims[i];
     if (t->type != type)
         return fail(LGX_UNSUPPORTED, "%s: tensor %s has ggml type %u (expected %u)", path.c_str(),
-                    name.c_str(), t->type, type);
+                    shown(name).c_str(), t->type, type);
     if (d0 != cols || rest != rows)
         return fail(LGX_INVALID_ARGUMENT, "%s: tensor %s is %lld x %lld (expected %lld x %lld)",
-                    path.c_str(), name.c_str(), (long long)rest, (long long)d0, (long long)rows,
+                    path.c_str(), shown(name).c_str(), (long long)rest, (long long)d0, (long long)rows,
                     (long long)cols);
     if (fseeko(f, (off_t)(data_start + t->offset), SEEK_SET) != 0)
-        return fail(LGX_MODULE_LOAD_FAILED, "%s: seek to %s failed", path.c_str(), name.c_str());
+        return fail(LGX_MODULE_LOAD_FAILED, "%s: seek to %s failed", path.c_str(),
+                    shown(name).c_str());
     return LGX_OK;
 }
 
 lgx_status Gguf::read_q8(const std::string& name, int64_t rows, int64_t cols, int8_t* qs,
                          uint16_t* d) const {
-    if (cols % 32) return fail(LGX_UNSUPPORTED, "%s: row length %lld", name.c_str(), (long long)cols);
+    if (cols % 32)
+        return fail(LGX_UNSUPPORTED, "%s: row length %lld", shown(name).c_str(), (long long)cols);
     lgx_status st = seek(name, GGML_Q8_0, rows, cols);
     if (st != LGX_OK) return st;
     const int64_t nb = cols / 32;
     std::vector<uint8_t> row((size_t)nb * 34);
     for (int64_t r = 0; r < rows; ++r) {
         if (fread(row.data(), 1, row.size(), f) != row.size())
-            return fail(LGX_MODULE_LOAD_FAILED, "%s: short read of %s", path.c_str(), name.c_str());
+            return fail(LGX_MODULE_LOAD_FAILED, "%s: short read of %s", path.c_str(), shown(name).c_str());
         for (int64_t b = 0; b < nb; ++b) {
             const uint8_t* blk = row.data() + b * 34;
             d[r * nb + b] = (uint16_t)(blk[0] | (blk[1] << 8));
@@ -266,7 +281,7 @@ lgx_status Gguf::read_raw(const std::string& name, uint32_t type, int64_t rows, 
     if (st != LGX_OK) return st;
     const size_t nbytes = (size_t)tensor_bytes(type, (uint64_t)rows * cols);
     if (fread(out, 1, nbytes, f) != nbytes)
-        return fail(LGX_MODULE_LOAD_FAILED, "%s: short read of %s", path.c_str(), name.c_str());
+        return fail(LGX_MODULE_LOAD_FAILED, "%s: short read of %s", path.c_str(), shown(name).c_str());
     return LGX_OK;
 }
 
@@ -277,7 +292,7 @@ lgx_status Gguf::config(int32_t max_batch, int32_t max_seq, lgx_qwen_config* cfg
         return fail(LGX_INVALID_ARGUMENT, "%s: no general.architecture", path.c_str());
     if (arch->s != "qwen2")
         return fail(LGX_UNSUPPORTED, "%s: architecture %s (qwen2 is read)", path.c_str(),
-                    arch->s.c_str());
+                    shown(arch->s).c_str());
     auto num = [&](const char* key, double* v) -> lgx_status {
         const Meta* m = find(std::string("qwen2.") + key);
         if (!m || m->type == GT_STRING || m->type == GT_ARRAY)

@@ -112,3 +112,23 @@ def test_corrupt_tensor_extents(tmp_path):
             2**40 if k == "qwen2.embedding_length" else v) for k, ty, v in meta]
     gg.write_gguf(p, big, gg.qwen2_tensors(cfg, t))
     assert _err(p) == "LGX_INVALID_ARGUMENT"
+
+
+def test_non_text_names_in_errors(tmp_path):
+    """Names read from a damaged file reach the error message as printable
+    text: a tensor name of raw bytes with impossible dims gives
+    LGX_MODULE_LOAD_FAILED and a message the binding decodes."""
+    cfg = _tiny()
+    t = gg.random_qwen2(cfg, 2)
+    p = tmp_path / "names.gguf"
+    gg.write_gguf(p, gg.qwen2_meta(cfg), gg.qwen2_tensors(cfg, t))
+    name = "token_embd.weight"
+    _patch_info(p, name, 2, "dim0", 0)                      # a zero dimension: invalid dims
+    b = bytearray(p.read_bytes())
+    at = b.find(name.encode())
+    b[at:at + 5] = b"\xff\xfe\x80\x01\x7f"                   # not UTF-8, not printable
+    p.write_bytes(bytes(b))
+    with pytest.raises(lgx.LgxError) as e:
+        lgx.gguf_config(str(p), 1, 16)
+    assert e.value.status_name == "LGX_MODULE_LOAD_FAILED"
+    assert "tensor ?????_embd.weight has invalid dims" in str(e.value)
