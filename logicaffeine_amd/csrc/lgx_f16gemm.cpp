@@ -181,6 +181,12 @@ lgx_status f16gemm_run(F16Gemm* g, const uint16_t* w, const uint16_t* x, void* y
     const float alpha = 1.0f, beta = 0.0f;
     LGX_BLAS(hipblasLtMatmul(g->h, p.desc, &alpha, w, p.a, x, p.b, &beta, y, p.c, y, p.c, &p.algo, g->ws,
                              kWorkspace, (hipStream_t)stream));
+    if (trace_on()) {
+        int dev = -1;
+        (void)hipGetDevice(&dev);
+        trace_line("gemm dev=%d hipblaslt m=%d n=%d k=%d out=%s stream=%p", dev, m, n, k, y16 ? "f16" : "f32",
+                   stream);
+    }
     return LGX_OK;
 }
 

@@ -40,6 +40,30 @@ inline thread_local bool g_has_error = false;
 // never take timing events (creating them may allocate).
 inline thread_local bool g_untimed = false;
 
+// LGX_TRACE (set, non-empty and not "0"): one line on stderr for every kernel
+// launch, binary16 GEMM call and graph replay, written when the host issues
+// it (the launches of a recorded graph once, at capture, marked "captured").
+// The environment is read once per process.  After LOGOS_TIER_TRACE
+// (crates/logicaffeine_compile/src/vm/tier_trace.rs:1-29).
+inline bool trace_on() {
+    static const bool on = [] {
+        const char* v = std::getenv("LGX_TRACE");
+        return v != nullptr && v[0] != '\0' && std::strcmp(v, "0") != 0;
+    }();
+    return on;
+}
+
+// One trace line: "[lgx] " + the formatted text + newline, in one write.
+inline void trace_line(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    const int n = vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (n < 0) return;
+    std::fprintf(stderr, "[lgx] %s\n", buf);
+}
+
 inline lgx_status fail(lgx_status st, const char* fmt, ...) {
     char buf[1024];
     va_list ap;
@@ -316,7 +340,14 @@ lgx_status launch(lgx_ctx* c, Kern k, dim3 grid, dim3 block, const Args& args, v
     if (e != hipSuccess)
         return fail(LGX_HIP_ERROR, "hipModuleLaunchKernel(%s): %s", kKernelNames[k],
                     hipGetErrorString(e));
-    c->launches.fetch_add(1, std::memory_order_relaxed);
+    const uint64_t n = c->launches.fetch_add(1, std::memory_order_relaxed);
+    if (trace_on()) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        (void)hipStreamIsCapturing((hipStream_t)stream, &cs);
+        trace_line("launch dev=%d n=%llu %s grid=%ux%ux%u block=%ux%ux%u lds=%u stream=%p%s", c->device,
+                   (unsigned long long)n, kKernelNames[k], grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                   shmem, stream, cs == hipStreamCaptureStatusActive ? " captured" : "");
+    }
     return LGX_OK;
 }
 

@@ -1170,6 +1170,8 @@ lgx_status lgx_qwen_generate(lgx_model* m, int32_t B, int32_t* tokens, int32_t n
         for (int s = 0; s < nsteps; ++s) {
             if (exec) {
                 LGX_HIP(hipGraphLaunch(exec, (hipStream_t)stream));
+                if (trace_on())
+                    trace_line("graph dev=%d replay B=%d step=%d stream=%p", m->ctx->device, B, s, stream);
             } else if ((st = layers(m, B, tokens, 1, stream)) != LGX_OK ||
                        (st = head(m, B, tokens, stream)) != LGX_OK) {
                 return st;
