@@ -467,7 +467,8 @@ lgx_status lgx_model_set_sampling(lgx_model* m, float temperature, int32_t top_k
  * LGX_PREFILL_FAST does the mode's one-time work before it returns
  * (synchronising the device): the prefill buffers, every layer's weights
  * in binary16 (2 bytes per weight, kept until lgx_model_destroy), the GEMM
- * library and its plans for chunks of max_batch sequences.  Under
+ * library and its plans for chunks of max_batch sequences; if any of it
+ * fails, the error is returned and the mode stays as it was.  Under
  * LGX_PREFILL=serial (every position through the decode step) the mode has
  * no effect.  No counterpart in the reference. */
 enum { LGX_PREFILL_EXACT = 0, LGX_PREFILL_FAST = 1 };

@@ -87,6 +87,7 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
         c->prefill_chunk = env_int("LGX_PREFILL_CHUNK", 0);
         c->decode_fuse = env_int("LGX_DECODE_FUSE", 1) != 0;
         c->fuse_cols32 = env_int("LGX_FUSE_SWIGLU_COLS", 32) == 64 ? 2 : 1;
+        c->merge_o_tiles = std::min(std::max(env_int("LGX_MERGE_O_TILES", 8), 1), 16);
         c->tiled_swiglu = env_int("LGX_TILED_SWIGLU", 1) != 0;
         c->norm_waves = std::min(std::max(env_int("LGX_NORM_WAVES", 1), 0), 4);
         c->lm_cert = env_int("LGX_LM_CERT", 1) != 0;

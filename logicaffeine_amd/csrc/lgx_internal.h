@@ -165,7 +165,9 @@ enum Kern {
     K_SWIGLU_F16,
     K_FPA_D64_G1,    // + (gq - 1): fast (binary16 MFMA) prefill attention
     K_FPA_D128_G1 = K_FPA_D64_G1 + 8,
-    K_COUNT = K_FPA_D128_G1 + 8
+    K_MERGE_O_D64 = K_FPA_D128_G1 + 8,
+    K_MERGE_O_D128,
+    K_COUNT
 };
 inline const char* const kKernelNames[] = {
     "lgx_k_repack_t16", "lgx_k_quantize_q8_0", "lgx_k_q8q8_gemv",
@@ -207,6 +209,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_attn_prefill_fast_d128_g1", "lgx_k_attn_prefill_fast_d128_g2", "lgx_k_attn_prefill_fast_d128_g3",
     "lgx_k_attn_prefill_fast_d128_g4", "lgx_k_attn_prefill_fast_d128_g5", "lgx_k_attn_prefill_fast_d128_g6",
     "lgx_k_attn_prefill_fast_d128_g7", "lgx_k_attn_prefill_fast_d128_g8",
+    "lgx_k_attn_merge_o_d64", "lgx_k_attn_merge_o_d128",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -252,6 +255,7 @@ struct lgx_ctx {
                                    // rows through the streaming kernels
     bool decode_fuse = true;      // LGX_DECODE_FUSE=0: decode glue in kernels of its own
     int fuse_cols32 = 1;          // LGX_FUSE_SWIGLU_COLS: SwiGLU columns per fused workgroup / 32
+    int merge_o_tiles = 8;        // LGX_MERGE_O_TILES: o_proj row tiles per merge+o workgroup (1..16)
     bool tiled_swiglu = true;     // LGX_TILED_SWIGLU=0: tiled gate|up products leave their outputs to lgx_k_swiglu_quant
     int norm_waves = 1;           // LGX_NORM_WAVES: rows (waves) per workgroup of the wave norm (0: off)
     bool lm_cert = true;          // LGX_LM_CERT=0: greedy tied lm_head through the full logits

@@ -105,6 +105,17 @@ typedef struct {
     uint16_t* out16;           // fast prefill attention: binary16 out rows [rows][hq*d] (nullable)
 } lgx_attn_args;
 
+// Decode attention merge fused with o_proj (K = hq * d <= 1024, one range):
+// workgroup = (sequence, group of `tiles` row tiles of o), 16 waves; see
+// lgx_k_attn_merge_o_d*.
+typedef struct {
+    lgx_attn_args at;          // part, nchunk, hq, seq_len, len_add, maxlen of the merge
+    const int8_t* wt;          // o_proj T16 quants [n][k]
+    const uint16_t* wd;        // o_proj S16 scales
+    float* y;                  // [B][n]
+    int32_t n, k, ngroups, tiles;  // tiles: row tiles per workgroup, 1..16
+} lgx_merge_o_args;
+
 #define LGX_PAGE 16
 #define LGX_ATTN_CHUNK 256
 

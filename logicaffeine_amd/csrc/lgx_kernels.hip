@@ -44,6 +44,13 @@ __device__ __forceinline__ uint4 ld_buf_stream(__amdgpu_buffer_rsrc_t r, int off
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// The same load through the caches (cache policy 0): data that other
+// workgroups of the launch read again.
+__device__ __forceinline__ uint4 ld_buf_cached(__amdgpu_buffer_rsrc_t r, int off) {
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float h2f(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
@@ -2535,6 +2542,148 @@ extern "C" __global__ __launch_bounds__(64) void lgx_k_attn_combine_quant_d64(co
 }
 extern "C" __global__ __launch_bounds__(128) void lgx_k_attn_combine_quant_d128(const lgx_attn_args a) {
     attn_combine_quant_body<128>(a);
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention merge fused with o_proj, for an o_proj of K = hq * d <=
+// 1024 (one range: the small models' step).  grid = B * ngroups, 16 waves:
+// workgroup = (sequence b, group g of `tiles` 16-row tiles of o, <= 16).
+// Wave w requests the partials of head w of sequence b, then (w < the tile
+// count) its tile's weights and scales (through the cache: every sequence's
+// workgroups read them), and merges heads w, w + 16, ... (one memory round
+// up to 16 heads) from the chunk partials with the arithmetic of
+// attn_merge_one_round (M = max of the chunk maxima, w_c = lgx_expf(m_c - M),
+// L and O chains over the chunks in order, O / L; the chunk weights pass
+// between lanes by readlane instead of LDS), the workgroup quantises the row
+// to Q8_0 (quantize4, as lgx_k_attn_combine_quant) into LDS in the grouped
+// GEMV's (pair, chunk) slot order, and each wave runs grp_chain on its tile:
+// y[b][16 t + r] is then what lgx_k_attn_combine_quant followed by the o_proj
+// product gives.  The ngroups workgroups of a sequence each merge all of its
+// heads: a few KiB of partials per head from L2, where a kernel of its own
+// costs a launch and a memory round.  Up to 16 chunks (the launcher checks).
+// ---------------------------------------------------------------------------
+// One wave's merge of (sequence b, head h), in two halves so that its loads
+// can be issued ahead of others: merge_load requests chunk `lane`'s m and l
+// and the o_c of the lane's dimensions for the first 16 chunks (loads past
+// the sequence's chunk count read zeros through the descriptor);
+// merge_finish runs the arithmetic of attn_merge_one_round on them.
+template <int D>
+struct MergeLd {
+    float mc, lc, ov[D / 64][16];
+};
+template <int D>
+__device__ __forceinline__ void merge_load(const lgx_attn_args& a, int b, int h, int lane, MergeLd<D>& m) {
+    const float* pp = a.part + ((int64_t)b * a.hq + h) * a.nchunk * (D + 2);
+    const MergeRd<D> rd(pp, a.nchunk);
+    m.mc = rd(lane, D);
+    m.lc = rd(lane, D + 1);
+#pragma unroll
+    for (int e = 0; e < D / 64; ++e)
+#pragma unroll
+        for (int c = 0; c < 16; ++c) m.ov[e][c] = rd(c, lane + 64 * e);
+}
+template <int D>
+__device__ __forceinline__ void merge_finish(const lgx_attn_args& a, int b, int lane, const MergeLd<D>& m,
+                                             float (&out)[D / 64]) {
+    constexpr int E = D / 64;                     // dimensions per lane: lane + 64 e
+    const int L = min(a.seq_len[b] + a.len_add, a.maxlen);
+    const int nc = (max(L, 0) + LGX_ATTN_CHUNK - 1) / LGX_ATTN_CHUNK;
+    const float M = wave_max(lane < nc ? m.mc : -__builtin_inff());
+    const float wl = lgx_expf(m.mc - M);          // used by lanes < nc only
+    float Ls = 0.0f, O[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) O[e] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        if (c < nc) {                             // uniform
+            const float wc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), c));
+            const float lcc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m.lc), c));
+            Ls = fmaf(wc, lcc, Ls);
+#pragma unroll
+            for (int e = 0; e < E; ++e) O[e] = fmaf(wc, m.ov[e][c], O[e]);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) out[e] = nc > 0 ? O[e] / Ls : 0.0f;
+}
+
+template <int D, int NW>
+__device__ __forceinline__ void attn_merge_o_body(const lgx_merge_o_args& a) {
+    const int NT = min(a.tiles, NW);              // tiles per workgroup, one per wave
+    __shared__ float row_s[1024];
+    __shared__ __align__(16) int8_t xs[GRP_XSLOT];
+    float* dx = (float*)(xs + 1024);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = blockIdx.x / a.ngroups, g = blockIdx.x - b * a.ngroups;
+    const int k = a.k, np = k >> 6, nh = s16_nhalf(k);
+    const int ntiles = a.n >> 4;
+    const int t = NT * g + wave;
+    const bool on = wave < NT && t < ntiles;      // wave-uniform
+    const RangeInfo ri = range_info(0, k);
+    const lgx_attn_args& at = a.at;
+    // this wave's first head: its partials requested first, so the merge
+    // waits for them alone (loads complete in issue order)
+    MergeLd<D> ml;
+    const bool h0 = wave < at.hq;
+    if (h0) merge_load<D>(at, b, wave, lane, ml);
+    GrpRegs R;
+    if (on) {
+        const int r = lane & 15;
+        uint32_t d0[8], d1[8];
+        load_scales_half(a.wd, t, 0, nh, r, d0);
+        load_scales_half(a.wd, t, min(1, nh - 1), nh, r, d1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            R.dw[i] = d0[i];
+            R.dw[8 + i] = d1[i];
+        }
+        // the tile's units through a buffer descriptor of np KiB (units past
+        // it read zeros without a memory access), cache policy 0
+        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)((const uint4*)a.wt + (int64_t)t * np * 64), 0, np * 1024, LGX_BUF_DWORD3);
+#pragma unroll
+        for (int i = 0; i < GRP_WIN; ++i)
+            R.w[i] = ld_buf_cached(wr, (i * 64 + lane) * 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);            // issue order: partials, then weights
+    if (h0) {
+        float o[D / 64];
+        merge_finish<D>(at, b, lane, ml, o);
+#pragma unroll
+        for (int e = 0; e < D / 64; ++e) row_s[wave * D + lane + 64 * e] = o[e];
+    }
+    // heads past NW (more heads than waves): w + NW, w + 2 NW, ...
+    for (int h = wave + NW; h < at.hq; h += NW) {
+        MergeLd<D> m2;
+        merge_load<D>(at, b, h, lane, m2);
+        float o[D / 64];
+        merge_finish<D>(at, b, lane, m2, o);
+#pragma unroll
+        for (int e = 0; e < D / 64; ++e) row_s[h * D + lane + 64 * e] = o[e];
+    }
+    __syncthreads();
+    // Q8_0 of the row: thread q holds values 4q .. 4q + 3 (8 threads per
+    // block, whole 8-lane groups active since k % 32 == 0)
+    if (tid < k / 4) {
+        const float f[4] = {row_s[4 * tid], row_s[4 * tid + 1], row_s[4 * tid + 2], row_s[4 * tid + 3]};
+        uint16_t dh;
+        const uint32_t qw = quantize4(f, dh);
+        const int bl = tid >> 3, c = (tid & 7) >> 1;
+        *(uint32_t*)(xs + ((bl >> 1) * 4 + c) * 16 + (bl & 1) * 8 + 4 * (tid & 1)) = qw;
+        if ((tid & 7) == 0) dx[bl] = h2f(dh);
+    }
+    __syncthreads();
+    if (on) {
+        const float acc = grp_chain(ri, lane, R, xs, dx);
+        if (lane < 16) a.y[(int64_t)b * a.n + t * 16 + lane] = acc;
+    }
+}
+extern "C" __global__ __launch_bounds__(1024) void lgx_k_attn_merge_o_d64(const lgx_merge_o_args a) {
+    attn_merge_o_body<64, 16>(a);
+}
+extern "C" __global__ __launch_bounds__(1024) void lgx_k_attn_merge_o_d128(const lgx_merge_o_args a) {
+    attn_merge_o_body<128, 16>(a);
 }
 
 // SwiGLU from gate|up partials + Q8_0.  grid = (rows, ceil(blocks / 32)),

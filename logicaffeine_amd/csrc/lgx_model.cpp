@@ -368,6 +368,18 @@ bool fused(const lgx_model* md, int m) {
            (c->gemm_mt == 0 || c->gemm_mt == 16);
 }
 
+// Decode steps whose attention merge runs inside the o_proj product
+// (lgx_k_attn_merge_o_d*): o_proj's K = hq * d in one range, the merge in
+// one round of at most 16 chunks, products on the streaming kernels (the
+// tiled ones read each weight tile once for many rows; this kernel reads
+// o's weights once per sequence, from L2).
+bool merge_o(const lgx_model* md, int m) {
+    const lgx_qwen_config& cf = md->c;
+    const int k = cf.n_heads * cf.head_dim;
+    return md->ctx->decode_fuse && !dec_tiled(md, m) && k <= 1024 && k % 64 == 0 && md->nchunk <= 16 &&
+           (cf.head_dim == 64 || cf.head_dim == 128);
+}
+
 lgx_status run_fused(lgx_model* md, Kern kern, const DevQ8& W, int m, int tpw, int ngroups,
                      lgx_gemm_fused_args& f, void* stream) {
     lgx_gemv_args& a = f.g;
@@ -471,10 +483,28 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
         if ((st = launch(c, (Kern)attn_kernel(d, hq / hkv), dim3(md->nchunk, B * hkv), dim3(256), aa,
                          stream)) != LGX_OK)
             return st;
-        if ((st = launch(c, d == 64 ? K_ATTN_COMBINE_QUANT_D64 : K_ATTN_COMBINE_QUANT_D128,
-                         dim3(B * hq), dim3(d), aa, stream)) != LGX_OK)
-            return st;
-        if ((st = product(md, md->o[l], B, stream)) != LGX_OK) return st;
+        if (merge_o(md, B)) {
+            // merge and o_proj in one launch: workgroup = (sequence,
+            // merge_o_tiles row tiles of o), each merging the sequence's
+            // heads itself
+            lgx_merge_o_args mo{};
+            mo.at = aa;
+            mo.wt = md->o[l].m.qs;
+            mo.wd = md->o[l].m.d;
+            mo.y = md->part;
+            mo.n = H;
+            mo.k = hq * d;
+            mo.tiles = c->merge_o_tiles;
+            mo.ngroups = (int)cdiv(H / 16, mo.tiles);
+            if ((st = launch(c, d == 64 ? K_MERGE_O_D64 : K_MERGE_O_D128, dim3((unsigned)(B * mo.ngroups)),
+                             dim3(1024), mo, stream)) != LGX_OK)
+                return st;
+        } else {
+            if ((st = launch(c, d == 64 ? K_ATTN_COMBINE_QUANT_D64 : K_ATTN_COMBINE_QUANT_D128,
+                             dim3(B * hq), dim3(d), aa, stream)) != LGX_OK)
+                return st;
+            if ((st = product(md, md->o[l], B, stream)) != LGX_OK) return st;
+        }
         if ((st = norm(md, md->ffn_norm[l], B, H, parts(md, md->o[l], B), true, nullptr, true,
                        stream)) != LGX_OK)
             return st;
@@ -1338,11 +1368,14 @@ lgx_status lgx_model_set_prefill_mode(lgx_model* m, int32_t mode) {
         if (!valid_model(m)) return fail(LGX_INVALID_HANDLE, "invalid lgx_model handle");
         if (mode != LGX_PREFILL_EXACT && mode != LGX_PREFILL_FAST)
             return fail(LGX_INVALID_ARGUMENT, "prefill mode %d", mode);
-        m->fast_prefill = mode == LGX_PREFILL_FAST;
-        if (!m->fast_prefill || m->ctx->prefill_serial) return LGX_OK;
+        if (mode == LGX_PREFILL_EXACT || m->ctx->prefill_serial) {
+            m->fast_prefill = mode == LGX_PREFILL_FAST;
+            return LGX_OK;
+        }
         // the fast mode's one-time work, here rather than in the first
         // prefill: buffers, every layer's weights in binary16, the GEMM
-        // library and its plans for full chunks of max_batch sequences
+        // library and its plans for full chunks of max_batch sequences.  The
+        // mode changes only once all of it has succeeded.
         lgx_status st = enter(m->ctx);
         if (st != LGX_OK) return st;
         if ((st = prefill_alloc(m)) != LGX_OK || (st = prefill_fast_alloc(m, nullptr)) != LGX_OK)
@@ -1357,6 +1390,7 @@ lgx_status lgx_model_set_prefill_mode(lgx_model* m, int32_t mode) {
             (st = f16gemm_prepare(m->f16, w, m->pf.x16, m->pf.part, false, M, H, I, nullptr)))
             return st;
         LGX_HIP(hipDeviceSynchronize());
+        m->fast_prefill = true;
         return LGX_OK;
     });
 }

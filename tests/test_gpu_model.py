@@ -461,9 +461,10 @@ def _ctx_with(env):
 @pytest.mark.parametrize("name", ["tiny", "tiny_untied"])
 def test_fused_decode_consumers_bit_exact(name, env):
     """Decode batches of 2..32 rows run RoPE + KV append inside the qkv
-    product's workgroups (one per head and 16-row m-group) and SwiGLU + Q8_0
-    inside the gate|up product's (32 or 64 columns each); with the fusion
-    off they run as kernels of their own.  Every form leaves the oracle's
+    product's workgroups (one per head and 16-row m-group), SwiGLU + Q8_0
+    inside the gate|up product's (32 or 64 columns each) and, from one row,
+    the attention merge inside the o_proj product's (one per sequence and
+    four row tiles); with the fusion off they run as kernels of their own.  Every form leaves the oracle's
     tokens, logits, hidden state and KV bits: 24 rows (a second, partial
     m-group), 3 rows, and one row (the grouped GEMV), graph replays
     included."""
