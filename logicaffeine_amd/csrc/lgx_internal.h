@@ -167,6 +167,8 @@ enum Kern {
     K_FPA_D128_G1 = K_FPA_D64_G1 + 8,
     K_MERGE_O_D64 = K_FPA_D128_G1 + 8,
     K_MERGE_O_D128,
+    K_NORM_QKV_D64,
+    K_NORM_QKV_D128,
     K_COUNT
 };
 inline const char* const kKernelNames[] = {
@@ -209,7 +211,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_attn_prefill_fast_d128_g1", "lgx_k_attn_prefill_fast_d128_g2", "lgx_k_attn_prefill_fast_d128_g3",
     "lgx_k_attn_prefill_fast_d128_g4", "lgx_k_attn_prefill_fast_d128_g5", "lgx_k_attn_prefill_fast_d128_g6",
     "lgx_k_attn_prefill_fast_d128_g7", "lgx_k_attn_prefill_fast_d128_g8",
-    "lgx_k_attn_merge_o_d64", "lgx_k_attn_merge_o_d128",
+    "lgx_k_attn_merge_o_d64", "lgx_k_attn_merge_o_d128", "lgx_k_norm_qkv_d64", "lgx_k_norm_qkv_d128",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,

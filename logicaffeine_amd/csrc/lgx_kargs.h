@@ -190,6 +190,24 @@ typedef struct {
                            // of sequence b (0 or 1: one row per sequence)
 } lgx_qkv_args;
 
+// Decode residual + RMSNorm + Q8_0 fused with the qkv product and its RoPE /
+// KV-append consumer (hidden <= 1024, one range): workgroup = (sequence,
+// group of LGX_NQ_TILES row tiles of qkv = 128 columns), one wave per tile;
+// see lgx_k_norm_qkv_d*.
+#define LGX_NQ_TILES 8
+#define LGX_NQ_MAXR 8          // partial ranges of the residual's product
+typedef struct {
+    lgx_qkv_args q;            // consumer: bias, RoPE tables, cache, q_out, heads
+    const float* h;            // residual in [B][H]
+    const float* part;         // previous products' range partials [nr][B][H] (nr = 0: none)
+    float* h_out;              // residual out [B][H] (written by each sequence's group 0)
+    const float* w;            // RMSNorm weight [H]
+    const int8_t* wt;          // qkv T16 quants [n][H]
+    const uint16_t* wd;        // qkv S16 scales
+    int32_t nr, H, n, ngroups;
+    float eps;
+} lgx_norm_qkv_args;
+
 // a = silu(gate) * up from tree(part) ([nr][m][2*inter]), then Q8_0(a)
 // (xq/xd) and/or binary32 a (y); each output nullable.
 typedef struct {

@@ -2679,6 +2679,172 @@ __device__ __forceinline__ void attn_merge_o_body(const lgx_merge_o_args& a) {
         if (lane < 16) a.y[(int64_t)b * a.n + t * 16 + lane] = acc;
     }
 }
+// ---------------------------------------------------------------------------
+// Decode residual + RMSNorm + Q8_0 fused with the qkv product and its RoPE /
+// KV-append consumer, for hidden H <= 1024 (one range): grid = B * ngroups,
+// 8 waves: workgroup = (sequence b, group g of 8 row tiles of qkv, i.e. 128
+// columns: whole heads of d = 64 or 128; two workgroups per CU at 128 VGPRs,
+// so config 3's 288 run in one round).  Thread t requests h[b][j] and the
+// range partials of the previous product for j = t and t + 512, then wave w
+// its tile's weights
+// (through the cache) and the consumer's bias, RoPE and page entries are
+// requested; x_j = h_j + tree(partials) (group 0 writes it to h_out, a
+// buffer other than h: the other groups of the sequence still read h), the
+// sum of squares by orc_halving_sum's pairs over 1024 slots (zeros past H,
+// which add nothing: x^2 >= 0), evaluated by wave 0 from LDS as the norm
+// kernels do, y = (x * r) * w with r = 1 / sqrt(S / H + eps), Q8_0 of y
+// (quantize4) into the grouped GEMV's slots, the tile's grp_chain, and the
+// lgx_k_qkv_rope_append operations on the 128 columns: bias, rotate-half
+// RoPE at position seq_len[b], q to q_out, k and v to the cache.  Each group
+// repeats the sequence's norm (H values and their partials, from L2) where
+// a kernel of its own costs a launch and a memory round.
+// ---------------------------------------------------------------------------
+#define NQ_TILES LGX_NQ_TILES
+template <int D>
+__device__ __forceinline__ void norm_qkv_body(const lgx_norm_qkv_args& a) {
+    constexpr int NT = 64 * NQ_TILES;             // one wave per tile
+    constexpr int EP = 1024 / NT;                 // row elements per thread
+    constexpr int MAXR = LGX_NQ_MAXR;             // partial ranges (the launcher checks)
+    __shared__ float row_s[1024];
+    __shared__ float sq_s[1024];
+    __shared__ float out_s[NQ_TILES * 16];
+    __shared__ float rr_s;
+    __shared__ __align__(16) int8_t xs[GRP_XSLOT];
+    float* dx = (float*)(xs + 1024);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = blockIdx.x / a.ngroups, g = blockIdx.x - b * a.ngroups;
+    const int H = a.H, np = H >> 6, nh = s16_nhalf(H);
+    const int ntiles = a.n >> 4;
+    const int t = NQ_TILES * g + wave;
+    const bool on = t < ntiles;                   // wave-uniform
+    const lgx_qkv_args& q = a.q;
+    // 1. the row and its partials (elements j = tid + NT e), the weights of
+    // the thread's four Q8_0 values (4 tid ..), all issued first
+    float hv[EP], pv[EP][MAXR];
+    const int64_t stride = (int64_t)q.m * H;
+#pragma unroll
+    for (int e = 0; e < EP; ++e) {
+        const int jc = min(tid + NT * e, H - 1);
+        hv[e] = a.h[(int64_t)b * H + jc];
+        // ranges past nr re-read range nr - 1 (never added: the tree stops at nr)
+#pragma unroll
+        for (int r = 0; r < MAXR; ++r)
+            pv[e][r] = a.part ? a.part[(int64_t)min(r, max(a.nr, 1) - 1) * stride + (int64_t)b * H + jc] : 0.0f;
+    }
+    const int q4 = min(tid, H / 4 - 1);
+    const float4 w4 = *(const float4*)(a.w + 4 * q4);
+    // 2. the tile's weights and scales
+    const RangeInfo ri = range_info(0, H);
+    GrpRegs R;
+    if (on) {
+        const int r = lane & 15;
+        uint32_t d0[8], d1[8];
+        load_scales_half(a.wd, t, 0, nh, r, d0);
+        load_scales_half(a.wd, t, min(1, nh - 1), nh, r, d1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            R.dw[i] = d0[i];
+            R.dw[8 + i] = d1[i];
+        }
+        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)((const uint4*)a.wt + (int64_t)t * np * 64), 0, np * 1024, LGX_BUF_DWORD3);
+#pragma unroll
+        for (int i = 0; i < GRP_WIN; ++i) R.w[i] = ld_buf_cached(wr, (i * 64 + lane) * 16);
+    }
+    // 3. the consumer's inputs for column cc = tid (< 128) of the group:
+    // q / k head columns i < d/2 take the pair (i, i + d/2), v columns one
+    // value; the others idle
+    const int d = D, half = D / 2;
+    const int col = NQ_TILES * 16 * g + min(tid, NQ_TILES * 16 - 1);
+    const int head = col / d, ci = col - head * d;
+    const bool rot = head < q.hq + q.hkv;
+    const bool cact = tid < NQ_TILES * 16 && col < a.n && (rot ? ci < half : true);
+    const int pos = min(max(q.seq_len[b], 0), q.max_seq - 1);
+    const int page = min(max(q.page_table[(int64_t)b * q.maxp + pos / LGX_PAGE], 0), q.num_pages - 1);
+    const float b0 = q.bias ? q.bias[min(col, a.n - 1)] : 0.0f;
+    const float b1 = q.bias && rot ? q.bias[min(col + half, a.n - 1)] : 0.0f;
+    const float cs = rot ? q.cos_t[(int64_t)pos * half + min(ci, half - 1)] : 0.0f;
+    const float sn = rot ? q.sin_t[(int64_t)pos * half + min(ci, half - 1)] : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);            // issue order: row, weights, consumer
+    // 4. residual and squares
+#pragma unroll
+    for (int e = 0; e < EP; ++e) {
+        const int j = tid + NT * e;
+        float x = hv[e];
+        if (a.part && a.nr > 0) x = hv[e] + tree_sum_r<MAXR>(pv[e], a.nr);
+        if (j < H) {
+            row_s[j] = x;
+            if (g == 0) a.h_out[(int64_t)b * H + j] = x;
+        }
+        sq_s[j] = j < H ? x * x : 0.0f;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        // orc_halving_sum over the 1024 slots: lane l folds l + 64 j, j < 16
+        // (levels 512 .. 64), then the lane levels
+        float qv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) qv[j] = sq_s[tid + 64 * j];
+#pragma unroll
+        for (int s = 8; s >= 1; s >>= 1) {
+#pragma unroll
+            for (int j = 0; j < s; ++j) qv[j] = qv[j] + qv[j + s];
+        }
+        const float Ssq = wave_tree_sum(qv[0]);
+        if (tid == 0) rr_s = 1.0f / sqrtf(Ssq / (float)H + a.eps);
+    }
+    __syncthreads();
+    // 5. y = (x * r) * w and its Q8_0 (8 threads per block)
+    if (tid < H / 4) {
+        const float r = rr_s;
+        const float f[4] = {(row_s[4 * tid] * r) * w4.x, (row_s[4 * tid + 1] * r) * w4.y,
+                            (row_s[4 * tid + 2] * r) * w4.z, (row_s[4 * tid + 3] * r) * w4.w};
+        uint16_t dh;
+        const uint32_t qw = quantize4(f, dh);
+        const int bl = tid >> 3, c = (tid & 7) >> 1;
+        *(uint32_t*)(xs + ((bl >> 1) * 4 + c) * 16 + (bl & 1) * 8 + 4 * (tid & 1)) = qw;
+        if ((tid & 7) == 0) dx[bl] = h2f(dh);
+    }
+    __syncthreads();
+    // 6. the tiles' chains
+    if (on) {
+        const float acc = grp_chain(ri, lane, R, xs, dx);
+        if (lane < 16) out_s[wave * 16 + lane] = acc;
+    }
+    __syncthreads();
+    // 7. bias, RoPE, q out, KV append
+    if (cact) {
+        const int cc = tid;
+        const int slot = pos % LGX_PAGE;
+        if (rot) {
+            const float x0 = q.bias ? out_s[cc] + b0 : out_s[cc];
+            const float x1 = q.bias ? out_s[cc + half] + b1 : out_s[cc + half];
+            const float t0 = x0 * cs, t1 = x1 * sn, t2 = x1 * cs, t3 = x0 * sn;
+            const float y0 = t0 - t1, y1 = t2 + t3;
+            if (head < q.hq) {
+                float* qo = q.q_out + ((int64_t)b * q.hq + head) * d;
+                qo[ci] = y0;
+                qo[ci + half] = y1;
+            } else {
+                uint16_t* kd = q.kpages + (((int64_t)page * q.hkv + (head - q.hq)) * LGX_PAGE + slot) * d;
+                kd[ci] = f2h(y0);
+                kd[ci + half] = f2h(y1);
+            }
+        } else {
+            const int gv = head - q.hq - q.hkv;
+            uint16_t* vd = q.vpages + (((int64_t)page * q.hkv + gv) * LGX_PAGE + slot) * d;
+            vd[ci] = f2h(q.bias ? out_s[cc] + b0 : out_s[cc]);
+        }
+    }
+}
+extern "C" __global__ __launch_bounds__(64 * LGX_NQ_TILES) void lgx_k_norm_qkv_d64(const lgx_norm_qkv_args a) {
+    norm_qkv_body<64>(a);
+}
+extern "C" __global__ __launch_bounds__(64 * LGX_NQ_TILES) void lgx_k_norm_qkv_d128(const lgx_norm_qkv_args a) {
+    norm_qkv_body<128>(a);
+}
+
 extern "C" __global__ __launch_bounds__(1024) void lgx_k_attn_merge_o_d64(const lgx_merge_o_args a) {
     attn_merge_o_body<64, 16>(a);
 }

@@ -70,6 +70,8 @@ struct lgx_model {
     std::vector<int32_t> len;
     // activations for max_batch rows
     float* h = nullptr;
+    float* h2 = nullptr;       // second residual buffer (lgx_k_norm_qkv_d* writes its sum there)
+    float* hcur = nullptr;     // the buffer holding the residual after layers()
     float* xn = nullptr;
     int8_t* xq = nullptr;
     uint16_t* xd = nullptr;
@@ -380,6 +382,19 @@ bool merge_o(const lgx_model* md, int m) {
            (cf.head_dim == 64 || cf.head_dim == 128);
 }
 
+// Decode steps whose attention-side norm runs inside the qkv product
+// (lgx_k_norm_qkv_d*): hidden in one range, qkv columns in whole groups of
+// 128 (whole heads), at most LGX_NQ_MAXR partials of the down product,
+// products on the streaming kernels (each sequence's workgroups read the
+// qkv weights from L2).
+bool norm_qkv(const lgx_model* md, int m) {
+    const lgx_qwen_config& cf = md->c;
+    const int d = cf.head_dim;
+    return md->ctx->decode_fuse && !dec_tiled(md, m) && cf.hidden <= 1024 && cf.hidden % 64 == 0 &&
+           (d == 64 || d == 128) && md->qkv_n % (16 * LGX_NQ_TILES) == 0 &&
+           parts(md, md->dn[0], m) <= LGX_NQ_MAXR;
+}
+
 lgx_status run_fused(lgx_model* md, Kern kern, const DevQ8& W, int m, int tpw, int ngroups,
                      lgx_gemm_fused_args& f, void* stream) {
     lgx_gemv_args& a = f.g;
@@ -397,13 +412,13 @@ lgx_status run_fused(lgx_model* md, Kern kern, const DevQ8& W, int m, int tpw, i
     return launch(md->ctx, kern, dim3(ngroups * a.nmgroups), dim3(256), f, stream);
 }
 
-lgx_status norm(lgx_model* md, const float* w, int m, int n, int nr_part, bool with_part,
+lgx_status norm(lgx_model* md, float* h, const float* w, int m, int n, int nr_part, bool with_part,
                 float* xn, bool q8, void* stream, float* xt = nullptr) {
     lgx_norm_args a{};
     a.xt = xt;
     a.part = with_part ? md->part : nullptr;
     a.nr = nr_part;
-    a.h = md->h;
+    a.h = h;
     a.w = w;
     a.xn = xn;
     a.xq = q8 ? md->xq : nullptr;
@@ -424,10 +439,12 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
               hkv = cf.n_kv_heads;
     lgx_status st;
     if ((st = embed(md, tokens, tokens_stride, 1, md->h, B, stream)) != LGX_OK) return st;
+    float* hcur = md->h;   // the residual; lgx_k_norm_qkv_d* moves it to the other buffer
+    const bool nq = norm_qkv(md, B);
     for (int l = 0; l < cf.n_layers; ++l) {
         // norm (+ residual of the previous layer's down product) -> Q8
-        if ((st = norm(md, md->attn_norm[l], B, H, parts(md, md->dn[0], B), l > 0, nullptr, true,
-                       stream)) != LGX_OK)
+        if (!nq && (st = norm(md, hcur, md->attn_norm[l], B, H, parts(md, md->dn[0], B), l > 0, nullptr,
+                              true, stream)) != LGX_OK)
             return st;
         lgx_qkv_args qa{};
         qa.part = md->part;
@@ -447,7 +464,31 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
         qa.maxp = md->maxp;
         qa.num_pages = md->num_pages;
         qa.max_seq = cf.max_seq;
-        if (fused(md, B)) {
+        if (nq) {
+            // residual, norm, Q8_0, qkv, RoPE and KV append in one launch:
+            // workgroup = (sequence, LGX_NQ_TILES row tiles of qkv), each
+            // normalising the sequence's row itself; the residual moves to
+            // the other buffer (the sequence's other workgroups still read
+            // this one)
+            float* hnext = hcur == md->h ? md->h2 : md->h;
+            lgx_norm_qkv_args a{};
+            a.q = qa;
+            a.h = hcur;
+            a.part = l > 0 ? md->part : nullptr;
+            a.nr = l > 0 ? parts(md, md->dn[0], B) : 0;
+            a.h_out = hnext;
+            a.w = md->attn_norm[l];
+            a.wt = md->qkv[l].m.qs;
+            a.wd = md->qkv[l].m.d;
+            a.H = H;
+            a.n = md->qkv_n;
+            a.ngroups = md->qkv_n / (16 * LGX_NQ_TILES);
+            a.eps = cf.rms_eps;
+            if ((st = launch(c, d == 64 ? K_NORM_QKV_D64 : K_NORM_QKV_D128, dim3((unsigned)(B * a.ngroups)),
+                             dim3(64 * LGX_NQ_TILES), a, stream)) != LGX_OK)
+                return st;
+            hcur = hnext;
+        } else if (fused(md, B)) {
             // one workgroup per (head, 16-row m-group)
             lgx_gemm_fused_args f{};
             f.q = qa;
@@ -505,7 +546,7 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
                 return st;
             if ((st = product(md, md->o[l], B, stream)) != LGX_OK) return st;
         }
-        if ((st = norm(md, md->ffn_norm[l], B, H, parts(md, md->o[l], B), true, nullptr, true,
+        if ((st = norm(md, hcur, md->ffn_norm[l], B, H, parts(md, md->o[l], B), true, nullptr, true,
                        stream)) != LGX_OK)
             return st;
         if (fused(md, B) && I % (32 * c->fuse_cols32) == 0) {
@@ -535,6 +576,7 @@ lgx_status layers(lgx_model* md, int B, const int32_t* tokens, int tokens_stride
             return st;
         if ((st = product(md, md->dn[l], B, stream)) != LGX_OK) return st;
     }
+    md->hcur = hcur;
     return LGX_OK;
 }
 
@@ -545,7 +587,7 @@ lgx_status head(lgx_model* md, int B, int32_t* next, void* stream) {
     const int H = cf.hidden;
     lgx_status st;
     const bool tied = f16_head(md);
-    if ((st = norm(md, md->out_norm, B, H, parts(md, md->dn[0], B), true, md->xn, !tied, stream,
+    if ((st = norm(md, md->hcur, md->out_norm, B, H, parts(md, md->dn[0], B), true, md->xn, !tied, stream,
                    tied ? md->xt : nullptr)) != LGX_OK)
         return st;
     if (tied && md->lm_cert_ok && md->ctx->lm_cert && md->samp.top_k == 0 && B <= LGX_LMC_MAXB) {
@@ -1060,7 +1102,8 @@ lgx_status model_build(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed, So
         upd(2 * I, H);
         upd(H, I);
         if (!f16_head(m)) upd(cf.vocab, H);
-        if ((st = dev_alloc(m, &m->h, (size_t)B * H)) || (st = dev_alloc(m, &m->xn, (size_t)B * H)) ||
+        if ((st = dev_alloc(m, &m->h, (size_t)B * H)) || (st = dev_alloc(m, &m->h2, (size_t)B * H)) ||
+            (st = dev_alloc(m, &m->xn, (size_t)B * H)) ||
             (st = dev_alloc(m, &m->xq, (size_t)(B + 15) / 16 * 16 * kmax)) ||
             (st = dev_alloc(m, &m->xd, (size_t)B * kmax / 32)) ||
             (st = dev_alloc(m, &m->sq, (size_t)(B + 15) / 16 * 16 * I)) ||
@@ -1073,6 +1116,7 @@ lgx_status model_build(lgx_ctx* c, const lgx_qwen_config* cfg, uint64_t seed, So
             (cf.vocab <= 64 * LGX_ARGMAX_SLICE &&
              (st = dev_alloc(m, &m->scand, sample_cand_bytes(B, cf.vocab) / 8))))
             return done(st);
+        m->hcur = m->h;
         // staging no longer needed
         LGX_HIP(hipDeviceSynchronize());
         for (void* p : {(void*)stage_q, (void*)stage_d}) {

@@ -463,8 +463,11 @@ def test_fused_decode_consumers_bit_exact(name, env):
     """Decode batches of 2..32 rows run RoPE + KV append inside the qkv
     product's workgroups (one per head and 16-row m-group), SwiGLU + Q8_0
     inside the gate|up product's (32 or 64 columns each) and, from one row,
-    the attention merge inside the o_proj product's (one per sequence and
-    four row tiles); with the fusion off they run as kernels of their own.  Every form leaves the oracle's
+    the attention-side residual + RMSNorm + Q8_0 inside the qkv product's
+    (one per sequence and 128 columns, the residual alternating between two
+    buffers) and the attention merge inside the o_proj product's (one per
+    sequence and eight row tiles); with the fusion off they run as kernels
+    of their own.  Every form leaves the oracle's
     tokens, logits, hidden state and KV bits: 24 rows (a second, partial
     m-group), 3 rows, and one row (the grouped GEMV), graph replays
     included."""
