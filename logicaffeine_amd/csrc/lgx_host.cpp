@@ -88,6 +88,7 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
         c->decode_fuse = env_int("LGX_DECODE_FUSE", 1) != 0;
         c->fuse_cols32 = env_int("LGX_FUSE_SWIGLU_COLS", 32) == 64 ? 2 : 1;
         c->merge_o_tiles = std::min(std::max(env_int("LGX_MERGE_O_TILES", 8), 1), 16);
+        c->gemm_grpm = env_int("LGX_GEMM_GRPM", 1) != 0;
         c->tiled_swiglu = env_int("LGX_TILED_SWIGLU", 1) != 0;
         c->norm_waves = std::min(std::max(env_int("LGX_NORM_WAVES", 1), 0), 4);
         c->lm_cert = env_int("LGX_LM_CERT", 1) != 0;
@@ -97,6 +98,10 @@ lgx_status lgx_ctx_create(int32_t device, const char* hsaco_path, lgx_ctx** out)
                 hipSuccess &&
             ncu > 0)
             c->ncu = ncu;
+        int lds = 0;
+        if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess &&
+            lds > 0)
+            c->max_lds = lds;
         c->wg_target = env_int("LGX_WG_TARGET", 512);
         if (c->wg_target < 1) c->wg_target = 1;
         for (int k = 0; k < K_COUNT; ++k) {
@@ -558,6 +563,17 @@ lgx_status lgx_q8_gemm_quantize_group(lgx_ctx* c, int32_t count, const lgx_q8_ma
                 return a.k > b.k;
             });
             return run_gemv_group(c, mats, count, stream);
+        }
+        {
+            // 2..8 rows: one launch (quantisation, products, trees)
+            lgx_gemv_mat mats[LGX_GROUP_MAX];
+            for (int i = 0; i < count && count <= LGX_GROUP_MAX; ++i)
+                mats[i] = gemv_mat(&W[i], x[i], nullptr, nullptr, y[i], 0);
+            if (count <= LGX_GROUP_MAX && gemm_grpm_ok(c, mats, count, m)) {
+                std::stable_sort(mats, mats + count,
+                                 [](const lgx_gemv_mat& a, const lgx_gemv_mat& b) { return a.k > b.k; });
+                return run_gemm_grpm(c, mats, count, m, stream);
+            }
         }
         // the tiled product from 17 rows (config 1 at M = 32: 28.9 us against
         // 35.4 us per step on the 16-row streaming kernels)

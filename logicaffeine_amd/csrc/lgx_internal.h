@@ -169,6 +169,7 @@ enum Kern {
     K_MERGE_O_D128,
     K_NORM_QKV_D64,
     K_NORM_QKV_D128,
+    K_GEMM_GRPM16,
     K_COUNT
 };
 inline const char* const kKernelNames[] = {
@@ -212,6 +213,7 @@ inline const char* const kKernelNames[] = {
     "lgx_k_attn_prefill_fast_d128_g4", "lgx_k_attn_prefill_fast_d128_g5", "lgx_k_attn_prefill_fast_d128_g6",
     "lgx_k_attn_prefill_fast_d128_g7", "lgx_k_attn_prefill_fast_d128_g8",
     "lgx_k_attn_merge_o_d64", "lgx_k_attn_merge_o_d128", "lgx_k_norm_qkv_d64", "lgx_k_norm_qkv_d128",
+    "lgx_k_q8_gemm_grpm16",
 };
 
 static_assert(sizeof(kKernelNames) / sizeof(kKernelNames[0]) == K_COUNT,
@@ -258,6 +260,8 @@ struct lgx_ctx {
     bool decode_fuse = true;      // LGX_DECODE_FUSE=0: decode glue in kernels of its own
     int fuse_cols32 = 1;          // LGX_FUSE_SWIGLU_COLS: SwiGLU columns per fused workgroup / 32
     int merge_o_tiles = 8;        // LGX_MERGE_O_TILES: o_proj row tiles per merge+o workgroup (1..16)
+    bool gemm_grpm = true;        // LGX_GEMM_GRPM=0: grouped products of 2..8 rows on the multi-launch path
+    int max_lds = 65536;          // LDS bytes a workgroup may hold (the device's figure)
     bool tiled_swiglu = true;     // LGX_TILED_SWIGLU=0: tiled gate|up products leave their outputs to lgx_k_swiglu_quant
     int norm_waves = 1;           // LGX_NORM_WAVES: rows (waves) per workgroup of the wave norm (0: off)
     bool lm_cert = true;          // LGX_LM_CERT=0: greedy tied lm_head through the full logits
@@ -790,6 +794,66 @@ inline lgx_status run_gemv_group(lgx_ctx* c, const lgx_gemv_mat* mats, int count
     const Kern k = xf ? (W == 16 ? K_GEMV_GRP16 : W == 8 ? K_GEMV_GRP8 : K_GEMV_GRP4)
                       : (W == 16 ? K_GEMV_GRPQ16 : W == 8 ? K_GEMV_GRPQ8 : K_GEMV_GRPQ4);
     return launch(c, k, dim3(wgs), dim3(64 * W), ga, stream, (unsigned)lds);
+}
+
+// Grouped products of 2..LGX_GRPM_ROWS binary32 rows in one launch
+// (lgx_k_q8_gemm_grpm16): the grouped GEMV's tiles per workgroup, one wave
+// per (tile slot, range), every matrix at most 16 ranges (k <= 16384).
+inline bool gemm_grpm_ok(const lgx_ctx* c, const lgx_gemv_mat* mats, int count, int m) {
+    if (!c->gemm_grpm || m < 2 || m > LGX_GRPM_ROWS) return false;
+    for (int i = 0; i < count; ++i) {
+        const int nr = (mats[i].k / 32 + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS;
+        // the staging of every range and the partials of 16 / nr tiles
+        const size_t lds = (size_t)nr * LGX_GRPM_ROWS * (1024 + 32 * 4) + (size_t)16 * LGX_GRPM_ROWS * 16 * 4;
+        if (nr > 16 || lds > (size_t)c->max_lds) return false;
+    }
+    return true;
+}
+inline lgx_status run_gemm_grpm(lgx_ctx* c, const lgx_gemv_mat* mats, int count, int m, void* stream) {
+    constexpr int W = 16;
+    lgx_gemv_group_args ga{};
+    ga.count = count;
+    ga.pad = m;
+    int tmax[LGX_GROUP_MAX], tpw[LGX_GROUP_MAX], nrg[LGX_GROUP_MAX];
+    double tb[LGX_GROUP_MAX];
+    std::vector<double> cand;
+    for (int i = 0; i < count; ++i) {
+        nrg[i] = (mats[i].k / 32 + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS;
+        tmax[i] = W / nrg[i];
+        tb[i] = 17.0 * mats[i].k;                      // 16 rows x k x 1.0625 B
+        for (int j = 1; j <= tmax[i]; ++j) cand.push_back(j * tb[i]);
+    }
+    std::sort(cand.begin(), cand.end());
+    // as run_gemv_group: the smallest per-workgroup byte budget whose grid
+    // fits one workgroup per compute unit
+    auto grid_for = [&](double T, int* tp) {
+        int64_t n = 0;
+        for (int i = 0; i < count; ++i) {
+            tp[i] = std::max(1, std::min(tmax[i], (int)(T / tb[i] + 1e-9)));
+            n += (mats[i].n / 16 + tp[i] - 1) / tp[i];
+        }
+        return n;
+    };
+    for (int i = 0; i < count; ++i) tpw[i] = tmax[i];
+    for (double T : cand) {
+        int tp[LGX_GROUP_MAX];
+        if (grid_for(T, tp) <= (int64_t)c->ncu) {
+            std::copy(tp, tp + count, tpw);
+            break;
+        }
+    }
+    int wgs = 0;
+    size_t lds = 0;
+    for (int i = 0; i < count; ++i) {
+        ga.mat[i] = mats[i];
+        ga.mat[i].pad = tpw[i];
+        ga.tile0[i] = wgs;
+        wgs += (mats[i].n / 16 + tpw[i] - 1) / tpw[i];
+        lds = std::max(lds, (size_t)nrg[i] * LGX_GRPM_ROWS * (1024 + 32 * 4) +
+                                (size_t)tpw[i] * nrg[i] * LGX_GRPM_ROWS * 16 * 4);
+    }
+    ga.tile0[count] = wgs;
+    return launch(c, K_GEMM_GRPM16, dim3(wgs), dim3(64 * W), ga, stream, (unsigned)lds);
 }
 
 // Whether the M = 1 products of reduction length k go through run_gemv_group.

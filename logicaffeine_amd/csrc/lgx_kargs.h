@@ -69,8 +69,9 @@ typedef struct {
 typedef struct {
     lgx_gemv_mat mat[LGX_GROUP_MAX];
     int32_t tile0[LGX_GROUP_MAX + 1];  // first workgroup of each matrix; tile0[count] = grid
-    int32_t count, pad;
+    int32_t count, pad;                // pad: the activation rows of lgx_k_q8_gemm_grpm16
 } lgx_gemv_group_args;
+#define LGX_GRPM_ROWS 8                // most activation rows of lgx_k_q8_gemm_grpm16
 
 // Canonical tree over range partials: y[i] = tree(part[0][i], ..., part[g-1][i]).
 typedef struct {

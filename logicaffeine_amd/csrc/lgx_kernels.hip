@@ -1075,6 +1075,132 @@ extern "C" __global__ __launch_bounds__(1024) void lgx_k_q8_gemv_grpq16(const lg
 }
 
 // ---------------------------------------------------------------------------
+// Grouped Q8 product of 2..LGX_GRPM_ROWS binary32 activation rows in one
+// launch (lgx_q8_gemm_quantize_group at small m): the grouped GEMV's grid
+// and layout (workgroup = tpw row tiles of one matrix x all its ranges, one
+// wave per (tile slot, range); the launcher keeps the ranges <= 16) with the
+// m rows as the MFMA's A operand instead of one broadcast row.  The
+// workgroup stages each (range, row) of the binary32 activations as Q8_0
+// (the GEMV prologue's rule, one (range, row) per wave at a time) into LDS
+// slot (range, row) in the (pair, chunk) order, then every wave requests its
+// unit stream and scales; after one barrier each wave's block dots come
+// from int8 MFMA (lane l: activation rows 4 (l / 16) + v, weight row l % 16;
+// rows past m read zeros), the canonical chain per (row, output) over the
+// range's blocks, partials to LDS, and the pairwise tree over the ranges
+// gives y[row][16 t + r].  Exact like every product: the int32 block dots do
+// not depend on how the rows are packed.
+// LDS (dynamic): ranges x LGX_GRPM_ROWS x (1 KiB + 32 scales), then
+// [tpw][ranges][LGX_GRPM_ROWS][16] partials.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void grpm_chain(const RangeInfo& ri, int lane, int M, const GrpRegs& R,
+                                           const uint8_t* xsr, float (&acc)[4]) {
+    const int c = lane >> 4, r = lane & 15;
+    const uint32_t keep = r < M ? ~0u : 0u;        // A rows past m are zeros
+    const uint8_t* xa = xsr + min(r, LGX_GRPM_ROWS - 1) * GRP_XSLOT;
+    const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        if (i < ri.npairs) {                       // wave-uniform
+            const uint4 xv = *(const uint4*)(xa + (i * 4 + c) * 16);
+            const long a0 = (long)(((uint64_t)(xv.y & keep) << 32) | (xv.x & keep));
+            const long a1 = (long)(((uint64_t)(xv.w & keep) << 32) | (xv.z & keep));
+            const long b0 = (long)(((uint64_t)R.w[i].y << 32) | R.w[i].x);
+            const long b1 = (long)(((uint64_t)R.w[i].w << 32) | R.w[i].z);
+            const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b0, zero, 0, 0, 0);
+            const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b1, zero, 0, 0, 0);
+            const float dw0 = h2f(R.dw[i] & 0xffffu), dw1 = h2f(R.dw[i] >> 16);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float* dxr = (const float*)(xsr + min(4 * c + v, LGX_GRPM_ROWS - 1) * GRP_XSLOT + 1024);
+                acc[v] = fmaf((float)d0[v], dw0 * dxr[2 * i], acc[v]);
+                acc[v] = fmaf((float)d1[v], dw1 * dxr[2 * i + 1], acc[v]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <int W>
+__device__ __forceinline__ void q8_gemm_grpm_body(const lgx_gemv_group_args& ga) {
+    extern __shared__ __align__(16) uint8_t lds_dyn[];
+    constexpr int MR = LGX_GRPM_ROWS;
+    const int bx = blockIdx.x;
+    int g = 0, t0 = 0;
+#pragma unroll
+    for (int j = 1; j < LGX_GROUP_MAX; ++j) {
+        const bool in = j < ga.count && bx >= ga.tile0[j];
+        g += in ? 1 : 0;
+        t0 = in ? ga.tile0[j] : t0;
+    }
+    const lgx_gemv_mat a = grp_mat(ga, g);
+    const int M = ga.pad;                                 // activation rows, 2..MR
+    const int k = a.k, nb = k >> 5;
+    const int nr = (nb + LGX_Q8_RANGE_BLOCKS - 1) / LGX_Q8_RANGE_BLOCKS;   // <= W
+    const int tpw = a.pad;                                // tiles per workgroup, tpw * nr <= W
+    const int ntiles = a.n >> 4;
+    const int tile_base = (bx - t0) * tpw;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    uint8_t* xsl = lds_dyn;                               // [nr][MR] slots
+    float* ps = (float*)(lds_dyn + nr * MR * GRP_XSLOT);  // [tpw][nr][MR][16]
+    // wave / nr without an integer division (wave < 16, nr <= 16: see
+    // q8_gemv_grp_body)
+    const int ts = __builtin_amdgcn_readfirstlane((int)(((float)wave + 0.5f) * __builtin_amdgcn_rcpf((float)nr)));
+    const int rg = wave - ts * nr;
+    const int t = tile_base + ts;
+    const bool on = ts < tpw && t < ntiles;
+    const RangeInfo ri = range_info(rg, k);
+    // (range, row) stagings: staging j on wave W - 1 - j % W (the waves
+    // without a tile, the highest, take the first ones), round j / W, all
+    // before the unit stream is requested (loads complete in issue order: a
+    // staging requested after the units would wait for them; config 1 at
+    // m = 8, whose down workgroups stage 9 ranges x 8 rows: 16.5 against
+    // 17.2 us with the first staging ahead of the units and the others after)
+    const int nst = nr * M;
+    auto job = [&](int s) { return (W - 1 - wave) + W * s; };
+    auto load_job = [&](int j, uint4 (&xr)[4], uint32_t& xdr) {
+        const int r2 = j / M, m = j - r2 * M;
+        lgx_gemv_mat am = a;
+        am.xf = a.xf + (int64_t)m * k;
+        grp_x_load<true>(am, range_info(r2, k), lane, xr, xdr);
+    };
+    auto stage_job = [&](int j, const uint4 (&xr)[4], uint32_t xdr) {
+        const int r2 = j / M, m = j - r2 * M;
+        int8_t* xs = (int8_t*)xsl + (r2 * MR + m) * GRP_XSLOT;
+        grp_x_stage<true>(a, range_info(r2, k), lane, xr, xdr, xs, (float*)(xs + 1024), false);
+    };
+    uint4 xa[4];
+    uint32_t da = 0;
+    GrpRegs R;
+    for (int s = 0; job(s) < nst; ++s) {
+        load_job(job(s), xa, da);
+        stage_job(job(s), xa, da);
+    }
+    if (on) grp_issue<true>(a, t, ri, lane, false, R);  // units and scales, no activation
+    __syncthreads();
+    if (on) {
+        float acc[4];
+        grpm_chain(ri, lane, M, R, xsl + rg * MR * GRP_XSLOT, acc);
+        const int c = lane >> 4;
+        if (c < MR / 4) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) ps[((ts * nr + rg) * MR + 4 * c + v) * 16 + (lane & 15)] = acc[v];
+        }
+    }
+    __syncthreads();
+    for (int o = tid; o < tpw * M * 16; o += 64 * W) {
+        const int qt = o / (M * 16), rem = o - qt * M * 16, row = rem >> 4, col = rem & 15;
+        if (tile_base + qt < ntiles)
+            a.y[(int64_t)row * a.n + (tile_base + qt) * 16 + col] =
+                tree_read(nr, [&](int jj) { return ps[((qt * nr + jj) * MR + row) * 16 + col]; });
+    }
+}
+extern "C" __global__ __launch_bounds__(1024) void lgx_k_q8_gemm_grpm16(const lgx_gemv_group_args a) {
+    q8_gemm_grpm_body<16>(a);
+}
+
+// ---------------------------------------------------------------------------
 // Streaming Q8 x Q8 GEMM on int8 MFMA (v_mfma_i32_16x16x32_i8), M > 1.
 //
 // grid = (tile groups, ranges, m-groups of MT*16 rows); 4 waves per

@@ -444,11 +444,13 @@ def test_q8_gemm_7b_shapes_m64_streaming_and_tiled(ctx, orc, n, k):
 @pytest.mark.parametrize("m", [2, 8, 16, 17, 32, 33, 64, 100])
 def test_grouped_gemm_bit_exact(ctx, orc, m):
     """lgx_q8_gemm_quantize_group: the quantisation of every activation
-    matrix, the products and the range trees of several matrices in three
-    launches (streaming 16-row kernels below 17 rows, tiled from 17), each
-    output bit-identical to the oracle's Q8_0 + canonical product: config 1's
-    gate / up / down, a single tile of one 64-column pair, a K of two ranges
-    (the second partial), a ragged last row tile."""
+    matrix, the products and the range trees of several matrices in one
+    launch up to 8 rows (lgx_k_q8_gemm_grpm16, where the device's LDS per
+    workgroup holds every range's rows) or three (streaming 16-row kernels
+    below 17 rows, tiled from 17), each output bit-identical to the oracle's
+    Q8_0 + canonical product: config 1's gate / up / down, a single tile of
+    one 64-column pair, a K of two ranges (the second partial), a ragged last
+    row tile."""
     shapes = [(8960, 1536), (8960, 1536), (1536, 8960), (48, 64), (80, 1088)]
     Ws, xs, refs = [], [], []
     for i, (n, k) in enumerate(shapes):
@@ -460,7 +462,7 @@ def test_grouped_gemm_bit_exact(ctx, orc, m):
         refs.append(orc.q8_gemm(qs, d, xq, xd))
     before = ctx.launch_count
     ys = ctx.q8_gemm_quantize_group(Ws, xs)
-    assert ctx.launch_count - before in (2, 3)
+    assert ctx.launch_count - before in ((1, 2, 3) if m <= 8 else (2, 3))
     for i, (y, ref) in enumerate(zip(ys, refs)):
         assert np.array_equal(bits(host(y)), bits(ref)), (m, shapes[i])
     # a group of one and a repeat with other inputs (stale workspace)
@@ -471,6 +473,39 @@ def test_grouped_gemm_bit_exact(ctx, orc, m):
     qs0, d0 = orc.gen_q8_matrix(7, 300, 8960, 1536)
     y2 = ctx.q8_gemm_quantize_group([Ws[0]], [ctx.to_device(x2)])[0]
     assert np.array_equal(bits(host(y2)), bits(orc.q8_gemm(qs0, d0, xq2, xd2)))
+
+
+@pytest.mark.parametrize("m", [2, 3, 5, 8])
+def test_grouped_gemm_small_m_one_launch(ctx, orc, m):
+    """2..8 rows of a group whose matrices have at most four ranges go
+    through lgx_k_q8_gemm_grpm16 in one launch (the rows' Q8_0 staged per
+    range in LDS, the rows as the MFMA's A operand, rows past m zeros, the
+    tree over the ranges in the same workgroup): every output bit-identical
+    to the oracle, and to the three-launch path (LGX_GEMM_GRPM=0)."""
+    shapes = [(8960, 1536), (1536, 4096), (48, 64), (80, 1088), (160, 2112)]
+    Ws, xs, refs = [], [], []
+    for i, (n, k) in enumerate(shapes):
+        qs, d = orc.gen_q8_matrix(8, 700 + i, n, k)
+        x = orc.gen_normal_f32(8, 800 + i + m, (m, k))
+        x[0, :32] = 0.0                          # a zero block: scale 0, quants 0
+        xq, xd = orc.quantize_q8_0(x)
+        Ws.append(ctx.q8_matrix(qs, d))
+        xs.append(ctx.to_device(x))
+        refs.append(orc.q8_gemm(qs, d, xq, xd))
+    before = ctx.launch_count
+    ys = ctx.q8_gemm_quantize_group(Ws, xs)
+    assert ctx.launch_count - before == 1
+    for i, (y, ref) in enumerate(zip(ys, refs)):
+        assert np.array_equal(bits(host(y)), bits(ref)), (m, shapes[i])
+    c3 = _ctx_with_env(LGX_GEMM_GRPM="0")
+    Ws3 = [c3.q8_matrix(*orc.gen_q8_matrix(8, 700 + i, n, k)) for i, (n, k) in enumerate(shapes)]
+    before = c3.launch_count
+    ys3 = c3.q8_gemm_quantize_group(Ws3, [c3.to_device(host(x)) for x in xs])
+    assert c3.launch_count - before in (2, 3)
+    for y, y3 in zip(ys, ys3):
+        assert np.array_equal(bits(host(y)), bits(host(y3)))
+    del Ws3, ys3
+    c3.close()
 
 
 @pytest.mark.parametrize("m,env", [(160, {}), (64, dict(LGX_GEMM_TILED_ROWS="64"))],
