@@ -798,7 +798,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the path would shard by output rows, see DESIGN.md", file=sys.stderr)
+              "the products would shard by output rows and the attention by (sequence, KV head), "
+              "with no collective in the decode step", file=sys.stderr)
         sys.exit(2)
 
     import torch

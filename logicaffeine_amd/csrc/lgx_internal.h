@@ -230,7 +230,7 @@ inline int prefill_attn_kernel(int d, int gq) {
     if (gq < 1 || gq > 8) return -1;
     return (d == 64 ? K_PFA_D64_G1 : K_PFA_D128_G1) + gq - 1;
 }
-// Debug/tuning knobs read once per ctx (documented in DESIGN.md):
+// Debug/tuning knobs read once per ctx from the environment:
 //   LGX_GEMV=dot4   route lgx_q8q8_gemv to the v_dot4 GEMV instead of MFMA
 //   LGX_WG_TARGET=n workgroups the streaming kernels aim for (default 512)
 inline int env_int(const char* name, int dflt) {
