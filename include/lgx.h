@@ -156,12 +156,15 @@ lgx_status lgx_q8q8_gemv_quantize_group(lgx_ctx* ctx, int32_t count, const lgx_q
 lgx_status lgx_q8_gemm(lgx_ctx* ctx, const lgx_q8_matrix* W, const int8_t* xq,
                        const uint16_t* xd, int32_t m, float* y, void* stream);
 /* Grouped Y[i][m][n_i] = Q8_0(X[i]) W[i]^T for `count` (1..8) independent
- * matrices over m binary32 activation rows each (X[i] is [m][k_i]): the
- * Q8_0 of every X[i] in one launch, the products of all matrices in one
- * more, their range trees in a third (none when no matrix has several).
- * Row r of Y[i] is bit-identical to lgx_q8q8_gemv_quantize of row r of
- * X[i]; m = 1 is the grouped GEMV (lgx_q8q8_gemv_quantize_group).  The
- * quantised activations and range partials live in the ctx workspace.
+ * matrices over m binary32 activation rows each (X[i] is [m][k_i]): for
+ * m = 2..8 (every k_i <= 16384, where the device's LDS per workgroup holds
+ * the rows' ranges) the quantisation, products and range trees of all
+ * matrices in one launch; otherwise the Q8_0 of every X[i] in one launch,
+ * the products of all matrices in one more, their range trees in a third
+ * (none when no matrix has several).  Row r of Y[i] is bit-identical to
+ * lgx_q8q8_gemv_quantize of row r of X[i]; m = 1 is the grouped GEMV
+ * (lgx_q8q8_gemv_quantize_group).  The three-launch form's quantised
+ * activations and range partials live in the ctx workspace.
  * Like lgx_q8_gemm, this is the batched form of the reference's per-row
  * Q8_0 matrix-vector product. */
 lgx_status lgx_q8_gemm_quantize_group(lgx_ctx* ctx, int32_t count, const lgx_q8_matrix* W,
