@@ -553,3 +553,55 @@ def test_tied_model_hidden_above_1024(ctx, hidden):
         assert np.array_equal(host(tok), ref), ("sampled", s)
     gm.close()
     om.close()
+
+
+@pytest.mark.parametrize("fuse", ["1", "0"])
+@pytest.mark.parametrize("shape", [
+    dict(hidden=512, inter=1024, n_heads=6, n_kv=2, head_dim=64, tied=1),     # hq*d = 384 != H, gq 3
+    dict(hidden=384, inter=768, n_heads=2, n_kv=1, head_dim=128, tied=0),     # d = 128, hq*d = 256
+], ids=["h512-gq3-d64", "h384-gq2-d128"])
+def test_fused_decode_other_shapes_multi_chunk(shape, fuse):
+    """The decode step's per-sequence fused kernels (residual + RMSNorm +
+    Q8_0 inside the qkv product, the attention merge inside o_proj) on
+    shapes where the attention width hq * d differs from the hidden size and
+    the head groups are 3 or 2, with ragged contexts across three 256-token
+    chunks and every batch size from 1 to 5 rows; LGX_DECODE_FUSE=0 runs the
+    separate kernels.  Tokens, logits, hidden rows and the KV cache equal the
+    oracle's bit for bit."""
+    from oracle import oracle as orc
+
+    c = _ctx_with(dict(LGX_DECODE_FUSE=fuse))
+    cfg = dict(orc.qwen_config("tiny"), n_layers=2, vocab=1024, max_batch=5, max_seq=600, **shape)
+    gm = lgx.Model(c, cfg, 91)
+    om = orc.Model(cfg, 91)
+    rng = np.random.default_rng(17)
+    lens = [530, 300, 257, 40, 3]
+    # ragged contexts: sequence b takes lens[b] prompt tokens through
+    # teacher-forced decode steps of sequences 0..nb-1 (lens descending)
+    prompts = [rng.integers(0, cfg["vocab"], size=L).astype(np.int32) for L in lens]
+    P = max(lens)
+    for p in range(P):
+        nb = sum(1 for L in lens if L > p)     # lens are descending: sequences 0..nb-1
+        tok = np.array([prompts[b][p] for b in range(nb)], np.int32)
+        dtok = c.to_device(tok)
+        gm.decode_step(dtok)
+        om.step(np.arange(nb), tok)
+    ref = None
+    for nb in (5, 4, 3, 2, 1):
+        tok = rng.integers(0, cfg["vocab"], size=nb).astype(np.int32)
+        dtok = c.to_device(tok)
+        gm.decode_step(dtok)
+        ref, lg, hid = om.step(np.arange(nb), tok, want_logits=True, want_hidden=True)
+        assert np.array_equal(host(dtok), ref), nb
+        assert np.array_equal(bits(host(gm.logits(nb))), bits(lg)), nb
+        assert np.array_equal(bits(dev_array(gm, "hidden", np.float32, (5, cfg["hidden"]))[:nb]),
+                              bits(hid)), nb
+    lens2 = [int(x) for x in dev_array(gm, "seq_len", np.int32, (5,))]
+    for layer in range(cfg["n_layers"]):
+        for b in range(5):
+            for which in (0, 1):
+                assert np.array_equal(kv_dense(gm, cfg, layer, which, b, lens2[b]),
+                                      om.kv(layer, which, b, lens2[b])), (layer, b, which)
+    gm.close()
+    om.close()
+    c.close()
