@@ -4707,22 +4707,30 @@ LGX_PFA_KERNELS(128, 8)
 // maximum and sum per query column (the same in the column's four lanes;
 // the sum adds the binary16-rounded weights, so constant V comes out as V);
 // P^T in binary16 is then directly the B operand of the PV product
-// O^T[dim][query] += V^T . P^T (v_mfma_f32_16x16x16_f16, A from a transposed
-// LDS copy of V).  Tiles of FPA_T tokens pass through LDS once for all the
-// group's heads; tokens past the block's last length read as zeros.  Output
+// O^T[dim][query] += V^T . P^T (v_mfma_f32_16x16x16_f16).  V stays in token
+// order in LDS; its A operand (16 dimensions x 4 consecutive tokens per
+// 16-lane group) comes from the transposing LDS load ds_read_b64_tr_b16:
+// the 16 lanes of a group each load 4 halves of a 4 x 16 block (row j / 4,
+// columns 4 (j % 4) ..) and lane n receives column n.  Tiles of FPA_T tokens
+// pass through LDS once for all the group's heads; tokens past the block's
+// last length read as zeros.  Output
 // rows: binary32 to `out` and / or Q8_0 (the canonical quantisation rule) to
 // xq / xd in row-major or T16 order.
 // ---------------------------------------------------------------------------
 #define FPA_Q 16
 #define FPA_T 64
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
 template <int D, int GQ>
 __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
     constexpr int CH = D / 8;                 // 16-byte pieces per row
-    constexpr int VS = FPA_T + 4;             // V^T row stride (halves): rows 8 bytes apart in the banks
     constexpr int NKS = D / 32;               // k-steps of the score product
     constexpr int NT = 64 * GQ;
+    // V pieces swizzled by twice the token mod CH / 2: the four rows of one
+    // transposing load (consecutive tokens) fall on different 32-byte pairs
+    constexpr int VSW = CH / 2 - 1;
     __shared__ __align__(16) uint16_t k_s[FPA_T * D];     // [token][piece ^ (token % CH)]
-    __shared__ __align__(16) uint16_t vt_s[D * VS];       // [dim][token]
+    __shared__ __align__(16) uint16_t v_s[FPA_T * D];     // [token][piece ^ 2 (token % (CH / 2))]
     __shared__ int pg_s[FPA_T / LGX_PAGE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -4772,12 +4780,7 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
             uint4 kk = *(const uint4*)(a.kpages + off), vv = *(const uint4*)(a.vpages + off);
             if (!on) kk = vv = make_uint4(0u, 0u, 0u, 0u);
             *(uint4*)(k_s + t * D + (c ^ (t & (CH - 1))) * 8) = kk;
-            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                vt_s[(c * 8 + 2 * e) * VS + t] = (uint16_t)(vw[e] & 0xffffu);
-                vt_s[(c * 8 + 2 * e + 1) * VS + t] = (uint16_t)(vw[e] >> 16);
-            }
+            *(uint4*)(v_s + t * D + (c ^ ((t & VSW) << 1)) * 8) = vv;
         }
         __syncthreads();
         // S^T of the tile's four 16-token sub-tiles
@@ -4824,13 +4827,20 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
         m = mn;
 #pragma unroll
         for (int i = 0; i < D / 16; ++i) o[i] *= alpha;
+        // lane (qc, kg) loads token 16 u + 4 kg + qc / 4, dimensions
+        // 16 i + 4 (qc % 4) .. + 3, and receives dimension 16 i + qc of the
+        // tokens 16 u + 4 kg .. + 3
 #pragma unroll
-        for (int u = 0; u < FPA_T / 16; ++u)
+        for (int u = 0; u < FPA_T / 16; ++u) {
+            const int tv = 16 * u + 4 * kg + (qc >> 2);
 #pragma unroll
             for (int i = 0; i < D / 16; ++i) {
-                const uint2 vw = *(const uint2*)(vt_s + (16 * i + qc) * VS + 16 * u + 4 * kg);
+                const int cv = 2 * i + ((qc >> 1) & 1);
+                const v4s vw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_v4s*)(v_s + tv * D + (cv ^ ((tv & VSW) << 1)) * 8 + (qc & 1) * 4));
                 o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, vw), pt[u], o[i], 0, 0, 0);
             }
+        }
     }
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
