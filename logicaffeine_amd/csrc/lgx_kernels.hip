@@ -4721,6 +4721,22 @@ LGX_PFA_KERNELS(128, 8)
 #define FPA_T 64
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s lds_v4s;
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+typedef __attribute__((address_space(3))) uint4 lds_u4;
+// Tile staging: direct global->LDS loads into two buffers, the next tile's
+// issued right after the barrier that publishes the current one, so its
+// transfer overlaps the current tile's products.  A wave instruction moves
+// 1 KiB = 64 / CH tokens of one page; lane i lands at slot i of it, and its
+// source piece is chosen so that the slot holds the swizzled layout.  Rows
+// past the block's last length (last tile only) are cleared in V after the
+// tile lands (their scores are masked, their weights are 0, and 0 x V must
+// stay 0).
+template <int D>
+struct FpaBuf {
+    uint16_t k[FPA_T * D];                    // [token][piece ^ (token % CH)]
+    uint16_t v[FPA_T * D];                    // [token][piece ^ 2 (token % (CH / 2))]
+};
+
 template <int D, int GQ>
 __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
     constexpr int CH = D / 8;                 // 16-byte pieces per row
@@ -4729,14 +4745,20 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
     // V pieces swizzled by twice the token mod CH / 2: the four rows of one
     // transposing load (consecutive tokens) fall on different 32-byte pairs
     constexpr int VSW = CH / 2 - 1;
-    __shared__ __align__(16) uint16_t k_s[FPA_T * D];     // [token][piece ^ (token % CH)]
-    __shared__ __align__(16) uint16_t v_s[FPA_T * D];     // [token][piece ^ 2 (token % (CH / 2))]
-    __shared__ int pg_s[FPA_T / LGX_PAGE];
+    constexpr int TPI = 64 / CH;              // tokens per 1 KiB wave instruction
+    constexpr int NI = FPA_T / TPI;           // wave instructions per tile and tensor
+    constexpr int PPT = FPA_T / LGX_PAGE;     // pages per tile
+    static_assert(LGX_PAGE % TPI == 0 && PPT <= 64, "a wave instruction stays in one page");
+    // two buffers as two variables: a direct load into one is known not to
+    // alias reads of the other
+    __shared__ __align__(16) FpaBuf<D> sb0, sb1;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int qpr = max(a.qpr, 1), nqb = (qpr + FPA_Q - 1) / FPA_Q;
-    const int bg = blockIdx.x / nqb, qb = blockIdx.x - bg * nqb;
-    const int b = bg / a.hkv, g = bg - b * a.hkv;
+    // workgroup coordinates as scalars (divisions the compiler may place in
+    // vector registers; the page reads below must see a uniform address)
+    const int bg = __builtin_amdgcn_readfirstlane(blockIdx.x / nqb), qb = blockIdx.x - bg * nqb;
+    const int b = __builtin_amdgcn_readfirstlane(bg / a.hkv), g = bg - b * a.hkv;
     const int j0 = qb * FPA_Q;
     const int sl = a.seq_len[b];
     const int h = g * GQ + w;
@@ -4747,6 +4769,55 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
     const int jl = min(j0 + FPA_Q, qpr) - 1;
     const int Lmax = min(max(sl + jl + a.len_add, 0), a.maxlen);   // workgroup-uniform
     const int row = b * qpr + min(jq, qpr - 1);
+    const int ntile = (Lmax + FPA_T - 1) / FPA_T;
+    const int32_t* ptab = a.page_table + (int64_t)b * a.maxp;
+    // page table entries of tile tt as loaded, through the scalar cache (the
+    // row address is uniform): they are first used by the stage after next,
+    // and scalar loads do not count against the direct loads in flight;
+    // stage() clamps them
+    struct Pg {
+        int p[PPT];
+    };
+    const __attribute__((address_space(4))) int32_t* ptab_s =
+        (const __attribute__((address_space(4))) int32_t*)ptab;
+    auto tile_pages = [&](int tt) {
+        Pg r;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) r.p[i] = ptab_s[min(tt * PPT + i, a.maxp - 1)];
+        return r;
+    };
+    // the buffers as LDS-space pointers
+    lds_u16* const kb0 = (lds_u16*)sb0.k;
+    lds_u16* const vb0 = (lds_u16*)sb0.v;
+    lds_u16* const kb1 = (lds_u16*)sb1.k;
+    lds_u16* const vb1 = (lds_u16*)sb1.v;
+    // tile tt's loads into kb / vb (wave instruction j on wave j % GQ), pgv
+    // its tile_pages (an entry at or past the length gives slot 0, read but
+    // never used unmasked)
+    auto stage = [&](lds_u16* kb, lds_u16* vb, int tt, const Pg& pgv) __attribute__((always_inline)) {
+        // the lane's token within a wave instruction and its piece slot,
+        // derived here from an opaque copy of the lane index: the per-lane
+        // addresses are computed at each stage, not held in registers over
+        // the tile loop
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int tl = ln / CH, cl = ln % CH;
+        auto one = [&](int jj, bool isv) __attribute__((always_inline)) {
+            const int t = TPI * jj + tl;
+            const int ip = (TPI * jj) / LGX_PAGE;
+            const int pg = (tt * PPT + ip) * LGX_PAGE < Lmax ? min(max(pgv.p[ip], 0), a.num_pages - 1) : 0;
+            const int c = isv ? cl ^ ((t & VSW) << 1) : cl ^ (t & (CH - 1));
+            const uint16_t* src = (isv ? a.vpages : a.kpages) +
+                                  (((int64_t)pg * a.hkv + g) * LGX_PAGE + (t & 15)) * D + c * 8;
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)((isv ? vb : kb) + jj * 512), 16, 0, 0);
+        };
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+            if (j % GQ == w) one(j, false);       // uniform per wave
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+            if ((NI + j) % GQ == w) one(j, true);
+    };
     v8h qv[NKS];
     {
         const float* qr = a.q + ((int64_t)row * a.hq + h) * D;
@@ -4763,26 +4834,22 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
     v4f o[D / 16];
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) o[i] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
-    const int ntile = (Lmax + FPA_T - 1) / FPA_T;
-    for (int tt = 0; tt < ntile; ++tt) {
+    // tile tt from sb (landed), the next tile's loads into sn with its pages
+    // pgn; returns the pages of the tile after that
+    auto run = [&](int tt, lds_u16* k_s, lds_u16* v_s, lds_u16* kn, lds_u16* vn, const Pg& pgn)
+                   __attribute__((always_inline)) -> Pg {
         const int t0 = tt * FPA_T;
-        __syncthreads();                          // the previous tile is fully read
-        if (tid < FPA_T / LGX_PAGE) {
-            int pg = 0;
-            if (t0 + tid * LGX_PAGE < Lmax) pg = a.page_table[(int64_t)b * a.maxp + t0 / LGX_PAGE + tid];
-            pg_s[tid] = min(max(pg, 0), a.num_pages - 1);
+        __syncthreads();                          // tile tt landed (every wave waited); tile tt - 1 read
+        if (t0 + FPA_T > Lmax) {                  // uniform: the last tile, rows past Lmax cleared in V
+            for (int p = tid; p < FPA_T * CH; p += NT)
+                if (t0 + p / CH >= Lmax) *(lds_u4*)(v_s + p * 8) = make_uint4(0u, 0u, 0u, 0u);
+            __syncthreads();
         }
-        __syncthreads();
-        for (int p = tid; p < FPA_T * CH; p += NT) {
-            const int t = p / CH, c = p - t * CH;
-            const int64_t off = (((int64_t)pg_s[t >> 4] * a.hkv + g) * LGX_PAGE + (t & 15)) * D + c * 8;
-            const bool on = t0 + t < Lmax;
-            uint4 kk = *(const uint4*)(a.kpages + off), vv = *(const uint4*)(a.vpages + off);
-            if (!on) kk = vv = make_uint4(0u, 0u, 0u, 0u);
-            *(uint4*)(k_s + t * D + (c ^ (t & (CH - 1))) * 8) = kk;
-            *(uint4*)(v_s + t * D + (c ^ ((t & VSW) << 1)) * 8) = vv;
+        Pg pgnn = pgn;
+        if (tt + 1 < ntile) {
+            stage(kn, vn, tt + 1, pgn);
+            pgnn = tile_pages(min(tt + 2, ntile - 1));
         }
-        __syncthreads();
         // S^T of the tile's four 16-token sub-tiles
         v4f st[FPA_T / 16];
 #pragma unroll
@@ -4792,7 +4859,7 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
 #pragma unroll
             for (int s = 0; s < NKS; ++s) {
                 const int c = 4 * s + kg;
-                const v8h kv = as_v8h(*(const uint4*)(k_s + tr * D + (c ^ (tr & (CH - 1))) * 8));
+                const v8h kv = as_v8h(*(const lds_u4*)(k_s + tr * D + (c ^ (tr & (CH - 1))) * 8));
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qv[s], acc, 0, 0, 0);
             }
             st[u] = acc;
@@ -4841,6 +4908,16 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
                 o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, vw), pt[u], o[i], 0, 0, 0);
             }
         }
+        return pgnn;
+    };
+    if (ntile > 0) {
+        stage(kb0, vb0, 0, tile_pages(0));
+        Pg pgn = tile_pages(min(1, ntile - 1));
+#pragma unroll 1
+        for (int tt = 0; tt < ntile; tt += 2) {
+            pgn = run(tt, kb0, vb0, kb1, vb1, pgn);
+            if (tt + 1 < ntile) pgn = run(tt + 1, kb1, vb1, kb0, vb0, pgn);
+        }
     }
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
@@ -4882,8 +4959,8 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
 }
 
 #define LGX_FPA_KERNELS(D, G)                                                                     \
-    extern "C" __global__ __launch_bounds__(64 * G) void lgx_k_attn_prefill_fast_d##D##_g##G(     \
-        const lgx_attn_args a) {                                                                 \
+    extern "C" __global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(4)))     \
+    void lgx_k_attn_prefill_fast_d##D##_g##G(const lgx_attn_args a) {                            \
         attn_prefill_fast_body<D, G>(a);                                                         \
     }
 LGX_FPA_KERNELS(64, 1)
