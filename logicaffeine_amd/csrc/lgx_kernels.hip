@@ -4818,6 +4818,9 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
         for (int j = 0; j < NI; ++j)
             if ((NI + j) % GQ == w) one(j, true);
     };
+    // scores in base-2 units: q scaled by log2(e) / sqrt(d), so the weights
+    // are exp2(s - m)
+    const float qscale = a.scale * 1.44269504088896341f;
     v8h qv[NKS];
     {
         const float* qr = a.q + ((int64_t)row * a.hq + h) * D;
@@ -4827,7 +4830,7 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
             const float4 x1 = *(const float4*)(qr + 32 * s + 8 * kg + 4);
             const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) qv[s][e] = (_Float16)(xs[e] * a.scale);
+            for (int e = 0; e < 8; ++e) qv[s][e] = (_Float16)(xs[e] * qscale);
         }
     }
     float m = -__builtin_inff(), l = 0.0f;
@@ -4877,23 +4880,31 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
         mt = fmaxf(mt, shfl_xor_f(mt, 32));
         const float mn = fmaxf(m, mt);
         const bool none = mn == -__builtin_inff();          // nothing attended yet
-        const float alpha = none ? 1.0f : __expf(m - mn);
+        const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+        // v_exp_f32 (2^x; results below the normal range give 0): a masked
+        // score (-inf) gives 0 against any finite maximum; with nothing
+        // attended the reference is 0 (all weights 0)
+        const float mref = none ? 0.0f : mn;
         float ps = 0.0f;
         v4h pt[FPA_T / 16];
 #pragma unroll
         for (int u = 0; u < FPA_T / 16; ++u)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float pv = st[u][v] == -__builtin_inff() ? 0.0f : __expf(st[u][v] - mn);
-                pt[u][v] = (_Float16)pv;
+                pt[u][v] = (_Float16)__builtin_amdgcn_exp2f(st[u][v] - mref);
                 ps += (float)pt[u][v];            // the weights the PV product uses
             }
         ps += shfl_xor_f(ps, 16);
         ps += shfl_xor_f(ps, 32);
         l = l * alpha + ps;
         m = mn;
+        // o *= alpha only where some lane's alpha differs from 1 (a factor
+        // of 1 changes nothing): the running maxima settle after the first
+        // tiles
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-        for (int i = 0; i < D / 16; ++i) o[i] *= alpha;
+            for (int i = 0; i < D / 16; ++i) o[i] *= alpha;
+        }
         // lane (qc, kg) loads token 16 u + 4 kg + qc / 4, dimensions
         // 16 i + 4 (qc % 4) .. + 3, and receives dimension 16 i + qc of the
         // tokens 16 u + 4 kg .. + 3
