@@ -5,8 +5,10 @@
   is at most 2e-3 of the largest magnitude in that canonical output vector.
   Cases: those of the exact kernel (fresh and cached sequences, row counts
   not a multiple of 16, every head group 1..8, d 64 and 128), config 4's head
-  layout at a 4096-token context, and closed forms (constant V gives V; a
-  single cached token gives its V row exactly).
+  layout at a 4096-token context, closed forms (constant V gives V; a
+  single cached token gives its V row exactly), and a cache whose slots past
+  each sequence's length hold NaN keys and infinite values (the exact
+  prefill and decode kernels on it stay bit-exact).
 * A model prefilled in fast mode (binary16 GEMMs on dequantised weights,
   binary16 activations, the fast attention): the cache it leaves, loaded
   into the oracle, gives the device's next token, logits and last-position
@@ -91,6 +93,45 @@ def test_fast_prefill_attn_config4_shape_sampled(ctx, orc):
     rows = [0, 1, 15, 16, 31, 63, 64, 100, 127]
     lens = np.array([ctx_len[r // P] + r % P + 1 for r in rows], np.int32)
     within(out[rows], orc.gqa_decode_attn(q[rows], k, v, pt[[r // P for r in rows]], lens))
+
+
+def poison_past_lengths(k, v, pt, lens):
+    """Every cache slot at or past its sequence's length: NaN in K, +-inf in
+    V (the kernels read whole tiles and pages, and must not let those slots
+    reach an attended output)."""
+    k, v = k.copy(), v.copy()
+    for b, n in enumerate(lens):
+        for t in range(n, pt.shape[1] * 16):
+            pg, sl = pt[b, t // 16], t % 16
+            k[pg, :, sl, :] = 0x7E00
+            v[pg, :, sl, :] = 0x7C00 if t % 2 else 0xFC00
+    return k, v
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_fast_prefill_attn_nonfinite_past_length(ctx, orc, d):
+    """NaN keys and infinite values in every slot past a sequence's length
+    (the last tile's rows past the block's last length, the rest of its
+    pages): the fast outputs stay finite and within tolerance, and the exact
+    prefill and decode kernels on the same cache stay bit-exact."""
+    hq, hkv, P = 14, 2, 45
+    ctx_len = [0, 70, 129]
+    lens = [c + P for c in ctx_len]
+    k, v, pt, maxp = make_cache(len(ctx_len), hkv, d, [n + 40 for n in lens], seed=91 + d)
+    k, v = poison_past_lengths(k, v, pt, lens)
+    q = orc.gen_normal_f32(7, d, (len(ctx_len) * P, hq, d))
+    ref = prefill_ref(orc, q, k, v, pt, ctx_len, P)
+    assert np.all(np.isfinite(ref))
+    within(fast(ctx, q, k, v, pt, ctx_len, P, maxp * 16), ref)
+    exact = host(ctx.gqa_prefill_attn(ctx.to_device(q), ctx.to_device(k), ctx.to_device(v),
+                                      ctx.to_device(pt), ctx.to_device(np.asarray(ctx_len, np.int32)),
+                                      P, maxp * 16))
+    assert np.array_equal(bits(exact), bits(ref))
+    last = np.array([b * P + P - 1 for b in range(len(ctx_len))])
+    dec = host(ctx.gqa_decode_attn(ctx.to_device(np.ascontiguousarray(q[last])), ctx.to_device(k),
+                                   ctx.to_device(v), ctx.to_device(pt),
+                                   ctx.to_device(np.asarray(lens, np.int32)), maxp * 16))
+    assert np.array_equal(bits(dec), bits(ref[last]))
 
 
 def test_fast_prefill_attn_closed_forms(ctx, orc):
