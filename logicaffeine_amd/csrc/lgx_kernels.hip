@@ -4712,8 +4712,8 @@ LGX_PFA_KERNELS(128, 8)
 // 16-lane group) comes from the transposing LDS load ds_read_b64_tr_b16:
 // the 16 lanes of a group each load 4 halves of a 4 x 16 block (row j / 4,
 // columns 4 (j % 4) ..) and lane n receives column n.  Tiles of FPA_T tokens
-// pass through LDS once for all the group's heads; tokens past the block's
-// last length read as zeros.  Output
+// pass through LDS once for all the group's heads; V rows past the block's
+// last length are cleared (their scores are masked).  Output
 // rows: binary32 to `out` and / or Q8_0 (the canonical quantisation rule) to
 // xq / xd in row-major or T16 order.
 // ---------------------------------------------------------------------------
@@ -4837,8 +4837,8 @@ __device__ __forceinline__ void attn_prefill_fast_body(const lgx_attn_args& a) {
     v4f o[D / 16];
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) o[i] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
-    // tile tt from sb (landed), the next tile's loads into sn with its pages
-    // pgn; returns the pages of the tile after that
+    // tile tt from k_s / v_s (landed), the next tile's loads into kn / vn
+    // with its pages pgn; returns the pages of the tile after that
     auto run = [&](int tt, lds_u16* k_s, lds_u16* v_s, lds_u16* kn, lds_u16* vn, const Pg& pgn)
                    __attribute__((always_inline)) -> Pg {
         const int t0 = tt * FPA_T;
